@@ -1,0 +1,170 @@
+// Shared device helpers for the NKIPy gfx950 kernels: storage types,
+// bf16 / fp8-e4m3fn / fp16 conversions, 16-byte vector access and
+// wavefront / workgroup reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define NK_DEVICE __device__ __forceinline__
+
+namespace nk {
+
+// ---------------------------------------------------------------------------
+// Storage types.  Tensors cross the C ABI as raw bytes; kernels reinterpret
+// them with these tags.  bf16 and fp8 are stored as their bit patterns.
+// ---------------------------------------------------------------------------
+struct bf16 { uint16_t bits; };
+struct f16 { uint16_t bits; };
+struct e4m3 { uint8_t bits; };  // OCP float8 E4M3FN: bias 7, no inf, 0x7f/0xff NaN
+
+NK_DEVICE float bf16_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+// Round-to-nearest-even float -> bf16, NaN kept quiet.  Same closed form as
+// the oracle's numpy rounding (add 0x7fff plus the kept LSB, truncate).
+NK_DEVICE uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+NK_DEVICE float f16_to_f32(uint16_t h) {
+  _Float16 v;
+  __builtin_memcpy(&v, &h, 2);
+  return (float)v;
+}
+NK_DEVICE uint16_t f32_to_f16(float f) {
+  _Float16 v = (_Float16)f;
+  uint16_t h;
+  __builtin_memcpy(&h, &v, 2);
+  return h;
+}
+
+// E4M3FN decode: sign, 4-bit exponent (bias 7), 3-bit mantissa; exponent 0
+// is subnormal (2^-6 * m/8); 0x7f / 0xff are NaN; no infinities.
+NK_DEVICE float e4m3_to_f32(uint8_t b) {
+  uint32_t s = (uint32_t)(b & 0x80u) << 24;
+  uint32_t e = (b >> 3) & 0xfu;
+  uint32_t m = b & 0x7u;
+  if ((b & 0x7fu) == 0x7fu) return __uint_as_float(0x7fc00000u | s);
+  if (e == 0) {
+    float v = (float)m * 0.001953125f;  // m/8 * 2^-6
+    return __uint_as_float(__float_as_uint(v) | s);
+  }
+  return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
+}
+
+// Load / store of one element, converting to / from float.
+template <typename T> struct Elt;
+template <> struct Elt<float> {
+  static NK_DEVICE float load(const float *p, long i) { return p[i]; }
+  static NK_DEVICE void store(float *p, long i, float v) { p[i] = v; }
+};
+template <> struct Elt<bf16> {
+  static NK_DEVICE float load(const bf16 *p, long i) { return bf16_to_f32(p[i].bits); }
+  static NK_DEVICE void store(bf16 *p, long i, float v) { p[i].bits = f32_to_bf16(v); }
+};
+template <> struct Elt<f16> {
+  static NK_DEVICE float load(const f16 *p, long i) { return f16_to_f32(p[i].bits); }
+  static NK_DEVICE void store(f16 *p, long i, float v) { p[i].bits = f32_to_f16(v); }
+};
+
+// Eight consecutive elements (16 bytes for 2-byte types, 32 bytes for fp32)
+// loaded with 128-bit accesses.  `p` must be 16-byte aligned.
+template <typename T> struct Vec8;
+template <> struct Vec8<float> {
+  static NK_DEVICE void load(const float *p, float v[8]) {
+    const float4 *q = reinterpret_cast<const float4 *>(p);
+    float4 a = q[0], b = q[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  static NK_DEVICE void store(float *p, const float v[8]) {
+    float4 *q = reinterpret_cast<float4 *>(p);
+    q[0] = make_float4(v[0], v[1], v[2], v[3]);
+    q[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+};
+template <> struct Vec8<bf16> {
+  static NK_DEVICE void load(const bf16 *p, float v[8]) {
+    uint4 u = *reinterpret_cast<const uint4 *>(p);
+    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+  static NK_DEVICE void store(bf16 *p, const float v[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
+    *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+template <> struct Vec8<f16> {
+  static NK_DEVICE void load(const f16 *p, float v[8]) {
+    uint4 u = *reinterpret_cast<const uint4 *>(p);
+    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = f16_to_f32((uint16_t)(w[i] & 0xffffu));
+      v[2 * i + 1] = f16_to_f32((uint16_t)(w[i] >> 16));
+    }
+  }
+  static NK_DEVICE void store(f16 *p, const float v[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (uint32_t)f32_to_f16(v[2 * i]) | ((uint32_t)f32_to_f16(v[2 * i + 1]) << 16);
+    *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Reductions.  A wavefront is 64 lanes on CDNA4.
+// ---------------------------------------------------------------------------
+NK_DEVICE float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+NK_DEVICE float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Workgroup reductions over BLOCK threads (BLOCK a multiple of 64, <= 1024).
+// `red` is a __shared__ scratch of at least BLOCK/64 floats; the function
+// synchronises before reusing it, so back-to-back calls are safe.
+template <int BLOCK>
+NK_DEVICE float block_sum(float v, float *red) {
+  v = wave_sum(v);
+  if (BLOCK == 64) return v;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < BLOCK / 64; ++i) t += red[i];
+  return t;
+}
+template <int BLOCK>
+NK_DEVICE float block_max(float v, float *red) {
+  v = wave_max(v);
+  if (BLOCK == 64) return v;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float t = red[0];
+#pragma unroll
+  for (int i = 1; i < BLOCK / 64; ++i) t = fmaxf(t, red[i]);
+  return t;
+}
+
+}  // namespace nk

@@ -1,0 +1,263 @@
+// Fused elementwise + row-reduction kernels (gfx950).
+//
+//   softmax over the last axis:  y = exp(x - max_row) / sum_row(exp(x - max_row))
+//     -- the NumPy composition of softmax_kernel (README.md:125-128,
+//        tests/kernels/softmax.py:7-10) and its fp32-upcast variant
+//        (examples/models/qwen3_embedding/kernels/softmax.py:4-8).
+//   residual + RMSNorm:  h = x (+ r);  y = h / sqrt(mean(h^2) + eps) * w
+//     -- rmsnorm_kernel (examples/models/qwen3/kernels/rmsnorm.py:4-21)
+//        applied to z = x + h1 (examples/models/qwen3/kernels/transformer_layer.py:60),
+//        and the 1/sqrt form of tests/kernels/llama_decoder_dynamo.py:95-107.
+//
+// Layout: rows of `n` contiguous elements, row-major, one workgroup per row.
+// The register variants hold the whole row in VGPRs (CHUNKS x 8 elements per
+// thread, 128-bit loads, each input byte read once from HBM); the loop
+// variants take any n and re-read the row (fallback only).
+// Arithmetic is fp32 whatever the storage type; exp is the accurate libm
+// expf (no exp2 shortcut) so fp32 softmax stays within 1e-5 of NumPy.
+
+#include "common.h"
+
+using namespace nk;
+
+struct SoftmaxArgs {
+  const void *x;
+  void *y;
+  int64_t rows;
+  int32_t n;
+  int32_t pad;
+};
+
+template <typename TI, typename TO, int BLOCK, int CHUNKS>
+__device__ __forceinline__ void softmax_reg_body(const SoftmaxArgs &a) {
+  __shared__ float red[BLOCK / 64];
+  const int64_t row = blockIdx.x;
+  const int n = a.n;
+  const TI *x = reinterpret_cast<const TI *>(a.x) + row * n;
+  TO *y = reinterpret_cast<TO *>(a.y) + row * n;
+  const int tid = threadIdx.x;
+  float v[CHUNKS][8];
+  float m = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int idx = (c * BLOCK + tid) * 8;
+    if (idx < n) {
+      Vec8<TI>::load(x + idx, v[c]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, v[c][j]);
+    }
+  }
+  m = block_max<BLOCK>(m, red);
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int idx = (c * BLOCK + tid) * 8;
+    if (idx < n) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        v[c][j] = expf(v[c][j] - m);
+        s += v[c][j];
+      }
+    }
+  }
+  s = block_sum<BLOCK>(s, red);
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int idx = (c * BLOCK + tid) * 8;
+    if (idx < n) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[c][j] = v[c][j] / s;
+      Vec8<TO>::store(y + idx, v[c]);
+    }
+  }
+}
+
+template <typename TI, typename TO, int BLOCK>
+__device__ __forceinline__ void softmax_loop_body(const SoftmaxArgs &a) {
+  __shared__ float red[BLOCK / 64];
+  const int64_t row = blockIdx.x;
+  const int n = a.n;
+  const TI *x = reinterpret_cast<const TI *>(a.x) + row * n;
+  TO *y = reinterpret_cast<TO *>(a.y) + row * n;
+  float m = -INFINITY;
+  for (int i = threadIdx.x; i < n; i += BLOCK) m = fmaxf(m, Elt<TI>::load(x, i));
+  m = block_max<BLOCK>(m, red);
+  float s = 0.f;
+  for (int i = threadIdx.x; i < n; i += BLOCK) s += expf(Elt<TI>::load(x, i) - m);
+  s = block_sum<BLOCK>(s, red);
+  for (int i = threadIdx.x; i < n; i += BLOCK)
+    Elt<TO>::store(y, i, expf(Elt<TI>::load(x, i) - m) / s);
+}
+
+#define NK_SOFTMAX_REG(TI, TO, tin, ton, B, C)                                       \
+  extern "C" __global__ __launch_bounds__(B) void nk_softmax_reg_##tin##_##ton##_b##B##_c##C( \
+      SoftmaxArgs a) {                                                               \
+    softmax_reg_body<TI, TO, B, C>(a);                                               \
+  }
+#define NK_SOFTMAX_LOOP(TI, TO, tin, ton)                                             \
+  extern "C" __global__ __launch_bounds__(256) void nk_softmax_loop_##tin##_##ton(     \
+      SoftmaxArgs a) {                                                               \
+    softmax_loop_body<TI, TO, 256>(a);                                               \
+  }
+
+#define NK_SOFTMAX_ALL(TI, TO, tin, ton) \
+  NK_SOFTMAX_REG(TI, TO, tin, ton, 64, 1)  \
+  NK_SOFTMAX_REG(TI, TO, tin, ton, 256, 1) \
+  NK_SOFTMAX_REG(TI, TO, tin, ton, 256, 2) \
+  NK_SOFTMAX_REG(TI, TO, tin, ton, 256, 4) \
+  NK_SOFTMAX_REG(TI, TO, tin, ton, 512, 4) \
+  NK_SOFTMAX_LOOP(TI, TO, tin, ton)
+
+NK_SOFTMAX_ALL(float, float, f32, f32)
+NK_SOFTMAX_ALL(bf16, bf16, bf16, bf16)
+NK_SOFTMAX_ALL(bf16, float, bf16, f32)
+NK_SOFTMAX_ALL(float, bf16, f32, bf16)
+NK_SOFTMAX_ALL(f16, f16, f16, f16)
+
+// ---------------------------------------------------------------------------
+// Residual + RMSNorm
+// ---------------------------------------------------------------------------
+struct RmsNormArgs {
+  const void *x;
+  const void *r;  // residual (flag NK_RMS_RES)
+  const void *w;  // weight   (flag NK_RMS_W)
+  void *y;
+  void *h;        // residual sum out (flag NK_RMS_WRITE_H)
+  int64_t rows;
+  int32_t n;
+  float eps;
+  int32_t flags;
+  int32_t pad;
+};
+
+enum {
+  NK_RMS_RES = 1,        // h = x + r
+  NK_RMS_ROUND_H = 2,    // round h to the storage type before use (bf16 add)
+  NK_RMS_WRITE_H = 4,    // also store h
+  NK_RMS_MUL_RECIP = 8,  // y = h * (1/sqrt(.)) instead of h / sqrt(.)
+  NK_RMS_W = 16,         // multiply by weight
+};
+
+template <typename T>
+__device__ __forceinline__ float round_to(float v);
+template <> __device__ __forceinline__ float round_to<float>(float v) { return v; }
+template <> __device__ __forceinline__ float round_to<bf16>(float v) {
+  return bf16_to_f32(f32_to_bf16(v));
+}
+template <> __device__ __forceinline__ float round_to<f16>(float v) {
+  return f16_to_f32(f32_to_f16(v));
+}
+
+template <typename T, int BLOCK, int CHUNKS>
+__device__ __forceinline__ void rmsnorm_reg_body(const RmsNormArgs &a) {
+  __shared__ float red[BLOCK / 64];
+  const int64_t row = blockIdx.x;
+  const int n = a.n;
+  const int flags = a.flags;
+  const T *x = reinterpret_cast<const T *>(a.x) + row * n;
+  const T *r = reinterpret_cast<const T *>(a.r) + row * n;
+  const T *w = reinterpret_cast<const T *>(a.w);
+  T *y = reinterpret_cast<T *>(a.y) + row * n;
+  T *h = reinterpret_cast<T *>(a.h) + row * n;
+  const int tid = threadIdx.x;
+  float v[CHUNKS][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int idx = (c * BLOCK + tid) * 8;
+    if (idx < n) {
+      Vec8<T>::load(x + idx, v[c]);
+      if (flags & NK_RMS_RES) {
+        float rv[8];
+        Vec8<T>::load(r + idx, rv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[c][j] += rv[j];
+        if (flags & NK_RMS_ROUND_H) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[c][j] = round_to<T>(v[c][j]);
+        }
+        if (flags & NK_RMS_WRITE_H) Vec8<T>::store(h + idx, v[c]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += v[c][j] * v[c][j];
+    }
+  }
+  ss = block_sum<BLOCK>(ss, red);
+  const float ms = ss / (float)n;
+  const float s = sqrtf(ms + a.eps);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int idx = (c * BLOCK + tid) * 8;
+    if (idx < n) {
+      float wv[8];
+      if (flags & NK_RMS_W) Vec8<T>::load(w + idx, wv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float q = (flags & NK_RMS_MUL_RECIP) ? v[c][j] * inv : v[c][j] / s;
+        if (flags & NK_RMS_W) q = q * wv[j];
+        v[c][j] = q;
+      }
+      Vec8<T>::store(y + idx, v[c]);
+    }
+  }
+}
+
+template <typename T, int BLOCK>
+__device__ __forceinline__ void rmsnorm_loop_body(const RmsNormArgs &a) {
+  __shared__ float red[BLOCK / 64];
+  const int64_t row = blockIdx.x;
+  const int n = a.n;
+  const int flags = a.flags;
+  const T *x = reinterpret_cast<const T *>(a.x) + row * n;
+  const T *r = reinterpret_cast<const T *>(a.r) + row * n;
+  const T *w = reinterpret_cast<const T *>(a.w);
+  T *y = reinterpret_cast<T *>(a.y) + row * n;
+  T *h = reinterpret_cast<T *>(a.h) + row * n;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < n; i += BLOCK) {
+    float v = Elt<T>::load(x, i);
+    if (flags & NK_RMS_RES) {
+      v += Elt<T>::load(r, i);
+      if (flags & NK_RMS_ROUND_H) v = round_to<T>(v);
+    }
+    ss += v * v;
+  }
+  ss = block_sum<BLOCK>(ss, red);
+  const float ms = ss / (float)n;
+  const float s = sqrtf(ms + a.eps);
+  const float inv = 1.0f / s;
+  for (int i = threadIdx.x; i < n; i += BLOCK) {
+    float v = Elt<T>::load(x, i);
+    if (flags & NK_RMS_RES) {
+      v += Elt<T>::load(r, i);
+      if (flags & NK_RMS_ROUND_H) v = round_to<T>(v);
+      if (flags & NK_RMS_WRITE_H) Elt<T>::store(h, i, v);
+    }
+    float q = (flags & NK_RMS_MUL_RECIP) ? v * inv : v / s;
+    if (flags & NK_RMS_W) q = q * Elt<T>::load(w, i);
+    Elt<T>::store(y, i, q);
+  }
+}
+
+#define NK_RMS_REG(T, tn, B, C)                                                     \
+  extern "C" __global__ __launch_bounds__(B) void nk_rmsnorm_reg_##tn##_b##B##_c##C( \
+      RmsNormArgs a) {                                                              \
+    rmsnorm_reg_body<T, B, C>(a);                                                   \
+  }
+#define NK_RMS_LOOP(T, tn)                                                           \
+  extern "C" __global__ __launch_bounds__(256) void nk_rmsnorm_loop_##tn(RmsNormArgs a) { \
+    rmsnorm_loop_body<T, 256>(a);                                                   \
+  }
+#define NK_RMS_ALL(T, tn) \
+  NK_RMS_REG(T, tn, 64, 1)  \
+  NK_RMS_REG(T, tn, 256, 1) \
+  NK_RMS_REG(T, tn, 256, 2) \
+  NK_RMS_REG(T, tn, 512, 1) \
+  NK_RMS_REG(T, tn, 256, 4) \
+  NK_RMS_REG(T, tn, 512, 4) \
+  NK_RMS_LOOP(T, tn)
+
+NK_RMS_ALL(float, f32)
+NK_RMS_ALL(bf16, bf16)
+NK_RMS_ALL(f16, f16)

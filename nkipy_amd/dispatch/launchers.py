@@ -1,0 +1,197 @@
+"""Host-side launchers of the hand-written gfx950 kernels.
+
+Each launcher checks operand shapes / dtypes / alignment on the host, picks a
+kernel variant and a launch shape, and packs the kernel's argument struct.
+It returns a :class:`Launch` -- nothing here touches device memory -- so the
+same code serves direct calls, compiled kernel plans and the benchmark.
+Argument structs mirror the C structs in ``csrc/kernels/*.hip`` field by
+field; the kernel manifest's ``kernarg_size`` is checked at launch.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+from typing import Tuple
+
+import numpy as np
+
+from nkipy_amd.core import dtypes as dt
+
+
+class LaunchError(ValueError):
+    """Operands do not fit what a kernel and its grid assume."""
+
+
+@dataclass
+class Launch:
+    module: str
+    symbol: str
+    grid: Tuple[int, int, int]
+    block: Tuple[int, int, int]
+    args: ctypes.Structure
+    shared: int = 0
+    # algorithmic work of this launch, for roofline reporting
+    bytes: int = 0
+    flops: int = 0
+    note: str = ""
+    extra: dict = field(default_factory=dict)
+
+    def function(self, rt):
+        return rt.function(self.module, self.symbol)
+
+    def run(self, rt):
+        self.function(rt).launch(self.grid, self.block, self.args, self.shared)
+
+
+# dtype tag used in kernel symbol names
+_TAG = {
+    dt.float32: "f32",
+    dt.bfloat16: "bf16",
+    dt.float16: "f16",
+}
+
+
+def dtype_tag(d) -> str:
+    d = dt.canonical(d)
+    try:
+        return _TAG[d]
+    except KeyError:
+        raise LaunchError(f"dtype {dt.name(d)} has no kernel variant") from None
+
+
+# ---------------------------------------------------------------------------
+# Row softmax
+# ---------------------------------------------------------------------------
+class SoftmaxArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("rows", ctypes.c_int64),
+        ("n", ctypes.c_int32),
+        ("pad", ctypes.c_int32),
+    ]
+
+
+# (block, chunks) register variants: a row of up to block*chunks*8 elements
+_ROW_REG_VARIANTS = [(64, 1), (256, 1), (256, 2), (256, 4), (512, 4)]
+_SOFTMAX_TYPES = {("f32", "f32"), ("bf16", "bf16"), ("bf16", "f32"), ("f32", "bf16"), ("f16", "f16")}
+
+
+def _row_variant(n: int, elem_bytes: int, ptr_align_ok: bool):
+    """Pick the register-resident variant for a row of n elements, or None."""
+    if n % 8 != 0 or not ptr_align_ok:
+        return None
+    for block, chunks in _ROW_REG_VARIANTS:
+        if n <= block * chunks * 8:
+            # do not leave most of a large block idle
+            return block, chunks
+    return None
+
+
+def softmax_rows(x_ptr: int, y_ptr: int, rows: int, n: int, in_dtype, out_dtype) -> Launch:
+    """y[r, :] = softmax(x[r, :]) over rows of n contiguous elements."""
+    ti, to = dtype_tag(in_dtype), dtype_tag(out_dtype)
+    if (ti, to) not in _SOFTMAX_TYPES:
+        raise LaunchError(f"softmax has no {ti}->{to} variant")
+    if rows <= 0 or n <= 0:
+        raise LaunchError(f"softmax needs rows > 0 and n > 0, got rows={rows}, n={n}")
+    if rows >= 2**31:
+        raise LaunchError("softmax: too many rows for one launch")
+    aligned = x_ptr % 16 == 0 and y_ptr % 16 == 0
+    var = _row_variant(n, dt.itemsize(in_dtype), aligned)
+    args = SoftmaxArgs(x_ptr, y_ptr, rows, n, 0)
+    nbytes = rows * n * (dt.itemsize(in_dtype) + dt.itemsize(out_dtype))
+    if var is None:
+        return Launch("rowwise", f"nk_softmax_loop_{ti}_{to}", (rows, 1, 1), (256, 1, 1),
+                      args, bytes=nbytes, note="loop")
+    block, chunks = var
+    return Launch("rowwise", f"nk_softmax_reg_{ti}_{to}_b{block}_c{chunks}",
+                  (rows, 1, 1), (block, 1, 1), args, bytes=nbytes)
+
+
+# ---------------------------------------------------------------------------
+# Residual + RMSNorm
+# ---------------------------------------------------------------------------
+class RmsNormArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("r", ctypes.c_void_p),
+        ("w", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("h", ctypes.c_void_p),
+        ("rows", ctypes.c_int64),
+        ("n", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+        ("flags", ctypes.c_int32),
+        ("pad", ctypes.c_int32),
+    ]
+
+
+RMS_RES = 1
+RMS_ROUND_H = 2
+RMS_WRITE_H = 4
+RMS_MUL_RECIP = 8
+RMS_W = 16
+
+_RMS_REG_VARIANTS = [(64, 1), (256, 1), (256, 2), (512, 1), (256, 4), (512, 4)]
+
+
+def rmsnorm_rows(x_ptr: int, y_ptr: int, rows: int, n: int, dtype, eps: float,
+                 r_ptr: int = 0, w_ptr: int = 0, h_ptr: int = 0,
+                 round_h: bool = True, mul_recip: bool = False,
+                 block_chunks=None) -> Launch:
+    """y = h / sqrt(mean(h*h) + eps) * w with h = x (+ r), rows of n elements.
+
+    Every operand has the storage dtype ``dtype``; ``w`` has n elements.
+    ``round_h`` rounds x + r to ``dtype`` before use (the add happened in the
+    storage dtype); ``mul_recip`` multiplies by 1/sqrt instead of dividing.
+    """
+    tag = dtype_tag(dtype)
+    if rows <= 0 or n <= 0:
+        raise LaunchError(f"rmsnorm needs rows > 0 and n > 0, got rows={rows}, n={n}")
+    if rows >= 2**31:
+        raise LaunchError("rmsnorm: too many rows for one launch")
+    flags = 0
+    if r_ptr:
+        flags |= RMS_RES
+        if round_h:
+            flags |= RMS_ROUND_H
+        if h_ptr:
+            flags |= RMS_WRITE_H
+    elif h_ptr:
+        raise LaunchError("rmsnorm: h output requested without a residual")
+    if w_ptr:
+        flags |= RMS_W
+    if mul_recip:
+        flags |= RMS_MUL_RECIP
+    ptrs = [p for p in (x_ptr, y_ptr, r_ptr, w_ptr, h_ptr) if p]
+    aligned = all(p % 16 == 0 for p in ptrs)
+    isz = dt.itemsize(dtype)
+    nbytes = rows * n * isz * (2 + (1 if r_ptr else 0) + (1 if h_ptr else 0)) + (n * isz if w_ptr else 0)
+    args = RmsNormArgs(x_ptr, r_ptr or None, w_ptr or None, y_ptr, h_ptr or None,
+                       rows, n, float(eps), flags, 0)
+    var = None
+    if n % 8 == 0 and aligned:
+        if block_chunks is not None:
+            var = block_chunks
+            if n > var[0] * var[1] * 8:
+                raise LaunchError(f"rmsnorm variant {var} too small for n={n}")
+        else:
+            for b, c in _RMS_REG_VARIANTS:
+                if n <= b * c * 8:
+                    var = (b, c)
+                    break
+    if var is None:
+        return Launch("rowwise", f"nk_rmsnorm_loop_{tag}", (rows, 1, 1), (256, 1, 1), args,
+                      bytes=nbytes, note="loop")
+    b, c = var
+    return Launch("rowwise", f"nk_rmsnorm_reg_{tag}_b{b}_c{c}", (rows, 1, 1), (b, 1, 1), args,
+                  bytes=nbytes)
+
+
+def as_ptr(a) -> int:
+    """Device address of a DeviceTensor-like object or an int."""
+    if isinstance(a, (int, np.integer)):
+        return int(a)
+    return int(a.ptr)
