@@ -103,6 +103,7 @@ def read_kernel_metadata(hsaco: Path) -> dict:
     txt = _run([readelf, "--notes", str(hsaco)]).stdout
     kernels = {}
     cur = {}
+    arg = {}
     keys = {
         ".kernarg_segment_size": "kernarg_size",
         ".vgpr_count": "vgpr",
@@ -119,7 +120,16 @@ def read_kernel_metadata(hsaco: Path) -> dict:
             continue
         k, _, v = line.partition(":")
         k, v = k.strip(), v.strip()
-        if k in keys:
+        # explicit (non-hidden) argument bytes: what the caller packs
+        if k in (".offset", ".size"):
+            arg[k] = int(v)
+        elif k == ".value_kind":
+            if not v.startswith("hidden_") and ".offset" in arg and ".size" in arg:
+                cur["explicit_size"] = max(cur.get("explicit_size", 0), arg[".offset"] + arg[".size"])
+            if v.startswith("hidden_"):
+                cur["hidden_args"] = True
+            arg = {}
+        elif k in keys:
             try:
                 cur[keys[k]] = int(v)
             except ValueError:
@@ -128,6 +138,7 @@ def read_kernel_metadata(hsaco: Path) -> dict:
             cur["name"] = v
         # Keys are emitted in sorted order; .wavefront_size closes an entry.
         if k == ".wavefront_size" and "name" in cur:
+            cur.setdefault("explicit_size", 0)
             kernels[cur.pop("name")] = cur
             cur = {}
     return kernels

@@ -1,0 +1,1 @@
+"""Tracer front end: tensor refs, op registry, IR and NKIPyKernel."""

@@ -101,18 +101,21 @@ def is_bool(d) -> bool:
 # ---------------------------------------------------------------------------
 def f32_to_bf16_bits(a) -> np.ndarray:
     """uint16 bit patterns of float32 values rounded to bf16 (RNE, quiet NaN)."""
-    a = np.ascontiguousarray(a, dtype=np.float32)
-    u = a.view(np.uint32).astype(np.uint64)
+    a = np.asarray(a, dtype=np.float32)
+    shape = a.shape
+    u = np.ascontiguousarray(a).reshape(-1).view(np.uint32).astype(np.uint64)
     nan = (u & 0x7FFFFFFF) > 0x7F800000
     r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
     if nan.any():
         r = np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
-    return r
+    return r.reshape(shape)
 
 
 def bf16_bits_to_f32(b) -> np.ndarray:
-    b = np.ascontiguousarray(b).view(np.uint16)
-    return (b.astype(np.uint32) << 16).view(np.float32)
+    b = np.asarray(b)
+    shape = b.shape
+    b = np.ascontiguousarray(b).reshape(-1).view(np.uint16)
+    return (b.astype(np.uint32) << 16).view(np.float32).reshape(shape)
 
 
 def round_to_bf16(a) -> np.ndarray:
@@ -130,7 +133,8 @@ def to_bf16(a) -> np.ndarray:
 def bf16_to_f32(a) -> np.ndarray:
     if HAVE_ML_DTYPES:  # pragma: no cover
         return np.asarray(a).astype(np.float32)
-    return bf16_bits_to_f32(np.ascontiguousarray(a).view(np.uint16))
+    a = np.asarray(a)
+    return bf16_bits_to_f32(np.ascontiguousarray(a).reshape(-1).view(np.uint16)).reshape(a.shape)
 
 
 # ---------------------------------------------------------------------------
@@ -156,7 +160,8 @@ E4M3FN_MAX = 448.0
 
 
 def e4m3fn_bits_to_f32(b) -> np.ndarray:
-    return E4M3FN_VALUES[np.ascontiguousarray(b).view(np.uint8)]
+    b = np.asarray(b)
+    return E4M3FN_VALUES[np.ascontiguousarray(b).reshape(-1).view(np.uint8)].reshape(b.shape)
 
 
 def f32_to_e4m3fn_bits(a, saturate: bool = True) -> np.ndarray:

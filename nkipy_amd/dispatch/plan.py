@@ -1,0 +1,213 @@
+"""Kernel plans: the lowered form of a traced graph.
+
+A :class:`Plan` is a list of :class:`Step` objects over a set of device
+buffers.  Buffers are the kernel's inputs and outputs (bound per call to
+the caller's device tensors), temporaries (allocated once per loaded
+kernel) and constants (uploaded once).  Each graph value that is
+materialised lives in a :class:`Slot` -- a buffer plus a byte offset; a
+reshape shares its operand's slot.
+
+A step turns slot addresses into :class:`~nkipy_amd.dispatch.launchers.Launch`
+objects.  :class:`PlanExecutor` binds a plan to concrete buffers once per
+distinct set of argument addresses and replays the packed launches with a
+single ``nkh_launch_batch`` call, so the per-call host cost does not grow
+with argument validation or Python dispatch (the per-call work the
+reference does in SpikeModel.__call__, spike/src/spike/spike_model.py:228-268).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+from typing import Callable, Dict, List, Optional
+
+import numpy as np
+
+from nkipy_amd.core import dtypes as dt
+from nkipy_amd.core.backend.ir import Graph, Value
+from nkipy_amd.dispatch.launchers import Launch
+
+
+@dataclass
+class BufferSpec:
+    index: int
+    nbytes: int
+    kind: str  # "input" | "output" | "temp" | "const"
+    name: str = ""
+    data: Optional[np.ndarray] = None  # constant payload (raw bytes view)
+
+
+@dataclass
+class Slot:
+    buffer: int
+    offset: int = 0
+
+
+class Step:
+    """One lowered unit of work: one or more kernel launches."""
+
+    kind = "step"
+
+    def __init__(self, desc: str, inputs: List[Value], outputs: List[Value]):
+        self.desc = desc
+        self.inputs = inputs
+        self.outputs = outputs
+
+    def launches(self, addr: Callable[[Value], int]) -> List[Launch]:
+        raise NotImplementedError
+
+    def describe(self) -> dict:
+        return {
+            "kind": self.kind,
+            "desc": self.desc,
+            "inputs": [repr(v) for v in self.inputs],
+            "outputs": [repr(v) for v in self.outputs],
+        }
+
+
+@dataclass
+class Plan:
+    graph: Graph
+    buffers: List[BufferSpec] = field(default_factory=list)
+    slots: Dict[int, Slot] = field(default_factory=dict)
+    steps: List[Step] = field(default_factory=list)
+    # name -> buffer index
+    input_buffers: Dict[str, int] = field(default_factory=dict)
+    output_buffers: Dict[str, int] = field(default_factory=dict)
+    # output name -> input name whose buffer it must reuse (aliasing)
+    alias_outputs: Dict[str, str] = field(default_factory=dict)
+
+    def add_buffer(self, nbytes: int, kind: str, name: str = "", data=None) -> int:
+        b = BufferSpec(len(self.buffers), int(nbytes), kind, name, data)
+        self.buffers.append(b)
+        return b.index
+
+    def slot(self, v: Value) -> Slot:
+        try:
+            return self.slots[v.id]
+        except KeyError:
+            raise KeyError(f"value {v!r} has no storage in the plan") from None
+
+    @property
+    def kernel_kinds(self) -> List[str]:
+        return [s.kind for s in self.steps]
+
+    def describe(self) -> dict:
+        return {
+            "graph": self.graph.name,
+            "buffers": [
+                {"index": b.index, "kind": b.kind, "name": b.name, "nbytes": b.nbytes}
+                for b in self.buffers
+            ],
+            "steps": [s.describe() for s in self.steps],
+        }
+
+    def summary(self) -> str:
+        lines = [f"plan {self.graph.name}: {len(self.steps)} steps, "
+                 f"{sum(1 for b in self.buffers if b.kind == 'temp')} temporaries"]
+        for s in self.steps:
+            lines.append(f"  [{s.kind}] {s.desc}")
+        return "\n".join(lines)
+
+
+class BoundPlan:
+    """Launches of a plan with every address resolved, packed for replay."""
+
+    def __init__(self, launches: List[Launch], rt):
+        self.launches = launches
+        self.rt = rt
+        n = len(launches)
+        fns = [l.function(rt) for l in launches]
+        blobs = []
+        for f, l in zip(fns, launches):
+            f.check_block(l.block)
+            blobs.append(f.check_args(l.args))
+        offsets, off = [], 0
+        for b in blobs:
+            offsets.append(off)
+            off += (len(b) + 15) // 16 * 16
+        buf = bytearray(off)
+        for o, b in zip(offsets, blobs):
+            buf[o:o + len(b)] = b
+        vp = ctypes.c_void_p
+        u = ctypes.c_uint
+        sz = ctypes.c_size_t
+        self._n = n
+        self._fns = (vp * n)(*[f.handle for f in fns])
+        self._grids = (u * (3 * n))(*[g for l in launches for g in l.grid])
+        self._blocks = (u * (3 * n))(*[b for l in launches for b in l.block])
+        self._shared = (u * n)(*[l.shared for l in launches])
+        self._kernargs = bytes(buf)
+        self._offsets = (sz * n)(*offsets)
+        self._sizes = (sz * n)(*[len(b) for b in blobs])
+
+    def run(self):
+        from nkipy_amd.runtime.hip import _check
+
+        if self._n == 0:
+            return
+        _check(
+            self.rt.lib.nkh_launch_batch(
+                self._n, self._fns, self._grids, self._blocks, self._shared,
+                self._kernargs, self._offsets, self._sizes,
+            ),
+            "plan launch",
+        )
+
+
+class PlanExecutor:
+    """Owns a plan's temporaries and constants and runs it on bound I/O."""
+
+    def __init__(self, plan: Plan):
+        from nkipy_amd.runtime.device_tensor import DeviceBuffer
+        from nkipy_amd.runtime.hip import get_runtime
+
+        self.plan = plan
+        self.rt = get_runtime()
+        self._owned: Dict[int, DeviceBuffer] = {}
+        for b in plan.buffers:
+            if b.kind in ("temp", "const"):
+                buf = DeviceBuffer(max(b.nbytes, 16), name=f"{plan.graph.name}:{b.kind}{b.index}")
+                if b.kind == "const" and b.data is not None and b.data.nbytes:
+                    raw = np.ascontiguousarray(dt.numpy_storage(np.ascontiguousarray(b.data)))
+                    buf.write(raw.ctypes.data, raw.nbytes)
+                self._owned[b.index] = buf
+        self._bound: Dict[tuple, BoundPlan] = {}
+
+    def _bind(self, bases: Dict[int, int]) -> BoundPlan:
+        plan = self.plan
+
+        def addr(v: Value) -> int:
+            s = plan.slot(v)
+            return bases[s.buffer] + s.offset
+
+        launches: List[Launch] = []
+        for st in plan.steps:
+            launches.extend(st.launches(addr))
+        return BoundPlan(launches, self.rt)
+
+    def bind(self, io_ptrs: Dict[str, int]) -> BoundPlan:
+        """``io_ptrs``: input / output name -> device address."""
+        plan = self.plan
+        bases: Dict[int, int] = {i: b.ptr for i, b in self._owned.items()}
+        for name, idx in plan.input_buffers.items():
+            bases[idx] = io_ptrs[name]
+        for name, idx in plan.output_buffers.items():
+            bases[idx] = io_ptrs[name]
+        key = tuple(sorted((k, v) for k, v in io_ptrs.items()))
+        bp = self._bound.get(key)
+        if bp is None:
+            if len(self._bound) > 64:
+                self._bound.clear()
+            bp = self._bind(bases)
+            self._bound[key] = bp
+        return bp
+
+    def run(self, io_ptrs: Dict[str, int]):
+        self.bind(io_ptrs).run()
+
+    def close(self):
+        for b in self._owned.values():
+            b.free()
+        self._owned.clear()
+        self._bound.clear()

@@ -1,0 +1,9 @@
+"""NumPy kernels of the hot path, written the way NKIPy kernels are written:
+plain NumPy functions that run on the CPU when called directly and are
+traced onto the gfx950 kernels under ``trace`` / ``baremetal_jit`` /
+``DeviceKernel``.  They follow the reference's example kernels (cited per
+function) and the workloads of the backend's benchmark.
+"""
+
+from nkipy_amd.kernels.softmax import softmax_kernel, softmax_upcast_kernel  # noqa: F401
+from nkipy_amd.kernels.rmsnorm import residual_rmsnorm_kernel, rmsnorm_kernel  # noqa: F401

@@ -1,0 +1,14 @@
+"""Device runtime: tensors, loaded kernels and the jit entry points."""
+
+from nkipy_amd.runtime.decorators import baremetal_jit
+from nkipy_amd.runtime.device_kernel import BenchmarkResult, DeviceKernel
+from nkipy_amd.runtime.device_tensor import DeviceTensor
+from nkipy_amd.runtime.execute import baremetal_run_traced_kernel
+from nkipy_amd.runtime.hip import HipError, NrtError, SpikeError, SpikeRuntimeError
+from nkipy_amd.runtime.utils import is_gpu_available, is_neuron_compatible
+
+__all__ = [
+    "baremetal_jit", "baremetal_run_traced_kernel", "BenchmarkResult", "DeviceKernel",
+    "DeviceTensor", "HipError", "NrtError", "SpikeError", "SpikeRuntimeError",
+    "is_gpu_available", "is_neuron_compatible",
+]

@@ -194,7 +194,12 @@ class Function:
         self.name = name
         self.handle = handle
         self.meta = meta
-        self.kernarg_size = int(meta["kernarg_size"])
+        self.kernarg_size = int(meta.get("explicit_size", meta["kernarg_size"]))
+        if meta.get("hidden_args"):
+            raise KernelArgumentError(
+                f"kernel '{name}' uses hidden (implicit) arguments; kernels launched "
+                "through packed argument blocks must not read gridDim/blockDim"
+            )
         self.max_block = int(meta.get("max_block", 1024))
 
     def check_args(self, args) -> bytes:

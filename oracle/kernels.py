@@ -1,0 +1,169 @@
+"""NumPy restatements of the reference's CPU path for the hot-path kernels
+(test infrastructure only; see oracle/__init__.py).
+
+``*_kernel`` functions are the float32 NumPy formulas the reference runs on
+the CPU; ``*_f64`` functions are float64 brute-force forms used to pin them.
+bf16 inputs are float32 arrays holding bf16-rounded values.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from oracle.numerics import bf16_round
+
+# ---------------------------------------------------------------------------
+# softmax -- README.md:125-128, tests/kernels/softmax.py:7-10
+# ---------------------------------------------------------------------------
+
+
+def softmax_kernel(x):
+    exp_x = np.exp(x - np.max(x, axis=-1, keepdims=True))
+    sum_x = np.sum(exp_x, axis=-1, keepdims=True)
+    return exp_x / sum_x
+
+
+def softmax_f64(x):
+    x = np.asarray(x, dtype=np.float64)
+    out = np.empty_like(x)
+    flat = x.reshape(-1, x.shape[-1])
+    o = out.reshape(-1, x.shape[-1])
+    for i, row in enumerate(flat):
+        e = np.exp(row - row.max())
+        o[i] = e / e.sum()
+    return out
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm -- examples/models/qwen3/kernels/rmsnorm.py:4-21 (cast points kept:
+# upcast to fp32, mean of squares, (z + eps) cast back to the fp32 dtype,
+# x / sqrt(z), times weight, cast to the input dtype); residual as
+# examples/models/qwen3/kernels/transformer_layer.py:60 (z = x + h1, in the
+# storage dtype).
+# ---------------------------------------------------------------------------
+
+
+def rmsnorm_kernel(x, weight, eps, compute_dtype=np.float32, round_out=None):
+    x = np.asarray(x).astype(compute_dtype)
+    weight = np.asarray(weight).astype(compute_dtype)
+    z = np.square(x)
+    z = np.mean(z, axis=-1, keepdims=True)
+    z = (z + np.float32(eps)).astype(x.dtype)
+    z = x / np.sqrt(z)
+    res = z * weight
+    return round_out(res) if round_out is not None else res
+
+
+def residual_rmsnorm_bf16(x, r, weight, eps):
+    """bf16 storage: h = bf16(x + r); out = bf16(rmsnorm(h) * w)."""
+    h = bf16_round(np.asarray(x, np.float32) + np.asarray(r, np.float32))
+    return rmsnorm_kernel(h, weight, eps, round_out=bf16_round)
+
+
+def rmsnorm_f64(h, weight, eps):
+    h = np.asarray(h, dtype=np.float64)
+    ms = np.array([np.dot(row, row) / row.size for row in h.reshape(-1, h.shape[-1])])
+    ms = ms.reshape(h.shape[:-1] + (1,))
+    return h / np.sqrt(ms + eps) * np.asarray(weight, np.float64)
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU feed-forward -- examples/models/qwen3/kernels/feedforward.py:4-18
+# (silu(x) = x * (1 / (1 + exp(-x))); gate_up fused then split), bias variant
+# examples/models/qwen3_embedding/kernels/ffn.py:11-46.
+# ---------------------------------------------------------------------------
+
+
+def silu(x):
+    return x * (1 / (1 + np.exp(-x)))
+
+
+def swiglu_mlp(x, w_gate, w_up, w_down, round_h=None):
+    x = np.asarray(x, np.float32)
+    g = x @ np.asarray(w_gate, np.float32)
+    u = x @ np.asarray(w_up, np.float32)
+    h = silu(g) * u
+    if round_h is not None:
+        h = round_h(h)
+    return h @ np.asarray(w_down, np.float32)
+
+
+def feedforward_fused(x, gate_up, down, gate_up_bias=None, down_bias=None):
+    mm = np.asarray(x, np.float32) @ np.asarray(gate_up, np.float32)
+    if gate_up_bias is not None:
+        mm = mm + gate_up_bias
+    g, u = np.split(mm, 2, axis=-1)
+    out = (silu(g) * u) @ np.asarray(down, np.float32)
+    if down_bias is not None:
+        out = out + down_bias
+    return out
+
+
+def matmul_f64(a, b):
+    """Textbook triple loop (tiny shapes only)."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    M, K = a.shape
+    K2, N = b.shape
+    assert K == K2
+    c = np.zeros((M, N))
+    for i in range(M):
+        for j in range(N):
+            s = 0.0
+            for k in range(K):
+                s += a[i, k] * b[k, j]
+            c[i, j] = s
+    return c
+
+
+# ---------------------------------------------------------------------------
+# Chunked causal linear attention.  Nothing in the reference computes it;
+# the nearest analogue is the recurrent DeltaNet kernel
+# (examples/linear_attention/deltanet.py:74-128).  Feature map phi = elu + 1.
+#   o_t = phi(q_t)^T S_t / (phi(q_t)^T z_t),
+#   S_t = sum_{s<=t} phi(k_s) v_s^T,  z_t = sum_{s<=t} phi(k_s)
+# ---------------------------------------------------------------------------
+
+
+def elu_plus_one(x):
+    x = np.asarray(x)
+    return np.where(x > 0, x + 1, np.exp(np.minimum(x, 0)))
+
+
+def linear_attention_chunked(q, k, v, chunk=64):
+    """Chunk-by-chunk recurrence with an fp32 d x d state per head:
+    inter-chunk phi(Q) S_prev plus the masked intra-chunk (phi(Q) phi(K)^T) V."""
+    q = np.asarray(q, np.float32)
+    k = np.asarray(k, np.float32)
+    v = np.asarray(v, np.float32)
+    B, H, T, D = q.shape
+    assert T % chunk == 0
+    qf, kf = elu_plus_one(q).astype(np.float32), elu_plus_one(k).astype(np.float32)
+    out = np.empty((B, H, T, v.shape[-1]), np.float32)
+    mask = np.tril(np.ones((chunk, chunk), np.float32))
+    for b in range(B):
+        for h in range(H):
+            S = np.zeros((D, v.shape[-1]), np.float32)
+            z = np.zeros(D, np.float32)
+            for c0 in range(0, T, chunk):
+                Q = qf[b, h, c0:c0 + chunk]
+                K = kf[b, h, c0:c0 + chunk]
+                V = v[b, h, c0:c0 + chunk]
+                A = (Q @ K.T) * mask
+                num = Q @ S + A @ V
+                den = Q @ z + A.sum(axis=1)
+                out[b, h, c0:c0 + chunk] = num / den[:, None]
+                S = S + K.T @ V
+                z = z + K.sum(axis=0)
+    return out
+
+
+def linear_attention_quadratic_f64(q, k, v):
+    """O(T^2) masked form in float64 (tiny T)."""
+    qf = elu_plus_one(np.asarray(q, np.float64))
+    kf = elu_plus_one(np.asarray(k, np.float64))
+    v = np.asarray(v, np.float64)
+    T = q.shape[-2]
+    mask = np.tril(np.ones((T, T)))
+    A = np.einsum("bhtd,bhsd->bhts", qf, kf) * mask
+    return np.einsum("bhts,bhsd->bhtd", A, v) / A.sum(-1, keepdims=True)

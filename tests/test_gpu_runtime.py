@@ -1,0 +1,93 @@
+"""Native runtime error paths forced from the host (bounds, lifetime, bad code
+objects, unknown symbols, argument-size mismatch) and basic device I/O."""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from nkipy_amd.core import dtypes as dt
+from nkipy_amd.dispatch import launchers as LA
+from nkipy_amd.runtime import DeviceTensor, SpikeError
+from nkipy_amd.runtime.hip import HipError, KernelArgumentError
+
+pytestmark = pytest.mark.gpu
+
+
+def test_roundtrip_dtypes(gpu):
+    for arr in [np.arange(10, dtype=np.float32), np.arange(6, dtype=np.int32).reshape(2, 3),
+                dt.to_bf16(np.linspace(-2, 2, 9, dtype=np.float32)), np.array([True, False])]:
+        t = DeviceTensor.from_numpy(arr, name="t")
+        back = t.numpy()
+        assert back.dtype == arr.dtype and back.shape == arr.shape
+        np.testing.assert_array_equal(dt.numpy_storage(back), dt.numpy_storage(arr))
+
+
+def test_torch_roundtrip(gpu):
+    import torch
+
+    x = torch.randn(4, 5).to(torch.bfloat16)
+    t = DeviceTensor.from_torch(x, name="x")
+    assert t.dtype == dt.bfloat16
+    assert torch.equal(t.torch(), x)
+    t.write_from_torch(x * 2)
+    assert torch.equal(t.torch(), x * 2)
+
+
+def test_write_size_mismatch(gpu):
+    t = DeviceTensor.from_numpy(np.zeros(4, np.float32))
+    with pytest.raises(ValueError):
+        t.write_from_numpy(np.zeros(5, np.float32))
+
+
+def test_out_of_bounds_copy_is_rejected(gpu):
+    t = DeviceTensor.from_numpy(np.zeros(4, np.float32))
+    buf = np.zeros(8, np.float32)
+    with pytest.raises(SpikeError, match="bound"):
+        t.tensor_ref.write(buf.ctypes.data, buf.nbytes)
+    # past the end through the native bounds check too
+    with pytest.raises(SpikeError, match="bound"):
+        gpu.h2d(t.ptr + 8, buf.ctypes.data, 16)
+
+
+def test_use_after_free(gpu):
+    t = DeviceTensor.from_numpy(np.zeros(4, np.float32))
+    ptr = t.ptr
+    t.free()
+    with pytest.raises(SpikeError, match="freed"):
+        t.numpy()
+    with pytest.raises(SpikeError):
+        gpu.free(ptr)  # double free rejected natively
+
+
+def test_unknown_symbol_and_bad_code_object(gpu, tmp_path):
+    with pytest.raises(SpikeError):
+        gpu.function("rowwise", "nk_does_not_exist")
+    bad = tmp_path / "bad.hsaco"
+    bad.write_bytes(b"not an elf")
+    h = ctypes.c_void_p()
+    rc = gpu.lib.nkh_module_load(str(bad).encode(), ctypes.byref(h))
+    assert rc != 0
+    rc = gpu.lib.nkh_module_load(str(tmp_path / "missing.hsaco").encode(), ctypes.byref(h))
+    assert rc != 0 and b"not found" in gpu.lib.nkh_last_error()
+
+
+def test_kernel_argument_size_mismatch(gpu):
+    f = gpu.function("rowwise", "nk_softmax_reg_f32_f32_b256_c2")
+    with pytest.raises(KernelArgumentError):
+        f.launch((1, 1, 1), (256, 1, 1), b"\x00" * 8)
+    with pytest.raises(KernelArgumentError):
+        f.launch((1, 1, 1), (1024, 1, 1), LA.SoftmaxArgs())
+
+
+def test_launch_rejects_bad_shapes_on_host():
+    with pytest.raises(LA.LaunchError):
+        LA.softmax_rows(0, 0, 0, 10, dt.float32, dt.float32)
+    with pytest.raises(LA.LaunchError):
+        LA.rmsnorm_rows(0, 0, 4, 16, dt.float32, 1e-6, h_ptr=16)
+
+
+def test_device_info(gpu):
+    info = gpu.device_info()
+    assert info["arch"].startswith("gfx950")
+    assert info["cu_count"] > 0

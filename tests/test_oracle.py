@@ -1,0 +1,135 @@
+"""Pins of the CPU oracle: reference golden vectors, closed forms, float64
+brute force and invariants chosen so that a dropped term, a wrong sign or a
+transposed operand fails at least one check."""
+
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kernels as K
+from oracle import numerics as N
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def test_softmax_notebook_golden_vectors():
+    data = json.load(open(os.path.join(GOLDEN, "softmax_notebooks.json")))
+    for case in data["cases"]:
+        x = np.array(case["input"], np.float32)
+        np.testing.assert_allclose(K.softmax_kernel(x), case["output"], rtol=0, atol=2e-7 * 5)
+
+
+def test_softmax_matches_f64_and_invariants():
+    rng = np.random.default_rng(0)
+    x = (rng.standard_normal((64, 333)) * 4).astype(np.float32)
+    y = K.softmax_kernel(x)
+    ref = K.softmax_f64(x)
+    assert np.max(np.abs(y - ref) / ref) < 1e-5
+    np.testing.assert_allclose(y.sum(-1), 1.0, atol=1e-5)
+    np.testing.assert_allclose(K.softmax_kernel(x + np.float32(7.25)), y, rtol=2e-5, atol=1e-7)
+    # the max-subtraction matters: large inputs stay finite
+    assert np.isfinite(K.softmax_kernel(x * 100)).all()
+
+
+def test_rmsnorm_closed_form_and_invariants():
+    rng = np.random.default_rng(1)
+    h = rng.standard_normal((16, 96)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 96).astype(np.float32)
+    y = K.rmsnorm_kernel(h, w, 1e-6)
+    np.testing.assert_allclose(y, K.rmsnorm_f64(h, w, 1e-6), rtol=2e-6, atol=1e-6)
+    # scale invariance (eps negligible) and linearity in w
+    np.testing.assert_allclose(K.rmsnorm_kernel(h * 3.0, w, 1e-12), K.rmsnorm_kernel(h, w, 1e-12), rtol=1e-5)
+    np.testing.assert_allclose(K.rmsnorm_kernel(h, 2 * w, 1e-6), 2 * y, rtol=1e-6)
+    # rows of constant magnitude c normalise to +-w
+    s = np.sign(rng.standard_normal((4, 96))).astype(np.float32)
+    np.testing.assert_allclose(K.rmsnorm_kernel(3.5 * s, w, 0.0), s * w, rtol=1e-6)
+
+
+def test_residual_rmsnorm_rounds_the_sum_in_bf16():
+    rng = np.random.default_rng(2)
+    x = N.bf16_round(rng.standard_normal((8, 64)))
+    r = N.bf16_round(rng.standard_normal((8, 64)))
+    w = N.bf16_round(rng.uniform(0.5, 1.5, 64))
+    y = K.residual_rmsnorm_bf16(x, r, w, 1e-6)
+    h = N.bf16_round(x + r)
+    # outputs are bf16 values within one bf16 rounding of the float64 form
+    np.testing.assert_array_equal(y, N.bf16_round(y))
+    assert np.max(np.abs(y - K.rmsnorm_f64(h, w, 1e-6)) / (np.abs(K.rmsnorm_f64(h, w, 1e-6)) + 1e-3)) < 8e-3
+
+
+def test_swiglu_brute_force_and_special_cases():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((3, 5)).astype(np.float32)
+    wg, wu = rng.standard_normal((5, 4)).astype(np.float32), rng.standard_normal((5, 4)).astype(np.float32)
+    wd = rng.standard_normal((4, 6)).astype(np.float32)
+    g, u = K.matmul_f64(x, wg), K.matmul_f64(x, wu)
+    h = g / (1 + np.exp(-g)) * u
+    ref = K.matmul_f64(h, wd)
+    np.testing.assert_allclose(K.swiglu_mlp(x, wg, wu, wd), ref, rtol=1e-5, atol=1e-5)
+    # fused gate_up + split equals the two-weight form
+    np.testing.assert_allclose(K.feedforward_fused(x, np.concatenate([wg, wu], 1), wd), ref, rtol=1e-5, atol=1e-5)
+    # K = 1 and identity weights
+    x1 = rng.standard_normal((4, 1)).astype(np.float32)
+    w1 = rng.standard_normal((1, 3)).astype(np.float32)
+    np.testing.assert_allclose(K.matmul_f64(x1, w1), x1.astype(np.float64) * w1, rtol=1e-12)
+    eye = np.eye(5, dtype=np.float32)
+    np.testing.assert_allclose(K.matmul_f64(x, eye), x, rtol=1e-12)
+    # silu: silu(0) = 0, silu(x) - silu(-x) = x
+    np.testing.assert_allclose(K.silu(np.float32(0)), 0)
+    np.testing.assert_allclose(K.silu(x) - K.silu(-x), x, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("chunk", [4, 8, 16])
+def test_linear_attention_chunked_equals_quadratic(chunk):
+    rng = np.random.default_rng(4)
+    q, k, v = [(rng.standard_normal((2, 3, 16, 8)) / np.sqrt(8)).astype(np.float32) for _ in range(3)]
+    ref = K.linear_attention_quadratic_f64(q, k, v)
+    np.testing.assert_allclose(K.linear_attention_chunked(q, k, v, chunk), ref, rtol=2e-5, atol=2e-6)
+
+
+def test_linear_attention_quadratic_brute_force():
+    rng = np.random.default_rng(5)
+    q, k, v = [rng.standard_normal((1, 1, 6, 3)) for _ in range(3)]
+    phi = lambda a: np.where(a > 0, a + 1, np.exp(a))
+    out = np.zeros((6, 3))
+    for t in range(6):
+        wts = np.array([phi(q[0, 0, t]) @ phi(k[0, 0, s]) for s in range(t + 1)])
+        out[t] = (wts[:, None] * v[0, 0, :t + 1]).sum(0) / wts.sum()
+    np.testing.assert_allclose(K.linear_attention_quadratic_f64(q, k, v)[0, 0], out, rtol=1e-12)
+    # the first position attends only to itself
+    np.testing.assert_allclose(K.linear_attention_quadratic_f64(q, k, v)[0, 0, 0], v[0, 0, 0], rtol=1e-12)
+
+
+def test_bf16_rounding_matches_torch():
+    rng = np.random.default_rng(6)
+    a = np.concatenate([rng.standard_normal(100000).astype(np.float32) * 1e3,
+                        np.array([0.0, -0.0, 1.0 + 2**-8, 1.0 + 3 * 2**-8, 65504.0, 1e-40], np.float32)])
+    t = torch.from_numpy(a).to(torch.bfloat16).to(torch.float32).numpy()
+    np.testing.assert_array_equal(N.bf16_round(a), t)
+
+
+def test_e4m3fn_table_and_encode_match_torch():
+    codes = np.arange(256, dtype=np.uint8)
+    t = torch.from_numpy(codes).view(torch.float8_e4m3fn).to(torch.float32).numpy()
+    same = np.isnan(t) == np.isnan(N.E4M3FN_TABLE)
+    assert same.all()
+    np.testing.assert_array_equal(N.E4M3FN_TABLE[~np.isnan(t)], t[~np.isnan(t)])
+    assert N.E4M3FN_TABLE[0x7E] == 448.0 and N.E4M3FN_TABLE[0x01] == 2.0**-9
+    rng = np.random.default_rng(7)
+    a = (rng.standard_normal(50000) * 100).astype(np.float32)
+    ref = torch.from_numpy(np.clip(a, -448, 448)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(N.e4m3fn_encode(a), ref)
+
+
+def test_per_channel_quantisation_roundtrip():
+    rng = np.random.default_rng(8)
+    w = (rng.standard_normal((32, 64)) * 0.02).astype(np.float32)
+    codes, scale = N.quantize_per_channel_e4m3fn(w, axis=1)
+    assert scale.shape == (32,)
+    deq = N.dequantize_e4m3fn(codes, scale, axis=1)
+    # 3 mantissa bits: relative error of each element <= 2^-4 (+ subnormal floor)
+    assert np.all(np.abs(deq - w) <= np.abs(w) * 2.0**-4 + scale[:, None] * 2.0**-9)
+    np.testing.assert_allclose(np.abs(deq).max(1), np.abs(w).max(1), rtol=1e-6)
