@@ -55,6 +55,19 @@ NK_DEVICE float e4m3_to_f32(uint8_t b) {
   return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
 }
 
+// 128-bit nontemporal (streaming) global access: data read or written once
+// per kernel bypasses cache retention, which measurably raises achieved HBM
+// bandwidth for the row kernels.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+NK_DEVICE uint4 nt_load16(const void *p) {
+  u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
+NK_DEVICE void nt_store16(void *p, uint4 v) {
+  u32x4 t = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(t, reinterpret_cast<u32x4 *>(p));
+}
+
 // Load / store of one element, converting to / from float.
 template <typename T> struct Elt;
 template <> struct Elt<float> {
@@ -70,25 +83,43 @@ template <> struct Elt<f16> {
   static NK_DEVICE void store(f16 *p, long i, float v) { p[i].bits = f32_to_f16(v); }
 };
 
+// 16-byte global load / store, streaming (nontemporal) when NT.
+template <bool NT>
+NK_DEVICE uint4 ld16(const void *p) {
+  if (NT) return nt_load16(p);
+  return *reinterpret_cast<const uint4 *>(p);
+}
+template <bool NT>
+NK_DEVICE void st16(void *p, uint4 v) {
+  if (NT) nt_store16(p, v);
+  else *reinterpret_cast<uint4 *>(p) = v;
+}
+
 // Eight consecutive elements (16 bytes for 2-byte types, 32 bytes for fp32)
-// loaded with 128-bit accesses.  `p` must be 16-byte aligned.
+// with 128-bit accesses; `p` must be 16-byte aligned.  NT selects streaming
+// access for data touched once.
 template <typename T> struct Vec8;
 template <> struct Vec8<float> {
+  template <bool NT = false>
   static NK_DEVICE void load(const float *p, float v[8]) {
-    const float4 *q = reinterpret_cast<const float4 *>(p);
-    float4 a = q[0], b = q[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    uint4 a = ld16<NT>(p), b = ld16<NT>(p + 4);
+    v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y);
+    v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+    v[4] = __uint_as_float(b.x); v[5] = __uint_as_float(b.y);
+    v[6] = __uint_as_float(b.z); v[7] = __uint_as_float(b.w);
   }
+  template <bool NT = false>
   static NK_DEVICE void store(float *p, const float v[8]) {
-    float4 *q = reinterpret_cast<float4 *>(p);
-    q[0] = make_float4(v[0], v[1], v[2], v[3]);
-    q[1] = make_float4(v[4], v[5], v[6], v[7]);
+    st16<NT>(p, make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]),
+                           __float_as_uint(v[2]), __float_as_uint(v[3])));
+    st16<NT>(p + 4, make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]),
+                               __float_as_uint(v[6]), __float_as_uint(v[7])));
   }
 };
 template <> struct Vec8<bf16> {
+  template <bool NT = false>
   static NK_DEVICE void load(const bf16 *p, float v[8]) {
-    uint4 u = *reinterpret_cast<const uint4 *>(p);
+    uint4 u = ld16<NT>(p);
     uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -96,17 +127,19 @@ template <> struct Vec8<bf16> {
       v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
     }
   }
+  template <bool NT = false>
   static NK_DEVICE void store(bf16 *p, const float v[8]) {
     uint32_t w[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       w[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
-    *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    st16<NT>(p, make_uint4(w[0], w[1], w[2], w[3]));
   }
 };
 template <> struct Vec8<f16> {
+  template <bool NT = false>
   static NK_DEVICE void load(const f16 *p, float v[8]) {
-    uint4 u = *reinterpret_cast<const uint4 *>(p);
+    uint4 u = ld16<NT>(p);
     uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -114,14 +147,79 @@ template <> struct Vec8<f16> {
       v[2 * i + 1] = f16_to_f32((uint16_t)(w[i] >> 16));
     }
   }
+  template <bool NT = false>
   static NK_DEVICE void store(f16 *p, const float v[8]) {
     uint32_t w[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       w[i] = (uint32_t)f32_to_f16(v[2 * i]) | ((uint32_t)f32_to_f16(v[2 * i + 1]) << 16);
-    *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    st16<NT>(p, make_uint4(w[0], w[1], w[2], w[3]));
   }
 };
+
+// Raw form of an 8-element chunk: U 16-byte words (1 for 2-byte types, 2 for
+// fp32).  Kernels issue every raw load of a row first, then decode, so all
+// of a thread's HBM requests are in flight together.
+template <typename T> struct Raw8 {
+  static constexpr int U = sizeof(T) * 8 / 16;
+  uint4 w[U];
+  template <bool NT>
+  NK_DEVICE void load(const T *p) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) w[u] = ld16<NT>(reinterpret_cast<const uint8_t *>(p) + 16 * u);
+  }
+  template <bool NT>
+  NK_DEVICE void store(T *p) const {
+#pragma unroll
+    for (int u = 0; u < U; ++u) st16<NT>(reinterpret_cast<uint8_t *>(p) + 16 * u, w[u]);
+  }
+};
+
+NK_DEVICE void decode8(const Raw8<float> &r, float v[8]) {
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    v[4 * u + 0] = __uint_as_float(r.w[u].x);
+    v[4 * u + 1] = __uint_as_float(r.w[u].y);
+    v[4 * u + 2] = __uint_as_float(r.w[u].z);
+    v[4 * u + 3] = __uint_as_float(r.w[u].w);
+  }
+}
+NK_DEVICE void decode8(const Raw8<bf16> &r, float v[8]) {
+  uint32_t w[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(w[i] << 16);
+    v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+NK_DEVICE void decode8(const Raw8<f16> &r, float v[8]) {
+  uint32_t w[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = f16_to_f32((uint16_t)(w[i] & 0xffffu));
+    v[2 * i + 1] = f16_to_f32((uint16_t)(w[i] >> 16));
+  }
+}
+NK_DEVICE void encode8(const float v[8], Raw8<float> &r) {
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+    r.w[u] = make_uint4(__float_as_uint(v[4 * u]), __float_as_uint(v[4 * u + 1]),
+                        __float_as_uint(v[4 * u + 2]), __float_as_uint(v[4 * u + 3]));
+}
+NK_DEVICE void encode8(const float v[8], Raw8<bf16> &r) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
+  r.w[0] = make_uint4(w[0], w[1], w[2], w[3]);
+}
+NK_DEVICE void encode8(const float v[8], Raw8<f16> &r) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = (uint32_t)f32_to_f16(v[2 * i]) | ((uint32_t)f32_to_f16(v[2 * i + 1]) << 16);
+  r.w[0] = make_uint4(w[0], w[1], w[2], w[3]);
+}
 
 // ---------------------------------------------------------------------------
 // Reductions.  A wavefront is 64 lanes on CDNA4.

@@ -11,8 +11,10 @@
 //
 // Layout: rows of `n` contiguous elements, row-major, one workgroup per row.
 // The register variants hold the whole row in VGPRs (CHUNKS x 8 elements per
-// thread, 128-bit loads, each input byte read once from HBM); the loop
-// variants take any n and re-read the row (fallback only).
+// thread): every 16-byte streaming (nontemporal) load of the row is issued
+// before any arithmetic, so a thread's requests are all in flight together,
+// and each input byte is read from HBM once.  The loop variants take any n
+// and re-read the row (fallback only).
 // Arithmetic is fp32 whatever the storage type; exp is the accurate libm
 // expf (no exp2 shortcut) so fp32 softmax stays within 1e-5 of NumPy.
 
@@ -36,13 +38,19 @@ __device__ __forceinline__ void softmax_reg_body(const SoftmaxArgs &a) {
   const TI *x = reinterpret_cast<const TI *>(a.x) + row * n;
   TO *y = reinterpret_cast<TO *>(a.y) + row * n;
   const int tid = threadIdx.x;
+  Raw8<TI> raw[CHUNKS];
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int idx = (c * BLOCK + tid) * 8;
+    if (idx < n) raw[c].template load<true>(x + idx);
+  }
   float v[CHUNKS][8];
   float m = -INFINITY;
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
     const int idx = (c * BLOCK + tid) * 8;
     if (idx < n) {
-      Vec8<TI>::load(x + idx, v[c]);
+      decode8(raw[c], v[c]);
 #pragma unroll
       for (int j = 0; j < 8; ++j) m = fmaxf(m, v[c][j]);
     }
@@ -67,7 +75,9 @@ __device__ __forceinline__ void softmax_reg_body(const SoftmaxArgs &a) {
     if (idx < n) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) v[c][j] = v[c][j] / s;
-      Vec8<TO>::store(y + idx, v[c]);
+      Raw8<TO> o;
+      encode8(v[c], o);
+      o.template store<true>(y + idx);
     }
   }
 }
@@ -102,8 +112,10 @@ __device__ __forceinline__ void softmax_loop_body(const SoftmaxArgs &a) {
 
 #define NK_SOFTMAX_ALL(TI, TO, tin, ton) \
   NK_SOFTMAX_REG(TI, TO, tin, ton, 64, 1)  \
+  NK_SOFTMAX_REG(TI, TO, tin, ton, 128, 4) \
   NK_SOFTMAX_REG(TI, TO, tin, ton, 256, 1) \
   NK_SOFTMAX_REG(TI, TO, tin, ton, 256, 2) \
+  NK_SOFTMAX_REG(TI, TO, tin, ton, 512, 1) \
   NK_SOFTMAX_REG(TI, TO, tin, ton, 256, 4) \
   NK_SOFTMAX_REG(TI, TO, tin, ton, 512, 4) \
   NK_SOFTMAX_LOOP(TI, TO, tin, ton)
@@ -148,7 +160,9 @@ template <> __device__ __forceinline__ float round_to<f16>(float v) {
   return f16_to_f32(f32_to_f16(v));
 }
 
-template <typename T, int BLOCK, int CHUNKS>
+// RES (residual present) is a template parameter so that the residual loads
+// are issued together with the x loads, not behind a runtime branch.
+template <typename T, int BLOCK, int CHUNKS, bool RES>
 __device__ __forceinline__ void rmsnorm_reg_body(const RmsNormArgs &a) {
   __shared__ float red[BLOCK / 64];
   const int64_t row = blockIdx.x;
@@ -160,23 +174,36 @@ __device__ __forceinline__ void rmsnorm_reg_body(const RmsNormArgs &a) {
   T *y = reinterpret_cast<T *>(a.y) + row * n;
   T *h = reinterpret_cast<T *>(a.h) + row * n;
   const int tid = threadIdx.x;
+  Raw8<T> xr[CHUNKS], rr[CHUNKS];
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int idx = (c * BLOCK + tid) * 8;
+    if (idx < n) {
+      xr[c].template load<true>(x + idx);
+      if (RES) rr[c].template load<true>(r + idx);
+    }
+  }
   float v[CHUNKS][8];
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
     const int idx = (c * BLOCK + tid) * 8;
     if (idx < n) {
-      Vec8<T>::load(x + idx, v[c]);
-      if (flags & NK_RMS_RES) {
+      decode8(xr[c], v[c]);
+      if (RES) {
         float rv[8];
-        Vec8<T>::load(r + idx, rv);
+        decode8(rr[c], rv);
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[c][j] += rv[j];
         if (flags & NK_RMS_ROUND_H) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) v[c][j] = round_to<T>(v[c][j]);
         }
-        if (flags & NK_RMS_WRITE_H) Vec8<T>::store(h + idx, v[c]);
+        if (flags & NK_RMS_WRITE_H) {
+          Raw8<T> o;
+          encode8(v[c], o);
+          o.template store<true>(h + idx);
+        }
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) ss += v[c][j] * v[c][j];
@@ -198,7 +225,9 @@ __device__ __forceinline__ void rmsnorm_reg_body(const RmsNormArgs &a) {
         if (flags & NK_RMS_W) q = q * wv[j];
         v[c][j] = q;
       }
-      Vec8<T>::store(y + idx, v[c]);
+      Raw8<T> o;
+      encode8(v[c], o);
+      o.template store<true>(y + idx);
     }
   }
 }
@@ -240,17 +269,24 @@ __device__ __forceinline__ void rmsnorm_loop_body(const RmsNormArgs &a) {
   }
 }
 
-#define NK_RMS_REG(T, tn, B, C)                                                     \
-  extern "C" __global__ __launch_bounds__(B) void nk_rmsnorm_reg_##tn##_b##B##_c##C( \
-      RmsNormArgs a) {                                                              \
-    rmsnorm_reg_body<T, B, C>(a);                                                   \
+// Register variants: nk_rmsnorm_reg_<t>_b<BLOCK>_c<CHUNKS> (no residual) and
+// nk_rmsnorm_res_<t>_b<BLOCK>_c<CHUNKS> (residual).
+#define NK_RMS_REG(T, tn, B, C)                                                       \
+  extern "C" __global__ __launch_bounds__(B) void nk_rmsnorm_reg_##tn##_b##B##_c##C(   \
+      RmsNormArgs a) {                                                                \
+    rmsnorm_reg_body<T, B, C, false>(a);                                              \
+  }                                                                                   \
+  extern "C" __global__ __launch_bounds__(B) void nk_rmsnorm_res_##tn##_b##B##_c##C(   \
+      RmsNormArgs a) {                                                                \
+    rmsnorm_reg_body<T, B, C, true>(a);                                               \
   }
 #define NK_RMS_LOOP(T, tn)                                                           \
   extern "C" __global__ __launch_bounds__(256) void nk_rmsnorm_loop_##tn(RmsNormArgs a) { \
-    rmsnorm_loop_body<T, 256>(a);                                                   \
+    rmsnorm_loop_body<T, 256>(a);                                                    \
   }
 #define NK_RMS_ALL(T, tn) \
   NK_RMS_REG(T, tn, 64, 1)  \
+  NK_RMS_REG(T, tn, 128, 4) \
   NK_RMS_REG(T, tn, 256, 1) \
   NK_RMS_REG(T, tn, 256, 2) \
   NK_RMS_REG(T, tn, 512, 1) \

@@ -74,7 +74,11 @@ class SoftmaxArgs(ctypes.Structure):
 
 
 # (block, chunks) register variants: a row of up to block*chunks*8 elements
-_ROW_REG_VARIANTS = [(64, 1), (256, 1), (256, 2), (256, 4), (512, 4)]
+# first fit wins; for 2K-8K element rows the wider variants measured fastest
+# on MI355X (fewer resident waves per CU, all loads of a row in flight)
+_ROW_REG_VARIANTS = [(64, 1), (256, 1), (512, 4)]
+# every (block, chunks) pair compiled for the row kernels
+_ALL_REG_VARIANTS = {(64, 1), (128, 4), (256, 1), (256, 2), (512, 1), (256, 4), (512, 4)}
 _SOFTMAX_TYPES = {("f32", "f32"), ("bf16", "bf16"), ("bf16", "f32"), ("f32", "bf16"), ("f16", "f16")}
 
 
@@ -89,7 +93,8 @@ def _row_variant(n: int, elem_bytes: int, ptr_align_ok: bool):
     return None
 
 
-def softmax_rows(x_ptr: int, y_ptr: int, rows: int, n: int, in_dtype, out_dtype) -> Launch:
+def softmax_rows(x_ptr: int, y_ptr: int, rows: int, n: int, in_dtype, out_dtype,
+                 block_chunks=None) -> Launch:
     """y[r, :] = softmax(x[r, :]) over rows of n contiguous elements."""
     ti, to = dtype_tag(in_dtype), dtype_tag(out_dtype)
     if (ti, to) not in _SOFTMAX_TYPES:
@@ -100,6 +105,10 @@ def softmax_rows(x_ptr: int, y_ptr: int, rows: int, n: int, in_dtype, out_dtype)
         raise LaunchError("softmax: too many rows for one launch")
     aligned = x_ptr % 16 == 0 and y_ptr % 16 == 0
     var = _row_variant(n, dt.itemsize(in_dtype), aligned)
+    if block_chunks is not None and var is not None:
+        if n > block_chunks[0] * block_chunks[1] * 8 or tuple(block_chunks) not in _ALL_REG_VARIANTS:
+            raise LaunchError(f"softmax variant {block_chunks} does not fit n={n}")
+        var = tuple(block_chunks)
     args = SoftmaxArgs(x_ptr, y_ptr, rows, n, 0)
     nbytes = rows * n * (dt.itemsize(in_dtype) + dt.itemsize(out_dtype))
     if var is None:
@@ -134,7 +143,7 @@ RMS_WRITE_H = 4
 RMS_MUL_RECIP = 8
 RMS_W = 16
 
-_RMS_REG_VARIANTS = [(64, 1), (256, 1), (256, 2), (512, 1), (256, 4), (512, 4)]
+_RMS_REG_VARIANTS = [(64, 1), (256, 1), (256, 4), (512, 4)]
 
 
 def rmsnorm_rows(x_ptr: int, y_ptr: int, rows: int, n: int, dtype, eps: float,
@@ -174,8 +183,8 @@ def rmsnorm_rows(x_ptr: int, y_ptr: int, rows: int, n: int, dtype, eps: float,
     var = None
     if n % 8 == 0 and aligned:
         if block_chunks is not None:
-            var = block_chunks
-            if n > var[0] * var[1] * 8:
+            var = tuple(block_chunks)
+            if n > var[0] * var[1] * 8 or var not in _ALL_REG_VARIANTS:
                 raise LaunchError(f"rmsnorm variant {var} too small for n={n}")
         else:
             for b, c in _RMS_REG_VARIANTS:
@@ -186,7 +195,8 @@ def rmsnorm_rows(x_ptr: int, y_ptr: int, rows: int, n: int, dtype, eps: float,
         return Launch("rowwise", f"nk_rmsnorm_loop_{tag}", (rows, 1, 1), (256, 1, 1), args,
                       bytes=nbytes, note="loop")
     b, c = var
-    return Launch("rowwise", f"nk_rmsnorm_reg_{tag}_b{b}_c{c}", (rows, 1, 1), (b, 1, 1), args,
+    kind = "res" if r_ptr else "reg"
+    return Launch("rowwise", f"nk_rmsnorm_{kind}_{tag}_b{b}_c{c}", (rows, 1, 1), (b, 1, 1), args,
                   bytes=nbytes)
 
 
