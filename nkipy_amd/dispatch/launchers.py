@@ -205,3 +205,89 @@ def as_ptr(a) -> int:
     if isinstance(a, (int, np.integer)):
         return int(a)
     return int(a.ptr)
+
+
+# ---------------------------------------------------------------------------
+# MFMA GEMM (csrc/kernels/gemm.hip)
+# ---------------------------------------------------------------------------
+class GemmArgs(ctypes.Structure):
+    _fields_ = [
+        ("A", ctypes.c_void_p), ("B0", ctypes.c_void_p), ("B1", ctypes.c_void_p),
+        ("C", ctypes.c_void_p), ("bias", ctypes.c_void_p), ("scale0", ctypes.c_void_p),
+        ("scale1", ctypes.c_void_p), ("resid", ctypes.c_void_p),
+        ("M", ctypes.c_int64), ("N", ctypes.c_int64), ("K", ctypes.c_int64),
+        ("lda", ctypes.c_int64), ("ldb", ctypes.c_int64), ("ldc", ctypes.c_int64),
+        ("tiles_m", ctypes.c_int32), ("tiles_n", ctypes.c_int32),
+        ("flags", ctypes.c_int32), ("pad", ctypes.c_int32),
+    ]
+
+
+GEMM_BIAS = 1
+GEMM_SCALE = 2
+GEMM_RESID = 4
+GEMM_BM = 256
+GEMM_BN = 256
+
+
+def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: str,
+         b_dtype, c_dtype, lda: int = None, ldb: int = None, ldc: int = None,
+         bias_ptr: int = 0, scale_ptr: int = 0, resid_ptr: int = 0,
+         up_ptr: int = 0, up_scale_ptr: int = 0) -> Launch:
+    """C[M, N] = A[M, K] @ B (+ epilogue) on bf16 MFMA, fp32 accumulation.
+
+    ``layout`` "nn": B is K x N row-major (ldb >= N); "nt": B is N x K
+    row-major (ldb >= K).  ``b_dtype`` bf16 or float8_e4m3fn (then
+    ``scale_ptr`` gives fp32 per-column scales).  With ``up_ptr`` the kernel
+    computes the SwiGLU product silu(A @ B) * (A @ B_up) instead (B_up has the
+    layout and leading dimension of B).  ``bias_ptr`` (bf16, N) and
+    ``resid_ptr`` (C dtype, M x N, leading dimension ldc) are added.
+    """
+    if layout not in ("nn", "nt"):
+        raise LaunchError(f"unknown GEMM layout {layout}")
+    b_dtype, c_dtype = dt.canonical(b_dtype), dt.canonical(c_dtype)
+    fp8 = b_dtype == dt.float8_e4m3fn
+    if not fp8 and b_dtype != dt.bfloat16:
+        raise LaunchError(f"GEMM weights must be bf16 or float8_e4m3fn, got {dt.name(b_dtype)}")
+    if c_dtype not in (dt.bfloat16, dt.float32):
+        raise LaunchError(f"GEMM output must be bf16 or float32, got {dt.name(c_dtype)}")
+    if M <= 0 or N <= 0 or K <= 0:
+        raise LaunchError(f"GEMM needs positive sizes, got M={M} N={N} K={K}")
+    lda = K if lda is None else lda
+    ldb = (N if layout == "nn" else K) if ldb is None else ldb
+    ldc = N if ldc is None else ldc
+    swiglu = bool(up_ptr)
+    if K % 8 or lda % 8 or ldb % 8:
+        raise LaunchError("GEMM needs K, lda and ldb to be multiples of 8 (16-byte rows)")
+    if lda < K or ldc < N or (layout == "nn" and ldb < N) or (layout == "nt" and ldb < K):
+        raise LaunchError("GEMM leading dimension smaller than the matrix")
+    balign = 8 if fp8 else 16
+    for p, al in ((a_ptr, 16), (b_ptr, balign), (up_ptr, balign)):
+        if p and p % al:
+            raise LaunchError("GEMM operand pointer is not aligned for 128-bit access")
+    if layout == "nn" and N % 8:
+        raise LaunchError("NN GEMM needs N to be a multiple of 8")
+    if fp8 and not scale_ptr:
+        raise LaunchError("fp8 weights need per-column scales")
+    if swiglu and (fp8 != bool(up_scale_ptr)):
+        raise LaunchError("SwiGLU with fp8 weights needs scales for both weights")
+    if swiglu and (bias_ptr or resid_ptr or c_dtype != dt.bfloat16):
+        raise LaunchError("the SwiGLU epilogue writes bf16 without bias / residual")
+    bn = GEMM_BN // 2 if swiglu else GEMM_BN
+    tiles_m = -(-M // GEMM_BM)
+    tiles_n = -(-N // bn)
+    if tiles_m * tiles_n >= 2**31:
+        raise LaunchError("GEMM grid too large")
+    flags = (GEMM_BIAS if bias_ptr else 0) | (GEMM_SCALE if scale_ptr else 0) | (GEMM_RESID if resid_ptr else 0)
+    args = GemmArgs(a_ptr, b_ptr, up_ptr or None, c_ptr, bias_ptr or None, scale_ptr or None,
+                    up_scale_ptr or None, resid_ptr or None, M, N, K, lda, ldb, ldc,
+                    tiles_m, tiles_n, flags, 0)
+    btag = "e4m3" if fp8 else "bf16"
+    ctag = "bf16" if c_dtype == dt.bfloat16 else "f32"
+    if swiglu:
+        symbol = f"nk_gemm_swiglu_{layout}_{btag}_bf16"
+    else:
+        symbol = f"nk_gemm_{layout}_{btag}_{ctag}"
+    n_mm = 2 if swiglu else 1
+    nbytes = M * K * 2 + n_mm * N * K * b_dtype.itemsize + M * N * c_dtype.itemsize
+    return Launch("gemm", symbol, (tiles_m * tiles_n, 1, 1), (256, 1, 1), args,
+                  bytes=nbytes, flops=2 * M * N * K * n_mm)

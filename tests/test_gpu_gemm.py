@@ -1,0 +1,122 @@
+"""GPU parity of the MFMA GEMM kernels (launcher level) against NumPy fp32
+matmul on the same bf16 / fp8 values, across layouts, edge tiles and fused
+epilogues."""
+
+import numpy as np
+import pytest
+
+from nkipy_amd.core import dtypes as dt
+from nkipy_amd.dispatch import launchers as LA
+from nkipy_amd.runtime import DeviceTensor
+from oracle import kernels as K
+from oracle import numerics as N
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16(rng, shape, scale=1.0):
+    return N.bf16_round(rng.standard_normal(shape) * scale)
+
+
+def _close(got, ref, tol=2e-2):
+    """bf16-level check: |got - ref| <= tol * (|ref| + rms(ref))."""
+    ref = np.asarray(ref, np.float64)
+    scale = np.sqrt(np.mean(ref ** 2)) + 1e-30
+    err = np.abs(np.asarray(got, np.float64) - ref)
+    assert np.all(err <= tol * (np.abs(ref) + scale)), float(np.max(err / (np.abs(ref) + scale)))
+
+
+def _run(gpu, launch):
+    launch.run(gpu)
+    gpu.sync()
+
+
+SHAPES = [(256, 256, 64), (512, 768, 320), (300, 520, 136), (64, 40, 16), (1000, 1000, 1000)]
+
+
+@pytest.mark.parametrize("layout", ["nn", "nt"])
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+def test_gemm_bf16(gpu, layout, shape, out):
+    M, Nn, Kk = shape
+    if layout == "nn" and Nn % 8:
+        pytest.skip("NN needs N % 8 == 0")
+    rng = np.random.default_rng(M + Nn + Kk)
+    a = _bf16(rng, (M, Kk))
+    b = _bf16(rng, (Kk, Nn) if layout == "nn" else (Nn, Kk), 0.05)
+    bmat = b if layout == "nn" else b.T
+    ref = a.astype(np.float64) @ bmat.astype(np.float64)
+    ad = DeviceTensor.from_numpy(dt.to_bf16(a))
+    bd = DeviceTensor.from_numpy(dt.to_bf16(b))
+    cdt = dt.bfloat16 if out == "bf16" else dt.float32
+    cd = DeviceTensor.empty((M, Nn), cdt)
+    _run(gpu, LA.gemm(ad.ptr, bd.ptr, cd.ptr, M, Nn, Kk, layout=layout, b_dtype=dt.bfloat16, c_dtype=cdt))
+    got = dt.to_float32(cd.numpy())
+    if out == "f32":
+        np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
+    else:
+        _close(got, ref)
+
+
+@pytest.mark.parametrize("layout", ["nn", "nt"])
+def test_gemm_swiglu(gpu, layout):
+    M, F, Kk = 512, 384, 256
+    rng = np.random.default_rng(7)
+    x = _bf16(rng, (M, Kk))
+    wg = _bf16(rng, (Kk, F), 0.05)
+    wu = _bf16(rng, (Kk, F), 0.05)
+    ref = K.silu(x.astype(np.float64) @ wg) * (x.astype(np.float64) @ wu)
+    if layout == "nn":
+        # fused gate_up weight (K, 2F): up is a column offset of the same matrix
+        gu = np.concatenate([wg, wu], axis=1)
+        bd = DeviceTensor.from_numpy(dt.to_bf16(gu))
+        b0, b1, ldb = bd.ptr, bd.ptr + F * 2, 2 * F
+    else:
+        gd = DeviceTensor.from_numpy(dt.to_bf16(np.ascontiguousarray(wg.T)))
+        ud = DeviceTensor.from_numpy(dt.to_bf16(np.ascontiguousarray(wu.T)))
+        b0, b1, ldb, bd = gd.ptr, ud.ptr, Kk, (gd, ud)
+    xd = DeviceTensor.from_numpy(dt.to_bf16(x))
+    hd = DeviceTensor.empty((M, F), dt.bfloat16)
+    _run(gpu, LA.gemm(xd.ptr, b0, hd.ptr, M, F, Kk, layout=layout, b_dtype=dt.bfloat16,
+                      c_dtype=dt.bfloat16, ldb=ldb, up_ptr=b1))
+    _close(dt.to_float32(hd.numpy()), ref)
+
+
+def test_gemm_fp8_nt_scales_bias_residual(gpu):
+    M, Nn, Kk = 384, 512, 448
+    rng = np.random.default_rng(11)
+    x = _bf16(rng, (M, Kk))
+    w = (rng.standard_normal((Nn, Kk)) * 0.02).astype(np.float32)
+    codes, scale = N.quantize_per_channel_e4m3fn(w, axis=1)
+    wdq = N.dequantize_e4m3fn(codes, scale, axis=1)
+    bias = N.bf16_round(rng.standard_normal(Nn) * 0.1)
+    res = N.bf16_round(rng.standard_normal((M, Nn)))
+    ref = x.astype(np.float64) @ wdq.T.astype(np.float64) + bias + res
+    xd = DeviceTensor.from_numpy(dt.to_bf16(x))
+    wd = DeviceTensor.from_numpy(codes.view(dt.float8_e4m3fn))
+    sd = DeviceTensor.from_numpy(scale.astype(np.float32))
+    bd = DeviceTensor.from_numpy(dt.to_bf16(bias))
+    rd = DeviceTensor.from_numpy(dt.to_bf16(res))
+    cd = DeviceTensor.empty((M, Nn), dt.bfloat16)
+    _run(gpu, LA.gemm(xd.ptr, wd.ptr, cd.ptr, M, Nn, Kk, layout="nt", b_dtype=dt.float8_e4m3fn,
+                      c_dtype=dt.bfloat16, scale_ptr=sd.ptr, bias_ptr=bd.ptr, resid_ptr=rd.ptr))
+    _close(dt.to_float32(cd.numpy()), ref)
+
+
+def test_gemm_fp8_swiglu_nt(gpu):
+    M, F, Kk = 256, 256, 512
+    rng = np.random.default_rng(12)
+    x = _bf16(rng, (M, Kk))
+    wg = (rng.standard_normal((F, Kk)) * 0.02).astype(np.float32)
+    wu = (rng.standard_normal((F, Kk)) * 0.02).astype(np.float32)
+    cg, sg = N.quantize_per_channel_e4m3fn(wg, axis=1)
+    cu, su = N.quantize_per_channel_e4m3fn(wu, axis=1)
+    g = x.astype(np.float64) @ N.dequantize_e4m3fn(cg, sg, axis=1).T
+    u = x.astype(np.float64) @ N.dequantize_e4m3fn(cu, su, axis=1).T
+    ref = K.silu(g) * u
+    t = [DeviceTensor.from_numpy(v) for v in (dt.to_bf16(x), cg.view(dt.float8_e4m3fn), cu.view(dt.float8_e4m3fn),
+                                              sg.astype(np.float32), su.astype(np.float32))]
+    hd = DeviceTensor.empty((M, F), dt.bfloat16)
+    _run(gpu, LA.gemm(t[0].ptr, t[1].ptr, hd.ptr, M, F, Kk, layout="nt", b_dtype=dt.float8_e4m3fn,
+                      c_dtype=dt.bfloat16, scale_ptr=t[3].ptr, up_ptr=t[2].ptr, up_scale_ptr=t[4].ptr))
+    _close(dt.to_float32(hd.numpy()), ref)
