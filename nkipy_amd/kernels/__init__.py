@@ -7,3 +7,6 @@ function) and the workloads of the backend's benchmark.
 
 from nkipy_amd.kernels.softmax import softmax_kernel, softmax_upcast_kernel  # noqa: F401
 from nkipy_amd.kernels.rmsnorm import residual_rmsnorm_kernel, rmsnorm_kernel  # noqa: F401
+from nkipy_amd.kernels.feedforward import (  # noqa: F401
+    feedforward_bias_kernel, feedforward_kernel, linear_nt_kernel, swiglu_mlp_kernel,
+)
