@@ -159,6 +159,94 @@ def bench_softmax(steps, warmup, rt):
     }
 
 
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def bench_swiglu(steps, warmup, rt):
+    """SwiGLU MLP: x (4096, 4096), W_gate / W_up (4096, 14336), W_down
+    (14336, 4096), bf16, fp32 accumulation.  One step = the whole MLP (the
+    fused gate/up kernel and the down GEMM)."""
+    from nkipy_amd.core import dtypes as dt
+    from nkipy_amd.kernels import swiglu_mlp_kernel
+    from nkipy_amd.runtime import DeviceKernel, DeviceTensor
+
+    M, H, F = 4096, 4096, 14336
+    rng = np.random.default_rng(42)
+    x = dt.round_to_bf16(rng.standard_normal((M, H)).astype(np.float32))
+    ws = [dt.round_to_bf16((rng.standard_normal(s) * 0.02).astype(np.float32))
+          for s in ((H, F), (H, F), (F, H))]
+    args = [dt.to_bf16(a) for a in [x] + ws]
+    dk = DeviceKernel.compile_and_load(swiglu_mlp_kernel, *args, name="swiglu_mlp")
+    if dk.plan.kernel_kinds != ["gemm_swiglu", "gemm"]:
+        raise RuntimeError(f"SwiGLU did not lower to the fused GEMMs: {dk.plan.kernel_kinds}")
+    names = ("x", "w_gate", "w_up", "w_down")
+    ins = {n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(names, args)}
+    out = DeviceTensor.empty((M, H), dt.bfloat16, name="output0")
+    bound = dk.executor.bind({**{k: v.ptr for k, v in ins.items()}, "output0": out.ptr})
+    flops = 3 * 2 * M * H * F
+    ms_step, _ = _time_bound([bound], steps, warmup, rt)
+    # per-kernel times from single-launch timing (HIP events on the runtime stream)
+    per = []
+    for l in bound.launches:
+        f = l.function(rt)
+        ms = f.time(l.grid, l.block, l.args, warmup=2, iters=max(3, steps // 4))
+        per.append({"kernel": l.symbol, "us": round(ms * 1e3, 2),
+                    "tflops": round(l.flops / (ms * 1e-3) / 1e12, 1),
+                    "frac_bf16_peak": round(l.flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)})
+    from oracle import kernels as K
+
+    rows = np.arange(0, M, M // 16)
+    ref = K.swiglu_mlp(x[rows], *ws)
+    got = dt.to_float32(out.numpy()[rows])
+    scale = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+    ok = bool(np.all(np.abs(got - ref) <= 2e-2 * (np.abs(ref) + scale)))
+    tflops = flops / (ms_step * 1e-3) / 1e12
+    return {
+        "workload": "swiglu_mlp", "shape": {"M": M, "hidden": H, "ffn": F}, "dtype": "bf16",
+        "flops_per_step": flops, "us_per_step": round(ms_step * 1e3, 2),
+        "tflops": round(tflops, 1), "frac_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4),
+        "kernels": per, "parity_ok": ok,
+    }
+
+
+def bench_linattn(steps, warmup, rt):
+    """Chunked causal linear attention: B=4, H=16, T=8192, d=128 bf16."""
+    from nkipy_amd.core import dtypes as dt
+    from nkipy_amd.kernels import chunked_linear_attention_kernel
+    from nkipy_amd.runtime import DeviceKernel, DeviceTensor
+
+    B, H, T, D = 4, 16, 8192, 128
+    rng = np.random.default_rng(42)
+    host = [dt.round_to_bf16((rng.standard_normal((B, H, T, D)) / np.sqrt(D)).astype(np.float32))
+            for _ in range(3)]
+    args = [dt.to_bf16(a) for a in host]
+    dk = DeviceKernel.compile_and_load(chunked_linear_attention_kernel, *args, name="linear_attention")
+    if dk.plan.kernel_kinds != ["linear_attention"]:
+        raise RuntimeError(f"linear attention did not lower to the fused kernel: {dk.plan.kernel_kinds}")
+    alg_bytes = 4 * B * H * T * D * 2
+    nsets = _sets_for(alg_bytes)
+    sets = [[DeviceTensor.from_numpy(a, name=nm) for nm, a in zip("qkv", args)]
+            + [DeviceTensor.empty((B, H, T, D), dt.bfloat16, name="output0")] for _ in range(nsets)]
+    bounds = [dk.executor.bind({"q": s[0].ptr, "k": s[1].ptr, "v": s[2].ptr, "output0": s[3].ptr})
+              for s in sets]
+    ms_step, ms_launch = _time_bound(bounds, steps, warmup, rt)
+    from oracle import kernels as K
+
+    got = dt.to_float32(sets[0][3].numpy()[1:2, 5:6])
+    ref = K.linear_attention_chunked(*[a[1:2, 5:6] for a in host])
+    scale = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+    ok = bool(np.all(np.abs(got - ref) <= 2e-2 * (np.abs(ref) + scale)))
+    gbs = alg_bytes / (ms_launch * 1e-3) / 1e9
+    return {
+        "workload": "chunked_linear_attention", "shape": [B, H, T, D], "chunk": 64, "dtype": "bf16",
+        "kernel": bounds[0].launches[0].symbol, "bytes_per_launch": alg_bytes,
+        "us_per_launch": round(ms_launch * 1e3, 2), "gbs": round(gbs, 1),
+        "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+        "tflops": round(bounds[0].launches[0].flops / (ms_launch * 1e-3) / 1e12, 1),
+        "parity_ok": ok,
+    }
+
+
 def cpu_baseline_rmsnorm(host, budget_s=12.0):
     from oracle import kernels as K
 
@@ -208,6 +296,11 @@ def main():
         f"({rms['kernel']}), parity_ok={rms['parity_ok']}")
     sm = bench_softmax(args.steps, args.warmup, rt)
     log(f"softmax: {sm['us_per_launch']:.2f} us/launch, {sm['gbs']:.0f} GB/s, rel err {sm['max_rel_err']:.2e}")
+    sw = bench_swiglu(max(5, args.steps // 20), max(2, args.warmup // 5), rt)
+    log(f"swiglu mlp: {sw['us_per_step']:.1f} us/step, {sw['tflops']:.1f} TFLOP/s "
+        f"({sw['frac_bf16_peak'] * 100:.1f}% of bf16 peak), parity_ok={sw['parity_ok']}")
+    la = bench_linattn(max(5, args.steps // 20), max(2, args.warmup // 5), rt)
+    log(f"linear attention: {la['us_per_launch']:.1f} us, {la['gbs']:.0f} GB/s, parity_ok={la['parity_ok']}")
 
     cpu = None
     if not args.no_cpu:
@@ -248,6 +341,8 @@ def main():
         "parity_ok": rms["parity_ok"],
         "kernels": {
             "softmax": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in sm.items()},
+            "swiglu_mlp": sw,
+            "linear_attention": la,
         },
     }
     print(json.dumps(line), flush=True)

@@ -157,6 +157,12 @@ template <> struct Vec8<f16> {
   }
 };
 
+// 16-bit element e (0..7) of a 16-byte word holding 8 two-byte values.
+NK_DEVICE uint32_t h16_of(const uint4 &v, int e) {
+  uint32_t w = (e < 2) ? v.x : (e < 4) ? v.y : (e < 6) ? v.z : v.w;
+  return (e & 1) ? (w >> 16) : (w & 0xffffu);
+}
+
 // Raw form of an 8-element chunk: U 16-byte words (1 for 2-byte types, 2 for
 // fp32).  Kernels issue every raw load of a row first, then decode, so all
 // of a thread's HBM requests are in flight together.

@@ -455,26 +455,30 @@ class DotStep(Step):
         lc, rc = list(at["lhs_contract"]), list(at["rhs_contract"])
         lf = [i for i in range(src_a.ndim) if i not in lb and i not in lc]
         rf = [i for i in range(src_b.ndim) if i not in rb and i not in rc]
-        if len(lc) != 1 or len(rf) > 1 or len(lb) > 1:
-            raise LaunchError("generic dot supports one contracting dim, <=1 batch dim and a rank<=2 rhs")
-        # lhs free dims must collapse to a single M with uniform stride
-        M = int(np.prod([src_a.shape[i] for i in lf])) if lf else 1
-        sam = int(a_s[lf[-1]]) if lf else 0
-        exp = sam
-        for i in reversed(lf):
-            if int(a_s[i]) != exp:
-                raise LaunchError("generic dot: lhs free dims are not collapsible")
-            exp *= src_a.shape[i]
-        self.M = M
-        self.sam = sam
+        if len(lc) != 1 or len(rf) > 1 or len(lb) != len(rb):
+            raise LaunchError("generic dot supports one contracting dim and a rank<=2 rhs per batch")
+
+        def collapse(dims, shape, strides, what):
+            """(size, stride) of dims merged into one; LaunchError if the
+            strides do not describe one uniform axis."""
+            if not dims:
+                return 1, 0
+            st = int(strides[dims[-1]])
+            expect = st
+            for i in reversed(dims):
+                if shape[i] != 1 and int(strides[i]) != expect:
+                    raise LaunchError(f"generic dot: {what} dims are not collapsible")
+                expect *= shape[i]
+            return int(np.prod([shape[i] for i in dims])), st
+
+        self.M, self.sam = collapse(lf, src_a.shape, a_s, "lhs free")
+        self.batch, self.sab = collapse(lb, src_a.shape, a_s, "lhs batch")
+        _, self.sbb = collapse(rb, src_b.shape, b_s, "rhs batch")
         self.sak = int(a_s[lc[0]])
         self.K = src_a.shape[lc[0]]
         self.N = src_b.shape[rf[0]] if rf else 1
         self.sbn = int(b_s[rf[0]]) if rf else 0
         self.sbk = int(b_s[rc[0]])
-        self.batch = src_a.shape[lb[0]] if lb else 1
-        self.sab = int(a_s[lb[0]]) if lb else 0
-        self.sbb = int(b_s[rb[0]]) if rb else 0
         self.a_v, self.a_o, self.b_v, self.b_o = a_v, a_o, b_v, b_o
 
     def launches(self, addr):

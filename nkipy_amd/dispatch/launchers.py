@@ -291,3 +291,35 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
     nbytes = M * K * 2 + n_mm * N * K * b_dtype.itemsize + M * N * c_dtype.itemsize
     return Launch("gemm", symbol, (tiles_m * tiles_n, 1, 1), (256, 1, 1), args,
                   bytes=nbytes, flops=2 * M * N * K * n_mm)
+
+
+# ---------------------------------------------------------------------------
+# Chunked causal linear attention (csrc/kernels/linattn.hip)
+# ---------------------------------------------------------------------------
+class LinAttnArgs(ctypes.Structure):
+    _fields_ = [("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+                ("o", ctypes.c_void_p), ("BH", ctypes.c_int64), ("T", ctypes.c_int64)]
+
+
+LINATTN_CHUNK = 64
+LINATTN_D = 128
+
+
+def linear_attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, BH: int, T: int,
+                     D: int = 128, Dv: int = 128, chunk: int = 64) -> Launch:
+    """o = causal linear attention with phi = elu + 1 over (BH, T, D) bf16
+    sequences, chunk 64, head dims 128 (the compiled variant)."""
+    if (D, Dv, chunk) != (LINATTN_D, LINATTN_D, LINATTN_CHUNK):
+        raise LaunchError(f"linear attention kernel is built for d = d_v = 128, chunk 64; "
+                          f"got d={D}, d_v={Dv}, chunk={chunk}")
+    if BH <= 0 or T <= 0 or T % chunk:
+        raise LaunchError(f"linear attention needs T a positive multiple of {chunk}, got T={T}")
+    if any(p % 16 for p in (q_ptr, k_ptr, v_ptr, o_ptr)):
+        raise LaunchError("linear attention operands must be 16-byte aligned")
+    if BH * 4 >= 2**31:
+        raise LaunchError("linear attention grid too large")
+    n = T // chunk
+    flops_chunk = 2 * chunk * chunk * D + 2 * chunk * D * Dv + 2 * chunk * chunk * Dv + 2 * D * Dv * chunk
+    return Launch("linattn", "nk_linattn_c64_d128", (BH * 4, 1, 1), (256, 1, 1),
+                  LinAttnArgs(q_ptr, k_ptr, v_ptr, o_ptr, BH, T),
+                  bytes=4 * BH * T * D * 2, flops=BH * n * flops_chunk)

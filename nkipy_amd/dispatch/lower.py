@@ -52,6 +52,7 @@ class Lowering:
         self.alias_reshape: Set[int] = set()  # reshape values sharing the operand's slot
         self.matches = []
         self.covered: Dict[int, object] = {}  # id(node) -> match
+        self.dot_contig: Set[int] = set()  # dots that read contiguous operands
 
     # ------------------------------------------------------------------
     def n_users(self, v: Value) -> int:
@@ -95,8 +96,17 @@ class Lowering:
             if id(n) in self.covered:
                 continue
             if n.op in ("reduce", "argmax", "argmin", "dot") and n.out.id in self.mat:
-                for v in n.inputs:
-                    base, _, _ = G.strided_access(v, self.is_mat)
+                accs = [G.strided_access(v, self.is_mat) for v in n.inputs]
+                if n.op == "dot":
+                    try:
+                        G.DotStep(n, *accs)
+                    except G.LaunchError:
+                        # strides do not collapse: read contiguous copies
+                        self.dot_contig.add(id(n))
+                        for v in n.inputs:
+                            self.need(v)
+                        continue
+                for base, _, _ in accs:
                     self.need(base)
         self._settle_programs()
         # 3. storage and 4. steps
@@ -245,8 +255,11 @@ class Lowering:
             base, strides, off = G.strided_access(n.inputs[0], self.is_mat)
             return [G.ReduceStep(n, base, strides, off)]
         if op == "dot":
-            lhs = G.strided_access(n.inputs[0], self.is_mat)
-            rhs = G.strided_access(n.inputs[1], self.is_mat)
+            if id(n) in self.dot_contig:
+                lhs, rhs = [(v, G.contiguous_strides(v.shape), 0) for v in n.inputs]
+            else:
+                lhs = G.strided_access(n.inputs[0], self.is_mat)
+                rhs = G.strided_access(n.inputs[1], self.is_mat)
             return [G.DotStep(n, lhs, rhs)]
         if op in ("take", "take_along_axis"):
             return [G.GatherStep(n)]

@@ -459,14 +459,12 @@ class RmsNormPattern:
 
 
 def _default_patterns():
-    pats = [SoftmaxPattern(), RmsNormPattern()]
-    try:
-        from nkipy_amd.dispatch.patterns_gemm import GEMM_PATTERNS
+    from nkipy_amd.dispatch.patterns_gemm import GemmPattern, SwigluPattern
+    from nkipy_amd.dispatch.patterns_linattn import LinearAttentionPattern
 
-        pats = GEMM_PATTERNS[:1] + pats + GEMM_PATTERNS[1:]
-    except ImportError:
-        pass
-    return pats
+    # larger structures first: they contain matmuls the GEMM pattern would claim
+    return [LinearAttentionPattern(), SwigluPattern(), SoftmaxPattern(), RmsNormPattern(),
+            GemmPattern()]
 
 
 DEFAULT_PATTERNS = _default_patterns()

@@ -10,3 +10,4 @@ from nkipy_amd.kernels.rmsnorm import residual_rmsnorm_kernel, rmsnorm_kernel  #
 from nkipy_amd.kernels.feedforward import (  # noqa: F401
     feedforward_bias_kernel, feedforward_kernel, linear_nt_kernel, swiglu_mlp_kernel,
 )
+from nkipy_amd.kernels.linear_attention import chunked_linear_attention_kernel  # noqa: F401
