@@ -70,11 +70,14 @@ def _time_bound(bounds, steps: int, warmup: int, rt):
 
 
 def _traffic(kernel_key):
+    """HBM bytes per launch of ``kernel_key`` from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs (scaled by the copy-kernel calibration)."""
     try:
         with open(TRAFFIC_FILE) as f:
-            return json.load(f).get(kernel_key)
+            entry = json.load(f).get(kernel_key)
     except (OSError, ValueError):
         return None
+    return entry.get("total_bytes") if isinstance(entry, dict) else None
 
 
 def bench_rmsnorm(steps, warmup, rt):
@@ -247,6 +250,22 @@ def bench_linattn(steps, warmup, rt):
     }
 
 
+def calibrate_copy(rt, nbytes=1 << 30, reps=3):
+    """Plain streaming copy of a known size: rocprof's FETCH_SIZE / WRITE_SIZE
+    for nk_copy16 read against 1 GiB give the counter scale factors."""
+    from nkipy_amd.dispatch.generic import copy16
+
+    src, dst = rt.malloc(nbytes), rt.malloc(nbytes)
+    rt.memset(src, 0x5a, nbytes)
+    l = copy16(src, dst, nbytes)
+    for _ in range(reps):
+        l.run(rt)
+    rt.sync()
+    rt.free(src)
+    rt.free(dst)
+    log(f"copy calibration: {reps} x nk_copy16 of {nbytes} bytes")
+
+
 def cpu_baseline_rmsnorm(host, budget_s=12.0):
     from oracle import kernels as K
 
@@ -279,6 +298,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 1 GiB streaming copy (calibrates HBM traffic counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU; --gpus {args.gpus} is not supported "
@@ -291,6 +312,8 @@ def main():
     info = rt.device_info()
     log(f"device {info['arch']} CUs={info['cu_count']} sclk={info['clock_khz'] / 1e6:.2f} GHz")
 
+    if args.calibrate_copy:
+        calibrate_copy(rt)
     rms = bench_rmsnorm(args.steps, args.warmup, rt)
     log(f"rmsnorm: {rms['us_per_launch']:.2f} us/launch, {rms['gbs_launch']:.0f} GB/s "
         f"({rms['kernel']}), parity_ok={rms['parity_ok']}")

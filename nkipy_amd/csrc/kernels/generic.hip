@@ -459,3 +459,19 @@ extern "C" __global__ __launch_bounds__(256) void nk_cumsum(CumsumArgs a) {
     store_any(a.out, off, a.out_dtype, acc);
   }
 }
+
+// ---------------------------------------------------------------------------
+// Streaming copy of n16 16-byte words (plan flat copies; also the plain copy
+// kernel of known size that calibrates the HBM traffic counters).
+// ---------------------------------------------------------------------------
+struct Copy16Args {
+  const uint4 *src;
+  uint4 *dst;
+  int64_t n16;
+  int64_t nthreads;  // grid size * 256
+};
+
+extern "C" __global__ __launch_bounds__(256) void nk_copy16(Copy16Args a) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.n16; i += a.nthreads)
+    nt_store16(a.dst + i, nt_load16(a.src + i));
+}

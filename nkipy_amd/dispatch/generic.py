@@ -135,6 +135,21 @@ class CumsumArgs(ctypes.Structure):
     ]
 
 
+class Copy16Args(ctypes.Structure):
+    _fields_ = [("src", ctypes.c_void_p), ("dst", ctypes.c_void_p),
+                ("n16", ctypes.c_int64), ("nthreads", ctypes.c_int64)]
+
+
+def copy16(src_ptr: int, dst_ptr: int, nbytes: int) -> Launch:
+    """Streaming device copy of ``nbytes`` (multiple of 16, 16-byte aligned)."""
+    if nbytes % 16 or src_ptr % 16 or dst_ptr % 16:
+        raise LaunchError("copy16 needs 16-byte aligned pointers and a multiple of 16 bytes")
+    n16 = nbytes // 16
+    grid = max(1, min((n16 + 255) // 256, 1 << 20))
+    return Launch("generic", "nk_copy16", (grid, 1, 1), (256, 1, 1),
+                  Copy16Args(src_ptr, dst_ptr, n16, grid * 256), bytes=2 * nbytes)
+
+
 def _grid_for(total: int, max_blocks: int = 16384) -> int:
     return max(1, min((total + 255) // 256, max_blocks))
 
@@ -324,7 +339,8 @@ class ProgramBuilder:
 
 
 class ProgramStep(Step):
-    """One ``nk_ew_program`` launch writing ``shape`` elements of ``out``."""
+    """One ``nk_ew_program`` launch writing ``shape`` elements of ``out``
+    (a plain copy of a contiguous value takes the streaming copy kernel)."""
 
     kind = "elementwise"
 
@@ -367,6 +383,11 @@ class ProgramStep(Step):
             I.op, I.dst, I.a, I.b, I.c, I.dtype, I.flags, I.imm = op, dst, x, y, z, dtc, flags, imm
         if total == 0:
             return []
+        if getattr(p, "flat_copy", False) and self.out_offset == 0 and self.out_dtype == p.inputs[0][0].dtype:
+            src = a.inp[0].ptr
+            nbytes = total * self.out_dtype.itemsize
+            if nbytes % 16 == 0 and src % 16 == 0 and a.out % 16 == 0:
+                return [copy16(src, a.out, nbytes)]
         return [Launch("generic", "nk_ew_program", (grid, 1, 1), (256, 1, 1), a,
                        bytes=total * self.out_dtype.itemsize)]
 
@@ -572,5 +593,6 @@ def flat_copy_program(src: Value) -> Program:
     prog = Program((src.size,))
     r = prog.load(src, (1,), 0)
     prog.result = r
+    prog.flat_copy = True
     return prog
 
