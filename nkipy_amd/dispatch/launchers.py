@@ -323,3 +323,44 @@ def linear_attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, BH: int, T:
     return Launch("linattn", "nk_linattn_c64_d128", (BH * 4, 1, 1), (256, 1, 1),
                   LinAttnArgs(q_ptr, k_ptr, v_ptr, o_ptr, BH, T),
                   bytes=4 * BH * T * D * 2, flops=BH * n * flops_chunk)
+
+
+# ---------------------------------------------------------------------------
+# Causal GQA attention (csrc/kernels/attention.hip)
+# ---------------------------------------------------------------------------
+class AttnArgs(ctypes.Structure):
+    _fields_ = [("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+                ("o", ctypes.c_void_p)] + \
+        [(f"{t}_{s}", ctypes.c_int64) for t in "qkvo" for s in ("sb", "ss", "sh")] + \
+        [("B", ctypes.c_int32), ("S", ctypes.c_int32), ("Hq", ctypes.c_int32),
+         ("Hkv", ctypes.c_int32), ("scale", ctypes.c_float), ("causal", ctypes.c_int32)]
+
+
+def attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, B: int, S: int, Hq: int, Hkv: int,
+              D: int, scale: float, strides: dict, causal: bool = True) -> Launch:
+    """Flash-style attention over bf16 q (B, S, Hq, D), k / v (B, S, Hkv, D) and
+    o (B, S, Hq, D), each addressed by element strides {"q": (sb, ss, sh), ...}
+    with the head dim contiguous.  KV head of query head h is h // (Hq // Hkv)."""
+    if D != 128:
+        raise LaunchError(f"attention kernel is built for head_dim 128, got {D}")
+    if S % 128 or S <= 0:
+        raise LaunchError(f"attention needs the sequence length to be a multiple of 128, got {S}")
+    if Hq % Hkv:
+        raise LaunchError("query heads must be a multiple of KV heads")
+    for name in "qkvo":
+        st = strides[name]
+        if any(s % 8 for s in st):
+            raise LaunchError("attention strides must keep 16-byte alignment")
+    for p in (q_ptr, k_ptr, v_ptr, o_ptr):
+        if p % 16:
+            raise LaunchError("attention operands must be 16-byte aligned")
+    vals = [q_ptr, k_ptr, v_ptr, o_ptr]
+    for name in "qkvo":
+        vals += list(strides[name])
+    args = AttnArgs(*vals, B, S, Hq, Hkv, float(scale), 1 if causal else 0)
+    nblocks = B * Hq * (S // 128)
+    if nblocks >= 2**31:
+        raise LaunchError("attention grid too large")
+    flops = 4 * B * Hq * S * S * D // (2 if causal else 1)
+    return Launch("attention", "nk_attention_causal_d128", (nblocks, 1, 1), (256, 1, 1), args,
+                  bytes=(2 * B * S * Hq * D + 2 * B * S * Hkv * D) * 2, flops=flops)

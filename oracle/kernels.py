@@ -167,3 +167,42 @@ def linear_attention_quadratic_f64(q, k, v):
     mask = np.tril(np.ones((T, T)))
     A = np.einsum("bhtd,bhsd->bhts", qf, kf) * mask
     return np.einsum("bhts,bhsd->bhtd", A, v) / A.sum(-1, keepdims=True)
+
+
+# ---------------------------------------------------------------------------
+# Causal GQA attention -- examples/models/qwen3/kernels/attention.py:109-140
+# (np.repeat of KV heads, q @ k^T / sqrt(d), causal mask, softmax, @ v).
+# q (B, S, Hq, D), k / v (B, S, Hkv, D) -> (B, S, Hq, D).
+# ---------------------------------------------------------------------------
+
+
+def causal_gqa_attention(q, k, v, scale=None):
+    q = np.asarray(q, np.float32)
+    k = np.asarray(k, np.float32)
+    v = np.asarray(v, np.float32)
+    B, S, Hq, D = q.shape
+    rep = Hq // k.shape[2]
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    kk = np.repeat(k, rep, axis=2).transpose(0, 2, 3, 1)   # (B, Hq, D, S)
+    vv = np.repeat(v, rep, axis=2).transpose(0, 2, 1, 3)   # (B, Hq, S, D)
+    s = (q.transpose(0, 2, 1, 3) @ kk) * np.float32(scale)
+    s = s + np.triu(np.full((S, S), -np.inf, np.float32), 1)
+    s = s - s.max(-1, keepdims=True)
+    p = np.exp(s)
+    p = p / p.sum(-1, keepdims=True)
+    return (p @ vv).transpose(0, 2, 1, 3)
+
+
+def causal_attention_f64_loop(q, k, v):
+    """Per-query float64 loop (tiny shapes): pins causal_gqa_attention."""
+    q, k, v = (np.asarray(a, np.float64) for a in (q, k, v))
+    B, S, Hq, D = q.shape
+    rep = Hq // k.shape[2]
+    out = np.zeros_like(q)
+    for b in range(B):
+        for h in range(Hq):
+            for t in range(S):
+                w = np.array([q[b, t, h] @ k[b, s, h // rep] for s in range(t + 1)]) / np.sqrt(D)
+                w = np.exp(w - w.max())
+                out[b, t, h] = (w[:, None] * v[b, :t + 1, h // rep]).sum(0) / w.sum()
+    return out

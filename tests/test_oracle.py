@@ -133,3 +133,12 @@ def test_per_channel_quantisation_roundtrip():
     # 3 mantissa bits: relative error of each element <= 2^-4 (+ subnormal floor)
     assert np.all(np.abs(deq - w) <= np.abs(w) * 2.0**-4 + scale[:, None] * 2.0**-9)
     np.testing.assert_allclose(np.abs(deq).max(1), np.abs(w).max(1), rtol=1e-6)
+
+
+def test_causal_gqa_attention_vs_f64_loop():
+    rng = np.random.default_rng(10)
+    q = rng.standard_normal((1, 6, 4, 8)).astype(np.float32)
+    k = rng.standard_normal((1, 6, 2, 8)).astype(np.float32)
+    v = rng.standard_normal((1, 6, 2, 8)).astype(np.float32)
+    np.testing.assert_allclose(K.causal_gqa_attention(q, k, v), K.causal_attention_f64_loop(q, k, v),
+                               rtol=1e-5, atol=1e-6)
