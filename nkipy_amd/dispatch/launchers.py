@@ -364,3 +364,39 @@ def attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, B: int, S: int, Hq
     flops = 4 * B * Hq * S * S * D // (2 if causal else 1)
     return Launch("attention", "nk_attention_causal_d128", (nblocks, 1, 1), (256, 1, 1), args,
                   bytes=(2 * B * S * Hq * D + 2 * B * S * Hkv * D) * 2, flops=flops)
+
+
+# ---------------------------------------------------------------------------
+# Rotary position embedding (csrc/kernels/rope.hip)
+# ---------------------------------------------------------------------------
+class RopeArgs(ctypes.Structure):
+    _fields_ = [("x", ctypes.c_void_p), ("cos_t", ctypes.c_void_p), ("sin_t", ctypes.c_void_p),
+                ("out", ctypes.c_void_p)] + \
+        [(f"{t}_{s}", ctypes.c_int64) for t in "xo" for s in ("sb", "ss", "sh")] + \
+        [("x_half", ctypes.c_int64), ("t_ss", ctypes.c_int64), ("groups", ctypes.c_int64),
+         ("S", ctypes.c_int32), ("H", ctypes.c_int32), ("half", ctypes.c_int32),
+         ("nthreads", ctypes.c_int32)]
+
+
+def rope(x_ptr: int, cos_ptr: int, sin_ptr: int, out_ptr: int, B: int, S: int, H: int, D: int,
+         x_strides, out_strides, x_half: int, table_stride: int) -> Launch:
+    """Split-half rotary embedding of bf16 x (B, S, H, D) read through element
+    strides (sb, ss, sh) with d contiguous, the second half ``x_half``
+    elements after the first; fp32 cos / sin tables indexed [s * table_stride
+    + d]; bf16 out through ``out_strides``."""
+    if D % 16 or D <= 0:
+        raise LaunchError(f"rope needs the head dim to be a multiple of 16, got {D}")
+    half = D // 2
+    if any(int(s) % 8 for s in tuple(x_strides) + tuple(out_strides) + (x_half,)):
+        raise LaunchError("rope strides must keep 16-byte alignment")
+    if table_stride % 4 or table_stride < half:
+        raise LaunchError("rope tables need a row stride that is a multiple of 4 and covers D/2")
+    if any(p % 16 for p in (x_ptr, cos_ptr, sin_ptr, out_ptr)):
+        raise LaunchError("rope operands must be 16-byte aligned")
+    groups = B * S * H * (half // 8)
+    blocks = max(1, min((groups + 255) // 256, 65536))
+    args = RopeArgs(x_ptr, cos_ptr, sin_ptr, out_ptr, *[int(s) for s in x_strides],
+                    *[int(s) for s in out_strides], int(x_half), int(table_stride), groups,
+                    S, H, half, blocks * 256)
+    return Launch("rope", "nk_rope_bf16", (blocks, 1, 1), (256, 1, 1), args,
+                  bytes=2 * B * S * H * D * 2 + 2 * S * half * 4, flops=6 * B * S * H * half)

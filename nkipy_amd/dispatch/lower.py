@@ -41,10 +41,10 @@ def _users(live: List[Node]) -> Dict[int, List[Node]]:
 
 class Lowering:
     def __init__(self, graph: Graph, patterns=None):
-        from nkipy_amd.dispatch.patterns import DEFAULT_PATTERNS
+        from nkipy_amd.dispatch.patterns import default_patterns
 
         self.g = graph
-        self.patterns = DEFAULT_PATTERNS if patterns is None else patterns
+        self.patterns = default_patterns() if patterns is None else patterns
         self.live = graph.live_nodes()
         self.users = _users(self.live)
         self.result_ids = {r.id for r in graph.results}

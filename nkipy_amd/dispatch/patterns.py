@@ -195,7 +195,9 @@ class SoftmaxPattern:
             if m is not None and m.validate(L):
                 yield m
 
-    def _match(self, L, n):
+    @staticmethod
+    def structure(L, n) -> Optional[Tuple[Value, List[Node]]]:
+        """``n`` (a divide) is a last-axis softmax of X -> (X, nodes)."""
         E, B2 = n.inputs
         shape = n.out.shape
         if not shape or shape[-1] < 1 or E.shape != shape:
@@ -218,11 +220,18 @@ class SoftmaxPattern:
         rm = reduce_last(m_val, "maximum")
         if rm is None or rm[0] is not X:
             return None
-        nodes = [n, rs[1], E.node, sub.node, rm[1]] + nodes_b1 + nodes_b2
+        return X, [n, rs[1], E.node, sub.node, rm[1]] + nodes_b1 + nodes_b2
+
+    def _match(self, L, n):
+        st = self.structure(L, n)
+        if st is None:
+            return None
+        X, nodes = st
+        sub, rm = nodes[3], nodes[4]
         x_in = X
         if op_of(X) == "convert" and X.dtype == dt.float32 and \
                 X.node.inputs[0].dtype in (dt.bfloat16, dt.float16) and X.id not in L.result_ids and \
-                all(id(u) in {id(sub.node), id(rm[1])} for u in _users_of(L, X)):
+                all(id(u) in {id(sub), id(rm)} for u in _users_of(L, X)):
             x_in = X.node.inputs[0]
             nodes.append(X.node)
         out, extra = _fold_output_convert(L, n.out, (dt.bfloat16, dt.float32, dt.float16))
@@ -407,7 +416,8 @@ class RmsNormPattern:
             return None
         # residual
         x, r, h_out, round_h = Hs, None, None, True
-        if op_of(Hs) == "add" and Hs.node.inputs[0].shape == shape and Hs.node.inputs[1].shape == shape:
+        if op_of(Hs) == "add" and id(Hs.node) not in L.covered and \
+                Hs.node.inputs[0].shape == shape and Hs.node.inputs[1].shape == shape:
             a, b = Hs.node.inputs
             if a.dtype == T and b.dtype == T:
                 x, r = a, b
@@ -458,13 +468,24 @@ class RmsNormPattern:
         return RmsNormMatch(nodes, x, r, w, out, h_out, eps, round_h, mul_recip)
 
 
-def _default_patterns():
+_DEFAULT = []
+
+
+def default_patterns():
+    """The pattern list the lowering tries, in order (built on first use)."""
+    if not _DEFAULT:
+        _DEFAULT.extend(_build_default_patterns())
+    return _DEFAULT
+
+
+def _build_default_patterns():
+    from nkipy_amd.dispatch.patterns_attention import AttentionPattern, RopePattern
     from nkipy_amd.dispatch.patterns_gemm import GemmPattern, SwigluPattern
     from nkipy_amd.dispatch.patterns_linattn import LinearAttentionPattern
 
-    # larger structures first: they contain matmuls the GEMM pattern would claim
-    return [LinearAttentionPattern(), SwigluPattern(), SoftmaxPattern(), RmsNormPattern(),
-            GemmPattern()]
+    # larger structures first: they contain matmuls / softmaxes that smaller
+    # patterns would claim; GEMMs before RMSNorm so that a residual add
+    # after a projection goes into the GEMM epilogue
+    return [LinearAttentionPattern(), AttentionPattern(), RopePattern(), SwigluPattern(),
+            GemmPattern(), SoftmaxPattern(), RmsNormPattern()]
 
-
-DEFAULT_PATTERNS = _default_patterns()

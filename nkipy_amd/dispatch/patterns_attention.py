@@ -1,0 +1,361 @@
+"""Attention-block patterns -> csrc/kernels/rope.hip and attention.hip.
+
+Rotary embedding, split-half form (examples/models/qwen3/kernels/rope.py:
+23-48), anchored on the ``np.concatenate`` that joins the two halves::
+
+    x0, x1 = x[..., :D/2], x[..., D/2:]          (x bf16, upcast to fp32)
+    out = concatenate([x0 * cos - x1 * sin, x0 * sin + x1 * cos], -1).astype(bf16)
+
+with fp32 cos / sin tables indexed by one position axis and the frequency
+(broadcast over the other axes).
+
+Causal softmax attention with grouped-query heads (examples/models/qwen3/
+kernels/attention.py:109-140; tests/kernels/llama_decoder_dynamo.py:
+180-288), anchored on the second product::
+
+    scores = (q @ k_t) * scale      (or / c)           fp32, q / k bf16 upcast
+    scores = scores + mask          mask = triu(<= -1e4, k=1), zeros below
+    p = softmax(scores, -1)
+    o = (p @ v)[.transpose(0, 2, 1, 3)][.reshape(..)].astype(bf16)
+
+q, k and v are read in place through strided views (``views.resolve``):
+``np.split`` of a fused QKV projection, reshapes into heads, transposes and
+``np.repeat`` of the KV heads cost no copies.  The additive mask must be
+large enough that exp() of a masked score underflows to exactly zero in
+fp32, which makes it identical to dropping the key.
+"""
+
+from __future__ import annotations
+
+from typing import List, Optional, Tuple
+
+import numpy as np
+
+from nkipy_amd.core import dtypes as dt
+from nkipy_amd.core.backend.ir import Node, Value
+from nkipy_amd.dispatch import launchers as LA
+from nkipy_amd.dispatch.patterns import (
+    LaunchStep, Match, SoftmaxPattern, _users_of, op_of, scalar_value,
+)
+from nkipy_amd.dispatch.views import View, resolve
+
+MASK_LIMIT = -1.0e4
+
+
+def _contiguous(shape) -> List[int]:
+    s, out = 1, []
+    for n in reversed(shape):
+        out.append(s)
+        s *= int(n)
+    return out[::-1]
+
+
+def _const_payload(v: Value) -> Optional[np.ndarray]:
+    if v.node is None or v.node.op != "constant":
+        return None
+    p = v.node.attrs["value"]
+    return dt.to_float32(p) if p.dtype.fields is not None else np.asarray(p, np.float32)
+
+
+def _owned(L, view: View, inside: set) -> List[Node]:
+    """The view's layout nodes (and a constant base) if they feed only the match."""
+    chain = list(view.nodes)
+    if view.base.node is not None and view.base.node.op == "constant":
+        chain.append(view.base.node)
+    ids = set(inside) | {id(n) for n in chain}
+    for n in chain:
+        if n.out.id in L.result_ids or any(id(u) not in ids for u in _users_of(L, n.out)):
+            return []
+    return chain
+
+
+def _bf16_view(v: Value) -> Optional[View]:
+    vw = resolve(v)
+    return vw if vw.base.dtype == dt.bfloat16 else None
+
+
+# ---------------------------------------------------------------------------
+# RoPE
+# ---------------------------------------------------------------------------
+class RopeMatch(Match):
+    name = "rope"
+
+    def __init__(self, nodes, x: View, x_half: int, cos: View, sin: View, roles, out: Value):
+        ins = [x.base, cos.base, sin.base]
+        super().__init__(nodes, list(dict.fromkeys(ins)), [out])
+        self.x, self.x_half, self.cos, self.sin, self.roles, self.out = x, x_half, cos, sin, roles, out
+
+    def steps(self, plan):
+        x, cos, sin, out = self.x, self.cos, self.sin, self.out
+        (B, S, H), x_str, o_str, t_ss = self.roles
+        D = out.shape[-1]
+        xi, ti = x.base.dtype.itemsize, 4
+
+        def make(addr):
+            return LA.rope(addr(x.base) + xi * x.offset, addr(cos.base) + ti * cos.offset,
+                           addr(sin.base) + ti * sin.offset, addr(out), B, S, H, D,
+                           x_str, o_str, self.x_half, t_ss)
+
+        return [LaunchStep("rope", f"rope B={B} S={S} H={H} D={D}", self.inputs, self.outputs, make)]
+
+
+class RopePattern:
+    def find(self, L):
+        for n in L.live:
+            if n.op != "concatenate" or id(n) in L.covered:
+                continue
+            m = self._match(L, n)
+            if m is not None and m.validate(L):
+                yield m
+
+    @staticmethod
+    def _product(v: Value):
+        """v = a * b with one bf16 activation view and one fp32 table view."""
+        if op_of(v) != "multiply":
+            return None
+        for a, b in (v.node.inputs, v.node.inputs[::-1]):
+            xa = _bf16_view(a)
+            tb = resolve(b, widen_ok=False)
+            if xa is not None and tb.base.dtype == dt.float32 and not tb.widened:
+                return xa, tb, v.node
+        return None
+
+    def _match(self, L, n: Node):
+        if len(n.inputs) != 2 or n.attrs["dimension"] != n.out.ndim - 1 or n.out.dtype != dt.float32:
+            return None
+        A, Bv = n.inputs
+        nd = n.out.ndim
+        half = A.shape[-1]
+        if Bv.shape != A.shape or nd < 2 or nd > 4 or half % 8:
+            return None
+        if op_of(A) != "subtract" or op_of(Bv) != "add":
+            return None
+        pa = [self._product(t) for t in A.node.inputs]
+        pb = [self._product(t) for t in Bv.node.inputs]
+        if any(p is None for p in pa + pb):
+            return None
+        (x0, c0, m0), (x1, s0, m1) = pa
+        key = lambda vw: (vw.base.id, vw.offset, [tuple(d) for d in vw.dims])
+        # B = x0 * sin + x1 * cos, either order
+        if key(pb[0][0]) == key(x0) and key(pb[1][0]) == key(x1):
+            s1, c1 = pb[0][1], pb[1][1]
+        elif key(pb[1][0]) == key(x0) and key(pb[0][0]) == key(x1):
+            s1, c1 = pb[1][1], pb[0][1]
+        else:
+            return None
+        if x0.base is not x1.base or [tuple(d) for d in x0.dims] != [tuple(d) for d in x1.dims]:
+            return None
+        x_half = x1.offset - x0.offset
+        # the tables: one position axis, frequency contiguous, same content in both uses
+        for ta, tb in ((c0, c1), (s0, s1)):
+            pa_, pb_ = _const_payload(ta.base), _const_payload(tb.base)
+            if ta.base is not tb.base:
+                if pa_ is None or pb_ is None or not np.array_equal(ta.materialize_check(pa_),
+                                                                    tb.materialize_check(pb_)):
+                    return None
+            elif key(ta) != key(tb):
+                return None
+        pos = [d for d in range(nd - 1) if c0.simple(d) != 0]
+        if len(pos) != 1 or c0.simple(nd - 1) != 1 or x0.simple(nd - 1) != 1:
+            return None
+        sd = pos[0]
+        if s0.simple(sd) != c0.simple(sd) or s0.simple(nd - 1) != 1 or \
+                any(s0.simple(d) != 0 for d in range(nd - 1) if d != sd):
+            return None
+        rest = [d for d in range(nd - 1) if d != sd]
+        xs = [x0.simple(d) for d in range(nd - 1)]
+        if any(s is None for s in xs):
+            return None
+        out, tail = n.out, []
+        us = _users_of(L, out)
+        if out.id in L.result_ids or len(us) != 1 or us[0].op != "convert" or us[0].out.dtype != dt.bfloat16:
+            return None
+        tail.append(us[0])
+        out = us[0].out
+        ostr = _contiguous(out.shape)
+        shape = out.shape
+        # kernel roles: b = first other axis, h = second other axis, s = position axis
+        b_ax = rest[0] if len(rest) >= 1 else None
+        h_ax = rest[1] if len(rest) >= 2 else None
+        size = lambda ax: shape[ax] if ax is not None else 1
+        stride = lambda arr, ax: arr[ax] if ax is not None else 0
+        roles = ((size(b_ax), shape[sd], size(h_ax)),
+                 (stride(xs, b_ax), xs[sd], stride(xs, h_ax)),
+                 (stride(ostr, b_ax), ostr[sd], stride(ostr, h_ax)),
+                 c0.simple(sd))
+        if c0.shape[sd] < shape[sd]:
+            return None
+        nodes = [n, A.node, Bv.node, m0, m1, pb[0][2], pb[1][2]] + tail
+        inside = {id(q) for q in nodes}
+        for vw in (c1, s1):
+            if vw.base is not c0.base and vw.base is not s0.base:
+                nodes += _owned(L, vw, inside)
+        return RopeMatch(nodes, x0, x_half, c0, s0, roles, out)
+
+
+# ---------------------------------------------------------------------------
+# causal GQA attention
+# ---------------------------------------------------------------------------
+class AttentionMatch(Match):
+    name = "attention"
+
+    def __init__(self, nodes, q: View, k: View, v: View, out: Value, dims, scale, causal, o_str):
+        ins = list(dict.fromkeys([q.base, k.base, v.base]))
+        super().__init__(nodes, ins, [out])
+        self.q, self.k, self.v, self.out = q, k, v, out
+        self.dims, self.scale, self.causal, self.o_str = dims, scale, causal, o_str
+
+    def steps(self, plan):
+        q, k, v, out = self.q, self.k, self.v, self.out
+        B, S, Hq, Hkv, D, strides = self.dims
+
+        def make(addr):
+            return LA.attention(addr(q.base) + 2 * q.offset, addr(k.base) + 2 * k.offset,
+                                addr(v.base) + 2 * v.offset, addr(out), B, S, Hq, Hkv, D,
+                                self.scale, dict(strides, o=self.o_str), causal=self.causal)
+
+        desc = f"{'causal ' if self.causal else ''}attention B={B} S={S} Hq={Hq} Hkv={Hkv} D={D}"
+        return [LaunchStep("attention", desc, self.inputs, self.outputs, make)]
+
+
+def _qk_dot(n: Node) -> bool:
+    at = n.attrs
+    return (n.op == "dot" and n.out.ndim == 4 and tuple(at["lhs_batch"]) == (0, 1)
+            and tuple(at["rhs_batch"]) == (0, 1) and tuple(at["lhs_contract"]) == (3,)
+            and tuple(at["rhs_contract"]) == (2,))
+
+
+class AttentionPattern:
+    def find(self, L):
+        for n in L.live:
+            if id(n) in L.covered or not _qk_dot(n):
+                continue
+            m = self._match(L, n)
+            if m is not None and m.validate(L):
+                yield m
+
+    @staticmethod
+    def _scaled(v: Value):
+        """v = dot * c | c * dot | dot / c -> (dot node, scale, nodes)."""
+        if op_of(v) == "dot":
+            return v.node, 1.0, []
+        if op_of(v) == "multiply":
+            for d, c in (v.node.inputs, v.node.inputs[::-1]):
+                cv, cn = scalar_value(c)
+                if cv is not None and op_of(d) == "dot":
+                    return d.node, cv, [v.node] + cn
+        if op_of(v) == "divide":
+            d, c = v.node.inputs
+            cv, cn = scalar_value(c)
+            if cv is not None and cv != 0 and op_of(d) == "dot":
+                return d.node, 1.0 / cv, [v.node] + cn
+        return None
+
+    @staticmethod
+    def _mask(v: Value, S: int):
+        """An additive causal mask over (b, h, s, t) -> view, or None."""
+        mv = resolve(v, widen_ok=False)
+        payload = _const_payload(mv.base)
+        if payload is None or mv.shape[-2:] != (S, S):
+            return None
+        if mv.simple(0) != 0 or mv.simple(1) != 0:
+            return None
+        m = mv.materialize_check(payload.reshape(mv.base.shape))[0, 0]
+        lower = np.tril(np.ones((S, S), bool))
+        if np.any(m[lower] != 0) or np.any(m[~lower] > MASK_LIMIT):
+            return None
+        return mv
+
+    def _match(self, L, n2: Node):
+        p_val, kv_op = n2.inputs
+        nodes = [n2]
+        while op_of(p_val) in ("convert", "copy") and p_val.dtype == dt.float32:
+            nodes.append(p_val.node)
+            p_val = p_val.node.inputs[0]
+        if op_of(p_val) != "divide" or p_val.dtype != dt.float32:
+            return None
+        st = SoftmaxPattern.structure(L, p_val.node)
+        if st is None:
+            return None
+        X, smx = st
+        nodes += smx
+        causal, mask_nodes = False, []
+        sc = self._scaled(X)
+        if sc is None and op_of(X) == "add":
+            for a, b in (X.node.inputs, X.node.inputs[::-1]):
+                sc = self._scaled(a)
+                if sc is None:
+                    continue
+                mv = self._mask(b, a.shape[-1])
+                if mv is None:
+                    sc = None
+                    continue
+                causal = True
+                nodes.append(X.node)
+                mask_nodes = (mv, b)
+                break
+        if sc is None:
+            return None
+        d1, scale, snodes = sc
+        if not _qk_dot(d1) or d1.out.dtype != dt.float32:
+            return None
+        nodes += [d1] + snodes
+        q = _bf16_view(d1.inputs[0])
+        k = _bf16_view(d1.inputs[1])
+        v = _bf16_view(kv_op)
+        if q is None or k is None or v is None:
+            return None
+        B, Hq, S, D = q.shape
+        if k.shape != (B, Hq, D, S) or v.shape != (B, Hq, S, D) or n2.out.shape != (B, Hq, S, D):
+            return None
+        qs = [q.simple(0), q.simple(2), q.simple(1)]
+        kg, vg = k.grouped(1), v.grouped(1)
+        ks = [k.simple(0), k.simple(3)]
+        vs = [v.simple(0), v.simple(2)]
+        if None in qs + ks + vs or kg is None or vg is None:
+            return None
+        if q.simple(3) != 1 or k.simple(2) != 1 or v.simple(3) != 1:
+            return None
+        if kg[0] != vg[0] or kg[2] != vg[2] or kg[0] * kg[2] != Hq:
+            return None
+        Hkv = kg[0]
+        # output tail: transposes, casts and a reshape after the second product
+        out, perm, reshaped = n2.out, [0, 1, 2, 3], False
+        while True:
+            us = _users_of(L, out)
+            if out.id in L.result_ids or len(us) != 1:
+                break
+            u = us[0]
+            if u.op == "transpose" and not reshaped:
+                perm = [perm[p] for p in u.attrs["permutation"]]
+            elif u.op in ("convert", "copy") and (u.out.dtype == out.dtype or (
+                    out.dtype == dt.float32 and u.out.dtype == dt.bfloat16)):
+                pass
+            elif u.op == "reshape" and not reshaped:
+                reshaped = True
+            else:
+                break
+            nodes.append(u)
+            out = u.out
+        if out.dtype != dt.bfloat16 or perm not in ([0, 1, 2, 3], [0, 2, 1, 3]):
+            return None
+        logical = [(B, Hq, S, D)[p] for p in perm]
+        cs = _contiguous(logical)
+        pos = {ax: i for i, ax in enumerate(perm)}  # dot axis -> position in the output
+        o_str = (cs[pos[0]], cs[pos[2]], cs[pos[1]])
+        try:
+            LA.attention(16, 16, 16, 16, B, S, Hq, Hkv, D, scale,
+                         {"q": qs, "k": (ks[0], ks[1], kg[1]), "v": (vs[0], vs[1], vg[1]), "o": o_str},
+                         causal=causal)
+        except LA.LaunchError:
+            return None
+        if any((vw.offset * 2) % 16 for vw in (q, k, v)):
+            return None
+        if mask_nodes:
+            mv, b = mask_nodes
+            nodes += _owned(L, mv, {id(x) for x in nodes})
+        strides = {"q": tuple(qs), "k": (ks[0], ks[1], kg[1]), "v": (vs[0], vs[1], vg[1])}
+        return AttentionMatch(nodes, q, k, v, out, (B, S, Hq, Hkv, D, strides), scale, causal, o_str)
+
+
+ATTENTION_PATTERNS = [AttentionPattern(), RopePattern()]

@@ -35,10 +35,28 @@ from nkipy_amd.dispatch.patterns import (
 
 
 def _strip_converts(v: Value) -> Tuple[Value, List[Node]]:
+    """Follow float converts down (used where the cast of a dequantised
+    weight is absorbed into the kernel's fp32 epilogue)."""
     nodes = []
     while op_of(v) in ("convert", "copy") and dt.is_float(v.node.inputs[0].dtype):
         nodes.append(v.node)
         v = v.node.inputs[0]
+    return v, nodes
+
+
+_EXACT_WIDEN = {(dt.bfloat16, dt.float32), (dt.float16, dt.float32)}
+
+
+def _strip_widening(v: Value) -> Tuple[Value, List[Node]]:
+    """Follow converts that preserve every value (bf16 / f16 -> f32, same-dtype
+    copies) down to the narrow source."""
+    nodes = []
+    while op_of(v) in ("convert", "copy"):
+        src = v.node.inputs[0]
+        if src.dtype != v.dtype and (src.dtype, v.dtype) not in _EXACT_WIDEN:
+            break
+        nodes.append(v.node)
+        v = src
     return v, nodes
 
 
@@ -90,7 +108,7 @@ def resolve_weight(rhs: Value) -> Optional[Weight]:
         if dq is not None:
             w8, sc, dn = dq
             return Weight(w8, "nt", nodes + dn, sc)
-        src_b, sn = _strip_converts(src)
+        src_b, sn = _strip_widening(src)
         if src_b.dtype == dt.bfloat16:
             return Weight(src_b, "nt", nodes + sn)
         return None
@@ -98,7 +116,7 @@ def resolve_weight(rhs: Value) -> Optional[Weight]:
     if dq is not None:
         w8, sc, dn = dq
         return Weight(w8, "nn", dn, sc)
-    b, sn = _strip_converts(rhs)
+    b, sn = _strip_widening(rhs)
     if b.dtype == dt.bfloat16:
         return Weight(b, "nn", sn)
     return None
@@ -114,7 +132,7 @@ def _plain_dot(n: Node) -> bool:
 
 
 def resolve_activation(lhs: Value) -> Optional[Tuple[Value, List[Node]]]:
-    x, nodes = _strip_converts(lhs)
+    x, nodes = _strip_widening(lhs)
     if x.dtype != dt.bfloat16:
         return None
     return x, nodes
@@ -295,8 +313,8 @@ class SwigluPattern:
             if sl is None:
                 continue
             g, snodes = sl
-            g0, gcn = _strip_converts(g)
-            u0, ucn = _strip_converts(u_val)
+            g0, gcn = _strip_widening(g)
+            u0, ucn = _strip_widening(u_val)
             nodes = [n] + snodes + gcn + ucn
             m = self._fused_gate_up(L, n, g0, u0, nodes) or self._two_weights(L, n, g0, u0, nodes)
             if m is not None:

@@ -11,3 +11,7 @@ from nkipy_amd.kernels.feedforward import (  # noqa: F401
     feedforward_bias_kernel, feedforward_kernel, linear_nt_kernel, swiglu_mlp_kernel,
 )
 from nkipy_amd.kernels.linear_attention import chunked_linear_attention_kernel  # noqa: F401
+from nkipy_amd.kernels.decoder import (  # noqa: F401
+    attention_block_fp8, causal_gqa_attention_kernel, llama_decoder_layer_fp8, mlp_block_fp8,
+    qkv_rope_fp8, rope_kernel, rope_tables,
+)

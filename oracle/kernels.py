@@ -206,3 +206,130 @@ def causal_attention_f64_loop(q, k, v):
                 w = np.exp(w - w.max())
                 out[b, t, h] = (w[:, None] * v[b, :t + 1, h // rep]).sum(0) / w.sum()
     return out
+
+
+# ---------------------------------------------------------------------------
+# Rotary embedding -- examples/models/qwen3/kernels/rope.py:4-48 (tables:
+# float64 frequencies 1 / theta^(2i/d), fp32 cos / sin of position * freq;
+# split-half rotation in fp32).
+# ---------------------------------------------------------------------------
+
+
+def rope_tables(head_dim, seq_len, theta):
+    freqs = 1.0 / (theta ** (np.arange(0, head_dim, 2)[: head_dim // 2] / head_dim))
+    ang = np.outer(np.arange(seq_len, dtype=np.float32), freqs)
+    return np.cos(ang, dtype=np.float32), np.sin(ang, dtype=np.float32)
+
+
+def rope_split_half(x, cos, sin):
+    """x (B, S, H, D) fp32 values; tables (S, D/2).  fp32 result."""
+    x = np.asarray(x, np.float32)
+    h = x.shape[-1] // 2
+    c = cos[None, :, None, :]
+    s = sin[None, :, None, :]
+    x0, x1 = x[..., :h], x[..., h:]
+    return np.concatenate([x0 * c - x1 * s, x0 * s + x1 * c], axis=-1)
+
+
+def rope_complex_f64(x, theta):
+    """Rotation as complex multiplication in float64 (pins rope_split_half):
+    (x0 + i x1) * exp(i * pos * freq)."""
+    x = np.asarray(x, np.float64)
+    B, S, H, D = x.shape
+    h = D // 2
+    freqs = theta ** (-2.0 * np.arange(h) / D)
+    ph = np.exp(1j * np.arange(S)[:, None] * freqs[None, :])[None, :, None, :]
+    z = (x[..., :h] + 1j * x[..., h:]) * ph
+    return np.concatenate([z.real, z.imag], axis=-1)
+
+
+# ---------------------------------------------------------------------------
+# fp8 decoder layer -- tests/kernels/llama_decoder_dynamo.py:95-337 with the
+# weights of a torch Linear (out, in) stored as e4m3fn codes and a per-output
+# channel fp32 scale; the cast points of the NumPy kernel
+# (bf16 storage after each projection, after RoPE, after attention, after
+# each residual add; fp32 products, softmax and RoPE).
+# ---------------------------------------------------------------------------
+
+
+def linear_fp8(x, codes, scale):
+    from oracle.numerics import dequantize_e4m3fn
+
+    w = dequantize_e4m3fn(codes, scale, axis=1)
+    return np.asarray(x, np.float32) @ w.T
+
+
+def decoder_attention_fp8(x, w):
+    """Returns (attention output before o_proj (B, S, Hq*D), z = x + o_proj)."""
+    B, S, hid = x.shape
+    Hq, Hkv, eps, theta = w["n_heads"], w["n_kv_heads"], w["eps"], w["rope_theta"]
+    D = hid // Hq
+    h = rmsnorm_kernel(x, w["attn_norm"], eps, round_out=bf16_round)
+    qkv = bf16_round(linear_fp8(h, w["wqkv"], w["wqkv_scale"]))
+    q = qkv[..., :Hq * D].reshape(B, S, Hq, D)
+    k = qkv[..., Hq * D:(Hq + Hkv) * D].reshape(B, S, Hkv, D)
+    v = qkv[..., (Hq + Hkv) * D:].reshape(B, S, Hkv, D)
+    cos, sin = rope_tables(D, S, theta)
+    q = bf16_round(rope_split_half(q, cos, sin))
+    k = bf16_round(rope_split_half(k, cos, sin))
+    a = bf16_round(causal_gqa_attention(q, k, v)).reshape(B, S, Hq * D)
+    z = bf16_round(x + bf16_round(linear_fp8(a, w["wo"], w["wo_scale"])))
+    return a, z
+
+
+def decoder_mlp_fp8(z, w):
+    """Returns (silu(gate) * up in bf16, y = z + down)."""
+    h = rmsnorm_kernel(z, w["mlp_norm"], w["eps"], round_out=bf16_round)
+    g = linear_fp8(h, w["w_gate"], w["w_gate_scale"])
+    u = linear_fp8(h, w["w_up"], w["w_up_scale"])
+    act = bf16_round(silu(g) * u)
+    y = bf16_round(z + bf16_round(linear_fp8(act, w["w_down"], w["w_down_scale"])))
+    return act, y
+
+
+def decoder_layer_fp8(x, w):
+    a, z = decoder_attention_fp8(x, w)
+    act, y = decoder_mlp_fp8(z, w)
+    return {"attn": a, "z": z, "act": act, "y": y}
+
+
+def decoder_layer_fp8_rows(x_seq, w, rows):
+    """The layer for selected positions of ONE sequence x_seq (S, hidden):
+    projections of every position up to max(rows), attention and everything
+    after it only for ``rows``.  Same cast points as decoder_layer_fp8."""
+    S, hid = x_seq.shape
+    Hq, Hkv, eps, theta = w["n_heads"], w["n_kv_heads"], w["eps"], w["rope_theta"]
+    D = hid // Hq
+    rows = np.asarray(rows)
+    T = int(rows.max()) + 1
+    x = np.asarray(x_seq[:T], np.float32)
+    h = rmsnorm_kernel(x, w["attn_norm"], eps, round_out=bf16_round)
+    qkv = bf16_round(linear_fp8(h, w["wqkv"], w["wqkv_scale"]))
+    cos, sin = rope_tables(D, S, theta)
+    q = bf16_round(rope_split_half(qkv[None, rows, :Hq * D].reshape(1, len(rows), Hq, D),
+                                   cos[rows], sin[rows]))[0]
+    k = bf16_round(rope_split_half(qkv[None, :, Hq * D:(Hq + Hkv) * D].reshape(1, T, Hkv, D),
+                                   cos[:T], sin[:T]))[0]
+    v = qkv[:, (Hq + Hkv) * D:].reshape(T, Hkv, D)
+    rep = Hq // Hkv
+    a = np.empty((len(rows), Hq, D), np.float32)
+    for i, t in enumerate(rows):
+        for hh in range(Hq):
+            g = hh // rep
+            s = (k[:t + 1, g] @ q[i, hh]) * np.float32(1.0 / np.sqrt(D))
+            p = np.exp(s - s.max())
+            a[i, hh] = (p / p.sum()) @ v[:t + 1, g]
+    a = bf16_round(a).reshape(len(rows), Hq * D)
+    z = bf16_round(x[rows] + bf16_round(linear_fp8(a, w["wo"], w["wo_scale"])))
+    act, y = decoder_mlp_fp8(z, w)
+    return {"attn": a, "z": z, "act": act, "y": y}
+
+
+def decoder_oproj_residual(x, attn, w):
+    """z = x + o_proj(attn), both rounded to bf16 (x, attn: (..., hidden))."""
+    return bf16_round(np.asarray(x, np.float32) + bf16_round(linear_fp8(attn, w["wo"], w["wo_scale"])))
+
+
+def decoder_down_residual(z, act, w):
+    """y = z + down(act), both rounded to bf16."""
+    return bf16_round(np.asarray(z, np.float32) + bf16_round(linear_fp8(act, w["w_down"], w["w_down_scale"])))

@@ -1,0 +1,187 @@
+"""GPU parity of the fp8 decoder layer (RoPE, causal GQA attention, fp8
+projections, SwiGLU, residuals) traced from the NumPy kernels, against the
+oracle's restatement with the same cast points."""
+
+import numpy as np
+import pytest
+import torch
+
+from nkipy_amd.core import dtypes as dt
+from nkipy_amd.kernels.decoder import (
+    causal_gqa_attention_kernel, linear_fp8, llama_decoder_layer_fp8, qkv_rope_fp8, rope_kernel,
+    rope_tables,
+)
+from nkipy_amd.kernels.feedforward import silu_kernel_
+from nkipy_amd.kernels.rmsnorm import rmsnorm_kernel
+from nkipy_amd.runtime import DeviceKernel, DeviceTensor
+from oracle import kernels as K
+from oracle import numerics as N
+
+pytestmark = pytest.mark.gpu
+
+DECODER_KINDS = ["rmsnorm", "gemm", "rope", "rope", "attention", "gemm", "rmsnorm", "gemm_swiglu", "gemm"]
+
+
+def _close(got, ref, tol=2e-2, axis=None):
+    """rtol 2e-2 with an absolute floor of 2e-2 x RMS (of each row along
+    ``axis``, or of the whole tensor)."""
+    ref = np.asarray(ref, np.float64)
+    scale = np.sqrt(np.mean(ref ** 2, axis=axis, keepdims=axis is not None))
+    err = np.abs(np.asarray(got, np.float64) - ref) / (np.abs(ref) + scale)
+    assert err.max() <= tol, err.max()
+
+
+def _quantize(rng, shape):
+    """N(0, 0.02) weights -> e4m3fn codes with per-output-channel scales
+    amax / 448 (torch's fp8 conversion, the same RNE the oracle pins)."""
+    w = torch.from_numpy((rng.standard_normal(shape, dtype=np.float32) * 0.02))
+    scale = (w.abs().amax(dim=1) / 448.0).clamp_min(1e-12)
+    codes = (w / scale[:, None]).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    return codes, scale.numpy().astype(np.float32)
+
+
+def _weights(rng, hid, Hq, Hkv, F):
+    D = hid // Hq
+    w = {"n_heads": Hq, "n_kv_heads": Hkv, "eps": 1e-5, "rope_theta": 5.0e5,
+         "attn_norm": np.ones(hid, np.float32), "mlp_norm": np.ones(hid, np.float32)}
+    for name, shape in (("wqkv", ((Hq + 2 * Hkv) * D, hid)), ("wo", (hid, Hq * D)),
+                        ("w_gate", (F, hid)), ("w_up", (F, hid)), ("w_down", (hid, F))):
+        w[name], w[name + "_scale"] = _quantize(rng, shape)
+    return w
+
+
+def _args(x, w):
+    f8 = lambda c: c.view(dt.float8_e4m3fn)
+    return [dt.to_bf16(x), dt.to_bf16(w["attn_norm"]), f8(w["wqkv"]), w["wqkv_scale"],
+            f8(w["wo"]), w["wo_scale"], dt.to_bf16(w["mlp_norm"]), f8(w["w_gate"]), w["w_gate_scale"],
+            f8(w["w_up"]), w["w_up_scale"], f8(w["w_down"]), w["w_down_scale"]]
+
+
+def _probe_kernel(Hq, Hkv):
+    """The decoder layer returning the attention output, the residual stream
+    after attention and the SwiGLU activation as well."""
+
+    def decoder_probe(x, an, wqkv, sq, wo, so, mn, wg, sg, wu, su, wd, sd):
+        h = rmsnorm_kernel(x, an, 1e-5)
+        xq, xk, xv = qkv_rope_fp8(h, wqkv, sq, Hq, Hkv, 5.0e5)
+        a = causal_gqa_attention_kernel(xq, xk, xv)
+        z = x + linear_fp8(a, wo, so).astype(x.dtype)
+        h2 = rmsnorm_kernel(z, mn, 1e-5)
+        act = (silu_kernel_(linear_fp8(h2, wg, sg)) * linear_fp8(h2, wu, su)).astype(x.dtype)
+        y = z + linear_fp8(act, wd, sd).astype(x.dtype)
+        return y, a, z, act
+
+    return decoder_probe
+
+
+def _check_blocks(x, w, a, z, act, y, ref, Hq):
+    """Each block against the oracle fed the GPU's own input to that block
+    (attention from x; o_proj + residual from the GPU attention; RMSNorm +
+    SwiGLU from the GPU residual stream; down + residual from the GPU
+    activation), then the layer output against the oracle's end-to-end run."""
+    heads = lambda t: t.reshape(t.shape[:-1] + (Hq, 128))
+    _close(heads(a), heads(ref["attn"]), axis=-1)
+    _close(z, K.decoder_oproj_residual(x, a, w))
+    _close(act, K.decoder_mlp_fp8(z, w)[0])
+    _close(y, K.decoder_down_residual(z, act, w))
+    _close(y, ref["y"])
+
+
+@pytest.mark.parametrize("shape", [(1, 128, 1, 1), (2, 256, 4, 2), (1, 384, 4, 4)])
+def test_rope_bit_exact(gpu, shape):
+    """RoPE traced alone: fp32 products and differences, one bf16 rounding."""
+    B, S, H, D = shape[0], shape[1], shape[2], 128
+    rng = np.random.default_rng(S + H)
+    x = N.bf16_round(rng.standard_normal((B, S, H, D)) * 2)
+    cos, sin = rope_tables(D, S, 5.0e5)
+
+    def rope_only(x):
+        return rope_kernel(x, cos, sin).astype(x.dtype)
+
+    dk = DeviceKernel.compile_and_load(rope_only, dt.to_bf16(x))
+    assert dk.plan.kernel_kinds == ["rope"]
+    got = dt.to_float32(dk({"x": DeviceTensor.from_numpy(dt.to_bf16(x), name="x")})["output0"].numpy())
+    ocos, osin = K.rope_tables(D, S, 5.0e5)
+    np.testing.assert_array_equal(got, N.bf16_round(K.rope_split_half(x, ocos, osin)))
+
+
+def test_rope_reads_fused_qkv_in_place(gpu):
+    """q / k RoPE straight from the columns of a fused projection output."""
+    B, S, Hq, Hkv, D = 2, 128, 4, 2, 128
+    rng = np.random.default_rng(3)
+    qkv = N.bf16_round(rng.standard_normal((B, S, (Hq + 2 * Hkv) * D)))
+    cos, sin = rope_tables(D, S, 5.0e5)
+
+    def split_rope(qkv):
+        q, k, v = np.split(qkv, [Hq * D, (Hq + Hkv) * D], axis=-1)
+        q = rope_kernel(q.reshape(B, S, Hq, D), cos, sin).astype(qkv.dtype)
+        k = rope_kernel(k.reshape(B, S, Hkv, D), cos, sin).astype(qkv.dtype)
+        return q, k
+
+    dk = DeviceKernel.compile_and_load(split_rope, dt.to_bf16(qkv))
+    assert dk.plan.kernel_kinds == ["rope", "rope"]
+    out = dk({"qkv": DeviceTensor.from_numpy(dt.to_bf16(qkv), name="qkv")})
+    ocos, osin = K.rope_tables(D, S, 5.0e5)
+    q_ref = N.bf16_round(K.rope_split_half(qkv[..., :Hq * D].reshape(B, S, Hq, D), ocos, osin))
+    k_ref = N.bf16_round(K.rope_split_half(qkv[..., Hq * D:(Hq + Hkv) * D].reshape(B, S, Hkv, D), ocos, osin))
+    np.testing.assert_array_equal(dt.to_float32(out["output0"].numpy()), q_ref)
+    np.testing.assert_array_equal(dt.to_float32(out["output1"].numpy()), k_ref)
+
+
+@pytest.mark.parametrize("shape", [(1, 128, 1, 1), (2, 256, 4, 2), (1, 384, 8, 2)])
+def test_traced_gqa_attention(gpu, shape):
+    """np.repeat GQA attention traced onto the flash kernel (K / V read in
+    place through the repeat), against the oracle's matrix form."""
+    B, S, Hq, Hkv = shape
+    D = 128
+    rng = np.random.default_rng(S * Hq)
+    q, k, v = (N.bf16_round(rng.standard_normal((B, S, h, D))) for h in (Hq, Hkv, Hkv))
+    args = [dt.to_bf16(a) for a in (q, k, v)]
+    dk = DeviceKernel.compile_and_load(causal_gqa_attention_kernel, *args)
+    assert dk.plan.kernel_kinds == ["attention"]
+    ins = {n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(("xq", "xk", "xv"), args)}
+    got = dt.to_float32(dk(ins)["output0"].numpy()).reshape(B, S, Hq, D)
+    _close(got, K.causal_gqa_attention(q, k, v), axis=-1)
+
+
+def test_decoder_layer_small(gpu):
+    B, S, Hq, Hkv, F = 2, 256, 4, 2, 1024
+    hid = Hq * 128
+    rng = np.random.default_rng(21)
+    w = _weights(rng, hid, Hq, Hkv, F)
+    x = N.bf16_round(rng.standard_normal((B, S, hid)))
+    args = _args(x, w)
+    dk = DeviceKernel.compile_and_load(_probe_kernel(Hq, Hkv), *args)
+    assert dk.plan.kernel_kinds == DECODER_KINDS
+    names = ["x", "an", "wqkv", "sq", "wo", "so", "mn", "wg", "sg", "wu", "su", "wd", "sd"]
+    out = dk({n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(names, args)})
+    y, a, z, act = (dt.to_float32(out[f"output{i}"].numpy()) for i in range(4))
+    _check_blocks(x, w, a, z, act, y, K.decoder_layer_fp8(x, w), Hq)
+
+    # the product kernel (no probes) lowers to the same nine kernels
+    dk2 = DeviceKernel.compile_and_load(llama_decoder_layer_fp8, *args, n_heads=Hq, n_kv_heads=Hkv)
+    assert dk2.plan.kernel_kinds == DECODER_KINDS
+    names2 = [p.name for p in dk2.graph.parameters]
+    y2 = dt.to_float32(dk2({n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(names2, args)})
+                       ["output0"].numpy())
+    np.testing.assert_array_equal(y2, y)
+
+
+def test_decoder_layer_config_sampled(gpu):
+    """hidden 4096, 32 / 8 heads, FFN 14336, batch 8 x 2048 tokens; positions
+    of two sequences checked against the oracle's per-position form."""
+    B, S, Hq, Hkv, F = 8, 2048, 32, 8, 14336
+    hid = Hq * 128
+    rng = np.random.default_rng(5)
+    w = _weights(rng, hid, Hq, Hkv, F)
+    x = N.bf16_round(rng.standard_normal((B, S, hid), dtype=np.float32))
+    args = _args(x, w)
+    dk = DeviceKernel.compile_and_load(_probe_kernel(Hq, Hkv), *args)
+    assert dk.plan.kernel_kinds == DECODER_KINDS
+    names = ["x", "an", "wqkv", "sq", "wo", "so", "mn", "wg", "sg", "wu", "su", "wd", "sd"]
+    out = dk({n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(names, args)})
+    y, a, z, act = (out[f"output{i}"].numpy() for i in range(4))
+    rows = np.array([0, 1, 127, 128, 1029, 2047])
+    for b in (0, 7):
+        got = [dt.to_float32(t[b, rows]) for t in (a, z, act, y)]
+        _check_blocks(x[b, rows], w, *got, K.decoder_layer_fp8_rows(x[b], w, rows), Hq)

@@ -142,3 +142,73 @@ def test_causal_gqa_attention_vs_f64_loop():
     v = rng.standard_normal((1, 6, 2, 8)).astype(np.float32)
     np.testing.assert_allclose(K.causal_gqa_attention(q, k, v), K.causal_attention_f64_loop(q, k, v),
                                rtol=1e-5, atol=1e-6)
+
+
+def test_rope_split_half_is_the_complex_rotation():
+    rng = np.random.default_rng(11)
+    x = N.bf16_round(rng.standard_normal((2, 9, 3, 16)))
+    cos, sin = K.rope_tables(16, 9, 5.0e5)
+    y = K.rope_split_half(x, cos, sin)
+    np.testing.assert_allclose(y, K.rope_complex_f64(x, 5.0e5), rtol=1e-5, atol=2e-5)
+    # position 0 is the identity; each (i, i + D/2) pair keeps its length
+    np.testing.assert_array_equal(y[:, 0], x[:, 0])
+    n_in = x[..., :8] ** 2 + x[..., 8:] ** 2
+    n_out = y[..., :8] ** 2 + y[..., 8:] ** 2
+    np.testing.assert_allclose(n_out, n_in, rtol=1e-5, atol=1e-6)
+    # table closed form: angle = pos * theta^(-2i/D)
+    ang = np.arange(9)[:, None] * 5.0e5 ** (-2.0 * np.arange(8) / 16)
+    np.testing.assert_allclose(cos, np.cos(ang), atol=1e-6)
+    np.testing.assert_allclose(sin, np.sin(ang), atol=1e-6)
+
+
+def _decoder_weights(rng, hid, Hq, Hkv, F, zero=()):
+    D = hid // Hq
+    w = {"n_heads": Hq, "n_kv_heads": Hkv, "eps": 1e-5, "rope_theta": 5.0e5,
+         "attn_norm": N.bf16_round(rng.uniform(0.5, 1.5, hid)),
+         "mlp_norm": N.bf16_round(rng.uniform(0.5, 1.5, hid))}
+    for name, shape in (("wqkv", ((Hq + 2 * Hkv) * D, hid)), ("wo", (hid, Hq * D)),
+                        ("w_gate", (F, hid)), ("w_up", (F, hid)), ("w_down", (hid, F))):
+        m = rng.standard_normal(shape) * 0.02
+        if name in zero:
+            m = m * 0
+        w[name], w[name + "_scale"] = N.quantize_per_channel_e4m3fn(m, axis=1)
+    return w
+
+
+def test_decoder_rows_form_matches_full_layer():
+    """The per-position form (attention by a loop over keys) agrees with the
+    batched form (matrix attention) on the positions it computes."""
+    rng = np.random.default_rng(12)
+    B, S, hid, Hq, Hkv, F = 2, 24, 64, 4, 2, 96
+    w = _decoder_weights(rng, hid, Hq, Hkv, F)
+    x = N.bf16_round(rng.standard_normal((B, S, hid)))
+    full = K.decoder_layer_fp8(x, w)
+    rows = np.array([0, 5, 23])
+    part = K.decoder_layer_fp8_rows(x[1], w, rows)
+    for key in ("attn", "z", "act", "y"):
+        ref = full[key][1, rows]
+        err = np.abs(part[key] - ref) / (np.abs(ref) + np.sqrt(np.mean(ref ** 2)))
+        assert err.max() < 1e-2, key
+
+
+def test_decoder_zero_projections_and_gqa_sharing():
+    rng = np.random.default_rng(13)
+    B, S, hid, Hq, Hkv, F = 1, 16, 64, 4, 2, 96
+    x = N.bf16_round(rng.standard_normal((B, S, hid)))
+    # a zero o_proj leaves the residual stream unchanged; a zero down-proj too
+    w = _decoder_weights(rng, hid, Hq, Hkv, F, zero=("wo", "w_down"))
+    out = K.decoder_layer_fp8(x, w)
+    np.testing.assert_array_equal(out["z"], x)
+    np.testing.assert_array_equal(out["y"], x)
+    # Hkv = 2 with query heads {0,1} -> kv 0, {2,3} -> kv 1 equals Hkv = 4
+    # with each kv head's projection rows duplicated for its query heads
+    w = _decoder_weights(rng, hid, Hq, Hkv, F)
+    D = hid // Hq
+    codes, sc = w["wqkv"], w["wqkv_scale"]
+    q_rows = np.arange(Hq * D)
+    kv = lambda base: np.concatenate([base + (h // 2) * D + np.arange(D) for h in range(Hq)])
+    idx = np.concatenate([q_rows, kv(Hq * D), kv((Hq + Hkv) * D)])
+    w4 = dict(w, n_kv_heads=Hq, wqkv=codes[idx], wqkv_scale=sc[idx])
+    a2 = K.decoder_layer_fp8(x, w)["attn"]
+    a4 = K.decoder_layer_fp8(x, w4)["attn"]
+    np.testing.assert_array_equal(a2, a4)
