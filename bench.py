@@ -250,6 +250,74 @@ def bench_linattn(steps, warmup, rt):
     }
 
 
+def _quantize_fp8(rng, shape):
+    """N(0, 0.02) weights -> e4m3fn codes, per-output-channel scale amax / 448."""
+    import torch
+
+    w = torch.from_numpy(rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02))
+    scale = (w.abs().amax(dim=1) / 448.0).clamp_min(1e-12)
+    codes = (w / scale[:, None]).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    return codes, scale.numpy().astype(np.float32)
+
+
+def bench_decoder(steps, warmup, rt):
+    """Llama-style decoder layer, fp8 weights: hidden 4096, 32 / 8 heads,
+    head_dim 128, FFN 14336, RoPE theta 5e5, causal attention, x bf16
+    (8, 2048, 4096).  One step = the whole layer (nine kernels)."""
+    from nkipy_amd.core import dtypes as dt
+    from nkipy_amd.kernels import llama_decoder_layer_fp8
+    from nkipy_amd.runtime import DeviceKernel, DeviceTensor
+
+    B, S, Hq, Hkv, D, F = 8, 2048, 32, 8, 128, 14336
+    hid = Hq * D
+    rng = np.random.default_rng(42)
+    x = dt.round_to_bf16(rng.standard_normal((B, S, hid), dtype=np.float32))
+    w = {"n_heads": Hq, "n_kv_heads": Hkv, "eps": 1e-5, "rope_theta": 5.0e5,
+         "attn_norm": np.ones(hid, np.float32), "mlp_norm": np.ones(hid, np.float32)}
+    for name, shape in (("wqkv", ((Hq + 2 * Hkv) * D, hid)), ("wo", (hid, hid)),
+                        ("w_gate", (F, hid)), ("w_up", (F, hid)), ("w_down", (hid, F))):
+        w[name], w[name + "_scale"] = _quantize_fp8(rng, shape)
+    f8 = lambda c: c.view(dt.float8_e4m3fn)
+    args = [dt.to_bf16(x), dt.to_bf16(w["attn_norm"]), f8(w["wqkv"]), w["wqkv_scale"], f8(w["wo"]),
+            w["wo_scale"], dt.to_bf16(w["mlp_norm"]), f8(w["w_gate"]), w["w_gate_scale"], f8(w["w_up"]),
+            w["w_up_scale"], f8(w["w_down"]), w["w_down_scale"]]
+    dk = DeviceKernel.compile_and_load(llama_decoder_layer_fp8, *args, name="decoder_layer_fp8")
+    kinds = ["rmsnorm", "gemm", "rope", "rope", "attention", "gemm", "rmsnorm", "gemm_swiglu", "gemm"]
+    if dk.plan.kernel_kinds != kinds:
+        raise RuntimeError(f"decoder layer did not lower to the fused kernels: {dk.plan.kernel_kinds}")
+    names = [p.name for p in dk.graph.parameters]
+    ins = {n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(names, args)}
+    out = DeviceTensor.empty((B, S, hid), dt.bfloat16, name="output0")
+    bound = dk.executor.bind({**{k: v.ptr for k, v in ins.items()}, "output0": out.ptr})
+    ms_step, _ = _time_bound([bound], steps, warmup, rt)
+    per = []
+    for kind, l in zip(kinds, bound.launches):
+        ms = l.function(rt).time(l.grid, l.block, l.args, warmup=2, iters=max(3, steps // 2))
+        e = {"kind": kind, "kernel": l.symbol, "us": round(ms * 1e3, 2)}
+        if l.flops and kind in ("gemm", "gemm_swiglu", "attention"):
+            tf = l.flops / (ms * 1e-3) / 1e12
+            e.update(tflops=round(tf, 1), frac_bf16_peak=round(tf / BF16_PEAK_TFLOPS, 4))
+        else:
+            gbs = l.bytes / (ms * 1e-3) / 1e9
+            e.update(gbs=round(gbs, 1), frac_hbm=round(gbs / HBM_PEAK_GBS, 4))
+        per.append(e)
+    from oracle import kernels as K
+
+    rows = np.array([0, 1029, 2047])
+    ref = K.decoder_layer_fp8_rows(x[3], w, rows)["y"]
+    got = dt.to_float32(out.numpy()[3, rows])
+    scale = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+    ok = bool(np.all(np.abs(got - ref) <= 2e-2 * (np.abs(ref) + scale)))
+    flops = sum(l.flops for l in bound.launches)
+    return {
+        "workload": "llama_decoder_layer_fp8",
+        "shape": {"batch": B, "seq": S, "hidden": hid, "heads": Hq, "kv_heads": Hkv, "head_dim": D, "ffn": F},
+        "dtype": "bf16 activations, e4m3fn weights (decoded exactly to bf16 for the MFMA)",
+        "us_per_layer": round(ms_step * 1e3, 1), "flops_per_layer": flops,
+        "tflops": round(flops / (ms_step * 1e-3) / 1e12, 1), "kernels": per, "parity_ok": ok,
+    }
+
+
 def calibrate_copy(rt, nbytes=1 << 30, reps=3):
     """Plain streaming copy of a known size: rocprof's FETCH_SIZE / WRITE_SIZE
     for nk_copy16 read against 1 GiB give the counter scale factors."""
@@ -324,6 +392,11 @@ def main():
         f"({sw['frac_bf16_peak'] * 100:.1f}% of bf16 peak), parity_ok={sw['parity_ok']}")
     la = bench_linattn(max(5, args.steps // 20), max(2, args.warmup // 5), rt)
     log(f"linear attention: {la['us_per_launch']:.1f} us, {la['gbs']:.0f} GB/s, parity_ok={la['parity_ok']}")
+    dec = bench_decoder(max(5, args.steps // 20), max(2, args.warmup // 5), rt)
+    log(f"decoder layer fp8: {dec['us_per_layer']:.1f} us/layer, {dec['tflops']:.1f} TFLOP/s, "
+        f"parity_ok={dec['parity_ok']}")
+    for k in dec["kernels"]:
+        log(f"   {k}")
 
     cpu = None
     if not args.no_cpu:
@@ -366,6 +439,7 @@ def main():
             "softmax": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in sm.items()},
             "swiglu_mlp": sw,
             "linear_attention": la,
+            "decoder_layer_fp8": dec,
         },
     }
     print(json.dumps(line), flush=True)

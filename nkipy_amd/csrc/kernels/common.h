@@ -55,6 +55,23 @@ NK_DEVICE float e4m3_to_f32(uint8_t b) {
   return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
 }
 
+// 8 fp8 E4M3FN (one 64-bit word) -> 8 bf16, exact (3 mantissa bits fit in
+// bf16's 7; E4M3 subnormals are bf16 normals).  gfx950's
+// v_cvt_scalef32_pk_bf16_fp8 decodes two OCP E4M3FN codes per instruction;
+// the scale operand 1.0 leaves the values unscaled.
+typedef __bf16 nk_bf16x2 __attribute__((ext_vector_type(2)));
+NK_DEVICE uint32_t bf16x2_bits(nk_bf16x2 v) {
+  uint32_t u;
+  __builtin_memcpy(&u, &v, 4);
+  return u;
+}
+NK_DEVICE uint4 e4m3x8_to_bf16x8(uint2 q) {
+  return make_uint4(bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q.x, 1.0f, false)),
+                    bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q.x, 1.0f, true)),
+                    bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q.y, 1.0f, false)),
+                    bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q.y, 1.0f, true)));
+}
+
 // 128-bit nontemporal (streaming) global access: data read or written once
 // per kernel bypasses cache retention, which measurably raises achieved HBM
 // bandwidth for the row kernels.

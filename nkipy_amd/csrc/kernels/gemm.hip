@@ -63,20 +63,7 @@ struct GemmArgs {
 // ---------------------------------------------------------------------------
 // element helpers
 // ---------------------------------------------------------------------------
-// 8 fp8 E4M3FN (one 64-bit word) -> 8 bf16 (exact: 3-bit mantissa fits)
-__device__ __forceinline__ uint4 e4m3x8_to_bf16x8(uint2 q) {
-  uint32_t b[2] = {q.x, q.y};
-  uint32_t w[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    uint32_t lo = (b[i >> 1] >> (16 * (i & 1))) & 0xffu;
-    uint32_t hi = (b[i >> 1] >> (16 * (i & 1) + 8)) & 0xffu;
-    uint16_t l = f32_to_bf16(e4m3_to_f32((uint8_t)lo));
-    uint16_t h = f32_to_bf16(e4m3_to_f32((uint8_t)hi));
-    w[i] = (uint32_t)l | ((uint32_t)h << 16);
-  }
-  return make_uint4(w[0], w[1], w[2], w[3]);
-}
+// fp8 -> bf16 staging uses nk::e4m3x8_to_bf16x8 (common.h)
 
 template <typename TC> struct OutT;
 template <> struct OutT<bf16> {

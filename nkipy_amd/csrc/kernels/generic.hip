@@ -475,3 +475,17 @@ extern "C" __global__ __launch_bounds__(256) void nk_copy16(Copy16Args a) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.n16; i += a.nthreads)
     nt_store16(a.dst + i, nt_load16(a.src + i));
 }
+
+// fp8 E4M3FN codes -> bf16 with the decode the GEMM staging uses (8 codes per
+// thread).  Weight preparation and the exhaustive check of the decode.
+struct DecodeE4m3Args {
+  const uint2 *src;
+  uint4 *dst;
+  int64_t n8;
+  int64_t nthreads;
+};
+
+extern "C" __global__ __launch_bounds__(256) void nk_decode_e4m3_bf16(DecodeE4m3Args a) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.n8; i += a.nthreads)
+    a.dst[i] = e4m3x8_to_bf16x8(a.src[i]);
+}

@@ -150,6 +150,22 @@ def copy16(src_ptr: int, dst_ptr: int, nbytes: int) -> Launch:
                   Copy16Args(src_ptr, dst_ptr, n16, grid * 256), bytes=2 * nbytes)
 
 
+class DecodeE4m3Args(ctypes.Structure):
+    _fields_ = [("src", ctypes.c_void_p), ("dst", ctypes.c_void_p), ("n8", ctypes.c_int64),
+                ("nthreads", ctypes.c_int64)]
+
+
+def decode_e4m3(src_ptr: int, dst_ptr: int, n: int) -> Launch:
+    """fp8 E4M3FN codes -> bf16 (``n`` a multiple of 8; 8- / 16-byte aligned)
+    with the decode the GEMM kernel stages its fp8 operand through."""
+    if n % 8 or src_ptr % 8 or dst_ptr % 16:
+        raise LaunchError("decode_e4m3 needs n % 8 == 0, 8-byte aligned codes, 16-byte aligned output")
+    n8 = n // 8
+    grid = max(1, min((n8 + 255) // 256, 1 << 20))
+    return Launch("generic", "nk_decode_e4m3_bf16", (grid, 1, 1), (256, 1, 1),
+                  DecodeE4m3Args(src_ptr, dst_ptr, n8, grid * 256), bytes=3 * n)
+
+
 def _grid_for(total: int, max_blocks: int = 16384) -> int:
     return max(1, min((total + 255) // 256, max_blocks))
 

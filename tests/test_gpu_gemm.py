@@ -120,3 +120,23 @@ def test_gemm_fp8_swiglu_nt(gpu):
     _run(gpu, LA.gemm(t[0].ptr, t[1].ptr, hd.ptr, M, F, Kk, layout="nt", b_dtype=dt.float8_e4m3fn,
                       c_dtype=dt.bfloat16, scale_ptr=t[3].ptr, up_ptr=t[2].ptr, up_scale_ptr=t[4].ptr))
     _close(dt.to_float32(hd.numpy()), ref)
+
+
+def test_fp8_decode_all_codes(gpu):
+    """The fp8 -> bf16 decode used by the GEMM staging, on every E4M3FN code
+    (zeros, subnormals, normals, +-448, NaN) against the oracle's table."""
+    from nkipy_amd.dispatch.generic import decode_e4m3
+
+    codes = np.tile(np.arange(256, dtype=np.uint8), 4)
+    src = DeviceTensor.from_numpy(codes.view(dt.float8_e4m3fn))
+    dst = DeviceTensor.empty(codes.shape, dt.bfloat16)
+    decode_e4m3(src.ptr, dst.ptr, codes.size).run(gpu)
+    gpu.sync()
+    got = dt.to_float32(dst.numpy())
+    ref = N.E4M3FN_TABLE[codes]
+    nan = np.isnan(ref)
+    np.testing.assert_array_equal(np.isnan(got), nan)
+    np.testing.assert_array_equal(got[~nan], ref[~nan])
+    # signed zero survives
+    bits = dst.numpy().view(np.uint16)
+    assert bits[0x80] == 0x8000 and bits[0x00] == 0x0000
