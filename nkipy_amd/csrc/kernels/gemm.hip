@@ -32,6 +32,7 @@ using namespace nk;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 #define BM 256
 #define BN 256
@@ -92,122 +93,153 @@ __device__ __forceinline__ uint32_t h16(const uint4 &v, int i) {
 __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
 // ---------------------------------------------------------------------------
-// global -> register staging
+// global -> LDS movement
 // ---------------------------------------------------------------------------
-// A tile: 256 rows x 64 k = 2048 chunks of 8 bf16; 8 per thread.
-struct StageA {
+// Operands are read through buffer resources: 32-bit offsets from one base
+// (no per-load 64-bit addresses), and an offset past the end (OOB) reads
+// zeros, which pads the M / N / K edges without branches.
+#define OOB 0x80000000u
+#define BUF_WORD3 0x00020000  // gfx9 buffer resource word 3 (raw, untyped)
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, BUF_WORD3);
+}
+
+// One wave moves 1 KiB: lane l's 16 bytes land at lds_block + 16 * l.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds_block, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_block, 16, off, 0, 0, 0);
+}
+
+// A tile (and a bf16 B^T tile): 256 rows x 64 bf16 = 128-byte rows, 16-byte
+// chunks stored at chunk ^ swz(row).  Wave w moves blocks b = 4 j + w of
+// 8 rows; lane l fills stored slot (row, l % 8), so it fetches logical chunk
+// (l % 8) ^ swz(row).
+__device__ __forceinline__ void dma_rows_bf16(__amdgpu_buffer_rsrc_t r0, __amdgpu_buffer_rsrc_t r1,
+                                              bool split, uint8_t *S, int64_t r_first, int64_t nrows,
+                                              int64_t ld, int64_t k0, int64_t K, int wave, int lane) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int b = j * 4 + wave;
+    const int row = b * 8 + (lane >> 3);
+    const int lc = (lane & 7) ^ swz(row, 0);
+    const bool second = split && b >= 16;
+    const int64_t rr = r_first + (second ? row - 128 : row);
+    const int64_t k = k0 + lc * 8;
+    const uint32_t off = (rr < nrows && k < K) ? (uint32_t)((rr * ld + k) * 2) : OOB;
+    dma16(second ? r1 : r0, S + b * 1024, off);
+  }
+}
+
+// fp8 B^T tile (NT weights): 256 rows x 64 codes = 64-byte rows, 16-byte
+// chunks stored at chunk ^ ((row >> 2) & 3).  Blocks of 16 rows.
+__device__ __forceinline__ int swz8(int row) { return (row >> 2) & 3; }
+
+__device__ __forceinline__ void dma_rows_fp8(__amdgpu_buffer_rsrc_t r0, __amdgpu_buffer_rsrc_t r1,
+                                             bool split, uint8_t *S, int64_t r_first, int64_t nrows,
+                                             int64_t ld, int64_t k0, int64_t K, int wave, int lane) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int b = j * 4 + wave;
+    const int row = b * 16 + (lane >> 2);
+    const int lc = (lane & 3) ^ swz8(row);
+    const bool second = split && b >= 8;
+    const int64_t rr = r_first + (second ? row - 128 : row);
+    const int64_t k = k0 + lc * 16;
+    const uint32_t off = (rr < nrows && k < K) ? (uint32_t)(rr * ld + k) : OOB;
+    dma16(second ? r1 : r0, S + b * 1024, off);
+  }
+}
+
+// NN weights (K x N, N contiguous) go through registers: thread -> (8 k rows,
+// 8 columns); the 8 x 8 block is transposed in registers into B^T rows.
+struct StageNN {
   uint4 r[8];
 };
 
-__device__ __forceinline__ void load_a(StageA &s, const GemmArgs &a, int64_t m0, int64_t k0) {
-  const uint16_t *A = reinterpret_cast<const uint16_t *>(a.A);
+template <bool FP8, bool SWIGLU>
+__device__ __forceinline__ void load_nn(StageNN &s, const GemmArgs &a, __amdgpu_buffer_rsrc_t r0,
+                                        __amdgpu_buffer_rsrc_t r1, int64_t n0, int64_t k0) {
+  const int kb = threadIdx.x >> 5, nc = threadIdx.x & 31;
+  const bool second = SWIGLU && nc >= 16;
+  const int64_t col = n0 + (SWIGLU ? (nc & 15) * 8 : nc * 8);
+  const __amdgpu_buffer_rsrc_t r = second ? r1 : r0;
+  uint4 in[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int64_t k = k0 + kb * 8 + j;
+    const bool ok = k < a.K && col < a.N;
+    if (FP8) {
+      const uint32_t off = ok ? (uint32_t)(k * a.ldb + col) : OOB;
+      u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+      in[j] = e4m3x8_to_bf16x8(make_uint2(q[0], q[1]));
+    } else {
+      const uint32_t off = ok ? (uint32_t)((k * a.ldb + col) * 2) : OOB;
+      u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+      in[j] = make_uint4(q[0], q[1], q[2], q[3]);
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int c = threadIdx.x + NTHREADS * i;
-    const int row = c >> 3, kc = c & 7;
-    const int64_t m = m0 + row, k = k0 + kc * 8;
-    if (m < a.M && k < a.K)
-      s.r[i] = *reinterpret_cast<const uint4 *>(A + m * a.lda + k);
-    else
-      s.r[i] = make_uint4(0, 0, 0, 0);
+    uint32_t w[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) w[p] = h16(in[2 * p], i) | (h16(in[2 * p + 1], i) << 16);
+    s.r[i] = make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
 
-__device__ __forceinline__ void store_a(const StageA &s, uint16_t *As) {
+__device__ __forceinline__ void store_nn(const StageNN &s, uint8_t *Bs) {
+  const int kb = threadIdx.x >> 5, nc = threadIdx.x & 31;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int c = threadIdx.x + NTHREADS * i;
-    const int row = c >> 3, kc = c & 7;
-    *reinterpret_cast<uint4 *>(As + row * BK + swz(row, kc) * 8) = s.r[i];
+    const int nt = nc * 8 + i;
+    *reinterpret_cast<uint4 *>(Bs + nt * 128 + swz(nt, kb) * 16) = s.r[i];
   }
 }
 
-// B tile staged as B^T[256 n][64 k].
-template <bool NT, bool FP8>
-struct StageB {
-  // NT: 8 chunks of 8 k (one n row each); NN: 8 k rows x 8 n of one n chunk
-  uint4 r[8];
-};
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
-// column (n) of the B^T tile row `nt` (0..255) -> (matrix, global column)
-template <bool SWIGLU>
-__device__ __forceinline__ const void *b_src(const GemmArgs &a, int nt, int64_t n0, int64_t &col) {
-  if (SWIGLU) {
-    col = n0 + (nt & 127);
-    return nt < 128 ? a.B0 : a.B1;
+// ---------------------------------------------------------------------------
+// MFMA over one staged K tile (64 = 4 steps of 16), operand fragments of
+// step kk + 1 read from LDS while step kk's MFMAs run
+// ---------------------------------------------------------------------------
+template <bool FP8B>
+__device__ __forceinline__ void read_frags(bf16x8_t (&af)[4], bf16x8_t (&bf)[4], const uint8_t *As,
+                                           const uint8_t *Bs, int kk, int wm, const int (&brow)[4],
+                                           int l32, int lhi) {
+  const int chunk = kk * 2 + lhi;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = wm * 128 + i * 32 + l32;
+    af[i] = *reinterpret_cast<const bf16x8_t *>(As + row * 128 + swz(row, chunk) * 16);
   }
-  col = n0 + nt;
-  return a.B0;
-}
-
-template <bool NT, bool FP8, bool SWIGLU>
-__device__ __forceinline__ void load_b(StageB<NT, FP8> &s, const GemmArgs &a, int64_t n0, int64_t k0) {
-  if (NT) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = threadIdx.x + NTHREADS * i;
-      const int nt = c >> 3, kc = c & 7;
-      int64_t col;
-      const void *B = b_src<SWIGLU>(a, nt, n0, col);
-      const int64_t k = k0 + kc * 8;
-      if (col < a.N && k < a.K) {
-        if (FP8) {
-          uint2 q = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint8_t *>(B) + col * a.ldb + k);
-          s.r[i] = e4m3x8_to_bf16x8(q);
-        } else {
-          s.r[i] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(B) + col * a.ldb + k);
-        }
-      } else {
-        s.r[i] = make_uint4(0, 0, 0, 0);
-      }
-    }
-  } else {
-    // thread -> (k block of 8 rows, n chunk of 8 columns)
-    const int kb = threadIdx.x >> 5, nc = threadIdx.x & 31;
-    int64_t col;
-    const void *B = b_src<SWIGLU>(a, nc * 8, n0, col);
-    uint4 in[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t k = k0 + kb * 8 + j;
-      if (k < a.K && col < a.N) {
-        if (FP8) {
-          uint2 q = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint8_t *>(B) + k * a.ldb + col);
-          in[j] = e4m3x8_to_bf16x8(q);
-        } else {
-          in[j] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(B) + k * a.ldb + col);
-        }
-      } else {
-        in[j] = make_uint4(0, 0, 0, 0);
-      }
-    }
-    // 8 x 8 transpose: r[i] = the 8 k values of column nc*8 + i
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      uint32_t w[4];
-#pragma unroll
-      for (int p = 0; p < 4; ++p) w[p] = h16(in[2 * p], i) | (h16(in[2 * p + 1], i) << 16);
-      s.r[i] = make_uint4(w[0], w[1], w[2], w[3]);
+  for (int j = 0; j < 4; ++j) {
+    const int row = brow[j] + l32;
+    if (FP8B) {
+      const uint2 q = *reinterpret_cast<const uint2 *>(Bs + row * 64 + (kk ^ swz8(row)) * 16 + lhi * 8);
+      const uint4 w = e4m3x8_to_bf16x8(q);
+      bf[j] = *reinterpret_cast<const bf16x8_t *>(&w);
+    } else {
+      bf[j] = *reinterpret_cast<const bf16x8_t *>(Bs + row * 128 + swz(row, chunk) * 16);
     }
   }
 }
 
-template <bool NT, bool FP8>
-__device__ __forceinline__ void store_b(const StageB<NT, FP8> &s, uint16_t *Bs) {
-  if (NT) {
+template <bool FP8B>
+__device__ __forceinline__ void mma_tile(f32x16 (&acc)[4][4], const uint8_t *As, const uint8_t *Bs, int wm,
+                                         const int (&brow)[4], int l32, int lhi) {
+  bf16x8_t af[2][4], bf[2][4];
+  read_frags<FP8B>(af[0], bf[0], As, Bs, 0, wm, brow, l32, lhi);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = threadIdx.x + NTHREADS * i;
-      const int nt = c >> 3, kc = c & 7;
-      *reinterpret_cast<uint4 *>(Bs + nt * BK + swz(nt, kc) * 8) = s.r[i];
-    }
-  } else {
-    const int kb = threadIdx.x >> 5, nc = threadIdx.x & 31;
+  for (int kk = 0; kk < BK / 16; ++kk) {
+    if (kk + 1 < BK / 16) read_frags<FP8B>(af[(kk + 1) & 1], bf[(kk + 1) & 1], As, Bs, kk + 1, wm, brow, l32, lhi);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int nt = nc * 8 + i;
-      *reinterpret_cast<uint4 *>(Bs + nt * BK + swz(nt, kb) * 8) = s.r[i];
-    }
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk & 1][i], bf[kk & 1][j], acc[i][j], 0, 0, 0);
   }
 }
 
@@ -216,8 +248,12 @@ __device__ __forceinline__ void store_b(const StageB<NT, FP8> &s, uint16_t *Bs) 
 // ---------------------------------------------------------------------------
 template <bool NT, bool FP8, bool SWIGLU, typename TC>
 __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * BK];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * BK];
+  constexpr bool FP8B = NT && FP8;             // fp8 codes staged raw, decoded per fragment
+  constexpr int BROW = FP8B ? 64 : 128;        // bytes per B^T row in LDS
+  __shared__ __attribute__((aligned(1024))) uint8_t A0[BM * 128];
+  __shared__ __attribute__((aligned(1024))) uint8_t A1[BM * 128];
+  __shared__ __attribute__((aligned(1024))) uint8_t B0[BN * BROW];
+  __shared__ __attribute__((aligned(1024))) uint8_t B1[BN * BROW];
 
   // XCD-aware tile order
   const int ntiles = a.tiles_m * a.tiles_n;
@@ -252,49 +288,55 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
     brow[j] = SWIGLU ? ((j < 2) ? (wn * 64 + j * 32) : (128 + wn * 64 + (j - 2) * 32))
                      : (wn * 128 + j * 32);
 
-  StageA sa;
-  StageB<NT, FP8> sb;
+  const int bsz = FP8 ? 1 : 2;
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.A, a.M * a.lda * 2);
+  const int64_t brows = NT ? a.N : a.K;  // rows of the stored B matrix
+  const __amdgpu_buffer_rsrc_t rb0 = make_rsrc(a.B0, brows * a.ldb * bsz);
+  const __amdgpu_buffer_rsrc_t rb1 = make_rsrc(SWIGLU ? a.B1 : a.B0, brows * a.ldb * bsz);
+
+  StageNN sn;
+  auto issue = [&](uint8_t *As, uint8_t *Bs, int64_t k0) {
+    dma_rows_bf16(ra, ra, false, As, m0, a.M, a.lda, k0, a.K, wave, lane);
+    if (NT) {
+      if (FP8)
+        dma_rows_fp8(rb0, rb1, SWIGLU, Bs, n0, a.N, a.ldb, k0, a.K, wave, lane);
+      else
+        dma_rows_bf16(rb0, rb1, SWIGLU, Bs, n0, a.N, a.ldb, k0, a.K, wave, lane);
+    } else {
+      load_nn<FP8, SWIGLU>(sn, a, rb0, rb1, n0, k0);
+    }
+  };
+
   const int ktiles = (int)((a.K + BK - 1) / BK);
-  load_a(sa, a, m0, 0);
-  load_b<NT, FP8, SWIGLU>(sb, a, n0, 0);
-  store_a(sa, As[0]);
-  store_b<NT, FP8>(sb, Bs[0]);
+  issue(A0, B0, 0);
+  if (!NT) {
+    wait_vmem();
+    store_nn(sn, B0);
+  }
+  wait_vmem();
   __syncthreads();
 
-  for (int t = 0; t < ktiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ktiles) {
-      load_a(sa, a, m0, (int64_t)(t + 1) * BK);
-      load_b<NT, FP8, SWIGLU>(sb, a, n0, (int64_t)(t + 1) * BK);
+  int t = 0;
+  for (; t + 2 <= ktiles; t += 2) {
+    issue(A1, B1, (int64_t)(t + 1) * BK);
+    mma_tile<FP8B>(acc, A0, B0, wm, brow, l32, lhi);
+    if (!NT) {
+      wait_vmem();
+      store_nn(sn, B1);
     }
-    const uint16_t *as = As[buf];
-    const uint16_t *bs = Bs[buf];
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      const int chunk = kk * 2 + lhi;
-      bf16x8_t af[4], bfr[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = wm * 128 + i * 32 + l32;
-        af[i] = *reinterpret_cast<const bf16x8_t *>(as + row * BK + swz(row, chunk) * 8);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int row = brow[j] + l32;
-        bfr[j] = *reinterpret_cast<const bf16x8_t *>(bs + row * BK + swz(row, chunk) * 8);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    wait_vmem();
+    __syncthreads();
+    const bool more = t + 2 < ktiles;
+    if (more) issue(A0, B0, (int64_t)(t + 2) * BK);
+    mma_tile<FP8B>(acc, A1, B1, wm, brow, l32, lhi);
+    if (!NT && more) {
+      wait_vmem();
+      store_nn(sn, B0);
     }
-    if (t + 1 < ktiles) {
-      store_a(sa, As[buf ^ 1]);
-      store_b<NT, FP8>(sb, Bs[buf ^ 1]);
-    }
+    wait_vmem();
     __syncthreads();
   }
+  if (t < ktiles) mma_tile<FP8B>(acc, A0, B0, wm, brow, l32, lhi);
 
   // epilogue: lane holds column l32 of each 32 x 32 tile and rows
   // (r / 4) * 8 + lhi * 4 + r % 4

@@ -260,10 +260,16 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
         raise LaunchError("GEMM needs K, lda and ldb to be multiples of 8 (16-byte rows)")
     if lda < K or ldc < N or (layout == "nn" and ldb < N) or (layout == "nt" and ldb < K):
         raise LaunchError("GEMM leading dimension smaller than the matrix")
-    balign = 8 if fp8 else 16
+    balign = 8 if (fp8 and layout == "nn") else 16
     for p, al in ((a_ptr, 16), (b_ptr, balign), (up_ptr, balign)):
         if p and p % al:
             raise LaunchError("GEMM operand pointer is not aligned for 128-bit access")
+    if fp8 and layout == "nt" and (K % 16 or ldb % 16):
+        raise LaunchError("NT GEMM with fp8 weights needs K and ldb to be multiples of 16 (16-byte rows)")
+    # operands are addressed with 32-bit byte offsets from one base
+    b_rows = N if layout == "nt" else K
+    if M * lda * 2 >= 2**31 or b_rows * ldb * b_dtype.itemsize >= 2**31:
+        raise LaunchError("GEMM operands must be smaller than 2 GiB each")
     if layout == "nn" and N % 8:
         raise LaunchError("NN GEMM needs N to be a multiple of 8")
     if fp8 and not scale_ptr:

@@ -140,3 +140,21 @@ def test_fp8_decode_all_codes(gpu):
     # signed zero survives
     bits = dst.numpy().view(np.uint16)
     assert bits[0x80] == 0x8000 and bits[0x00] == 0x0000
+
+
+@pytest.mark.parametrize("shape", [(300, 520, 136), (256, 256, 64), (130, 264, 200)])
+def test_gemm_fp8_nn_scales(gpu, shape):
+    """fp8 (in, out) weights: codes staged through registers and transposed."""
+    M, Nn, Kk = shape
+    rng = np.random.default_rng(M * 3 + Kk)
+    x = _bf16(rng, (M, Kk))
+    w = (rng.standard_normal((Nn, Kk)) * 0.02).astype(np.float32)
+    codes, scale = N.quantize_per_channel_e4m3fn(w, axis=1)
+    ref = x.astype(np.float64) @ N.dequantize_e4m3fn(codes, scale, axis=1).T.astype(np.float64)
+    xd = DeviceTensor.from_numpy(dt.to_bf16(x))
+    wd = DeviceTensor.from_numpy(np.ascontiguousarray(codes.T).view(dt.float8_e4m3fn))
+    sd = DeviceTensor.from_numpy(scale.astype(np.float32))
+    cd = DeviceTensor.empty((M, Nn), dt.bfloat16)
+    _run(gpu, LA.gemm(xd.ptr, wd.ptr, cd.ptr, M, Nn, Kk, layout="nn", b_dtype=dt.float8_e4m3fn,
+                      c_dtype=dt.bfloat16, scale_ptr=sd.ptr))
+    _close(dt.to_float32(cd.numpy()), ref)
