@@ -152,6 +152,28 @@ __device__ __forceinline__ void dma_rows_fp8(__amdgpu_buffer_rsrc_t r0, __amdgpu
   }
 }
 
+// bf16 NN B tile (K x N weights, N contiguous): stored as two column halves
+// [64 k][128 n] with 256-byte rows (half 0 = tile columns 0..127, half 1 =
+// 128..255; in SwiGLU mode gate and up), 16-byte chunks at chunk ^ nnswz(k).
+// MFMA fragments are read with ds_read_b64_tr_b16 (below).  Blocks of 4 rows.
+__device__ __forceinline__ int nnswz(int k) { return (k & 3) << 2; }
+
+__device__ __forceinline__ void dma_nn_bf16(__amdgpu_buffer_rsrc_t r0, __amdgpu_buffer_rsrc_t r1, bool split,
+                                            uint8_t *S, int64_t n0, int64_t N, int64_t ld, int64_t k0,
+                                            int64_t K, int wave, int lane) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int b = j * 4 + wave;
+    const int half = b >> 4;
+    const int k = (b & 15) * 4 + (lane >> 4);
+    const int lc = (lane & 15) ^ nnswz(k);
+    const int64_t col = n0 + (split ? 0 : half * 128) + lc * 8;
+    const int64_t kg = k0 + k;
+    const uint32_t off = (kg < K && col < N) ? (uint32_t)((kg * ld + col) * 2) : OOB;
+    dma16((split && half) ? r1 : r0, S + b * 1024, off);
+  }
+}
+
 // NN weights (K x N, N contiguous) go through registers: thread -> (8 k rows,
 // 8 columns); the 8 x 8 block is transposed in registers into B^T rows.
 struct StageNN {
@@ -204,10 +226,17 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 // MFMA over one staged K tile (64 = 4 steps of 16), operand fragments of
 // step kk + 1 read from LDS while step kk's MFMAs run
 // ---------------------------------------------------------------------------
-template <bool FP8B>
+// B staging modes: raw fp8 NT rows, bf16 B^T rows, bf16 NN column halves
+enum BMode { B_T16 = 0, B_T8 = 1, B_NN16 = 2 };
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+template <int BM_>
 __device__ __forceinline__ void read_frags(bf16x8_t (&af)[4], bf16x8_t (&bf)[4], const uint8_t *As,
                                            const uint8_t *Bs, int kk, int wm, const int (&brow)[4],
-                                           int l32, int lhi) {
+                                           int lane) {
+  const int l32 = lane & 31, lhi = lane >> 5;
   const int chunk = kk * 2 + lhi;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -216,25 +245,42 @@ __device__ __forceinline__ void read_frags(bf16x8_t (&af)[4], bf16x8_t (&bf)[4],
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int row = brow[j] + l32;
-    if (FP8B) {
+    if (BM_ == B_T8) {
+      const int row = brow[j] + l32;
       const uint2 q = *reinterpret_cast<const uint2 *>(Bs + row * 64 + (kk ^ swz8(row)) * 16 + lhi * 8);
       const uint4 w = e4m3x8_to_bf16x8(q);
       bf[j] = *reinterpret_cast<const bf16x8_t *>(&w);
-    } else {
+    } else if (BM_ == B_T16) {
+      const int row = brow[j] + l32;
       bf[j] = *reinterpret_cast<const bf16x8_t *>(Bs + row * 128 + swz(row, chunk) * 16);
+    } else {
+      // brow[j] = tile column; half = column / 128.  Lane (group g, index i):
+      // source of row k = kk*16 + 8*(g/2) + 4*s + i/4, columns c + 16*(g%2) + 4*(i%4).
+      const int half = brow[j] >> 7, c = brow[j] & 127;
+      const int g = lane >> 4, i = lane & 15;
+      const int nl = c + (g & 1) * 16 + 4 * (i & 3);
+      s16x4 v[2];
+#pragma unroll
+      for (int sidx = 0; sidx < 2; ++sidx) {
+        const int k = kk * 16 + (g >> 1) * 8 + 4 * sidx + (i >> 2);
+        const uint8_t *p = Bs + half * 16384 + k * 256 + (((nl >> 3) ^ nnswz(k)) << 4) + (nl & 7) * 2;
+        v[sidx] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)p);
+      }
+      bf[j] = __builtin_shufflevector(__builtin_bit_cast(__attribute__((ext_vector_type(4))) __bf16, v[0]),
+                                      __builtin_bit_cast(__attribute__((ext_vector_type(4))) __bf16, v[1]),
+                                      0, 1, 2, 3, 4, 5, 6, 7);
     }
   }
 }
 
-template <bool FP8B>
+template <int BM_>
 __device__ __forceinline__ void mma_tile(f32x16 (&acc)[4][4], const uint8_t *As, const uint8_t *Bs, int wm,
-                                         const int (&brow)[4], int l32, int lhi) {
+                                         const int (&brow)[4], int lane) {
   bf16x8_t af[2][4], bf[2][4];
-  read_frags<FP8B>(af[0], bf[0], As, Bs, 0, wm, brow, l32, lhi);
+  read_frags<BM_>(af[0], bf[0], As, Bs, 0, wm, brow, lane);
 #pragma unroll
   for (int kk = 0; kk < BK / 16; ++kk) {
-    if (kk + 1 < BK / 16) read_frags<FP8B>(af[(kk + 1) & 1], bf[(kk + 1) & 1], As, Bs, kk + 1, wm, brow, l32, lhi);
+    if (kk + 1 < BK / 16) read_frags<BM_>(af[(kk + 1) & 1], bf[(kk + 1) & 1], As, Bs, kk + 1, wm, brow, lane);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -248,8 +294,11 @@ __device__ __forceinline__ void mma_tile(f32x16 (&acc)[4][4], const uint8_t *As,
 // ---------------------------------------------------------------------------
 template <bool NT, bool FP8, bool SWIGLU, typename TC>
 __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
-  constexpr bool FP8B = NT && FP8;             // fp8 codes staged raw, decoded per fragment
-  constexpr int BROW = FP8B ? 64 : 128;        // bytes per B^T row in LDS
+  // fp8 NT codes staged raw (decoded per fragment); bf16 NN through LDS DMA
+  // and transpose reads; fp8 NN through registers into bf16 B^T rows
+  constexpr int BMODE = (NT && FP8) ? B_T8 : (!NT && !FP8) ? B_NN16 : B_T16;
+  constexpr bool REG_B = !NT && FP8;
+  constexpr int BROW = BMODE == B_T8 ? 64 : 128;  // bytes per B row in LDS
   __shared__ __attribute__((aligned(1024))) uint8_t A0[BM * 128];
   __shared__ __attribute__((aligned(1024))) uint8_t A1[BM * 128];
   __shared__ __attribute__((aligned(1024))) uint8_t B0[BN * BROW];
@@ -302,14 +351,16 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
         dma_rows_fp8(rb0, rb1, SWIGLU, Bs, n0, a.N, a.ldb, k0, a.K, wave, lane);
       else
         dma_rows_bf16(rb0, rb1, SWIGLU, Bs, n0, a.N, a.ldb, k0, a.K, wave, lane);
-    } else {
+    } else if (REG_B) {
       load_nn<FP8, SWIGLU>(sn, a, rb0, rb1, n0, k0);
+    } else {
+      dma_nn_bf16(rb0, rb1, SWIGLU, Bs, n0, a.N, a.ldb, k0, a.K, wave, lane);
     }
   };
 
   const int ktiles = (int)((a.K + BK - 1) / BK);
   issue(A0, B0, 0);
-  if (!NT) {
+  if (REG_B) {
     wait_vmem();
     store_nn(sn, B0);
   }
@@ -319,8 +370,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
   int t = 0;
   for (; t + 2 <= ktiles; t += 2) {
     issue(A1, B1, (int64_t)(t + 1) * BK);
-    mma_tile<FP8B>(acc, A0, B0, wm, brow, l32, lhi);
-    if (!NT) {
+    mma_tile<BMODE>(acc, A0, B0, wm, brow, lane);
+    if (REG_B) {
       wait_vmem();
       store_nn(sn, B1);
     }
@@ -328,15 +379,15 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
     __syncthreads();
     const bool more = t + 2 < ktiles;
     if (more) issue(A0, B0, (int64_t)(t + 2) * BK);
-    mma_tile<FP8B>(acc, A1, B1, wm, brow, l32, lhi);
-    if (!NT && more) {
+    mma_tile<BMODE>(acc, A1, B1, wm, brow, lane);
+    if (REG_B && more) {
       wait_vmem();
       store_nn(sn, B0);
     }
     wait_vmem();
     __syncthreads();
   }
-  if (t < ktiles) mma_tile<FP8B>(acc, A0, B0, wm, brow, l32, lhi);
+  if (t < ktiles) mma_tile<BMODE>(acc, A0, B0, wm, brow, lane);
 
   // epilogue: lane holds column l32 of each 32 x 32 tile and rows
   // (r / 4) * 8 + lhi * 4 + r % 4
