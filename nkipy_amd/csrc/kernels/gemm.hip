@@ -112,23 +112,48 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds_blo
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_block, 16, off, 0, 0, 0);
 }
 
+// Each thread's DMA sources are fixed up to the K offset: per 16-byte move j
+// the byte offset at k0 = 0 (OOB if its row / column is outside the matrix)
+// and the K index of its chunk.  Per K tile: off = base + k0 * kstep, or OOB
+// past K.  Wave index `wave` is wave-uniform (scalar), so the LDS block
+// addresses (M0) are scalar too.
+template <int NJ>
+struct DmaPlan {
+  uint32_t base[NJ];
+  int kofs;  // chunk K index common to all j (row-major operands), else per j below
+};
+
+__device__ __forceinline__ uint32_t dma_off(uint32_t base, int64_t k0, int kidx, int64_t K, int64_t kstep) {
+  return (base != OOB && k0 + kidx < K) ? base + (uint32_t)(k0 * kstep) : OOB;
+}
+
 // A tile (and a bf16 B^T tile): 256 rows x 64 bf16 = 128-byte rows, 16-byte
 // chunks stored at chunk ^ swz(row).  Wave w moves blocks b = 4 j + w of
 // 8 rows; lane l fills stored slot (row, l % 8), so it fetches logical chunk
-// (l % 8) ^ swz(row).
-__device__ __forceinline__ void dma_rows_bf16(__amdgpu_buffer_rsrc_t r0, __amdgpu_buffer_rsrc_t r1,
-                                              bool split, uint8_t *S, int64_t r_first, int64_t nrows,
-                                              int64_t ld, int64_t k0, int64_t K, int wave, int lane) {
+// (l % 8) ^ swz(row) -- the same chunk for every j, since swz(row) only
+// depends on (4 w + l / 16) mod 8.
+__device__ __forceinline__ DmaPlan<8> plan_rows_bf16(bool split, int64_t r_first, int64_t nrows, int64_t ld,
+                                                     int wave, int lane) {
+  DmaPlan<8> p;
+  const int lc = (lane & 7) ^ swz(wave * 8 + (lane >> 3), 0);  // row of move j = 0
+  p.kofs = lc * 8;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int b = j * 4 + wave;
     const int row = b * 8 + (lane >> 3);
-    const int lc = (lane & 7) ^ swz(row, 0);
-    const bool second = split && b >= 16;
-    const int64_t rr = r_first + (second ? row - 128 : row);
-    const int64_t k = k0 + lc * 8;
-    const uint32_t off = (rr < nrows && k < K) ? (uint32_t)((rr * ld + k) * 2) : OOB;
-    dma16(second ? r1 : r0, S + b * 1024, off);
+    const int64_t rr = r_first + ((split && b >= 16) ? row - 128 : row);
+    p.base[j] = rr < nrows ? (uint32_t)((rr * ld + p.kofs) * 2) : OOB;
+  }
+  return p;
+}
+
+__device__ __forceinline__ void dma_rows_bf16(const DmaPlan<8> &p, __amdgpu_buffer_rsrc_t r0,
+                                              __amdgpu_buffer_rsrc_t r1, bool split, uint8_t *S, int64_t k0,
+                                              int64_t K, int wave) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int b = j * 4 + wave;
+    dma16((split && b >= 16) ? r1 : r0, S + b * 1024, dma_off(p.base[j], k0, p.kofs, K, 2));
   }
 }
 
@@ -136,41 +161,64 @@ __device__ __forceinline__ void dma_rows_bf16(__amdgpu_buffer_rsrc_t r0, __amdgp
 // chunks stored at chunk ^ ((row >> 2) & 3).  Blocks of 16 rows.
 __device__ __forceinline__ int swz8(int row) { return (row >> 2) & 3; }
 
-__device__ __forceinline__ void dma_rows_fp8(__amdgpu_buffer_rsrc_t r0, __amdgpu_buffer_rsrc_t r1,
-                                             bool split, uint8_t *S, int64_t r_first, int64_t nrows,
-                                             int64_t ld, int64_t k0, int64_t K, int wave, int lane) {
+__device__ __forceinline__ DmaPlan<4> plan_rows_fp8(bool split, int64_t r_first, int64_t nrows, int64_t ld,
+                                                    int wave, int lane) {
+  DmaPlan<4> p;
+  const int lc = (lane & 3) ^ swz8(wave * 16 + (lane >> 2));  // row of move j = 0
+  p.kofs = lc * 16;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int b = j * 4 + wave;
     const int row = b * 16 + (lane >> 2);
-    const int lc = (lane & 3) ^ swz8(row);
-    const bool second = split && b >= 8;
-    const int64_t rr = r_first + (second ? row - 128 : row);
-    const int64_t k = k0 + lc * 16;
-    const uint32_t off = (rr < nrows && k < K) ? (uint32_t)(rr * ld + k) : OOB;
-    dma16(second ? r1 : r0, S + b * 1024, off);
+    const int64_t rr = r_first + ((split && b >= 8) ? row - 128 : row);
+    p.base[j] = rr < nrows ? (uint32_t)(rr * ld + p.kofs) : OOB;
+  }
+  return p;
+}
+
+__device__ __forceinline__ void dma_rows_fp8(const DmaPlan<4> &p, __amdgpu_buffer_rsrc_t r0,
+                                             __amdgpu_buffer_rsrc_t r1, bool split, uint8_t *S, int64_t k0,
+                                             int64_t K, int wave) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int b = j * 4 + wave;
+    dma16((split && b >= 8) ? r1 : r0, S + b * 1024, dma_off(p.base[j], k0, p.kofs, K, 1));
   }
 }
 
 // bf16 NN B tile (K x N weights, N contiguous): stored as two column halves
 // [64 k][128 n] with 256-byte rows (half 0 = tile columns 0..127, half 1 =
 // 128..255; in SwiGLU mode gate and up), 16-byte chunks at chunk ^ nnswz(k).
-// MFMA fragments are read with ds_read_b64_tr_b16 (below).  Blocks of 4 rows.
+// MFMA fragments are read with ds_read_b64_tr_b16 (below).  Blocks of 4 rows;
+// move j covers k row ((4 j + w) mod 16) * 4 + l / 16.
 __device__ __forceinline__ int nnswz(int k) { return (k & 3) << 2; }
 
-__device__ __forceinline__ void dma_nn_bf16(__amdgpu_buffer_rsrc_t r0, __amdgpu_buffer_rsrc_t r1, bool split,
-                                            uint8_t *S, int64_t n0, int64_t N, int64_t ld, int64_t k0,
-                                            int64_t K, int wave, int lane) {
+__device__ __forceinline__ int nn_krow(int j, int wave, int lane) { return ((j * 4 + wave) & 15) * 4 + (lane >> 4); }
+
+__device__ __forceinline__ DmaPlan<8> plan_nn_bf16(bool split, int64_t n0, int64_t N, int64_t ld, int wave,
+                                                   int lane) {
+  DmaPlan<8> p;
+  p.kofs = 0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int b = j * 4 + wave;
     const int half = b >> 4;
-    const int k = (b & 15) * 4 + (lane >> 4);
+    const int k = nn_krow(j, wave, lane);
     const int lc = (lane & 15) ^ nnswz(k);
     const int64_t col = n0 + (split ? 0 : half * 128) + lc * 8;
-    const int64_t kg = k0 + k;
-    const uint32_t off = (kg < K && col < N) ? (uint32_t)((kg * ld + col) * 2) : OOB;
-    dma16((split && half) ? r1 : r0, S + b * 1024, off);
+    p.base[j] = col < N ? (uint32_t)((k * ld + col) * 2) : OOB;
+  }
+  return p;
+}
+
+__device__ __forceinline__ void dma_nn_bf16(const DmaPlan<8> &p, __amdgpu_buffer_rsrc_t r0,
+                                            __amdgpu_buffer_rsrc_t r1, bool split, uint8_t *S, int64_t k0,
+                                            int64_t K, int64_t ld, int wave, int lane) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int b = j * 4 + wave;
+    dma16((split && (b >> 4)) ? r1 : r0, S + b * 1024,
+          dma_off(p.base[j], k0, nn_krow(j, wave, lane), K, ld * 2));
   }
 }
 
@@ -289,6 +337,29 @@ __device__ __forceinline__ void mma_tile(f32x16 (&acc)[4][4], const uint8_t *As,
   }
 }
 
+// Instruction order of one K tile (one scheduling region: the DMA issue of
+// the next tile plus the MFMAs of this one): the fragments of step 0, then
+// per step the fragments of step + 1 ahead of the step's 16 MFMAs, and one
+// DMA after every 4 MFMAs.  Each fragment read has a whole step (16 MFMAs,
+// ~512 cycles) to land before it is used.
+template <int NDS, int NVMEM>
+__device__ __forceinline__ void schedule_ktile() {
+  __builtin_amdgcn_sched_group_barrier(0x100, NDS, 0);  // DS reads, step 0
+  int vm = 0;
+#pragma unroll
+  for (int kk = 0; kk < BK / 16; ++kk) {
+    if (kk + 1 < BK / 16) __builtin_amdgcn_sched_group_barrier(0x100, NDS, 0);  // DS reads, step kk + 1
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // 4 MFMA
+      if (vm < NVMEM) {
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 VMEM read (DMA)
+        ++vm;
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // main kernel
 // ---------------------------------------------------------------------------
@@ -318,9 +389,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
   const int64_t n0 = (int64_t)tn * (SWIGLU ? BN / 2 : BN);
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int l32 = lane & 31, lhi = lane >> 5;
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -344,17 +414,23 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
   const __amdgpu_buffer_rsrc_t rb1 = make_rsrc(SWIGLU ? a.B1 : a.B0, brows * a.ldb * bsz);
 
   StageNN sn;
+  const DmaPlan<8> pa = plan_rows_bf16(false, m0, a.M, a.lda, wave, lane);
+  DmaPlan<8> pb16;
+  DmaPlan<4> pb8;
+  if (NT && FP8) pb8 = plan_rows_fp8(SWIGLU, n0, a.N, a.ldb, wave, lane);
+  if (NT && !FP8) pb16 = plan_rows_bf16(SWIGLU, n0, a.N, a.ldb, wave, lane);
+  if (!NT && !FP8) pb16 = plan_nn_bf16(SWIGLU, n0, a.N, a.ldb, wave, lane);
   auto issue = [&](uint8_t *As, uint8_t *Bs, int64_t k0) {
-    dma_rows_bf16(ra, ra, false, As, m0, a.M, a.lda, k0, a.K, wave, lane);
+    dma_rows_bf16(pa, ra, ra, false, As, k0, a.K, wave);
     if (NT) {
       if (FP8)
-        dma_rows_fp8(rb0, rb1, SWIGLU, Bs, n0, a.N, a.ldb, k0, a.K, wave, lane);
+        dma_rows_fp8(pb8, rb0, rb1, SWIGLU, Bs, k0, a.K, wave);
       else
-        dma_rows_bf16(rb0, rb1, SWIGLU, Bs, n0, a.N, a.ldb, k0, a.K, wave, lane);
+        dma_rows_bf16(pb16, rb0, rb1, SWIGLU, Bs, k0, a.K, wave);
     } else if (REG_B) {
       load_nn<FP8, SWIGLU>(sn, a, rb0, rb1, n0, k0);
     } else {
-      dma_nn_bf16(rb0, rb1, SWIGLU, Bs, n0, a.N, a.ldb, k0, a.K, wave, lane);
+      dma_nn_bf16(pb16, rb0, rb1, SWIGLU, Bs, k0, a.K, a.ldb, wave, lane);
     }
   };
 
@@ -367,20 +443,25 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
   wait_vmem();
   __syncthreads();
 
+  // fragment reads per step and DMA moves per K tile of this variant
+  constexpr int NDS = BMODE == B_NN16 ? 12 : 8;
+  constexpr int NVM = REG_B ? 16 : (BMODE == B_T8 ? 12 : 16);
   int t = 0;
   for (; t + 2 <= ktiles; t += 2) {
     issue(A1, B1, (int64_t)(t + 1) * BK);
     mma_tile<BMODE>(acc, A0, B0, wm, brow, lane);
+    schedule_ktile<NDS, NVM>();
     if (REG_B) {
       wait_vmem();
       store_nn(sn, B1);
     }
     wait_vmem();
     __syncthreads();
-    const bool more = t + 2 < ktiles;
-    if (more) issue(A0, B0, (int64_t)(t + 2) * BK);
+    // past the last tile this reads zeros (K offset out of range) into the idle stage
+    issue(A0, B0, (int64_t)(t + 2) * BK);
     mma_tile<BMODE>(acc, A1, B1, wm, brow, lane);
-    if (REG_B && more) {
+    schedule_ktile<NDS, NVM>();
+    if (REG_B && t + 2 < ktiles) {
       wait_vmem();
       store_nn(sn, B0);
     }
@@ -389,6 +470,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
   }
   if (t < ktiles) mma_tile<BMODE>(acc, A0, B0, wm, brow, lane);
 
+  const int l32 = lane & 31, lhi = lane >> 5;
   // epilogue: lane holds column l32 of each 32 x 32 tile and rows
   // (r / 4) * 8 + lhi * 4 + r % 4
   if (SWIGLU) {
