@@ -9,16 +9,25 @@
 // heads, q @ k^T scaled, causal mask added, softmax over keys, @ v.
 //
 // Work split: one workgroup (4 waves) per (b, h, block of 128 queries); each
-// wave owns 32 queries.  The kernel computes S^T = K Q^T and O^T = V^T P^T
-// with v_mfma_f32_32x32x16_bf16 so that every lane owns one query column:
-// the running max / sum of the online softmax are lane-local (the two lane
-// halves holding the same query combine with one xor-32 shuffle), and the
-// P^T operand of the second product is taken straight from the S^T
-// accumulators -- V^T is read in the matching permuted key order.
-// Q fragments stay in registers; K tiles (64 keys x 128) and V^T tiles
-// (128 x 64 keys, transposed in registers on the way in) are double-buffered
-// in LDS.  Scores and softmax are fp32; P enters the second MFMA as bf16.
-// Query blocks are issued longest-first (causal work grows with position).
+// wave owns 32 queries; two workgroups share a CU.  The kernel computes
+// S^T = K Q^T and O^T = V^T P^T with v_mfma_f32_32x32x16_bf16 so that every
+// lane owns one query column: the running max / sum of the online softmax
+// are lane-local (the two lane halves holding the same query combine with
+// one xor-32 shuffle), and the P^T operand of the second product is taken
+// straight from the S^T accumulators, whose key order the V^T fragments
+// follow.
+//
+// Data movement: Q fragments stay in registers.  K and V tiles (64 keys x
+// 128 d, d contiguous, exactly as they lie in memory) move global -> LDS by
+// DMA (buffer_load ... lds), double-buffered, so the next tile streams in
+// while the current one feeds the MFMAs.  K fragments are plain 16-byte LDS
+// reads; V^T fragments come from ds_read_b64_tr_b16, which transposes 4 x 4
+// bf16 blocks across lanes on the way out of LDS.  Both tiles are
+// XOR-swizzled so that these reads are bank-conflict free.  Scores and the
+// softmax are fp32; P enters the second MFMA as bf16.  Causal masking is only
+// evaluated on blocks that cross the diagonal of a wave's queries, and
+// blocks entirely above it are skipped.  Query blocks are issued
+// longest-first (causal work grows with position).
 
 #include "common.h"
 
@@ -27,10 +36,14 @@ using namespace nk;
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) void lds_void;
 
 #define AQ 128  // queries per workgroup
 #define AK 64   // keys per block
 #define AD 128  // head dim
+#define TILE_BYTES (AK * AD * 2)
 
 struct AttnArgs {
   const uint16_t *q;
@@ -46,19 +59,36 @@ struct AttnArgs {
   int32_t causal;
 };
 
-__device__ __forceinline__ int koff(int row, int col) {  // K tile: rows of 128
-  return row * AD + ((((col >> 3) ^ (row & 15))) << 3) + (col & 7);
-}
-__device__ __forceinline__ int voff(int row, int col) {  // V^T tile: rows of 64
-  return row * AK + ((((col >> 3) ^ ((row >> 1) & 7))) << 3) + (col & 7);
+// K tile row (key) r: 16-byte chunk c stored at c ^ (r & 15): the 32 rows of
+// a K fragment read hit 16 distinct bank slots (two per cycle's worth).
+__device__ __forceinline__ int kswz(int r) { return r & 15; }
+// V tile: chunk c of row r at c ^ 4 (r & 3): the 4 rows x 4 chunks of one
+// transpose read land in 16 distinct slots.
+__device__ __forceinline__ int vswz(int r) { return (r & 3) << 2; }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
 }
 
-extern "C" __global__ __launch_bounds__(256, 1) void nk_attention_causal_d128(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][AK * AD];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][AD * AK];
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds_block, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_block, 16, off, 0, 0, 0);
+}
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+struct Tile {
+  uint8_t *K;
+  uint8_t *V;
+};
+
+extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(AttnArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t K0[TILE_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t K1[TILE_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t V0[TILE_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t V1[TILE_BYTES];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31, lhi = lane >> 5;
 
   // block -> (b, h, query block), longest (last) query blocks first
@@ -74,9 +104,12 @@ extern "C" __global__ __launch_bounds__(256, 1) void nk_attention_causal_d128(At
   const uint16_t *kp = a.k + (int64_t)b * a.k_sb + (int64_t)g * a.k_sh;
   const uint16_t *vp = a.v + (int64_t)b * a.v_sb + (int64_t)g * a.v_sh;
   uint16_t *op = a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp, (int64_t)a.S * a.k_ss * 2);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp, (int64_t)a.S * a.v_ss * 2);
 
   // this lane's query (column of S^T / O^T) and its Q fragments (B operand)
-  const int qrow = q0 + wave * 32 + l32;
+  const int wq0 = q0 + wave * 32;
+  const int qrow = wq0 + l32;
   bf16x8_t qf[AD / 16];
 #pragma unroll
   for (int kk = 0; kk < AD / 16; ++kk)
@@ -93,89 +126,68 @@ extern "C" __global__ __launch_bounds__(256, 1) void nk_attention_causal_d128(At
   const int kend = a.causal ? (q0 + AQ) : a.S;
   const int nkb = kend / AK;
 
-  // staging: threads 0..127 transpose an 8 x 8 block of V, 128..255 load K
-  uint4 stage[8];
-  auto load_tile = [&](int kb) {
-    const int t0 = kb * AK;
-    if (tid < 128) {
-      const int kblk = tid >> 4, dblk = tid & 15;  // 8 key blocks x 16 d blocks
+  // DMA plan: a tile pair is 32 moves of 1 KiB (4 rows of 256 bytes); wave w
+  // does moves m = 4 j + w: j < 4 K rows, j >= 4 V rows.  The chunk a lane
+  // fetches is the same for every j (the swizzles only see row & 15).
+  const int kchunk = (lane & 15) ^ kswz(wave * 4 + (lane >> 4));
+  const int vchunk = (lane & 15) ^ vswz(wave * 4 + (lane >> 4));
+  uint32_t kbase[4], vbase[4];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        stage[j] = *reinterpret_cast<const uint4 *>(vp + (int64_t)(t0 + kblk * 8 + j) * a.v_ss + dblk * 8);
-    } else {
-      const int t = tid - 128;
+  for (int j = 0; j < 4; ++j) {
+    const int row = (j * 4 + wave) * 4 + (lane >> 4);
+    kbase[j] = (uint32_t)(((int64_t)row * a.k_ss + kchunk * 8) * 2);
+    vbase[j] = (uint32_t)(((int64_t)row * a.v_ss + vchunk * 8) * 2);
+  }
+  auto load_tile = [&](Tile t, int kb) {
+    const uint32_t kst = (uint32_t)((int64_t)kb * AK * a.k_ss * 2);
+    const uint32_t vst = (uint32_t)((int64_t)kb * AK * a.v_ss * 2);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int c = t + 128 * i;
-        const int row = c >> 4, col = (c & 15) * 8;
-        stage[i] = *reinterpret_cast<const uint4 *>(kp + (int64_t)(t0 + row) * a.k_ss + col);
-      }
-    }
-  };
-  auto store_tile = [&](int buf) {
-    if (tid < 128) {
-      const int kblk = tid >> 4, dblk = tid & 15;
+    for (int j = 0; j < 4; ++j) dma16(rk, t.K + (j * 4 + wave) * 1024, kbase[j] + kst);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        uint32_t w[4];
-#pragma unroll
-        for (int p = 0; p < 4; ++p)
-          w[p] = h16_of(stage[2 * p], i) | (h16_of(stage[2 * p + 1], i) << 16);
-        *reinterpret_cast<uint4 *>(Vt[buf] + voff(dblk * 8 + i, kblk * 8)) = make_uint4(w[0], w[1], w[2], w[3]);
-      }
-    } else {
-      const int t = tid - 128;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int c = t + 128 * i;
-        const int row = c >> 4, col = (c & 15) * 8;
-        *reinterpret_cast<uint4 *>(Ks[buf] + koff(row, col)) = stage[i];
-      }
-    }
+    for (int j = 0; j < 4; ++j) dma16(rv, t.V + (j * 4 + wave) * 1024, vbase[j] + vst);
   };
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int buf = kb & 1;
-    if (kb + 1 < nkb) load_tile(kb + 1);
-
-    // S^T = K Q^T for 64 keys: two 32 x 32 tiles (keys ktile*32 + ..)
+  // one 64-key block against this wave's 32 queries
+  auto block = [&](Tile t, int kb) {
+    const int key0 = kb * AK;
+    if (a.causal && key0 > wq0 + 31) return;  // entirely above the diagonal for this wave
     f32x16 s[2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[kt][r] = 0.f;
+      const int row = kt * 32 + l32;
 #pragma unroll
       for (int kk = 0; kk < AD / 16; ++kk) {
-        bf16x8_t kf = *reinterpret_cast<const bf16x8_t *>(Ks[buf] + koff(kt * 32 + l32, kk * 16 + lhi * 8));
+        const bf16x8_t kf =
+            *reinterpret_cast<const bf16x8_t *>(t.K + row * 256 + (((kk * 2 + lhi) ^ kswz(row)) << 4));
         s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[kt], 0, 0, 0);
       }
     }
-    // scale (in log2 units), causal mask, block max
-    const int key0 = kb * AK;
+    // scale (log2 units), causal mask on diagonal blocks, block max
     float bmax = -INFINITY;
+    const bool diag = a.causal && key0 + AK - 1 > wq0;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = key0 + kt * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
         float x = s[kt][r] * sl2;
-        if (a.causal && key > qrow) x = -INFINITY;
+        if (diag) {
+          const int key = key0 + kt * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
+          if (key > qrow) x = -INFINITY;
+        }
         s[kt][r] = x;
         bmax = fmaxf(bmax, x);
       }
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-    const float m_new = fmaxf(m_run, bmax);
-    const float alpha = exp2f(m_run - m_new);  // 0 on the first block
+    const float m_new = fmaxf(m_run, bmax);  // finite: every row sees key 0 in its first block
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first block
     float bsum = 0.f;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = exp2f(s[kt][r] - m_new);
+        const float p = __builtin_amdgcn_exp2f(s[kt][r] - m_new);
         s[kt][r] = p;
         bsum += p;
       }
@@ -183,12 +195,16 @@ extern "C" __global__ __launch_bounds__(256, 1) void nk_attention_causal_d128(At
     l_run = l_run * alpha + bsum;
     m_run = m_new;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t2 = 0; t2 < 4; ++t2)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc_o[t][r] *= alpha;
+      for (int r = 0; r < 16; ++r) acc_o[t2][r] *= alpha;
 
-    // O^T += V^T P^T; k-step j covers keys 16j..16j+15 in the permuted order
-    // this lane's P values already have: {16j + 4*lhi + 0..3, 16j + 8 + 4*lhi + 0..3}
+    // O^T += V^T P^T.  Step j covers 16 keys; this lane's P values (S^T rows)
+    // are keys 16 j + 4 lhi + {0..3} and 16 j + 8 + 4 lhi + {0..3}, which is
+    // the order of the two transpose reads below.  Transpose read (group
+    // g = lane / 16, i = lane % 16): source row key0' + i / 4, columns
+    // n + 4 (i % 4); output lane i gets column n + i for 4 consecutive keys.
+    const int grp = lane >> 4, gi = lane & 15;
 #pragma unroll
     for (int j = 0; j < AK / 16; ++j) {
       const int kt = j >> 1, g0 = (j & 1) * 8;
@@ -196,19 +212,38 @@ extern "C" __global__ __launch_bounds__(256, 1) void nk_attention_causal_d128(At
 #pragma unroll
       for (int e = 0; e < 8; ++e) pf[e] = (__bf16)s[kt][g0 + e];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int d = t * 32 + l32;
-        const bf16x4_t lo = *reinterpret_cast<const bf16x4_t *>(Vt[buf] + voff(d, 16 * j + 4 * lhi));
-        const bf16x4_t hi = *reinterpret_cast<const bf16x4_t *>(Vt[buf] + voff(d, 16 * j + 8 + 4 * lhi));
-        bf16x8_t vf;
-        vf[0] = lo[0]; vf[1] = lo[1]; vf[2] = lo[2]; vf[3] = lo[3];
-        vf[4] = hi[0]; vf[5] = hi[1]; vf[6] = hi[2]; vf[7] = hi[3];
-        acc_o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, acc_o[t], 0, 0, 0);
+      for (int dt = 0; dt < 4; ++dt) {
+        const int nl = dt * 32 + (grp & 1) * 16 + 4 * (gi & 3);
+        s16x4 v[2];
+#pragma unroll
+        for (int si = 0; si < 2; ++si) {
+          const int key = 16 * j + 8 * si + 4 * (grp >> 1) + (gi >> 2);
+          const uint8_t *p = t.V + key * 256 + (((nl >> 3) ^ vswz(key)) << 4) + (nl & 7) * 2;
+          v[si] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)p);
+        }
+        const bf16x8_t vf = __builtin_shufflevector(__builtin_bit_cast(bf16x4_t, v[0]),
+                                                    __builtin_bit_cast(bf16x4_t, v[1]), 0, 1, 2, 3, 4, 5, 6, 7);
+        acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, acc_o[dt], 0, 0, 0);
       }
     }
-    if (kb + 1 < nkb) store_tile(buf ^ 1);
+  };
+
+  const Tile T0{K0, V0}, T1{K1, V1};
+  load_tile(T0, 0);
+  wait_vmem();
+  __syncthreads();
+  int kb = 0;
+  for (; kb + 2 <= nkb; kb += 2) {
+    if (kb + 1 < nkb) load_tile(T1, kb + 1);
+    block(T0, kb);
+    wait_vmem();
+    __syncthreads();
+    if (kb + 2 < nkb) load_tile(T0, kb + 2);
+    block(T1, kb + 1);
+    wait_vmem();
     __syncthreads();
   }
+  if (kb < nkb) block(T0, kb);
 
   // normalise and store: lane holds d = t*32 + (r>>2)*8 + lhi*4 + (r&3) of its query
   const float inv_l = 1.0f / l_run;
