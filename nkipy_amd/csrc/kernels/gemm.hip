@@ -44,6 +44,7 @@ enum {
   GEMM_BIAS = 1,      // + bias[col] (bf16)
   GEMM_SCALE = 2,     // * scale[col] (fp32), per output column (fp8 weights)
   GEMM_RESID = 4,     // + residual[row][col] (same dtype as C)
+  GEMM_VEC = 8,       // C / residual rows allow aligned 4-element vector access
 };
 
 struct GemmArgs {
@@ -74,6 +75,18 @@ template <> struct OutT<bf16> {
   static __device__ __forceinline__ float load(const void *C, int64_t i) {
     return bf16_to_f32(reinterpret_cast<const uint16_t *>(C)[i]);
   }
+  static __device__ __forceinline__ void store4(void *C, int64_t i, const float (&v)[4]) {
+    *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(C) + i) =
+        make_uint2((uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
+                   (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16));
+  }
+  static __device__ __forceinline__ void load4(const void *C, int64_t i, float (&v)[4]) {
+    const uint2 w = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(C) + i);
+    v[0] = __uint_as_float(w.x << 16);
+    v[1] = __uint_as_float(w.x & 0xffff0000u);
+    v[2] = __uint_as_float(w.y << 16);
+    v[3] = __uint_as_float(w.y & 0xffff0000u);
+  }
 };
 template <> struct OutT<float> {
   static __device__ __forceinline__ void store(void *C, int64_t i, float v) {
@@ -81,6 +94,16 @@ template <> struct OutT<float> {
   }
   static __device__ __forceinline__ float load(const void *C, int64_t i) {
     return reinterpret_cast<const float *>(C)[i];
+  }
+  static __device__ __forceinline__ void store4(void *C, int64_t i, const float (&v)[4]) {
+    *reinterpret_cast<float4 *>(reinterpret_cast<float *>(C) + i) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+  static __device__ __forceinline__ void load4(const void *C, int64_t i, float (&v)[4]) {
+    const float4 w = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(C) + i);
+    v[0] = w.x;
+    v[1] = w.y;
+    v[2] = w.z;
+    v[3] = w.w;
   }
 };
 
@@ -333,7 +356,7 @@ __device__ __forceinline__ void mma_tile(f32x16 (&acc)[4][4], const uint8_t *As,
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk & 1][i], bf[kk & 1][j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[kk & 1][j], af[kk & 1][i], acc[i][j], 0, 0, 0);
   }
 }
 
@@ -470,48 +493,93 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
   }
   if (t < ktiles) mma_tile<BMODE>(acc, A0, B0, wm, brow, lane);
 
+  // epilogue.  The MFMAs computed C^T tiles (B fragment as the A operand),
+  // so a lane holds row m = m0 + wm*128 + i*32 + l32 of C and, per tile,
+  // 16 columns n = (tile column) + 8 q + 4 lhi + e (q, e = 0..3): runs of 4
+  // consecutive columns, stored / read as one vector.
   const int l32 = lane & 31, lhi = lane >> 5;
-  // epilogue: lane holds column l32 of each 32 x 32 tile and rows
-  // (r / 4) * 8 + lhi * 4 + r % 4
+  const bool vec = (a.flags & GEMM_VEC) != 0;
+  auto put4 = [&](int64_t row, int64_t col, const float (&v)[4]) {
+    if (vec && col + 3 < a.N) {
+      OutT<TC>::store4(a.C, row * a.ldc + col, v);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (col + e < a.N) OutT<TC>::store(a.C, row * a.ldc + col + e, v[e]);
+    }
+  };
   if (SWIGLU) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 2; ++j) {
+      const int64_t nb = n0 + wn * 64 + j * 32 + lhi * 4;
+      float sg[16], su[16];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int64_t col = n0 + wn * 64 + j * 32 + l32;
-        if (col >= a.N) continue;
-        const float sg = (a.flags & GEMM_SCALE) ? a.scale0[col] : 1.f;
-        const float su = (a.flags & GEMM_SCALE) ? a.scale1[col] : 1.f;
+      for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t row = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
-          if (row < a.M) {
-            const float g = acc[i][j][r] * sg;
-            const float u = acc[i][j + 2][r] * su;
-            const float h = g * (1.0f / (1.0f + expf(-g))) * u;
-            OutT<TC>::store(a.C, row * a.ldc + col, h);
+        for (int e = 0; e < 4; ++e) {
+          const int64_t col = nb + q * 8 + e;
+          const bool in = (a.flags & GEMM_SCALE) && col < a.N;
+          sg[q * 4 + e] = in ? a.scale0[col] : 1.f;
+          su[q * 4 + e] = in ? a.scale1[col] : 1.f;
+        }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t row = m0 + wm * 128 + i * 32 + l32;
+        if (row >= a.M) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t col = nb + q * 8;
+          if (col >= a.N) continue;
+          float h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float g = acc[i][j][q * 4 + e] * sg[q * 4 + e];
+            const float u = acc[i][j + 2][q * 4 + e] * su[q * 4 + e];
+            h[e] = g * (1.0f / (1.0f + expf(-g))) * u;
           }
+          put4(row, col, h);
         }
       }
+    }
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 4; ++j) {
+      const int64_t nb = n0 + wn * 128 + j * 32 + lhi * 4;
+      float sc[16], bi[16];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t col = n0 + wn * 128 + j * 32 + l32;
-        if (col >= a.N) continue;
-        const float sc = (a.flags & GEMM_SCALE) ? a.scale0[col] : 1.f;
-        const float bi = (a.flags & GEMM_BIAS) ? bf16_to_f32(reinterpret_cast<const uint16_t *>(a.bias)[col]) : 0.f;
+      for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t row = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
-          if (row < a.M) {
-            float v = acc[i][j][r] * sc + bi;
-            if (a.flags & GEMM_RESID) v += OutT<TC>::load(a.resid, row * a.ldc + col);
-            OutT<TC>::store(a.C, row * a.ldc + col, v);
+        for (int e = 0; e < 4; ++e) {
+          const int64_t col = nb + q * 8 + e;
+          sc[q * 4 + e] = ((a.flags & GEMM_SCALE) && col < a.N) ? a.scale0[col] : 1.f;
+          bi[q * 4 + e] = ((a.flags & GEMM_BIAS) && col < a.N)
+                              ? bf16_to_f32(reinterpret_cast<const uint16_t *>(a.bias)[col]) : 0.f;
+        }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t row = m0 + wm * 128 + i * 32 + l32;
+        if (row >= a.M) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t col = nb + q * 8;
+          if (col >= a.N) continue;
+          float r4[4] = {0.f, 0.f, 0.f, 0.f};
+          if (a.flags & GEMM_RESID) {
+            if (vec && col + 3 < a.N) {
+              OutT<TC>::load4(a.resid, row * a.ldc + col, r4);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (col + e < a.N) r4[e] = OutT<TC>::load(a.resid, row * a.ldc + col + e);
+            }
           }
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = acc[i][j][q * 4 + e] * sc[q * 4 + e] + bi[q * 4 + e] + r4[e];
+          put4(row, col, v);
         }
       }
+    }
   }
 }
 

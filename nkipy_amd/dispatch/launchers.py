@@ -225,6 +225,7 @@ class GemmArgs(ctypes.Structure):
 GEMM_BIAS = 1
 GEMM_SCALE = 2
 GEMM_RESID = 4
+GEMM_VEC = 8
 GEMM_BM = 256
 GEMM_BN = 256
 
@@ -284,6 +285,10 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
     if tiles_m * tiles_n >= 2**31:
         raise LaunchError("GEMM grid too large")
     flags = (GEMM_BIAS if bias_ptr else 0) | (GEMM_SCALE if scale_ptr else 0) | (GEMM_RESID if resid_ptr else 0)
+    # 4-element vector access to C (and the residual) when rows keep 8 / 16-byte alignment
+    vbytes = 4 * c_dtype.itemsize
+    if ldc % 4 == 0 and c_ptr % vbytes == 0 and (not resid_ptr or resid_ptr % vbytes == 0):
+        flags |= GEMM_VEC
     args = GemmArgs(a_ptr, b_ptr, up_ptr or None, c_ptr, bias_ptr or None, scale_ptr or None,
                     up_scale_ptr or None, resid_ptr or None, M, N, K, lda, ldb, ldc,
                     tiles_m, tiles_n, flags, 0)
