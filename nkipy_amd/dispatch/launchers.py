@@ -76,7 +76,9 @@ class SoftmaxArgs(ctypes.Structure):
 # (block, chunks) register variants: a row of up to block*chunks*8 elements
 # first fit wins; for 2K-8K element rows the wider variants measured fastest
 # on MI355X (fewer resident waves per CU, all loads of a row in flight)
-_ROW_REG_VARIANTS = [(64, 1), (256, 1), (512, 4)]
+# first fitting (block, chunks) for a row; rows of up to 4096 elements take
+# 128 threads x 4 chunks (measured best for fp32 rows of 4096 on MI355X)
+_ROW_REG_VARIANTS = [(64, 1), (256, 1), (128, 4), (512, 4)]
 # every (block, chunks) pair compiled for the row kernels
 _ALL_REG_VARIANTS = {(64, 1), (128, 4), (256, 1), (256, 2), (512, 1), (256, 4), (512, 4)}
 _SOFTMAX_TYPES = {("f32", "f32"), ("bf16", "bf16"), ("bf16", "f32"), ("f32", "bf16"), ("f16", "f16")}
