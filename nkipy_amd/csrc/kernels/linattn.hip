@@ -11,18 +11,30 @@
 // (no reference kernel computes this; the nearest analogue is the recurrent
 // DeltaNet kernel, examples/linear_attention/deltanet.py:74-128).
 //
-// Layout: q, k, v, o are (B*H, T, 128) row-major bf16.  One workgroup of 4
-// waves owns one (b, h) sequence and a 32-column slice of d_v, so the four
-// slices of a head run as four workgroups (256 workgroups for B*H = 64) and
-// each keeps its 128 x 32 fp32 state slice in MFMA accumulator registers for
-// the whole sequence.  Per chunk: the next chunk's q / k / v tile is fetched
-// into registers while the current one is processed; phi is applied on the
-// way into LDS; A = phi(Q) phi(K)^T (32x32x16 MFMA), phi(Q) S (16x16x32),
-// A V (16x16x32) and the state update phi(K)^T V (32x32x16) run on fp16 MFMA
-// with fp32 accumulation; the normaliser is a VALU dot product; the output
-// tile is staged in LDS and written with 16-byte stores.  The state enters
-// the phi(Q) S product as an fp16 copy (double-buffered in LDS); the running
-// state itself stays fp32.
+// Layout: q, k, v, o are (B*H, T, 128) row-major bf16.  One workgroup of 8
+// waves owns one (b, h) sequence and a 32-column slice j0.. of d_v; the four
+// slices of a head run as four workgroups placed on one XCD (shared L2).
+//
+// Per chunk, query wave w (0..3) owns queries 16w..16w+15 and state wave w
+// (4..7) owns state rows d = 32(w-4)..+31; two waves share each SIMD, so one
+// wave's VALU work overlaps the other's MFMAs.  Products are in transposed
+// form so that every lane owns one query column:
+//   A^T = phi(K) phi(Q_w)^T            16x16x32 MFMA, key tiles 0..w, causal
+//                                       mask on the diagonal tile
+//   O^T = S_{c-1}^T phi(Q_w)^T + V^T A^T   (32 j x 16 queries); A^T enters
+//                                       the second product straight from its
+//                                       accumulators, V^T fragments follow
+//                                       its key order (ds_read_b64_tr_b16)
+//   den = rowsum(A^T) (lane-local) + phi(Q_w) z_{c-1} (VALU dot)
+//   S[d-slice] += phi(K)^T V           32x32x16 MFMA, K^T and V fragments by
+//                                       transpose reads; z from the same MFMA
+//                                       against an all-ones B operand
+// The output rows are normalised and stored (8-byte stores) by the wave that
+// owns them; the new state's fp16 copy S^T and z go to the other LDS buffer
+// for the next chunk.  phi of the next chunk (the VALU-bound part: one exp
+// per element) is computed between this chunk's MFMAs and the barrier, from
+// q / k / v fetched two chunks ahead into registers, so that it overlaps the
+// MFMAs.  One barrier per chunk.
 //
 // MFMA operands are fp16, not bf16: phi(x) = 1 + x + ... for the small inputs
 // of attention, so the information sits in deviations from 1 and in
@@ -36,8 +48,11 @@
 using namespace nk;
 
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 #define LC 64    // chunk length
 #define LD 128   // head dim (q, k)
@@ -53,31 +68,90 @@ struct LinAttnArgs {
   int64_t T;       // sequence length (multiple of 64)
 };
 
-// swizzled element offsets of the LDS tiles (16-byte chunks permuted by row)
-__device__ __forceinline__ int off128(int row, int col) {  // rows of 128 16-bit values
-  return row * 128 + ((((col >> 3) ^ (row & 15))) << 3) + (col & 7);
+// Byte offsets in the LDS tiles.  Rows of 256 bytes (phi(Q), phi(K) [t][d],
+// S^T [j][d]): 16-byte chunk c of row r at c ^ (r & 15).  V [s][j]: rows of
+// 64 bytes, chunk c at c ^ ((r >> 2) & 3).
+__device__ __forceinline__ int o256(int r, int byte) {
+  return r * 256 + (((byte >> 4) ^ (r & 15)) << 4) + (byte & 15);
 }
-__device__ __forceinline__ int off64(int row, int col) {  // rows of 64 16-bit values
-  return row * 64 + ((((col >> 3) ^ ((row >> 1) & 7))) << 3) + (col & 7);
+__device__ __forceinline__ int o64(int r, int byte) {
+  return r * 64 + (((byte >> 4) ^ ((r >> 2) & 3)) << 4) + (byte & 15);
 }
 
-__device__ __forceinline__ float phi(float x) { return x > 0.f ? x + 1.f : __expf(x); }
+// ds_read_b64_tr_b16: within each 16-lane group, source lane q + 4 j points
+// at 4 values of row j; output lane t receives column t of the 4 rows.
+__device__ __forceinline__ f16x4_t tr_read(const uint8_t *p) {
+  return __builtin_bit_cast(f16x4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)p));
+}
 
-extern "C" __global__ __launch_bounds__(256, 1) void nk_linattn_c64_d128(LinAttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t Qs[LC * LD];       // [t][d]
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[LC * LD];       // [s][d]
-  __shared__ __attribute__((aligned(16))) uint16_t Kts[LD * LC];      // [d][s]
-  __shared__ __attribute__((aligned(16))) uint16_t Vts[LS * LC];      // [j][s]
-  __shared__ __attribute__((aligned(16))) uint16_t As[LC * LC];       // [t][s]
-  __shared__ __attribute__((aligned(16))) uint16_t St[2][LS * LD];    // [j][d]
-  __shared__ __attribute__((aligned(16))) uint16_t Os[LC * LS];       // [t][j]
-  __shared__ float zs[2][LD];
-  __shared__ float dens[LC];
+__device__ __forceinline__ f16x8_t cat(f16x4_t a, f16x4_t b) {
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+// phi of 8 bf16 values -> 8 fp16 (16 bytes): exp(min(x, 0)) + max(x, 0) in
+// packed fp16 arithmetic.  bf16 -> fp16 is exact for |x| >= 2^-14 (8
+// significant bits fit in 11), so the round-toward-zero pack only truncates
+// fp16 subnormals, where phi(x) = 1 + x rounds to 1 anyway.
+__device__ __forceinline__ uint4 phi8(uint4 raw) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  const h2 zero = {(_Float16)0.f, (_Float16)0.f};
+  const h2 l2e = {(_Float16)1.44269504088896340736f, (_Float16)1.44269504088896340736f};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const h2 x = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(w[i] << 16),
+                                                                   __uint_as_float(w[i] & 0xffff0000u)));
+    const h2 t = __builtin_elementwise_min(x, zero) * l2e;
+    h2 e;
+    e[0] = __builtin_exp2f16(t[0]);
+    e[1] = __builtin_exp2f16(t[1]);
+    o[i] = __builtin_bit_cast(uint32_t, e + __builtin_elementwise_max(x, zero));
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// bf16 x 8 -> fp16 x 8 (round to nearest even; V may be large)
+__device__ __forceinline__ uint4 to_f16x8(uint4 raw) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    o[i] = (uint32_t)f32_to_f16(__uint_as_float(w[i] << 16)) |
+           ((uint32_t)f32_to_f16(__uint_as_float(w[i] & 0xffff0000u)) << 16);
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+struct Stage {  // one chunk's operands in LDS
+  uint8_t *Q;   // phi(Q) [64 t][128 d] fp16
+  uint8_t *K;   // phi(K) [64 s][128 d] fp16
+  uint8_t *V;   // V slice [64 s][32 j] fp16
+  uint8_t *St;  // S^T of the state before this chunk [32 j][128 d] fp16
+  float *z;     // z before this chunk [128]
+};
+
+struct Raw {  // one chunk's inputs in registers (this thread's share)
+  uint4 q[2], k[2], v;
+};
+
+extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttnArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t Q0[LC * 256];
+  __shared__ __attribute__((aligned(1024))) uint8_t Q1[LC * 256];
+  __shared__ __attribute__((aligned(1024))) uint8_t K0[LC * 256];
+  __shared__ __attribute__((aligned(1024))) uint8_t K1[LC * 256];
+  __shared__ __attribute__((aligned(1024))) uint8_t V0[LC * 64];
+  __shared__ __attribute__((aligned(1024))) uint8_t V1[LC * 64];
+  __shared__ __attribute__((aligned(1024))) uint8_t ST0[LS * 256];
+  __shared__ __attribute__((aligned(1024))) uint8_t ST1[LS * 256];
+  __shared__ float Z0[LD], Z1[LD];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int l32 = lane & 31, lhi = lane >> 5;
-  const int l16 = lane & 15, lq = lane >> 4;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, grp = lane >> 4;  // 16x16 operand roles
+  const int l32 = lane & 31, lhi = lane >> 5;  // 32x32 operand roles
+
   // The four d_v slices of a head read the same q / k tiles: give them
   // workgroup ids that are equal modulo 8 so they land on the same XCD and
   // share its L2 (workgroups are dealt to the 8 XCDs round robin).
@@ -95,201 +169,190 @@ extern "C" __global__ __launch_bounds__(256, 1) void nk_linattn_c64_d128(LinAttn
   const int64_t base = bh * a.T * LD;
   const int nchunks = (int)(a.T / LC);
 
-  // state accumulator: rows d = wave*32 + ..., cols j (32), fp32
-  f32x16 S;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) S[r] = 0.f;
-  if (tid < LD) zs[0][tid] = 0.f;
-  for (int i = tid; i < LS * LD; i += 256) St[0][i] = 0;  // S_0 = 0 (fp16 zero bits)
-
-  // register staging: two chunks in flight (prefetch distance 2)
-  uint4 rqA[4], rkA[4], rvA, rqB[4], rkB[4], rvB;
-  auto load_chunk = [&](int c, uint4 (&rq)[4], uint4 (&rk)[4], uint4 &rv) {
+  // ---------------- input staging -----------------------------------------
+  // thread -> q / k chunks (row tid/16 + 32 i, 8 columns at 8 (tid % 16));
+  // threads 0..255 -> v chunk (row tid / 4, 8 columns j0 + 8 (tid % 4)).
+  // q / k are read by the four slice workgroups of the head: plain (cached)
+  // loads.
+  auto load_raw = [&](Raw &r, int c) {
     const int64_t cb = base + (int64_t)c * LC * LD;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ci = tid + 256 * i;
-      const int row = ci >> 4, col = (ci & 15) * 8;
-      rq[i] = *reinterpret_cast<const uint4 *>(a.q + cb + row * LD + col);
-      rk[i] = *reinterpret_cast<const uint4 *>(a.k + cb + row * LD + col);
+    for (int i = 0; i < 2; ++i) {
+      const int row = (tid >> 4) + 32 * i, col = (tid & 15) * 8;
+      r.q[i] = *reinterpret_cast<const uint4 *>(a.q + cb + row * LD + col);
+      r.k[i] = *reinterpret_cast<const uint4 *>(a.k + cb + row * LD + col);
     }
-    const int vrow = tid >> 2, vcol = j0 + (tid & 3) * 8;
-    rv = *reinterpret_cast<const uint4 *>(a.v + cb + vrow * LDV + vcol);
+    if (tid < 256) r.v = *reinterpret_cast<const uint4 *>(a.v + cb + (tid >> 2) * LDV + j0 + (tid & 3) * 8);
+  };
+  auto stage_in = [&](const Raw &r, const Stage &s) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = (tid >> 4) + 32 * i, byte = (tid & 15) * 16;
+      *reinterpret_cast<uint4 *>(s.Q + o256(row, byte)) = phi8(r.q[i]);
+      *reinterpret_cast<uint4 *>(s.K + o256(row, byte)) = phi8(r.k[i]);
+    }
+    if (tid < 256) *reinterpret_cast<uint4 *>(s.V + o64(tid >> 2, (tid & 3) * 16)) = to_f16x8(r.v);
   };
 
-  auto body = [&](int c, uint4 (&rq)[4], uint4 (&rk)[4], uint4 &rv) {
-    const int cur = c & 1, nxt = cur ^ 1;
-    // ---- step 1: phi and staging into LDS ---------------------------------
+  // ---------------- per-wave state ------------------------------------------
+  f32x16 S, Z;  // S[d = 32w + row][j = col] and z[d] (in every column), fp32
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ci = tid + 256 * i;
-      const int row = ci >> 4, col = (ci & 15) * 8;
-      float fq[8], fk[8];
-      Raw8<bf16> rr;
-      rr.w[0] = rq[i];
-      decode8(rr, fq);
-      rr.w[0] = rk[i];
-      decode8(rr, fk);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        fq[e] = phi(fq[e]);
-        fk[e] = phi(fk[e]);
-      }
-      Raw8<f16> oq, ok;
-      encode8(fq, oq);
-      encode8(fk, ok);
-      *reinterpret_cast<uint4 *>(Qs + off128(row, col)) = oq.w[0];
-      *reinterpret_cast<uint4 *>(Ks + off128(row, col)) = ok.w[0];
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        Kts[off64(col + e, row)] = (uint16_t)h16_of(ok.w[0], e);
-    }
-    {
-      const int vrow = tid >> 2, vc = (tid & 3) * 8;
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        Vts[off64(vc + e, vrow)] = f32_to_f16(bf16_to_f32((uint16_t)h16_of(rv, e)));
-    }
-    if (c + 2 < nchunks) load_chunk(c + 2, rq, rk, rv);
-    __syncthreads();  // B1
-    // flush the previous chunk's output tile (staged in Os)
-    if (c > 0) {
-      const int row = tid >> 2, part = (tid & 3) * 8;
-      const int64_t o_off = base + ((int64_t)(c - 1) * LC + row) * LDV + j0 + part;
-      nt_store16(a.o + o_off, *reinterpret_cast<const uint4 *>(Os + row * LS + part));
-    }
-
-    // ---- step 2a: A = phi(Q) phi(K)^T (wave tile (wave>>1, wave&1)), masked
-    {
-      const int ti = wave >> 1, tj = wave & 1;
-      f32x16 acc;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < LD / 16; ++kk) {
-        const int col = kk * 16 + lhi * 8;
-        f16x8_t af = *reinterpret_cast<const f16x8_t *>(Qs + off128(ti * 32 + l32, col));
-        f16x8_t bf = *reinterpret_cast<const f16x8_t *>(Ks + off128(tj * 32 + l32, col));
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc, 0, 0, 0);
-      }
-      const int s = tj * 32 + l32;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int t = ti * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
-        const float val = (s <= t) ? acc[r] : 0.f;
-        As[off64(t, s)] = f32_to_f16(val);
-      }
-    }
-    // ---- step 2b: O = phi(Q) S_prev (rows wave*16.., both 16-col tiles) ----
-    f32x4 o0, o1;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) { o0[r] = 0.f; o1[r] = 0.f; }
-    {
-      const uint16_t *st = St[cur];
-#pragma unroll
-      for (int kk = 0; kk < LD / 32; ++kk) {
-        const int col = kk * 32 + lq * 8;
-        f16x8_t af = *reinterpret_cast<const f16x8_t *>(Qs + off128(wave * 16 + l16, col));
-        f16x8_t b0 = *reinterpret_cast<const f16x8_t *>(st + off128(l16, col));
-        f16x8_t b1 = *reinterpret_cast<const f16x8_t *>(st + off128(16 + l16, col));
-        o0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, b0, o0, 0, 0, 0);
-        o1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, b1, o1, 0, 0, 0);
-      }
-    }
-    // ---- step 2c: state update S += phi(K)^T V; fp16 copy for the next chunk
-    {
-#pragma unroll
-      for (int kk = 0; kk < LC / 16; ++kk) {
-        const int col = kk * 16 + lhi * 8;
-        f16x8_t af = *reinterpret_cast<const f16x8_t *>(Kts + off64(wave * 32 + l32, col));
-        f16x8_t bf = *reinterpret_cast<const f16x8_t *>(Vts + off64(l32, col));
-        S = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, S, 0, 0, 0);
-      }
-      uint16_t *stn = St[nxt];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int d = wave * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
-        stn[off128(l32, d)] = f32_to_f16(S[r]);
-      }
-    }
-    // ---- step 2d: z_next = z + colsum(phi(K)) (fp16 values, as in S) -------
-    if (tid < LD) {
-      float zsum = zs[cur][tid];
-#pragma unroll
-      for (int s8 = 0; s8 < LC / 8; ++s8) {
-        float f[8];
-        Raw8<f16> rr;
-        rr.w[0] = *reinterpret_cast<const uint4 *>(Kts + off64(tid, s8 * 8));
-        decode8(rr, f);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) zsum += f[e];
-      }
-      zs[nxt][tid] = zsum;
-    }
-    __syncthreads();  // B2: As complete
-
-    // ---- step 3a: O += A V ------------------------------------------------
-#pragma unroll
-    for (int kk = 0; kk < LC / 32; ++kk) {
-      const int col = kk * 32 + lq * 8;
-      f16x8_t af = *reinterpret_cast<const f16x8_t *>(As + off64(wave * 16 + l16, col));
-      f16x8_t b0 = *reinterpret_cast<const f16x8_t *>(Vts + off64(l16, col));
-      f16x8_t b1 = *reinterpret_cast<const f16x8_t *>(Vts + off64(16 + l16, col));
-      o0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, b0, o0, 0, 0, 0);
-      o1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, b1, o1, 0, 0, 0);
-    }
-    // ---- step 3b: den[t] = phi(q_t) . z_prev + rowsum(A[t]) ---------------
-    {
-      const int t = tid >> 2, p = tid & 3;
-      float acc = 0.f;
-      // intra: 16 columns of A
-#pragma unroll
-      for (int s8 = 0; s8 < 2; ++s8) {
-        float f[8];
-        Raw8<f16> rr;
-        rr.w[0] = *reinterpret_cast<const uint4 *>(As + off64(t, p * 16 + s8 * 8));
-        decode8(rr, f);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc += f[e];
-      }
-      // inter: 32 feature dims
-      const float *z = zs[cur];
-#pragma unroll
-      for (int d8 = 0; d8 < 4; ++d8) {
-        float f[8];
-        Raw8<f16> rr;
-        const int d0 = p * 32 + d8 * 8;
-        rr.w[0] = *reinterpret_cast<const uint4 *>(Qs + off128(t, d0));
-        decode8(rr, f);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc = fmaf(f[e], z[d0 + e], acc);
-      }
-      acc += __shfl_xor(acc, 1, 64);
-      acc += __shfl_xor(acc, 2, 64);
-      if (p == 0) dens[t] = acc;
-    }
-    __syncthreads();  // B3: dens complete
-
-    // ---- step 4: normalise and stage the output tile ----------------------
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = wave * 16 + lq * 4 + r;
-      const float den = dens[t];
-      Os[t * LS + l16] = f32_to_bf16(o0[r] / den);
-      Os[t * LS + 16 + l16] = f32_to_bf16(o1[r] / den);
-    }
-  };
-
-  load_chunk(0, rqA, rkA, rvA);
-  if (nchunks > 1) load_chunk(1, rqB, rkB, rvB);
-  for (int c = 0; c < nchunks; c += 2) {
-    body(c, rqA, rkA, rvA);
-    if (c + 1 < nchunks) body(c + 1, rqB, rkB, rvB);
+  for (int r = 0; r < 16; ++r) {
+    S[r] = 0.f;
+    Z[r] = 0.f;
   }
+  f16x8_t ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
+
+  // ---------------- one chunk -----------------------------------------------
+  auto query_side = [&](const Stage &cur, int c, const int wave) {
+    // phi(Q_w) fragments: rows (queries) 16w + l16, d = 32 st + 8 grp + 0..7
+    f16x8_t qf[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+      qf[st] = *reinterpret_cast<const f16x8_t *>(cur.Q + o256(16 * wave + l16, (32 * st + 8 * grp) * 2));
+
+    // A^T tiles (keys 16 kt + .., queries 16w + ..); lane: column = query l16,
+    // rows = keys 4 grp + r
+    f32x4 at[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) at[kt][r] = 0.f;
+      if (kt <= wave) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const f16x8_t kf =
+              *reinterpret_cast<const f16x8_t *>(cur.K + o256(16 * kt + l16, (32 * st + 8 * grp) * 2));
+          at[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[st], at[kt], 0, 0, 0);
+        }
+        if (kt == wave) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (4 * grp + r > l16) at[kt][r] = 0.f;  // key > query
+        }
+      }
+    }
+    // normaliser: in-chunk sum over keys (this lane's rows) plus
+    // phi(q) . z_prev over d = 32 grp .. 32 grp + 31, then over the 4 groups
+    float den = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) den += at[kt][r];
+    {
+      const int q = 16 * wave + l16;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const f16x8_t pq = *reinterpret_cast<const f16x8_t *>(cur.Q + o256(q, (32 * grp + 8 * u) * 2));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) den = fmaf((float)pq[e], cur.z[32 * grp + 8 * u + e], den);
+      }
+    }
+    den += __shfl_xor(den, 16, 64);
+    den += __shfl_xor(den, 32, 64);
+
+    // O^T (j tiles jt: rows j = 16 jt + 4 grp + r, column = query l16)
+    f32x4 ot[2];
+#pragma unroll
+    for (int jt = 0; jt < 2; ++jt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ot[jt][r] = 0.f;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const f16x8_t sf =
+            *reinterpret_cast<const f16x8_t *>(cur.St + o256(16 * jt + l16, (32 * st + 8 * grp) * 2));
+        ot[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sf, qf[st], ot[jt], 0, 0, 0);
+      }
+    }
+    // + V^T A^T: 32 keys per step p = key tiles (2p, 2p+1); B element e of
+    // lane group g is key 16 (2p + e/4) + 4 g + e%4
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      if (2 * p > wave) continue;
+      f16x8_t pf;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pf[e] = (_Float16)at[2 * p][e];
+        pf[4 + e] = (_Float16)at[2 * p + 1][e];
+      }
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt) {
+        // transpose reads: source row 16 tile + 4 grp + l16/4, columns 16 jt + 4 (l16 % 4)
+        const int jb = (16 * jt + 4 * (l16 & 3)) * 2;
+        const f16x4_t v0 = tr_read(cur.V + o64(16 * (2 * p) + 4 * grp + (l16 >> 2), jb));
+        const f16x4_t v1 = tr_read(cur.V + o64(16 * (2 * p + 1) + 4 * grp + (l16 >> 2), jb));
+        ot[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cat(v0, v1), pf, ot[jt], 0, 0, 0);
+      }
+    }
+    // normalise and store: o[t][j0 + j], 4 consecutive j per lane
+    {
+      const float inv = 1.0f / den;
+      const int64_t t = (int64_t)c * LC + 16 * wave + l16;
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt) {
+        const uint32_t w0 = (uint32_t)f32_to_bf16(ot[jt][0] * inv) | ((uint32_t)f32_to_bf16(ot[jt][1] * inv) << 16);
+        const uint32_t w1 = (uint32_t)f32_to_bf16(ot[jt][2] * inv) | ((uint32_t)f32_to_bf16(ot[jt][3] * inv) << 16);
+        *reinterpret_cast<uint2 *>(a.o + base + t * LDV + j0 + 16 * jt + 4 * grp) = make_uint2(w0, w1);
+      }
+    }
+  };
+  auto state_side = [&](const Stage &cur, const Stage &nxt, const int wave) {
+    // state update for rows d = 32w + ..: S += phi(K)^T V, z += phi(K)^T 1.
+    // A operand (K^T): row d = 32w + l32, keys 16 st + 8 lhi + 0..7 -> two
+    // transpose reads of 4 keys; B operand (V): column j = l32, same keys.
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int kb = 16 * st + 8 * (grp >> 1) + (l16 >> 2);
+      const int db = (32 * wave + 16 * (grp & 1) + 4 * (l16 & 3)) * 2;
+      const int jb = (16 * (grp & 1) + 4 * (l16 & 3)) * 2;
+      const f16x8_t kf = cat(tr_read(cur.K + o256(kb, db)), tr_read(cur.K + o256(kb + 4, db)));
+      const f16x8_t vf = cat(tr_read(cur.V + o64(kb, jb)), tr_read(cur.V + o64(kb + 4, jb)));
+      S = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, vf, S, 0, 0, 0);
+      Z = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ones, Z, 0, 0, 0);
+    }
+    // fp16 S^T and z for the next chunk: lane holds column j = l32 and rows
+    // d = 32w + 8 (r/4) + 4 lhi + r%4
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d = 32 * wave + 8 * g4 + 4 * lhi;
+      const uint32_t w0 = (uint32_t)f32_to_f16(S[4 * g4 + 0]) | ((uint32_t)f32_to_f16(S[4 * g4 + 1]) << 16);
+      const uint32_t w1 = (uint32_t)f32_to_f16(S[4 * g4 + 2]) | ((uint32_t)f32_to_f16(S[4 * g4 + 3]) << 16);
+      *reinterpret_cast<uint2 *>(nxt.St + o256(l32, d * 2)) = make_uint2(w0, w1);
+      if (l32 == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) nxt.z[d + r] = Z[4 * g4 + r];
+      }
+    }
+  };
+  auto chunk = [&](const Stage &cur, const Stage &nxt, int c) {
+    if (wave < 4)
+      query_side(cur, c, wave);
+    else
+      state_side(cur, nxt, wave - 4);
+  };
+
+  const Stage s0{Q0, K0, V0, ST0, Z0}, s1{Q1, K1, V1, ST1, Z1};
+  // S_0 = 0, z_0 = 0
+  for (int i = tid; i < LS * 256 / 16; i += 512) reinterpret_cast<uint4 *>(ST0)[i] = make_uint4(0, 0, 0, 0);
+  if (tid < LD) Z0[tid] = 0.f;
+  Raw ra, rb;
+  load_raw(ra, 0);
+  if (nchunks > 1) load_raw(rb, 1);
+  stage_in(ra, s0);
   __syncthreads();
-  {
-    const int row = tid >> 2, part = (tid & 3) * 8;
-    const int64_t o_off = base + ((int64_t)(nchunks - 1) * LC + row) * LDV + j0 + part;
-    nt_store16(a.o + o_off, *reinterpret_cast<const uint4 *>(Os + row * LS + part));
+  // iteration c: fetch chunk c + 2, compute chunk c, stage chunk c + 1
+  int c = 0;
+  for (; c + 2 <= nchunks; c += 2) {
+    if (c + 2 < nchunks) load_raw(ra, c + 2);
+    chunk(s0, s1, c);
+    stage_in(rb, s1);
+    __syncthreads();
+    if (c + 3 < nchunks) load_raw(rb, c + 3);
+    chunk(s1, s0, c + 1);
+    if (c + 2 < nchunks) stage_in(ra, s0);
+    __syncthreads();
   }
+  if (c < nchunks) chunk(s0, s1, c);
 }

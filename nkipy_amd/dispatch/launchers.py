@@ -333,7 +333,7 @@ def linear_attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, BH: int, T:
         raise LaunchError("linear attention grid too large")
     n = T // chunk
     flops_chunk = 2 * chunk * chunk * D + 2 * chunk * D * Dv + 2 * chunk * chunk * Dv + 2 * D * Dv * chunk
-    return Launch("linattn", "nk_linattn_c64_d128", (BH * 4, 1, 1), (256, 1, 1),
+    return Launch("linattn", "nk_linattn_c64_d128", (BH * 4, 1, 1), (512, 1, 1),
                   LinAttnArgs(q_ptr, k_ptr, v_ptr, o_ptr, BH, T),
                   bytes=4 * BH * T * D * 2, flops=BH * n * flops_chunk)
 
