@@ -1,0 +1,246 @@
+"""Host-side tests (no GPU): the C-ABI library and its exports, the tracer's
+naming and promotion contract, strided views, pattern lowering of every
+hot-path kernel at its workload shape, and the launchers' operand checks."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from nkipy_amd import _build
+from nkipy_amd.core import dtypes as dt
+from nkipy_amd.core.backend import promotion as P
+from nkipy_amd.core.trace import NKIPyKernel
+from nkipy_amd.dispatch import launchers as LA
+from nkipy_amd.dispatch.lower import lower
+from nkipy_amd.dispatch.views import resolve
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+# ---------------------------------------------------------------------------
+# C ABI
+# ---------------------------------------------------------------------------
+def _declared_symbols():
+    text = open(os.path.join(ROOT, "include", "nkipy_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nkh_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    path = _build.RUNTIME_LIB
+    assert path.exists(), "build the runtime first (__graft_entry__.build())"
+    lib = ctypes.CDLL(str(path))
+    names = _declared_symbols()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_last_error_and_uninitialised_calls_fail_cleanly():
+    lib = ctypes.CDLL(str(_build.RUNTIME_LIB))
+    lib.nkh_last_error.restype = ctypes.c_char_p
+    flag = ctypes.c_int(-1)
+    assert lib.nkh_is_initialized(ctypes.byref(flag)) == 0
+    if flag.value == 0:
+        # device calls before nkh_init report NOT_INIT instead of touching HIP
+        assert lib.nkh_sync() == 3
+        assert b"init" in lib.nkh_last_error().lower()
+
+
+def test_every_kernel_object_has_a_manifest():
+    for src in _build.kernel_sources():
+        hsaco = _build.hsaco_path(src.stem)
+        assert hsaco.exists(), hsaco
+        assert hsaco.with_suffix(".json").exists()
+
+
+# ---------------------------------------------------------------------------
+# promotion rules (expectations of tests/unit/test_type_promotion.py)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("t0,t1,expected", [
+    (dt.bool_, dt.int32, dt.int32), (dt.bool_, dt.float32, dt.float32),
+    (dt.bool_, P.WEAK_INT, dt.int32), (dt.bool_, P.WEAK_FLOAT, dt.float32),
+    (P.WEAK_INT, dt.int8, dt.int8), (P.WEAK_INT, dt.float32, dt.float32),
+    (P.WEAK_FLOAT, dt.int32, dt.float32), (P.WEAK_FLOAT, dt.float16, dt.float16),
+    (dt.int8, dt.int16, dt.int16), (dt.int32, dt.int64, dt.int64), (dt.uint8, dt.uint32, dt.uint32),
+    (dt.int8, dt.uint8, dt.int16), (dt.int32, dt.uint64, dt.float32),
+    (dt.float16, dt.float32, dt.float32), (dt.float16, dt.bfloat16, dt.float32),
+    (P.WEAK_FLOAT, dt.bfloat16, dt.bfloat16), (dt.bfloat16, dt.float32, dt.float32),
+])
+def test_promotion_table_samples(t0, t1, expected):
+    assert P.lookup(t0, t1) == expected
+    assert P.lookup(t1, t0) == expected
+
+
+def test_promotion_keys_and_common_types():
+    assert P.type_key(True) == dt.bool_
+    assert P.type_key(3) is P.WEAK_INT and P.type_key(2.5) is P.WEAK_FLOAT
+    assert P.type_key(np.int32(5)) == dt.int32
+    assert P.find_common_type(np.array([True, False]), 1000) == dt.int32
+    assert P.find_common_type(np.array([1, 2], np.int8), 100) == dt.int8
+    assert P.find_common_type(np.array([1, 2], np.int8), 3.14) == dt.float32
+    with pytest.raises(TypeError):
+        P.lookup(dt.float32, np.dtype(np.float64))  # float64 is rejected, not narrowed
+    assert P.lookup(dt.float8_e4m3fn, dt.int32) == dt.float8_e4m3fn
+
+
+# ---------------------------------------------------------------------------
+# tracer naming contract
+# ---------------------------------------------------------------------------
+def test_trace_names_inputs_outputs_and_aliases():
+    def kern(a, b):
+        a[0] = b[0]          # mutates a: a.must_alias_input, result named "a"
+        return a * 2, b + 1  # other results: output{i}
+
+    x = np.zeros((4, 8), np.float32)
+    g = NKIPyKernel.trace(kern).specialize(x, x.copy())
+    pnames = [p.name for p in g.parameters]
+    assert pnames == ["a.must_alias_input", "b"]
+    rnames = [r.name for r in g.results]
+    assert "a" in rnames and "output0" in rnames and "output1" in rnames
+
+
+# ---------------------------------------------------------------------------
+# strided views
+# ---------------------------------------------------------------------------
+def test_view_of_split_repeat_transpose():
+    B, S = 2, 5
+
+    def f(qkv):
+        q, k, v = np.split(qkv, [64, 80], axis=-1)
+        vv = np.repeat(v.reshape(B, S, 2, 8), 4, axis=2).transpose(0, 2, 1, 3)
+        kk = np.repeat(k.reshape(B, S, 2, 8), 4, axis=2).transpose(0, 2, 3, 1)
+        return vv * 1.0, kk * 1.0
+
+    x = np.arange(B * S * 96, dtype=np.float32).reshape(B, S, 96)
+    g = NKIPyKernel.trace(f).specialize(x)
+    q, k, v = np.split(x, [64, 80], axis=-1)
+    refs = (np.repeat(v.reshape(B, S, 2, 8), 4, axis=2).transpose(0, 2, 1, 3),
+            np.repeat(k.reshape(B, S, 2, 8), 4, axis=2).transpose(0, 2, 3, 1))
+    for r, ref in zip(g.results, refs):
+        op = r.node.inputs[0] if r.node.inputs[0].ndim == 4 else r.node.inputs[1]
+        vw = resolve(op)
+        assert vw.base.shape == x.shape
+        np.testing.assert_array_equal(vw.materialize_check(x), ref)
+        assert vw.grouped(1) == (2, 8, 4)  # 2 KV heads, stride 8, each repeated 4x
+
+
+def test_view_reshape_merge_and_split():
+    def f(x):
+        return x.reshape(12, 10) * 2.0, x[:, 1:5, :].reshape(2, 4, 2, 5) * 2.0
+
+    x = np.arange(120, dtype=np.float32).reshape(2, 6, 10)
+    g = NKIPyKernel.trace(f).specialize(x)
+    refs = (x.reshape(12, 10), x[:, 1:5, :].reshape(2, 4, 2, 5))
+    for r, ref in zip(g.results, refs):
+        op = next(v for v in r.node.inputs if v.shape == ref.shape and v.size > 1)
+        vw = resolve(op)
+        assert vw.base.is_parameter
+        np.testing.assert_array_equal(vw.materialize_check(x), ref)
+
+
+# ---------------------------------------------------------------------------
+# pattern lowering at the workload shapes
+# ---------------------------------------------------------------------------
+def _bf16(shape):
+    return np.zeros(shape, dt.bfloat16)
+
+
+def _fp8(shape):
+    return np.zeros(shape, np.uint8).view(dt.float8_e4m3fn)
+
+
+def _kinds(fn, *args, **kw):
+    return lower(NKIPyKernel.trace(fn).specialize(*args, **kw)).kernel_kinds
+
+
+def test_lowering_softmax_and_rmsnorm():
+    from nkipy_amd.kernels import residual_rmsnorm_kernel, rmsnorm_kernel, softmax_kernel
+
+    assert _kinds(softmax_kernel, np.zeros((2048, 4096), np.float32)) == ["softmax"]
+    assert _kinds(residual_rmsnorm_kernel, _bf16((8192, 4096)), _bf16((8192, 4096)), _bf16((4096,)),
+                  1e-6) == ["rmsnorm"]
+    assert _kinds(rmsnorm_kernel, _bf16((64, 4096)), _bf16((4096,)), 1e-6) == ["rmsnorm"]
+
+
+def test_lowering_swiglu_and_linear_attention():
+    from nkipy_amd.kernels import chunked_linear_attention_kernel, feedforward_kernel, swiglu_mlp_kernel
+
+    assert _kinds(swiglu_mlp_kernel, _bf16((4096, 4096)), _bf16((4096, 14336)), _bf16((4096, 14336)),
+                  _bf16((14336, 4096))) == ["gemm_swiglu", "gemm"]
+    assert _kinds(feedforward_kernel, _bf16((256, 512)), _bf16((512, 2048)), _bf16((1024, 512))) == \
+        ["gemm_swiglu", "gemm"]
+    q = _bf16((4, 16, 8192, 128))
+    assert _kinds(chunked_linear_attention_kernel, q, q, q) == ["linear_attention"]
+    # fp32 inputs are not the kernel's dtype: generic lowering, no fused step
+    f = np.zeros((1, 2, 128, 16), np.float32)
+    kinds = _kinds(chunked_linear_attention_kernel, f, f, f, 32)
+    assert "linear_attention" not in kinds and kinds
+
+
+def test_lowering_decoder_layer_fp8():
+    from nkipy_amd.kernels import llama_decoder_layer_fp8
+
+    B, S, Hq, Hkv, D, F = 8, 2048, 32, 8, 128, 14336
+    hid = Hq * D
+    one = lambda n: np.ones(n, np.float32)
+    args = [_bf16((B, S, hid)), _bf16((hid,)), _fp8(((Hq + 2 * Hkv) * D, hid)), one((Hq + 2 * Hkv) * D),
+            _fp8((hid, hid)), one(hid), _bf16((hid,)), _fp8((F, hid)), one(F), _fp8((F, hid)), one(F),
+            _fp8((hid, F)), one(hid)]
+    assert _kinds(llama_decoder_layer_fp8, *args) == [
+        "rmsnorm", "gemm", "rope", "rope", "attention", "gemm", "rmsnorm", "gemm_swiglu", "gemm"]
+
+
+def test_lowering_attention_variants_and_non_matches():
+    from nkipy_amd.kernels import causal_gqa_attention_kernel
+    from nkipy_amd.kernels.softmax import softmax_kernel
+
+    q = _bf16((1, 256, 8, 128))
+    assert _kinds(causal_gqa_attention_kernel, q, _bf16((1, 256, 1, 128)), _bf16((1, 256, 1, 128))) == \
+        ["attention"]   # one KV head shared by all (stride 0)
+    assert _kinds(causal_gqa_attention_kernel, q, q, q) == ["attention"]  # no GQA
+
+    def anti_causal(xq, xk, xv):  # mask on the wrong side: not the causal kernel
+        S, D = xq.shape[1], xq.shape[3]
+        q = xq.transpose(0, 2, 1, 3).astype(np.float32)
+        k = xk.transpose(0, 2, 3, 1).astype(np.float32)
+        v = xv.transpose(0, 2, 1, 3).astype(np.float32)
+        s = np.matmul(q, k) / np.float32(np.sqrt(D)) + np.tril(np.full((S, S), -1e5, np.float32), k=-1)
+        return np.matmul(softmax_kernel(s), v).astype(xq.dtype)
+
+    kinds = _kinds(anti_causal, q, q, q)
+    assert "attention" not in kinds and "dot" in kinds
+
+    def head_dim_64(xq, xk, xv):
+        return causal_gqa_attention_kernel(xq, xk, xv)
+
+    q64 = _bf16((1, 256, 2, 64))
+    assert "attention" not in _kinds(head_dim_64, q64, q64, q64)
+
+
+# ---------------------------------------------------------------------------
+# launcher operand checks (host side, nothing launched)
+# ---------------------------------------------------------------------------
+def test_launchers_reject_operands_the_kernels_cannot_take():
+    A = 1 << 20
+    with pytest.raises(LA.LaunchError):
+        LA.gemm(A, A, A, 64, 64, 12, layout="nt", b_dtype=dt.bfloat16, c_dtype=dt.bfloat16)  # K % 8
+    with pytest.raises(LA.LaunchError):
+        LA.gemm(A, A, A, 64, 64, 24, layout="nt", b_dtype=dt.float8_e4m3fn, c_dtype=dt.bfloat16,
+                scale_ptr=A)  # fp8 NT needs K % 16
+    with pytest.raises(LA.LaunchError):
+        LA.gemm(A + 4, A, A, 64, 64, 64, layout="nn", b_dtype=dt.bfloat16, c_dtype=dt.bfloat16)  # align
+    st = {n: (256 * 128, 128, 128) for n in "qkvo"}
+    with pytest.raises(LA.LaunchError):
+        LA.attention(A, A, A, A, 1, 200, 1, 1, 128, 0.1, st)  # S % 128
+    with pytest.raises(LA.LaunchError):
+        LA.attention(A, A, A, A, 1, 256, 1, 1, 64, 0.1, st)  # head dim
+    with pytest.raises(LA.LaunchError):
+        LA.linear_attention(A, A, A, A, 4, 100)  # T % 64
+    with pytest.raises(LA.LaunchError):
+        LA.rope(A, A, A, A, 1, 8, 2, 128, (1024, 256, 130), (1024, 256, 128), 64, 64)  # stride alignment
+    ok = LA.gemm(A, A, A, 300, 520, 136, layout="nn", b_dtype=dt.bfloat16, c_dtype=dt.bfloat16)
+    assert ok.grid[0] == 2 * 3 and ok.flops == 2 * 300 * 520 * 136
