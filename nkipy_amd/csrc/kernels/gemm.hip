@@ -361,25 +361,22 @@ __device__ __forceinline__ void mma_tile(f32x16 (&acc)[4][4], const uint8_t *As,
 }
 
 // Instruction order of one K tile (one scheduling region: the DMA issue of
-// the next tile plus the MFMAs of this one): the fragments of step 0, then
-// per step the fragments of step + 1 ahead of the step's 16 MFMAs, and one
-// DMA after every 4 MFMAs.  Each fragment read has a whole step (16 MFMAs,
-// ~512 cycles) to land before it is used.
+// the next tile plus the MFMAs of this one): half of the next tile's DMAs
+// first and the other half after the first step's 8 MFMAs, so that each has
+// most of the tile's MFMA time to land before the closing vmcnt(0) wait
+// (measured best among up-front, spread and split issue); fragments of step
+// 0 first, and per step the fragments of step + 1 ahead of the step's 16
+// MFMAs, so each read has a whole step (~512 cycles) to land.
 template <int NDS, int NVMEM>
 __device__ __forceinline__ void schedule_ktile() {
-  __builtin_amdgcn_sched_group_barrier(0x100, NDS, 0);  // DS reads, step 0
-  int vm = 0;
+  __builtin_amdgcn_sched_group_barrier(0x020, NVMEM / 2, 0);  // VMEM reads (DMA)
+  __builtin_amdgcn_sched_group_barrier(0x100, NDS, 0);        // DS reads, step 0
 #pragma unroll
   for (int kk = 0; kk < BK / 16; ++kk) {
     if (kk + 1 < BK / 16) __builtin_amdgcn_sched_group_barrier(0x100, NDS, 0);  // DS reads, step kk + 1
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // 4 MFMA
-      if (vm < NVMEM) {
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 VMEM read (DMA)
-        ++vm;
-      }
-    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);                           // 8 MFMA
+    if (kk == 0) __builtin_amdgcn_sched_group_barrier(0x020, NVMEM - NVMEM / 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);                           // 8 MFMA
   }
 }
 
