@@ -76,6 +76,10 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds_blo
 
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
+template <bool B> struct Flag {
+  static constexpr bool value = B;
+};
+
 struct Tile {
   uint8_t *K;
   uint8_t *V;
@@ -147,64 +151,89 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
     for (int j = 0; j < 4; ++j) dma16(rv, t.V + (j * 4 + wave) * 1024, vbase[j] + vst);
   };
 
-  // one 64-key block against this wave's 32 queries
-  auto block = [&](Tile t, int kb) {
+  // Per-lane LDS byte offsets, fixed for the whole loop (the swizzles only
+  // see lane bits), so every fragment read is lane offset + immediate.
+  // K fragment (row kt*32 + l32, chunk 2 kk + lhi): kt*8192 + koff[kk].
+  int koff[AD / 16];
+#pragma unroll
+  for (int kk = 0; kk < AD / 16; ++kk) koff[kk] = l32 * 256 + (((kk * 2 + lhi) ^ kswz(l32)) << 4);
+  // V^T transpose read (group g = lane/16, i = lane%16): source row
+  // 16 j + 8 si + 4 (g/2) + i/4, columns dt*32 + 16 (g%2) + 4 (i%4):
+  // (16 j + 8 si) * 256 + voff[dt].
+  int voff[4];
+  {
+    const int grp = lane >> 4, gi = lane & 15;
+    const int c0 = (grp & 1) * 2 + ((gi & 3) >> 1), vsh = (gi >> 2) & 3;
+    const int lb = (4 * (grp >> 1) + (gi >> 2)) * 256 + (c0 << 4) + (gi & 1) * 8;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) voff[dt] = lb + ((dt ^ vsh) << 6);
+  }
+
+  // One 64-key block against this wave's 32 queries.  DIAG blocks are the
+  // last two of a causal row of blocks: they may cross or lie above the
+  // diagonal of this wave's queries; every other block lies below it for
+  // all four waves and is processed without mask code.
+  auto block = [&](Tile t, int kb, auto diag_flag) __attribute__((always_inline)) {
+    constexpr bool DIAG = decltype(diag_flag)::value;
     const int key0 = kb * AK;
-    if (a.causal && key0 > wq0 + 31) return;  // entirely above the diagonal for this wave
+    if (DIAG && key0 > wq0 + 31) return;  // entirely above the diagonal for this wave
     f32x16 s[2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[kt][r] = 0.f;
-      const int row = kt * 32 + l32;
 #pragma unroll
       for (int kk = 0; kk < AD / 16; ++kk) {
-        const bf16x8_t kf =
-            *reinterpret_cast<const bf16x8_t *>(t.K + row * 256 + (((kk * 2 + lhi) ^ kswz(row)) << 4));
+        const bf16x8_t kf = *reinterpret_cast<const bf16x8_t *>(t.K + kt * 8192 + koff[kk]);
         s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[kt], 0, 0, 0);
       }
     }
-    // scale (log2 units), causal mask on diagonal blocks, block max
+    // causal mask on diagonal blocks; block max of the raw scores (the scale
+    // is positive, so it commutes with the max)
     float bmax = -INFINITY;
-    const bool diag = a.causal && key0 + AK - 1 > wq0;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float x = s[kt][r] * sl2;
-        if (diag) {
+        if constexpr (DIAG) {
           const int key = key0 + kt * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
-          if (key > qrow) x = -INFINITY;
+          if (key > qrow) s[kt][r] = -INFINITY;
         }
-        s[kt][r] = x;
-        bmax = fmaxf(bmax, x);
+        bmax = fmaxf(bmax, s[kt][r]);
       }
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-    const float m_new = fmaxf(m_run, bmax);  // finite: every row sees key 0 in its first block
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first block
+    // Running max m_run in log2 units, kept stale: it moves only when some
+    // row's block max exceeds it by more than 8, so every P stays <= 2^8 and
+    // the O / l rescale runs on a few blocks per row instead of all of them.
+    // The first block (key 0, seen by every row) always moves it from -inf.
+    const float m_blk = bmax * sl2;
+    if (__any(m_blk > m_run + 8.0f)) {
+      const float m_new = fmaxf(m_run, m_blk);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first block
+      l_run *= alpha;
+#pragma unroll
+      for (int t2 = 0; t2 < 4; ++t2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_o[t2][r] *= alpha;
+      m_run = m_new;
+    }
     float bsum = 0.f;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(s[kt][r] - m_new);
+        const float p = __builtin_amdgcn_exp2f(fmaf(s[kt][r], sl2, -m_run));
         s[kt][r] = p;
         bsum += p;
       }
     bsum += __shfl_xor(bsum, 32, 64);
-    l_run = l_run * alpha + bsum;
-    m_run = m_new;
-#pragma unroll
-    for (int t2 = 0; t2 < 4; ++t2)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc_o[t2][r] *= alpha;
+    l_run += bsum;
 
     // O^T += V^T P^T.  Step j covers 16 keys; this lane's P values (S^T rows)
     // are keys 16 j + 4 lhi + {0..3} and 16 j + 8 + 4 lhi + {0..3}, which is
-    // the order of the two transpose reads below.  Transpose read (group
-    // g = lane / 16, i = lane % 16): source row key0' + i / 4, columns
-    // n + 4 (i % 4); output lane i gets column n + i for 4 consecutive keys.
-    const int grp = lane >> 4, gi = lane & 15;
+    // the order of the two transpose reads below (source row 16 j + 8 si +
+    // 4 (g/2) + i/4; output lane i of group g gets column dt*32 + 16 (g%2) + i
+    // for 4 consecutive keys).
 #pragma unroll
     for (int j = 0; j < AK / 16; ++j) {
       const int kt = j >> 1, g0 = (j & 1) * 8;
@@ -213,14 +242,11 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
       for (int e = 0; e < 8; ++e) pf[e] = (__bf16)s[kt][g0 + e];
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const int nl = dt * 32 + (grp & 1) * 16 + 4 * (gi & 3);
         s16x4 v[2];
 #pragma unroll
-        for (int si = 0; si < 2; ++si) {
-          const int key = 16 * j + 8 * si + 4 * (grp >> 1) + (gi >> 2);
-          const uint8_t *p = t.V + key * 256 + (((nl >> 3) ^ vswz(key)) << 4) + (nl & 7) * 2;
-          v[si] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)p);
-        }
+        for (int si = 0; si < 2; ++si)
+          v[si] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4 *)(t.V + (16 * j + 8 * si) * 256 + voff[dt]));
         const bf16x8_t vf = __builtin_shufflevector(__builtin_bit_cast(bf16x4_t, v[0]),
                                                     __builtin_bit_cast(bf16x4_t, v[1]), 0, 1, 2, 3, 4, 5, 6, 7);
         acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, acc_o[dt], 0, 0, 0);
@@ -228,22 +254,27 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
     }
   };
 
+  // Blocks go in pairs over the two static tile buffers (nkb is even: S and
+  // the causal extent are multiples of 128 keys).  Only a causal row's final
+  // pair can touch the diagonal.
   const Tile T0{K0, V0}, T1{K1, V1};
+  auto pair = [&](int kb, auto diag_flag) __attribute__((always_inline)) {
+    load_tile(T1, kb + 1);
+    block(T0, kb, diag_flag);
+    wait_vmem();
+    __syncthreads();
+    if (kb + 2 < nkb) load_tile(T0, kb + 2);
+    block(T1, kb + 1, diag_flag);
+    wait_vmem();
+    __syncthreads();
+  };
+  const int nclean = a.causal ? nkb - 2 : nkb;
   load_tile(T0, 0);
   wait_vmem();
   __syncthreads();
   int kb = 0;
-  for (; kb + 2 <= nkb; kb += 2) {
-    if (kb + 1 < nkb) load_tile(T1, kb + 1);
-    block(T0, kb);
-    wait_vmem();
-    __syncthreads();
-    if (kb + 2 < nkb) load_tile(T0, kb + 2);
-    block(T1, kb + 1);
-    wait_vmem();
-    __syncthreads();
-  }
-  if (kb < nkb) block(T0, kb);
+  for (; kb < nclean; kb += 2) pair(kb, Flag<false>{});
+  if (kb < nkb) pair(kb, Flag<true>{});
 
   // normalise and store: lane holds d = t*32 + (r>>2)*8 + lhi*4 + (r&3) of its query
   const float inv_l = 1.0f / l_run;

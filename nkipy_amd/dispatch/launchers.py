@@ -367,6 +367,8 @@ def attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, B: int, S: int, Hq
     for p in (q_ptr, k_ptr, v_ptr, o_ptr):
         if p % 16:
             raise LaunchError("attention operands must be 16-byte aligned")
+    if not scale > 0:
+        raise LaunchError("attention kernel needs a positive score scale")
     if S * max(strides["k"][1], strides["v"][1], 128) * 2 >= 2**31:
         raise LaunchError("attention K / V rows of one sequence must span less than 2 GiB")
     vals = [q_ptr, k_ptr, v_ptr, o_ptr]
