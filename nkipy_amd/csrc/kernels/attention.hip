@@ -19,15 +19,19 @@
 //
 // Data movement: Q fragments stay in registers.  K and V tiles (64 keys x
 // 128 d, d contiguous, exactly as they lie in memory) move global -> LDS by
-// DMA (buffer_load ... lds), double-buffered, so the next tile streams in
-// while the current one feeds the MFMAs.  K fragments are plain 16-byte LDS
-// reads; V^T fragments come from ds_read_b64_tr_b16, which transposes 4 x 4
-// bf16 blocks across lanes on the way out of LDS.  Both tiles are
-// XOR-swizzled so that these reads are bank-conflict free.  Scores and the
-// softmax are fp32; P enters the second MFMA as bf16.  Causal masking is only
-// evaluated on blocks that cross the diagonal of a wave's queries, and
-// blocks entirely above it are skipped.  Query blocks are issued
-// longest-first (causal work grows with position).
+// DMA (buffer_load ... lds), double-buffered.  The block loop is software
+// pipelined: the step for block j runs the scores of block j + 1 on the
+// MFMA pipe while the VALU does block j's softmax, so K runs one tile ahead
+// of V.  K fragments are plain 16-byte LDS reads; V^T fragments come from
+// ds_read_b64_tr_b16, which transposes 4 x 4 bf16 blocks across lanes on the
+// way out of LDS.  Both tiles are XOR-swizzled so that these reads are bank
+// conflict free.  Scores and the softmax are fp32 (running max kept stale
+// up to a factor 2^8, so the O rescale is rare); P enters the second MFMA as
+// bf16.  Causal masking is only evaluated on the final pair of blocks, and
+// blocks entirely above a wave's diagonal are skipped.  Each XCD takes a
+// contiguous range of (KV head, query head, query block) work items so one
+// KV head's tiles are re-read from that XCD's L2; within a KV head the
+// longest query blocks go first (causal work grows with position).
 
 #include "common.h"
 
@@ -80,11 +84,6 @@ template <bool B> struct Flag {
   static constexpr bool value = B;
 };
 
-struct Tile {
-  uint8_t *K;
-  uint8_t *V;
-};
-
 extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(AttnArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t K0[TILE_BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t K1[TILE_BYTES];
@@ -95,13 +94,22 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31, lhi = lane >> 5;
 
-  // block -> (b, h, query block), longest (last) query blocks first
+  // Workgroup -> (b, KV head g, query head h, query block).  Workgroups are
+  // dispatched round-robin over the 8 XCDs, so workgroup i runs on XCD i % 8;
+  // giving each XCD a contiguous range of work items keeps the query heads
+  // and blocks that share one K / V head on one XCD, whose L2 then serves
+  // the K / V re-reads.  Within a KV head, the longest (last) query blocks
+  // go first.
   const int nqb = a.S / AQ;
-  const int bid = blockIdx.x;
-  const int qb = nqb - 1 - (bid % nqb);
-  const int bh = bid / nqb;
-  const int h = bh % a.Hq, b = bh / a.Hq;
-  const int g = h / (a.Hq / a.Hkv);
+  const int rep = a.Hq / a.Hkv;
+  const int per_kv = rep * nqb;
+  const int nwg = a.B * a.Hkv * per_kv;  // the grid size
+  int w = blockIdx.x;
+  if ((nwg & 7) == 0) w = (w & 7) * (nwg >> 3) + (w >> 3);
+  const int bg = w / per_kv, within = w % per_kv;
+  const int qb = nqb - 1 - within / rep;
+  const int g = bg % a.Hkv, b = bg / a.Hkv;
+  const int h = g * rep + within % rep;
   const int q0 = qb * AQ;
 
   const uint16_t *qp = a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh;
@@ -142,13 +150,15 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
     kbase[j] = (uint32_t)(((int64_t)row * a.k_ss + kchunk * 8) * 2);
     vbase[j] = (uint32_t)(((int64_t)row * a.v_ss + vchunk * 8) * 2);
   }
-  auto load_tile = [&](Tile t, int kb) {
+  auto load_k = [&](uint8_t *dst, int kb) {
     const uint32_t kst = (uint32_t)((int64_t)kb * AK * a.k_ss * 2);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(rk, dst + (j * 4 + wave) * 1024, kbase[j] + kst);
+  };
+  auto load_v = [&](uint8_t *dst, int kb) {
     const uint32_t vst = (uint32_t)((int64_t)kb * AK * a.v_ss * 2);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dma16(rk, t.K + (j * 4 + wave) * 1024, kbase[j] + kst);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) dma16(rv, t.V + (j * 4 + wave) * 1024, vbase[j] + vst);
+    for (int j = 0; j < 4; ++j) dma16(rv, dst + (j * 4 + wave) * 1024, vbase[j] + vst);
   };
 
   // Per-lane LDS byte offsets, fixed for the whole loop (the swizzles only
@@ -169,66 +179,74 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
     for (int dt = 0; dt < 4; ++dt) voff[dt] = lb + ((dt ^ vsh) << 6);
   }
 
-  // One 64-key block against this wave's 32 queries.  DIAG blocks are the
-  // last two of a causal row of blocks: they may cross or lie above the
-  // diagonal of this wave's queries; every other block lies below it for
-  // all four waves and is processed without mask code.
-  auto block = [&](Tile t, int kb, auto diag_flag) __attribute__((always_inline)) {
-    constexpr bool DIAG = decltype(diag_flag)::value;
-    const int key0 = kb * AK;
-    if (DIAG && key0 > wq0 + 31) return;  // entirely above the diagonal for this wave
-    f32x16 s[2];
+  // S^T = K Q^T for one 64-key block (keys kt*32 + row, this lane's query)
+  auto qk = [&](const uint8_t *Kt, f32x16 (&s)[2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[kt][r] = 0.f;
 #pragma unroll
       for (int kk = 0; kk < AD / 16; ++kk) {
-        const bf16x8_t kf = *reinterpret_cast<const bf16x8_t *>(t.K + kt * 8192 + koff[kk]);
+        const bf16x8_t kf = *reinterpret_cast<const bf16x8_t *>(Kt + kt * 8192 + koff[kk]);
         s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[kt], 0, 0, 0);
       }
     }
-    // causal mask on diagonal blocks; block max of the raw scores (the scale
-    // is positive, so it commutes with the max)
-    float bmax = -INFINITY;
+  };
+
+  // Online softmax of one block's scores and O^T += V^T P^T.  DIAG blocks
+  // are the final pair of a row of blocks: under a causal mask they may
+  // cross the diagonal of this wave's queries; every other block lies below
+  // it for all four waves and runs without mask code.
+  auto finish = [&](f32x16 (&s)[2], const uint8_t *Vt, int key0, auto diag_flag) __attribute__((always_inline)) {
+    constexpr bool DIAG = decltype(diag_flag)::value;
+    // block max of the raw scores (the scale is positive, so it commutes
+    // with the max), as a tree
+    float mx[8];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (DIAG) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        if constexpr (DIAG) {
+        for (int e = 0; e < 4; ++e) {
+          const int kt = i >> 2, r = (i & 3) * 4 + e;
           const int key = key0 + kt * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
-          if (key > qrow) s[kt][r] = -INFINITY;
+          if (a.causal && key > qrow) s[kt][r] = -INFINITY;
         }
-        bmax = fmaxf(bmax, s[kt][r]);
       }
+      const int kt = i >> 2, r0 = (i & 3) * 4;
+      mx[i] = fmaxf(fmaxf(s[kt][r0], s[kt][r0 + 1]), fmaxf(s[kt][r0 + 2], s[kt][r0 + 3]));
+    }
+    float bmax = fmaxf(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])),
+                       fmaxf(fmaxf(mx[4], mx[5]), fmaxf(mx[6], mx[7])));
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
     // Running max m_run in log2 units, kept stale: it moves only when some
     // row's block max exceeds it by more than 8, so every P stays <= 2^8 and
-    // the O / l rescale runs on a few blocks per row instead of all of them.
-    // The first block (key 0, seen by every row) always moves it from -inf.
+    // the O rescale runs on a few blocks per row instead of all of them.  The
+    // first block (key 0, seen by every row) always moves it from -inf.
     const float m_blk = bmax * sl2;
-    if (__any(m_blk > m_run + 8.0f)) {
-      const float m_new = fmaxf(m_run, m_blk);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first block
-      l_run *= alpha;
+    const bool moved = __any(m_blk > m_run + 8.0f);
+    const float m_new = moved ? fmaxf(m_run, m_blk) : m_run;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first block, 1 if unmoved
+    m_run = m_new;
+    float ps[4] = {0.f, 0.f, 0.f, 0.f};
+    bf16x8_t pf[AK / 16];
+#pragma unroll
+    for (int j = 0; j < AK / 16; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int kt = j >> 1, r = (j & 1) * 8 + e;
+        const float p = __builtin_amdgcn_exp2f(fmaf(s[kt][r], sl2, -m_new));
+        ps[j] += p;
+        pf[j][e] = (__bf16)p;
+      }
+    float bsum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+    bsum += __shfl_xor(bsum, 32, 64);
+    l_run = fmaf(l_run, alpha, bsum);
+    if (moved) {
 #pragma unroll
       for (int t2 = 0; t2 < 4; ++t2)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc_o[t2][r] *= alpha;
-      m_run = m_new;
     }
-    float bsum = 0.f;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(s[kt][r], sl2, -m_run));
-        s[kt][r] = p;
-        bsum += p;
-      }
-    bsum += __shfl_xor(bsum, 32, 64);
-    l_run += bsum;
-
     // O^T += V^T P^T.  Step j covers 16 keys; this lane's P values (S^T rows)
     // are keys 16 j + 4 lhi + {0..3} and 16 j + 8 + 4 lhi + {0..3}, which is
     // the order of the two transpose reads below (source row 16 j + 8 si +
@@ -236,45 +254,56 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
     // for 4 consecutive keys).
 #pragma unroll
     for (int j = 0; j < AK / 16; ++j) {
-      const int kt = j >> 1, g0 = (j & 1) * 8;
-      bf16x8_t pf;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pf[e] = (__bf16)s[kt][g0 + e];
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         s16x4 v[2];
 #pragma unroll
         for (int si = 0; si < 2; ++si)
           v[si] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_s16x4 *)(t.V + (16 * j + 8 * si) * 256 + voff[dt]));
+              (lds_s16x4 *)(Vt + (16 * j + 8 * si) * 256 + voff[dt]));
         const bf16x8_t vf = __builtin_shufflevector(__builtin_bit_cast(bf16x4_t, v[0]),
                                                     __builtin_bit_cast(bf16x4_t, v[1]), 0, 1, 2, 3, 4, 5, 6, 7);
-        acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, acc_o[dt], 0, 0, 0);
+        acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[j], acc_o[dt], 0, 0, 0);
       }
     }
   };
 
-  // Blocks go in pairs over the two static tile buffers (nkb is even: S and
-  // the causal extent are multiples of 128 keys).  Only a causal row's final
-  // pair can touch the diagonal.
-  const Tile T0{K0, V0}, T1{K1, V1};
-  auto pair = [&](int kb, auto diag_flag) __attribute__((always_inline)) {
-    load_tile(T1, kb + 1);
-    block(T0, kb, diag_flag);
-    wait_vmem();
-    __syncthreads();
-    if (kb + 2 < nkb) load_tile(T0, kb + 2);
-    block(T1, kb + 1, diag_flag);
+  // Software pipeline over blocks: block j's K tile sits in K[j & 1] and its
+  // V tile in V[j & 1]; the step for block j computes the scores of block
+  // j + 1 while it runs block j's softmax and PV, and streams in K_{j+2} and
+  // V_{j+1} meanwhile (K runs one tile ahead of V).  The buffers a step
+  // overwrites were last read before the previous step's barrier.
+  f32x16 sa[2], sb[2];
+  auto step = [&](int j, f32x16 (&cur)[2], f32x16 (&nxt)[2], uint8_t *kdst, uint8_t *vdst, const uint8_t *knext,
+                  const uint8_t *vcur) __attribute__((always_inline)) {
+    load_k(kdst, j + 2);
+    load_v(vdst, j + 1);
+    qk(knext, nxt);
+    finish(cur, vcur, j * AK, Flag<false>{});
     wait_vmem();
     __syncthreads();
   };
-  const int nclean = a.causal ? nkb - 2 : nkb;
-  load_tile(T0, 0);
+  load_k(K0, 0);
+  load_v(V0, 0);
+  load_k(K1, 1);  // nkb >= 2: S and the causal extent are multiples of 128 keys
   wait_vmem();
   __syncthreads();
+  qk(K0, sa);
+  __syncthreads();
+  // Blocks 0 .. nkb-3 lie below the diagonal of every wave; nkb is even.
   int kb = 0;
-  for (; kb < nclean; kb += 2) pair(kb, Flag<false>{});
-  if (kb < nkb) pair(kb, Flag<true>{});
+  for (; kb < nkb - 2; kb += 2) {
+    step(kb, sa, sb, K0, V1, K1, V0);
+    step(kb + 1, sb, sa, K1, V0, K0, V1);
+  }
+  // final pair: blocks nkb-2 (scores in sa, V in V0) and nkb-1 (K in K1)
+  load_v(V1, nkb - 1);
+  const bool need_last = !a.causal || (nkb - 1) * AK <= wq0 + 31;
+  if (need_last) qk(K1, sb);
+  finish(sa, V0, (nkb - 2) * AK, Flag<true>{});
+  wait_vmem();
+  __syncthreads();
+  if (need_last) finish(sb, V1, (nkb - 1) * AK, Flag<true>{});
 
   // normalise and store: lane holds d = t*32 + (r>>2)*8 + lhi*4 + (r&3) of its query
   const float inv_l = 1.0f / l_run;
