@@ -292,6 +292,25 @@ __device__ __forceinline__ void store_nn(const StageNN &s, uint8_t *Bs) {
 }
 
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+// vmcnt(N): all but the N most recent vector memory loads have completed
+// (loads retire in issue order)
+template <int N>
+__device__ __forceinline__ void wait_vmem_but() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+// Workgroup barrier without __syncthreads()'s release fence, which would
+// wait for every outstanding load (vmcnt(0)), including the DMA of the tile
+// after next.  Ordering is explicit instead: each wave waits (vmcnt) for the
+// DMAs the next tile needs before the barrier, and every LDS read of a stage
+// has been consumed by an MFMA before the barrier that precedes the stage's
+// refill.  The empty asm statements keep the compiler from moving memory
+// accesses across the barrier.
+__device__ __forceinline__ void barrier_no_fence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 // ---------------------------------------------------------------------------
 // MFMA over one staged K tile (64 = 4 steps of 16), operand fragments of
@@ -390,10 +409,15 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
   constexpr int BMODE = (NT && FP8) ? B_T8 : (!NT && !FP8) ? B_NN16 : B_T16;
   constexpr bool REG_B = !NT && FP8;
   constexpr int BROW = BMODE == B_T8 ? 64 : 128;  // bytes per B row in LDS
+  // LDS ring of K-tile stages: three when a stage is 48 KiB (fp8 B^T), else
+  // two (64 KiB stages)
+  constexpr int NS = BMODE == B_T8 ? 3 : 2;
   __shared__ __attribute__((aligned(1024))) uint8_t A0[BM * 128];
   __shared__ __attribute__((aligned(1024))) uint8_t A1[BM * 128];
+  __shared__ __attribute__((aligned(1024))) uint8_t A2[NS > 2 ? BM * 128 : 16];
   __shared__ __attribute__((aligned(1024))) uint8_t B0[BN * BROW];
   __shared__ __attribute__((aligned(1024))) uint8_t B1[BN * BROW];
+  __shared__ __attribute__((aligned(1024))) uint8_t B2[NS > 2 ? BN * BROW : 16];
 
   // XCD-aware tile order
   const int ntiles = a.tiles_m * a.tiles_n;
@@ -455,40 +479,68 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
   };
 
   const int ktiles = (int)((a.K + BK - 1) / BK);
-  issue(A0, B0, 0);
-  if (REG_B) {
-    wait_vmem();
-    store_nn(sn, B0);
-  }
-  wait_vmem();
-  __syncthreads();
-
   // fragment reads per step and DMA moves per K tile of this variant
   constexpr int NDS = BMODE == B_NN16 ? 12 : 8;
   constexpr int NVM = REG_B ? 16 : (BMODE == B_T8 ? 12 : 16);
-  int t = 0;
-  for (; t + 2 <= ktiles; t += 2) {
-    issue(A1, B1, (int64_t)(t + 1) * BK);
-    mma_tile<BMODE>(acc, A0, B0, wm, brow, lane);
-    schedule_ktile<NDS, NVM>();
-    if (REG_B) {
-      wait_vmem();
-      store_nn(sn, B1);
+
+  if constexpr (NS == 3) {
+    // Three-stage ring: the DMA of tile t + 2 is issued while tile t feeds
+    // the MFMAs, and the closing wait only needs tile t + 1 (issued a whole
+    // tile earlier), so the DMA latency tail stays off the critical path.
+    // A step past the last tile reads zeros (K offset out of range) into a
+    // stage that is never consumed.
+    issue(A0, B0, 0);
+    issue(A1, B1, BK);
+    wait_vmem_but<NVM>();
+    barrier_no_fence();
+    auto step = [&](uint8_t *Ac, uint8_t *Bc, uint8_t *An, uint8_t *Bn, int tt) __attribute__((always_inline)) {
+      issue(An, Bn, (int64_t)(tt + 2) * BK);
+      mma_tile<BMODE>(acc, Ac, Bc, wm, brow, lane);
+      schedule_ktile<NDS, NVM>();
+      wait_vmem_but<NVM>();
+      barrier_no_fence();
+    };
+    int t = 0;
+    for (; t + 3 <= ktiles; t += 3) {
+      step(A0, B0, A2, B2, t);
+      step(A1, B1, A0, B0, t + 1);
+      step(A2, B2, A1, B1, t + 2);
     }
+    if (t < ktiles) step(A0, B0, A2, B2, t);
+    if (t + 1 < ktiles) mma_tile<BMODE>(acc, A1, B1, wm, brow, lane);
     wait_vmem();
-    __syncthreads();
-    // past the last tile this reads zeros (K offset out of range) into the idle stage
-    issue(A0, B0, (int64_t)(t + 2) * BK);
-    mma_tile<BMODE>(acc, A1, B1, wm, brow, lane);
-    schedule_ktile<NDS, NVM>();
-    if (REG_B && t + 2 < ktiles) {
+  } else {
+    issue(A0, B0, 0);
+    if (REG_B) {
       wait_vmem();
       store_nn(sn, B0);
     }
     wait_vmem();
     __syncthreads();
+    int t = 0;
+    for (; t + 2 <= ktiles; t += 2) {
+      issue(A1, B1, (int64_t)(t + 1) * BK);
+      mma_tile<BMODE>(acc, A0, B0, wm, brow, lane);
+      schedule_ktile<NDS, NVM>();
+      if (REG_B) {
+        wait_vmem();
+        store_nn(sn, B1);
+      }
+      wait_vmem();
+      __syncthreads();
+      // past the last tile this reads zeros (K offset out of range) into the idle stage
+      issue(A0, B0, (int64_t)(t + 2) * BK);
+      mma_tile<BMODE>(acc, A1, B1, wm, brow, lane);
+      schedule_ktile<NDS, NVM>();
+      if (REG_B && t + 2 < ktiles) {
+        wait_vmem();
+        store_nn(sn, B0);
+      }
+      wait_vmem();
+      __syncthreads();
+    }
+    if (t < ktiles) mma_tile<BMODE>(acc, A0, B0, wm, brow, lane);
   }
-  if (t < ktiles) mma_tile<BMODE>(acc, A0, B0, wm, brow, lane);
 
   // epilogue.  The MFMAs computed C^T tiles (B fragment as the A operand),
   // so a lane holds row m = m0 + wm*128 + i*32 + l32 of C and, per tile,

@@ -103,6 +103,26 @@ def test_gemm_fp8_nt_scales_bias_residual(gpu):
     _close(dt.to_float32(cd.numpy()), ref)
 
 
+@pytest.mark.parametrize("Kk", [16, 64, 128, 192, 208, 576])
+def test_gemm_fp8_nt_k_tiles(gpu, Kk):
+    """fp8 NT weights stream through a three-stage LDS ring; K of 1..9 tiles
+    of 64 covers every ring phase at the loop exit (fp32 output, so the check
+    is at fp32-accumulation level)."""
+    M, Nn = 320, 272
+    rng = np.random.default_rng(Kk)
+    x = _bf16(rng, (M, Kk))
+    w = (rng.standard_normal((Nn, Kk)) * 0.02).astype(np.float32)
+    codes, scale = N.quantize_per_channel_e4m3fn(w, axis=1)
+    ref = x.astype(np.float64) @ N.dequantize_e4m3fn(codes, scale, axis=1).T.astype(np.float64)
+    xd = DeviceTensor.from_numpy(dt.to_bf16(x))
+    wd = DeviceTensor.from_numpy(codes.view(dt.float8_e4m3fn))
+    sd = DeviceTensor.from_numpy(scale.astype(np.float32))
+    cd = DeviceTensor.empty((M, Nn), dt.float32)
+    _run(gpu, LA.gemm(xd.ptr, wd.ptr, cd.ptr, M, Nn, Kk, layout="nt", b_dtype=dt.float8_e4m3fn,
+                      c_dtype=dt.float32, scale_ptr=sd.ptr))
+    np.testing.assert_allclose(cd.numpy(), ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
+
+
 def test_gemm_fp8_swiglu_nt(gpu):
     M, F, Kk = 256, 256, 512
     rng = np.random.default_rng(12)
