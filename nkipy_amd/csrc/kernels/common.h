@@ -65,6 +65,13 @@ NK_DEVICE uint32_t bf16x2_bits(nk_bf16x2 v) {
   __builtin_memcpy(&u, &v, 4);
   return u;
 }
+// Two floats -> packed bf16 pair (lo in bits 0..15) with the hardware
+// round-to-nearest-even conversion (v_cvt_pk_bf16_f32); NaN inputs give a
+// quiet NaN.
+NK_DEVICE uint32_t pack_bf16x2(float lo, float hi) {
+  const nk_bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return bf16x2_bits(v);
+}
 NK_DEVICE uint4 e4m3x8_to_bf16x8(uint2 q) {
   return make_uint4(bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q.x, 1.0f, false)),
                     bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q.x, 1.0f, true)),

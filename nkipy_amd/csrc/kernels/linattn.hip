@@ -128,7 +128,11 @@ struct Stage {  // one chunk's operands in LDS
   uint8_t *K;   // phi(K) [64 s][128 d] fp16
   uint8_t *V;   // V slice [64 s][32 j] fp16
   uint8_t *St;  // S^T of the state before this chunk [32 j][128 d] fp16
-  float *z;     // z before this chunk [128]
+  uint8_t *z;   // z / 256 before this chunk [128] fp16
+};
+
+template <int N> struct Int {
+  static constexpr int value = N;
 };
 
 struct Raw {  // one chunk's inputs in registers (this thread's share)
@@ -144,7 +148,8 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
   __shared__ __attribute__((aligned(1024))) uint8_t V1[LC * 64];
   __shared__ __attribute__((aligned(1024))) uint8_t ST0[LS * 256];
   __shared__ __attribute__((aligned(1024))) uint8_t ST1[LS * 256];
-  __shared__ float Z0[LD], Z1[LD];
+  __shared__ __attribute__((aligned(16))) uint8_t Z0[LD * 2];
+  __shared__ __attribute__((aligned(16))) uint8_t Z1[LD * 2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -206,71 +211,73 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
   for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
 
   // ---------------- one chunk -----------------------------------------------
-  auto query_side = [&](const Stage &cur, int c, const int wave) {
-    // phi(Q_w) fragments: rows (queries) 16w + l16, d = 32 st + 8 grp + 0..7
+  // Query wave W (queries 16W..16W+15) is specialised per W so the causal
+  // structure (key tiles 0..W) is static: one basic block per chunk, in which
+  // the compiler interleaves the staging of the next chunk with the MFMA
+  // chains.  The normaliser comes out of the same MFMAs as a third output
+  // tile: its A operand row 0 is z_prev / 256 for the S^T Q^T part and 1/256
+  // for the V^T A^T part, so row 0 of that tile is den / 256 (z / 256 keeps
+  // the fp16 copy of z finite up to z = 2^24; the power-of-two scale is
+  // exact).
+  f16x8_t zrow_ones;  // A operand of the normaliser tile in V^T A^T
+#pragma unroll
+  for (int e = 0; e < 8; ++e) zrow_ones[e] = (_Float16)(l16 == 0 ? 0.00390625f : 0.f);
+  auto query_side = [&](const Stage &cur, int c, auto wtag) __attribute__((always_inline)) {
+    constexpr int W = decltype(wtag)::value;
+    // phi(Q_W) fragments: rows (queries) 16W + l16, d = 32 st + 8 grp + 0..7
     f16x8_t qf[4];
 #pragma unroll
     for (int st = 0; st < 4; ++st)
-      qf[st] = *reinterpret_cast<const f16x8_t *>(cur.Q + o256(16 * wave + l16, (32 * st + 8 * grp) * 2));
+      qf[st] = *reinterpret_cast<const f16x8_t *>(cur.Q + o256(16 * W + l16, (32 * st + 8 * grp) * 2));
 
-    // A^T tiles (keys 16 kt + .., queries 16w + ..); lane: column = query l16,
-    // rows = keys 4 grp + r
+    // O^T tiles 0, 1: rows j = 16 jt + 4 grp + r; tile 2 row 0: den / 256
+    // (column = query l16)
+    f32x4 ot[3];
+#pragma unroll
+    for (int jt = 0; jt < 3; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ot[jt][r] = 0.f;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt) {
+        const f16x8_t sf =
+            *reinterpret_cast<const f16x8_t *>(cur.St + o256(16 * jt + l16, (32 * st + 8 * grp) * 2));
+        ot[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sf, qf[st], ot[jt], 0, 0, 0);
+      }
+      f16x8_t zf = *reinterpret_cast<const f16x8_t *>(cur.z + (32 * st + 8 * grp) * 2);
+      if (l16 != 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) zf[e] = (_Float16)0.f;
+      }
+      ot[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(zf, qf[st], ot[2], 0, 0, 0);
+    }
+
+    // A^T tiles (keys 16 kt + .., queries 16W + ..), kt = 0..W; lane: column
+    // = query l16, rows = keys 4 grp + r
     f32x4 at[4];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) at[kt][r] = 0.f;
-      if (kt <= wave) {
+      if (kt <= W) {
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
           const f16x8_t kf =
               *reinterpret_cast<const f16x8_t *>(cur.K + o256(16 * kt + l16, (32 * st + 8 * grp) * 2));
           at[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[st], at[kt], 0, 0, 0);
         }
-        if (kt == wave) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (4 * grp + r > l16) at[kt][r] = 0.f;  // key > query
-        }
       }
     }
-    // normaliser: in-chunk sum over keys (this lane's rows) plus
-    // phi(q) . z_prev over d = 32 grp .. 32 grp + 31, then over the 4 groups
-    float den = 0.f;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) den += at[kt][r];
-    {
-      const int q = 16 * wave + l16;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const f16x8_t pq = *reinterpret_cast<const f16x8_t *>(cur.Q + o256(q, (32 * grp + 8 * u) * 2));
-#pragma unroll
-        for (int e = 0; e < 8; ++e) den = fmaf((float)pq[e], cur.z[32 * grp + 8 * u + e], den);
-      }
-    }
-    den += __shfl_xor(den, 16, 64);
-    den += __shfl_xor(den, 32, 64);
+    for (int r = 0; r < 4; ++r)
+      if (4 * grp + r > l16) at[W][r] = 0.f;  // key > query on the diagonal tile
 
-    // O^T (j tiles jt: rows j = 16 jt + 4 grp + r, column = query l16)
-    f32x4 ot[2];
-#pragma unroll
-    for (int jt = 0; jt < 2; ++jt) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) ot[jt][r] = 0.f;
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const f16x8_t sf =
-            *reinterpret_cast<const f16x8_t *>(cur.St + o256(16 * jt + l16, (32 * st + 8 * grp) * 2));
-        ot[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sf, qf[st], ot[jt], 0, 0, 0);
-      }
-    }
     // + V^T A^T: 32 keys per step p = key tiles (2p, 2p+1); B element e of
     // lane group g is key 16 (2p + e/4) + 4 g + e%4
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      if (2 * p > wave) continue;
+      if (2 * p > W) continue;
       f16x8_t pf;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -285,15 +292,18 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
         const f16x4_t v1 = tr_read(cur.V + o64(16 * (2 * p + 1) + 4 * grp + (l16 >> 2), jb));
         ot[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cat(v0, v1), pf, ot[jt], 0, 0, 0);
       }
+      ot[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(zrow_ones, pf, ot[2], 0, 0, 0);
     }
+    // den: row 0 of tile 2 sits in lane l16 (group 0), element 0
+    const float den = 256.0f * __shfl(ot[2][0], l16, 64);
     // normalise and store: o[t][j0 + j], 4 consecutive j per lane
     {
       const float inv = 1.0f / den;
-      const int64_t t = (int64_t)c * LC + 16 * wave + l16;
+      const int64_t t = (int64_t)c * LC + 16 * W + l16;
 #pragma unroll
       for (int jt = 0; jt < 2; ++jt) {
-        const uint32_t w0 = (uint32_t)f32_to_bf16(ot[jt][0] * inv) | ((uint32_t)f32_to_bf16(ot[jt][1] * inv) << 16);
-        const uint32_t w1 = (uint32_t)f32_to_bf16(ot[jt][2] * inv) | ((uint32_t)f32_to_bf16(ot[jt][3] * inv) << 16);
+        const uint32_t w0 = pack_bf16x2(ot[jt][0] * inv, ot[jt][1] * inv);
+        const uint32_t w1 = pack_bf16x2(ot[jt][2] * inv, ot[jt][3] * inv);
         *reinterpret_cast<uint2 *>(a.o + base + t * LDV + j0 + 16 * jt + 4 * grp) = make_uint2(w0, w1);
       }
     }
@@ -312,8 +322,8 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
       S = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, vf, S, 0, 0, 0);
       Z = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ones, Z, 0, 0, 0);
     }
-    // fp16 S^T and z for the next chunk: lane holds column j = l32 and rows
-    // d = 32w + 8 (r/4) + 4 lhi + r%4
+    // fp16 S^T and z / 256 for the next chunk: lane holds column j = l32 and
+    // rows d = 32w + 8 (r/4) + 4 lhi + r%4
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
       const int d = 32 * wave + 8 * g4 + 4 * lhi;
@@ -321,38 +331,48 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
       const uint32_t w1 = (uint32_t)f32_to_f16(S[4 * g4 + 2]) | ((uint32_t)f32_to_f16(S[4 * g4 + 3]) << 16);
       *reinterpret_cast<uint2 *>(nxt.St + o256(l32, d * 2)) = make_uint2(w0, w1);
       if (l32 == 0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) nxt.z[d + r] = Z[4 * g4 + r];
+        const uint32_t z0 = (uint32_t)f32_to_f16(Z[4 * g4 + 0] * 0.00390625f) |
+                            ((uint32_t)f32_to_f16(Z[4 * g4 + 1] * 0.00390625f) << 16);
+        const uint32_t z1 = (uint32_t)f32_to_f16(Z[4 * g4 + 2] * 0.00390625f) |
+                            ((uint32_t)f32_to_f16(Z[4 * g4 + 3] * 0.00390625f) << 16);
+        *(__attribute__((address_space(3))) uint2 *)(nxt.z + d * 2) = make_uint2(z0, z1);
       }
     }
   };
-  auto chunk = [&](const Stage &cur, const Stage &nxt, int c) {
-    if (wave < 4)
-      query_side(cur, c, wave);
-    else
-      state_side(cur, nxt, wave - 4);
+  // one chunk plus the staging of the next one (raw inputs r) into nxt
+  auto chunk = [&](const Stage &cur, const Stage &nxt, int c, const Raw &r) {
+    switch (wave) {
+      case 0: query_side(cur, c, Int<0>{}); break;
+      case 1: query_side(cur, c, Int<1>{}); break;
+      case 2: query_side(cur, c, Int<2>{}); break;
+      case 3: query_side(cur, c, Int<3>{}); break;
+      default: state_side(cur, nxt, wave - 4); break;
+    }
+    stage_in(r, nxt);
   };
 
   const Stage s0{Q0, K0, V0, ST0, Z0}, s1{Q1, K1, V1, ST1, Z1};
   // S_0 = 0, z_0 = 0
   for (int i = tid; i < LS * 256 / 16; i += 512) reinterpret_cast<uint4 *>(ST0)[i] = make_uint4(0, 0, 0, 0);
-  if (tid < LD) Z0[tid] = 0.f;
-  Raw ra, rb;
+  if (tid < LD) reinterpret_cast<uint16_t *>(Z0)[tid] = 0;
+  Raw ra{}, rb{};
   load_raw(ra, 0);
   if (nchunks > 1) load_raw(rb, 1);
   stage_in(ra, s0);
   __syncthreads();
-  // iteration c: fetch chunk c + 2, compute chunk c, stage chunk c + 1
+  // iteration c: fetch chunk c + 2, compute chunk c, stage chunk c + 1.  The
+  // fetches are unconditional (past the end they re-read the last chunk, and
+  // the staging writes it into the idle stage, which nothing reads), so the
+  // loop body is straight-line code and the compiler's vmcnt waits only cover
+  // the registers being staged, not the fetch just issued.
   int c = 0;
   for (; c + 2 <= nchunks; c += 2) {
-    if (c + 2 < nchunks) load_raw(ra, c + 2);
-    chunk(s0, s1, c);
-    stage_in(rb, s1);
+    load_raw(ra, min(c + 2, nchunks - 1));
+    chunk(s0, s1, c, rb);
     __syncthreads();
-    if (c + 3 < nchunks) load_raw(rb, c + 3);
-    chunk(s1, s0, c + 1);
-    if (c + 2 < nchunks) stage_in(ra, s0);
+    load_raw(rb, min(c + 3, nchunks - 1));
+    chunk(s1, s0, c + 1, ra);
     __syncthreads();
   }
-  if (c < nchunks) chunk(s0, s1, c);
+  if (c < nchunks) chunk(s0, s1, c, rb);
 }
