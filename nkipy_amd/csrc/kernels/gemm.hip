@@ -409,15 +409,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
   constexpr int BMODE = (NT && FP8) ? B_T8 : (!NT && !FP8) ? B_NN16 : B_T16;
   constexpr bool REG_B = !NT && FP8;
   constexpr int BROW = BMODE == B_T8 ? 64 : 128;  // bytes per B row in LDS
-  // LDS ring of K-tile stages: three when a stage is 48 KiB (fp8 B^T), else
-  // two (64 KiB stages)
-  constexpr int NS = BMODE == B_T8 ? 3 : 2;
-  __shared__ __attribute__((aligned(1024))) uint8_t A0[BM * 128];
-  __shared__ __attribute__((aligned(1024))) uint8_t A1[BM * 128];
-  __shared__ __attribute__((aligned(1024))) uint8_t A2[NS > 2 ? BM * 128 : 16];
-  __shared__ __attribute__((aligned(1024))) uint8_t B0[BN * BROW];
-  __shared__ __attribute__((aligned(1024))) uint8_t B1[BN * BROW];
-  __shared__ __attribute__((aligned(1024))) uint8_t B2[NS > 2 ? BN * BROW : 16];
 
   // XCD-aware tile order
   const int ntiles = a.tiles_m * a.tiles_n;
@@ -464,8 +455,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
   if (NT && FP8) pb8 = plan_rows_fp8(SWIGLU, n0, a.N, a.ldb, wave, lane);
   if (NT && !FP8) pb16 = plan_rows_bf16(SWIGLU, n0, a.N, a.ldb, wave, lane);
   if (!NT && !FP8) pb16 = plan_nn_bf16(SWIGLU, n0, a.N, a.ldb, wave, lane);
-  auto issue = [&](uint8_t *As, uint8_t *Bs, int64_t k0) {
-    dma_rows_bf16(pa, ra, ra, false, As, k0, a.K, wave);
+  auto issue_a = [&](uint8_t *As, int64_t k0) { dma_rows_bf16(pa, ra, ra, false, As, k0, a.K, wave); };
+  auto issue_b = [&](uint8_t *Bs, int64_t k0) {
     if (NT) {
       if (FP8)
         dma_rows_fp8(pb8, rb0, rb1, SWIGLU, Bs, k0, a.K, wave);
@@ -477,18 +468,31 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
       dma_nn_bf16(pb16, rb0, rb1, SWIGLU, Bs, k0, a.K, a.ldb, wave, lane);
     }
   };
+  auto issue = [&](uint8_t *As, uint8_t *Bs, int64_t k0) {
+    issue_a(As, k0);
+    issue_b(Bs, k0);
+  };
 
   const int ktiles = (int)((a.K + BK - 1) / BK);
   // fragment reads per step and DMA moves per K tile of this variant
   constexpr int NDS = BMODE == B_NN16 ? 12 : 8;
   constexpr int NVM = REG_B ? 16 : (BMODE == B_T8 ? 12 : 16);
 
-  if constexpr (NS == 3) {
-    // Three-stage ring: the DMA of tile t + 2 is issued while tile t feeds
-    // the MFMAs, and the closing wait only needs tile t + 1 (issued a whole
-    // tile earlier), so the DMA latency tail stays off the critical path.
-    // A step past the last tile reads zeros (K offset out of range) into a
-    // stage that is never consumed.
+  // DMA moves of the B tile per K tile
+  constexpr int NVB = BMODE == B_T8 ? 4 : 8;
+
+  if constexpr (BMODE == B_T8) {
+    // fp8 B^T: 48 KiB stages, a three-stage ring (144 KiB).  The DMA of tile
+    // t + 2 is issued while tile t feeds the MFMAs, and the closing wait only
+    // needs tile t + 1 (issued a whole tile earlier), so the DMA latency tail
+    // stays off the critical path.  A step past the last tile reads zeros (K
+    // offset out of range) into a stage that is never consumed.
+    __shared__ __attribute__((aligned(1024))) uint8_t A0[BM * 128];
+    __shared__ __attribute__((aligned(1024))) uint8_t A1[BM * 128];
+    __shared__ __attribute__((aligned(1024))) uint8_t A2[BM * 128];
+    __shared__ __attribute__((aligned(1024))) uint8_t B0[BN * BROW];
+    __shared__ __attribute__((aligned(1024))) uint8_t B1[BN * BROW];
+    __shared__ __attribute__((aligned(1024))) uint8_t B2[BN * BROW];
     issue(A0, B0, 0);
     issue(A1, B1, BK);
     wait_vmem_but<NVM>();
@@ -509,12 +513,58 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
     if (t < ktiles) step(A0, B0, A2, B2, t);
     if (t + 1 < ktiles) mma_tile<BMODE>(acc, A1, B1, wm, brow, lane);
     wait_vmem();
-  } else {
-    issue(A0, B0, 0);
-    if (REG_B) {
-      wait_vmem();
-      store_nn(sn, B0);
+  } else if constexpr (!REG_B) {
+    // bf16 B: 32 KiB A and B tiles.  The weights (B) stream from HBM, so they
+    // get a three-stage ring and the activations (A, L2 resident in the
+    // MLP / projection shapes) two stages: 2 x 32 + 3 x 32 = 160 KiB, all of
+    // the CU's LDS.  Per tile t: A(t + 1) is issued first, then B(t + 2);
+    // the closing vmcnt leaves only B(t + 2) in flight, so A(t + 1) and
+    // B(t + 1) (issued a tile earlier) have landed.  The loop is unrolled
+    // six ways so every stage address is static.
+    __shared__ __attribute__((aligned(1024))) uint8_t A0[BM * 128];
+    __shared__ __attribute__((aligned(1024))) uint8_t A1[BM * 128];
+    __shared__ __attribute__((aligned(1024))) uint8_t B0[BN * BROW];
+    __shared__ __attribute__((aligned(1024))) uint8_t B1[BN * BROW];
+    __shared__ __attribute__((aligned(1024))) uint8_t B2[BN * BROW];
+    issue_a(A0, 0);
+    issue_b(B0, 0);
+    issue_b(B1, BK);
+    wait_vmem_but<NVB>();
+    barrier_no_fence();
+    auto step = [&](uint8_t *Ac, uint8_t *Bc, uint8_t *An, uint8_t *Bn, int tt) __attribute__((always_inline)) {
+      issue_a(An, (int64_t)(tt + 1) * BK);
+      issue_b(Bn, (int64_t)(tt + 2) * BK);
+      mma_tile<BMODE>(acc, Ac, Bc, wm, brow, lane);
+      schedule_ktile<NDS, NVM>();
+      wait_vmem_but<NVB>();
+      barrier_no_fence();
+    };
+    // tile t: A in A[t % 2], B in B[t % 3]; step writes A[(t+1) % 2], B[(t+2) % 3]
+    int t = 0;
+    for (; t + 6 <= ktiles; t += 6) {
+      step(A0, B0, A1, B2, t);
+      step(A1, B1, A0, B0, t + 1);
+      step(A0, B2, A1, B1, t + 2);
+      step(A1, B0, A0, B2, t + 3);
+      step(A0, B1, A1, B0, t + 4);
+      step(A1, B2, A0, B1, t + 5);
     }
+    // remaining 0..5 tiles, same rotation
+    if (t < ktiles) step(A0, B0, A1, B2, t);
+    if (t + 1 < ktiles) step(A1, B1, A0, B0, t + 1);
+    if (t + 2 < ktiles) step(A0, B2, A1, B1, t + 2);
+    if (t + 3 < ktiles) step(A1, B0, A0, B2, t + 3);
+    if (t + 4 < ktiles) step(A0, B1, A1, B0, t + 4);
+    wait_vmem();
+  } else {
+    // fp8 NN weights go through registers (transposed there): two stages
+    __shared__ __attribute__((aligned(1024))) uint8_t A0[BM * 128];
+    __shared__ __attribute__((aligned(1024))) uint8_t A1[BM * 128];
+    __shared__ __attribute__((aligned(1024))) uint8_t B0[BN * BROW];
+    __shared__ __attribute__((aligned(1024))) uint8_t B1[BN * BROW];
+    issue(A0, B0, 0);
+    wait_vmem();
+    store_nn(sn, B0);
     wait_vmem();
     __syncthreads();
     int t = 0;
@@ -522,17 +572,15 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
       issue(A1, B1, (int64_t)(t + 1) * BK);
       mma_tile<BMODE>(acc, A0, B0, wm, brow, lane);
       schedule_ktile<NDS, NVM>();
-      if (REG_B) {
-        wait_vmem();
-        store_nn(sn, B1);
-      }
+      wait_vmem();
+      store_nn(sn, B1);
       wait_vmem();
       __syncthreads();
       // past the last tile this reads zeros (K offset out of range) into the idle stage
       issue(A0, B0, (int64_t)(t + 2) * BK);
       mma_tile<BMODE>(acc, A1, B1, wm, brow, lane);
       schedule_ktile<NDS, NVM>();
-      if (REG_B && t + 2 < ktiles) {
+      if (t + 2 < ktiles) {
         wait_vmem();
         store_nn(sn, B0);
       }
