@@ -57,15 +57,33 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 #define LC 64    // chunk length
 #define LD 128   // head dim (q, k)
 #define LDV 128  // head dim (v, o)
-#define LS 32    // d_v columns per workgroup
+#define LS 64    // d_v columns per workgroup (two 32-column V tiles)
 
 struct LinAttnArgs {
   const uint16_t *q;
   const uint16_t *k;
   const uint16_t *v;
   uint16_t *o;
-  int64_t BH;      // batch * heads
-  int64_t T;       // sequence length (multiple of 64)
+  const float *part;  // prefix-state partial sums (segments > 0), else null
+  int64_t BH;         // batch * heads
+  int64_t T;          // sequence length (multiple of 64 * nseg)
+  int32_t nseg;       // sequence segments per head, run concurrently
+  int32_t rchunks;    // chunks per partial-sum range (divides T / 64 / nseg)
+};
+
+// Partial state sums over ranges of rchunks chunks: for head bh and range r,
+// S_r[d][j] = sum phi(k_t)[d] v_t[j] and z_r[d] = sum phi(k_t)[d] over the
+// range's tokens; ranges cover the segments before the last one.  Layout:
+// part[((bh * R + r) * (LD + 1) + d) * LDV + j] with row d = LD holding z_r
+// (in columns 0..127).
+struct LinAttnStateArgs {
+  const uint16_t *k;
+  const uint16_t *v;
+  float *part;
+  int64_t BH;
+  int64_t T;
+  int32_t nranges;  // R
+  int32_t rchunks;
 };
 
 // Byte offsets in the LDS tiles.  Rows of 256 bytes (phi(Q), phi(K) [t][d],
@@ -112,22 +130,28 @@ __device__ __forceinline__ uint4 phi8(uint4 raw) {
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+typedef float f2 __attribute__((ext_vector_type(2)));
+
+// two floats -> packed fp16 pair, round to nearest even (v_cvt_pk_f16_f32)
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  const f2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
+}
+
 // bf16 x 8 -> fp16 x 8 (round to nearest even; V may be large)
 __device__ __forceinline__ uint4 to_f16x8(uint4 raw) {
   const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
   uint32_t o[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    o[i] = (uint32_t)f32_to_f16(__uint_as_float(w[i] << 16)) |
-           ((uint32_t)f32_to_f16(__uint_as_float(w[i] & 0xffff0000u)) << 16);
+  for (int i = 0; i < 4; ++i) o[i] = pack_f16x2(__uint_as_float(w[i] << 16), __uint_as_float(w[i] & 0xffff0000u));
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 struct Stage {  // one chunk's operands in LDS
   uint8_t *Q;   // phi(Q) [64 t][128 d] fp16
   uint8_t *K;   // phi(K) [64 s][128 d] fp16
-  uint8_t *V;   // V slice [64 s][32 j] fp16
-  uint8_t *St;  // S^T of the state before this chunk [32 j][128 d] fp16
+  uint8_t *V;   // V slice: two tiles [64 s][32 j] fp16, 4 KiB apart
+  uint8_t *St;  // S^T of the state before this chunk [64 j][128 d] fp16
   uint8_t *z;   // z / 256 before this chunk [128] fp16
 };
 
@@ -144,8 +168,8 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
   __shared__ __attribute__((aligned(1024))) uint8_t Q1[LC * 256];
   __shared__ __attribute__((aligned(1024))) uint8_t K0[LC * 256];
   __shared__ __attribute__((aligned(1024))) uint8_t K1[LC * 256];
-  __shared__ __attribute__((aligned(1024))) uint8_t V0[LC * 64];
-  __shared__ __attribute__((aligned(1024))) uint8_t V1[LC * 64];
+  __shared__ __attribute__((aligned(1024))) uint8_t V0[LC * 128];
+  __shared__ __attribute__((aligned(1024))) uint8_t V1[LC * 128];
   __shared__ __attribute__((aligned(1024))) uint8_t ST0[LS * 256];
   __shared__ __attribute__((aligned(1024))) uint8_t ST1[LS * 256];
   __shared__ __attribute__((aligned(16))) uint8_t Z0[LD * 2];
@@ -157,37 +181,41 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
   const int l16 = lane & 15, grp = lane >> 4;  // 16x16 operand roles
   const int l32 = lane & 31, lhi = lane >> 5;  // 32x32 operand roles
 
-  // The four d_v slices of a head read the same q / k tiles: give them
-  // workgroup ids that are equal modulo 8 so they land on the same XCD and
-  // share its L2 (workgroups are dealt to the 8 XCDs round robin).
-  int64_t bh;
-  int slice;
-  if ((a.BH & 7) == 0) {
+  // workgroup -> (sequence bh, segment seg, d_v half).  The two halves of a
+  // (bh, seg) read the same q / k tiles: their ids are equal modulo 8 so
+  // they land on the same XCD and share its L2 (workgroups are dealt to the
+  // 8 XCDs round robin).
+  const int64_t units = a.BH * a.nseg;
+  int64_t unit;
+  int half;
+  if ((units & 7) == 0) {
     const int id = blockIdx.x;
-    bh = (int64_t)(id >> 5) * 8 + (id & 7);
-    slice = (id >> 3) & 3;
+    unit = (int64_t)(id >> 4) * 8 + (id & 7);
+    half = (id >> 3) & 1;
   } else {
-    bh = blockIdx.x >> 2;
-    slice = blockIdx.x & 3;
+    unit = blockIdx.x >> 1;
+    half = blockIdx.x & 1;
   }
-  const int j0 = slice * LS;
+  const int64_t bh = unit / a.nseg;
+  const int seg = (int)(unit % a.nseg);
+  const int j0 = half * LS;
   const int64_t base = bh * a.T * LD;
-  const int nchunks = (int)(a.T / LC);
+  const int nchunks = (int)(a.T / LC / a.nseg);  // chunks of this segment
+  const int c0 = seg * nchunks;                   // first chunk of the segment
 
   // ---------------- input staging -----------------------------------------
-  // thread -> q / k chunks (row tid/16 + 32 i, 8 columns at 8 (tid % 16));
-  // threads 0..255 -> v chunk (row tid / 4, 8 columns j0 + 8 (tid % 4)).
-  // q / k are read by the four slice workgroups of the head: plain (cached)
-  // loads.
+  // thread -> q / k chunks (row tid/16 + 32 i, 8 columns at 8 (tid % 16)) and
+  // one v chunk (row tid / 8, 8 columns j0 + 8 (tid % 8)).  q / k are read
+  // by both halves of the segment: plain (cached) loads.
   auto load_raw = [&](Raw &r, int c) {
-    const int64_t cb = base + (int64_t)c * LC * LD;
+    const int64_t cb = base + (int64_t)(c0 + c) * LC * LD;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int row = (tid >> 4) + 32 * i, col = (tid & 15) * 8;
       r.q[i] = *reinterpret_cast<const uint4 *>(a.q + cb + row * LD + col);
       r.k[i] = *reinterpret_cast<const uint4 *>(a.k + cb + row * LD + col);
     }
-    if (tid < 256) r.v = *reinterpret_cast<const uint4 *>(a.v + cb + (tid >> 2) * LDV + j0 + (tid & 3) * 8);
+    r.v = *reinterpret_cast<const uint4 *>(a.v + cb + (tid >> 3) * LDV + j0 + (tid & 7) * 8);
   };
   auto stage_in = [&](const Raw &r, const Stage &s) {
 #pragma unroll
@@ -196,15 +224,33 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
       *reinterpret_cast<uint4 *>(s.Q + o256(row, byte)) = phi8(r.q[i]);
       *reinterpret_cast<uint4 *>(s.K + o256(row, byte)) = phi8(r.k[i]);
     }
-    if (tid < 256) *reinterpret_cast<uint4 *>(s.V + o64(tid >> 2, (tid & 3) * 16)) = to_f16x8(r.v);
+    *reinterpret_cast<uint4 *>(s.V + ((tid >> 2) & 1) * 4096 + o64(tid >> 3, (tid & 3) * 16)) = to_f16x8(r.v);
   };
 
   // ---------------- per-wave state ------------------------------------------
-  f32x16 S, Z;  // S[d = 32w + row][j = col] and z[d] (in every column), fp32
+  // state wave w: S[d = 32w + row][j = 32 jt2 + col] and z[d] (in every
+  // column), fp32; segments after the first start from the sum of the
+  // partial states of all earlier ranges
+  f32x16 S[2], Z;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    S[r] = 0.f;
+    S[0][r] = 0.f;
+    S[1][r] = 0.f;
     Z[r] = 0.f;
+  }
+  if (seg > 0 && wave >= 4) {
+    const int nr = seg * nchunks / a.rchunks;
+    const int R = (a.nseg - 1) * nchunks / a.rchunks;
+    for (int rr = 0; rr < nr; ++rr) {
+      const float *pr = a.part + (bh * R + rr) * (int64_t)(LD + 1) * LDV;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = 32 * (wave - 4) + 8 * (r >> 2) + 4 * lhi + (r & 3);
+        S[0][r] += pr[(int64_t)d * LDV + j0 + l32];
+        S[1][r] += pr[(int64_t)d * LDV + j0 + 32 + l32];
+        Z[r] += pr[(int64_t)LD * LDV + d];
+      }
+    }
   }
   f16x8_t ones;
 #pragma unroll
@@ -214,7 +260,7 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
   // Query wave W (queries 16W..16W+15) is specialised per W so the causal
   // structure (key tiles 0..W) is static: one basic block per chunk, in which
   // the compiler interleaves the staging of the next chunk with the MFMA
-  // chains.  The normaliser comes out of the same MFMAs as a third output
+  // chains.  The normaliser comes out of the same MFMAs as a fifth output
   // tile: its A operand row 0 is z_prev / 256 for the S^T Q^T part and 1/256
   // for the V^T A^T part, so row 0 of that tile is den / 256 (z / 256 keeps
   // the fp16 copy of z finite up to z = 2^24; the power-of-two scale is
@@ -230,17 +276,17 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
     for (int st = 0; st < 4; ++st)
       qf[st] = *reinterpret_cast<const f16x8_t *>(cur.Q + o256(16 * W + l16, (32 * st + 8 * grp) * 2));
 
-    // O^T tiles 0, 1: rows j = 16 jt + 4 grp + r; tile 2 row 0: den / 256
+    // O^T tiles 0..3: rows j = 16 jt + 4 grp + r; tile 4 row 0: den / 256
     // (column = query l16)
-    f32x4 ot[3];
+    f32x4 ot[5];
 #pragma unroll
-    for (int jt = 0; jt < 3; ++jt)
+    for (int jt = 0; jt < 5; ++jt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) ot[jt][r] = 0.f;
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
 #pragma unroll
-      for (int jt = 0; jt < 2; ++jt) {
+      for (int jt = 0; jt < 4; ++jt) {
         const f16x8_t sf =
             *reinterpret_cast<const f16x8_t *>(cur.St + o256(16 * jt + l16, (32 * st + 8 * grp) * 2));
         ot[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sf, qf[st], ot[jt], 0, 0, 0);
@@ -250,7 +296,7 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
 #pragma unroll
         for (int e = 0; e < 8; ++e) zf[e] = (_Float16)0.f;
       }
-      ot[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(zf, qf[st], ot[2], 0, 0, 0);
+      ot[4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(zf, qf[st], ot[4], 0, 0, 0);
     }
 
     // A^T tiles (keys 16 kt + .., queries 16W + ..), kt = 0..W; lane: column
@@ -285,23 +331,25 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
         pf[4 + e] = (_Float16)at[2 * p + 1][e];
       }
 #pragma unroll
-      for (int jt = 0; jt < 2; ++jt) {
-        // transpose reads: source row 16 tile + 4 grp + l16/4, columns 16 jt + 4 (l16 % 4)
-        const int jb = (16 * jt + 4 * (l16 & 3)) * 2;
-        const f16x4_t v0 = tr_read(cur.V + o64(16 * (2 * p) + 4 * grp + (l16 >> 2), jb));
-        const f16x4_t v1 = tr_read(cur.V + o64(16 * (2 * p + 1) + 4 * grp + (l16 >> 2), jb));
+      for (int jt = 0; jt < 4; ++jt) {
+        // transpose reads from V tile jt / 2: source row 16 tile + 4 grp +
+        // l16/4, columns 16 (jt % 2) + 4 (l16 % 4)
+        const uint8_t *vt = cur.V + (jt >> 1) * 4096;
+        const int jb = (16 * (jt & 1) + 4 * (l16 & 3)) * 2;
+        const f16x4_t v0 = tr_read(vt + o64(16 * (2 * p) + 4 * grp + (l16 >> 2), jb));
+        const f16x4_t v1 = tr_read(vt + o64(16 * (2 * p + 1) + 4 * grp + (l16 >> 2), jb));
         ot[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cat(v0, v1), pf, ot[jt], 0, 0, 0);
       }
-      ot[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(zrow_ones, pf, ot[2], 0, 0, 0);
+      ot[4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(zrow_ones, pf, ot[4], 0, 0, 0);
     }
-    // den: row 0 of tile 2 sits in lane l16 (group 0), element 0
-    const float den = 256.0f * __shfl(ot[2][0], l16, 64);
+    // den: row 0 of tile 4 sits in lane l16 (group 0), element 0
+    const float den = 256.0f * __shfl(ot[4][0], l16, 64);
     // normalise and store: o[t][j0 + j], 4 consecutive j per lane
     {
       const float inv = 1.0f / den;
-      const int64_t t = (int64_t)c * LC + 16 * W + l16;
+      const int64_t t = (int64_t)(c0 + c) * LC + 16 * W + l16;
 #pragma unroll
-      for (int jt = 0; jt < 2; ++jt) {
+      for (int jt = 0; jt < 4; ++jt) {
         const uint32_t w0 = pack_bf16x2(ot[jt][0] * inv, ot[jt][1] * inv);
         const uint32_t w1 = pack_bf16x2(ot[jt][2] * inv, ot[jt][3] * inv);
         *reinterpret_cast<uint2 *>(a.o + base + t * LDV + j0 + 16 * jt + 4 * grp) = make_uint2(w0, w1);
@@ -311,30 +359,36 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
   auto state_side = [&](const Stage &cur, const Stage &nxt, const int wave) {
     // state update for rows d = 32w + ..: S += phi(K)^T V, z += phi(K)^T 1.
     // A operand (K^T): row d = 32w + l32, keys 16 st + 8 lhi + 0..7 -> two
-    // transpose reads of 4 keys; B operand (V): column j = l32, same keys.
+    // transpose reads of 4 keys; B operand (V): column j = 32 jt2 + l32,
+    // same keys.
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const int kb = 16 * st + 8 * (grp >> 1) + (l16 >> 2);
       const int db = (32 * wave + 16 * (grp & 1) + 4 * (l16 & 3)) * 2;
       const int jb = (16 * (grp & 1) + 4 * (l16 & 3)) * 2;
       const f16x8_t kf = cat(tr_read(cur.K + o256(kb, db)), tr_read(cur.K + o256(kb + 4, db)));
-      const f16x8_t vf = cat(tr_read(cur.V + o64(kb, jb)), tr_read(cur.V + o64(kb + 4, jb)));
-      S = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, vf, S, 0, 0, 0);
+#pragma unroll
+      for (int jt2 = 0; jt2 < 2; ++jt2) {
+        const uint8_t *vt = cur.V + jt2 * 4096;
+        const f16x8_t vf = cat(tr_read(vt + o64(kb, jb)), tr_read(vt + o64(kb + 4, jb)));
+        S[jt2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, vf, S[jt2], 0, 0, 0);
+      }
       Z = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ones, Z, 0, 0, 0);
     }
-    // fp16 S^T and z / 256 for the next chunk: lane holds column j = l32 and
-    // rows d = 32w + 8 (r/4) + 4 lhi + r%4
+    // fp16 S^T and z / 256 for the next chunk: lane holds column j = 32 jt2
+    // + l32 and rows d = 32w + 8 (r/4) + 4 lhi + r%4
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
       const int d = 32 * wave + 8 * g4 + 4 * lhi;
-      const uint32_t w0 = (uint32_t)f32_to_f16(S[4 * g4 + 0]) | ((uint32_t)f32_to_f16(S[4 * g4 + 1]) << 16);
-      const uint32_t w1 = (uint32_t)f32_to_f16(S[4 * g4 + 2]) | ((uint32_t)f32_to_f16(S[4 * g4 + 3]) << 16);
-      *reinterpret_cast<uint2 *>(nxt.St + o256(l32, d * 2)) = make_uint2(w0, w1);
+#pragma unroll
+      for (int jt2 = 0; jt2 < 2; ++jt2) {
+        const uint32_t w0 = pack_f16x2(S[jt2][4 * g4 + 0], S[jt2][4 * g4 + 1]);
+        const uint32_t w1 = pack_f16x2(S[jt2][4 * g4 + 2], S[jt2][4 * g4 + 3]);
+        *reinterpret_cast<uint2 *>(nxt.St + o256(32 * jt2 + l32, d * 2)) = make_uint2(w0, w1);
+      }
       if (l32 == 0) {
-        const uint32_t z0 = (uint32_t)f32_to_f16(Z[4 * g4 + 0] * 0.00390625f) |
-                            ((uint32_t)f32_to_f16(Z[4 * g4 + 1] * 0.00390625f) << 16);
-        const uint32_t z1 = (uint32_t)f32_to_f16(Z[4 * g4 + 2] * 0.00390625f) |
-                            ((uint32_t)f32_to_f16(Z[4 * g4 + 3] * 0.00390625f) << 16);
+        const uint32_t z0 = pack_f16x2(Z[4 * g4 + 0] * 0.00390625f, Z[4 * g4 + 1] * 0.00390625f);
+        const uint32_t z1 = pack_f16x2(Z[4 * g4 + 2] * 0.00390625f, Z[4 * g4 + 3] * 0.00390625f);
         *(__attribute__((address_space(3))) uint2 *)(nxt.z + d * 2) = make_uint2(z0, z1);
       }
     }
@@ -352,12 +406,28 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
   };
 
   const Stage s0{Q0, K0, V0, ST0, Z0}, s1{Q1, K1, V1, ST1, Z1};
-  // S_0 = 0, z_0 = 0
-  for (int i = tid; i < LS * 256 / 16; i += 512) reinterpret_cast<uint4 *>(ST0)[i] = make_uint4(0, 0, 0, 0);
-  if (tid < LD) reinterpret_cast<uint16_t *>(Z0)[tid] = 0;
+  // initial S^T and z / 256 (zero, or the prefix state of this segment)
+  if (wave >= 4) {
+    const int w4 = wave - 4;
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d = 32 * w4 + 8 * g4 + 4 * lhi;
+#pragma unroll
+      for (int jt2 = 0; jt2 < 2; ++jt2) {
+        const uint32_t w0 = pack_f16x2(S[jt2][4 * g4 + 0], S[jt2][4 * g4 + 1]);
+        const uint32_t w1 = pack_f16x2(S[jt2][4 * g4 + 2], S[jt2][4 * g4 + 3]);
+        *reinterpret_cast<uint2 *>(ST0 + o256(32 * jt2 + l32, d * 2)) = make_uint2(w0, w1);
+      }
+      if (l32 == 0) {
+        const uint32_t z0 = pack_f16x2(Z[4 * g4 + 0] * 0.00390625f, Z[4 * g4 + 1] * 0.00390625f);
+        const uint32_t z1 = pack_f16x2(Z[4 * g4 + 2] * 0.00390625f, Z[4 * g4 + 3] * 0.00390625f);
+        *(__attribute__((address_space(3))) uint2 *)(Z0 + d * 2) = make_uint2(z0, z1);
+      }
+    }
+  }
   Raw ra{}, rb{};
   load_raw(ra, 0);
-  if (nchunks > 1) load_raw(rb, 1);
+  load_raw(rb, min(1, nchunks - 1));
   stage_in(ra, s0);
   __syncthreads();
   // iteration c: fetch chunk c + 2, compute chunk c, stage chunk c + 1.  The
@@ -375,4 +445,102 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
     __syncthreads();
   }
   if (c < nchunks) chunk(s0, s1, c, rb);
+}
+
+// Partial states of ranges of rchunks chunks (the prefix of later segments):
+// one workgroup (4 waves) per (sequence, range, d_v half); wave w owns state
+// rows d = 32w..32w+31.  Per chunk: phi(K) and the V half are staged in LDS
+// (fp16, the layouts of the scan kernel) and S += phi(K)^T V, z += phi(K)^T 1
+// accumulate in the MFMA accumulators; the sums go out in fp32.
+extern "C" __global__ __launch_bounds__(256, 2) void nk_linattn_state_c64_d128(LinAttnStateArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t KS[2][LC * 256];
+  __shared__ __attribute__((aligned(1024))) uint8_t VS[2][LC * 128];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, grp = lane >> 4;
+  const int l32 = lane & 31, lhi = lane >> 5;
+
+  const int id = blockIdx.x;
+  const int half = id & 1;
+  const int64_t rr = (id >> 1) % a.nranges;
+  const int64_t bh = (id >> 1) / a.nranges;
+  const int j0 = half * LS;
+  const int64_t base = bh * a.T * LD + rr * a.rchunks * LC * LD;
+
+  f32x16 S[2], Z;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    S[0][r] = 0.f;
+    S[1][r] = 0.f;
+    Z[r] = 0.f;
+  }
+  f16x8_t ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
+
+  // thread -> k rows tid/16 + 16 i (i < 4), 8 columns at 8 (tid % 16); v
+  // rows tid/8 + 32 i (i < 2), 8 columns j0 + 8 (tid % 8)
+  auto load = [&](uint4 (&kr)[4], uint4 (&vr)[2], int c) {
+    const int64_t cb = base + (int64_t)c * LC * LD;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      kr[i] = *reinterpret_cast<const uint4 *>(a.k + cb + ((tid >> 4) + 16 * i) * LD + (tid & 15) * 8);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      vr[i] = *reinterpret_cast<const uint4 *>(a.v + cb + ((tid >> 3) + 32 * i) * LDV + j0 + (tid & 7) * 8);
+  };
+  auto stage = [&](const uint4 (&kr)[4], const uint4 (&vr)[2], int b) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<uint4 *>(KS[b] + o256((tid >> 4) + 16 * i, (tid & 15) * 16)) = phi8(kr[i]);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      *reinterpret_cast<uint4 *>(VS[b] + ((tid >> 2) & 1) * 4096 + o64((tid >> 3) + 32 * i, (tid & 3) * 16)) =
+          to_f16x8(vr[i]);
+  };
+  auto update = [&](int b) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int kb = 16 * st + 8 * (grp >> 1) + (l16 >> 2);
+      const int db = (32 * wave + 16 * (grp & 1) + 4 * (l16 & 3)) * 2;
+      const int jb = (16 * (grp & 1) + 4 * (l16 & 3)) * 2;
+      const f16x8_t kf = cat(tr_read(KS[b] + o256(kb, db)), tr_read(KS[b] + o256(kb + 4, db)));
+#pragma unroll
+      for (int jt2 = 0; jt2 < 2; ++jt2) {
+        const uint8_t *vt = VS[b] + jt2 * 4096;
+        const f16x8_t vf = cat(tr_read(vt + o64(kb, jb)), tr_read(vt + o64(kb + 4, jb)));
+        S[jt2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, vf, S[jt2], 0, 0, 0);
+      }
+      Z = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ones, Z, 0, 0, 0);
+    }
+  };
+
+  uint4 ka[4], va[2], kb4[4], vb[2];
+  load(ka, va, 0);
+  load(kb4, vb, min(1, a.rchunks - 1));
+  stage(ka, va, 0);
+  __syncthreads();
+  int c = 0;
+  for (; c + 2 <= a.rchunks; c += 2) {
+    load(ka, va, min(c + 2, a.rchunks - 1));
+    update(0);
+    stage(kb4, vb, 1);
+    __syncthreads();
+    load(kb4, vb, min(c + 3, a.rchunks - 1));
+    update(1);
+    stage(ka, va, 0);
+    __syncthreads();
+  }
+  if (c < a.rchunks) update(0);
+
+  float *out = a.part + (bh * a.nranges + rr) * (int64_t)(LD + 1) * LDV;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int d = 32 * wave + 8 * (r >> 2) + 4 * lhi + (r & 3);
+    out[(int64_t)d * LDV + j0 + l32] = S[0][r];
+    out[(int64_t)d * LDV + j0 + 32 + l32] = S[1][r];
+    if (half == 0 && l32 == 0) out[(int64_t)LD * LDV + d] = Z[r];
+  }
 }

@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass, field
-from typing import Tuple
+from typing import List, Tuple
 
 import numpy as np
 
@@ -311,17 +311,56 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
 # ---------------------------------------------------------------------------
 class LinAttnArgs(ctypes.Structure):
     _fields_ = [("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
-                ("o", ctypes.c_void_p), ("BH", ctypes.c_int64), ("T", ctypes.c_int64)]
+                ("o", ctypes.c_void_p), ("part", ctypes.c_void_p), ("BH", ctypes.c_int64),
+                ("T", ctypes.c_int64), ("nseg", ctypes.c_int32), ("rchunks", ctypes.c_int32)]
+
+
+class LinAttnStateArgs(ctypes.Structure):
+    _fields_ = [("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("part", ctypes.c_void_p),
+                ("BH", ctypes.c_int64), ("T", ctypes.c_int64), ("nranges", ctypes.c_int32),
+                ("rchunks", ctypes.c_int32)]
 
 
 LINATTN_CHUNK = 64
 LINATTN_D = 128
+# workgroups per (sequence, segment): two 64-column halves of d_v
+LINATTN_HALVES = 2
+# the scan is serial over a sequence's chunks; with fewer than this many
+# workgroups the sequence is cut into segments whose prefix states come from
+# a separate partial-sum kernel
+LINATTN_TARGET_WGS = 256
+
+
+def linear_attention_split(BH: int, T: int):
+    """(segments per sequence, chunks per partial-sum range, ranges) for the
+    linear-attention scan of BH sequences of length T."""
+    nchunks = T // LINATTN_CHUNK
+    nseg = 1
+    while (BH * LINATTN_HALVES * nseg < LINATTN_TARGET_WGS and nchunks % (2 * nseg) == 0
+           and nchunks // (2 * nseg) >= 8):
+        nseg *= 2
+    cs = nchunks // nseg
+    rchunks = cs // 4 if cs % 4 == 0 else cs
+    nranges = (nseg - 1) * (cs // rchunks)
+    return nseg, rchunks, nranges
+
+
+def linear_attention_workspace_bytes(BH: int, T: int) -> int:
+    """Device workspace (fp32 partial prefix states) the launch needs; 0 if
+    the sequences run unsegmented."""
+    _, _, nranges = linear_attention_split(BH, T)
+    return BH * nranges * (LINATTN_D + 1) * LINATTN_D * 4
 
 
 def linear_attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, BH: int, T: int,
-                     D: int = 128, Dv: int = 128, chunk: int = 64) -> Launch:
+                     D: int = 128, Dv: int = 128, chunk: int = 64, part_ptr: int = 0) -> List[Launch]:
     """o = causal linear attention with phi = elu + 1 over (BH, T, D) bf16
-    sequences, chunk 64, head dims 128 (the compiled variant)."""
+    sequences, chunk 64, head dims 128 (the compiled variant).
+
+    Returns the launches in order: when the sequences are cut into segments,
+    a partial-sum kernel writes the prefix states into ``part_ptr`` (a
+    workspace of :func:`linear_attention_workspace_bytes` bytes) before the
+    scan reads them."""
     if (D, Dv, chunk) != (LINATTN_D, LINATTN_D, LINATTN_CHUNK):
         raise LaunchError(f"linear attention kernel is built for d = d_v = 128, chunk 64; "
                           f"got d={D}, d_v={Dv}, chunk={chunk}")
@@ -329,13 +368,26 @@ def linear_attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, BH: int, T:
         raise LaunchError(f"linear attention needs T a positive multiple of {chunk}, got T={T}")
     if any(p % 16 for p in (q_ptr, k_ptr, v_ptr, o_ptr)):
         raise LaunchError("linear attention operands must be 16-byte aligned")
-    if BH * 4 >= 2**31:
+    nseg, rchunks, nranges = linear_attention_split(BH, T)
+    if BH * nseg * LINATTN_HALVES >= 2**31 or BH * max(nranges, 1) * LINATTN_HALVES >= 2**31:
         raise LaunchError("linear attention grid too large")
+    if nranges and not part_ptr:
+        raise LaunchError(f"linear attention of {BH} x {T} runs in {nseg} segments and needs a "
+                          f"workspace of {linear_attention_workspace_bytes(BH, T)} bytes")
+    if part_ptr % 16:
+        raise LaunchError("linear attention workspace must be 16-byte aligned")
     n = T // chunk
     flops_chunk = 2 * chunk * chunk * D + 2 * chunk * D * Dv + 2 * chunk * chunk * Dv + 2 * D * Dv * chunk
-    return Launch("linattn", "nk_linattn_c64_d128", (BH * 4, 1, 1), (512, 1, 1),
-                  LinAttnArgs(q_ptr, k_ptr, v_ptr, o_ptr, BH, T),
-                  bytes=4 * BH * T * D * 2, flops=BH * n * flops_chunk)
+    launches = []
+    if nranges:
+        launches.append(Launch("linattn", "nk_linattn_state_c64_d128", (BH * nranges * LINATTN_HALVES, 1, 1),
+                               (256, 1, 1), LinAttnStateArgs(k_ptr, v_ptr, part_ptr, BH, T, nranges, rchunks),
+                               bytes=2 * BH * nranges * rchunks * chunk * D * 2,
+                               flops=BH * nranges * rchunks * 2 * chunk * D * Dv))
+    launches.append(Launch("linattn", "nk_linattn_c64_d128", (BH * nseg * LINATTN_HALVES, 1, 1), (512, 1, 1),
+                           LinAttnArgs(q_ptr, k_ptr, v_ptr, o_ptr, part_ptr or None, BH, T, nseg, rchunks),
+                           bytes=4 * BH * T * D * 2, flops=BH * n * flops_chunk))
+    return launches
 
 
 # ---------------------------------------------------------------------------

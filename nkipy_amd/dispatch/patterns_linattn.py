@@ -25,6 +25,7 @@ import numpy as np
 
 from nkipy_amd.core import dtypes as dt
 from nkipy_amd.dispatch import launchers as LA
+from nkipy_amd.dispatch.plan import Slot
 from nkipy_amd.dispatch.patterns import LaunchStep, Match, _users_of, op_of, scalar_value, through_views
 
 
@@ -103,9 +104,13 @@ class LinearAttentionMatch(Match):
     def steps(self, plan):
         q, k, v, out = self.q, self.k, self.v, self.out
         B, H, T, D = q.shape
+        # segmented scans take their prefix states from a workspace temporary
+        ws_bytes = LA.linear_attention_workspace_bytes(B * H, T)
+        ws = Slot(plan.add_buffer(ws_bytes, "temp", "linear_attention.prefix")) if ws_bytes else None
 
         def make(addr):
-            return LA.linear_attention(addr(q), addr(k), addr(v), addr(out), B * H, T, D, v.shape[-1], 64)
+            return LA.linear_attention(addr(q), addr(k), addr(v), addr(out), B * H, T, D, v.shape[-1], 64,
+                                       part_ptr=addr(ws) if ws is not None else 0)
 
         return [LaunchStep("linear_attention", f"chunked causal linear attention B*H={B * H} T={T} d={D}",
                            self.inputs, self.outputs, make)]

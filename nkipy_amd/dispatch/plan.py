@@ -177,8 +177,9 @@ class PlanExecutor:
     def _bind(self, bases: Dict[int, int]) -> BoundPlan:
         plan = self.plan
 
-        def addr(v: Value) -> int:
-            s = plan.slot(v)
+        def addr(v) -> int:
+            # a graph value, or a Slot of a step's own workspace temporary
+            s = v if isinstance(v, Slot) else plan.slot(v)
             return bases[s.buffer] + s.offset
 
         launches: List[Launch] = []

@@ -23,7 +23,11 @@ def _run(gpu, q, k, v):
     B, H, T, D = q.shape
     t = [DeviceTensor.from_numpy(dt.to_bf16(a)) for a in (q, k, v)]
     o = DeviceTensor.empty((B, H, T, D), dt.bfloat16)
-    LA.linear_attention(t[0].ptr, t[1].ptr, t[2].ptr, o.ptr, B * H, T).run(gpu)
+    ws_bytes = LA.linear_attention_workspace_bytes(B * H, T)
+    ws = DeviceTensor.empty((max(ws_bytes, 16),), dt.uint8) if ws_bytes else None
+    for launch in LA.linear_attention(t[0].ptr, t[1].ptr, t[2].ptr, o.ptr, B * H, T,
+                                      part_ptr=ws.ptr if ws is not None else 0):
+        launch.run(gpu)
     gpu.sync()
     return dt.to_float32(o.numpy())
 
@@ -37,6 +41,17 @@ def _close(got, ref, tol=2e-2):
 
 @pytest.mark.parametrize("shape", [(1, 1, 64, 128), (1, 2, 128, 128), (2, 2, 256, 128)])
 def test_linattn_matches_quadratic_form(gpu, shape):
+    q, k, v = _qkv(*shape, seed=sum(shape))
+    got = _run(gpu, q, k, v)
+    _close(got, K.linear_attention_quadratic_f64(q, k, v))
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 1024, 128), (1, 1, 4096, 128)])
+def test_linattn_segmented_matches_quadratic_form(gpu, shape):
+    """Few sequences: the scan is cut into segments whose prefix states come
+    from the partial-sum kernel (segments, ranges as chosen by the launcher)."""
+    B, H, T, D = shape
+    assert LA.linear_attention_split(B * H, T)[0] > 1
     q, k, v = _qkv(*shape, seed=sum(shape))
     got = _run(gpu, q, k, v)
     _close(got, K.linear_attention_quadratic_f64(q, k, v))
