@@ -57,7 +57,6 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 #define LC 64    // chunk length
 #define LD 128   // head dim (q, k)
 #define LDV 128  // head dim (v, o)
-#define LS 64    // d_v columns per workgroup (two 32-column V tiles)
 
 struct LinAttnArgs {
   const uint16_t *q;
@@ -148,10 +147,9 @@ __device__ __forceinline__ uint4 to_f16x8(uint4 raw) {
 }
 
 struct Stage {  // one chunk's operands in LDS
-  uint8_t *Q;   // phi(Q) [64 t][128 d] fp16
   uint8_t *K;   // phi(K) [64 s][128 d] fp16
-  uint8_t *V;   // V slice: two tiles [64 s][32 j] fp16, 4 KiB apart
-  uint8_t *St;  // S^T of the state before this chunk [64 j][128 d] fp16
+  uint8_t *V;   // V: four tiles [64 s][32 j] fp16, 4 KiB apart
+  uint8_t *St;  // S^T of the state before this chunk [128 j][128 d] fp16
   uint8_t *z;   // z / 256 before this chunk [128] fp16
 };
 
@@ -159,19 +157,25 @@ template <int N> struct Int {
   static constexpr int value = N;
 };
 
-struct Raw {  // one chunk's inputs in registers (this thread's share)
-  uint4 q[2], k[2], v;
+// One chunk's inputs in registers (this thread's share).  Query waves hold
+// their own 16 q rows (4 x 16 bytes per lane, in the MFMA fragment layout);
+// state waves hold 4 k chunks; every thread holds 2 v chunks.
+struct Raw {
+  uint4 x[4];  // q (query waves) or k (state waves)
+  uint4 v[2];
 };
 
+// V chunk i (16 bytes: row i / 16, columns 8 (i % 16) ..) -> byte offset in
+// the four 32-column V tiles
+__device__ __forceinline__ int voff(int i) { return ((i >> 2) & 3) * 4096 + o64(i >> 4, (i & 3) * 16); }
+
 extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttnArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint8_t Q0[LC * 256];
-  __shared__ __attribute__((aligned(1024))) uint8_t Q1[LC * 256];
   __shared__ __attribute__((aligned(1024))) uint8_t K0[LC * 256];
   __shared__ __attribute__((aligned(1024))) uint8_t K1[LC * 256];
-  __shared__ __attribute__((aligned(1024))) uint8_t V0[LC * 128];
-  __shared__ __attribute__((aligned(1024))) uint8_t V1[LC * 128];
-  __shared__ __attribute__((aligned(1024))) uint8_t ST0[LS * 256];
-  __shared__ __attribute__((aligned(1024))) uint8_t ST1[LS * 256];
+  __shared__ __attribute__((aligned(1024))) uint8_t V0[LC * 256];
+  __shared__ __attribute__((aligned(1024))) uint8_t V1[LC * 256];
+  __shared__ __attribute__((aligned(1024))) uint8_t ST0[LDV * 256];
+  __shared__ __attribute__((aligned(1024))) uint8_t ST1[LDV * 256];
   __shared__ __attribute__((aligned(16))) uint8_t Z0[LD * 2];
   __shared__ __attribute__((aligned(16))) uint8_t Z1[LD * 2];
 
@@ -180,65 +184,70 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, grp = lane >> 4;  // 16x16 operand roles
   const int l32 = lane & 31, lhi = lane >> 5;  // 32x32 operand roles
+  const bool qwave = wave < 4;
 
-  // workgroup -> (sequence bh, segment seg, d_v half).  The two halves of a
-  // (bh, seg) read the same q / k tiles: their ids are equal modulo 8 so
-  // they land on the same XCD and share its L2 (workgroups are dealt to the
-  // 8 XCDs round robin).
-  const int64_t units = a.BH * a.nseg;
-  int64_t unit;
-  int half;
-  if ((units & 7) == 0) {
-    const int id = blockIdx.x;
-    unit = (int64_t)(id >> 4) * 8 + (id & 7);
-    half = (id >> 3) & 1;
-  } else {
-    unit = blockIdx.x >> 1;
-    half = blockIdx.x & 1;
-  }
+  // workgroup -> (sequence bh, segment seg); all of d_v
+  const int64_t unit = blockIdx.x;
   const int64_t bh = unit / a.nseg;
   const int seg = (int)(unit % a.nseg);
-  const int j0 = half * LS;
   const int64_t base = bh * a.T * LD;
   const int nchunks = (int)(a.T / LC / a.nseg);  // chunks of this segment
   const int c0 = seg * nchunks;                   // first chunk of the segment
 
   // ---------------- input staging -----------------------------------------
-  // thread -> q / k chunks (row tid/16 + 32 i, 8 columns at 8 (tid % 16)) and
-  // one v chunk (row tid / 8, 8 columns j0 + 8 (tid % 8)).  q / k are read
-  // by both halves of the segment: plain (cached) loads.
+  // query wave W: q rows 16W + l16, d = 32 st + 8 grp (its own fragments);
+  // state thread u = tid - 256: k chunks u + 256 i (row / 16, 8 columns);
+  // every thread: v chunks tid + 512 i.  Plain (cached) loads.
   auto load_raw = [&](Raw &r, int c) {
     const int64_t cb = base + (int64_t)(c0 + c) * LC * LD;
+    if (qwave) {
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+        r.x[st] = *reinterpret_cast<const uint4 *>(a.q + cb + (16 * wave + l16) * LD + 32 * st + 8 * grp);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int idx = tid - 256 + 256 * i;
+        r.x[i] = *reinterpret_cast<const uint4 *>(a.k + cb + (idx >> 4) * LD + (idx & 15) * 8);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int row = (tid >> 4) + 32 * i, col = (tid & 15) * 8;
-      r.q[i] = *reinterpret_cast<const uint4 *>(a.q + cb + row * LD + col);
-      r.k[i] = *reinterpret_cast<const uint4 *>(a.k + cb + row * LD + col);
+      const int idx = tid + 512 * i;
+      r.v[i] = *reinterpret_cast<const uint4 *>(a.v + cb + (idx >> 4) * LDV + (idx & 15) * 8);
     }
-    r.v = *reinterpret_cast<const uint4 *>(a.v + cb + (tid >> 3) * LDV + j0 + (tid & 7) * 8);
   };
-  auto stage_in = [&](const Raw &r, const Stage &s) {
+  // phi(Q) fragments of the next chunk (query waves, registers)
+  f16x8_t qf[4];
+  auto make_qf = [&](const Raw &r) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int row = (tid >> 4) + 32 * i, byte = (tid & 15) * 16;
-      *reinterpret_cast<uint4 *>(s.Q + o256(row, byte)) = phi8(r.q[i]);
-      *reinterpret_cast<uint4 *>(s.K + o256(row, byte)) = phi8(r.k[i]);
+    for (int st = 0; st < 4; ++st) qf[st] = __builtin_bit_cast(f16x8_t, phi8(r.x[st]));
+  };
+  // phi(K) and V of the next chunk into LDS
+  auto stage_in = [&](const Raw &r, const Stage &s) {
+    if (!qwave) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int idx = tid - 256 + 256 * i;
+        *reinterpret_cast<uint4 *>(s.K + o256(idx >> 4, (idx & 15) * 16)) = phi8(r.x[i]);
+      }
     }
-    *reinterpret_cast<uint4 *>(s.V + ((tid >> 2) & 1) * 4096 + o64(tid >> 3, (tid & 3) * 16)) = to_f16x8(r.v);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<uint4 *>(s.V + voff(tid + 512 * i)) = to_f16x8(r.v[i]);
   };
 
   // ---------------- per-wave state ------------------------------------------
-  // state wave w: S[d = 32w + row][j = 32 jt2 + col] and z[d] (in every
+  // state wave w: S[d = 32w + row][j = 32 jt4 + col] and z[d] (in every
   // column), fp32; segments after the first start from the sum of the
   // partial states of all earlier ranges
-  f32x16 S[2], Z;
+  f32x16 S[4], Z;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    S[0][r] = 0.f;
-    S[1][r] = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) S[t][r] = 0.f;
     Z[r] = 0.f;
   }
-  if (seg > 0 && wave >= 4) {
+  if (seg > 0 && !qwave) {
     const int nr = seg * nchunks / a.rchunks;
     const int R = (a.nseg - 1) * nchunks / a.rchunks;
     for (int rr = 0; rr < nr; ++rr) {
@@ -246,8 +255,8 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int d = 32 * (wave - 4) + 8 * (r >> 2) + 4 * lhi + (r & 3);
-        S[0][r] += pr[(int64_t)d * LDV + j0 + l32];
-        S[1][r] += pr[(int64_t)d * LDV + j0 + 32 + l32];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) S[t][r] += pr[(int64_t)d * LDV + 32 * t + l32];
         Z[r] += pr[(int64_t)LD * LDV + d];
       }
     }
@@ -256,11 +265,31 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
 #pragma unroll
   for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
 
+  // fp16 S^T and z / 256 into a stage: lane holds column j = 32 t + l32 and
+  // rows d = 32w + 8 (r/4) + 4 lhi + r%4
+  auto write_state = [&](const Stage &nxt, int w) {
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d = 32 * w + 8 * g4 + 4 * lhi;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t w0 = pack_f16x2(S[t][4 * g4 + 0], S[t][4 * g4 + 1]);
+        const uint32_t w1 = pack_f16x2(S[t][4 * g4 + 2], S[t][4 * g4 + 3]);
+        *reinterpret_cast<uint2 *>(nxt.St + o256(32 * t + l32, d * 2)) = make_uint2(w0, w1);
+      }
+      if (l32 == 0) {
+        const uint32_t z0 = pack_f16x2(Z[4 * g4 + 0] * 0.00390625f, Z[4 * g4 + 1] * 0.00390625f);
+        const uint32_t z1 = pack_f16x2(Z[4 * g4 + 2] * 0.00390625f, Z[4 * g4 + 3] * 0.00390625f);
+        *(__attribute__((address_space(3))) uint2 *)(nxt.z + d * 2) = make_uint2(z0, z1);
+      }
+    }
+  };
+
   // ---------------- one chunk -----------------------------------------------
   // Query wave W (queries 16W..16W+15) is specialised per W so the causal
   // structure (key tiles 0..W) is static: one basic block per chunk, in which
   // the compiler interleaves the staging of the next chunk with the MFMA
-  // chains.  The normaliser comes out of the same MFMAs as a fifth output
+  // chains.  The normaliser comes out of the same MFMAs as a ninth output
   // tile: its A operand row 0 is z_prev / 256 for the S^T Q^T part and 1/256
   // for the V^T A^T part, so row 0 of that tile is den / 256 (z / 256 keeps
   // the fp16 copy of z finite up to z = 2^24; the power-of-two scale is
@@ -270,23 +299,17 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
   for (int e = 0; e < 8; ++e) zrow_ones[e] = (_Float16)(l16 == 0 ? 0.00390625f : 0.f);
   auto query_side = [&](const Stage &cur, int c, auto wtag) __attribute__((always_inline)) {
     constexpr int W = decltype(wtag)::value;
-    // phi(Q_W) fragments: rows (queries) 16W + l16, d = 32 st + 8 grp + 0..7
-    f16x8_t qf[4];
-#pragma unroll
-    for (int st = 0; st < 4; ++st)
-      qf[st] = *reinterpret_cast<const f16x8_t *>(cur.Q + o256(16 * W + l16, (32 * st + 8 * grp) * 2));
-
-    // O^T tiles 0..3: rows j = 16 jt + 4 grp + r; tile 4 row 0: den / 256
+    // O^T tiles 0..7: rows j = 16 jt + 4 grp + r; tile 8 row 0: den / 256
     // (column = query l16)
-    f32x4 ot[5];
+    f32x4 ot[9];
 #pragma unroll
-    for (int jt = 0; jt < 5; ++jt)
+    for (int jt = 0; jt < 9; ++jt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) ot[jt][r] = 0.f;
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
+      for (int jt = 0; jt < 8; ++jt) {
         const f16x8_t sf =
             *reinterpret_cast<const f16x8_t *>(cur.St + o256(16 * jt + l16, (32 * st + 8 * grp) * 2));
         ot[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sf, qf[st], ot[jt], 0, 0, 0);
@@ -296,7 +319,7 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
 #pragma unroll
         for (int e = 0; e < 8; ++e) zf[e] = (_Float16)0.f;
       }
-      ot[4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(zf, qf[st], ot[4], 0, 0, 0);
+      ot[8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(zf, qf[st], ot[8], 0, 0, 0);
     }
 
     // A^T tiles (keys 16 kt + .., queries 16W + ..), kt = 0..W; lane: column
@@ -331,7 +354,7 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
         pf[4 + e] = (_Float16)at[2 * p + 1][e];
       }
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
+      for (int jt = 0; jt < 8; ++jt) {
         // transpose reads from V tile jt / 2: source row 16 tile + 4 grp +
         // l16/4, columns 16 (jt % 2) + 4 (l16 % 4)
         const uint8_t *vt = cur.V + (jt >> 1) * 4096;
@@ -340,94 +363,64 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
         const f16x4_t v1 = tr_read(vt + o64(16 * (2 * p + 1) + 4 * grp + (l16 >> 2), jb));
         ot[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cat(v0, v1), pf, ot[jt], 0, 0, 0);
       }
-      ot[4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(zrow_ones, pf, ot[4], 0, 0, 0);
+      ot[8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(zrow_ones, pf, ot[8], 0, 0, 0);
     }
-    // den: row 0 of tile 4 sits in lane l16 (group 0), element 0
-    const float den = 256.0f * __shfl(ot[4][0], l16, 64);
-    // normalise and store: o[t][j0 + j], 4 consecutive j per lane
+    // den: row 0 of tile 8 sits in lane l16 (group 0), element 0
+    const float den = 256.0f * __shfl(ot[8][0], l16, 64);
+    // normalise and store: o[t][j], 4 consecutive j per lane
     {
       const float inv = 1.0f / den;
       const int64_t t = (int64_t)(c0 + c) * LC + 16 * W + l16;
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
+      for (int jt = 0; jt < 8; ++jt) {
         const uint32_t w0 = pack_bf16x2(ot[jt][0] * inv, ot[jt][1] * inv);
         const uint32_t w1 = pack_bf16x2(ot[jt][2] * inv, ot[jt][3] * inv);
-        *reinterpret_cast<uint2 *>(a.o + base + t * LDV + j0 + 16 * jt + 4 * grp) = make_uint2(w0, w1);
+        *reinterpret_cast<uint2 *>(a.o + base + t * LDV + 16 * jt + 4 * grp) = make_uint2(w0, w1);
       }
     }
   };
-  auto state_side = [&](const Stage &cur, const Stage &nxt, const int wave) {
+  auto state_side = [&](const Stage &cur, const Stage &nxt, const int w) {
     // state update for rows d = 32w + ..: S += phi(K)^T V, z += phi(K)^T 1.
     // A operand (K^T): row d = 32w + l32, keys 16 st + 8 lhi + 0..7 -> two
-    // transpose reads of 4 keys; B operand (V): column j = 32 jt2 + l32,
-    // same keys.
+    // transpose reads of 4 keys; B operand (V): column j = 32 t + l32, same
+    // keys.
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const int kb = 16 * st + 8 * (grp >> 1) + (l16 >> 2);
-      const int db = (32 * wave + 16 * (grp & 1) + 4 * (l16 & 3)) * 2;
+      const int db = (32 * w + 16 * (grp & 1) + 4 * (l16 & 3)) * 2;
       const int jb = (16 * (grp & 1) + 4 * (l16 & 3)) * 2;
       const f16x8_t kf = cat(tr_read(cur.K + o256(kb, db)), tr_read(cur.K + o256(kb + 4, db)));
 #pragma unroll
-      for (int jt2 = 0; jt2 < 2; ++jt2) {
-        const uint8_t *vt = cur.V + jt2 * 4096;
+      for (int t = 0; t < 4; ++t) {
+        const uint8_t *vt = cur.V + t * 4096;
         const f16x8_t vf = cat(tr_read(vt + o64(kb, jb)), tr_read(vt + o64(kb + 4, jb)));
-        S[jt2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, vf, S[jt2], 0, 0, 0);
+        S[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, vf, S[t], 0, 0, 0);
       }
       Z = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ones, Z, 0, 0, 0);
     }
-    // fp16 S^T and z / 256 for the next chunk: lane holds column j = 32 jt2
-    // + l32 and rows d = 32w + 8 (r/4) + 4 lhi + r%4
-#pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const int d = 32 * wave + 8 * g4 + 4 * lhi;
-#pragma unroll
-      for (int jt2 = 0; jt2 < 2; ++jt2) {
-        const uint32_t w0 = pack_f16x2(S[jt2][4 * g4 + 0], S[jt2][4 * g4 + 1]);
-        const uint32_t w1 = pack_f16x2(S[jt2][4 * g4 + 2], S[jt2][4 * g4 + 3]);
-        *reinterpret_cast<uint2 *>(nxt.St + o256(32 * jt2 + l32, d * 2)) = make_uint2(w0, w1);
-      }
-      if (l32 == 0) {
-        const uint32_t z0 = pack_f16x2(Z[4 * g4 + 0] * 0.00390625f, Z[4 * g4 + 1] * 0.00390625f);
-        const uint32_t z1 = pack_f16x2(Z[4 * g4 + 2] * 0.00390625f, Z[4 * g4 + 3] * 0.00390625f);
-        *(__attribute__((address_space(3))) uint2 *)(nxt.z + d * 2) = make_uint2(z0, z1);
-      }
-    }
+    write_state(nxt, w);
   };
-  // one chunk plus the staging of the next one (raw inputs r) into nxt
-  auto chunk = [&](const Stage &cur, const Stage &nxt, int c, const Raw &r) {
-    switch (wave) {
-      case 0: query_side(cur, c, Int<0>{}); break;
-      case 1: query_side(cur, c, Int<1>{}); break;
-      case 2: query_side(cur, c, Int<2>{}); break;
-      case 3: query_side(cur, c, Int<3>{}); break;
-      default: state_side(cur, nxt, wave - 4); break;
+  // One chunk plus the staging of the next one (raw inputs r) into nxt /
+  // qf.  Each role (query wave W, state wave) runs its own copy of the chunk
+  // loop, so loop-invariant addresses of one role do not stay live in the
+  // other's registers; all copies pass the same barriers.
+  auto chunk = [&](const Stage &cur, const Stage &nxt, int c, const Raw &r, auto rtag) __attribute__((always_inline)) {
+    constexpr int ROLE = decltype(rtag)::value;  // 0..3 query wave W, 4 state wave
+    if constexpr (ROLE < 4) {
+      query_side(cur, c, Int<ROLE>{});
+      make_qf(r);
+    } else {
+      state_side(cur, nxt, wave - 4);
     }
     stage_in(r, nxt);
   };
 
-  const Stage s0{Q0, K0, V0, ST0, Z0}, s1{Q1, K1, V1, ST1, Z1};
-  // initial S^T and z / 256 (zero, or the prefix state of this segment)
-  if (wave >= 4) {
-    const int w4 = wave - 4;
-#pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const int d = 32 * w4 + 8 * g4 + 4 * lhi;
-#pragma unroll
-      for (int jt2 = 0; jt2 < 2; ++jt2) {
-        const uint32_t w0 = pack_f16x2(S[jt2][4 * g4 + 0], S[jt2][4 * g4 + 1]);
-        const uint32_t w1 = pack_f16x2(S[jt2][4 * g4 + 2], S[jt2][4 * g4 + 3]);
-        *reinterpret_cast<uint2 *>(ST0 + o256(32 * jt2 + l32, d * 2)) = make_uint2(w0, w1);
-      }
-      if (l32 == 0) {
-        const uint32_t z0 = pack_f16x2(Z[4 * g4 + 0] * 0.00390625f, Z[4 * g4 + 1] * 0.00390625f);
-        const uint32_t z1 = pack_f16x2(Z[4 * g4 + 2] * 0.00390625f, Z[4 * g4 + 3] * 0.00390625f);
-        *(__attribute__((address_space(3))) uint2 *)(Z0 + d * 2) = make_uint2(z0, z1);
-      }
-    }
-  }
+  const Stage s0{K0, V0, ST0, Z0}, s1{K1, V1, ST1, Z1};
+  if (!qwave) write_state(s0, wave - 4);  // initial S^T and z / 256
   Raw ra{}, rb{};
   load_raw(ra, 0);
   load_raw(rb, min(1, nchunks - 1));
+  if (qwave) make_qf(ra);
   stage_in(ra, s0);
   __syncthreads();
   // iteration c: fetch chunk c + 2, compute chunk c, stage chunk c + 1.  The
@@ -435,38 +428,47 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
   // the staging writes it into the idle stage, which nothing reads), so the
   // loop body is straight-line code and the compiler's vmcnt waits only cover
   // the registers being staged, not the fetch just issued.
-  int c = 0;
-  for (; c + 2 <= nchunks; c += 2) {
-    load_raw(ra, min(c + 2, nchunks - 1));
-    chunk(s0, s1, c, rb);
-    __syncthreads();
-    load_raw(rb, min(c + 3, nchunks - 1));
-    chunk(s1, s0, c + 1, ra);
-    __syncthreads();
+  auto run = [&](auto rtag) __attribute__((always_inline)) {
+    int c = 0;
+    for (; c + 2 <= nchunks; c += 2) {
+      load_raw(ra, min(c + 2, nchunks - 1));
+      chunk(s0, s1, c, rb, rtag);
+      __syncthreads();
+      load_raw(rb, min(c + 3, nchunks - 1));
+      chunk(s1, s0, c + 1, ra, rtag);
+      __syncthreads();
+    }
+    if (c < nchunks) chunk(s0, s1, c, rb, rtag);
+  };
+  switch (wave) {
+    case 0: run(Int<0>{}); break;
+    case 1: run(Int<1>{}); break;
+    case 2: run(Int<2>{}); break;
+    case 3: run(Int<3>{}); break;
+    default: run(Int<4>{}); break;
   }
-  if (c < nchunks) chunk(s0, s1, c, rb);
 }
 
 // Partial states of ranges of rchunks chunks (the prefix of later segments):
-// one workgroup (4 waves) per (sequence, range, d_v half); wave w owns state
-// rows d = 32w..32w+31.  Per chunk: phi(K) and the V half are staged in LDS
-// (fp16, the layouts of the scan kernel) and S += phi(K)^T V, z += phi(K)^T 1
-// accumulate in the MFMA accumulators; the sums go out in fp32.
-extern "C" __global__ __launch_bounds__(256, 2) void nk_linattn_state_c64_d128(LinAttnStateArgs a) {
+// one workgroup (8 waves) per (sequence, range); wave w owns state rows
+// d = 32 (w % 4).. and the d_v columns 64 (w / 4)...  Per chunk: phi(K) and V
+// are staged in LDS (fp16, the layouts of the scan kernel) and
+// S += phi(K)^T V, z += phi(K)^T 1 accumulate in the MFMA accumulators; the
+// sums go out in fp32.
+extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_state_c64_d128(LinAttnStateArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t KS[2][LC * 256];
-  __shared__ __attribute__((aligned(1024))) uint8_t VS[2][LC * 128];
+  __shared__ __attribute__((aligned(1024))) uint8_t VS[2][LC * 256];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, grp = lane >> 4;
   const int l32 = lane & 31, lhi = lane >> 5;
+  const int wd = wave & 3, half = wave >> 2;
 
-  const int id = blockIdx.x;
-  const int half = id & 1;
-  const int64_t rr = (id >> 1) % a.nranges;
-  const int64_t bh = (id >> 1) / a.nranges;
-  const int j0 = half * LS;
+  const int64_t unit = blockIdx.x;
+  const int64_t rr = unit % a.nranges;
+  const int64_t bh = unit / a.nranges;
   const int64_t base = bh * a.T * LD + rr * a.rchunks * LC * LD;
 
   f32x16 S[2], Z;
@@ -480,55 +482,53 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_linattn_state_c64_d128(L
 #pragma unroll
   for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
 
-  // thread -> k rows tid/16 + 16 i (i < 4), 8 columns at 8 (tid % 16); v
-  // rows tid/8 + 32 i (i < 2), 8 columns j0 + 8 (tid % 8)
-  auto load = [&](uint4 (&kr)[4], uint4 (&vr)[2], int c) {
+  // thread -> k and v chunks tid + 512 i (row / 16, 8 columns at 8 (% 16))
+  auto load = [&](uint4 (&kr)[2], uint4 (&vr)[2], int c) {
     const int64_t cb = base + (int64_t)c * LC * LD;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      kr[i] = *reinterpret_cast<const uint4 *>(a.k + cb + ((tid >> 4) + 16 * i) * LD + (tid & 15) * 8);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-      vr[i] = *reinterpret_cast<const uint4 *>(a.v + cb + ((tid >> 3) + 32 * i) * LDV + j0 + (tid & 7) * 8);
+    for (int i = 0; i < 2; ++i) {
+      const int idx = tid + 512 * i;
+      kr[i] = *reinterpret_cast<const uint4 *>(a.k + cb + (idx >> 4) * LD + (idx & 15) * 8);
+      vr[i] = *reinterpret_cast<const uint4 *>(a.v + cb + (idx >> 4) * LDV + (idx & 15) * 8);
+    }
   };
-  auto stage = [&](const uint4 (&kr)[4], const uint4 (&vr)[2], int b) {
+  auto stage = [&](const uint4 (&kr)[2], const uint4 (&vr)[2], int b) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<uint4 *>(KS[b] + o256((tid >> 4) + 16 * i, (tid & 15) * 16)) = phi8(kr[i]);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-      *reinterpret_cast<uint4 *>(VS[b] + ((tid >> 2) & 1) * 4096 + o64((tid >> 3) + 32 * i, (tid & 3) * 16)) =
-          to_f16x8(vr[i]);
+    for (int i = 0; i < 2; ++i) {
+      const int idx = tid + 512 * i;
+      *reinterpret_cast<uint4 *>(KS[b] + o256(idx >> 4, (idx & 15) * 16)) = phi8(kr[i]);
+      *reinterpret_cast<uint4 *>(VS[b] + voff(idx)) = to_f16x8(vr[i]);
+    }
   };
   auto update = [&](int b) {
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const int kb = 16 * st + 8 * (grp >> 1) + (l16 >> 2);
-      const int db = (32 * wave + 16 * (grp & 1) + 4 * (l16 & 3)) * 2;
+      const int db = (32 * wd + 16 * (grp & 1) + 4 * (l16 & 3)) * 2;
       const int jb = (16 * (grp & 1) + 4 * (l16 & 3)) * 2;
       const f16x8_t kf = cat(tr_read(KS[b] + o256(kb, db)), tr_read(KS[b] + o256(kb + 4, db)));
 #pragma unroll
-      for (int jt2 = 0; jt2 < 2; ++jt2) {
-        const uint8_t *vt = VS[b] + jt2 * 4096;
+      for (int t = 0; t < 2; ++t) {
+        const uint8_t *vt = VS[b] + (2 * half + t) * 4096;
         const f16x8_t vf = cat(tr_read(vt + o64(kb, jb)), tr_read(vt + o64(kb + 4, jb)));
-        S[jt2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, vf, S[jt2], 0, 0, 0);
+        S[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, vf, S[t], 0, 0, 0);
       }
-      Z = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ones, Z, 0, 0, 0);
+      if (half == 0) Z = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ones, Z, 0, 0, 0);
     }
   };
 
-  uint4 ka[4], va[2], kb4[4], vb[2];
+  uint4 ka[2], va[2], kb2[2], vb[2];
   load(ka, va, 0);
-  load(kb4, vb, min(1, a.rchunks - 1));
+  load(kb2, vb, min(1, a.rchunks - 1));
   stage(ka, va, 0);
   __syncthreads();
   int c = 0;
   for (; c + 2 <= a.rchunks; c += 2) {
     load(ka, va, min(c + 2, a.rchunks - 1));
     update(0);
-    stage(kb4, vb, 1);
+    stage(kb2, vb, 1);
     __syncthreads();
-    load(kb4, vb, min(c + 3, a.rchunks - 1));
+    load(kb2, vb, min(c + 3, a.rchunks - 1));
     update(1);
     stage(ka, va, 0);
     __syncthreads();
@@ -538,9 +538,9 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_linattn_state_c64_d128(L
   float *out = a.part + (bh * a.nranges + rr) * (int64_t)(LD + 1) * LDV;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const int d = 32 * wave + 8 * (r >> 2) + 4 * lhi + (r & 3);
-    out[(int64_t)d * LDV + j0 + l32] = S[0][r];
-    out[(int64_t)d * LDV + j0 + 32 + l32] = S[1][r];
+    const int d = 32 * wd + 8 * (r >> 2) + 4 * lhi + (r & 3);
+    out[(int64_t)d * LDV + 64 * half + l32] = S[0][r];
+    out[(int64_t)d * LDV + 64 * half + 32 + l32] = S[1][r];
     if (half == 0 && l32 == 0) out[(int64_t)LD * LDV + d] = Z[r];
   }
 }

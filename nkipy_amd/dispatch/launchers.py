@@ -323,8 +323,6 @@ class LinAttnStateArgs(ctypes.Structure):
 
 LINATTN_CHUNK = 64
 LINATTN_D = 128
-# workgroups per (sequence, segment): two 64-column halves of d_v
-LINATTN_HALVES = 2
 # the scan is serial over a sequence's chunks; with fewer than this many
 # workgroups the sequence is cut into segments whose prefix states come from
 # a separate partial-sum kernel
@@ -336,11 +334,13 @@ def linear_attention_split(BH: int, T: int):
     linear-attention scan of BH sequences of length T."""
     nchunks = T // LINATTN_CHUNK
     nseg = 1
-    while (BH * LINATTN_HALVES * nseg < LINATTN_TARGET_WGS and nchunks % (2 * nseg) == 0
+    while (BH * nseg < LINATTN_TARGET_WGS and nchunks % (2 * nseg) == 0
            and nchunks // (2 * nseg) >= 8):
         nseg *= 2
     cs = nchunks // nseg
-    rchunks = cs // 4 if cs % 4 == 0 else cs
+    # one partial sum per earlier segment when that already gives the
+    # partial-sum kernel a workgroup per CU or so; else quarter ranges
+    rchunks = cs if BH * (nseg - 1) >= LINATTN_TARGET_WGS // 2 or cs % 4 else cs // 4
     nranges = (nseg - 1) * (cs // rchunks)
     return nseg, rchunks, nranges
 
@@ -369,7 +369,7 @@ def linear_attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, BH: int, T:
     if any(p % 16 for p in (q_ptr, k_ptr, v_ptr, o_ptr)):
         raise LaunchError("linear attention operands must be 16-byte aligned")
     nseg, rchunks, nranges = linear_attention_split(BH, T)
-    if BH * nseg * LINATTN_HALVES >= 2**31 or BH * max(nranges, 1) * LINATTN_HALVES >= 2**31:
+    if BH * nseg >= 2**31 or BH * max(nranges, 1) >= 2**31:
         raise LaunchError("linear attention grid too large")
     if nranges and not part_ptr:
         raise LaunchError(f"linear attention of {BH} x {T} runs in {nseg} segments and needs a "
@@ -380,11 +380,11 @@ def linear_attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, BH: int, T:
     flops_chunk = 2 * chunk * chunk * D + 2 * chunk * D * Dv + 2 * chunk * chunk * Dv + 2 * D * Dv * chunk
     launches = []
     if nranges:
-        launches.append(Launch("linattn", "nk_linattn_state_c64_d128", (BH * nranges * LINATTN_HALVES, 1, 1),
-                               (256, 1, 1), LinAttnStateArgs(k_ptr, v_ptr, part_ptr, BH, T, nranges, rchunks),
+        launches.append(Launch("linattn", "nk_linattn_state_c64_d128", (BH * nranges, 1, 1),
+                               (512, 1, 1), LinAttnStateArgs(k_ptr, v_ptr, part_ptr, BH, T, nranges, rchunks),
                                bytes=2 * BH * nranges * rchunks * chunk * D * 2,
                                flops=BH * nranges * rchunks * 2 * chunk * D * Dv))
-    launches.append(Launch("linattn", "nk_linattn_c64_d128", (BH * nseg * LINATTN_HALVES, 1, 1), (512, 1, 1),
+    launches.append(Launch("linattn", "nk_linattn_c64_d128", (BH * nseg, 1, 1), (512, 1, 1),
                            LinAttnArgs(q_ptr, k_ptr, v_ptr, o_ptr, part_ptr or None, BH, T, nseg, rchunks),
                            bytes=4 * BH * T * D * 2, flops=BH * n * flops_chunk))
     return launches
