@@ -12,8 +12,15 @@
 // DeltaNet kernel, examples/linear_attention/deltanet.py:74-128).
 //
 // Layout: q, k, v, o are (B*H, T, 128) row-major bf16.  One workgroup of 8
-// waves owns one (b, h) sequence and a 32-column slice j0.. of d_v; the four
-// slices of a head run as four workgroups placed on one XCD (shared L2).
+// waves owns one segment of one (b, h) sequence and all 128 columns of d_v,
+// so phi of every q / k element is evaluated once.  The scan is serial over
+// a segment's chunks; a sequence is cut into nseg segments (chosen by the
+// launcher so that the grid fills the GPU), and a segment starts from the
+// state S, z at its first token: the sum of fp32 partial states over ranges
+// of the earlier segments, written beforehand by nk_linattn_state_c64_d128
+// (one workgroup per (sequence, range), the state-update half of the scan
+// without queries).  That kernel re-reads those k / v, the price of the
+// parallelism.
 //
 // Per chunk, query wave w (0..3) owns queries 16w..16w+15 and state wave w
 // (4..7) owns state rows d = 32(w-4)..+31; two waves share each SIMD, so one
@@ -21,20 +28,23 @@
 // form so that every lane owns one query column:
 //   A^T = phi(K) phi(Q_w)^T            16x16x32 MFMA, key tiles 0..w, causal
 //                                       mask on the diagonal tile
-//   O^T = S_{c-1}^T phi(Q_w)^T + V^T A^T   (32 j x 16 queries); A^T enters
+//   O^T = S_{c-1}^T phi(Q_w)^T + V^T A^T   (128 j x 16 queries); A^T enters
 //                                       the second product straight from its
 //                                       accumulators, V^T fragments follow
 //                                       its key order (ds_read_b64_tr_b16)
-//   den = rowsum(A^T) (lane-local) + phi(Q_w) z_{c-1} (VALU dot)
+//   den                                 a ninth output tile of the same MFMAs
+//                                       (row 0 of its A operand: z / 256 and
+//                                       1/256)
 //   S[d-slice] += phi(K)^T V           32x32x16 MFMA, K^T and V fragments by
 //                                       transpose reads; z from the same MFMA
 //                                       against an all-ones B operand
 // The output rows are normalised and stored (8-byte stores) by the wave that
 // owns them; the new state's fp16 copy S^T and z go to the other LDS buffer
-// for the next chunk.  phi of the next chunk (the VALU-bound part: one exp
-// per element) is computed between this chunk's MFMAs and the barrier, from
-// q / k / v fetched two chunks ahead into registers, so that it overlaps the
-// MFMAs.  One barrier per chunk.
+// for the next chunk.  Each query wave keeps phi(Q) of its own rows in
+// registers (no LDS); the state waves stage phi(K) and everyone stages V
+// into LDS, from q / k / v fetched two chunks ahead into registers, so that
+// the VALU-bound phi (one exp per element) overlaps the MFMAs.  One barrier
+// per chunk.
 //
 // MFMA operands are fp16, not bf16: phi(x) = 1 + x + ... for the small inputs
 // of attention, so the information sits in deviations from 1 and in

@@ -338,9 +338,15 @@ def linear_attention_split(BH: int, T: int):
            and nchunks // (2 * nseg) >= 8):
         nseg *= 2
     cs = nchunks // nseg
-    # one partial sum per earlier segment when that already gives the
-    # partial-sum kernel a workgroup per CU or so; else quarter ranges
-    rchunks = cs if BH * (nseg - 1) >= LINATTN_TARGET_WGS // 2 or cs % 4 else cs // 4
+    # two partial sums per earlier segment when that gives the partial-sum
+    # kernel a workgroup per CU or more (measured best at the 64 x 8192
+    # configuration), else quarter ranges
+    if cs % 4:
+        rchunks = cs
+    elif BH * (nseg - 1) * 2 >= LINATTN_TARGET_WGS:
+        rchunks = cs // 2
+    else:
+        rchunks = cs // 4
     nranges = (nseg - 1) * (cs // rchunks)
     return nseg, rchunks, nranges
 
