@@ -32,6 +32,7 @@ using namespace nk;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 #define BM 256
@@ -151,18 +152,19 @@ __device__ __forceinline__ uint32_t dma_off(uint32_t base, int64_t k0, int kidx,
 }
 
 // A tile (and a bf16 B^T tile): 256 rows x 64 bf16 = 128-byte rows, 16-byte
-// chunks stored at chunk ^ swz(row).  Wave w moves blocks b = 4 j + w of
-// 8 rows; lane l fills stored slot (row, l % 8), so it fetches logical chunk
-// (l % 8) ^ swz(row) -- the same chunk for every j, since swz(row) only
-// depends on (4 w + l / 16) mod 8.
-__device__ __forceinline__ DmaPlan<8> plan_rows_bf16(bool split, int64_t r_first, int64_t nrows, int64_t ld,
-                                                     int wave, int lane) {
-  DmaPlan<8> p;
+// chunks stored at chunk ^ swz(row).  With NW waves, wave w moves blocks
+// b = NW j + w of 8 rows; lane l fills stored slot (row, l % 8), so it fetches
+// logical chunk (l % 8) ^ swz(row) -- the same chunk for every j, since
+// swz(row) only depends on (4 b + l / 16) mod 8 and b = w mod 2.
+template <int NW>
+__device__ __forceinline__ DmaPlan<32 / NW> plan_rows_bf16(bool split, int64_t r_first, int64_t nrows, int64_t ld,
+                                                           int wave, int lane) {
+  DmaPlan<32 / NW> p;
   const int lc = (lane & 7) ^ swz(wave * 8 + (lane >> 3), 0);  // row of move j = 0
   p.kofs = lc * 8;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int b = j * 4 + wave;
+  for (int j = 0; j < 32 / NW; ++j) {
+    const int b = j * NW + wave;
     const int row = b * 8 + (lane >> 3);
     const int64_t rr = r_first + ((split && b >= 16) ? row - 128 : row);
     p.base[j] = rr < nrows ? (uint32_t)((rr * ld + p.kofs) * 2) : OOB;
@@ -170,12 +172,13 @@ __device__ __forceinline__ DmaPlan<8> plan_rows_bf16(bool split, int64_t r_first
   return p;
 }
 
-__device__ __forceinline__ void dma_rows_bf16(const DmaPlan<8> &p, __amdgpu_buffer_rsrc_t r0,
+template <int NW>
+__device__ __forceinline__ void dma_rows_bf16(const DmaPlan<32 / NW> &p, __amdgpu_buffer_rsrc_t r0,
                                               __amdgpu_buffer_rsrc_t r1, bool split, uint8_t *S, int64_t k0,
                                               int64_t K, int wave) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int b = j * 4 + wave;
+  for (int j = 0; j < 32 / NW; ++j) {
+    const int b = j * NW + wave;
     dma16((split && b >= 16) ? r1 : r0, S + b * 1024, dma_off(p.base[j], k0, p.kofs, K, 2));
   }
 }
@@ -184,14 +187,15 @@ __device__ __forceinline__ void dma_rows_bf16(const DmaPlan<8> &p, __amdgpu_buff
 // chunks stored at chunk ^ ((row >> 2) & 3).  Blocks of 16 rows.
 __device__ __forceinline__ int swz8(int row) { return (row >> 2) & 3; }
 
-__device__ __forceinline__ DmaPlan<4> plan_rows_fp8(bool split, int64_t r_first, int64_t nrows, int64_t ld,
-                                                    int wave, int lane) {
-  DmaPlan<4> p;
+template <int NW>
+__device__ __forceinline__ DmaPlan<16 / NW> plan_rows_fp8(bool split, int64_t r_first, int64_t nrows, int64_t ld,
+                                                          int wave, int lane) {
+  DmaPlan<16 / NW> p;
   const int lc = (lane & 3) ^ swz8(wave * 16 + (lane >> 2));  // row of move j = 0
   p.kofs = lc * 16;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int b = j * 4 + wave;
+  for (int j = 0; j < 16 / NW; ++j) {
+    const int b = j * NW + wave;
     const int row = b * 16 + (lane >> 2);
     const int64_t rr = r_first + ((split && b >= 8) ? row - 128 : row);
     p.base[j] = rr < nrows ? (uint32_t)(rr * ld + p.kofs) : OOB;
@@ -199,12 +203,13 @@ __device__ __forceinline__ DmaPlan<4> plan_rows_fp8(bool split, int64_t r_first,
   return p;
 }
 
-__device__ __forceinline__ void dma_rows_fp8(const DmaPlan<4> &p, __amdgpu_buffer_rsrc_t r0,
+template <int NW>
+__device__ __forceinline__ void dma_rows_fp8(const DmaPlan<16 / NW> &p, __amdgpu_buffer_rsrc_t r0,
                                              __amdgpu_buffer_rsrc_t r1, bool split, uint8_t *S, int64_t k0,
                                              int64_t K, int wave) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int b = j * 4 + wave;
+  for (int j = 0; j < 16 / NW; ++j) {
+    const int b = j * NW + wave;
     dma16((split && b >= 8) ? r1 : r0, S + b * 1024, dma_off(p.base[j], k0, p.kofs, K, 1));
   }
 }
@@ -213,20 +218,22 @@ __device__ __forceinline__ void dma_rows_fp8(const DmaPlan<4> &p, __amdgpu_buffe
 // [64 k][128 n] with 256-byte rows (half 0 = tile columns 0..127, half 1 =
 // 128..255; in SwiGLU mode gate and up), 16-byte chunks at chunk ^ nnswz(k).
 // MFMA fragments are read with ds_read_b64_tr_b16 (below).  Blocks of 4 rows;
-// move j covers k row ((4 j + w) mod 16) * 4 + l / 16.
+// block b = NW j + w covers k rows (b mod 16) * 4 + l / 16 of half b / 16.
 __device__ __forceinline__ int nnswz(int k) { return (k & 3) << 2; }
 
-__device__ __forceinline__ int nn_krow(int j, int wave, int lane) { return ((j * 4 + wave) & 15) * 4 + (lane >> 4); }
+template <int NW>
+__device__ __forceinline__ int nn_krow(int j, int wave, int lane) { return ((j * NW + wave) & 15) * 4 + (lane >> 4); }
 
-__device__ __forceinline__ DmaPlan<8> plan_nn_bf16(bool split, int64_t n0, int64_t N, int64_t ld, int wave,
-                                                   int lane) {
-  DmaPlan<8> p;
+template <int NW>
+__device__ __forceinline__ DmaPlan<32 / NW> plan_nn_bf16(bool split, int64_t n0, int64_t N, int64_t ld, int wave,
+                                                         int lane) {
+  DmaPlan<32 / NW> p;
   p.kofs = 0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int b = j * 4 + wave;
+  for (int j = 0; j < 32 / NW; ++j) {
+    const int b = j * NW + wave;
     const int half = b >> 4;
-    const int k = nn_krow(j, wave, lane);
+    const int k = nn_krow<NW>(j, wave, lane);
     const int lc = (lane & 15) ^ nnswz(k);
     const int64_t col = n0 + (split ? 0 : half * 128) + lc * 8;
     p.base[j] = col < N ? (uint32_t)((k * ld + col) * 2) : OOB;
@@ -234,14 +241,15 @@ __device__ __forceinline__ DmaPlan<8> plan_nn_bf16(bool split, int64_t n0, int64
   return p;
 }
 
-__device__ __forceinline__ void dma_nn_bf16(const DmaPlan<8> &p, __amdgpu_buffer_rsrc_t r0,
+template <int NW>
+__device__ __forceinline__ void dma_nn_bf16(const DmaPlan<32 / NW> &p, __amdgpu_buffer_rsrc_t r0,
                                             __amdgpu_buffer_rsrc_t r1, bool split, uint8_t *S, int64_t k0,
                                             int64_t K, int64_t ld, int wave, int lane) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int b = j * 4 + wave;
+  for (int j = 0; j < 32 / NW; ++j) {
+    const int b = j * NW + wave;
     dma16((split && (b >> 4)) ? r1 : r0, S + b * 1024,
-          dma_off(p.base[j], k0, nn_krow(j, wave, lane), K, ld * 2));
+          dma_off(p.base[j], k0, nn_krow<NW>(j, wave, lane), K, ld * 2));
   }
 }
 
@@ -322,15 +330,17 @@ enum BMode { B_T16 = 0, B_T8 = 1, B_NN16 = 2 };
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-template <int BM_>
-__device__ __forceinline__ void read_frags(bf16x8_t (&af)[4], bf16x8_t (&bf)[4], const uint8_t *As,
-                                           const uint8_t *Bs, int kk, int wm, const int (&brow)[4],
+// Fragments of k16 step kk: NA A tiles (rows arow0 + 32 i ..) and the four
+// B tiles of brow.
+template <int BM_, int NA>
+__device__ __forceinline__ void read_frags(bf16x8_t (&af)[NA], bf16x8_t (&bf)[4], const uint8_t *As,
+                                           const uint8_t *Bs, int kk, int arow0, const int (&brow)[4],
                                            int lane) {
   const int l32 = lane & 31, lhi = lane >> 5;
   const int chunk = kk * 2 + lhi;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = wm * 128 + i * 32 + l32;
+  for (int i = 0; i < NA; ++i) {
+    const int row = arow0 + i * 32 + l32;
     af[i] = *reinterpret_cast<const bf16x8_t *>(As + row * 128 + swz(row, chunk) * 16);
   }
 #pragma unroll
@@ -367,10 +377,11 @@ template <int BM_>
 __device__ __forceinline__ void mma_tile(f32x16 (&acc)[4][4], const uint8_t *As, const uint8_t *Bs, int wm,
                                          const int (&brow)[4], int lane) {
   bf16x8_t af[2][4], bf[2][4];
-  read_frags<BM_>(af[0], bf[0], As, Bs, 0, wm, brow, lane);
+  read_frags<BM_, 4>(af[0], bf[0], As, Bs, 0, wm * 128, brow, lane);
 #pragma unroll
   for (int kk = 0; kk < BK / 16; ++kk) {
-    if (kk + 1 < BK / 16) read_frags<BM_>(af[(kk + 1) & 1], bf[(kk + 1) & 1], As, Bs, kk + 1, wm, brow, lane);
+    if (kk + 1 < BK / 16)
+      read_frags<BM_, 4>(af[(kk + 1) & 1], bf[(kk + 1) & 1], As, Bs, kk + 1, wm * 128, brow, lane);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -399,6 +410,119 @@ __device__ __forceinline__ void schedule_ktile() {
   }
 }
 
+// Epilogue.  The MFMAs computed C^T tiles (B fragment as the A operand), so
+// a lane holds row rbase + 32 i + l32 of C and, per tile, 16 columns
+// n = (tile column) + 8 q + 4 lhi + e (q, e = 0..3): runs of 4 consecutive
+// columns, stored / read as one vector.
+template <bool SWIGLU, typename TC, int NA>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs &a, const f32x16 (&acc)[NA][4], int64_t rbase,
+                                              int64_t n0, int wn, int lane) {
+  const int l32 = lane & 31, lhi = lane >> 5;
+  const bool vec = (a.flags & GEMM_VEC) != 0;
+  auto put4 = [&](int64_t row, int64_t col, const float (&v)[4]) {
+    if (vec && col + 3 < a.N) {
+      OutT<TC>::store4(a.C, row * a.ldc + col, v);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (col + e < a.N) OutT<TC>::store(a.C, row * a.ldc + col + e, v[e]);
+    }
+  };
+  if (SWIGLU) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t nb = n0 + wn * 64 + j * 32 + lhi * 4;
+      float sg[16], su[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t col = nb + q * 8 + e;
+          const bool in = (a.flags & GEMM_SCALE) && col < a.N;
+          sg[q * 4 + e] = in ? a.scale0[col] : 1.f;
+          su[q * 4 + e] = in ? a.scale1[col] : 1.f;
+        }
+#pragma unroll
+      for (int i = 0; i < NA; ++i) {
+        const int64_t row = rbase + i * 32 + l32;
+        if (row >= a.M) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t col = nb + q * 8;
+          if (col >= a.N) continue;
+          float h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float g = acc[i][j][q * 4 + e] * sg[q * 4 + e];
+            const float u = acc[i][j + 2][q * 4 + e] * su[q * 4 + e];
+            // silu(g) = g / (1 + exp(-g)) from the hardware 2^x and
+            // reciprocal (about 2 ulp in fp32, far below the bf16 output
+            // rounding); the accurate expf / division sequences would keep
+            // the MFMA pipe idle for ~10% of a K = 4096 tile
+            const float ex = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+            h[e] = g * __builtin_amdgcn_rcpf(1.0f + ex) * u;
+          }
+          put4(row, col, h);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t nb = n0 + wn * 128 + j * 32 + lhi * 4;
+      float sc[16], bi[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t col = nb + q * 8 + e;
+          sc[q * 4 + e] = ((a.flags & GEMM_SCALE) && col < a.N) ? a.scale0[col] : 1.f;
+          bi[q * 4 + e] = ((a.flags & GEMM_BIAS) && col < a.N)
+                              ? bf16_to_f32(reinterpret_cast<const uint16_t *>(a.bias)[col]) : 0.f;
+        }
+#pragma unroll
+      for (int i = 0; i < NA; ++i) {
+        const int64_t row = rbase + i * 32 + l32;
+        if (row >= a.M) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t col = nb + q * 8;
+          if (col >= a.N) continue;
+          float r4[4] = {0.f, 0.f, 0.f, 0.f};
+          if (a.flags & GEMM_RESID) {
+            if (vec && col + 3 < a.N) {
+              OutT<TC>::load4(a.resid, row * a.ldc + col, r4);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (col + e < a.N) r4[e] = OutT<TC>::load(a.resid, row * a.ldc + col + e);
+            }
+          }
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = acc[i][j][q * 4 + e] * sc[q * 4 + e] + bi[q * 4 + e] + r4[e];
+          put4(row, col, v);
+        }
+      }
+    }
+  }
+}
+
+// Output tile of this workgroup, XCD aware: consecutive workgroup ids are
+// dealt to the 8 XCDs round robin, so ids are remapped so that each XCD
+// receives a contiguous run of tiles, walked in groups of GROUP_M tile rows.
+__device__ __forceinline__ void gemm_tile(const GemmArgs &a, int &tm, int &tn) {
+  const int ntiles = a.tiles_m * a.tiles_n;
+  int pid = blockIdx.x;
+  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+  const int in_group = GROUP_M * a.tiles_n;
+  const int group = pid / in_group;
+  const int first_m = group * GROUP_M;
+  const int gsize = min(a.tiles_m - first_m, GROUP_M);
+  tm = first_m + (pid % in_group) % gsize;
+  tn = (pid % in_group) / gsize;
+}
+
 // ---------------------------------------------------------------------------
 // main kernel
 // ---------------------------------------------------------------------------
@@ -410,16 +534,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
   constexpr bool REG_B = !NT && FP8;
   constexpr int BROW = BMODE == B_T8 ? 64 : 128;  // bytes per B row in LDS
 
-  // XCD-aware tile order
-  const int ntiles = a.tiles_m * a.tiles_n;
-  int pid = blockIdx.x;
-  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
-  const int in_group = GROUP_M * a.tiles_n;
-  const int group = pid / in_group;
-  const int first_m = group * GROUP_M;
-  const int gsize = min(a.tiles_m - first_m, GROUP_M);
-  const int tm = first_m + (pid % in_group) % gsize;
-  const int tn = (pid % in_group) / gsize;
+  int tm, tn;
+  gemm_tile(a, tm, tn);
   const int64_t m0 = (int64_t)tm * BM;
   const int64_t n0 = (int64_t)tn * (SWIGLU ? BN / 2 : BN);
 
@@ -449,23 +565,23 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
   const __amdgpu_buffer_rsrc_t rb1 = make_rsrc(SWIGLU ? a.B1 : a.B0, brows * a.ldb * bsz);
 
   StageNN sn;
-  const DmaPlan<8> pa = plan_rows_bf16(false, m0, a.M, a.lda, wave, lane);
+  const DmaPlan<8> pa = plan_rows_bf16<4>(false, m0, a.M, a.lda, wave, lane);
   DmaPlan<8> pb16;
   DmaPlan<4> pb8;
-  if (NT && FP8) pb8 = plan_rows_fp8(SWIGLU, n0, a.N, a.ldb, wave, lane);
-  if (NT && !FP8) pb16 = plan_rows_bf16(SWIGLU, n0, a.N, a.ldb, wave, lane);
-  if (!NT && !FP8) pb16 = plan_nn_bf16(SWIGLU, n0, a.N, a.ldb, wave, lane);
-  auto issue_a = [&](uint8_t *As, int64_t k0) { dma_rows_bf16(pa, ra, ra, false, As, k0, a.K, wave); };
+  if (NT && FP8) pb8 = plan_rows_fp8<4>(SWIGLU, n0, a.N, a.ldb, wave, lane);
+  if (NT && !FP8) pb16 = plan_rows_bf16<4>(SWIGLU, n0, a.N, a.ldb, wave, lane);
+  if (!NT && !FP8) pb16 = plan_nn_bf16<4>(SWIGLU, n0, a.N, a.ldb, wave, lane);
+  auto issue_a = [&](uint8_t *As, int64_t k0) { dma_rows_bf16<4>(pa, ra, ra, false, As, k0, a.K, wave); };
   auto issue_b = [&](uint8_t *Bs, int64_t k0) {
     if (NT) {
       if (FP8)
-        dma_rows_fp8(pb8, rb0, rb1, SWIGLU, Bs, k0, a.K, wave);
+        dma_rows_fp8<4>(pb8, rb0, rb1, SWIGLU, Bs, k0, a.K, wave);
       else
-        dma_rows_bf16(pb16, rb0, rb1, SWIGLU, Bs, k0, a.K, wave);
+        dma_rows_bf16<4>(pb16, rb0, rb1, SWIGLU, Bs, k0, a.K, wave);
     } else if (REG_B) {
       load_nn<FP8, SWIGLU>(sn, a, rb0, rb1, n0, k0);
     } else {
-      dma_nn_bf16(pb16, rb0, rb1, SWIGLU, Bs, k0, a.K, a.ldb, wave, lane);
+      dma_nn_bf16<4>(pb16, rb0, rb1, SWIGLU, Bs, k0, a.K, a.ldb, wave, lane);
     }
   };
   auto issue = [&](uint8_t *As, uint8_t *Bs, int64_t k0) {
@@ -590,11 +706,56 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
     if (t < ktiles) mma_tile<BMODE>(acc, A0, B0, wm, brow, lane);
   }
 
-  // epilogue.  The MFMAs computed C^T tiles (B fragment as the A operand),
-  // so a lane holds row m = m0 + wm*128 + i*32 + l32 of C and, per tile,
-  // 16 columns n = (tile column) + 8 q + 4 lhi + e (q, e = 0..3): runs of 4
-  // consecutive columns, stored / read as one vector.
-  const int l32 = lane & 31, lhi = lane >> 5;
+  gemm_epilogue<SWIGLU, TC, 4>(a, acc, m0 + wm * 128, n0, wn, lane);
+}
+
+template <int N> struct Int {
+  static constexpr int value = N;
+};
+
+// ---------------------------------------------------------------------------
+// 8-wave ping-pong kernel (NT weights, and bf16 NN weights; the default)
+// ---------------------------------------------------------------------------
+// Same 256 x 256 output tiles, 512 threads: wave w sits on SIMD w % 4, so each
+// SIMD hosts one wave of group 0 (waves 0..3, output rows 0..127 of the
+// tile) and one of group 1 (waves 4..7, rows 128..255); each wave owns 64
+// rows x 128 B^T rows (4 x 8 tiles of v_mfma_f32_16x16x32_bf16, which
+// sustains a higher rate than the 32x32x16 form on random operands; 128
+// accumulators).  K advances in phases of 32 (one MFMA k step); phase p is
+// computed by group 0 in slot 2p and by group 1 in slot 2p + 1, slots being
+// separated by workgroup barriers, and each group reads (and, for fp8,
+// decodes) a phase's fragments from LDS into registers in the slot before it
+// computes it:
+//   slot 2p:     group 0 computes phase p,  group 1 loads phase p
+//   slot 2p + 1: group 1 computes phase p,  group 0 loads phase p + 1
+// so the matrix pipe of a SIMD is fed alternately by its two waves and the
+// barrier of one slot is covered by the MFMAs the other wave has queued.
+// LDS holds a ring of R half-tile stages (A 256 x 32 bf16, B 256 x 32 bf16
+// or fp8): the stage of phase p is free once slot 2p ends, so in slot 2p + 1
+// the DMAs of phase p + R go into it; before the barrier that closes slot 2p
+// each wave waits until its DMAs of phase p + 1 have landed (all but the
+// R - 2 newest phases), which leaves 2R - 2 slots for a DMA to arrive.  The
+// DMAs are issued from inline asm: the compiler does not track them, so it
+// adds no waits of its own (its tracking of LDS DMA targets is lost across
+// the loop's back edge, and its waits then drain the whole ring); every
+// ordering is the explicit vmcnt / lgkmcnt / barrier above.
+//
+// Half-tile layouts (16-byte chunks XOR-swizzled by row, conflict-free for
+// the fragment reads below):
+//   A, bf16 B^T: 256 rows x 64 bytes, chunk c (k 8c..8c+7) at c ^ hswz(row)
+//   fp8 B^T:     256 rows x 32 bytes, chunk c (k 16c..) at c ^ hswz8(row)
+//   NN bf16 B:   [2 column halves][32 k][256 bytes], chunk at c ^ nnswz(k)
+__device__ __forceinline__ int hswz(int row) { return (row >> 2) & 3; }
+__device__ __forceinline__ int hswz8(int row) { return (row >> 3) & 1; }
+
+// Epilogue of the 16x16 tiles of the 8-wave kernel: lane (g, i) holds, per
+// tile (i', j), output row rbase + 16 i' + i and the 4 consecutive columns
+// cbase + 16 j + 4 g + 0..3 (SwiGLU: tiles j < 4 gate and j + 4 up of the
+// same output columns cbase + 16 j + ..).
+template <bool SWIGLU, typename TC, int NI>
+__device__ __forceinline__ void gemm_epilogue16(const GemmArgs &a, const f32x4 (&acc)[NI][8], int64_t rbase,
+                                                int64_t cbase, int lane) {
+  const int l16 = lane & 15, g4 = lane >> 4;
   const bool vec = (a.flags & GEMM_VEC) != 0;
   auto put4 = [&](int64_t row, int64_t col, const float (&v)[4]) {
     if (vec && col + 3 < a.N) {
@@ -605,84 +766,321 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a) {
         if (col + e < a.N) OutT<TC>::store(a.C, row * a.ldc + col + e, v[e]);
     }
   };
-  if (SWIGLU) {
+  constexpr int NJ = SWIGLU ? 4 : 8;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t nb = n0 + wn * 64 + j * 32 + lhi * 4;
-      float sg[16], su[16];
+  for (int j = 0; j < NJ; ++j) {
+    const int64_t col = cbase + 16 * j + 4 * g4;
+    float sc[4], su[4], bi[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t col = nb + q * 8 + e;
-          const bool in = (a.flags & GEMM_SCALE) && col < a.N;
-          sg[q * 4 + e] = in ? a.scale0[col] : 1.f;
-          su[q * 4 + e] = in ? a.scale1[col] : 1.f;
-        }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t row = m0 + wm * 128 + i * 32 + l32;
-        if (row >= a.M) continue;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int64_t col = nb + q * 8;
-          if (col >= a.N) continue;
-          float h[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float g = acc[i][j][q * 4 + e] * sg[q * 4 + e];
-            const float u = acc[i][j + 2][q * 4 + e] * su[q * 4 + e];
-            // silu(g) = g / (1 + exp(-g)) from the hardware 2^x and
-            // reciprocal (about 2 ulp in fp32, far below the bf16 output
-            // rounding); the accurate expf / division sequences would keep
-            // the MFMA pipe idle for ~10% of a K = 4096 tile
-            const float ex = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
-            h[e] = g * __builtin_amdgcn_rcpf(1.0f + ex) * u;
-          }
-          put4(row, col, h);
-        }
-      }
+    for (int e = 0; e < 4; ++e) {
+      const bool in = col + e < a.N;
+      sc[e] = ((a.flags & GEMM_SCALE) && in) ? a.scale0[col + e] : 1.f;
+      su[e] = (SWIGLU && (a.flags & GEMM_SCALE) && in) ? a.scale1[col + e] : 1.f;
+      bi[e] = (!SWIGLU && (a.flags & GEMM_BIAS) && in)
+                  ? bf16_to_f32(reinterpret_cast<const uint16_t *>(a.bias)[col + e]) : 0.f;
     }
-  } else {
+    if (col >= a.N) continue;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t nb = n0 + wn * 128 + j * 32 + lhi * 4;
-      float sc[16], bi[16];
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
+    for (int i = 0; i < NI; ++i) {
+      const int64_t row = rbase + 16 * i + l16;
+      if (row >= a.M) continue;
+      float v[4];
+      if constexpr (SWIGLU) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int64_t col = nb + q * 8 + e;
-          sc[q * 4 + e] = ((a.flags & GEMM_SCALE) && col < a.N) ? a.scale0[col] : 1.f;
-          bi[q * 4 + e] = ((a.flags & GEMM_BIAS) && col < a.N)
-                              ? bf16_to_f32(reinterpret_cast<const uint16_t *>(a.bias)[col]) : 0.f;
+          const float g = acc[i][j][e] * sc[e];
+          const float u = acc[i][j + 4][e] * su[e];
+          // silu(g) = g / (1 + exp(-g)) from the hardware 2^x and reciprocal
+          const float ex = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+          v[e] = g * __builtin_amdgcn_rcpf(1.0f + ex) * u;
         }
+      } else {
+        float r4[4] = {0.f, 0.f, 0.f, 0.f};
+        if (a.flags & GEMM_RESID) {
+          if (vec && col + 3 < a.N) {
+            OutT<TC>::load4(a.resid, row * a.ldc + col, r4);
+          } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t row = m0 + wm * 128 + i * 32 + l32;
-        if (row >= a.M) continue;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int64_t col = nb + q * 8;
-          if (col >= a.N) continue;
-          float r4[4] = {0.f, 0.f, 0.f, 0.f};
-          if (a.flags & GEMM_RESID) {
-            if (vec && col + 3 < a.N) {
-              OutT<TC>::load4(a.resid, row * a.ldc + col, r4);
-            } else {
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                if (col + e < a.N) r4[e] = OutT<TC>::load(a.resid, row * a.ldc + col + e);
-            }
+            for (int e = 0; e < 4; ++e)
+              if (col + e < a.N) r4[e] = OutT<TC>::load(a.resid, row * a.ldc + col + e);
           }
-          float v[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = acc[i][j][q * 4 + e] * sc[q * 4 + e] + bi[q * 4 + e] + r4[e];
-          put4(row, col, v);
         }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][e] * sc[e] + bi[e] + r4[e];
       }
+      put4(row, col, v);
     }
   }
+}
+
+// LDS DMA issued as inline asm: the compiler's wait insertion does not model
+// it, so it adds no waits of its own for it; every ordering is explicit
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4_t rsrc_words(const void *p, int64_t bytes) {
+  const uint64_t a = (uint64_t)p;
+  i32x4_t r;
+  r[0] = (int)(uint32_t)a;
+  r[1] = (int)(uint32_t)(a >> 32) & 0xffff;
+  r[2] = (int)bytes;
+  r[3] = BUF_WORD3;
+  return r;
+}
+// LDS byte address of a shared-memory pointer
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) { return (uint32_t)(uintptr_t)(lds_void *)p; }
+// lds: wave-uniform LDS byte address of the 1 KiB block (lane l fills
+// lds + 16 l)
+__device__ __forceinline__ void dma16_asm(i32x4_t r, uint32_t lds, uint32_t off) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :: "v"(off), "s"(r), "s"(m) : "memory", "m0");
+}
+
+template <bool NT, bool FP8, bool SWIGLU, typename TC>
+__device__ __forceinline__ void gemm_pp_body(const GemmArgs &a) {
+  static_assert(NT || !FP8, "fp8 NN weights use the 4-wave kernel");
+  constexpr int BMODE = (NT && FP8) ? B_T8 : NT ? B_T16 : B_NN16;
+  constexpr int HB = BMODE == B_T8 ? 8192 : 16384;  // B bytes per half-tile stage
+  constexpr int R = BMODE == B_T8 ? 6 : 5;          // ring stages: 144 / 160 KiB
+  constexpr bool DMA_G0 = BMODE == B_NN16;  // see the issue plan below
+  constexpr int ND = (BMODE == B_T8 ? 3 : 4) * (DMA_G0 ? 2 : 1);  // DMA moves per issuing wave per phase
+  constexpr int KP = 32;                            // k per phase
+
+  int tm, tn;
+  gemm_tile(a, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM;
+  const int64_t n0 = (int64_t)tn * (SWIGLU ? BN / 2 : BN);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2, wi = wave & 3;
+  const int wm = wi >> 1, wn = wi & 1;
+  const int arow0 = 128 * grp + 64 * wm;
+
+  // 4 x 8 tiles of v_mfma_f32_16x16x32_bf16 (which sustains a higher rate
+  // than the 32x32x16 form on random operands): A tile i = rows 16 i..,
+  // B tile j = B^T rows bw0 + brel[j]..
+  f32x4 acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.f;
+
+  const int bsz = FP8 ? 1 : 2;
+  const i32x4_t ra = rsrc_words(a.A, a.M * a.lda * 2);
+  const int64_t brows = NT ? a.N : a.K;
+  const i32x4_t rb0 = rsrc_words(a.B0, brows * a.ldb * bsz);
+  const i32x4_t rb1 = rsrc_words(SWIGLU ? a.B1 : a.B0, brows * a.ldb * bsz);
+
+  // DMA_G0: only group 0 issues the DMAs (a whole stage per phase, in its
+  // load slot), so the computing wave's MFMA issue never queues behind a
+  // vector memory instruction; otherwise all 8 waves issue a share
+  constexpr int NWD = DMA_G0 ? 4 : 8;
+  // DMA sources: one per-lane base per operand plus a uniform stride per
+  // block j (wave wd moves blocks b = NWD j + wd).  Rows past M (A), N (NT
+  // B) or K (NN B) land past the buffer's end and read zeros; chunks past K
+  // (row-major operands) or past N (NN B columns) are sent out of range.
+  const int wd = wave & (NWD - 1);
+  const int lc16 = (lane & 3) ^ ((lane >> 4) & 3);  // A / bf16 B^T: logical chunk of this lane
+  const int lc8 = (lane & 1) ^ ((lane >> 4) & 1);   // fp8 B^T
+  const uint32_t abase = (uint32_t)(((m0 + wd * 16 + (lane >> 2)) * a.lda + lc16 * 8) * 2);
+  const uint32_t astr = (uint32_t)(16 * NWD * a.lda * 2);
+  uint32_t bbase = 0, bstr = 0, bup = 0, bhalf = 0;
+  int bkofs = 0, nn_colok = 0;
+  if constexpr (BMODE == B_T16) {
+    bbase = (uint32_t)(((n0 + wd * 16 + (lane >> 2)) * a.ldb + lc16 * 8) * 2);
+    bstr = (uint32_t)(16 * NWD * a.ldb * 2);
+    bup = (uint32_t)(128 * a.ldb * 2);
+    bkofs = lc16 * 8;
+  } else if constexpr (BMODE == B_T8) {
+    bbase = (uint32_t)((n0 + wd * 32 + (lane >> 1)) * a.ldb + lc8 * 16);
+    bstr = (uint32_t)(32 * NWD * a.ldb);
+    bup = (uint32_t)(128 * a.ldb);
+    bkofs = lc8 * 16;
+  } else {
+    // block b: column half b / 8, k rows (b mod 8) * 4 + l / 16; lane slot
+    // l % 16 holds logical chunk (l % 16) ^ nnswz(k)
+    const int kq = lane >> 4;
+    const int lc = (lane & 15) ^ nnswz(kq);
+    bbase = (uint32_t)(((int64_t)(wd % 8 * 4 + kq) * a.ldb + n0 + lc * 8) * 2);
+    bstr = (uint32_t)(16 * a.ldb * 2);  // +4 blocks within a half (NWD = 4)
+    bhalf = SWIGLU ? 0u : 256u;          // column half 1: +128 columns
+    const int64_t c0 = n0 + lc * 8, c1 = n0 + (SWIGLU ? 0 : 128) + lc * 8;
+    nn_colok = (c0 < a.N ? 1 : 0) | (c1 < a.N ? 2 : 0);
+  }
+  // DMA of phase q (k0 = 32 q) into a stage; past K the offsets are out of
+  // range and read zeros
+  auto issue = [&](uint8_t *As, uint8_t *Bs, int64_t k0) __attribute__((always_inline)) {
+    const uint32_t kk0 = (uint32_t)k0;
+    const bool ka = k0 + lc16 * 8 < a.K;
+    const uint32_t la = lds_addr(As), lb = lds_addr(Bs);
+#pragma unroll
+    for (int j = 0; j < 16 / NWD; ++j)
+      dma16_asm(ra, la + (j * NWD + wd) * 1024, ka ? abase + j * astr + kk0 * 2 : OOB);
+    if constexpr (BMODE == B_T8) {
+      const bool kb = k0 + bkofs < a.K;
+#pragma unroll
+      for (int j = 0; j < 8 / NWD; ++j) {
+        const bool up = SWIGLU && (j * NWD + wd) >= 4;  // blocks 4..7: the up weight
+        dma16_asm(up ? rb1 : rb0, lb + (j * NWD + wd) * 1024, kb ? bbase + j * bstr - (up ? bup : 0) + kk0 : OOB);
+      }
+    } else if constexpr (BMODE == B_T16) {
+      const bool kb = k0 + bkofs < a.K;
+#pragma unroll
+      for (int j = 0; j < 16 / NWD; ++j) {
+        const bool up = SWIGLU && (j * NWD + wd) >= 8;  // blocks 8..15: the up weight
+        dma16_asm(up ? rb1 : rb0, lb + (j * NWD + wd) * 1024,
+                  kb ? bbase + j * bstr - (up ? bup : 0) + kk0 * 2 : OOB);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16 / NWD; ++j) {
+        const int b = j * NWD + wd;  // wave-uniform
+        const int h = b >> 3;
+        const bool ok = (nn_colok >> h) & 1;
+        // k rows (b mod 8) * 4 = wd * 4 (in bbase) + 16 (j mod 2) for NWD = 4,
+        // or wd * 4 for NWD = 8 (j = h)
+        const uint32_t krow_ofs = NWD == 4 ? (uint32_t)(j & 1) * bstr : 0u;
+        dma16_asm((SWIGLU && h) ? rb1 : rb0, lb + b * 1024,
+                  ok ? bbase + krow_ofs + h * bhalf + kk0 * (uint32_t)(a.ldb * 2) : OOB);
+      }
+    }
+  };
+
+  // Per-lane LDS byte offsets of the fragments.  16x16x32 operands: lane
+  // (g = l / 16, i = l % 16) holds row i of a 16-row tile and k 8 g..8 g+7
+  // of the phase (logical chunk g of a 64-byte half-tile row).  The A tile
+  // (+16 rows) and B tile (brel) parts are immediates; row bases are
+  // multiples of 16, so the row swizzles only depend on i.
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int bw0 = SWIGLU ? wn * 64 : wn * 128;  // B^T rows of tile j: bw0 + brel[j]
+  constexpr int brel[8] = {0, 16, 32, 48, SWIGLU ? 128 : 64, SWIGLU ? 144 : 80, SWIGLU ? 160 : 96,
+                           SWIGLU ? 176 : 112};
+  const uint32_t aoff = (arow0 + l16) * 64 + ((g4 ^ hswz(l16)) << 4);
+  const uint32_t boff = (bw0 + l16) * 64 + ((g4 ^ hswz(l16)) << 4);
+  const uint32_t b8off = (bw0 + l16) * 32 + (((g4 >> 1) ^ hswz8(l16)) << 4) + 8 * (g4 & 1);
+  // NN B (ds_read_b64_tr_b16): per B tile j, lane (g, i) reads k rows
+  // 8 g + 4 s + i / 4 (s immediate) and columns c + 4 (i % 4) of column half
+  // (bw0 + brel[j]) / 128
+  uint32_t nnoff[8];
+  if (BMODE == B_NN16) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int br = bw0 + brel[j];
+      const int half = br >> 7, c = br & 127;
+      const int nl = c + 4 * (l16 & 3);
+      const int k = 8 * g4 + (l16 >> 2);
+      nnoff[j] = half * 8192 + k * 256 + (((nl >> 3) ^ nnswz(k)) << 4) + (nl & 7) * 2;
+    }
+  }
+
+  // fragments of one phase (one k32 step)
+  bf16x8_t af[4], bf[8];
+  auto load = [&](const uint8_t *As, const uint8_t *Bs) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8_t *>(As + aoff + i * 1024);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (BMODE == B_T16) {
+        bf[j] = *reinterpret_cast<const bf16x8_t *>(Bs + boff + brel[j] * 64);
+      } else if (BMODE == B_T8) {
+        const uint4 w = e4m3x8_to_bf16x8(*reinterpret_cast<const uint2 *>(Bs + b8off + brel[j] * 32));
+        bf[j] = *reinterpret_cast<const bf16x8_t *>(&w);
+      } else {
+        s16x4 v[2];
+#pragma unroll
+        for (int sidx = 0; sidx < 2; ++sidx)
+          v[sidx] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(Bs + nnoff[j] + 4 * sidx * 256));
+        bf[j] = __builtin_shufflevector(__builtin_bit_cast(__attribute__((ext_vector_type(4))) __bf16, v[0]),
+                                        __builtin_bit_cast(__attribute__((ext_vector_type(4))) __bf16, v[1]),
+                                        0, 1, 2, 3, 4, 5, 6, 7);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the fragments are in registers
+  };
+  // C^T tiles (B fragment as the A operand): lane (g, i) of tile (i', j)
+  // holds output row 16 i' + i and columns (tile column) + 4 g + 0..3
+  auto compute = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
+  };
+  // slot boundary: the scheduling fences keep the MFMAs (register-only
+  // instructions, which the memory clobbers do not pin) inside their slot
+  auto slot_end = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    barrier_no_fence();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // ring stages [A | B]: one array each, so that the compiler sees that DMA
+  // targets and fragment sources of different stages never alias (it tracks
+  // a few LDS DMA targets individually; more would make its own waits
+  // conservative)
+  constexpr int SS = 16384 + HB;
+  __shared__ __attribute__((aligned(1024))) uint8_t ST0[SS], ST1[SS], ST2[SS], ST3[SS], ST4[SS], ST5[SS];
+  auto sa = [&](auto stag) __attribute__((always_inline)) -> uint8_t * {
+    constexpr int S = decltype(stag)::value;
+    if constexpr (S == 0) return ST0; else if constexpr (S == 1) return ST1; else if constexpr (S == 2) return ST2;
+    else if constexpr (S == 3) return ST3; else if constexpr (S == 4) return ST4; else return ST5;
+  };
+  auto sb = [&](auto stag) __attribute__((always_inline)) -> uint8_t * { return sa(stag) + 16384; };
+
+  const int nph = (int)((a.K + KP - 1) / KP);
+  if (!DMA_G0 || grp == 0) {
+    issue(ST0, ST0 + 16384, 0);
+    issue(ST1, ST1 + 16384, KP);
+    issue(ST2, ST2 + 16384, 2 * KP);
+    issue(ST3, ST3 + 16384, 3 * KP);
+    issue(ST4, ST4 + 16384, 4 * KP);
+    if constexpr (R > 5) issue(ST5, ST5 + 16384, 5 * KP);
+  }
+  wait_vmem_but<ND * (R - 1)>();  // phase 0 landed
+  slot_end();
+  if (grp == 0) load(ST0, ST0 + 16384);
+  slot_end();
+  // phase p in stage S = p mod R; G = this wave's group
+  auto phase = [&](auto stag, int p, auto gtag) __attribute__((always_inline)) {
+    constexpr int S = decltype(stag)::value;
+    constexpr int G = decltype(gtag)::value;
+    uint8_t *As = sa(Int<S>{}), *Bs = sb(Int<S>{});
+    const uint8_t *An = sa(Int<(S + 1) % R>{}), *Bn = sb(Int<(S + 1) % R>{});
+    if (G == 0) compute(); else load(As, Bs);
+    wait_vmem_but<ND * (R - 2)>();  // phase p + 1 landed
+    slot_end();
+    // group 0 reads the next phase unconditionally (past the last phase it
+    // reads a stage nothing will consume), then every wave refills stage S
+    if (G == 0) load(An, Bn);
+    if (!DMA_G0 || G == 0) issue(As, Bs, (int64_t)(p + R) * KP);
+    if (G == 1) compute();
+    slot_end();
+  };
+  auto run = [&](auto gtag) __attribute__((always_inline)) {
+    int p = 0;
+    for (; p + R <= nph; p += R) {
+      phase(Int<0>{}, p, gtag);
+      phase(Int<1>{}, p + 1, gtag);
+      phase(Int<2>{}, p + 2, gtag);
+      phase(Int<3>{}, p + 3, gtag);
+      phase(Int<4>{}, p + 4, gtag);
+      if constexpr (R > 5) phase(Int<5>{}, p + 5, gtag);
+    }
+    if (p < nph) phase(Int<0>{}, p, gtag);
+    if (p + 1 < nph) phase(Int<1>{}, p + 1, gtag);
+    if (p + 2 < nph) phase(Int<2>{}, p + 2, gtag);
+    if (p + 3 < nph) phase(Int<3>{}, p + 3, gtag);
+    if constexpr (R > 5)
+      if (p + 4 < nph) phase(Int<4>{}, p + 4, gtag);
+  };
+  if (grp == 0)
+    run(Int<0>{});
+  else
+    run(Int<1>{});
+  wait_vmem();
+  gemm_epilogue16<SWIGLU, TC, 4>(a, acc, m0 + arow0, n0 + bw0, lane);
 }
 
 #define NK_GEMM(NT, FP8, SW, TC, name)                                                   \
@@ -700,3 +1098,18 @@ NK_GEMM(true, true, false, bf16, nk_gemm_nt_e4m3_bf16)
 NK_GEMM(true, true, false, float, nk_gemm_nt_e4m3_f32)
 NK_GEMM(true, true, true, bf16, nk_gemm_swiglu_nt_e4m3_bf16)
 NK_GEMM(false, true, false, bf16, nk_gemm_nn_e4m3_bf16)
+
+#define NK_GEMM_PP(NT, FP8, SW, TC, name)                                                \
+  extern "C" __global__ __launch_bounds__(512, 1) void name(GemmArgs a) {                \
+    gemm_pp_body<NT, FP8, SW, TC>(a);                                                    \
+  }
+
+NK_GEMM_PP(false, false, false, bf16, nk_gemm8_nn_bf16_bf16)
+NK_GEMM_PP(false, false, false, float, nk_gemm8_nn_bf16_f32)
+NK_GEMM_PP(true, false, false, bf16, nk_gemm8_nt_bf16_bf16)
+NK_GEMM_PP(true, false, false, float, nk_gemm8_nt_bf16_f32)
+NK_GEMM_PP(false, false, true, bf16, nk_gemm8_swiglu_nn_bf16_bf16)
+NK_GEMM_PP(true, false, true, bf16, nk_gemm8_swiglu_nt_bf16_bf16)
+NK_GEMM_PP(true, true, false, bf16, nk_gemm8_nt_e4m3_bf16)
+NK_GEMM_PP(true, true, false, float, nk_gemm8_nt_e4m3_f32)
+NK_GEMM_PP(true, true, true, bf16, nk_gemm8_swiglu_nt_e4m3_bf16)

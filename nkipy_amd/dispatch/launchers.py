@@ -235,7 +235,7 @@ GEMM_BN = 256
 def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: str,
          b_dtype, c_dtype, lda: int = None, ldb: int = None, ldc: int = None,
          bias_ptr: int = 0, scale_ptr: int = 0, resid_ptr: int = 0,
-         up_ptr: int = 0, up_scale_ptr: int = 0) -> Launch:
+         up_ptr: int = 0, up_scale_ptr: int = 0, pingpong: bool = None) -> Launch:
     """C[M, N] = A[M, K] @ B (+ epilogue) on bf16 MFMA, fp32 accumulation.
 
     ``layout`` "nn": B is K x N row-major (ldb >= N); "nt": B is N x K
@@ -244,6 +244,9 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
     computes the SwiGLU product silu(A @ B) * (A @ B_up) instead (B_up has the
     layout and leading dimension of B).  ``bias_ptr`` (bf16, N) and
     ``resid_ptr`` (C dtype, M x N, leading dimension ldc) are added.
+    ``pingpong`` selects the 8-wave kernel (two waves per SIMD alternating
+    between MFMAs and fragment loads; the default where it exists, i.e. for
+    every layout except fp8 NN weights) or the 4-wave kernel.
     """
     if layout not in ("nn", "nt"):
         raise LaunchError(f"unknown GEMM layout {layout}")
@@ -296,13 +299,19 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
                     tiles_m, tiles_n, flags, 0)
     btag = "e4m3" if fp8 else "bf16"
     ctag = "bf16" if c_dtype == dt.bfloat16 else "f32"
+    has_pp = not (fp8 and layout == "nn")
+    if pingpong is None:
+        pingpong = has_pp
+    if pingpong and not has_pp:
+        raise LaunchError("the 8-wave GEMM has no fp8 NN variant")
+    prefix = "nk_gemm8" if pingpong else "nk_gemm"
     if swiglu:
-        symbol = f"nk_gemm_swiglu_{layout}_{btag}_bf16"
+        symbol = f"{prefix}_swiglu_{layout}_{btag}_bf16"
     else:
-        symbol = f"nk_gemm_{layout}_{btag}_{ctag}"
+        symbol = f"{prefix}_{layout}_{btag}_{ctag}"
     n_mm = 2 if swiglu else 1
     nbytes = M * K * 2 + n_mm * N * K * b_dtype.itemsize + M * N * c_dtype.itemsize
-    return Launch("gemm", symbol, (tiles_m * tiles_n, 1, 1), (256, 1, 1), args,
+    return Launch("gemm", symbol, (tiles_m * tiles_n, 1, 1), (512 if pingpong else 256, 1, 1), args,
                   bytes=nbytes, flops=2 * M * N * K * n_mm)
 
 

@@ -34,10 +34,15 @@ def _run(gpu, launch):
 SHAPES = [(256, 256, 64), (512, 768, 320), (300, 520, 136), (64, 40, 16), (1000, 1000, 1000)]
 
 
+# pp: the 8-wave kernel (default) and the 4-wave kernel
+PP = [True, False]
+
+
+@pytest.mark.parametrize("pp", PP)
 @pytest.mark.parametrize("layout", ["nn", "nt"])
 @pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("out", ["bf16", "f32"])
-def test_gemm_bf16(gpu, layout, shape, out):
+def test_gemm_bf16(gpu, layout, shape, out, pp):
     M, Nn, Kk = shape
     if layout == "nn" and Nn % 8:
         pytest.skip("NN needs N % 8 == 0")
@@ -50,7 +55,8 @@ def test_gemm_bf16(gpu, layout, shape, out):
     bd = DeviceTensor.from_numpy(dt.to_bf16(b))
     cdt = dt.bfloat16 if out == "bf16" else dt.float32
     cd = DeviceTensor.empty((M, Nn), cdt)
-    _run(gpu, LA.gemm(ad.ptr, bd.ptr, cd.ptr, M, Nn, Kk, layout=layout, b_dtype=dt.bfloat16, c_dtype=cdt))
+    _run(gpu, LA.gemm(ad.ptr, bd.ptr, cd.ptr, M, Nn, Kk, layout=layout, b_dtype=dt.bfloat16, c_dtype=cdt,
+                      pingpong=pp))
     got = dt.to_float32(cd.numpy())
     if out == "f32":
         np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
@@ -58,8 +64,9 @@ def test_gemm_bf16(gpu, layout, shape, out):
         _close(got, ref)
 
 
+@pytest.mark.parametrize("pp", PP)
 @pytest.mark.parametrize("layout", ["nn", "nt"])
-def test_gemm_swiglu(gpu, layout):
+def test_gemm_swiglu(gpu, layout, pp):
     M, F, Kk = 512, 384, 256
     rng = np.random.default_rng(7)
     x = _bf16(rng, (M, Kk))
@@ -78,11 +85,12 @@ def test_gemm_swiglu(gpu, layout):
     xd = DeviceTensor.from_numpy(dt.to_bf16(x))
     hd = DeviceTensor.empty((M, F), dt.bfloat16)
     _run(gpu, LA.gemm(xd.ptr, b0, hd.ptr, M, F, Kk, layout=layout, b_dtype=dt.bfloat16,
-                      c_dtype=dt.bfloat16, ldb=ldb, up_ptr=b1))
+                      c_dtype=dt.bfloat16, ldb=ldb, up_ptr=b1, pingpong=pp))
     _close(dt.to_float32(hd.numpy()), ref)
 
 
-def test_gemm_fp8_nt_scales_bias_residual(gpu):
+@pytest.mark.parametrize("pp", PP)
+def test_gemm_fp8_nt_scales_bias_residual(gpu, pp):
     M, Nn, Kk = 384, 512, 448
     rng = np.random.default_rng(11)
     x = _bf16(rng, (M, Kk))
@@ -99,15 +107,18 @@ def test_gemm_fp8_nt_scales_bias_residual(gpu):
     rd = DeviceTensor.from_numpy(dt.to_bf16(res))
     cd = DeviceTensor.empty((M, Nn), dt.bfloat16)
     _run(gpu, LA.gemm(xd.ptr, wd.ptr, cd.ptr, M, Nn, Kk, layout="nt", b_dtype=dt.float8_e4m3fn,
-                      c_dtype=dt.bfloat16, scale_ptr=sd.ptr, bias_ptr=bd.ptr, resid_ptr=rd.ptr))
+                      c_dtype=dt.bfloat16, scale_ptr=sd.ptr, bias_ptr=bd.ptr, resid_ptr=rd.ptr,
+                      pingpong=pp))
     _close(dt.to_float32(cd.numpy()), ref)
 
 
+@pytest.mark.parametrize("pp", PP)
 @pytest.mark.parametrize("Kk", [16, 64, 128, 192, 208, 576])
-def test_gemm_fp8_nt_k_tiles(gpu, Kk):
-    """fp8 NT weights stream through a three-stage LDS ring; K of 1..9 tiles
-    of 64 covers every ring phase at the loop exit (fp32 output, so the check
-    is at fp32-accumulation level)."""
+def test_gemm_fp8_nt_k_tiles(gpu, Kk, pp):
+    """fp8 NT weights stream through an LDS ring (three stages in the 4-wave
+    kernel, two in the 8-wave one); K of 1..9 tiles of 64 covers every ring
+    phase at the loop exit (fp32 output, so the check is at
+    fp32-accumulation level)."""
     M, Nn = 320, 272
     rng = np.random.default_rng(Kk)
     x = _bf16(rng, (M, Kk))
@@ -119,11 +130,12 @@ def test_gemm_fp8_nt_k_tiles(gpu, Kk):
     sd = DeviceTensor.from_numpy(scale.astype(np.float32))
     cd = DeviceTensor.empty((M, Nn), dt.float32)
     _run(gpu, LA.gemm(xd.ptr, wd.ptr, cd.ptr, M, Nn, Kk, layout="nt", b_dtype=dt.float8_e4m3fn,
-                      c_dtype=dt.float32, scale_ptr=sd.ptr))
+                      c_dtype=dt.float32, scale_ptr=sd.ptr, pingpong=pp))
     np.testing.assert_allclose(cd.numpy(), ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
 
 
-def test_gemm_fp8_swiglu_nt(gpu):
+@pytest.mark.parametrize("pp", PP)
+def test_gemm_fp8_swiglu_nt(gpu, pp):
     M, F, Kk = 256, 256, 512
     rng = np.random.default_rng(12)
     x = _bf16(rng, (M, Kk))
@@ -138,7 +150,8 @@ def test_gemm_fp8_swiglu_nt(gpu):
                                               sg.astype(np.float32), su.astype(np.float32))]
     hd = DeviceTensor.empty((M, F), dt.bfloat16)
     _run(gpu, LA.gemm(t[0].ptr, t[1].ptr, hd.ptr, M, F, Kk, layout="nt", b_dtype=dt.float8_e4m3fn,
-                      c_dtype=dt.bfloat16, scale_ptr=t[3].ptr, up_ptr=t[2].ptr, up_scale_ptr=t[4].ptr))
+                      c_dtype=dt.bfloat16, scale_ptr=t[3].ptr, up_ptr=t[2].ptr, up_scale_ptr=t[4].ptr,
+                      pingpong=pp))
     _close(dt.to_float32(hd.numpy()), ref)
 
 
