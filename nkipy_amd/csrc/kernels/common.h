@@ -295,4 +295,16 @@ NK_DEVICE float block_max(float v, float *red) {
   return t;
 }
 
+// Workgroup barrier for LDS hand-offs.  __syncthreads() carries a release
+// fence, which also waits for every outstanding global load (vmcnt(0)) and
+// so drains a register prefetch issued ahead of the barrier.  This waits only
+// for the wave's own LDS operations (lgkmcnt(0)) before s_barrier; the empty
+// asm statements keep the compiler from moving memory accesses across it.
+NK_DEVICE void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 }  // namespace nk

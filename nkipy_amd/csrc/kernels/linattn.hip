@@ -432,7 +432,7 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
   load_raw(rb, min(1, nchunks - 1));
   if (qwave) make_qf(ra);
   stage_in(ra, s0);
-  __syncthreads();
+  lds_barrier();
   // iteration c: fetch chunk c + 2, compute chunk c, stage chunk c + 1.  The
   // fetches are unconditional (past the end they re-read the last chunk, and
   // the staging writes it into the idle stage, which nothing reads), so the
@@ -443,10 +443,10 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
     for (; c + 2 <= nchunks; c += 2) {
       load_raw(ra, min(c + 2, nchunks - 1));
       chunk(s0, s1, c, rb, rtag);
-      __syncthreads();
+      lds_barrier();
       load_raw(rb, min(c + 3, nchunks - 1));
       chunk(s1, s0, c + 1, ra, rtag);
-      __syncthreads();
+      lds_barrier();
     }
     if (c < nchunks) chunk(s0, s1, c, rb, rtag);
   };
@@ -465,7 +465,8 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
 // are staged in LDS (fp16, the layouts of the scan kernel) and
 // S += phi(K)^T V, z += phi(K)^T 1 accumulate in the MFMA accumulators; the
 // sums go out in fp32.
-extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_state_c64_d128(LinAttnStateArgs a) {
+// (at most 128 VGPRs: two workgroups share a CU, so all of them are resident)
+extern "C" __global__ __launch_bounds__(512, 4) void nk_linattn_state_c64_d128(LinAttnStateArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t KS[2][LC * 256];
   __shared__ __attribute__((aligned(1024))) uint8_t VS[2][LC * 256];
 
@@ -527,21 +528,24 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_state_c64_d128(L
     }
   };
 
+  // Two register sets: iteration c computes chunk c from LDS stage c % 2 and
+  // stages chunk c + 1; the fetch of chunk c + 2, issued at its start, stays
+  // in flight across the barrier (which waits for LDS operations only).
   uint4 ka[2], va[2], kb2[2], vb[2];
   load(ka, va, 0);
   load(kb2, vb, min(1, a.rchunks - 1));
   stage(ka, va, 0);
-  __syncthreads();
+  lds_barrier();
   int c = 0;
   for (; c + 2 <= a.rchunks; c += 2) {
     load(ka, va, min(c + 2, a.rchunks - 1));
     update(0);
     stage(kb2, vb, 1);
-    __syncthreads();
+    lds_barrier();
     load(kb2, vb, min(c + 3, a.rchunks - 1));
     update(1);
     stage(ka, va, 0);
-    __syncthreads();
+    lds_barrier();
   }
   if (c < a.rchunks) update(0);
 
