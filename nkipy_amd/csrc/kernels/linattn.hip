@@ -95,14 +95,22 @@ struct LinAttnStateArgs {
   int32_t rchunks;
 };
 
-// Byte offsets in the LDS tiles.  Rows of 256 bytes (phi(Q), phi(K) [t][d],
-// S^T [j][d]): 16-byte chunk c of row r at c ^ (r & 15).  V [s][j]: rows of
-// 64 bytes, chunk c at c ^ ((r >> 2) & 3).
+// Byte offsets in the LDS tiles, bank-conflict free for every access below
+// (64 banks of 4 bytes).
+// Rows of 256 bytes (phi(K) [s][d], S^T [j][d]): 16-byte chunk c of row r at
+// c ^ ((r & 3) << 2 | (r >> 2) & 3).  That is a bijection on each block of
+// 16 rows, so 16 lanes reading one chunk of 16 rows hit 16 distinct chunks,
+// and 4 consecutive rows spread an aligned group of 4 chunks over all 16
+// chunk positions (the transposed phi(K)^T reads).
 __device__ __forceinline__ int o256(int r, int byte) {
-  return r * 256 + (((byte >> 4) ^ (r & 15)) << 4) + (byte & 15);
+  return r * 256 + (((byte >> 4) ^ (((r & 3) << 2) | ((r >> 2) & 3))) << 4) + (byte & 15);
 }
-__device__ __forceinline__ int o64(int r, int byte) {
-  return r * 64 + (((byte >> 4) ^ ((r >> 2) & 3)) << 4) + (byte & 15);
+// V: four tiles [64 s][32 j] (64-byte rows) 4 KiB apart.  Tile t stores row
+// r in row slot r ^ t (so the four tiles' copies of one row fall in
+// different banks) and flips the 32-byte halves of rows with bit 2 set (so
+// rows r and r + 4 of a transposed read do not collide).
+__device__ __forceinline__ int o64(int t, int r, int byte) {
+  return t * 4096 + (r ^ t) * 64 + (((byte >> 4) ^ (((r >> 2) & 1) << 1)) << 4) + (byte & 15);
 }
 
 // ds_read_b64_tr_b16: within each 16-lane group, source lane q + 4 j points
@@ -177,7 +185,7 @@ struct Raw {
 
 // V chunk i (16 bytes: row i / 16, columns 8 (i % 16) ..) -> byte offset in
 // the four 32-column V tiles
-__device__ __forceinline__ int voff(int i) { return ((i >> 2) & 3) * 4096 + o64(i >> 4, (i & 3) * 16); }
+__device__ __forceinline__ int voff(int i) { return o64((i >> 2) & 3, i >> 4, (i & 3) * 16); }
 
 extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttnArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t K0[LC * 256];
@@ -367,10 +375,9 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
       for (int jt = 0; jt < 8; ++jt) {
         // transpose reads from V tile jt / 2: source row 16 tile + 4 grp +
         // l16/4, columns 16 (jt % 2) + 4 (l16 % 4)
-        const uint8_t *vt = cur.V + (jt >> 1) * 4096;
         const int jb = (16 * (jt & 1) + 4 * (l16 & 3)) * 2;
-        const f16x4_t v0 = tr_read(vt + o64(16 * (2 * p) + 4 * grp + (l16 >> 2), jb));
-        const f16x4_t v1 = tr_read(vt + o64(16 * (2 * p + 1) + 4 * grp + (l16 >> 2), jb));
+        const f16x4_t v0 = tr_read(cur.V + o64(jt >> 1, 16 * (2 * p) + 4 * grp + (l16 >> 2), jb));
+        const f16x4_t v1 = tr_read(cur.V + o64(jt >> 1, 16 * (2 * p + 1) + 4 * grp + (l16 >> 2), jb));
         ot[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cat(v0, v1), pf, ot[jt], 0, 0, 0);
       }
       ot[8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(zrow_ones, pf, ot[8], 0, 0, 0);
@@ -402,8 +409,7 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
       const f16x8_t kf = cat(tr_read(cur.K + o256(kb, db)), tr_read(cur.K + o256(kb + 4, db)));
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const uint8_t *vt = cur.V + t * 4096;
-        const f16x8_t vf = cat(tr_read(vt + o64(kb, jb)), tr_read(vt + o64(kb + 4, jb)));
+        const f16x8_t vf = cat(tr_read(cur.V + o64(t, kb, jb)), tr_read(cur.V + o64(t, kb + 4, jb)));
         S[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, vf, S[t], 0, 0, 0);
       }
       Z = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ones, Z, 0, 0, 0);
@@ -465,8 +471,7 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
 // are staged in LDS (fp16, the layouts of the scan kernel) and
 // S += phi(K)^T V, z += phi(K)^T 1 accumulate in the MFMA accumulators; the
 // sums go out in fp32.
-// (at most 128 VGPRs: two workgroups share a CU, so all of them are resident)
-extern "C" __global__ __launch_bounds__(512, 4) void nk_linattn_state_c64_d128(LinAttnStateArgs a) {
+extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_state_c64_d128(LinAttnStateArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t KS[2][LC * 256];
   __shared__ __attribute__((aligned(1024))) uint8_t VS[2][LC * 256];
 
@@ -493,14 +498,25 @@ extern "C" __global__ __launch_bounds__(512, 4) void nk_linattn_state_c64_d128(L
 #pragma unroll
   for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
 
-  // thread -> k and v chunks tid + 512 i (row / 16, 8 columns at 8 (% 16))
-  auto load = [&](uint4 (&kr)[2], uint4 (&vr)[2], int c) {
-    const int64_t cb = base + (int64_t)c * LC * LD;
+  // thread -> k and v chunks tid + 512 i (row / 16, 8 columns at 8 (% 16)).
+  // Buffer loads: one per-lane 32-bit offset, the chunk offset in a scalar
+  // register and move i as an immediate (no 64-bit addresses held live).
+  const int64_t rbytes = (int64_t)a.rchunks * LC * LD * 2;
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.k + base), (short)0, (int)rbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.v + base), (short)0, (int)rbytes, 0x00020000);
+  const uint32_t loff = (uint32_t)((tid >> 4) * LD + (tid & 15) * 8) * 2;
+  typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+  auto ld16 = [&](__amdgpu_buffer_rsrc_t r, uint32_t off, int c) __attribute__((always_inline)) {
+    const u32x4v q = __builtin_amdgcn_raw_buffer_load_b128(r, off, c * (LC * LD * 2), 0);
+    return make_uint4(q[0], q[1], q[2], q[3]);
+  };
+  auto load = [&](uint4 (&kr)[2], uint4 (&vr)[2], int c) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int idx = tid + 512 * i;
-      kr[i] = *reinterpret_cast<const uint4 *>(a.k + cb + (idx >> 4) * LD + (idx & 15) * 8);
-      vr[i] = *reinterpret_cast<const uint4 *>(a.v + cb + (idx >> 4) * LDV + (idx & 15) * 8);
+      kr[i] = ld16(rk, loff + i * 32 * LD * 2, c);
+      vr[i] = ld16(rv, loff + i * 32 * LDV * 2, c);
     }
   };
   auto stage = [&](const uint4 (&kr)[2], const uint4 (&vr)[2], int b) {
@@ -511,43 +527,60 @@ extern "C" __global__ __launch_bounds__(512, 4) void nk_linattn_state_c64_d128(L
       *reinterpret_cast<uint4 *>(VS[b] + voff(idx)) = to_f16x8(vr[i]);
     }
   };
-  auto update = [&](int b) {
+  // All fragment reads of a chunk first (LDS latency paid once), then the
+  // MFMAs.  Every wave accumulates z (no branch in the loop); only the
+  // d_v-half-0 waves write it out.
+  auto update = [&](int b) __attribute__((always_inline)) {
+    f16x8_t kf[4], vf[4][2];
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const int kb = 16 * st + 8 * (grp >> 1) + (l16 >> 2);
       const int db = (32 * wd + 16 * (grp & 1) + 4 * (l16 & 3)) * 2;
       const int jb = (16 * (grp & 1) + 4 * (l16 & 3)) * 2;
-      const f16x8_t kf = cat(tr_read(KS[b] + o256(kb, db)), tr_read(KS[b] + o256(kb + 4, db)));
+      kf[st] = cat(tr_read(KS[b] + o256(kb, db)), tr_read(KS[b] + o256(kb + 4, db)));
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const uint8_t *vt = VS[b] + (2 * half + t) * 4096;
-        const f16x8_t vf = cat(tr_read(vt + o64(kb, jb)), tr_read(vt + o64(kb + 4, jb)));
-        S[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, vf, S[t], 0, 0, 0);
-      }
-      if (half == 0) Z = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ones, Z, 0, 0, 0);
+      for (int t = 0; t < 2; ++t)
+        vf[st][t] = cat(tr_read(VS[b] + o64(2 * half + t, kb, jb)), tr_read(VS[b] + o64(2 * half + t, kb + 4, jb)));
+    }
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) S[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[st], vf[st][t], S[t], 0, 0, 0);
+      Z = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[st], ones, Z, 0, 0, 0);
     }
   };
 
-  // Two register sets: iteration c computes chunk c from LDS stage c % 2 and
-  // stages chunk c + 1; the fetch of chunk c + 2, issued at its start, stays
-  // in flight across the barrier (which waits for LDS operations only).
-  uint4 ka[2], va[2], kb2[2], vb[2];
-  load(ka, va, 0);
-  load(kb2, vb, min(1, a.rchunks - 1));
-  stage(ka, va, 0);
+  // Four register sets fetch four chunks ahead of the LDS stage being
+  // filled (two LDS stages): iteration c computes chunk c from stage c % 2,
+  // stages chunk c + 1 (set (c + 1) % 4) into the other stage and refills
+  // that set with chunk c + 5.  The fetches stay in flight across the
+  // barriers (which wait for LDS operations only).  Past the end they re-read
+  // the last chunk and the staging fills a stage nothing reads.  Unrolled
+  // four ways so every set and stage index is static.
+  uint4 kr[4][2], vr[4][2];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) load(kr[q], vr[q], min(q, a.rchunks - 1));
+  stage(kr[0], vr[0], 0);
+  load(kr[0], vr[0], min(4, a.rchunks - 1));
   lds_barrier();
+  auto iter = [&](auto qtag, int c) __attribute__((always_inline)) {
+    constexpr int Q = decltype(qtag)::value;  // c mod 4
+    constexpr int SN = (Q + 1) % 4;           // set holding chunk c + 1
+    update(Q & 1);
+    stage(kr[SN], vr[SN], (Q + 1) & 1);
+    load(kr[SN], vr[SN], min(c + 5, a.rchunks - 1));
+    lds_barrier();
+  };
   int c = 0;
-  for (; c + 2 <= a.rchunks; c += 2) {
-    load(ka, va, min(c + 2, a.rchunks - 1));
-    update(0);
-    stage(kb2, vb, 1);
-    lds_barrier();
-    load(kb2, vb, min(c + 3, a.rchunks - 1));
-    update(1);
-    stage(ka, va, 0);
-    lds_barrier();
+  for (; c + 4 <= a.rchunks; c += 4) {
+    iter(Int<0>{}, c);
+    iter(Int<1>{}, c + 1);
+    iter(Int<2>{}, c + 2);
+    iter(Int<3>{}, c + 3);
   }
-  if (c < a.rchunks) update(0);
+  if (c < a.rchunks) iter(Int<0>{}, c);
+  if (c + 1 < a.rchunks) iter(Int<1>{}, c + 1);
+  if (c + 2 < a.rchunks) iter(Int<2>{}, c + 2);
 
   float *out = a.part + (bh * a.nranges + rr) * (int64_t)(LD + 1) * LDV;
 #pragma unroll

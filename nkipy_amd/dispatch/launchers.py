@@ -347,12 +347,14 @@ def linear_attention_split(BH: int, T: int):
            and nchunks // (2 * nseg) >= 8):
         nseg *= 2
     cs = nchunks // nseg
-    # two partial sums per earlier segment when that gives the partial-sum
-    # kernel a workgroup per CU or more (measured best at the 64 x 8192
-    # configuration), else quarter ranges
-    if cs % 4:
+    # One partial sum per earlier segment when that already occupies 3/4 of
+    # the CUs: the partial-sum kernel runs one workgroup per CU with a deep
+    # prefetch, so fewer, longer ranges beat a second round of workgroups
+    # (and halve the partial-state traffic); else halves or quarters.
+    wgs = BH * (nseg - 1)
+    if cs % 4 or 4 * wgs >= 3 * LINATTN_TARGET_WGS:
         rchunks = cs
-    elif BH * (nseg - 1) * 2 >= LINATTN_TARGET_WGS:
+    elif 2 * wgs >= LINATTN_TARGET_WGS:
         rchunks = cs // 2
     else:
         rchunks = cs // 4
