@@ -312,10 +312,8 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
   for (int t = 0; t < 4; ++t)
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
-      uint32_t w0 = (uint32_t)f32_to_bf16(acc_o[t][gq * 4 + 0] * inv_l) |
-                    ((uint32_t)f32_to_bf16(acc_o[t][gq * 4 + 1] * inv_l) << 16);
-      uint32_t w1 = (uint32_t)f32_to_bf16(acc_o[t][gq * 4 + 2] * inv_l) |
-                    ((uint32_t)f32_to_bf16(acc_o[t][gq * 4 + 3] * inv_l) << 16);
+      const uint32_t w0 = pack_bf16x2(acc_o[t][gq * 4 + 0] * inv_l, acc_o[t][gq * 4 + 1] * inv_l);
+      const uint32_t w1 = pack_bf16x2(acc_o[t][gq * 4 + 2] * inv_l, acc_o[t][gq * 4 + 3] * inv_l);
       *reinterpret_cast<uint2 *>(orow + t * 32 + gq * 8 + lhi * 4) = make_uint2(w0, w1);
     }
 }

@@ -20,13 +20,30 @@ struct e4m3 { uint8_t bits; };  // OCP float8 E4M3FN: bias 7, no inf, 0x7f/0xff 
 
 NK_DEVICE float bf16_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
-// Round-to-nearest-even float -> bf16, NaN kept quiet.  Same closed form as
-// the oracle's numpy rounding (add 0x7fff plus the kept LSB, truncate).
+// Round-to-nearest-even float -> bf16 with the hardware conversion
+// (v_cvt_pk_bf16_f32): for every non-NaN input it equals the closed form
+// "add 0x7fff plus the kept LSB, truncate"; a NaN stays a (quiet) NaN.  The
+// branch-free instruction replaces a per-element NaN test that compiled to
+// divergent branches.
 NK_DEVICE uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const __bf16 b = (__bf16)f;
+  uint16_t h;
+  __builtin_memcpy(&h, &b, 2);
+  return h;
+}
+
+// Correctly rounded a / b from rb = RN(1 / b), for a row of quotients that
+// share one divisor: q = RN(a * rb) is within one ulp of a / b, the fma
+// residual a - q * b and one fma correction then give RN(a / b) (Markstein,
+// IBM J. Res. Dev. 34(1), 1990).  Three instructions instead of the
+// scale / reciprocal / fixup sequence of a full division.  A non-finite
+// correction (b infinite, a infinite or NaN) falls back to q, which then
+// equals the IEEE quotient.
+NK_DEVICE float div_rn(float a, float b, float rb) {
+  const float q = a * rb;
+  const float r = __builtin_fmaf(-q, b, a);
+  const float c = __builtin_fmaf(r, rb, q);
+  return __builtin_isfinite(c) ? c : q;
 }
 
 NK_DEVICE float f16_to_f32(uint16_t h) {
@@ -156,7 +173,7 @@ template <> struct Vec8<bf16> {
     uint32_t w[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      w[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
+      w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
     st16<NT>(p, make_uint4(w[0], w[1], w[2], w[3]));
   }
 };
@@ -240,7 +257,7 @@ NK_DEVICE void encode8(const float v[8], Raw8<bf16> &r) {
   uint32_t w[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    w[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
+    w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
   r.w[0] = make_uint4(w[0], w[1], w[2], w[3]);
 }
 NK_DEVICE void encode8(const float v[8], Raw8<f16> &r) {

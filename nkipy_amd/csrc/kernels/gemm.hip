@@ -78,8 +78,7 @@ template <> struct OutT<bf16> {
   }
   static __device__ __forceinline__ void store4(void *C, int64_t i, const float (&v)[4]) {
     *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(C) + i) =
-        make_uint2((uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
-                   (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16));
+        make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
   }
   static __device__ __forceinline__ void load4(const void *C, int64_t i, float (&v)[4]) {
     const uint2 w = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(C) + i);

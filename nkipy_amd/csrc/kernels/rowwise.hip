@@ -69,12 +69,13 @@ __device__ __forceinline__ void softmax_reg_body(const SoftmaxArgs &a) {
     }
   }
   s = block_sum<BLOCK>(s, red);
+  const float inv_s = 1.0f / s;
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
     const int idx = (c * BLOCK + tid) * 8;
     if (idx < n) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[c][j] = v[c][j] / s;
+      for (int j = 0; j < 8; ++j) v[c][j] = div_rn(v[c][j], s, inv_s);
       Raw8<TO> o;
       encode8(v[c], o);
       o.template store<true>(y + idx);
@@ -221,7 +222,7 @@ __device__ __forceinline__ void rmsnorm_reg_body(const RmsNormArgs &a) {
       if (flags & NK_RMS_W) Vec8<T>::load(w + idx, wv);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        float q = (flags & NK_RMS_MUL_RECIP) ? v[c][j] * inv : v[c][j] / s;
+        float q = (flags & NK_RMS_MUL_RECIP) ? v[c][j] * inv : div_rn(v[c][j], s, inv);
         if (flags & NK_RMS_W) q = q * wv[j];
         v[c][j] = q;
       }
