@@ -269,59 +269,71 @@ NK_DEVICE void encode8(const float v[8], Raw8<f16> &r) {
 }
 
 // ---------------------------------------------------------------------------
-// Reductions.  A wavefront is 64 lanes on CDNA4.
-// ---------------------------------------------------------------------------
-NK_DEVICE float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-NK_DEVICE float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-
-// Workgroup reductions over BLOCK threads (BLOCK a multiple of 64, <= 1024).
-// `red` is a __shared__ scratch of at least BLOCK/64 floats; the function
-// synchronises before reusing it, so back-to-back calls are safe.
-template <int BLOCK>
-NK_DEVICE float block_sum(float v, float *red) {
-  v = wave_sum(v);
-  if (BLOCK == 64) return v;
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) red[wid] = v;
-  __syncthreads();
-  float t = 0.f;
-#pragma unroll
-  for (int i = 0; i < BLOCK / 64; ++i) t += red[i];
-  return t;
-}
-template <int BLOCK>
-NK_DEVICE float block_max(float v, float *red) {
-  v = wave_max(v);
-  if (BLOCK == 64) return v;
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) red[wid] = v;
-  __syncthreads();
-  float t = red[0];
-#pragma unroll
-  for (int i = 1; i < BLOCK / 64; ++i) t = fmaxf(t, red[i]);
-  return t;
-}
-
 // Workgroup barrier for LDS hand-offs.  __syncthreads() carries a release
 // fence, which also waits for every outstanding global load (vmcnt(0)) and
 // so drains a register prefetch issued ahead of the barrier.  This waits only
 // for the wave's own LDS operations (lgkmcnt(0)) before s_barrier; the empty
 // asm statements keep the compiler from moving memory accesses across it.
+// ---------------------------------------------------------------------------
 NK_DEVICE void lds_barrier() {
   __builtin_amdgcn_s_waitcnt(0xC07F);
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+}
+
+// ---------------------------------------------------------------------------
+// Reductions.  A wavefront is 64 lanes on CDNA4, in four rows of 16.  Within
+// a row, DPP operands (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_ror 4,
+// row_ror 8) combine lanes without LDS traffic; the four row results are then
+// read with v_readlane.  Every lane must be active.
+// ---------------------------------------------------------------------------
+template <bool MAX>
+NK_DEVICE float red_op(float a, float b) {
+  return MAX ? fmaxf(a, b) : a + b;
+}
+template <int CTRL>
+NK_DEVICE float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <bool MAX>
+NK_DEVICE float wave_reduce(float v) {
+  v = red_op<MAX>(v, dpp<0xB1>(v));
+  v = red_op<MAX>(v, dpp<0x4E>(v));
+  v = red_op<MAX>(v, dpp<0x124>(v));
+  v = red_op<MAX>(v, dpp<0x128>(v));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return red_op<MAX>(red_op<MAX>(r0, r1), red_op<MAX>(r2, r3));
+}
+NK_DEVICE float wave_sum(float v) { return wave_reduce<false>(v); }
+NK_DEVICE float wave_max(float v) { return wave_reduce<true>(v); }
+
+// Workgroup reductions over BLOCK threads (BLOCK a multiple of 64, <= 1024).
+// `red` is a __shared__ scratch of at least BLOCK/64 floats; the function
+// synchronises before reusing it, so back-to-back calls are safe.
+template <int BLOCK, bool MAX>
+NK_DEVICE float block_reduce(float v, float *red) {
+  v = wave_reduce<MAX>(v);
+  if (BLOCK == 64) return v;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  lds_barrier();
+  if (lane == 0) red[wid] = v;
+  lds_barrier();
+  float t = red[0];
+#pragma unroll
+  for (int i = 1; i < BLOCK / 64; ++i) t = red_op<MAX>(t, red[i]);
+  return t;
+}
+template <int BLOCK>
+NK_DEVICE float block_sum(float v, float *red) {
+  return block_reduce<BLOCK, false>(v, red);
+}
+template <int BLOCK>
+NK_DEVICE float block_max(float v, float *red) {
+  return block_reduce<BLOCK, true>(v, red);
 }
 
 }  // namespace nk

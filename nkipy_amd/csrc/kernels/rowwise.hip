@@ -30,7 +30,10 @@ struct SoftmaxArgs {
   int32_t pad;
 };
 
-template <typename TI, typename TO, int BLOCK, int CHUNKS>
+// NTS selects streaming stores.  The one-wave rows (BLOCK 64) store through
+// the cache: measured on (2048, 4096) fp32, streaming stores there cost
+// 18.0 us against 14.4 us; the larger blocks measure the other way round.
+template <typename TI, typename TO, int BLOCK, int CHUNKS, bool NTS = true>
 __device__ __forceinline__ void softmax_reg_body(const SoftmaxArgs &a) {
   __shared__ float red[BLOCK / 64];
   const int64_t row = blockIdx.x;
@@ -78,7 +81,7 @@ __device__ __forceinline__ void softmax_reg_body(const SoftmaxArgs &a) {
       for (int j = 0; j < 8; ++j) v[c][j] = div_rn(v[c][j], s, inv_s);
       Raw8<TO> o;
       encode8(v[c], o);
-      o.template store<true>(y + idx);
+      o.template store<NTS>(y + idx);
     }
   }
 }
@@ -103,7 +106,7 @@ __device__ __forceinline__ void softmax_loop_body(const SoftmaxArgs &a) {
 #define NK_SOFTMAX_REG(TI, TO, tin, ton, B, C)                                       \
   extern "C" __global__ __launch_bounds__(B) void nk_softmax_reg_##tin##_##ton##_b##B##_c##C( \
       SoftmaxArgs a) {                                                               \
-    softmax_reg_body<TI, TO, B, C>(a);                                               \
+    softmax_reg_body<TI, TO, B, C, (B > 64)>(a);                                     \
   }
 #define NK_SOFTMAX_LOOP(TI, TO, tin, ton)                                             \
   extern "C" __global__ __launch_bounds__(256) void nk_softmax_loop_##tin##_##ton(     \
@@ -113,6 +116,7 @@ __device__ __forceinline__ void softmax_loop_body(const SoftmaxArgs &a) {
 
 #define NK_SOFTMAX_ALL(TI, TO, tin, ton) \
   NK_SOFTMAX_REG(TI, TO, tin, ton, 64, 1)  \
+  NK_SOFTMAX_REG(TI, TO, tin, ton, 64, 8)  \
   NK_SOFTMAX_REG(TI, TO, tin, ton, 128, 4) \
   NK_SOFTMAX_REG(TI, TO, tin, ton, 256, 1) \
   NK_SOFTMAX_REG(TI, TO, tin, ton, 256, 2) \
