@@ -46,6 +46,33 @@ NK_DEVICE float div_rn(float a, float b, float rb) {
   return __builtin_isfinite(c) ? c : q;
 }
 
+// The same correction without the fallback, for quotients known to stay
+// finite (a finite, b finite and >= 1).
+NK_DEVICE float div_rn_finite(float a, float b, float rb) {
+  const float q = a * rb;
+  const float r = __builtin_fmaf(-q, b, a);
+  return __builtin_fmaf(r, rb, q);
+}
+
+// e^x from the hardware 2^t (v_exp_f32, about one ulp) at t = RN(x * L),
+// L = RN(log2 e), corrected by the part of x * log2 e that t leaves out:
+// e = (x * L - t) + x * (log2 e - L), the first term exact from one fma, so
+// x * log2 e = t + e to within |x| * 2^-48, and 2^(t + e) = 2^t (1 + e ln 2)
+// to within e^2 < 1e-10.  Within about two ulp of e^x over the normal range
+// (the product t alone would lose up to |x| * 6e-8 relative).  Inputs below
+// -200 are clamped, where the result underflows to 0 either way, so -inf
+// gives 0 and NaN stays NaN.
+NK_DEVICE float exp_acc(float x) {
+  constexpr float L = 1.44269502f;        // RN(log2 e)
+  constexpr float LLO = 1.925963033e-8f;  // log2 e - L
+  constexpr float LN2 = 0.693147182f;
+  x = x < -200.f ? -200.f : x;
+  const float t = x * L;
+  const float e = __builtin_fmaf(x, LLO, __builtin_fmaf(x, L, -t));
+  const float p = __builtin_amdgcn_exp2f(t);
+  return __builtin_fmaf(p, e * LN2, p);
+}
+
 NK_DEVICE float f16_to_f32(uint16_t h) {
   _Float16 v;
   __builtin_memcpy(&v, &h, 2);
@@ -204,12 +231,41 @@ NK_DEVICE uint32_t h16_of(const uint4 &v, int e) {
   return (e & 1) ? (w >> 16) : (w & 0xffffu);
 }
 
+// Buffer resource over `bytes` bytes at p: a load past the end reads zeros
+// and a store past the end is dropped, so a partial row needs no branch
+// around its memory accesses.  NT sets the streaming (nontemporal) policy.
+NK_DEVICE __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+typedef unsigned int nk_u32x4 __attribute__((ext_vector_type(4)));
+template <bool NT>
+NK_DEVICE uint4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const nk_u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, NT ? 2 : 0);
+  return make_uint4(q[0], q[1], q[2], q[3]);
+}
+template <bool NT>
+NK_DEVICE void buf_st16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 v) {
+  const nk_u32x4 q = {v.x, v.y, v.z, v.w};
+  __builtin_amdgcn_raw_buffer_store_b128(q, r, off, 0, NT ? 2 : 0);
+}
+
 // Raw form of an 8-element chunk: U 16-byte words (1 for 2-byte types, 2 for
 // fp32).  Kernels issue every raw load of a row first, then decode, so all
 // of a thread's HBM requests are in flight together.
 template <typename T> struct Raw8 {
   static constexpr int U = sizeof(T) * 8 / 16;
   uint4 w[U];
+  // chunk at byte offset `off` of a buffer resource (zeros past its end)
+  template <bool NT>
+  NK_DEVICE void load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) w[u] = buf_ld16<NT>(r, off + 16 * u);
+  }
+  template <bool NT>
+  NK_DEVICE void store_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) const {
+#pragma unroll
+    for (int u = 0; u < U; ++u) buf_st16<NT>(r, off + 16 * u, w[u]);
+  }
   template <bool NT>
   NK_DEVICE void load(const T *p) {
 #pragma unroll

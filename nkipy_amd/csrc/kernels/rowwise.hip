@@ -15,8 +15,10 @@
 // before any arithmetic, so a thread's requests are all in flight together,
 // and each input byte is read from HBM once.  The loop variants take any n
 // and re-read the row (fallback only).
-// Arithmetic is fp32 whatever the storage type; exp is the accurate libm
-// expf (no exp2 shortcut) so fp32 softmax stays within 1e-5 of NumPy.
+// Arithmetic is fp32 whatever the storage type.  The register softmax takes
+// e^x from the hardware 2^t with the rounding error of t = x log2 e folded
+// back in (exp_acc, about two ulp), so fp32 softmax stays within 1e-5 of
+// NumPy; the loop fallback calls libm expf.
 
 #include "common.h"
 
@@ -33,56 +35,52 @@ struct SoftmaxArgs {
 // NTS selects streaming stores.  The one-wave rows (BLOCK 64) store through
 // the cache: measured on (2048, 4096) fp32, streaming stores there cost
 // 18.0 us against 14.4 us; the larger blocks measure the other way round.
+// The row is addressed through buffer resources of exactly n elements: the
+// chunks past its end load zeros and drop their stores, and are left out of
+// the max and the sum by a select, so no memory access sits behind a branch
+// (the compiler then waits for each load only where its chunk is used).
 template <typename TI, typename TO, int BLOCK, int CHUNKS, bool NTS = true>
 __device__ __forceinline__ void softmax_reg_body(const SoftmaxArgs &a) {
   __shared__ float red[BLOCK / 64];
   const int64_t row = blockIdx.x;
   const int n = a.n;
-  const TI *x = reinterpret_cast<const TI *>(a.x) + row * n;
-  TO *y = reinterpret_cast<TO *>(a.y) + row * n;
+  const auto xr = buf_rsrc(reinterpret_cast<const TI *>(a.x) + row * n, (uint32_t)n * sizeof(TI));
+  const auto yr = buf_rsrc(reinterpret_cast<TO *>(a.y) + row * n, (uint32_t)n * sizeof(TO));
   const int tid = threadIdx.x;
   Raw8<TI> raw[CHUNKS];
 #pragma unroll
-  for (int c = 0; c < CHUNKS; ++c) {
-    const int idx = (c * BLOCK + tid) * 8;
-    if (idx < n) raw[c].template load<true>(x + idx);
-  }
+  for (int c = 0; c < CHUNKS; ++c) raw[c].template load_buf<true>(xr, (c * BLOCK + tid) * 8 * sizeof(TI));
   float v[CHUNKS][8];
   float m = -INFINITY;
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
-    const int idx = (c * BLOCK + tid) * 8;
-    if (idx < n) {
-      decode8(raw[c], v[c]);
+    decode8(raw[c], v[c]);
+    float mc = v[c][0];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) m = fmaxf(m, v[c][j]);
-    }
+    for (int j = 1; j < 8; ++j) mc = fmaxf(mc, v[c][j]);
+    m = (c * BLOCK + tid) * 8 < n ? fmaxf(m, mc) : m;
   }
   m = block_max<BLOCK>(m, red);
   float s = 0.f;
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
-    const int idx = (c * BLOCK + tid) * 8;
-    if (idx < n) {
+    float sc = 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        v[c][j] = expf(v[c][j] - m);
-        s += v[c][j];
-      }
+    for (int j = 0; j < 8; ++j) {
+      v[c][j] = exp_acc(v[c][j] - m);
+      sc += v[c][j];
     }
+    s += (c * BLOCK + tid) * 8 < n ? sc : 0.f;
   }
   s = block_sum<BLOCK>(s, red);
   const float inv_s = 1.0f / s;
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
-    const int idx = (c * BLOCK + tid) * 8;
-    if (idx < n) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[c][j] = div_rn(v[c][j], s, inv_s);
-      Raw8<TO> o;
-      encode8(v[c], o);
-      o.template store<NTS>(y + idx);
-    }
+    for (int j = 0; j < 8; ++j) v[c][j] = div_rn_finite(v[c][j], s, inv_s);
+    Raw8<TO> o;
+    encode8(v[c], o);
+    o.template store_buf<NTS>(yr, (c * BLOCK + tid) * 8 * sizeof(TO));
   }
 }
 
@@ -166,53 +164,53 @@ template <> __device__ __forceinline__ float round_to<f16>(float v) {
 }
 
 // RES (residual present) is a template parameter so that the residual loads
-// are issued together with the x loads, not behind a runtime branch.
+// are issued together with the x loads, not behind a runtime branch.  Rows
+// are addressed through buffer resources of exactly n elements: chunks past
+// the end load zeros (adding nothing to the sum of squares) and drop their
+// stores, so no memory access sits behind a branch.
 template <typename T, int BLOCK, int CHUNKS, bool RES>
 __device__ __forceinline__ void rmsnorm_reg_body(const RmsNormArgs &a) {
   __shared__ float red[BLOCK / 64];
   const int64_t row = blockIdx.x;
   const int n = a.n;
   const int flags = a.flags;
-  const T *x = reinterpret_cast<const T *>(a.x) + row * n;
-  const T *r = reinterpret_cast<const T *>(a.r) + row * n;
-  const T *w = reinterpret_cast<const T *>(a.w);
-  T *y = reinterpret_cast<T *>(a.y) + row * n;
-  T *h = reinterpret_cast<T *>(a.h) + row * n;
+  const uint32_t rb = (uint32_t)n * sizeof(T);
+  const auto xr = buf_rsrc(reinterpret_cast<const T *>(a.x) + row * n, rb);
+  const auto rr_ = buf_rsrc(RES ? reinterpret_cast<const T *>(a.r) + row * n : nullptr, RES ? rb : 0);
+  const auto wr = buf_rsrc(a.w, (flags & NK_RMS_W) ? rb : 0);
+  const auto yr = buf_rsrc(reinterpret_cast<T *>(a.y) + row * n, rb);
+  const auto hr = buf_rsrc((flags & NK_RMS_WRITE_H) ? reinterpret_cast<T *>(a.h) + row * n : nullptr,
+                           (flags & NK_RMS_WRITE_H) ? rb : 0);
   const int tid = threadIdx.x;
-  Raw8<T> xr[CHUNKS], rr[CHUNKS];
+  Raw8<T> xv[CHUNKS], rv_[CHUNKS];
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
-    const int idx = (c * BLOCK + tid) * 8;
-    if (idx < n) {
-      xr[c].template load<true>(x + idx);
-      if (RES) rr[c].template load<true>(r + idx);
-    }
+    const uint32_t off = (c * BLOCK + tid) * 8 * sizeof(T);
+    xv[c].template load_buf<true>(xr, off);
+    if (RES) rv_[c].template load_buf<true>(rr_, off);
   }
   float v[CHUNKS][8];
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
-    const int idx = (c * BLOCK + tid) * 8;
-    if (idx < n) {
-      decode8(xr[c], v[c]);
-      if (RES) {
-        float rv[8];
-        decode8(rr[c], rv);
+    decode8(xv[c], v[c]);
+    if (RES) {
+      float rv[8];
+      decode8(rv_[c], rv);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[c][j] += rv[j];
-        if (flags & NK_RMS_ROUND_H) {
+      for (int j = 0; j < 8; ++j) v[c][j] += rv[j];
+      if (flags & NK_RMS_ROUND_H) {
 #pragma unroll
-          for (int j = 0; j < 8; ++j) v[c][j] = round_to<T>(v[c][j]);
-        }
-        if (flags & NK_RMS_WRITE_H) {
-          Raw8<T> o;
-          encode8(v[c], o);
-          o.template store<true>(h + idx);
-        }
+        for (int j = 0; j < 8; ++j) v[c][j] = round_to<T>(v[c][j]);
       }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ss += v[c][j] * v[c][j];
+      if (flags & NK_RMS_WRITE_H) {
+        Raw8<T> o;
+        encode8(v[c], o);
+        o.template store_buf<true>(hr, (c * BLOCK + tid) * 8 * sizeof(T));
+      }
     }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += v[c][j] * v[c][j];
   }
   ss = block_sum<BLOCK>(ss, red);
   const float ms = ss / (float)n;
@@ -220,20 +218,22 @@ __device__ __forceinline__ void rmsnorm_reg_body(const RmsNormArgs &a) {
   const float inv = 1.0f / s;
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
-    const int idx = (c * BLOCK + tid) * 8;
-    if (idx < n) {
-      float wv[8];
-      if (flags & NK_RMS_W) Vec8<T>::load(w + idx, wv);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float q = (flags & NK_RMS_MUL_RECIP) ? v[c][j] * inv : div_rn(v[c][j], s, inv);
-        if (flags & NK_RMS_W) q = q * wv[j];
-        v[c][j] = q;
-      }
-      Raw8<T> o;
-      encode8(v[c], o);
-      o.template store<true>(y + idx);
+    const uint32_t off = (c * BLOCK + tid) * 8 * sizeof(T);
+    float wv[8];
+    if (flags & NK_RMS_W) {
+      Raw8<T> wraw;
+      wraw.template load_buf<false>(wr, off);
+      decode8(wraw, wv);
     }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float q = (flags & NK_RMS_MUL_RECIP) ? v[c][j] * inv : div_rn(v[c][j], s, inv);
+      if (flags & NK_RMS_W) q = q * wv[j];
+      v[c][j] = q;
+    }
+    Raw8<T> o;
+    encode8(v[c], o);
+    o.template store_buf<true>(yr, off);
   }
 }
 
