@@ -32,9 +32,10 @@ struct SoftmaxArgs {
   int32_t pad;
 };
 
-// NTS selects streaming stores.  The one-wave rows (BLOCK 64) store through
-// the cache: measured on (2048, 4096) fp32, streaming stores there cost
-// 18.0 us against 14.4 us; the larger blocks measure the other way round.
+// Loads go through the cache; NTS selects streaming stores.  Measured on
+// (2048, 4096) fp32 (us, cached / streaming loads): one wave x 8 chunks with
+// cached stores 13.8 / 14.4, with streaming stores 18.8 / 18.6; 512 x 1
+// with streaming stores 14.6 / 14.8 and cached 15.2 / 16.0.
 // The row is addressed through buffer resources of exactly n elements: the
 // chunks past its end load zeros and drop their stores, and are left out of
 // the max and the sum by a select, so no memory access sits behind a branch
@@ -49,7 +50,7 @@ __device__ __forceinline__ void softmax_reg_body(const SoftmaxArgs &a) {
   const int tid = threadIdx.x;
   Raw8<TI> raw[CHUNKS];
 #pragma unroll
-  for (int c = 0; c < CHUNKS; ++c) raw[c].template load_buf<true>(xr, (c * BLOCK + tid) * 8 * sizeof(TI));
+  for (int c = 0; c < CHUNKS; ++c) raw[c].template load_buf<false>(xr, (c * BLOCK + tid) * 8 * sizeof(TI));
   float v[CHUNKS][8];
   float m = -INFINITY;
 #pragma unroll
@@ -164,7 +165,10 @@ template <> __device__ __forceinline__ float round_to<f16>(float v) {
 }
 
 // RES (residual present) is a template parameter so that the residual loads
-// are issued together with the x loads, not behind a runtime branch.  Rows
+// are issued together with the x loads, not behind a runtime branch.  With
+// a residual the loads stream (nontemporal), without one they go through the
+// cache: bf16 (8192, 4096) measured 33.8 us streaming / 35.9 us cached with
+// a residual, 24.0 us / 20.9 us without.  Rows
 // are addressed through buffer resources of exactly n elements: chunks past
 // the end load zeros (adding nothing to the sum of squares) and drop their
 // stores, so no memory access sits behind a branch.
@@ -186,8 +190,8 @@ __device__ __forceinline__ void rmsnorm_reg_body(const RmsNormArgs &a) {
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
     const uint32_t off = (c * BLOCK + tid) * 8 * sizeof(T);
-    xv[c].template load_buf<true>(xr, off);
-    if (RES) rv_[c].template load_buf<true>(rr_, off);
+    xv[c].template load_buf<RES>(xr, off);
+    if (RES) rv_[c].template load_buf<RES>(rr_, off);
   }
   float v[CHUNKS][8];
   float ss = 0.f;
