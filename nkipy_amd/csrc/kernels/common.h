@@ -238,10 +238,16 @@ NK_DEVICE __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
 }
 typedef unsigned int nk_u32x4 __attribute__((ext_vector_type(4)));
+// `soff` is a wave-uniform byte offset (an SGPR operand of the instruction).
 template <bool NT>
-NK_DEVICE uint4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const nk_u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, NT ? 2 : 0);
+NK_DEVICE uint4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff = 0) {
+  const nk_u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, NT ? 2 : 0);
   return make_uint4(q[0], q[1], q[2], q[3]);
+}
+typedef unsigned int nk_u32x2 __attribute__((ext_vector_type(2)));
+NK_DEVICE void buf_st8(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff, uint2 v) {
+  const nk_u32x2 q = {v.x, v.y};
+  __builtin_amdgcn_raw_buffer_store_b64(q, r, off, soff, 0);
 }
 template <bool NT>
 NK_DEVICE void buf_st16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 v) {

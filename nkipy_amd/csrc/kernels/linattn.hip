@@ -194,8 +194,10 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
   __shared__ __attribute__((aligned(1024))) uint8_t V1[LC * 256];
   __shared__ __attribute__((aligned(1024))) uint8_t ST0[LDV * 256];
   __shared__ __attribute__((aligned(1024))) uint8_t ST1[LDV * 256];
-  __shared__ __attribute__((aligned(16))) uint8_t Z0[LD * 2];
-  __shared__ __attribute__((aligned(16))) uint8_t Z1[LD * 2];
+  // z / 256 (first 256 bytes) and 256 bytes of zeros: the normaliser tile's
+  // A operand reads z in lanes l16 == 0 and zeros elsewhere
+  __shared__ __attribute__((aligned(16))) uint8_t Z0[LD * 4];
+  __shared__ __attribute__((aligned(16))) uint8_t Z1[LD * 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -215,25 +217,29 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
   // ---------------- input staging -----------------------------------------
   // query wave W: q rows 16W + l16, d = 32 st + 8 grp (its own fragments);
   // state thread u = tid - 256: k chunks u + 256 i (row / 16, 8 columns);
-  // every thread: v chunks tid + 512 i.  Plain (cached) loads.
+  // every thread: v chunks tid + 512 i.  Plain (cached) loads through buffer
+  // resources over the segment: a lane-constant byte offset plus the chunk's
+  // offset as a scalar operand, so no per-chunk address arithmetic.
+  const int64_t seg0 = base + (int64_t)c0 * LC * LD;
+  const uint32_t seg_bytes = (uint32_t)nchunks * LC * LD * 2;
+  const auto rq = buf_rsrc(a.q + seg0, seg_bytes);
+  const auto rk = buf_rsrc(a.k + seg0, seg_bytes);
+  const auto rv = buf_rsrc(a.v + seg0, seg_bytes);
+  const auto ro = buf_rsrc(a.o + seg0, seg_bytes);
+  const uint32_t xoff = qwave ? (uint32_t)(((16 * wave + l16) * LD + 8 * grp) * 2)
+                              : (uint32_t)((((tid - 256) >> 4) * LD + ((tid - 256) & 15) * 8) * 2);
+  const uint32_t vloff = (uint32_t)(((tid >> 4) * LDV + (tid & 15) * 8) * 2);
   auto load_raw = [&](Raw &r, int c) {
-    const int64_t cb = base + (int64_t)(c0 + c) * LC * LD;
+    const uint32_t cs = (uint32_t)c * (LC * LD * 2);
     if (qwave) {
 #pragma unroll
-      for (int st = 0; st < 4; ++st)
-        r.x[st] = *reinterpret_cast<const uint4 *>(a.q + cb + (16 * wave + l16) * LD + 32 * st + 8 * grp);
+      for (int st = 0; st < 4; ++st) r.x[st] = buf_ld16<false>(rq, xoff + 64 * st, cs);
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int idx = tid - 256 + 256 * i;
-        r.x[i] = *reinterpret_cast<const uint4 *>(a.k + cb + (idx >> 4) * LD + (idx & 15) * 8);
-      }
+      for (int i = 0; i < 4; ++i) r.x[i] = buf_ld16<false>(rk, xoff, cs + 16 * LD * 2 * i);
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int idx = tid + 512 * i;
-      r.v[i] = *reinterpret_cast<const uint4 *>(a.v + cb + (idx >> 4) * LDV + (idx & 15) * 8);
-    }
+    for (int i = 0; i < 2; ++i) r.v[i] = buf_ld16<false>(rv, vloff, cs + 32 * LDV * 2 * i);
   };
   // phi(Q) fragments of the next chunk (query waves, registers)
   f16x8_t qf[4];
@@ -312,6 +318,7 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
   // for the V^T A^T part, so row 0 of that tile is den / 256 (z / 256 keeps
   // the fp16 copy of z finite up to z = 2^24; the power-of-two scale is
   // exact).
+  const int zsel = l16 == 0 ? 0 : LD * 2;  // z row or the zero block
   f16x8_t zrow_ones;  // A operand of the normaliser tile in V^T A^T
 #pragma unroll
   for (int e = 0; e < 8; ++e) zrow_ones[e] = (_Float16)(l16 == 0 ? 0.00390625f : 0.f);
@@ -332,11 +339,7 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
             *reinterpret_cast<const f16x8_t *>(cur.St + o256(16 * jt + l16, (32 * st + 8 * grp) * 2));
         ot[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sf, qf[st], ot[jt], 0, 0, 0);
       }
-      f16x8_t zf = *reinterpret_cast<const f16x8_t *>(cur.z + (32 * st + 8 * grp) * 2);
-      if (l16 != 0) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) zf[e] = (_Float16)0.f;
-      }
+      const f16x8_t zf = *reinterpret_cast<const f16x8_t *>(cur.z + zsel + (32 * st + 8 * grp) * 2);
       ot[8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(zf, qf[st], ot[8], 0, 0, 0);
     }
 
@@ -384,15 +387,17 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
     }
     // den: row 0 of tile 8 sits in lane l16 (group 0), element 0
     const float den = 256.0f * __shfl(ot[8][0], l16, 64);
-    // normalise and store: o[t][j], 4 consecutive j per lane
+    // normalise and store: o[t][j], 4 consecutive j per lane (row
+    // t = 64 c + 16 W + l16 of the segment)
     {
       const float inv = 1.0f / den;
-      const int64_t t = (int64_t)(c0 + c) * LC + 16 * W + l16;
+      const uint32_t ooff = (uint32_t)(((16 * W + l16) * LDV + 4 * grp) * 2);
+      const uint32_t cs = (uint32_t)c * (LC * LDV * 2);
 #pragma unroll
       for (int jt = 0; jt < 8; ++jt) {
         const uint32_t w0 = pack_bf16x2(ot[jt][0] * inv, ot[jt][1] * inv);
         const uint32_t w1 = pack_bf16x2(ot[jt][2] * inv, ot[jt][3] * inv);
-        *reinterpret_cast<uint2 *>(a.o + base + t * LDV + 16 * jt + 4 * grp) = make_uint2(w0, w1);
+        buf_st8(ro, ooff + 32 * jt, cs, make_uint2(w0, w1));
       }
     }
   };
@@ -433,6 +438,7 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
 
   const Stage s0{K0, V0, ST0, Z0}, s1{K1, V1, ST1, Z1};
   if (!qwave) write_state(s0, wave - 4);  // initial S^T and z / 256
+  if (tid < 32) *reinterpret_cast<uint4 *>((tid < 16 ? Z0 : Z1) + LD * 2 + 16 * (tid & 15)) = make_uint4(0, 0, 0, 0);
   Raw ra{}, rb{};
   load_raw(ra, 0);
   load_raw(rb, min(1, nchunks - 1));
