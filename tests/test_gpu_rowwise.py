@@ -46,7 +46,10 @@ def test_softmax_notebook_golden(gpu):
         np.testing.assert_allclose(y, case["output"], rtol=0, atol=1e-6)
 
 
-@pytest.mark.parametrize("shape", [(1, 1), (3, 100), (7, 128), (5, 8192), (2, 20000), (2, 3, 64), (4, 2)])
+# (3, 3000), (2, 4088), (6, 1000): rows that end inside the last chunk of a
+# register variant (loads past the end read zeros, stores are dropped)
+@pytest.mark.parametrize("shape", [(1, 1), (3, 100), (7, 128), (5, 8192), (2, 20000), (2, 3, 64), (4, 2),
+                                   (3, 3000), (2, 4088), (6, 1000)])
 def test_softmax_ragged_shapes(gpu, shape):
     rng = np.random.default_rng(sum(shape))
     x = (rng.standard_normal(shape) * 4).astype(np.float32)
@@ -91,7 +94,7 @@ def test_residual_rmsnorm_config_parity(gpu):
     assert np.mean(y == ref) > 0.99
 
 
-@pytest.mark.parametrize("shape", [(1, 8), (3, 40), (5, 4096), (2, 3, 96), (4, 9000), (2, 13)])
+@pytest.mark.parametrize("shape", [(1, 8), (3, 40), (5, 4096), (2, 3, 96), (4, 9000), (2, 13), (3, 3000), (2, 1000)])
 def test_rmsnorm_shapes_f32(gpu, shape):
     rng = np.random.default_rng(len(shape))
     x = rng.standard_normal(shape).astype(np.float32)
@@ -119,6 +122,15 @@ def test_rmsnorm_llama_reciprocal_form(gpu):
     assert _kinds(llama_norm, x, w) == ["rmsnorm"]
     y = baremetal_jit(llama_norm)(x, w)
     assert _rel(y, K.rmsnorm_f64(x, w, 1e-5)) <= 1e-5
+
+
+@pytest.mark.parametrize("shape", [(5, 1000), (3, 3000), (2, 4088)])
+def test_residual_rmsnorm_partial_chunks(gpu, shape):
+    """Rows ending inside a register variant's last chunk (bf16, residual)."""
+    x, r, w = _bf16_inputs(shape, seed=shape[1])
+    args = (dt.to_bf16(x), dt.to_bf16(r), dt.to_bf16(w), 1e-6)
+    y = dt.to_float32(baremetal_jit(residual_rmsnorm_kernel)(*args))
+    np.testing.assert_allclose(y, K.residual_rmsnorm_bf16(x, r, w, 1e-6), rtol=2e-2, atol=0)
 
 
 def test_residual_rmsnorm_with_residual_output(gpu):
