@@ -39,7 +39,11 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 #define BN 256
 #define BK 64
 #define NTHREADS 256
-#define GROUP_M 8
+// Tile rows per group of the XCD-local walk.  Measured on MI355X (us, 8-wave
+// kernel, GROUP_M 1 / 2 / 4 / 8): NT bf16 16384x6144x4096 731 / 709 / 685 /
+// 771, NT fp8 same shape 692 / 694 / 668 / 730, NN 4096x4096x14336 353 /
+// 352 / 351 / 358, fp8 SwiGLU 16384x14336x4096 unchanged.
+#define GROUP_M 4
 
 enum {
   GEMM_BIAS = 1,      // + bias[col] (bf16)
