@@ -64,7 +64,8 @@ struct GemmArgs {
   int64_t M, N, K;     // N = output columns
   int64_t lda, ldb, ldc;
   int32_t tiles_m, tiles_n;
-  int32_t flags, pad;
+  int32_t flags;
+  int32_t group_m;     // tile rows per group of the tile walk; 0: GROUP_M
 };
 
 // ---------------------------------------------------------------------------
@@ -518,10 +519,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a, int &tm, int &tn) {
   const int ntiles = a.tiles_m * a.tiles_n;
   int pid = blockIdx.x;
   if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
-  const int in_group = GROUP_M * a.tiles_n;
+  const int gm = a.group_m > 0 ? a.group_m : GROUP_M;
+  const int in_group = gm * a.tiles_n;
   const int group = pid / in_group;
-  const int first_m = group * GROUP_M;
-  const int gsize = min(a.tiles_m - first_m, GROUP_M);
+  const int first_m = group * gm;
+  const int gsize = min(a.tiles_m - first_m, gm);
   tm = first_m + (pid % in_group) % gsize;
   tn = (pid % in_group) / gsize;
 }

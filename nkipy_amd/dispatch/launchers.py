@@ -223,7 +223,7 @@ class GemmArgs(ctypes.Structure):
         ("M", ctypes.c_int64), ("N", ctypes.c_int64), ("K", ctypes.c_int64),
         ("lda", ctypes.c_int64), ("ldb", ctypes.c_int64), ("ldc", ctypes.c_int64),
         ("tiles_m", ctypes.c_int32), ("tiles_n", ctypes.c_int32),
-        ("flags", ctypes.c_int32), ("pad", ctypes.c_int32),
+        ("flags", ctypes.c_int32), ("group_m", ctypes.c_int32),
     ]
 
 
