@@ -191,3 +191,26 @@ def test_gemm_fp8_nn_scales(gpu, shape):
     _run(gpu, LA.gemm(xd.ptr, wd.ptr, cd.ptr, M, Nn, Kk, layout="nn", b_dtype=dt.float8_e4m3fn,
                       c_dtype=dt.bfloat16, scale_ptr=sd.ptr))
     _close(dt.to_float32(cd.numpy()), ref)
+
+
+@pytest.mark.parametrize("pp", PP)
+@pytest.mark.parametrize("group_m", [1, 3, 6])
+def test_gemm_tile_walk_group(gpu, group_m, pp):
+    """The tile-walk group size only reorders tiles: results are bit-identical
+    to the default walk, including a ragged edge (tiles_m = 5, tiles_n = 3)."""
+    M, Nn, Kk = 1100, 700, 320
+    rng = np.random.default_rng(group_m)
+    a = _bf16(rng, (M, Kk))
+    b = _bf16(rng, (Nn, Kk), 0.05)
+    ad = DeviceTensor.from_numpy(dt.to_bf16(a))
+    bd = DeviceTensor.from_numpy(dt.to_bf16(b))
+    outs = []
+    for g in (0, group_m):
+        cd = DeviceTensor.empty((M, Nn), dt.bfloat16)
+        launch = LA.gemm(ad.ptr, bd.ptr, cd.ptr, M, Nn, Kk, layout="nt", b_dtype=dt.bfloat16,
+                         c_dtype=dt.bfloat16, pingpong=pp)
+        launch.args.group_m = g
+        _run(gpu, launch)
+        outs.append(cd.numpy())
+    np.testing.assert_array_equal(outs[0], outs[1])
+    _close(dt.to_float32(outs[1]), a.astype(np.float64) @ b.T.astype(np.float64))
