@@ -389,7 +389,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU; --gpus {args.gpus} is not supported "
-              "(the hot path has no multi-GPU leg in this build)", file=sys.stderr)
+              "(the kernels run on one GPU's share of the work; no multi-GPU leg is implemented)", file=sys.stderr)
         sys.exit(2)
 
     from nkipy_amd.runtime.hip import get_runtime

@@ -6,7 +6,8 @@ kernels: the reference runs a kernel by calling the NumPy function directly
 formula.  Each function cites the reference file:line it follows.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
-import this package, and only as the checker or the reported CPU baseline.
+import this package, and only as the reference that results are compared
+with or as the reported CPU baseline.
 The product (nkipy_amd) never imports it.
 
 Pins (tests/test_oracle.py):
