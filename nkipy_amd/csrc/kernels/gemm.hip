@@ -50,7 +50,11 @@ enum {
   GEMM_SCALE = 2,     // * scale[col] (fp32), per output column (fp8 weights)
   GEMM_RESID = 4,     // + residual[row][col] (same dtype as C)
   GEMM_VEC = 8,       // C / residual rows allow aligned 4-element vector access
+  GEMM_RND_BIAS = 16, // round the (scaled) product to bf16 before the bias add
+  GEMM_RND_RESID = 32,// round to bf16 before the residual add
 };
+// The rounding flags keep the cast points of the traced NumPy code: e.g.
+// ``z + (x @ w).astype(bf16)`` rounds the product before the add.
 
 struct GemmArgs {
   const void *A;       // M x K
@@ -72,6 +76,14 @@ struct GemmArgs {
 // element helpers
 // ---------------------------------------------------------------------------
 // fp8 -> bf16 staging uses nk::e4m3x8_to_bf16x8 (common.h)
+
+// (product + bias) + residual with the optional bf16 roundings in between
+__device__ __forceinline__ float epilogue(int flags, float prod, float bias, float resid) {
+  if (flags & GEMM_RND_BIAS) prod = bf16_to_f32(f32_to_bf16(prod));
+  float v = prod + bias;
+  if (flags & GEMM_RND_RESID) v = bf16_to_f32(f32_to_bf16(v));
+  return v + resid;
+}
 
 template <typename TC> struct OutT;
 template <> struct OutT<bf16> {
@@ -504,7 +516,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs &a, const f32x16 (&
           }
           float v[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = acc[i][j][q * 4 + e] * sc[q * 4 + e] + bi[q * 4 + e] + r4[e];
+          for (int e = 0; e < 4; ++e) v[e] = epilogue(a.flags, acc[i][j][q * 4 + e] * sc[q * 4 + e],
+                                                      bi[q * 4 + e], r4[e]);
           put4(row, col, v);
         }
       }
@@ -811,7 +824,7 @@ __device__ __forceinline__ void gemm_epilogue16(const GemmArgs &a, const f32x4 (
           }
         }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][e] * sc[e] + bi[e] + r4[e];
+        for (int e = 0; e < 4; ++e) v[e] = epilogue(a.flags, acc[i][j][e] * sc[e], bi[e], r4[e]);
       }
       put4(row, col, v);
     }

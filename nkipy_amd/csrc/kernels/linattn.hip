@@ -50,8 +50,12 @@
 // of attention, so the information sits in deviations from 1 and in
 // A = phi(Q) phi(K)^T ~ d + small terms; bf16's 8-bit significand loses about
 // 5% of those deviations, fp16's 11 bits keep the output within 0.4% of the
-// fp32 recurrence (same MFMA rate on gfx950).  Limit: the fp16 state copy
-// overflows if an entry of S exceeds 65504.
+// fp32 recurrence (same MFMA rate on gfx950).  Range: the fp16 copies carry
+// S / 256, z / 256 and A / 256 (A = phi(Q) phi(K)^T), so numerator and
+// normaliser share one power-of-two scale (exact) and the quotient is
+// unchanged; the copies stay finite while |S|, z and A are below 2^24
+// (e.g. v of mean 8 over 2^21 tokens).  V and phi(K) enter as fp16 inputs:
+// |v| and k must stay below 65504.
 
 #include "common.h"
 
@@ -289,16 +293,17 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
 #pragma unroll
   for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
 
-  // fp16 S^T and z / 256 into a stage: lane holds column j = 32 t + l32 and
-  // rows d = 32w + 8 (r/4) + 4 lhi + r%4
+  // fp16 S^T / 256 and z / 256 into a stage: lane holds column j = 32 t +
+  // l32 and rows d = 32w + 8 (r/4) + 4 lhi + r%4
   auto write_state = [&](const Stage &nxt, int w) {
+    constexpr float k256 = 0.00390625f;
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
       const int d = 32 * w + 8 * g4 + 4 * lhi;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const uint32_t w0 = pack_f16x2(S[t][4 * g4 + 0], S[t][4 * g4 + 1]);
-        const uint32_t w1 = pack_f16x2(S[t][4 * g4 + 2], S[t][4 * g4 + 3]);
+        const uint32_t w0 = pack_f16x2(S[t][4 * g4 + 0] * k256, S[t][4 * g4 + 1] * k256);
+        const uint32_t w1 = pack_f16x2(S[t][4 * g4 + 2] * k256, S[t][4 * g4 + 3] * k256);
         *reinterpret_cast<uint2 *>(nxt.St + o256(32 * t + l32, d * 2)) = make_uint2(w0, w1);
       }
       if (l32 == 0) {
@@ -313,19 +318,20 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
   // Query wave W (queries 16W..16W+15) is specialised per W so the causal
   // structure (key tiles 0..W) is static: one basic block per chunk, in which
   // the compiler interleaves the staging of the next chunk with the MFMA
-  // chains.  The normaliser comes out of the same MFMAs as a ninth output
-  // tile: its A operand row 0 is z_prev / 256 for the S^T Q^T part and 1/256
-  // for the V^T A^T part, so row 0 of that tile is den / 256 (z / 256 keeps
-  // the fp16 copy of z finite up to z = 2^24; the power-of-two scale is
-  // exact).
+  // chains.  Every fp16 operand carries a factor 1/256: S^T / 256 from the
+  // state copy, A^T / 256 converted from the accumulators, so the output
+  // tiles hold num / 256.  The normaliser comes out of the same MFMAs as a
+  // ninth output tile: its A operand row 0 is z_prev / 256 for the S^T Q^T
+  // part and 1 for the V^T (A^T / 256) part, so row 0 of that tile is
+  // den / 256 and the quotient needs no rescale.
   const int zsel = l16 == 0 ? 0 : LD * 2;  // z row or the zero block
   f16x8_t zrow_ones;  // A operand of the normaliser tile in V^T A^T
 #pragma unroll
-  for (int e = 0; e < 8; ++e) zrow_ones[e] = (_Float16)(l16 == 0 ? 0.00390625f : 0.f);
+  for (int e = 0; e < 8; ++e) zrow_ones[e] = (_Float16)(l16 == 0 ? 1.0f : 0.f);
   auto query_side = [&](const Stage &cur, int c, auto wtag) __attribute__((always_inline)) {
     constexpr int W = decltype(wtag)::value;
-    // O^T tiles 0..7: rows j = 16 jt + 4 grp + r; tile 8 row 0: den / 256
-    // (column = query l16)
+    // O^T tiles 0..7: rows j = 16 jt + 4 grp + r, num / 256; tile 8 row 0:
+    // den / 256 (column = query l16)
     f32x4 ot[9];
 #pragma unroll
     for (int jt = 0; jt < 9; ++jt)
@@ -368,11 +374,11 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       if (2 * p > W) continue;
-      f16x8_t pf;
+      f16x8_t pf;  // A^T / 256
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        pf[e] = (_Float16)at[2 * p][e];
-        pf[4 + e] = (_Float16)at[2 * p + 1][e];
+        pf[e] = (_Float16)(at[2 * p][e] * 0.00390625f);
+        pf[4 + e] = (_Float16)(at[2 * p + 1][e] * 0.00390625f);
       }
 #pragma unroll
       for (int jt = 0; jt < 8; ++jt) {
@@ -385,8 +391,8 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
       }
       ot[8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(zrow_ones, pf, ot[8], 0, 0, 0);
     }
-    // den: row 0 of tile 8 sits in lane l16 (group 0), element 0
-    const float den = 256.0f * __shfl(ot[8][0], l16, 64);
+    // den / 256: row 0 of tile 8 sits in lane l16 (group 0), element 0
+    const float den = __shfl(ot[8][0], l16, 64);
     // normalise and store: o[t][j], 4 consecutive j per lane (row
     // t = 64 c + 16 W + l16 of the segment)
     {

@@ -231,6 +231,8 @@ GEMM_BIAS = 1
 GEMM_SCALE = 2
 GEMM_RESID = 4
 GEMM_VEC = 8
+GEMM_RND_BIAS = 16
+GEMM_RND_RESID = 32
 GEMM_BM = 256
 GEMM_BN = 256
 
@@ -238,7 +240,8 @@ GEMM_BN = 256
 def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: str,
          b_dtype, c_dtype, lda: int = None, ldb: int = None, ldc: int = None,
          bias_ptr: int = 0, scale_ptr: int = 0, resid_ptr: int = 0,
-         up_ptr: int = 0, up_scale_ptr: int = 0, pingpong: bool = None) -> Launch:
+         up_ptr: int = 0, up_scale_ptr: int = 0, pingpong: bool = None,
+         round_before_bias: bool = False, round_before_resid: bool = False) -> Launch:
     """C[M, N] = A[M, K] @ B (+ epilogue) on bf16 MFMA, fp32 accumulation.
 
     ``layout`` "nn": B is K x N row-major (ldb >= N); "nt": B is N x K
@@ -246,7 +249,9 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
     ``scale_ptr`` gives fp32 per-column scales).  With ``up_ptr`` the kernel
     computes the SwiGLU product silu(A @ B) * (A @ B_up) instead (B_up has the
     layout and leading dimension of B).  ``bias_ptr`` (bf16, N) and
-    ``resid_ptr`` (C dtype, M x N, leading dimension ldc) are added.
+    ``resid_ptr`` (C dtype, M x N, leading dimension ldc) are added;
+    ``round_before_bias`` / ``round_before_resid`` round the running value to
+    bf16 before that add (the cast points of ``(x @ w).astype(bf16) + r``).
     ``pingpong`` selects the 8-wave kernel (two waves per SIMD alternating
     between MFMAs and fragment loads; the default where it exists, i.e. for
     every layout except fp8 NN weights) or the 4-wave kernel.
@@ -293,6 +298,10 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
     if tiles_m * tiles_n >= 2**31:
         raise LaunchError("GEMM grid too large")
     flags = (GEMM_BIAS if bias_ptr else 0) | (GEMM_SCALE if scale_ptr else 0) | (GEMM_RESID if resid_ptr else 0)
+    if round_before_bias and bias_ptr:
+        flags |= GEMM_RND_BIAS
+    if round_before_resid and resid_ptr:
+        flags |= GEMM_RND_RESID
     # 4-element vector access to C (and the residual) when rows keep 8 / 16-byte alignment
     vbytes = 4 * c_dtype.itemsize
     if ldc % 4 == 0 and c_ptr % vbytes == 0 and (not resid_ptr or resid_ptr % vbytes == 0):

@@ -191,9 +191,8 @@ class Lowering:
             res = g.results[a.output_index]
             p = param_by_name[f"{a.param_name}.must_alias_input"]
             prod = res.node
-            readers = [u for u in self.users.get(p.id, []) if u is not prod]
-            late = prod is not None and any(order.get(id(u), -1) > order.get(id(prod), -1) for u in readers)
-            if late or prod is None:
+            late = prod is None or not self._reads_done_before(p, prod, order)
+            if late:
                 # the producer writes a staging temporary; a final copy moves
                 # it into the caller's (aliased) buffer
                 outv = Value(res.shape, res.dtype, None, name=res.name)
@@ -243,6 +242,43 @@ class Lowering:
         for res, outv in deferred:
             plan.steps.append(G.ProgramStep(f"write back {res.name}", G.flat_copy_program(res), outv))
         return plan
+
+    _INPLACE_OPS = ("dynamic_update_slice", "scatter_along_axis", "put_along_axis", "scatter_strided")
+
+    def _reads_done_before(self, p: Value, prod: Node, order: Dict[int, int]) -> bool:
+        """True when every read of parameter ``p`` happens in a step that runs
+        before ``prod``'s step, so ``prod`` may overwrite ``p``'s buffer.
+
+        A read is deferred when the reading node is not materialised (a
+        fused elementwise / layout node, or a reshape sharing ``p``'s
+        storage): it happens inside the step of a later consumer, so the
+        consumers are followed transitively.  ``prod`` itself may read ``p``
+        only as the operand it updates in place."""
+        limit = order[id(prod)]
+        work, seen = [p], {p.id}
+        while work:
+            x = work.pop()
+            for u in self.users.get(x.id, ()):
+                if u is prod:
+                    in_place_target = (x is p and prod.op in self._INPLACE_OPS and prod.inputs[0] is p
+                                       and not any(y is p for y in prod.inputs[1:]))
+                    if not in_place_target:
+                        return False
+                    continue
+                m = self.covered.get(id(u))
+                if m is not None:
+                    if order[id(m.last)] >= limit:
+                        return False
+                    continue
+                v = u.out
+                if v.id in self.mat and (v.id not in self.alias_reshape or v.id in self.result_ids):
+                    if order[id(u)] >= limit:
+                        return False
+                    continue
+                if v.id not in seen:  # evaluated later, inside a consumer's step
+                    seen.add(v.id)
+                    work.append(v)
+        return True
 
     # ------------------------------------------------------------------
     def _lower_node(self, n: Node, plan: Plan, inplace: bool) -> list:

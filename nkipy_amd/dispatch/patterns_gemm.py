@@ -142,7 +142,7 @@ class GemmMatch(Match):
     name = "gemm"
 
     def __init__(self, nodes, x: Value, w: Weight, out: Value, *, bias=None, resid=None,
-                 up: Weight = None, up_offset: int = 0, n_out: int = None):
+                 up: Weight = None, up_offset: int = 0, n_out: int = None, rnd=(False, False)):
         ins = [x, w.value] + ([w.scale] if w.scale is not None else [])
         if up is not None and up.value is not w.value:
             ins.append(up.value)
@@ -153,6 +153,7 @@ class GemmMatch(Match):
         self.x, self.w, self.out, self.bias, self.resid = x, w, out, bias, resid
         self.up, self.up_offset = up, up_offset
         self.n_out = n_out
+        self.rnd = rnd
 
     def steps(self, plan):
         x, w, out = self.x, self.w, self.out
@@ -162,6 +163,7 @@ class GemmMatch(Match):
         ldb = w.value.shape[1]
         up, off = self.up, self.up_offset
         bias, resid = self.bias, self.resid
+        rnd_bias, rnd_resid = self.rnd
 
         def make(addr):
             up_ptr = 0
@@ -174,7 +176,8 @@ class GemmMatch(Match):
                            bias_ptr=addr(bias) if bias is not None else 0,
                            scale_ptr=addr(w.scale) if w.scale is not None else 0,
                            resid_ptr=addr(resid) if resid is not None else 0,
-                           up_ptr=up_ptr, up_scale_ptr=up_scale)
+                           up_ptr=up_ptr, up_scale_ptr=up_scale,
+                           round_before_bias=rnd_bias, round_before_resid=rnd_resid)
 
         kind = "gemm_swiglu" if up is not None else "gemm"
         desc = (f"{'swiglu ' if up is not None else ''}gemm {w.layout} M={M} N={N} K={K} "
@@ -183,9 +186,20 @@ class GemmMatch(Match):
         return [LaunchStep(kind, desc, self.inputs, self.outputs, make)]
 
 
+class Epilogue:
+    """What a GEMM's epilogue folds in, with the traced code's cast points:
+    ``rnd_bias`` / ``rnd_resid`` say the running value was rounded to bf16
+    (a bf16 product, an ``astype``, a bf16 add) before that add."""
+
+    def __init__(self):
+        self.bias = self.resid = None
+        self.rnd_bias = self.rnd_resid = False
+
+
 def _fold_epilogue(L, v: Value, nodes: List[Node]):
     """Fold single-user bias / residual adds and a final cast after ``v``."""
-    bias = resid = None
+    ep = Epilogue()
+    rounded = v.dtype == dt.bfloat16  # the product itself is stored as bf16
     while True:
         us = _users_of(L, v)
         if v.id in L.result_ids or len(us) != 1:
@@ -194,27 +208,29 @@ def _fold_epilogue(L, v: Value, nodes: List[Node]):
         if u.op == "add" and u.out.dtype == v.dtype:
             other = u.inputs[1] if u.inputs[0] is v else u.inputs[0]
             cb = col_broadcast(other, v.shape)
-            if bias is None and resid is None and cb is not None and cb[0].dtype == dt.bfloat16:
-                bias = cb[0]
+            if ep.bias is None and ep.resid is None and cb is not None and cb[0].dtype == dt.bfloat16:
+                ep.bias, ep.rnd_bias = cb[0], rounded
                 nodes += [u] + cb[1]
                 v = u.out
+                rounded = v.dtype == dt.bfloat16
                 continue
-            ob, on = through_views(other)
-            if resid is None and other.shape == v.shape and other.dtype == v.dtype and \
+            if ep.resid is None and other.shape == v.shape and other.dtype == v.dtype and \
                     (other.node is None or other.node.op != "broadcast_in_dim"):
-                resid = other
+                ep.resid, ep.rnd_resid = other, rounded
                 nodes.append(u)
                 v = u.out
+                rounded = v.dtype == dt.bfloat16
                 continue
             break
         if u.op in ("convert", "copy") and u.out.dtype in (dt.bfloat16, dt.float32) and dt.is_float(v.dtype):
-            if resid is not None and u.out.dtype != v.dtype:
+            if ep.resid is not None and u.out.dtype != v.dtype:
                 break  # the residual must have the output dtype
             nodes.append(u)
             v = u.out
+            rounded = rounded or v.dtype == dt.bfloat16
             continue
         break
-    return v, bias, resid
+    return v, ep
 
 
 class GemmPattern:
@@ -237,12 +253,13 @@ class GemmPattern:
         if w.layout == "nn" and w.value.shape[1] % 8:
             return None
         nodes = [n] + xn + w.nodes
-        out, bias, resid = _fold_epilogue(L, n.out, nodes)
+        out, ep = _fold_epilogue(L, n.out, nodes)
         if out.dtype not in (dt.bfloat16, dt.float32):
             return None
-        if resid is not None and resid.dtype != out.dtype:
+        if ep.resid is not None and ep.resid.dtype != out.dtype:
             return None
-        return GemmMatch(nodes, x, w, out, bias=bias, resid=resid)
+        return GemmMatch(nodes, x, w, out, bias=ep.bias, resid=ep.resid,
+                         rnd=(ep.rnd_bias, ep.rnd_resid))
 
 
 # ---------------------------------------------------------------------------

@@ -142,8 +142,9 @@ class BoundPlan:
         self._sizes = (sz * n)(*[len(b) for b in blobs])
 
     def run(self):
-        from nkipy_amd.runtime.hip import _check
+        from nkipy_amd.runtime.hip import _check, check_current
 
+        check_current(self.rt, "plan")
         if self._n == 0:
             return
         _check(
@@ -189,6 +190,9 @@ class PlanExecutor:
 
     def bind(self, io_ptrs: Dict[str, int]) -> BoundPlan:
         """``io_ptrs``: input / output name -> device address."""
+        from nkipy_amd.runtime.hip import check_current
+
+        check_current(self.rt, "plan")
         plan = self.plan
         bases: Dict[int, int] = {i: b.ptr for i, b in self._owned.items()}
         for name, idx in plan.input_buffers.items():
@@ -206,6 +210,12 @@ class PlanExecutor:
 
     def run(self, io_ptrs: Dict[str, int]):
         self.bind(io_ptrs).run()
+
+    def forget(self):
+        """Drop every bound launch list and owned buffer without touching the
+        device (the runtime they belong to is gone)."""
+        self._owned.clear()
+        self._bound.clear()
 
     def close(self):
         for b in self._owned.values():

@@ -44,6 +44,7 @@ from nkipy_amd.core.logger import get_logger
 from nkipy_amd.core.trace import NKIPyKernel, trace
 from nkipy_amd.runtime.device_tensor import DeviceTensor
 from nkipy_amd.runtime.hip import SpikeError, get_runtime
+from nkipy_amd.runtime.hip import on_reset as hip_on_reset
 
 logger = get_logger()
 
@@ -51,10 +52,13 @@ _LOADED_KERNELS: Dict[str, "DeviceKernel"] = {}
 
 
 def _cleanup_kernels():
+    for dk in _LOADED_KERNELS.values():
+        dk.executor.forget()
     _LOADED_KERNELS.clear()
 
 
 atexit.register(_cleanup_kernels)
+hip_on_reset(_cleanup_kernels)
 
 BACKEND_ID = "nkipy-hip-gfx950-v1"
 

@@ -403,13 +403,32 @@ def get_runtime() -> HipRuntime:
     return _runtime
 
 
+_reset_hooks = []
+
+
+def on_reset(fn):
+    """Register ``fn()`` to run when the process-wide runtime is reset (caches
+    of loaded kernels drop their handles there)."""
+    _reset_hooks.append(fn)
+    return fn
+
+
 def reset_runtime():
-    """Close the process-wide runtime (every device buffer becomes invalid)."""
+    """Close the process-wide runtime (every device buffer, code object and
+    loaded kernel becomes invalid)."""
     global _runtime
     with _runtime_lock:
         if _runtime is not None and not _runtime.is_closed:
             _runtime.close()
         _runtime = None
+    for fn in list(_reset_hooks):
+        fn()
+
+
+def check_current(rt: "HipRuntime", what: str = "kernel"):
+    """Raise SpikeError unless ``rt`` is the live process-wide runtime."""
+    if rt.is_closed or rt is not _runtime:
+        raise SpikeError(f"{what} belongs to a runtime that has been reset or closed; load it again")
 
 
 def runtime_is_active() -> bool:

@@ -79,6 +79,8 @@ def silu(x):
 
 
 def swiglu_mlp(x, w_gate, w_up, w_down, round_h=None):
+    """fp32 products and SwiGLU; ``round_h`` rounds the activation h (the
+    intermediate a bf16 kernel stores) before the down projection."""
     x = np.asarray(x, np.float32)
     g = x @ np.asarray(w_gate, np.float32)
     u = x @ np.asarray(w_up, np.float32)
@@ -88,12 +90,15 @@ def swiglu_mlp(x, w_gate, w_up, w_down, round_h=None):
     return h @ np.asarray(w_down, np.float32)
 
 
-def feedforward_fused(x, gate_up, down, gate_up_bias=None, down_bias=None):
+def feedforward_fused(x, gate_up, down, gate_up_bias=None, down_bias=None, round_h=None):
     mm = np.asarray(x, np.float32) @ np.asarray(gate_up, np.float32)
     if gate_up_bias is not None:
         mm = mm + gate_up_bias
     g, u = np.split(mm, 2, axis=-1)
-    out = (silu(g) * u) @ np.asarray(down, np.float32)
+    h = silu(g) * u
+    if round_h is not None:
+        h = round_h(h)
+    out = h @ np.asarray(down, np.float32)
     if down_bias is not None:
         out = out + down_bias
     return out
@@ -176,7 +181,8 @@ def linear_attention_quadratic_f64(q, k, v):
 # ---------------------------------------------------------------------------
 
 
-def causal_gqa_attention(q, k, v, scale=None):
+def causal_gqa_attention(q, k, v, scale=None, causal=True):
+    """``causal=False`` drops the mask (every query sees every key)."""
     q = np.asarray(q, np.float32)
     k = np.asarray(k, np.float32)
     v = np.asarray(v, np.float32)
@@ -186,14 +192,15 @@ def causal_gqa_attention(q, k, v, scale=None):
     kk = np.repeat(k, rep, axis=2).transpose(0, 2, 3, 1)   # (B, Hq, D, S)
     vv = np.repeat(v, rep, axis=2).transpose(0, 2, 1, 3)   # (B, Hq, S, D)
     s = (q.transpose(0, 2, 1, 3) @ kk) * np.float32(scale)
-    s = s + np.triu(np.full((S, S), -np.inf, np.float32), 1)
+    if causal:
+        s = s + np.triu(np.full((S, S), -np.inf, np.float32), 1)
     s = s - s.max(-1, keepdims=True)
     p = np.exp(s)
     p = p / p.sum(-1, keepdims=True)
     return (p @ vv).transpose(0, 2, 1, 3)
 
 
-def causal_attention_f64_loop(q, k, v):
+def causal_attention_f64_loop(q, k, v, causal=True):
     """Per-query float64 loop (tiny shapes): pins causal_gqa_attention."""
     q, k, v = (np.asarray(a, np.float64) for a in (q, k, v))
     B, S, Hq, D = q.shape
@@ -202,9 +209,10 @@ def causal_attention_f64_loop(q, k, v):
     for b in range(B):
         for h in range(Hq):
             for t in range(S):
-                w = np.array([q[b, t, h] @ k[b, s, h // rep] for s in range(t + 1)]) / np.sqrt(D)
+                n = t + 1 if causal else S
+                w = np.array([q[b, t, h] @ k[b, s, h // rep] for s in range(n)]) / np.sqrt(D)
                 w = np.exp(w - w.max())
-                out[b, t, h] = (w[:, None] * v[b, :t + 1, h // rep]).sum(0) / w.sum()
+                out[b, t, h] = (w[:, None] * v[b, :n, h // rep]).sum(0) / w.sum()
     return out
 
 
@@ -259,8 +267,9 @@ def linear_fp8(x, codes, scale):
     return np.asarray(x, np.float32) @ w.T
 
 
-def decoder_attention_fp8(x, w):
-    """Returns (attention output before o_proj (B, S, Hq*D), z = x + o_proj)."""
+def decoder_attention_fp8(x, w, pos0=0):
+    """Returns (attention output before o_proj (B, S, Hq*D), z = x + o_proj).
+    ``pos0``: position of the first token (the RoPE tables start there)."""
     B, S, hid = x.shape
     Hq, Hkv, eps, theta = w["n_heads"], w["n_kv_heads"], w["eps"], w["rope_theta"]
     D = hid // Hq
@@ -269,7 +278,8 @@ def decoder_attention_fp8(x, w):
     q = qkv[..., :Hq * D].reshape(B, S, Hq, D)
     k = qkv[..., Hq * D:(Hq + Hkv) * D].reshape(B, S, Hkv, D)
     v = qkv[..., (Hq + Hkv) * D:].reshape(B, S, Hkv, D)
-    cos, sin = rope_tables(D, S, theta)
+    cos, sin = rope_tables(D, pos0 + S, theta)
+    cos, sin = cos[pos0:], sin[pos0:]
     q = bf16_round(rope_split_half(q, cos, sin))
     k = bf16_round(rope_split_half(k, cos, sin))
     a = bf16_round(causal_gqa_attention(q, k, v)).reshape(B, S, Hq * D)

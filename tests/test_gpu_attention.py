@@ -1,7 +1,10 @@
 """GPU parity of the causal GQA flash-attention kernel against the oracle."""
 
+import os
+
 import numpy as np
 import pytest
+from parity import assert_close
 
 from nkipy_amd.core import dtypes as dt
 from nkipy_amd.dispatch import launchers as LA
@@ -12,14 +15,10 @@ from oracle import numerics as N
 pytestmark = pytest.mark.gpu
 
 
-def _close(got, ref, tol=2e-2):
-    """rtol 2e-2 with an absolute floor of 2e-2 of each output row's RMS over
-    the head dim (rows attend over very different numbers of keys, so their
-    scales differ by an order of magnitude)."""
-    ref = np.asarray(ref, np.float64)
-    scale = np.sqrt(np.mean(ref ** 2, axis=-1, keepdims=True))
-    err = np.abs(got - ref) / (np.abs(ref) + scale)
-    assert err.max() <= tol, err.max()
+def _close(got, ref, tol=2e-2, axis=-1):
+    """bf16 bar of tests/parity.py (rtol 2e-2, atol min(1e-2, 2e-2 RMS))."""
+    name = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    assert_close(got, ref, name, rtol=tol, axis=axis)
 
 
 def _run(gpu, q, k, v):
@@ -55,3 +54,33 @@ def test_attention_config_sampled(gpu):
     for b in (0, 7):
         ref = K.causal_gqa_attention(q[b:b + 1], k[b:b + 1], v[b:b + 1])
         _close(got[b:b + 1], ref)
+
+
+def test_noncausal_gqa_attention_traced(gpu):
+    """Unmasked softmax(q k^T / sqrt(d)) v with GQA lowers to the fused
+    kernel with the mask off, and matches the float64 loop."""
+    from nkipy_amd.kernels.softmax import softmax_kernel
+    from nkipy_amd.runtime import DeviceKernel, baremetal_jit
+
+    def full_attention(xq, xk, xv):
+        B, S, Hq, D = xq.shape
+        rep = Hq // xk.shape[2]
+        q = xq.transpose(0, 2, 1, 3).astype(np.float32)
+        kt = np.repeat(xk, rep, axis=2).transpose(0, 2, 3, 1).astype(np.float32)
+        v = np.repeat(xv, rep, axis=2).transpose(0, 2, 1, 3).astype(np.float32)
+        p = softmax_kernel(np.matmul(q, kt) / np.float32(np.sqrt(D)))
+        return np.matmul(p, v).transpose(0, 2, 1, 3).astype(xq.dtype)
+
+    B, S, Hq, Hkv = 1, 256, 4, 2
+    rng = np.random.default_rng(17)
+    q = N.bf16_round(rng.standard_normal((B, S, Hq, 128)) * 0.5)
+    k = N.bf16_round(rng.standard_normal((B, S, Hkv, 128)) * 0.5)
+    v = N.bf16_round(rng.standard_normal((B, S, Hkv, 128)))
+    args = [dt.to_bf16(a) for a in (q, k, v)]
+    dk = DeviceKernel.compile_and_load(full_attention, *args)
+    assert dk.plan.kernel_kinds == ["attention"]
+    got = dt.to_float32(baremetal_jit(full_attention)(*args))
+    ref = K.causal_gqa_attention(q, k, v, causal=False)
+    _close(got, ref)
+    rows = [0, 77, 255]
+    _close(got[:, rows], K.causal_attention_f64_loop(q, k, v, causal=False)[:, rows])

@@ -5,8 +5,11 @@ Tolerance for bf16 outputs: |got - ref| <= 2e-2 * (|ref| + rms(ref)), i.e.
 rtol 2e-2 with an absolute floor of 2e-2 of the output's RMS (dot products
 near zero have no meaningful relative error)."""
 
+import os
+
 import numpy as np
 import pytest
+from parity import assert_close
 
 from nkipy_amd.core import dtypes as dt
 from nkipy_amd.kernels import feedforward_kernel, linear_nt_kernel, swiglu_mlp_kernel
@@ -17,12 +20,10 @@ from oracle import numerics as N
 pytestmark = pytest.mark.gpu
 
 
-def _close(got, ref, tol=2e-2):
-    ref = np.asarray(ref, np.float64)
-    got = np.asarray(got, np.float64)
-    scale = np.sqrt(np.mean(ref ** 2))
-    bad = np.abs(got - ref) > tol * (np.abs(ref) + scale)
-    assert not bad.any(), f"{bad.sum()} elements out of tolerance, worst {np.max(np.abs(got - ref) / (np.abs(ref) + scale)):.3e}"
+def _close(got, ref, tol=2e-2, axis=None):
+    """bf16 bar of tests/parity.py (rtol 2e-2, atol min(1e-2, 2e-2 RMS))."""
+    name = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    assert_close(got, ref, name, rtol=tol, axis=axis)
 
 
 def _inputs(M, H, F, seed=42):
@@ -40,7 +41,7 @@ def test_swiglu_mlp_small(gpu):
     kinds = DeviceKernel.compile_and_load(swiglu_mlp_kernel, *args).plan.kernel_kinds
     assert kinds == ["gemm_swiglu", "gemm"]
     y = dt.to_float32(baremetal_jit(swiglu_mlp_kernel)(*args))
-    _close(y, K.swiglu_mlp(x, wg, wu, wd))
+    _close(y, K.swiglu_mlp(x, wg, wu, wd, round_h=N.bf16_round))
 
 
 def test_feedforward_fused_gate_up(gpu):
@@ -50,7 +51,7 @@ def test_feedforward_fused_gate_up(gpu):
     args = [dt.to_bf16(a) for a in (x3, gu, wd)]
     assert DeviceKernel.compile_and_load(feedforward_kernel, *args).plan.kernel_kinds == ["gemm_swiglu", "gemm"]
     y = dt.to_float32(baremetal_jit(feedforward_kernel)(*args))
-    _close(y, K.feedforward_fused(x3, gu, wd))
+    _close(y, K.feedforward_fused(x3, gu, wd, round_h=N.bf16_round))
 
 
 def test_linear_nt(gpu):
@@ -72,5 +73,5 @@ def test_swiglu_mlp_config_row_sample(gpu):
     ins = {n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(("x", "w_gate", "w_up", "w_down"), args)}
     out = k(ins)["output0"].numpy()
     rows = np.random.default_rng(0).choice(M, 48, replace=False)
-    ref = K.swiglu_mlp(x[rows], wg, wu, wd)
+    ref = K.swiglu_mlp(x[rows], wg, wu, wd, round_h=N.bf16_round)
     _close(dt.to_float32(out[rows]), ref)

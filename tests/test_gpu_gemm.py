@@ -2,8 +2,11 @@
 matmul on the same bf16 / fp8 values, across layouts, edge tiles and fused
 epilogues."""
 
+import os
+
 import numpy as np
 import pytest
+from parity import assert_close
 
 from nkipy_amd.core import dtypes as dt
 from nkipy_amd.dispatch import launchers as LA
@@ -18,12 +21,10 @@ def _bf16(rng, shape, scale=1.0):
     return N.bf16_round(rng.standard_normal(shape) * scale)
 
 
-def _close(got, ref, tol=2e-2):
-    """bf16-level check: |got - ref| <= tol * (|ref| + rms(ref))."""
-    ref = np.asarray(ref, np.float64)
-    scale = np.sqrt(np.mean(ref ** 2)) + 1e-30
-    err = np.abs(np.asarray(got, np.float64) - ref)
-    assert np.all(err <= tol * (np.abs(ref) + scale)), float(np.max(err / (np.abs(ref) + scale)))
+def _close(got, ref, tol=2e-2, axis=None, rounded=None):
+    """bf16 bar of tests/parity.py (rtol 2e-2, atol min(1e-2, 2e-2 RMS))."""
+    name = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    assert_close(got, ref, name, rtol=tol, axis=axis, rounded=rounded)
 
 
 def _run(gpu, launch):
@@ -214,3 +215,31 @@ def test_gemm_tile_walk_group(gpu, group_m, pp):
         outs.append(cd.numpy())
     np.testing.assert_array_equal(outs[0], outs[1])
     _close(dt.to_float32(outs[1]), a.astype(np.float64) @ b.T.astype(np.float64))
+
+
+def test_traced_residual_keeps_cast_points(gpu):
+    """``z + (x @ W^T).astype(bf16)``: the product is rounded to bf16 before
+    the residual add, as the NumPy code says (the fused epilogue must not add
+    the fp32 product).  Cancellation between z and the product exposes a
+    missing rounding as errors of a whole ulp of the product."""
+    from nkipy_amd.runtime import DeviceKernel, baremetal_jit
+
+    def proj_residual(z, x, w):
+        return z + np.matmul(x, np.transpose(w)).astype(z.dtype)
+
+    rng = np.random.default_rng(31)
+    m, n, k = 256, 512, 1024
+    x = N.bf16_round(rng.standard_normal((m, k)))
+    w = N.bf16_round(rng.standard_normal((n, k)) * 0.3)
+    prod = N.bf16_round(x @ w.T)
+    z = N.bf16_round(-prod + rng.standard_normal((m, n)) * 0.05)  # y = z + prod is small
+    args = [dt.to_bf16(a) for a in (z, x, w)]
+    dk = DeviceKernel.compile_and_load(proj_residual, *args)
+    assert dk.plan.kernel_kinds == ["gemm"]
+    got = dt.to_float32(baremetal_jit(proj_residual)(*args))
+    p = x.astype(np.float64) @ w.T.astype(np.float64)
+    ref = N.bf16_round(z + N.bf16_round(p))
+    _close(got, ref, rounded=p)
+    # without the rounding of the product, most elements would be off
+    unrounded = N.bf16_round(z + p)
+    assert np.mean(unrounded != ref) > 0.2

@@ -125,3 +125,34 @@ def test_dynamic_index_setitem(gpu):
     exp = np.zeros((5, 4), np.float32)
     exp[3] = 7
     np.testing.assert_array_equal(out, exp)
+
+
+def test_alias_deferred_reader_sees_old_contents(gpu):
+    """A fused read of a mutated input that precedes the update must see the
+    old contents, also when the fused chain is evaluated after the update."""
+
+    def kern(cache, new):
+        old = cache * 2.0
+        cache[0:1] = new
+        return old + 1.0
+
+    cache = np.arange(32, dtype=np.float32).reshape(4, 8)
+    new = -np.ones((1, 8), np.float32)
+    exp_cache = cache.copy()
+    exp_out = kern(exp_cache, new)
+    out = baremetal_jit(kern)(cache, new)
+    np.testing.assert_array_equal(out, exp_out)
+    np.testing.assert_array_equal(cache, exp_cache)
+
+
+def test_alias_overlapping_self_update(gpu):
+    def kern(cache):
+        cache[1:3] = cache[0:2]
+        return cache + 0.0
+
+    cache = np.arange(32, dtype=np.float32).reshape(4, 8)
+    exp_cache = cache.copy()
+    exp_out = kern(exp_cache)
+    out = baremetal_jit(kern)(cache)
+    np.testing.assert_array_equal(out, exp_out)
+    np.testing.assert_array_equal(cache, exp_cache)

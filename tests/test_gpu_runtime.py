@@ -91,3 +91,27 @@ def test_device_info(gpu):
     info = gpu.device_info()
     assert info["arch"].startswith("gfx950")
     assert info["cu_count"] > 0
+
+
+def test_reset_runtime_invalidates_loaded_kernels(gpu):
+    """After a reset, a kernel loaded before it refuses to run (its code
+    objects and temporaries are gone) and a fresh load works."""
+    from nkipy_amd.runtime import DeviceKernel
+    from nkipy_amd.runtime.hip import get_runtime, reset_runtime
+
+    def kern(a):
+        return a * 2.0 + 1.0
+
+    x = np.arange(64, dtype=np.float32).reshape(8, 8)
+    dk = DeviceKernel.compile_and_load(kern, x, name="reset_probe")
+    ins = {"a": DeviceTensor.from_numpy(x, name="a")}
+    np.testing.assert_array_equal(dk(ins)["output0"].numpy(), x * 2 + 1)
+    reset_runtime()
+    with pytest.raises(SpikeError):
+        dk.executor.bind({"a": 1 << 20, "output0": 1 << 21})
+    fresh = {"a": DeviceTensor.from_numpy(x, name="a")}
+    with pytest.raises(SpikeError):
+        dk(fresh)
+    dk2 = DeviceKernel.compile_and_load(kern, x, name="reset_probe")
+    assert dk2 is not dk and dk2.executor.rt is get_runtime()
+    np.testing.assert_array_equal(dk2(fresh)["output0"].numpy(), x * 2 + 1)

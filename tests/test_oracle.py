@@ -161,14 +161,14 @@ def test_rope_split_half_is_the_complex_rotation():
     np.testing.assert_allclose(sin, np.sin(ang), atol=1e-6)
 
 
-def _decoder_weights(rng, hid, Hq, Hkv, F, zero=()):
+def _decoder_weights(rng, hid, Hq, Hkv, F, zero=(), std=0.02):
     D = hid // Hq
     w = {"n_heads": Hq, "n_kv_heads": Hkv, "eps": 1e-5, "rope_theta": 5.0e5,
          "attn_norm": N.bf16_round(rng.uniform(0.5, 1.5, hid)),
          "mlp_norm": N.bf16_round(rng.uniform(0.5, 1.5, hid))}
     for name, shape in (("wqkv", ((Hq + 2 * Hkv) * D, hid)), ("wo", (hid, Hq * D)),
                         ("w_gate", (F, hid)), ("w_up", (F, hid)), ("w_down", (hid, F))):
-        m = rng.standard_normal(shape) * 0.02
+        m = rng.standard_normal(shape) * std
         if name in zero:
             m = m * 0
         w[name], w[name + "_scale"] = N.quantize_per_channel_e4m3fn(m, axis=1)
@@ -212,3 +212,68 @@ def test_decoder_zero_projections_and_gqa_sharing():
     a2 = K.decoder_layer_fp8(x, w)["attn"]
     a4 = K.decoder_layer_fp8(x, w4)["attn"]
     np.testing.assert_array_equal(a2, a4)
+
+
+def test_decoder_rope_relative_position_invariance():
+    """RoPE on q and k from the same tables makes every score depend only on
+    the distance between positions, so starting the sequence at another
+    position leaves the attention output unchanged (up to the bf16 rounding
+    of the rotated q / k).  A missing rotation on k, or tables that differ
+    between q and k, breaks this by O(1)."""
+    rng = np.random.default_rng(14)
+    B, S, hid, Hq, Hkv, F = 1, 16, 64, 4, 2, 32
+    w = _decoder_weights(rng, hid, Hq, Hkv, F, std=0.1)  # scores of O(1): softmax far from uniform
+    w["rope_theta"] = 100.0  # large angles over few positions
+    x = N.bf16_round(rng.standard_normal((B, S, hid)))
+    a0, _ = K.decoder_attention_fp8(x, w, pos0=0)
+    a1, _ = K.decoder_attention_fp8(x, w, pos0=37)
+    scale = np.sqrt(np.mean(a0 ** 2))
+    assert np.abs(a1 - a0).max() <= 5e-2 * scale
+
+    # the pin is sensitive: rotate q only (k left unrotated) and it fails
+    real = K.rope_split_half
+    calls = []
+
+    def q_only(x_, c, s_):
+        calls.append(1)
+        return real(x_, c, s_) if len(calls) % 2 == 1 else np.asarray(x_, np.float32)
+
+    K.rope_split_half = q_only
+    try:
+        b0, _ = K.decoder_attention_fp8(x, w, pos0=0)
+        b1, _ = K.decoder_attention_fp8(x, w, pos0=37)
+    finally:
+        K.rope_split_half = real
+    assert np.abs(b1 - b0).max() > 0.5 * scale
+
+
+def test_decoder_norm_weight_placement():
+    """A zero attention-norm weight zeroes q, k, v, so the attention output is
+    zero and z = x exactly; a zero MLP-norm weight zeroes gate and up, so
+    y = z exactly while z differs from x.  Swapped or misplaced norm weights
+    fail one of the two."""
+    rng = np.random.default_rng(15)
+    B, S, hid, Hq, Hkv, F = 1, 8, 64, 4, 2, 32
+    x = N.bf16_round(rng.standard_normal((B, S, hid)))
+    w = _decoder_weights(rng, hid, Hq, Hkv, F)
+    w0 = dict(w, attn_norm=np.zeros(hid, np.float32))
+    out = K.decoder_layer_fp8(x, w0)
+    np.testing.assert_array_equal(out["attn"], 0)
+    np.testing.assert_array_equal(out["z"], x)
+    assert np.abs(out["y"] - x).max() > 0
+    w1 = dict(w, mlp_norm=np.zeros(hid, np.float32))
+    out = K.decoder_layer_fp8(x, w1)
+    np.testing.assert_array_equal(out["act"], 0)
+    np.testing.assert_array_equal(out["y"], out["z"])
+    assert np.abs(out["z"] - x).max() > 0
+
+
+def test_noncausal_attention_vs_f64_loop():
+    rng = np.random.default_rng(16)
+    q = rng.standard_normal((1, 6, 4, 8)).astype(np.float32)
+    k = rng.standard_normal((1, 6, 2, 8)).astype(np.float32)
+    v = rng.standard_normal((1, 6, 2, 8)).astype(np.float32)
+    got = K.causal_gqa_attention(q, k, v, causal=False)
+    np.testing.assert_allclose(got, K.causal_attention_f64_loop(q, k, v, causal=False), rtol=1e-5, atol=1e-6)
+    # the last query sees every key under both forms
+    np.testing.assert_allclose(got[:, -1], K.causal_gqa_attention(q, k, v)[:, -1], rtol=1e-6)
