@@ -125,6 +125,26 @@ int nkh_launch_batch(int count, void *const *functions,
                      const size_t *kernarg_offsets,
                      const size_t *kernarg_sizes);
 
+/* Chunked causal linear attention, phi = elu + 1, chunk 64, d = d_v = 128:
+ * o[s, t, :] = sum_{u<=t} (phi(q_t).phi(k_u)) v_u / sum_{u<=t} phi(q_t).phi(k_u)
+ * over `bh` sequences of `t` tokens; q, k, v, o are (bh, t, 128) bf16,
+ * row-major, 16-byte aligned.  Asynchronous on the runtime stream.
+ *
+ * The reference has no kernel for this (its nearest analogue is the
+ * recurrent DeltaNet kernel, examples/linear_attention/deltanet.py:74-128,
+ * run through nrt_execute, spike/src/model.cpp:90-110); this is the entry
+ * point a ctypes caller binds instead of tracing the NumPy kernel.
+ *
+ * With few sequences the scan is cut into segments whose prefix states go
+ * through `workspace` (device memory of at least the size
+ * nkh_linear_attention_workspace_size reports; 0 bytes means none is
+ * needed and `workspace` may be null).  The workspace is fully written
+ * before it is read: it needs no clearing. */
+int nkh_linear_attention_workspace_size(int64_t bh, int64_t t, size_t *bytes);
+int nkh_linear_attention(const void *q, const void *k, const void *v, void *o,
+                         int64_t bh, int64_t t, void *workspace,
+                         size_t workspace_size);
+
 #ifdef __cplusplus
 }
 #endif

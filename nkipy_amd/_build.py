@@ -47,16 +47,22 @@ def _run(cmd):
 
 
 def build_runtime() -> Path:
+    """The C-ABI library: the runtime core (host code) plus the compute entry
+    points, whose gfx950 kernels are compiled into the library."""
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     tmp = RUNTIME_LIB.with_suffix(".so.tmp")
     cmd = [
         HIPCC,
-        "-O2",
+        "-O3",
         "-fPIC",
         "-shared",
         "-std=c++17",
+        f"--offload-arch={ARCH}",
+        *NO_PACKED_FP32,
         f"-I{INCLUDE_DIR}",
+        f"-I{KERNEL_DIR}",
         str(CSRC / "runtime.cpp"),
+        str(CSRC / "entry.hip"),
         "-o",
         str(tmp),
     ]

@@ -309,7 +309,7 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
       if (l32 == 0) {
         const uint32_t z0 = pack_f16x2(Z[4 * g4 + 0] * 0.00390625f, Z[4 * g4 + 1] * 0.00390625f);
         const uint32_t z1 = pack_f16x2(Z[4 * g4 + 2] * 0.00390625f, Z[4 * g4 + 3] * 0.00390625f);
-        *(__attribute__((address_space(3))) uint2 *)(nxt.z + d * 2) = make_uint2(z0, z1);
+        *(__attribute__((address_space(3))) uint64_t *)(nxt.z + d * 2) = ((uint64_t)z1 << 32) | z0;
       }
     }
   };

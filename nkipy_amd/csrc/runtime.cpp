@@ -23,6 +23,7 @@
 #include <string>
 
 #include "../../include/nkipy_hip.h"
+#include "runtime_internal.h"
 
 namespace {
 
@@ -94,6 +95,21 @@ int check_range(const void *p, size_t n, const char *what) {
 
 }  // namespace
 
+namespace nkh_internal {
+
+int set_error(int code, const std::string &msg) { return ::set_error(code, msg); }
+
+int hip_error(hipError_t e, const char *what) { return ::hip_error(e, what); }
+
+int with_stream(const std::function<int(hipStream_t, int)> &fn) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc = require_init();
+  if (rc) return rc;
+  return fn(g_rt.stream, g_rt.device);
+}
+
+}  // namespace nkh_internal
+
 extern "C" {
 
 const char *nkh_last_error(void) { return g_last_error.c_str(); }
@@ -113,6 +129,11 @@ int nkh_init(int device) {
   hipStream_t s = nullptr;
   NKH_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking),
           "hipStreamCreateWithFlags");
+  int rc = nkh_internal::device_setup(device);
+  if (rc) {
+    hipStreamDestroy(s);
+    return rc;
+  }
   g_rt.device = device;
   g_rt.stream = s;
   g_rt.initialized = true;

@@ -116,3 +116,39 @@ def test_linattn_large_state_stays_finite(gpu):
     assert np.all(np.isfinite(got))
     ref = K.linear_attention_chunked(q, k, v)
     _close(got, ref)
+
+
+def _c_abi_run(gpu, q, k, v, workspace=True):
+    """nkh_linear_attention through the C ABI on device copies of q, k, v."""
+    import ctypes
+
+    B, H, T, D = q.shape
+    t = [DeviceTensor.from_numpy(dt.to_bf16(a)) for a in (q, k, v)]
+    o = DeviceTensor.empty((B, H, T, D), dt.bfloat16)
+    size = ctypes.c_size_t()
+    assert gpu.lib.nkh_linear_attention_workspace_size(B * H, T, ctypes.byref(size)) == 0
+    ws = DeviceTensor.empty((max(size.value, 16),), dt.uint8)
+    rc = gpu.lib.nkh_linear_attention(t[0].ptr, t[1].ptr, t[2].ptr, o.ptr, B * H, T,
+                                      ws.ptr if workspace else None, size.value if workspace else 0)
+    if rc:
+        return rc, gpu.lib.nkh_last_error()
+    gpu.sync()
+    return rc, o.numpy()
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 1024, 128), (4, 16, 8192, 128), (1, 1, 256, 128)])
+def test_c_abi_linear_attention_matches_launcher(gpu, shape):
+    """The C entry point runs the same kernels with the same split as the
+    plan's launcher: bit-identical output."""
+    q, k, v = _qkv(*shape, seed=sum(shape) + 1)
+    rc, raw = _c_abi_run(gpu, q, k, v)
+    assert rc == 0, raw
+    np.testing.assert_array_equal(dt.to_float32(raw), _run(gpu, q, k, v))
+    if shape[2] <= 1024:
+        _close(dt.to_float32(raw), K.linear_attention_quadratic_f64(q, k, v))
+
+
+def test_c_abi_linear_attention_rejects_missing_workspace(gpu):
+    q, k, v = _qkv(1, 1, 4096, 128, seed=5)
+    rc, msg = _c_abi_run(gpu, q, k, v, workspace=False)
+    assert rc == 2 and b"workspace" in msg

@@ -290,3 +290,20 @@ def test_alias_update_reading_its_own_target_is_not_in_place_read():
     # the source rows are copied out (or the update staged) before the
     # buffer is written, never read by the updating step itself
     assert descs[-1].startswith("write back") or (len(descs) == 2 and descs[1] == "update slice"), descs
+
+
+# ---------------------------------------------------------------------------
+# C-ABI linear attention: the library's work split equals the launcher's
+# ---------------------------------------------------------------------------
+def test_c_abi_linear_attention_workspace_matches_launcher():
+    from nkipy_amd.runtime.hip import load_library
+
+    lib = load_library()
+    size = ctypes.c_size_t()
+    for bh in (1, 2, 3, 4, 16, 64, 255, 256, 1024):
+        for t in (64, 128, 512, 1024, 4096, 8192, 16384, 65536):
+            assert lib.nkh_linear_attention_workspace_size(bh, t, ctypes.byref(size)) == 0
+            assert size.value == LA.linear_attention_workspace_bytes(bh, t), (bh, t)
+    for bh, t in ((0, 64), (4, 100), (4, 0), (-1, 64)):
+        assert lib.nkh_linear_attention_workspace_size(bh, t, ctypes.byref(size)) == 2
+        assert b"multiple of 64" in lib.nkh_last_error()
