@@ -145,6 +145,22 @@ int nkh_linear_attention(const void *q, const void *k, const void *v, void *o,
                          int64_t bh, int64_t t, void *workspace,
                          size_t workspace_size);
 
+/* nkh_linear_attention without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The partial prefix states go to a scratch array of
+ * NKH_NOALLOC_SCRATCH_BYTES that the library keeps on each device it was
+ * initialized on until the process ends; shapes whose workspace exceeds it
+ * are rejected with NKH_ERR_INVALID (use nkh_linear_attention then).  The
+ * call allocates and frees nothing.  Every call on a GPU shares that GPU's
+ * array: calls queued on the runtime stream run one after another, but
+ * calls that overlap on one GPU (another stream or process driving the
+ * same library state) race.  The array needs no clearing: each call writes
+ * every partial state before reading it. */
+#define NKH_NOALLOC_SCRATCH_BYTES (16u << 20)
+int nkh_linear_attention_noalloc(const void *q, const void *k, const void *v,
+                                 void *o, int64_t bh, int64_t t);
+
 #ifdef __cplusplus
 }
 #endif

@@ -14,6 +14,7 @@
 
 #include "kernels/linattn.hip"
 
+#include <mutex>
 #include <string>
 
 #include "../../include/nkipy_hip.h"
@@ -96,9 +97,36 @@ int launch_linattn(const void *q, const void *k, const void *v, void *o, int64_t
 
 }  // namespace
 
+// Scratch of nkh_linear_attention_noalloc: the partial prefix states.
+// Every device the library runs on holds its own copy until the process
+// ends.  Host code never uses this name as an address: the per-device
+// address comes from hipGetSymbolAddress at set-up (g_scratch).
+static __device__ __align__(256) uint8_t scratch[NKH_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+void *g_scratch[kMaxDevices] = {};  // device address of `scratch`, per device
+std::mutex g_scratch_mu;
+
+}  // namespace
+
 namespace nkh_internal {
 
-int device_setup(int) { return NKH_OK; }
+// Runs in nkh_init with `device` current: look up this device's copy of
+// the scratch array once.
+int device_setup(int device) {
+  if (device < 0 || device >= kMaxDevices)
+    return set_error(NKH_ERR_INVALID, "device index " + std::to_string(device) + " beyond the supported 64");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch[device]) return NKH_OK;
+  void *ptr = nullptr;
+  hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return hip_error(e, "hipGetSymbolAddress(scratch)");
+  if (!ptr) return set_error(NKH_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+  g_scratch[device] = ptr;
+  return NKH_OK;
+}
 
 }  // namespace nkh_internal
 
@@ -128,6 +156,30 @@ int nkh_linear_attention(const void *q, const void *k, const void *v, void *o, i
     return nkh_internal::set_error(NKH_ERR_INVALID, "linear attention workspace must be 16-byte aligned");
   return nkh_internal::with_stream([&](hipStream_t stream, int) {
     return launch_linattn(q, k, v, o, bh, t, static_cast<float *>(workspace), stream);
+  });
+}
+
+int nkh_linear_attention_noalloc(const void *q, const void *k, const void *v, void *o, int64_t bh, int64_t t) {
+  int rc = check_shape(bh, t);
+  if (rc) return rc;
+  rc = check_ptrs(q, k, v, o);
+  if (rc) return rc;
+  const size_t need = (size_t)workspace_bytes(bh, linattn_split(bh, t));
+  if (need > NKH_NOALLOC_SCRATCH_BYTES)
+    return nkh_internal::set_error(NKH_ERR_INVALID, "linear attention of BH=" + std::to_string(bh) + " T=" +
+                                                        std::to_string(t) + " needs " + std::to_string(need) +
+                                                        " bytes of scratch; the no-allocation entry point "
+                                                        "holds at most " +
+                                                        std::to_string(NKH_NOALLOC_SCRATCH_BYTES) +
+                                                        " (use nkh_linear_attention with a workspace)");
+  return nkh_internal::with_stream([&](hipStream_t stream, int device) {
+    void *ptr;
+    {
+      std::lock_guard<std::mutex> lk(g_scratch_mu);
+      ptr = (device >= 0 && device < kMaxDevices) ? g_scratch[device] : nullptr;
+    }
+    if (!ptr) return nkh_internal::set_error(NKH_ERR_NOT_INIT, "scratch of this device is not set up");
+    return launch_linattn(q, k, v, o, bh, t, static_cast<float *>(ptr), stream);
   });
 }
 

@@ -99,6 +99,7 @@ def _bind(lib):
     i64 = ctypes.c_int64
     sigs["nkh_linear_attention_workspace_size"] = ([i64, i64, ctypes.POINTER(sz)], ctypes.c_int)
     sigs["nkh_linear_attention"] = ([vp, vp, vp, vp, i64, i64, vp, sz], ctypes.c_int)
+    sigs["nkh_linear_attention_noalloc"] = ([vp, vp, vp, vp, i64, i64], ctypes.c_int)
     for name, (argtypes, restype) in sigs.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
@@ -115,6 +116,7 @@ EXPORTED_SYMBOLS = (
     "nkh_launch", "nkh_sync", "nkh_time_launch", "nkh_event_create",
     "nkh_event_destroy", "nkh_event_record", "nkh_event_elapsed_ms",
     "nkh_launch_batch", "nkh_linear_attention_workspace_size", "nkh_linear_attention",
+    "nkh_linear_attention_noalloc",
 )
 
 _lib = None
