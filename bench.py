@@ -1,26 +1,44 @@
 """Benchmark of the hot path on one MI355X.
 
-One JSON line on stdout.  The headline workload is the fused residual +
-RMSNorm over x, r bf16 (8192, 4096), w bf16 (4096,), eps 1e-6: one step is
-one pass of the traced kernel over the batch, run through the product path
-(traced NumPy kernel -> plan -> gfx950 kernel via the C-ABI runtime).
-Inputs are resident in HBM before timing starts; steps rotate over several
-buffer sets whose total exceeds the 256 MB Infinity Cache, so the bytes
-really come from HBM.
+One JSON line on stdout.  Five workloads run through the product path
+(traced NumPy kernel -> plan -> gfx950 kernels through the C-ABI runtime),
+each with its own roofline, CPU baseline and parity record:
 
-``value`` is achieved HBM bandwidth (algorithmic bytes / time per step).
-``roofline`` reports the dominant kernel's algorithmic bytes per launch over
-its mean launch duration, measured with HIP events on the runtime stream.
-``kernels`` carries the other hot-path kernels measured the same way.
-``cpu_baseline`` is the oracle's NumPy formula of the same kernel timed on
-the host.
+  1  row softmax, x fp32 (2048, 4096)
+  2  residual + RMSNorm, x, r bf16 (8192, 4096), w bf16 (4096,), eps 1e-6
+     -- the headline: ``value`` is its achieved HBM bandwidth per step
+  3  SwiGLU MLP, x (4096, 4096), W_gate / W_up (4096, 14336), W_down
+     (14336, 4096), bf16
+  4  chunked causal linear attention, q, k, v bf16 (4, 16, 8192, 128)
+  5  Llama-style decoder layer with fp8 weights, x bf16 (8, 2048, 4096),
+     32 / 8 heads, FFN 14336 -- reported as its latency per layer
+
+Timing: inputs are resident in HBM; bandwidth-bound steps rotate over
+buffer sets whose total exceeds the 256 MB Infinity Cache; every timed
+region follows 50 ms of untimed load of the same work (the part ramps its
+clocks) and is bracketed by HIP events on the runtime stream.  Per-kernel
+times inside multi-kernel steps come from HIP events recorded between the
+launches of whole steps.
+
+``cpu_baseline`` of each workload is the oracle's NumPy form of the same
+kernel (the reference's CPU path) timed on the host on a bounded sample;
+the same leg checks the GPU output against it (``parity``).
+
+Profiling: ``--mark-sections`` launches a marker copy kernel (grid 1000 +
+workload id) before each workload, so a rocprofv3 kernel trace or counter
+run of this script can be split per workload and per launch position;
+``python bench.py --summarize DIR`` prints those summaries (no GPU needed).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                       [--configs 1,2,3,4,5] [--mark-sections] [--calibrate-copy]
+       python bench.py --summarize DIR [--traffic-json PATH]
 """
 
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import math
 import os
@@ -33,8 +51,56 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0
 MALL_BYTES = 256 * 2**20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+METRIC = "per-kernel achieved HBM GB/s & MFMA TFLOP/s vs peak; fp8 decoder-layer latency (us)"
+
+# workload sizes
+SM_ROWS, SM_N = 2048, 4096
+RMS_ROWS, RMS_N, RMS_EPS = 8192, 4096, 1e-6
+MLP_M, MLP_H, MLP_F = 4096, 4096, 14336
+LA_B, LA_H, LA_T, LA_D = 4, 16, 8192, 128
+DEC_B, DEC_S, DEC_HQ, DEC_HKV, DEC_D, DEC_F = 8, 2048, 32, 8, 128, 14336
+DEC_HID = DEC_HQ * DEC_D
+DEC_M = DEC_B * DEC_S
+
+
+def _linattn_prefix_bytes():
+    from nkipy_amd.dispatch.launchers import linear_attention_split
+
+    _, rchunks, nranges = linear_attention_split(LA_B * LA_H, LA_T)
+    return 2 * LA_B * LA_H * nranges * rchunks * 64 * LA_D * 2
+
+
+# Per workload: (name, [(launch label, bound, algorithmic work per launch)])
+# -- bytes for "hbm", flops for "mfma"; the launches of one step, in order.
+def sections():
+    norm_bytes = 2 * DEC_M * DEC_HID * 2 + DEC_HID * 2
+    return {
+        1: ("softmax", [("softmax", "hbm", SM_ROWS * SM_N * 4 * 2)]),
+        2: ("residual_rmsnorm", [("residual_rmsnorm", "hbm", RMS_ROWS * RMS_N * 2 * 3 + RMS_N * 2)]),
+        3: ("swiglu_mlp", [("gate_up_swiglu", "mfma", 2 * 2 * MLP_M * MLP_H * MLP_F),
+                           ("down_proj", "mfma", 2 * MLP_M * MLP_F * MLP_H)]),
+        4: ("linear_attention", [("prefix_states", "hbm", _linattn_prefix_bytes()),
+                                 ("scan", "hbm", 4 * LA_B * LA_H * LA_T * LA_D * 2)]),
+        5: ("decoder_layer_fp8", [
+            ("attn_norm", "hbm", norm_bytes),
+            ("qkv_proj", "mfma", 2 * DEC_M * DEC_HID * (DEC_HQ + 2 * DEC_HKV) * DEC_D),
+            ("rope_q", "hbm", 2 * DEC_M * DEC_HQ * DEC_D * 2),
+            ("rope_k", "hbm", 2 * DEC_M * DEC_HKV * DEC_D * 2),
+            ("attention", "mfma", 4 * DEC_B * DEC_HQ * DEC_S * DEC_S * DEC_D // 2),
+            ("o_proj_residual", "mfma", 2 * DEC_M * DEC_HID * DEC_HID),
+            ("mlp_norm", "hbm", norm_bytes),
+            ("gate_up_swiglu", "mfma", 2 * 2 * DEC_M * DEC_HID * DEC_F),
+            ("down_proj_residual", "mfma", 2 * DEC_M * DEC_F * DEC_HID)]),
+        9: ("copy_calibration", [("copy16", "hbm", 2 * 2**30)]),
+    }
+
+
+MARK_BASE = 1000  # marker grid = MARK_BASE + workload id
+CUS, XCDS = 256, 8  # MI355X
 
 
 def log(*a):
@@ -49,21 +115,39 @@ def _sets_for(bytes_per_set: int) -> int:
     return max(2, math.ceil(3 * MALL_BYTES / bytes_per_set))
 
 
-def _time_bound(bounds, steps: int, warmup: int, rt):
-    """Run the bound plans round robin, back to back on the runtime stream.
+def _rate(bound, work, us):
+    """(achieved, peak, unit) of ``work`` done in ``us`` microseconds."""
+    if bound == "hbm":
+        return work / (us * 1e-6) / 1e9, HBM_PEAK_GBS, "GB/s"
+    return work / (us * 1e-6) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
 
-    Returns (ms per step, ms per launch): HIP events on the runtime stream
-    bracket the timed region; each step is one launch of the fused kernel,
-    so the mean launch duration is the region time over the launch count.
-    (Event pairs around every launch would insert a marker between kernels
-    and inflate each one by several microseconds.)"""
+
+class Marker:
+    """Marker launches that split a profiler trace per workload."""
+
+    def __init__(self, rt, enabled):
+        self.rt, self.enabled = rt, enabled
+        if enabled:
+            self.n = 4096 * (MARK_BASE + 16)
+            self.src, self.dst = rt.malloc(self.n), rt.malloc(self.n)
+
+    def mark(self, sid):
+        if self.enabled:
+            from nkipy_amd.dispatch.generic import copy16
+
+            copy16(self.src, self.dst, 4096 * (MARK_BASE + sid)).run(self.rt)
+
+
+def _time_steps(bounds, steps, warmup, rt):
+    """Mean milliseconds per step over ``steps`` steps run round robin over
+    the bound plans, back to back on the runtime stream, bracketed by HIP
+    events (event pairs around every launch would insert markers between
+    kernels)."""
     for i in range(warmup):
         bounds[i % len(bounds)].run()
     rt.sync()
-    # The part ramps its clocks over the first ~20 ms of sustained load (a
-    # residual RMSNorm step runs ~56 us in the first 8 ms, ~38 us from 30 ms
-    # on), so the timed region starts only after DEVICE_WARM_S of the same
-    # work: the figures are steady-state rates.
+    # The part ramps its clocks over the first ~20 ms of sustained load, so
+    # the timed region starts after DEVICE_WARM_S of the same work.
     t_end = time.perf_counter() + DEVICE_WARM_S
     i = 0
     while time.perf_counter() < t_end:
@@ -71,201 +155,294 @@ def _time_bound(bounds, steps: int, warmup: int, rt):
             bounds[i % len(bounds)].run()
             i += 1
         rt.sync()
-    region0, region1 = rt.event(), rt.event()
-    region0.record()
+    e0, e1 = rt.event(), rt.event()
+    e0.record()
     for k in range(steps):
         bounds[k % len(bounds)].run()
-    region1.record()
+    e1.record()
     rt.sync()
-    total = region0.elapsed_ms(region1)
-    region0.destroy()
-    region1.destroy()
-    launches = sum(len(bounds[k % len(bounds)].launches) for k in range(steps))
-    return total / steps, total / launches
+    total = e0.elapsed_ms(e1)
+    e0.destroy()
+    e1.destroy()
+    return total / steps
 
 
-def _traffic(kernel_key):
-    """HBM bytes per launch of ``kernel_key`` from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE runs (scaled by the copy-kernel calibration)."""
+def _time_in_step(bounds, reps, rt):
+    """Mean microseconds of each launch of a step: HIP events between the
+    launches of whole steps, over rotating buffer sets."""
+    n = len(bounds[0].launches)
+    sums = [0.0] * n
+    evs = [rt.event() for _ in range(n + 1)]
+    for r in range(reps):
+        b = bounds[r % len(bounds)]
+        evs[0].record()
+        for i in range(n):
+            b.run_range(i, i + 1)
+            evs[i + 1].record()
+        rt.sync()
+        for i in range(n):
+            sums[i] += evs[i].elapsed_ms(evs[i + 1])
+    for e in evs:
+        e.destroy()
+    return [s / reps * 1e3 for s in sums]
+
+
+def _shape_of(launch):
+    a = launch.args
+    if hasattr(a, "K") and hasattr(a, "M"):
+        return {"M": int(a.M), "N": int(a.N), "K": int(a.K)}
+    return None
+
+
+def _kernel_records(sid, launches, us_list):
+    recs = []
+    for (label, bound, work), l, us in zip(sections()[sid][1], launches, us_list):
+        ach, peak, unit = _rate(bound, work, us)
+        r = {"label": label, "kernel": l.symbol, "grid": l.grid[0], "us": round(us, 2),
+             "bound": bound, "work": work, "achieved": round(ach, 1), "peak": peak, "unit": unit,
+             "frac": round(ach / peak, 4)}
+        sh = _shape_of(l)
+        if sh:
+            r["shape"] = sh
+        recs.append(r)
+    return recs
+
+
+def _traffic(key):
+    """HBM bytes per launch of ``key`` ("workload/label") from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/traffic.json)."""
     try:
         with open(TRAFFIC_FILE) as f:
-            entry = json.load(f).get(kernel_key)
+            entry = json.load(f).get(key)
     except (OSError, ValueError):
         return None
     return entry.get("total_bytes") if isinstance(entry, dict) else None
 
 
-def bench_rmsnorm(steps, warmup, rt):
+def _roofline(sid, rec, us=None, work=None):
+    """Roofline block of one kernel record (or of a whole step with ``us`` /
+    ``work`` given)."""
+    name = sections()[sid][0]
+    bound = rec["bound"]
+    us = rec["us"] if us is None else us
+    work = rec["work"] if work is None else work
+    ach, peak, unit = _rate(bound, work, us)
+    return {"bound": bound, "kernel": rec["kernel"], "achieved": round(ach, 1), "peak": peak, "unit": unit,
+            "frac": round(ach / peak, 4), "traffic": _traffic(f"{name}/{rec['label']}"),
+            "work_per_launch": work, "us_per_launch": round(us, 3)}
+
+
+# ---------------------------------------------------------------------------
+# parity of a GPU output against the oracle (inside the cpu_baseline leg)
+# ---------------------------------------------------------------------------
+def _parity(got, ref, bar="bf16", atol=1e-2):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(got - ref)
+    out = {"n": int(err.size), "finite": bool(np.all(np.isfinite(got))), "max_abs": float(err.max()),
+           "max_rel": float(np.max(err / np.maximum(np.abs(ref), 1e-30)))}
+    if bar == "fp32":
+        ratio = out["max_rel"] / 1e-5
+        out["bar"] = "max |got - ref| / |ref| <= 1e-5"
+    else:
+        a = min(atol, 2e-2 * float(np.sqrt(np.mean(ref ** 2))))
+        ratio = float(np.max(err / (2e-2 * np.abs(ref) + a)))
+        out["bar"] = f"|got - ref| <= 2e-2 |ref| + {a:.3g}"
+    out["worst_of_bar"] = round(ratio, 4)
+    out["ok"] = bool(out["finite"] and ratio <= 1.0)
+    return out
+
+
+def _timed(fn, runs):
+    fn_out = None
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn_out = fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), times, fn_out
+
+
+def _blas_threads():
+    try:
+        from threadpoolctl import threadpool_info
+
+        return max((p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"), default=1)
+    except Exception:  # pragma: no cover
+        return None
+
+
+def _host_cores():
+    return len(os.sched_getaffinity(0))
+
+
+# ---------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------
+def bench_softmax(a, rt, mk):
+    from nkipy_amd.kernels import softmax_kernel
+    from nkipy_amd.runtime import DeviceKernel, DeviceTensor
+
+    rng = np.random.default_rng(42)
+    x = (rng.standard_normal((SM_ROWS, SM_N)) * 4).astype(np.float32)
+    dk = DeviceKernel.compile_and_load(softmax_kernel, x, name="softmax")
+    if dk.plan.kernel_kinds != ["softmax"]:
+        raise RuntimeError(f"softmax did not lower to the fused kernel: {dk.plan.kernel_kinds}")
+    work = sections()[1][1][0][2]
+    sets = [(DeviceTensor.from_numpy(x, name="x"), DeviceTensor.empty((SM_ROWS, SM_N), np.float32, name="output0"))
+            for _ in range(_sets_for(work))]
+    bounds = [dk.executor.bind({"x": s[0].ptr, "output0": s[1].ptr}) for s in sets]
+    mk.mark(1)
+    ms = _time_steps(bounds, a.steps, a.warmup, rt)
+    recs = _kernel_records(1, bounds[0].launches, [ms * 1e3])
+    entry = {"config": 1, "workload": "softmax", "shape": [SM_ROWS, SM_N], "dtype": "f32",
+             "us_per_step": round(ms * 1e3, 3), "roofline": _roofline(1, recs[0]), "kernels": recs,
+             "buffer_sets": len(sets)}
+
+    def cpu():
+        from oracle import kernels as K
+
+        t, ts, ref = _timed(lambda: K.softmax_kernel(x), 5)
+        return ({"value": round(work / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                 "sample": f"full workload, median of {len(ts)} runs ({sum(ts):.2f} s); NumPy elementwise "
+                           f"ops are single-threaded; host has {_host_cores()} cores",
+                 "ms": round(t * 1e3, 2)},
+                _parity(sets[0][1].numpy(), ref, bar="fp32"))
+
+    return entry, cpu
+
+
+def bench_rmsnorm(a, rt, mk):
     from nkipy_amd.core import dtypes as dt
     from nkipy_amd.kernels import residual_rmsnorm_kernel
     from nkipy_amd.runtime import DeviceKernel, DeviceTensor
 
-    rows, n, eps = 8192, 4096, 1e-6
     rng = np.random.default_rng(42)
-    x = dt.round_to_bf16(rng.standard_normal((rows, n)).astype(np.float32))
-    r = dt.round_to_bf16(rng.standard_normal((rows, n)).astype(np.float32))
-    w = dt.round_to_bf16(rng.uniform(0.5, 1.5, n).astype(np.float32))
+    x = dt.round_to_bf16(rng.standard_normal((RMS_ROWS, RMS_N)).astype(np.float32))
+    r = dt.round_to_bf16(rng.standard_normal((RMS_ROWS, RMS_N)).astype(np.float32))
+    w = dt.round_to_bf16(rng.uniform(0.5, 1.5, RMS_N).astype(np.float32))
     xb, rb, wb = dt.to_bf16(x), dt.to_bf16(r), dt.to_bf16(w)
-    dk = DeviceKernel.compile_and_load(residual_rmsnorm_kernel, xb, rb, wb, eps, name="residual_rmsnorm")
-    kinds = dk.plan.kernel_kinds
-    if kinds != ["rmsnorm"]:
-        raise RuntimeError(f"residual rmsnorm did not lower to the fused kernel: {kinds}")
-    alg_bytes = rows * n * 2 * 3 + n * 2
-    nsets = _sets_for(alg_bytes)
+    dk = DeviceKernel.compile_and_load(residual_rmsnorm_kernel, xb, rb, wb, RMS_EPS, name="residual_rmsnorm")
+    if dk.plan.kernel_kinds != ["rmsnorm"]:
+        raise RuntimeError(f"residual rmsnorm did not lower to the fused kernel: {dk.plan.kernel_kinds}")
+    work = sections()[2][1][0][2]
     wt = DeviceTensor.from_numpy(wb, name="weight")
-    sets = []
-    for i in range(nsets):
-        xt = DeviceTensor.from_numpy(xb, name="x")
-        rt_ = DeviceTensor.from_numpy(rb, name="residual")
-        yt = DeviceTensor.empty((rows, n), dt.bfloat16, name="output0")
-        sets.append((xt, rt_, yt))
-    bounds = [dk.executor.bind({"x": a.ptr, "residual": b.ptr, "weight": wt.ptr, "output0": c.ptr})
-              for a, b, c in sets]
-    ms_step, ms_launch = _time_bound(bounds, steps, warmup, rt)
-    # parity spot check of the timed output against the oracle formula
-    from oracle import kernels as K
+    sets = [(DeviceTensor.from_numpy(xb, name="x"), DeviceTensor.from_numpy(rb, name="residual"),
+             DeviceTensor.empty((RMS_ROWS, RMS_N), dt.bfloat16, name="output0")) for _ in range(_sets_for(work))]
+    bounds = [dk.executor.bind({"x": s[0].ptr, "residual": s[1].ptr, "weight": wt.ptr, "output0": s[2].ptr})
+              for s in sets]
+    mk.mark(2)
+    ms = _time_steps(bounds, a.steps, a.warmup, rt)
+    recs = _kernel_records(2, bounds[0].launches, [ms * 1e3])
+    entry = {"config": 2, "workload": "residual_rmsnorm", "shape": [RMS_ROWS, RMS_N], "dtype": "bf16",
+             "eps": RMS_EPS, "us_per_step": round(ms * 1e3, 3), "ms_per_step": ms,
+             "roofline": _roofline(2, recs[0]), "kernels": recs, "buffer_sets": len(sets)}
 
-    got = dt.to_float32(sets[0][2].numpy()[:256])
-    ref = K.residual_rmsnorm_bf16(x[:256], r[:256], w, eps)
-    ok = bool(np.allclose(got, ref, rtol=2e-2, atol=0))
-    return {
-        "workload": "residual_rmsnorm",
-        "shape": [rows, n], "dtype": "bf16", "eps": eps,
-        "kernel": dk.executor.bind({"x": sets[0][0].ptr, "residual": sets[0][1].ptr,
-                                    "weight": wt.ptr, "output0": sets[0][2].ptr}).launches[0].symbol,
-        "bytes_per_launch": alg_bytes,
-        "ms_per_step": ms_step,
-        "us_per_launch": ms_launch * 1e3,
-        "gbs_step": alg_bytes / (ms_step * 1e-3) / 1e9,
-        "gbs_launch": alg_bytes / (ms_launch * 1e-3) / 1e9,
-        "buffer_sets": nsets,
-        "parity_ok": ok,
-        "host": (x, r, w),
-    }
+    def cpu():
+        from oracle import kernels as K
+
+        K.residual_rmsnorm_bf16(x[:64], r[:64], w, RMS_EPS)
+        t, ts, ref = _timed(lambda: K.residual_rmsnorm_bf16(x, r, w, RMS_EPS), 5)
+        return ({"value": round(work / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                 "sample": f"full workload (bf16 values held in fp32 arrays), median of {len(ts)} runs "
+                           f"({sum(ts):.2f} s); NumPy elementwise ops are single-threaded; "
+                           f"host has {_host_cores()} cores",
+                 "ms": round(t * 1e3, 2)},
+                _parity(dt.to_float32(sets[0][2].numpy()), ref))
+
+    return entry, cpu
 
 
-def bench_softmax(steps, warmup, rt):
-    from nkipy_amd.kernels import softmax_kernel
-    from nkipy_amd.runtime import DeviceKernel, DeviceTensor
-
-    rows, n = 2048, 4096
-    rng = np.random.default_rng(42)
-    x = (rng.standard_normal((rows, n)) * 4).astype(np.float32)
-    dk = DeviceKernel.compile_and_load(softmax_kernel, x, name="softmax")
-    if dk.plan.kernel_kinds != ["softmax"]:
-        raise RuntimeError(f"softmax did not lower to the fused kernel: {dk.plan.kernel_kinds}")
-    alg_bytes = rows * n * 4 * 2
-    nsets = _sets_for(alg_bytes)
-    sets = [(DeviceTensor.from_numpy(x, name="x"), DeviceTensor.empty((rows, n), np.float32, name="output0"))
-            for _ in range(nsets)]
-    bounds = [dk.executor.bind({"x": a.ptr, "output0": b.ptr}) for a, b in sets]
-    ms_step, ms_launch = _time_bound(bounds, steps, warmup, rt)
-    from oracle import kernels as K
-
-    got = sets[0][1].numpy()[:128]
-    ref = K.softmax_kernel(x[:128])
-    rel = float(np.max(np.abs(got - ref) / np.abs(ref)))
-    return {
-        "workload": "softmax", "shape": [rows, n], "dtype": "f32",
-        "kernel": bounds[0].launches[0].symbol,
-        "bytes_per_launch": alg_bytes,
-        "us_per_launch": ms_launch * 1e3,
-        "gbs": alg_bytes / (ms_launch * 1e-3) / 1e9,
-        "frac_hbm": alg_bytes / (ms_launch * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        "max_rel_err": rel,
-        "buffer_sets": nsets,
-    }
-
-
-BF16_PEAK_TFLOPS = 2500.0
-
-
-def bench_swiglu(steps, warmup, rt):
-    """SwiGLU MLP: x (4096, 4096), W_gate / W_up (4096, 14336), W_down
-    (14336, 4096), bf16, fp32 accumulation.  One step = the whole MLP (the
-    fused gate/up kernel and the down GEMM)."""
+def bench_swiglu(a, rt, mk):
     from nkipy_amd.core import dtypes as dt
     from nkipy_amd.kernels import swiglu_mlp_kernel
     from nkipy_amd.runtime import DeviceKernel, DeviceTensor
 
-    M, H, F = 4096, 4096, 14336
     rng = np.random.default_rng(42)
-    x = dt.round_to_bf16(rng.standard_normal((M, H)).astype(np.float32))
+    x = dt.round_to_bf16(rng.standard_normal((MLP_M, MLP_H)).astype(np.float32))
     ws = [dt.round_to_bf16((rng.standard_normal(s) * 0.02).astype(np.float32))
-          for s in ((H, F), (H, F), (F, H))]
-    args = [dt.to_bf16(a) for a in [x] + ws]
+          for s in ((MLP_H, MLP_F), (MLP_H, MLP_F), (MLP_F, MLP_H))]
+    args = [dt.to_bf16(v) for v in [x] + ws]
     dk = DeviceKernel.compile_and_load(swiglu_mlp_kernel, *args, name="swiglu_mlp")
     if dk.plan.kernel_kinds != ["gemm_swiglu", "gemm"]:
         raise RuntimeError(f"SwiGLU did not lower to the fused GEMMs: {dk.plan.kernel_kinds}")
-    names = ("x", "w_gate", "w_up", "w_down")
-    ins = {n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(names, args)}
-    out = DeviceTensor.empty((M, H), dt.bfloat16, name="output0")
+    ins = {n: DeviceTensor.from_numpy(v, name=n) for n, v in zip(("x", "w_gate", "w_up", "w_down"), args)}
+    out = DeviceTensor.empty((MLP_M, MLP_H), dt.bfloat16, name="output0")
     bound = dk.executor.bind({**{k: v.ptr for k, v in ins.items()}, "output0": out.ptr})
-    flops = 3 * 2 * M * H * F
-    ms_step, _ = _time_bound([bound], steps, warmup, rt)
-    # per-kernel times from single-launch timing (HIP events on the runtime stream)
-    per = []
-    for l in bound.launches:
-        f = l.function(rt)
-        ms = f.time(l.grid, l.block, l.args, warmup=2, iters=max(3, steps // 4))
-        per.append({"kernel": l.symbol, "us": round(ms * 1e3, 2),
-                    "tflops": round(l.flops / (ms * 1e-3) / 1e12, 1),
-                    "frac_bf16_peak": round(l.flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)})
-    from oracle import kernels as K
+    steps, warm = max(5, a.steps // 20), max(2, a.warmup // 5)
+    mk.mark(3)
+    ms = _time_steps([bound], steps, warm, rt)
+    recs = _kernel_records(3, bound.launches, _time_in_step([bound], max(3, steps), rt))
+    flops = sum(w for _, _, w in sections()[3][1])
+    step_rec = {"label": "mlp", "kernel": " + ".join(l.symbol for l in bound.launches), "bound": "mfma"}
+    entry = {"config": 3, "workload": "swiglu_mlp", "shape": {"M": MLP_M, "hidden": MLP_H, "ffn": MLP_F},
+             "dtype": "bf16", "us_per_step": round(ms * 1e3, 2),
+             "roofline": _roofline(3, step_rec, us=ms * 1e3, work=flops), "kernels": recs}
 
-    rows = np.arange(0, M, M // 16)
-    ref = K.swiglu_mlp(x[rows], *ws)
-    got = dt.to_float32(out.numpy()[rows])
-    scale = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
-    ok = bool(np.all(np.abs(got - ref) <= 2e-2 * (np.abs(ref) + scale)))
-    tflops = flops / (ms_step * 1e-3) / 1e12
-    return {
-        "workload": "swiglu_mlp", "shape": {"M": M, "hidden": H, "ffn": F}, "dtype": "bf16",
-        "flops_per_step": flops, "us_per_step": round(ms_step * 1e3, 2),
-        "tflops": round(tflops, 1), "frac_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4),
-        "kernels": per, "parity_ok": ok,
-    }
+    def cpu():
+        from oracle import kernels as K
+        from oracle import numerics as N
+
+        rows = np.arange(0, MLP_M, 16)  # 256 rows: rows are independent
+        K.swiglu_mlp(x[:8], *ws)
+        t, ts, ref = _timed(lambda: K.swiglu_mlp(x[rows], *ws, round_h=N.bf16_round), 3)
+        f = flops * len(rows) / MLP_M
+        return ({"value": round(f / t / 1e12, 3), "unit": "TFLOP/s", "cores": _blas_threads(),
+                 "kind": "port", "blas_threads": _blas_threads(),
+                 "sample": f"{len(rows)} of {MLP_M} rows (fp32 NumPy matmuls on OpenBLAS), median of "
+                           f"{len(ts)} runs ({sum(ts):.2f} s); host has {_host_cores()} cores",
+                 "ms_full_equiv": round(t * MLP_M / len(rows) * 1e3, 1)},
+                _parity(dt.to_float32(out.numpy()[rows]), ref))
+
+    return entry, cpu
 
 
-def bench_linattn(steps, warmup, rt):
-    """Chunked causal linear attention: B=4, H=16, T=8192, d=128 bf16."""
+def bench_linattn(a, rt, mk):
     from nkipy_amd.core import dtypes as dt
     from nkipy_amd.kernels import chunked_linear_attention_kernel
     from nkipy_amd.runtime import DeviceKernel, DeviceTensor
 
-    B, H, T, D = 4, 16, 8192, 128
+    shape = (LA_B, LA_H, LA_T, LA_D)
     rng = np.random.default_rng(42)
-    host = [dt.round_to_bf16((rng.standard_normal((B, H, T, D)) / np.sqrt(D)).astype(np.float32))
-            for _ in range(3)]
-    args = [dt.to_bf16(a) for a in host]
+    host = [dt.round_to_bf16((rng.standard_normal(shape) / np.sqrt(LA_D)).astype(np.float32)) for _ in range(3)]
+    args = [dt.to_bf16(v) for v in host]
     dk = DeviceKernel.compile_and_load(chunked_linear_attention_kernel, *args, name="linear_attention")
     if dk.plan.kernel_kinds != ["linear_attention"]:
         raise RuntimeError(f"linear attention did not lower to the fused kernel: {dk.plan.kernel_kinds}")
-    alg_bytes = 4 * B * H * T * D * 2
-    nsets = _sets_for(alg_bytes)
-    sets = [[DeviceTensor.from_numpy(a, name=nm) for nm, a in zip("qkv", args)]
-            + [DeviceTensor.empty((B, H, T, D), dt.bfloat16, name="output0")] for _ in range(nsets)]
-    bounds = [dk.executor.bind({"q": s[0].ptr, "k": s[1].ptr, "v": s[2].ptr, "output0": s[3].ptr})
-              for s in sets]
-    # one step = the whole operation (the prefix-state kernel, when the scan
-    # is segmented, plus the scan)
-    ms_step, _ = _time_bound(bounds, steps, warmup, rt)
-    ms_launch = ms_step
-    from oracle import kernels as K
+    work = 4 * LA_B * LA_H * LA_T * LA_D * 2
+    sets = [[DeviceTensor.from_numpy(v, name=nm) for nm, v in zip("qkv", args)]
+            + [DeviceTensor.empty(shape, dt.bfloat16, name="output0")] for _ in range(_sets_for(work))]
+    bounds = [dk.executor.bind({"q": s[0].ptr, "k": s[1].ptr, "v": s[2].ptr, "output0": s[3].ptr}) for s in sets]
+    if len(bounds[0].launches) != len(sections()[4][1]):
+        raise RuntimeError("linear attention step has an unexpected launch count")
+    steps, warm = max(10, a.steps // 10), max(2, a.warmup // 5)
+    mk.mark(4)
+    ms = _time_steps(bounds, steps, warm, rt)
+    recs = _kernel_records(4, bounds[0].launches, _time_in_step(bounds, max(5, steps), rt))
+    step_rec = {"label": "step", "kernel": " + ".join(l.symbol for l in bounds[0].launches), "bound": "hbm"}
+    roof = _roofline(4, step_rec, us=ms * 1e3, work=work)
+    t_pre, t_scan = _traffic("linear_attention/prefix_states"), _traffic("linear_attention/scan")
+    roof["traffic"] = (t_pre + t_scan) if (t_pre and t_scan) else None
+    entry = {"config": 4, "workload": "chunked_linear_attention", "shape": list(shape), "chunk": 64,
+             "dtype": "bf16", "us_per_step": round(ms * 1e3, 2), "roofline": roof, "kernels": recs,
+             "flops_per_step": sum(l.flops for l in bounds[0].launches), "buffer_sets": len(sets)}
 
-    got = dt.to_float32(sets[0][3].numpy()[1:2, 5:6])
-    ref = K.linear_attention_chunked(*[a[1:2, 5:6] for a in host])
-    scale = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
-    ok = bool(np.all(np.abs(got - ref) <= 2e-2 * (np.abs(ref) + scale)))
-    gbs = alg_bytes / (ms_launch * 1e-3) / 1e9
-    return {
-        "workload": "chunked_linear_attention", "shape": [B, H, T, D], "chunk": 64, "dtype": "bf16",
-        "kernel": " + ".join(l.symbol for l in bounds[0].launches), "bytes_per_launch": alg_bytes,
-        "us_per_launch": round(ms_launch * 1e3, 2), "gbs": round(gbs, 1),
-        "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
-        "tflops": round(bounds[0].launches[-1].flops / (ms_launch * 1e-3) / 1e12, 1),
-        "parity_ok": ok,
-    }
+    def cpu():
+        from oracle import kernels as K
+
+        heads = [(0, 0), (3, 15)]
+        sample = lambda: [K.linear_attention_chunked(*[v[b:b + 1, h:h + 1] for v in host]) for b, h in heads]
+        t, ts, refs = _timed(sample, 3)
+        per_head = 4 * LA_T * LA_D * 2
+        got = dt.to_float32(sets[0][3].numpy())
+        return ({"value": round(per_head * len(heads) / t / 1e9, 3), "unit": "GB/s", "cores": _blas_threads(),
+                 "kind": "port", "blas_threads": _blas_threads(),
+                 "sample": f"{len(heads)} of {LA_B * LA_H} heads (fp32 chunked recurrence in NumPy), median "
+                           f"of {len(ts)} runs ({sum(ts):.2f} s); host has {_host_cores()} cores",
+                 "ms_full_equiv": round(t * LA_B * LA_H / len(heads) * 1e3, 1)},
+                _parity(np.concatenate([got[b:b + 1, h:h + 1] for b, h in heads]), np.concatenate(refs)))
+
+    return entry, cpu
 
 
 def _quantize_fp8(rng, shape):
@@ -278,23 +455,19 @@ def _quantize_fp8(rng, shape):
     return codes, scale.numpy().astype(np.float32)
 
 
-def bench_decoder(steps, warmup, rt):
-    """Llama-style decoder layer, fp8 weights: hidden 4096, 32 / 8 heads,
-    head_dim 128, FFN 14336, RoPE theta 5e5, causal attention, x bf16
-    (8, 2048, 4096).  One step = the whole layer (nine kernels)."""
+def bench_decoder(a, rt, mk):
     from nkipy_amd.core import dtypes as dt
     from nkipy_amd.kernels import llama_decoder_layer_fp8
     from nkipy_amd.runtime import DeviceKernel, DeviceTensor
 
-    B, S, Hq, Hkv, D, F = 8, 2048, 32, 8, 128, 14336
-    hid = Hq * D
+    B, S, hid = DEC_B, DEC_S, DEC_HID
     rng = np.random.default_rng(42)
     x = dt.round_to_bf16(rng.standard_normal((B, S, hid), dtype=np.float32))
-    w = {"n_heads": Hq, "n_kv_heads": Hkv, "eps": 1e-5, "rope_theta": 5.0e5,
+    w = {"n_heads": DEC_HQ, "n_kv_heads": DEC_HKV, "eps": 1e-5, "rope_theta": 5.0e5,
          "attn_norm": np.ones(hid, np.float32), "mlp_norm": np.ones(hid, np.float32)}
-    for name, shape in (("wqkv", ((Hq + 2 * Hkv) * D, hid)), ("wo", (hid, hid)),
-                        ("w_gate", (F, hid)), ("w_up", (F, hid)), ("w_down", (hid, F))):
-        w[name], w[name + "_scale"] = _quantize_fp8(rng, shape)
+    for name, shp in (("wqkv", ((DEC_HQ + 2 * DEC_HKV) * DEC_D, hid)), ("wo", (hid, hid)),
+                      ("w_gate", (DEC_F, hid)), ("w_up", (DEC_F, hid)), ("w_down", (hid, DEC_F))):
+        w[name], w[name + "_scale"] = _quantize_fp8(rng, shp)
     f8 = lambda c: c.view(dt.float8_e4m3fn)
     args = [dt.to_bf16(x), dt.to_bf16(w["attn_norm"]), f8(w["wqkv"]), w["wqkv_scale"], f8(w["wo"]),
             w["wo_scale"], dt.to_bf16(w["mlp_norm"]), f8(w["w_gate"]), w["w_gate_scale"], f8(w["w_up"]),
@@ -304,45 +477,58 @@ def bench_decoder(steps, warmup, rt):
     if dk.plan.kernel_kinds != kinds:
         raise RuntimeError(f"decoder layer did not lower to the fused kernels: {dk.plan.kernel_kinds}")
     names = [p.name for p in dk.graph.parameters]
-    ins = {n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(names, args)}
-    out = DeviceTensor.empty((B, S, hid), dt.bfloat16, name="output0")
-    bound = dk.executor.bind({**{k: v.ptr for k, v in ins.items()}, "output0": out.ptr})
-    ms_step, _ = _time_bound([bound], steps, warmup, rt)
-    per = []
-    for kind, l in zip(kinds, bound.launches):
-        ms = l.function(rt).time(l.grid, l.block, l.args, warmup=2, iters=max(3, steps // 2))
-        e = {"kind": kind, "kernel": l.symbol, "us": round(ms * 1e3, 2)}
-        if l.flops and kind in ("gemm", "gemm_swiglu", "attention"):
-            tf = l.flops / (ms * 1e-3) / 1e12
-            e.update(tflops=round(tf, 1), frac_bf16_peak=round(tf / BF16_PEAK_TFLOPS, 4))
-        else:
-            gbs = l.bytes / (ms * 1e-3) / 1e9
-            e.update(gbs=round(gbs, 1), frac_hbm=round(gbs / HBM_PEAK_GBS, 4))
-        per.append(e)
-    from oracle import kernels as K
+    ins = {n: DeviceTensor.from_numpy(v, name=n) for n, v in zip(names, args)}
+    # the activations rotate over three sets (384 MB), so the first RMSNorm
+    # reads x from HBM; the weights stay as they are
+    xs = [ins[names[0]]] + [DeviceTensor.from_numpy(args[0], name=names[0]) for _ in range(2)]
+    outs = [DeviceTensor.empty((B, S, hid), dt.bfloat16, name="output0") for _ in xs]
+    bounds = [dk.executor.bind({**{k: v.ptr for k, v in ins.items()}, names[0]: xv.ptr, "output0": o.ptr})
+              for xv, o in zip(xs, outs)]
+    steps, warm = max(5, a.steps // 20), max(2, a.warmup // 5)
+    mk.mark(5)
+    ms = _time_steps(bounds, steps, warm, rt)
+    recs = _kernel_records(5, bounds[0].launches, _time_in_step(bounds, max(6, steps), rt))
+    flops = sum(l.flops for l in bounds[0].launches)
+    ach = flops / (ms * 1e-3) / 1e12
+    roof = {"bound": "mfma", "kernel": "layer (9 kernels)", "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4),
+            "frac_of_fp8_peak": round(ach / FP8_PEAK_TFLOPS, 4), "traffic": None,
+            "work_per_launch": flops, "us_per_launch": round(ms * 1e3, 1),
+            "note": "fp8 weights are decoded exactly to bf16 for bf16 MFMAs (the activations stay bf16), "
+                    "so the bf16 dense peak is the ceiling; the fp8 fraction is given for reference"}
+    entry = {"config": 5, "workload": "llama_decoder_layer_fp8",
+             "shape": {"batch": B, "seq": S, "hidden": hid, "heads": DEC_HQ, "kv_heads": DEC_HKV,
+                       "head_dim": DEC_D, "ffn": DEC_F},
+             "dtype": "bf16 activations, e4m3fn weights with per-channel fp32 scales",
+             "value": round(ms * 1e3, 1), "unit": "us per layer", "higher_is_better": False,
+             "us_per_step": round(ms * 1e3, 1), "flops_per_layer": flops, "roofline": roof, "kernels": recs}
 
-    rows = np.array([0, 1029, 2047])
-    ref = K.decoder_layer_fp8_rows(x[3], w, rows)["y"]
-    got = dt.to_float32(out.numpy()[3, rows])
-    scale = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
-    ok = bool(np.all(np.abs(got - ref) <= 2e-2 * (np.abs(ref) + scale)))
-    flops = sum(l.flops for l in bound.launches)
-    return {
-        "workload": "llama_decoder_layer_fp8",
-        "shape": {"batch": B, "seq": S, "hidden": hid, "heads": Hq, "kv_heads": Hkv, "head_dim": D, "ffn": F},
-        "dtype": "bf16 activations, e4m3fn weights (decoded exactly to bf16 for the MFMA)",
-        "us_per_layer": round(ms_step * 1e3, 1), "flops_per_layer": flops,
-        "tflops": round(flops / (ms_step * 1e-3) / 1e12, 1), "kernels": per, "parity_ok": ok,
-    }
+    def cpu():
+        from oracle import kernels as K
+
+        t0 = time.perf_counter()
+        ref = K.decoder_layer_fp8(x[0:1], w)["y"]
+        t = time.perf_counter() - t0
+        f = flops / B
+        return ({"value": round(t * B * 1e6, 0), "unit": "us per layer (scaled from one sequence)",
+                 "tflops": round(f / t / 1e12, 3), "cores": _blas_threads(), "kind": "port",
+                 "blas_threads": _blas_threads(),
+                 "sample": f"1 of {B} sequences ({S} tokens, fp32 NumPy with OpenBLAS matmuls, weights "
+                           f"dequantized per call like the NumPy kernel), one run ({t:.2f} s); host has "
+                           f"{_host_cores()} cores"},
+                _parity(dt.to_float32(outs[0].numpy()[0:1]), ref, atol=np.inf))
+
+    return entry, cpu
 
 
-def calibrate_copy(rt, nbytes=1 << 30, reps=3):
+def calibrate_copy(rt, mk, nbytes=1 << 30, reps=3):
     """Plain streaming copy of a known size: rocprof's FETCH_SIZE / WRITE_SIZE
     for nk_copy16 read against 1 GiB give the counter scale factors."""
     from nkipy_amd.dispatch.generic import copy16
 
     src, dst = rt.malloc(nbytes), rt.malloc(nbytes)
     rt.memset(src, 0x5a, nbytes)
+    mk.mark(9)
     l = copy16(src, dst, nbytes)
     for _ in range(reps):
         l.run(rt)
@@ -352,113 +538,204 @@ def calibrate_copy(rt, nbytes=1 << 30, reps=3):
     log(f"copy calibration: {reps} x nk_copy16 of {nbytes} bytes")
 
 
-def cpu_baseline_rmsnorm(host, budget_s=12.0):
-    from oracle import kernels as K
-
-    x, r, w = host
-    rows = x.shape[0]
-    K.residual_rmsnorm_bf16(x[:64], r[:64], w, 1e-6)  # warm-up
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 20 and (time.perf_counter() < t_end or len(times) < 3):
-        t0 = time.perf_counter()
-        K.residual_rmsnorm_bf16(x, r, w, 1e-6)
-        times.append(time.perf_counter() - t0)
-    t = float(np.median(times))
-    nbytes = rows * x.shape[1] * 2 * 3 + x.shape[1] * 2
-    return {
-        "value": nbytes / t / 1e9,
-        "unit": "GB/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"full workload (8192x4096 bf16 as fp32-held values), median of {len(times)} "
-                  f"runs ({sum(times):.1f} s); NumPy elementwise is single-threaded; "
-                  f"host has {len(os.sched_getaffinity(0))} cores",
-        "ms": t * 1e3,
-    }
+# ---------------------------------------------------------------------------
+# profiler summaries (no GPU)
+# ---------------------------------------------------------------------------
+def _label_dispatches(rows):
+    """rows: dicts with name, wgs (workgroups), dispatch, sorted by dispatch.
+    Yields (workload id, launch label, row) for the launches of the marked
+    sections: a marker (nk_copy16 with MARK_BASE + id workgroups) opens a
+    section, whose launches are whole steps, labelled by position."""
+    secs = sections()
+    cur, pos = None, 0
+    for r in rows:
+        if r["name"].startswith("__amd"):
+            continue  # runtime copies and fills
+        if r["name"] == "nk_copy16" and (r["wgs"] - MARK_BASE) in secs:
+            cur, pos = r["wgs"] - MARK_BASE, 0
+            continue
+        if cur is None:
+            continue
+        labels = secs[cur][1]
+        yield cur, labels[pos % len(labels)][0], r
+        pos += 1
 
 
+def _order(secs):
+    return lambda kv: (kv[0][0], [l for l, _, _ in secs[kv[0][0]][1]].index(kv[0][1]))
+
+
+def summarize(d, traffic_json=None):
+    secs = sections()
+    out = []
+    for path in sorted(glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)):
+        rows = []
+        for r in csv.DictReader(open(path)):
+            rows.append({"name": r["Kernel_Name"],
+                         "wgs": int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"])),
+                         "dispatch": int(r["Dispatch_Id"]),
+                         "us": (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3})
+        rows.sort(key=lambda r: r["dispatch"])
+        agg = {}
+        for sid, label, r in _label_dispatches(rows):
+            agg.setdefault((sid, label), []).append(r)
+        out.append(f"kernel trace: {os.path.relpath(path, d)}")
+        out.append(f"{'workload/launch':<38} {'kernel':<34} {'wgs':>6} {'calls':>6} {'avg_us':>9} "
+                   f"{'min_us':>9} {'max_us':>9} {'achieved':>10} {'frac':>7}")
+        for (sid, label), rs in sorted(agg.items(), key=_order(secs)):
+            us = [r["us"] for r in rs]
+            avg = sum(us) / len(us)
+            bound, work = {l: (b, w) for l, b, w in secs[sid][1]}[label]
+            ach, peak, unit = _rate(bound, work, avg)
+            out.append(f"{secs[sid][0] + '/' + label:<38} {rs[0]['name'][:34]:<34} {rs[0]['wgs']:>6} "
+                       f"{len(us):>6} {avg:>9.2f} {min(us):>9.2f} {max(us):>9.2f} {ach:>8.1f} {unit[:2]} {ach / peak:>7.3f}")
+        out.append("")
+    traffic = {}
+    for path in sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)):
+        disp = {}
+        for r in csv.DictReader(open(path)):
+            k = int(r["Dispatch_Id"])
+            e = disp.setdefault(k, {"name": r["Kernel_Name"],
+                                    "wgs": int(r["Grid_Size"]) // max(1, int(r["Workgroup_Size"])),
+                                    "dispatch": k, "c": {}})
+            e["c"][r["Counter_Name"]] = e["c"].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        rows = sorted(disp.values(), key=lambda r: r["dispatch"])
+        agg = {}
+        for sid, label, r in _label_dispatches(rows):
+            agg.setdefault((sid, label), []).append(r)
+        names = sorted({c for r in rows for c in r["c"]})
+        out.append(f"counters: {os.path.relpath(path, d)} ({', '.join(names)}; per dispatch, mean)")
+        cal = agg.get((9, "copy16"))
+        scale = {}
+        if cal:
+            for c, alg in (("FETCH_SIZE", 2**30), ("WRITE_SIZE", 2**30)):
+                v = [r["c"][c] for r in cal if c in r["c"]]
+                if v:
+                    scale[c] = (sum(v) / len(v)) * 1024 / alg
+                    out.append(f"calibration: nk_copy16 of 1 GiB each way reads {c} = {sum(v) / len(v):.1f} KiB "
+                               f"(scale {scale[c]:.4f})")
+        for (sid, label), rs in sorted(agg.items(), key=_order(secs)):
+            if sid == 9:
+                continue
+            mean = {c: sum(r["c"].get(c, 0.0) for r in rs) / len(rs) for c in names}
+            parts = [f"{secs[sid][0] + '/' + label:<38}", f"n={len(rs):<4}"]
+            # GRBM_GUI_ACTIVE is summed over the 8 XCDs (each has its own
+            # GRBM), SQ_VALU_MFMA_BUSY_CYCLES over the 1024 SIMDs and
+            # SQ_BUSY_CU_CYCLES over the 256 CUs
+            gui = mean.get("GRBM_GUI_ACTIVE", 0.0) / XCDS
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in mean and gui:
+                parts.append(f"mfma_busy={mean['SQ_VALU_MFMA_BUSY_CYCLES'] / (4 * CUS * gui):.3f}")
+            if "SQ_BUSY_CU_CYCLES" in mean and gui:
+                parts.append(f"cu_busy={mean['SQ_BUSY_CU_CYCLES'] / (CUS * gui):.3f}")
+            for c in names:
+                parts.append(f"{c}={mean[c]:.6g}")
+            key = f"{secs[sid][0]}/{label}"
+            bound, work = {l: (b, w) for l, b, w in secs[sid][1]}[label]
+            for c in ("FETCH_SIZE", "WRITE_SIZE"):
+                if c in mean and c in scale:
+                    byts = mean[c] * 1024 / scale[c]
+                    parts.append(f"{c.split('_')[0].lower()}_MB={byts / 1e6:.1f}")
+                    traffic.setdefault(key, {})[c.lower().replace("_size", "_bytes")] = int(byts)
+                    if bound == "hbm":
+                        traffic[key]["algorithmic_bytes"] = work
+            out.append("  ".join(parts))
+        out.append("")
+    if traffic_json:
+        merged = {}
+        if os.path.exists(traffic_json):
+            with open(traffic_json) as f:
+                merged = json.load(f)
+        for key, e in traffic.items():
+            merged.setdefault(key, {}).update(e)
+        for e in merged.values():
+            if "fetch_bytes" in e and "write_bytes" in e:
+                e["total_bytes"] = e["fetch_bytes"] + e["write_bytes"]
+                if "algorithmic_bytes" in e:
+                    e["ratio"] = round(e["total_bytes"] / e["algorithmic_bytes"], 3)
+        with open(traffic_json, "w") as f:
+            json.dump(merged, f, indent=1, sort_keys=True)
+    print("\n".join(out))
+
+
+# ---------------------------------------------------------------------------
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--configs", default="1,2,3,4,5")
+    ap.add_argument("--mark-sections", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 1 GiB streaming copy (calibrates HBM traffic counters)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py runs on exactly one GPU; --gpus {args.gpus} is not supported "
+    ap.add_argument("--summarize", metavar="DIR", help="summarize rocprofv3 CSV output of a marked run")
+    ap.add_argument("--traffic-json", metavar="PATH", help="with --summarize: merge HBM traffic into PATH")
+    a = ap.parse_args()
+    if a.summarize:
+        summarize(a.summarize, a.traffic_json)
+        return
+    if a.gpus != 1:
+        print(f"bench.py runs on exactly one GPU; --gpus {a.gpus} is not supported "
               "(the kernels run on one GPU's share of the work; no multi-GPU leg is implemented)", file=sys.stderr)
         sys.exit(2)
+    want = {int(c) for c in a.configs.split(",") if c}
+    if 2 not in want:
+        want.add(2)  # the headline
 
     from nkipy_amd.runtime.hip import get_runtime
 
     rt = get_runtime()
     info = rt.device_info()
     log(f"device {info['arch']} CUs={info['cu_count']} sclk={info['clock_khz'] / 1e6:.2f} GHz")
+    mk = Marker(rt, a.mark_sections)
+    if a.calibrate_copy:
+        calibrate_copy(rt, mk)
 
-    if args.calibrate_copy:
-        calibrate_copy(rt)
-    rms = bench_rmsnorm(args.steps, args.warmup, rt)
-    log(f"rmsnorm: {rms['us_per_launch']:.2f} us/launch, {rms['gbs_launch']:.0f} GB/s "
-        f"({rms['kernel']}), parity_ok={rms['parity_ok']}")
-    sm = bench_softmax(args.steps, args.warmup, rt)
-    log(f"softmax: {sm['us_per_launch']:.2f} us/launch, {sm['gbs']:.0f} GB/s, rel err {sm['max_rel_err']:.2e}")
-    sw = bench_swiglu(max(5, args.steps // 20), max(2, args.warmup // 5), rt)
-    log(f"swiglu mlp: {sw['us_per_step']:.1f} us/step, {sw['tflops']:.1f} TFLOP/s "
-        f"({sw['frac_bf16_peak'] * 100:.1f}% of bf16 peak), parity_ok={sw['parity_ok']}")
-    la = bench_linattn(max(5, args.steps // 20), max(2, args.warmup // 5), rt)
-    log(f"linear attention: {la['us_per_launch']:.1f} us, {la['gbs']:.0f} GB/s, parity_ok={la['parity_ok']}")
-    dec = bench_decoder(max(5, args.steps // 20), max(2, args.warmup // 5), rt)
-    log(f"decoder layer fp8: {dec['us_per_layer']:.1f} us/layer, {dec['tflops']:.1f} TFLOP/s, "
-        f"parity_ok={dec['parity_ok']}")
-    for k in dec["kernels"]:
-        log(f"   {k}")
+    benches = {1: bench_softmax, 2: bench_rmsnorm, 3: bench_swiglu, 4: bench_linattn, 5: bench_decoder}
+    entries, legs = {}, {}
+    for cid in sorted(want):
+        e, leg = benches[cid](a, rt, mk)
+        entries[cid], legs[cid] = e, leg
+        r = e["roofline"]
+        log(f"config {cid} {e['workload']}: {e['us_per_step']} us/step, {r['achieved']} {r['unit']} "
+            f"({r['frac'] * 100:.1f}% of {r['peak']:.0f})")
+        for k in e["kernels"]:
+            log(f"   {k['label']:<20} {k['kernel']:<34} {k['us']:>9.2f} us  {k['achieved']:>8.1f} {k['unit']} "
+                f"({k['frac'] * 100:.1f}%)")
+    if not a.no_cpu:
+        for cid in sorted(want):
+            cpu, par = legs[cid]()
+            entries[cid]["cpu_baseline"], entries[cid]["parity"] = cpu, par
+            log(f"config {cid} cpu baseline: {cpu['value']} {cpu['unit']} ({cpu['sample']}); parity "
+                f"max_abs {par['max_abs']:.3e} worst/bar {par['worst_of_bar']} ok={par['ok']}")
+    else:
+        for cid in sorted(want):
+            entries[cid]["cpu_baseline"], entries[cid]["parity"] = None, None
 
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline_rmsnorm(rms["host"])
-        log(f"cpu baseline: {cpu['value']:.2f} GB/s ({cpu['ms']:.1f} ms per pass)")
-        cpu.pop("ms")
-
-    achieved = rms["gbs_launch"]
+    head = entries[2]
+    hr = head["roofline"]
     line = {
-        "metric": "per-kernel achieved HBM GB/s & MFMA TFLOP/s vs peak; fp8 decoder-layer latency (us)",
-        "value": round(rms["gbs_step"], 2),
+        "metric": METRIC,
+        "value": round(hr["work_per_launch"] / (head["ms_per_step"] * 1e-3) / 1e9, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": rms["ms_per_step"],
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded normal / uniform inputs of the workload's shapes)",
+        "data": "synthetic (seeded normal / uniform inputs of the workloads' shapes; random-init fp8 weights)",
         "config": {
             "workload": "residual_rmsnorm: x, r bf16 (8192, 4096), w bf16 (4096,), eps 1e-6, fp32 accumulation",
-            "rows": 8192, "hidden": 4096, "parallelism": "single-gpu",
+            "rows": RMS_ROWS, "hidden": RMS_N, "parallelism": "single-gpu",
         },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": rms["kernel"],
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": _traffic(rms["kernel"]),
-            "bytes_per_launch": rms["bytes_per_launch"],
-            "us_per_launch": round(rms["us_per_launch"], 3),
-        },
-        "cpu_baseline": cpu,
-        "parity_ok": rms["parity_ok"],
-        "kernels": {
-            "softmax": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in sm.items()},
-            "swiglu_mlp": sw,
-            "linear_attention": la,
-            "decoder_layer_fp8": dec,
-        },
+        "roofline": hr,
+        "cpu_baseline": head["cpu_baseline"],
+        "parity_ok": head["parity"]["ok"] if head["parity"] else None,
+        "decoder_layer_fp8_us": entries[5]["value"] if 5 in entries else None,
+        "configs": [entries[c] for c in sorted(entries)],
     }
     print(json.dumps(line), flush=True)
 

@@ -155,6 +155,29 @@ class BoundPlan:
             "plan launch",
         )
 
+    def run_range(self, start: int, stop: int):
+        """Launches ``start .. stop-1`` of the plan (all of them: ``run``)."""
+        from nkipy_amd.runtime.hip import _check, check_current
+
+        check_current(self.rt, "plan")
+        if not 0 <= start <= stop <= self._n:
+            raise IndexError(f"launch range {start}..{stop} outside 0..{self._n}")
+        if stop == start:
+            return
+        vp, u, sz = ctypes.c_void_p, ctypes.c_uint, ctypes.c_size_t
+
+        def at(arr, ctype, i):
+            return ctypes.cast(ctypes.addressof(arr) + i * ctypes.sizeof(ctype), ctypes.POINTER(ctype))
+
+        _check(
+            self.rt.lib.nkh_launch_batch(
+                stop - start, at(self._fns, vp, start), at(self._grids, u, 3 * start),
+                at(self._blocks, u, 3 * start), at(self._shared, u, start),
+                self._kernargs, at(self._offsets, sz, start), at(self._sizes, sz, start),
+            ),
+            "plan launch",
+        )
+
 
 class PlanExecutor:
     """Owns a plan's temporaries and constants and runs it on bound I/O."""
