@@ -180,26 +180,52 @@ class BoundPlan:
 
 
 class PlanExecutor:
-    """Owns a plan's temporaries and constants and runs it on bound I/O."""
+    """Owns a plan's temporaries and constants and runs it on bound I/O.
 
-    def __init__(self, plan: Plan):
+    ``plan`` is a lowered :class:`Plan` or a loaded relocatable artefact
+    (:class:`nkipy_amd.dispatch.artifact.RelocatablePlan`); an artefact binds
+    by patching addresses, and falls back to ``lower_fn()`` (the full plan,
+    lowered on first need) for I/O addresses that are not 256-byte aligned."""
+
+    def __init__(self, plan, lower_fn=None):
         from nkipy_amd.runtime.device_tensor import DeviceBuffer
         from nkipy_amd.runtime.hip import get_runtime
 
         self.plan = plan
+        self.lower_fn = lower_fn
+        self._full: Optional[Plan] = plan if isinstance(plan, Plan) else None
         self.rt = get_runtime()
         self._owned: Dict[int, DeviceBuffer] = {}
+        pname = plan.graph.name if isinstance(plan, Plan) else plan.name
         for b in plan.buffers:
             if b.kind in ("temp", "const"):
-                buf = DeviceBuffer(max(b.nbytes, 16), name=f"{plan.graph.name}:{b.kind}{b.index}")
+                buf = DeviceBuffer(max(b.nbytes, 16), name=f"{pname}:{b.kind}{b.index}")
                 if b.kind == "const" and b.data is not None and b.data.nbytes:
                     raw = np.ascontiguousarray(dt.numpy_storage(np.ascontiguousarray(b.data)))
                     buf.write(raw.ctypes.data, raw.nbytes)
                 self._owned[b.index] = buf
         self._bound: Dict[tuple, BoundPlan] = {}
 
+    def _full_plan(self) -> Plan:
+        from nkipy_amd.runtime.hip import SpikeError
+
+        if self._full is None:
+            if self.lower_fn is None:
+                raise SpikeError("this kernel was loaded from its artefact alone: its I/O must be 256-byte "
+                                 "aligned device buffers")
+            full = self.lower_fn()
+            if [(b.index, b.kind, b.nbytes) for b in full.buffers] != \
+                    [(b.index, b.kind, b.nbytes) for b in self.plan.buffers]:
+                raise SpikeError("the lowered plan does not match the loaded artefact")
+            self._full = full
+        return self._full
+
     def _bind(self, bases: Dict[int, int]) -> BoundPlan:
-        plan = self.plan
+        if not isinstance(self.plan, Plan) and all(
+                bases[i] % 256 == 0 for i in list(self.plan.input_buffers.values())
+                + list(self.plan.output_buffers.values())):
+            return self.plan.bind(bases, self.rt)
+        plan = self._full_plan()
 
         def addr(v) -> int:
             # a graph value, or a Slot of a step's own workspace temporary

@@ -8,8 +8,11 @@ spike/src/spike/spike_model.py:19-343):
   kernel on the given arguments (NumPy arrays, DeviceTensors or torch
   tensors -- only shapes and dtypes are read), lowers the graph to a plan of
   gfx950 kernels and loads it.  Loaded kernels are cached in memory by
-  ``name + content hash`` (``_LOADED_KERNELS``), and the plan is written to
-  ``build_dir/<name>_<hash>/plan.json`` as the build artefact.
+  ``name + content hash`` (``_LOADED_KERNELS``); the lowered plan is written
+  to ``build_dir/<name>_<hash>/plan.json`` in relocatable form, and a later
+  process tracing the same graph loads that artefact instead of lowering
+  (``nkipy_amd.dispatch.artifact``).  ``load_from_neff(path)`` loads an
+  artefact without its graph.
 * ``kernel(inputs, outputs=None)`` binds named DeviceTensors, validates
   names / shapes / dtypes, runs the plan and waits for it (the synchronous
   completion point of nrt_execute); with ``outputs=None`` it allocates and
@@ -125,23 +128,27 @@ class TensorMetadata:
 class DeviceKernel:
     """A traced kernel lowered to gfx950 kernels and loaded on the device."""
 
-    def __init__(self, graph, plan, name: str, build_path: Optional[str] = None):
+    def __init__(self, graph, plan, name: str, build_path: Optional[str] = None, lower_fn=None):
         from nkipy_amd.dispatch.plan import PlanExecutor
 
         self.graph = graph
         self.plan = plan
         self.name = name
         self.neff_path = build_path  # name kept from the reference API
-        self.executor = PlanExecutor(plan)
+        self.executor = PlanExecutor(plan, lower_fn=lower_fn)
         self.core_id = get_runtime().device
-        self.input_tensors_info = {
-            p.name: TensorMetadata(p.nbytes, dt.name(p.dtype), list(p.shape)) for p in graph.parameters
-        }
-        self.output_tensors_info = {
-            r.name: TensorMetadata(r.nbytes, dt.name(r.dtype), list(r.shape)) for r in graph.results
-        }
-        self._in_specs = {p.name: (tuple(p.shape), p.dtype) for p in graph.parameters}
-        self._out_specs = {r.name: (tuple(r.shape), r.dtype) for r in graph.results}
+        if graph is not None:
+            ins = [(p.name, tuple(p.shape), p.dtype) for p in graph.parameters]
+            outs = [(r.name, tuple(r.shape), r.dtype) for r in graph.results]
+        else:  # a loaded artefact carries the I/O contract
+            ins = [(n, tuple(sh), dt.canonical(d)) for n, sh, d in plan.io["inputs"]]
+            outs = [(n, tuple(sh), dt.canonical(d)) for n, sh, d in plan.io["outputs"]]
+        nbytes = lambda sh, d: int(np.prod(sh, dtype=np.int64)) * dt.itemsize(d)
+        self.input_tensors_info = {n: TensorMetadata(nbytes(sh, d), dt.name(d), list(sh)) for n, sh, d in ins}
+        self.output_tensors_info = {n: TensorMetadata(nbytes(sh, d), dt.name(d), list(sh)) for n, sh, d in outs}
+        self._in_specs = {n: (sh, dt.canonical(d)) for n, sh, d in ins}
+        self._out_specs = {n: (sh, dt.canonical(d)) for n, sh, d in outs}
+        self._staging: Dict[str, DeviceTensor] = {}
 
     # ------------------------------------------------------------------
     @classmethod
@@ -178,12 +185,37 @@ class DeviceKernel:
             raise SpikeError("collective execution is not supported by the single-GPU HIP backend")
         if is_spmd and distributed:
             dist.barrier()
-        plan = cls._lower(graph)
-        _write_plan(plan, plan_path)
-        dk = cls(graph, plan, name, plan_path)
+        from nkipy_amd.dispatch import artifact
+
+        cached = artifact.try_load(plan_path, graph) if use_cached_if_exists else None
+        if cached is not None:
+            # the artefact of an earlier process: no lowering (the reference
+            # skips neuronx-cc the same way, device_kernel.py:272-275)
+            logger.info(f"Kernel found in '{plan_path}', using cached (cache_key={cache_key})")
+            dk = cls(graph, cached, name, plan_path, lower_fn=lambda: cls._lower(graph))
+        else:
+            plan = cls._lower(graph)
+            artifact.write_artifact(plan, graph, plan_path)
+            dk = cls(graph, plan, name, plan_path)
         if use_cached_if_exists:
             _LOADED_KERNELS[cache_key] = dk
         return dk
+
+    @classmethod
+    def load_from_neff(cls, neff_path: str, name: Optional[str] = None, **kwargs) -> "DeviceKernel":
+        """Load a compiled artefact (the plan file ``compile_and_load`` or
+        ``compile_to_neff`` wrote) without its traced graph; the name is the
+        reference's (device_kernel.py:91-117)."""
+        from nkipy_amd.dispatch import artifact
+
+        try:
+            rp = artifact.RelocatablePlan.load(neff_path)
+        except (OSError, ValueError, KeyError) as e:
+            raise SpikeError(f"cannot load compiled kernel {neff_path}: {e}") from None
+        if not rp.is_current():
+            raise SpikeError(f"compiled kernel {neff_path} was built by other lowering code or code objects; "
+                             "compile it again")
+        return cls(None, rp, name or rp.name, neff_path)
 
     @staticmethod
     def _lower(graph):
@@ -233,6 +265,23 @@ class DeviceKernel:
         ptrs.update({k: v.ptr for k, v in outputs.items()})
         return ptrs
 
+    def _overlapping_outputs(self, inputs, outputs) -> List[str]:
+        """Outputs whose buffer overlaps an input other than the one it is
+        declared to alias (e.g. a layer writing its result over its own
+        input x, qwen3.py:281-338): the plan may still read that input after
+        writing the output, so such outputs go through a staging buffer."""
+        alias_in = self.plan.alias_outputs
+        hits = []
+        for on, ot in outputs.items():
+            lo, hi = ot.ptr, ot.ptr + ot.nbytes
+            for inn, it in inputs.items():
+                if alias_in.get(on) == inn:
+                    continue
+                if it.ptr < hi and lo < it.ptr + it.nbytes:
+                    hits.append(on)
+                    break
+        return hits
+
     def __call__(self, inputs: Dict[str, DeviceTensor], outputs: Dict[str, DeviceTensor] = None,
                  save_trace: bool = False, ntff_name: Optional[str] = None, sync: bool = True):
         auto = outputs is None
@@ -242,7 +291,21 @@ class DeviceKernel:
                 if in_name in inputs:
                     outputs[out_name] = inputs[in_name]
         self._validate_io(inputs, outputs)
-        self.executor.run(self._io_ptrs(inputs, outputs))
+        staged = self._overlapping_outputs(inputs, outputs)
+        if staged:
+            run_outputs = dict(outputs)
+            for on in staged:
+                st = self._staging.get(on)
+                if st is None or st.tensor_ref.is_freed:
+                    shape, dtype = self._out_specs[on]
+                    st = self._staging[on] = DeviceTensor.empty(shape, dtype, name=on)
+                run_outputs[on] = st
+            self.executor.run(self._io_ptrs(inputs, run_outputs))
+            rt = get_runtime()
+            for on in staged:
+                rt.d2d(outputs[on].ptr, run_outputs[on].ptr, outputs[on].nbytes)
+        else:
+            self.executor.run(self._io_ptrs(inputs, outputs))
         if sync:
             get_runtime().sync()
         if auto:
@@ -286,14 +349,3 @@ class DeviceKernel:
 
     def __repr__(self):
         return f"DeviceKernel('{self.name}', steps={[s.kind for s in self.plan.steps]})"
-
-
-def _write_plan(plan, path: Optional[str]):
-    if not path:
-        return
-    try:
-        os.makedirs(os.path.dirname(path), exist_ok=True)
-        with open(path, "w") as f:
-            json.dump(plan.describe(), f, indent=1)
-    except OSError as e:  # the artefact is informational
-        logger.warning(f"could not write plan artefact {path}: {e}")
