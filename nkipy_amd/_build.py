@@ -119,6 +119,7 @@ def read_kernel_metadata(hsaco: Path) -> dict:
         ".vgpr_spill_count": "vgpr_spill",
         ".sgpr_spill_count": "sgpr_spill",
         ".max_flat_workgroup_size": "max_block",
+        ".private_segment_fixed_size": "scratch",
     }
     for line in txt.splitlines():
         line = line.strip().lstrip("- ").strip()

@@ -127,28 +127,25 @@ __device__ __forceinline__ f16x8_t cat(f16x4_t a, f16x4_t b) {
   return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// phi of 2 bf16 values (one 32-bit word) -> 2 fp16: exp(min(x, 0)) +
+// max(x, 0) in packed fp16 arithmetic.  bf16 -> fp16 is exact for |x| >=
+// 2^-14 (8 significant bits fit in 11), so the round-toward-zero pack only
+// truncates fp16 subnormals, where phi(x) = 1 + x rounds to 1 anyway.
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-
-// phi of 8 bf16 values -> 8 fp16 (16 bytes): exp(min(x, 0)) + max(x, 0) in
-// packed fp16 arithmetic.  bf16 -> fp16 is exact for |x| >= 2^-14 (8
-// significant bits fit in 11), so the round-toward-zero pack only truncates
-// fp16 subnormals, where phi(x) = 1 + x rounds to 1 anyway.
-__device__ __forceinline__ uint4 phi8(uint4 raw) {
-  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+__device__ __forceinline__ uint32_t phi2(uint32_t w) {
   const h2 zero = {(_Float16)0.f, (_Float16)0.f};
   const h2 l2e = {(_Float16)1.44269504088896340736f, (_Float16)1.44269504088896340736f};
-  uint32_t o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const h2 x = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(w[i] << 16),
-                                                                   __uint_as_float(w[i] & 0xffff0000u)));
-    const h2 t = __builtin_elementwise_min(x, zero) * l2e;
-    h2 e;
-    e[0] = __builtin_exp2f16(t[0]);
-    e[1] = __builtin_exp2f16(t[1]);
-    o[i] = __builtin_bit_cast(uint32_t, e + __builtin_elementwise_max(x, zero));
-  }
-  return make_uint4(o[0], o[1], o[2], o[3]);
+  const h2 x = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u)));
+  const h2 t = __builtin_elementwise_min(x, zero) * l2e;
+  h2 e;
+  e[0] = __builtin_exp2f16(t[0]);
+  e[1] = __builtin_exp2f16(t[1]);
+  return __builtin_bit_cast(uint32_t, e + __builtin_elementwise_max(x, zero));
+}
+// phi of 8 bf16 values -> 8 fp16 (16 bytes); per word, with no local arrays
+// (an array indexed in a loop the compiler leaves rolled goes to scratch)
+__device__ __forceinline__ uint4 phi8(uint4 raw) {
+  return make_uint4(phi2(raw.x), phi2(raw.y), phi2(raw.z), phi2(raw.w));
 }
 
 typedef float f2 __attribute__((ext_vector_type(2)));
@@ -159,13 +156,12 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
 }
 
-// bf16 x 8 -> fp16 x 8 (round to nearest even; V may be large)
+// bf16 x 2 -> fp16 x 2, round to nearest even (V may be large)
+__device__ __forceinline__ uint32_t f16x2_of(uint32_t w) {
+  return pack_f16x2(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u));
+}
 __device__ __forceinline__ uint4 to_f16x8(uint4 raw) {
-  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-  uint32_t o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = pack_f16x2(__uint_as_float(w[i] << 16), __uint_as_float(w[i] & 0xffff0000u));
-  return make_uint4(o[0], o[1], o[2], o[3]);
+  return make_uint4(f16x2_of(raw.x), f16x2_of(raw.y), f16x2_of(raw.z), f16x2_of(raw.w));
 }
 
 struct Stage {  // one chunk's operands in LDS

@@ -50,6 +50,22 @@ def test_last_error_and_uninitialised_calls_fail_cleanly():
         assert b"init" in lib.nkh_last_error().lower()
 
 
+def test_no_kernel_uses_scratch_memory():
+    """Register spills or private arrays left in memory would put scratch
+    traffic into the kernels' inner loops."""
+    import json
+
+    # SwiGLU epilogues that hold both products at once (spill outside the
+    # K loop); the 4-wave kernels are not the default path
+    known = {"nk_gemm8_swiglu_nt_e4m3_bf16", "nk_gemm_swiglu_nn_bf16_bf16", "nk_gemm_swiglu_nt_e4m3_bf16"}
+    for src in _build.kernel_sources():
+        man = json.loads(_build.hsaco_path(src.stem).with_suffix(".json").read_text())
+        for name, meta in man.items():
+            if name in known:
+                continue
+            assert meta.get("scratch", 0) == 0 and meta.get("vgpr_spill", 0) == 0, (name, meta)
+
+
 def test_every_kernel_object_has_a_manifest():
     for src in _build.kernel_sources():
         hsaco = _build.hsaco_path(src.stem)
