@@ -489,3 +489,61 @@ extern "C" __global__ __launch_bounds__(256) void nk_decode_e4m3_bf16(DecodeE4m3
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.n8; i += a.nthreads)
     a.dst[i] = e4m3x8_to_bf16x8(a.src[i]);
 }
+
+// Row-wise top-k (indices) along the last axis: one workgroup per row.
+// Round r selects, among the elements that come after round r-1's pick in
+// the order (value descending, index ascending) -- ascending values when
+// `largest` is 0 -- the first one; each round is one pass over the row, so
+// the input is never modified.  k is small (sampling); rows must not hold
+// NaN.
+struct TopkArgs {
+  const void *in;
+  uint32_t *idx;  // rows x k
+  int64_t rows;
+  int64_t n;
+  int32_t k;
+  int32_t largest;
+  int32_t dtype;
+  int32_t pad;
+};
+
+extern "C" __global__ __launch_bounds__(256) void nk_topk(TopkArgs a) {
+  __shared__ double sv[256];
+  __shared__ int64_t si[256];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int64_t base = row * a.n;
+  const double sgn = a.largest ? 1.0 : -1.0;
+  double pv = 0.0;
+  int64_t pi = -1;  // previous pick (none before round 0)
+  for (int r = 0; r < a.k; ++r) {
+    double bv = -INFINITY;
+    int64_t bi = a.n;
+    for (int64_t j = tid; j < a.n; j += 256) {
+      const double v = sgn * load_any(a.in, base + j, a.dtype);
+      const bool after = pi < 0 || v < pv || (v == pv && j > pi);
+      if (after && (v > bv || (v == bv && j < bi))) {
+        bv = v;
+        bi = j;
+      }
+    }
+    sv[tid] = bv;
+    si[tid] = bi;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+      if (tid < s) {
+        const double ov = sv[tid + s];
+        const int64_t oi = si[tid + s];
+        if (ov > sv[tid] || (ov == sv[tid] && oi < si[tid])) {
+          sv[tid] = ov;
+          si[tid] = oi;
+        }
+      }
+      __syncthreads();
+    }
+    pv = sv[0];
+    pi = si[0] < a.n ? si[0] : a.n - 1;  // a row shorter than k repeats its last pick
+    if (tid == 0) a.idx[row * a.k + r] = (uint32_t)pi;
+    __syncthreads();
+  }
+}

@@ -582,6 +582,37 @@ class GatherStep(Step):
         return [Launch("generic", "nk_gather", (grid, 1, 1), (256, 1, 1), a)]
 
 
+class TopkArgs(ctypes.Structure):
+    _fields_ = [("inp", ctypes.c_void_p), ("idx", ctypes.c_void_p), ("rows", ctypes.c_int64),
+                ("n", ctypes.c_int64), ("k", ctypes.c_int32), ("largest", ctypes.c_int32),
+                ("dtype", ctypes.c_int32), ("pad", ctypes.c_int32)]
+
+
+class TopkStep(Step):
+    """Indices of the k largest (or smallest) elements of each row along the
+    last axis, ordered by value, ties by index (nk_topk)."""
+
+    kind = "topk"
+
+    def __init__(self, node):
+        x = node.inputs[0]
+        super().__init__("topk", [x], [node.out])
+        self.node, self.x = node, x
+        self.n = x.shape[-1] if x.ndim else 1
+        self.rows = x.size // max(self.n, 1)
+
+    def launches(self, addr):
+        at = self.node.attrs
+        if self.rows == 0:
+            return []
+        if self.rows >= 2**31:
+            raise LaunchError("topk: too many rows")
+        a = TopkArgs(addr(self.x), addr(self.node.out), self.rows, self.n, int(at["k"]),
+                     1 if at["largest"] else 0, dtype_code(self.x.dtype), 0)
+        return [Launch("generic", "nk_topk", (self.rows, 1, 1), (256, 1, 1), a,
+                       bytes=self.rows * self.n * self.x.dtype.itemsize * int(at["k"]))]
+
+
 class CumsumStep(Step):
     kind = "cumsum"
 

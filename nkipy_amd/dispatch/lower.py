@@ -304,6 +304,8 @@ class Lowering:
             return steps + [G.GatherStep(n)]
         if op == "cumsum":
             return [G.CumsumStep(n)]
+        if op == "topk":
+            return [G.TopkStep(n)]
         if op == "concatenate":
             ax = n.attrs["dimension"]
             s = G.contiguous_strides(v.shape)

@@ -343,3 +343,30 @@ def decoder_oproj_residual(x, attn, w):
 def decoder_down_residual(z, act, w):
     """y = z + down(act), both rounded to bf16."""
     return bf16_round(np.asarray(z, np.float32) + bf16_round(linear_fp8(act, w["w_down"], w["w_down_scale"])))
+
+
+# ---------------------------------------------------------------------------
+# top-k -- nkipy/src/nkipy/core/ops/nn.py:22-60 (CPU: argpartition of -x,
+# then the k picks sorted best first; indices uint32).  Rows are assumed free
+# of ties (the reference leaves their order to argpartition / argsort).
+# ---------------------------------------------------------------------------
+
+
+def topk(x, k, axis=-1, is_ascend=False):
+    x = np.asarray(x)
+    keys = x if is_ascend else -x
+    part = np.argpartition(keys, k - 1, axis=axis)
+    idx = np.take(part, np.arange(k), axis=axis)
+    vals = np.take_along_axis(keys, idx, axis=axis)
+    order = np.argsort(vals, axis=axis)
+    idx = np.take_along_axis(idx, order, axis=axis)
+    return np.take_along_axis(x, idx, axis=axis), idx.astype(np.uint32)
+
+
+def greedy_sampling_bf16(h, norm_weight, lm_head, eps):
+    """examples/models/qwen3/kernels/sampling.py:113-148 on one device: final
+    RMSNorm (bf16 out), logits of the last position rounded to bf16 (fp32
+    accumulation), index of the largest logit.  (B, S, H) -> (B, 1) uint32."""
+    hn = rmsnorm_kernel(h, norm_weight, eps, round_out=bf16_round)
+    logits = bf16_round(np.asarray(hn[:, -1, :], np.float32) @ np.asarray(lm_head, np.float32))
+    return topk(logits, 1, axis=1)[1]

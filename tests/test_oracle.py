@@ -277,3 +277,29 @@ def test_noncausal_attention_vs_f64_loop():
     np.testing.assert_allclose(got, K.causal_attention_f64_loop(q, k, v, causal=False), rtol=1e-5, atol=1e-6)
     # the last query sees every key under both forms
     np.testing.assert_allclose(got[:, -1], K.causal_gqa_attention(q, k, v)[:, -1], rtol=1e-6)
+
+
+def test_topk_against_full_sort():
+    rng = np.random.default_rng(17)
+    x = rng.permutation(4 * 37).reshape(4, 37).astype(np.float32) - 60.0  # distinct values
+    for k in (1, 5, 37):
+        for asc in (False, True):
+            v, i = K.topk(x, k, axis=1, is_ascend=asc)
+            order = np.argsort(x if asc else -x, axis=1)[:, :k]
+            np.testing.assert_array_equal(i, order.astype(np.uint32))
+            np.testing.assert_array_equal(v, np.take_along_axis(x, order, 1))
+    # along axis 0 as well
+    v, i = K.topk(x, 2, axis=0)
+    np.testing.assert_array_equal(v, -np.sort(-x, axis=0)[:2])
+
+
+def test_topk_kernel_cpu_backend_matches_oracle():
+    from nkipy_amd.core import tensor_apis
+
+    rng = np.random.default_rng(18)
+    x = rng.permutation(3 * 50).reshape(3, 50).astype(np.float32)
+    for asc in (False, True):
+        v, i = tensor_apis.topk(x, 7, axis=1, is_ascend=asc)  # no trace: the NumPy implementation
+        rv, ri = K.topk(x, 7, axis=1, is_ascend=asc)
+        np.testing.assert_array_equal(i, ri)
+        np.testing.assert_array_equal(v, rv)
