@@ -317,3 +317,168 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
       *reinterpret_cast<uint2 *>(orow + t * 32 + gq * 8 + lhi * 4) = make_uint2(w0, w1);
     }
 }
+
+// ---------------------------------------------------------------------------
+// Decode attention: one query token per sequence against a KV cache,
+//   o[b, h] = softmax(q[b, h] . K[b, 0..pos, h / rep]^T * scale) V[b, 0..pos, h / rep]
+// with rep = Hq / Hkv query heads per KV head and pos read from device memory
+// (the keys after it are the ones the causal mask row of position pos adds
+// -1e5 to: they contribute nothing).  The cast points of the traced NumPy
+// code are kept by flags: the q.k product rounded to bf16, the scaled score
+// rounded to bf16, and softmax with bf16 results per operation (s - m,
+// exp, the fp32-accumulated sum, the quotient); the weighted sum of values
+// accumulates in fp32.
+//
+// One workgroup (4 waves) per (batch, KV head) serves its rep query heads,
+// so each K / V row is read from HBM once.  Scores of all keys stay in LDS
+// (rep x Smax fp32 <= 64 KiB); K tiles of 128 keys are staged with rows
+// padded to 272 bytes (conflict-free row reads), V tiles unpadded (read
+// along d).
+#define DQ_MAX 16       // query heads per KV head
+#define DKB 128         // keys per tile
+#define DK_ROW 272      // padded K row (bytes)
+#define DSC_MAX 16384   // rep * Smax scores held in LDS
+
+enum { DEC_RND_PROD = 1, DEC_RND_SCORE = 2, DEC_SOFTMAX_BF16 = 4, DEC_DIVIDE = 8 };
+
+struct DecodeAttnArgs {
+  const uint16_t *q;   // (B, Hq, 128): q_sb, q_sh
+  const uint16_t *k;   // cache (B, Smax, Hkv, 128): k_sb, k_ss, k_sh
+  const uint16_t *v;   // v_sb, v_ss, v_sh
+  uint16_t *o;         // (B, Hq, 128): o_sb, o_sh
+  const int32_t *pos;  // last attended position (one value for every sequence)
+  int64_t q_sb, q_sh, k_sb, k_ss, k_sh, v_sb, v_ss, v_sh, o_sb, o_sh;
+  int32_t B, Smax, Hq, Hkv;
+  float scale;  // multiplied in (divided by with DEC_DIVIDE)
+  int32_t flags;
+};
+
+__device__ __forceinline__ float bf16r(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+extern "C" __global__ __launch_bounds__(256) void nk_decode_attention_d128(DecodeAttnArgs a) {
+  __shared__ __attribute__((aligned(16))) float qs[DQ_MAX][AD];
+  __shared__ __attribute__((aligned(16))) uint8_t kt[DKB * DK_ROW];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[DKB * AD];
+  __shared__ float sc[DSC_MAX];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int rep = a.Hq / a.Hkv;
+  const int b = blockIdx.x / a.Hkv, g = blockIdx.x % a.Hkv;
+  int pos = *a.pos;
+  pos = pos < 0 ? 0 : (pos >= a.Smax ? a.Smax - 1 : pos);
+  const int L = pos + 1;  // attended keys
+  const int ntiles = (L + DKB - 1) / DKB;
+  const uint16_t *kb = a.k + (int64_t)b * a.k_sb + (int64_t)g * a.k_sh;
+  const uint16_t *vb = a.v + (int64_t)b * a.v_sb + (int64_t)g * a.v_sh;
+  const bool rnd = (a.flags & DEC_SOFTMAX_BF16) != 0;
+
+  // q of the rep heads as fp32
+  for (int i = tid; i < rep * AD; i += 256) {
+    const int qi = i / AD, d = i % AD;
+    qs[qi][d] = bf16_to_f32(a.q[(int64_t)b * a.q_sb + (int64_t)(g * rep + qi) * a.q_sh + d]);
+  }
+
+  // scores: thread -> key r of the tile, queries qi = half, half + 2, ...
+  const int r = tid & (DKB - 1), half = tid >> 7;
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();  // previous tile's reads done (and q staged)
+    for (int i = tid; i < DKB * 16; i += 256) {
+      const int row = i >> 4, c = i & 15;
+      const int key = t * DKB + row;
+      uint4 w = make_uint4(0, 0, 0, 0);
+      if (key < L) w = *reinterpret_cast<const uint4 *>(kb + (int64_t)key * a.k_ss + c * 8);
+      *reinterpret_cast<uint4 *>(kt + row * DK_ROW + c * 16) = w;
+    }
+    __syncthreads();
+    const int key = t * DKB + r;
+    if (key < L) {
+      float acc[DQ_MAX / 2];
+#pragma unroll
+      for (int j = 0; j < DQ_MAX / 2; ++j) acc[j] = 0.f;
+      for (int c = 0; c < 16; ++c) {
+        const uint4 w = *reinterpret_cast<const uint4 *>(kt + r * DK_ROW + c * 16);
+        float kf[8];
+        kf[0] = __uint_as_float(w.x << 16); kf[1] = __uint_as_float(w.x & 0xffff0000u);
+        kf[2] = __uint_as_float(w.y << 16); kf[3] = __uint_as_float(w.y & 0xffff0000u);
+        kf[4] = __uint_as_float(w.z << 16); kf[5] = __uint_as_float(w.z & 0xffff0000u);
+        kf[6] = __uint_as_float(w.w << 16); kf[7] = __uint_as_float(w.w & 0xffff0000u);
+#pragma unroll
+        for (int j = 0; j < DQ_MAX / 2; ++j) {
+          const int qi = half + 2 * j;
+          if (qi < rep) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[j] = fmaf(qs[qi][c * 8 + e], kf[e], acc[j]);
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < DQ_MAX / 2; ++j) {
+        const int qi = half + 2 * j;
+        if (qi < rep) {
+          float s = acc[j];
+          if (a.flags & DEC_RND_PROD) s = bf16r(s);
+          s = (a.flags & DEC_DIVIDE) ? s / a.scale : s * a.scale;
+          if (a.flags & DEC_RND_SCORE) s = bf16r(s);
+          sc[qi * a.Smax + key] = s;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // softmax per query head (wave w: heads w, w + 4, ...)
+  for (int qi = wave; qi < rep; qi += 4) {
+    float *row = sc + qi * a.Smax;
+    float m = -INFINITY;
+    for (int j = lane; j < L; j += 64) m = fmaxf(m, row[j]);
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    float sum = 0.f;
+    for (int j = lane; j < L; j += 64) {
+      float d = row[j] - m;
+      if (rnd) d = bf16r(d);
+      float e = expf(d);
+      if (rnd) e = bf16r(e);
+      row[j] = e;
+      sum += e;
+    }
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    if (rnd) sum = bf16r(sum);
+    for (int j = lane; j < L; j += 64) {
+      float p = row[j] / sum;
+      if (rnd) p = bf16r(p);
+      row[j] = p;
+    }
+  }
+
+  // o = P V: thread -> column d, queries qi = half, half + 2, ...
+  const int dcol = tid & (AD - 1);
+  float acc[DQ_MAX / 2];
+#pragma unroll
+  for (int j = 0; j < DQ_MAX / 2; ++j) acc[j] = 0.f;
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();
+    for (int i = tid; i < DKB * 16; i += 256) {
+      const int row = i >> 4, c = i & 15;
+      const int key = t * DKB + row;
+      uint4 w = make_uint4(0, 0, 0, 0);
+      if (key < L) w = *reinterpret_cast<const uint4 *>(vb + (int64_t)key * a.v_ss + c * 8);
+      *reinterpret_cast<uint4 *>(vt + row * AD + c * 8) = w;
+    }
+    __syncthreads();
+    const int n = min(DKB, L - t * DKB);
+    for (int rr = 0; rr < n; ++rr) {
+      const float vv = bf16_to_f32(vt[rr * AD + dcol]);
+#pragma unroll
+      for (int j = 0; j < DQ_MAX / 2; ++j) {
+        const int qi = half + 2 * j;
+        if (qi < rep) acc[j] = fmaf(sc[qi * a.Smax + t * DKB + rr], vv, acc[j]);
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < DQ_MAX / 2; ++j) {
+    const int qi = half + 2 * j;
+    if (qi < rep) a.o[(int64_t)b * a.o_sb + (int64_t)(g * rep + qi) * a.o_sh + dcol] = f32_to_bf16(acc[j]);
+  }
+}

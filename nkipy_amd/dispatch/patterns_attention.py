@@ -358,4 +358,193 @@ class AttentionPattern:
         return AttentionMatch(nodes, q, k, v, out, (B, S, Hq, Hkv, D, strides), scale, causal, o_str)
 
 
+# ---------------------------------------------------------------------------
+# decode attention: one query token against a KV cache
+# ---------------------------------------------------------------------------
+class DecodeAttentionMatch(Match):
+    name = "decode_attention"
+
+    def __init__(self, nodes, q: View, k: View, v: View, pos: Value, out: Value, dims, scale, flags, o_str):
+        ins = list(dict.fromkeys([q.base, k.base, v.base, pos]))
+        super().__init__(nodes, ins, [out])
+        self.q, self.k, self.v, self.pos, self.out = q, k, v, pos, out
+        self.dims, self.scale, self.flags, self.o_str = dims, scale, flags, o_str
+
+    def steps(self, plan):
+        q, k, v, out, pos = self.q, self.k, self.v, self.out, self.pos
+        B, Sk, Hq, Hkv, D, strides = self.dims
+
+        def make(addr):
+            return LA.decode_attention(addr(q.base) + 2 * q.offset, addr(k.base) + 2 * k.offset,
+                                       addr(v.base) + 2 * v.offset, addr(out), addr(pos), B, Sk, Hq, Hkv, D,
+                                       self.scale, dict(strides, o=self.o_str), self.flags)
+
+        desc = f"decode attention B={B} cache={Sk} Hq={Hq} Hkv={Hkv} D={D} flags={self.flags}"
+        return [LaunchStep("decode_attention", desc, self.inputs, self.outputs, make)]
+
+
+class DecodeAttentionPattern:
+    """The decode step of examples/models/qwen3/kernels/attention.py:100-140:
+    one query position, keys and values from the (just updated) cache with
+    ``np.repeat`` GQA, scores scaled and optionally cast to bf16, plus the
+    causal-mask row of the runtime position, softmax, weighted values::
+
+        s = (q @ k_t) / c  [.astype(bf16)]      q (B, H, 1, D)
+        s = s + mask[start_pos, :S]             mask = triu(<= -1e4, k=1)
+        o = softmax(s) @ v
+    """
+
+    def find(self, L):
+        for n in L.live:
+            if id(n) in L.covered or not _qk_dot(n) or n.out.shape[2:3] != (1,):
+                continue
+            m = self._match(L, n)
+            if m is not None and m.validate(L):
+                yield m
+
+    @staticmethod
+    def _mask_row(L, v: Value, Sk: int):
+        """mask[pos, :Sk] broadcast over (b, h) -> (pos value, nodes), with
+        the mask a causal constant and pos an int32 scalar tensor."""
+        nodes = []
+        while op_of(v) in ("broadcast_in_dim", "reshape"):
+            nodes.append(v.node)
+            v = v.node.inputs[0]
+        if op_of(v) == "slice":
+            at = v.node.attrs
+            if any(st != 0 for st in at["start_indices"]) or any(sd != 1 for sd in at["strides"]):
+                return None
+            nodes.append(v.node)
+            v = v.node.inputs[0]
+        if op_of(v) != "take" or v.node.attrs["axis"] != 0 or v.shape[-1] != Sk:
+            return None
+        tk = v.node
+        C, pos = tk.inputs
+        if pos.dtype != dt.int32 or pos.size != 1:
+            return None
+        cast = None
+        if op_of(C) == "convert" and op_of(C.node.inputs[0]) == "constant":
+            cast, C = C.node, C.node.inputs[0]  # a float constant cast to the score dtype
+        payload = _const_payload(C)
+        if payload is None or payload.ndim != 2 or payload.shape[0] != payload.shape[1] or payload.shape[1] < Sk:
+            return None
+        m = payload[:, :Sk]
+        lower = np.tril(np.ones(m.shape, bool))
+        if np.any(m[lower] != 0) or np.any(m[~lower] > MASK_LIMIT):
+            return None
+        nodes.append(tk)
+        chain = ([cast] if cast is not None else []) + [C.node]
+        own = {id(tk)}
+        for cn in chain:  # the cast and the constant, if only this mask uses them
+            if cn.out.id in L.result_ids or any(id(u) not in own for u in _users_of(L, cn.out)):
+                break
+            nodes.append(cn)
+            own.add(id(cn))
+        return pos, nodes
+
+    def _match(self, L, n2: Node):
+        p_val, v_op = n2.inputs
+        nodes = [n2]
+        if op_of(p_val) != "divide" or p_val.dtype not in (dt.bfloat16, dt.float32):
+            return None
+        st = SoftmaxPattern.structure(L, p_val.node)
+        if st is None:
+            return None
+        X, smx = st
+        nodes += smx
+        flags = LA.DEC_SOFTMAX_BF16 if p_val.dtype == dt.bfloat16 else 0
+        if op_of(X) != "add":
+            return None
+        Sk = X.shape[-1]
+        sc = mask = None
+        for a, b in (X.node.inputs, X.node.inputs[::-1]):
+            mk = self._mask_row(L, b, Sk)
+            if mk is not None:
+                sc, mask = a, mk
+                break
+        if sc is None:
+            return None
+        nodes.append(X.node)
+        pos, mnodes = mask
+        nodes += mnodes
+        # score chain: [convert bf16] <- (divide | multiply by a scalar) <- [convert f32] <- dot
+        if op_of(sc) == "convert" and sc.dtype == dt.bfloat16:
+            flags |= LA.DEC_RND_SCORE
+            nodes.append(sc.node)
+            sc = sc.node.inputs[0]
+        if op_of(sc) not in ("divide", "multiply") or sc.dtype != dt.float32:
+            return None
+        a, c = sc.node.inputs
+        if op_of(sc) == "multiply" and scalar_value(a)[0] is not None:
+            a, c = c, a
+        cv, cn = scalar_value(c)
+        if cv is None or not cv > 0:
+            return None
+        if op_of(sc) == "divide":
+            flags |= LA.DEC_DIVIDE
+        nodes += [sc.node] + cn
+        if op_of(a) == "convert" and a.dtype == dt.float32:
+            nodes.append(a.node)
+            a = a.node.inputs[0]
+        if not (op_of(a) == "dot" and _qk_dot(a.node)):
+            return None
+        d1 = a.node
+        if d1.out.dtype == dt.bfloat16:
+            flags |= LA.DEC_RND_PROD
+        elif d1.out.dtype != dt.float32:
+            return None
+        nodes.append(d1)
+        q = _bf16_view(d1.inputs[0])
+        k = _bf16_view(d1.inputs[1])
+        v = _bf16_view(v_op)
+        if q is None or k is None or v is None:
+            return None
+        B, Hq, one, D = q.shape
+        if one != 1 or k.shape != (B, Hq, D, Sk) or v.shape != (B, Hq, Sk, D) or n2.out.shape != (B, Hq, 1, D):
+            return None
+        qs = [q.simple(0), q.simple(1)]
+        kg, vg = k.grouped(1), v.grouped(1)
+        ks = [k.simple(0), k.simple(3)]
+        vs = [v.simple(0), v.simple(2)]
+        if None in qs + ks + vs or kg is None or vg is None:
+            return None
+        if q.simple(3) != 1 or k.simple(2) != 1 or v.simple(3) != 1:
+            return None
+        if kg[0] != vg[0] or kg[2] != vg[2] or kg[0] * kg[2] != Hq:
+            return None
+        Hkv = kg[0]
+        # output tail: transposes / casts / one reshape (as for prefill)
+        out, perm, reshaped = n2.out, [0, 1, 2, 3], False
+        while True:
+            us = _users_of(L, out)
+            if out.id in L.result_ids or len(us) != 1:
+                break
+            u = us[0]
+            if u.op == "transpose" and not reshaped:
+                perm = [perm[pp] for pp in u.attrs["permutation"]]
+            elif u.op in ("convert", "copy") and (u.out.dtype == out.dtype or (
+                    out.dtype == dt.float32 and u.out.dtype == dt.bfloat16)):
+                pass
+            elif u.op == "reshape" and not reshaped:
+                reshaped = True
+            else:
+                break
+            nodes.append(u)
+            out = u.out
+        if out.dtype != dt.bfloat16 or perm not in ([0, 1, 2, 3], [0, 2, 1, 3]):
+            return None
+        logical = [(B, Hq, 1, D)[pp] for pp in perm]
+        cs = _contiguous(logical)
+        ps = {ax: i for i, ax in enumerate(perm)}
+        o_str = (cs[ps[0]], cs[ps[1]])
+        strides = {"q": tuple(qs), "k": (ks[0], ks[1], kg[1]), "v": (vs[0], vs[1], vg[1])}
+        try:
+            LA.decode_attention(16, 16, 16, 16, 16, B, Sk, Hq, Hkv, D, cv, dict(strides, o=o_str), flags)
+        except LA.LaunchError:
+            return None
+        if any((vw.offset * 2) % 16 for vw in (k, v)):
+            return None
+        return DecodeAttentionMatch(nodes, q, k, v, pos, out, (B, Sk, Hq, Hkv, D, strides), cv, flags, o_str)
+
+
 ATTENTION_PATTERNS = [AttentionPattern(), RopePattern()]

@@ -61,13 +61,16 @@ def qwen3_attention_kernel(x, qkv_weight, q_norm_weight, k_norm_weight, norm_eps
     xk = rmsnorm_kernel(xk.reshape(B, S, n_kv_heads, head_dim), k_norm_weight, norm_eps)
     xv = xv.reshape(B, S, n_kv_heads, head_dim)
 
+    # trace-time constants are built in fp32 and cast by traced ops (a host
+    # astype to bf16 needs ml_dtypes, which this environment may lack)
     max_seq = cache_k.shape[1]
-    cos, sin = compute_cos_sin_cache(head_dim, max_seq, base=rope_base, dtype=x.dtype)
+    cos, sin = compute_cos_sin_cache(head_dim, max_seq, base=rope_base)
+    cos = tensor_apis.constant(cos).astype(x.dtype)
+    sin = tensor_apis.constant(sin).astype(x.dtype)
     if prefill:
         cos, sin = cos[0:S], sin[0:S]
     else:
-        cos = tensor_apis.constant(cos)[start_pos]
-        sin = tensor_apis.constant(sin)[start_pos]
+        cos, sin = cos[start_pos], sin[start_pos]
     xq, xk = apply_rotary_emb_kernel(xq, xk, cos, sin)
 
     if prefill:
@@ -84,7 +87,8 @@ def qwen3_attention_kernel(x, qkv_weight, q_norm_weight, k_norm_weight, norm_eps
     v = values.transpose(0, 2, 1, 3)
     scores = (q @ k.transpose(0, 1, 3, 2)) / np.float32(np.sqrt(head_dim))
     scores = scores.astype(x.dtype)
-    mask = tensor_apis.constant(np.triu(np.ones((max_seq, max_seq)) * MASK_VALUE, k=1).astype(scores.dtype))
+    mask = tensor_apis.constant(np.triu(np.ones((max_seq, max_seq)) * MASK_VALUE, k=1).astype(np.float32))
+    mask = mask.astype(scores.dtype)
     if prefill:
         scores = scores + np.expand_dims(mask[:S, :max_seq], axis=[0, 1])
     else:

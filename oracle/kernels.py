@@ -370,3 +370,45 @@ def greedy_sampling_bf16(h, norm_weight, lm_head, eps):
     hn = rmsnorm_kernel(h, norm_weight, eps, round_out=bf16_round)
     logits = bf16_round(np.asarray(hn[:, -1, :], np.float32) @ np.asarray(lm_head, np.float32))
     return topk(logits, 1, axis=1)[1]
+
+
+# ---------------------------------------------------------------------------
+# Decode attention -- examples/models/qwen3/kernels/attention.py:101-140 at
+# one decode position: the cache holds keys / values of positions 0..pos
+# (the mask row of position pos removes the rest), q @ k^T divided by
+# sqrt(d), softmax, weighted values.  The bf16 cast points of the traced
+# NumPy code are optional: the product rounded to bf16 (a bf16 matmul), the
+# scaled score rounded (``.astype(bf16)``), softmax evaluated in bf16 (each
+# of s - m, exp, the fp32-accumulated sum and the quotient rounded).
+# q (B, Hq, D), cache (B, Smax, Hkv, D) -> (B, Hq, D) fp32.
+# ---------------------------------------------------------------------------
+
+
+def decode_attention(q, cache_k, cache_v, pos, round_prod=False, round_score=False, softmax_bf16=False):
+    q = np.asarray(q, np.float32)
+    B, Hq, D = q.shape
+    Hkv = cache_k.shape[2]
+    rep = Hq // Hkv
+    r = bf16_round
+    n = int(pos) + 1
+    out = np.zeros((B, Hq, D), np.float32)
+    for b in range(B):
+        for h in range(Hq):
+            k = np.asarray(cache_k[b, :n, h // rep], np.float32)
+            v = np.asarray(cache_v[b, :n, h // rep], np.float32)
+            s = (k.astype(np.float64) @ q[b, h].astype(np.float64)).astype(np.float32)
+            if round_prod:
+                s = r(s)
+            s = s / np.float32(np.sqrt(D))
+            if round_score:
+                s = r(s)
+            d = s - s.max()
+            e = np.exp(r(d) if softmax_bf16 else d)
+            if softmax_bf16:
+                e = r(e)
+            tot = np.float32(e.sum(dtype=np.float32))
+            p = e / (r(tot) if softmax_bf16 else tot)
+            if softmax_bf16:
+                p = r(p)
+            out[b, h] = (p.astype(np.float64) @ v.astype(np.float64)).astype(np.float32)
+    return out

@@ -303,3 +303,25 @@ def test_topk_kernel_cpu_backend_matches_oracle():
         rv, ri = K.topk(x, 7, axis=1, is_ascend=asc)
         np.testing.assert_array_equal(i, ri)
         np.testing.assert_array_equal(v, rv)
+
+
+def test_decode_attention_is_a_row_of_causal_attention():
+    """Without bf16 cast points, decode at position p equals row p of causal
+    attention over the first p + 1 tokens (the cache prefix)."""
+    rng = np.random.default_rng(19)
+    B, S, Hq, Hkv, D = 2, 9, 4, 2, 16
+    q = rng.standard_normal((B, S, Hq, D)).astype(np.float32)
+    k = rng.standard_normal((B, S, Hkv, D)).astype(np.float32)
+    v = rng.standard_normal((B, S, Hkv, D)).astype(np.float32)
+    full = K.causal_gqa_attention(q, k, v)
+    cache_k = np.concatenate([k, rng.standard_normal((B, 7, Hkv, D)).astype(np.float32)], axis=1)
+    cache_v = np.concatenate([v, rng.standard_normal((B, 7, Hkv, D)).astype(np.float32)], axis=1)
+    for p in (0, 4, S - 1):
+        got = K.decode_attention(q[:, p], cache_k, cache_v, p)
+        np.testing.assert_allclose(got, full[:, p], rtol=1e-5, atol=1e-6)
+    # the bf16 cast points move the result by bf16 rounding only
+    qb, kb, vb = (N.bf16_round(a) for a in (q, cache_k, cache_v))
+    exact = K.decode_attention(qb[:, 5], kb, vb, 5)
+    cast = K.decode_attention(qb[:, 5], kb, vb, 5, True, True, True)
+    assert np.abs(cast - exact).max() <= 0.05 * np.abs(exact).max()
+    assert np.abs(cast - exact).max() > 0
