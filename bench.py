@@ -87,9 +87,8 @@ def sections():
                                  ("scan", "hbm", 4 * LA_B * LA_H * LA_T * LA_D * 2)]),
         5: ("decoder_layer_fp8", [
             ("attn_norm", "hbm", norm_bytes),
-            ("qkv_proj", "mfma", 2 * DEC_M * DEC_HID * (DEC_HQ + 2 * DEC_HKV) * DEC_D),
-            ("rope_q", "hbm", 2 * DEC_M * DEC_HQ * DEC_D * 2),
-            ("rope_k", "hbm", 2 * DEC_M * DEC_HKV * DEC_D * 2),
+            # the QKV projection's epilogue also rotates q and k (RoPE)
+            ("qkv_proj_rope", "mfma", 2 * DEC_M * DEC_HID * (DEC_HQ + 2 * DEC_HKV) * DEC_D),
             ("attention", "mfma", 4 * DEC_B * DEC_HQ * DEC_S * DEC_S * DEC_D // 2),
             ("o_proj_residual", "mfma", 2 * DEC_M * DEC_HID * DEC_HID),
             ("mlp_norm", "hbm", norm_bytes),
@@ -473,7 +472,7 @@ def bench_decoder(a, rt, mk):
             w["wo_scale"], dt.to_bf16(w["mlp_norm"]), f8(w["w_gate"]), w["w_gate_scale"], f8(w["w_up"]),
             w["w_up_scale"], f8(w["w_down"]), w["w_down_scale"]]
     dk = DeviceKernel.compile_and_load(llama_decoder_layer_fp8, *args, name="decoder_layer_fp8")
-    kinds = ["rmsnorm", "gemm", "rope", "rope", "attention", "gemm", "rmsnorm", "gemm_swiglu", "gemm"]
+    kinds = ["rmsnorm", "gemm_rope", "attention", "gemm", "rmsnorm", "gemm_swiglu", "gemm"]
     if dk.plan.kernel_kinds != kinds:
         raise RuntimeError(f"decoder layer did not lower to the fused kernels: {dk.plan.kernel_kinds}")
     names = [p.name for p in dk.graph.parameters]

@@ -70,6 +70,14 @@ struct GemmArgs {
   int32_t tiles_m, tiles_n;
   int32_t flags;
   int32_t group_m;     // tile rows per group of the tile walk; 0: GROUP_M
+  // rotary embedding of the q / k columns (the *_rope kernels only)
+  const float *rope_cos;  // fp32 [position][64], row stride rope_ts
+  const float *rope_sin;
+  void *rope_q;           // M x rope_nq bf16: rotated columns 0 .. rope_nq-1
+  void *rope_k;           // M x rope_nk bf16: rotated columns rope_nq ..
+  int64_t rope_ts;
+  int32_t rope_seq;       // row m sits at position m % rope_seq
+  int32_t rope_nq, rope_nk, rope_pad;
 };
 
 // ---------------------------------------------------------------------------
@@ -770,6 +778,10 @@ __device__ __forceinline__ int hswz8(int row) { return (row >> 3) & 1; }
 // tile (i', j), output row rbase + 16 i' + i and the 4 consecutive columns
 // cbase + 16 j + 4 g + 0..3 (SwiGLU: tiles j < 4 gate and j + 4 up of the
 // same output columns cbase + 16 j + ..).
+// Loads are issued ahead of the stores: the residual of tile column j + 1 is
+// fetched before column j is stored (the compiler may not move a load past a
+// store that can alias it, and C may be the residual buffer itself -- each
+// lane reads only the elements it writes, so the early reads are exact).
 template <bool SWIGLU, typename TC, int NI>
 __device__ __forceinline__ void gemm_epilogue16(const GemmArgs &a, const f32x4 (&acc)[NI][8], int64_t rbase,
                                                 int64_t cbase, int lane) {
@@ -785,48 +797,148 @@ __device__ __forceinline__ void gemm_epilogue16(const GemmArgs &a, const f32x4 (
     }
   };
   constexpr int NJ = SWIGLU ? 4 : 8;
+  // per-column factors of every tile column, fetched up front
+  float sc[NJ][4], su[NJ][4], bi[NJ][4];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int64_t col = cbase + 16 * j + 4 * g4;
-    float sc[4], su[4], bi[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const bool in = col + e < a.N;
-      sc[e] = ((a.flags & GEMM_SCALE) && in) ? a.scale0[col + e] : 1.f;
-      su[e] = (SWIGLU && (a.flags & GEMM_SCALE) && in) ? a.scale1[col + e] : 1.f;
-      bi[e] = (!SWIGLU && (a.flags & GEMM_BIAS) && in)
-                  ? bf16_to_f32(reinterpret_cast<const uint16_t *>(a.bias)[col + e]) : 0.f;
+      sc[j][e] = ((a.flags & GEMM_SCALE) && in) ? a.scale0[col + e] : 1.f;
+      su[j][e] = (SWIGLU && (a.flags & GEMM_SCALE) && in) ? a.scale1[col + e] : 1.f;
+      bi[j][e] = (!SWIGLU && (a.flags & GEMM_BIAS) && in)
+                     ? bf16_to_f32(reinterpret_cast<const uint16_t *>(a.bias)[col + e]) : 0.f;
     }
-    if (col >= a.N) continue;
+  }
+  if constexpr (SWIGLU) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int64_t row = rbase + 16 * i + l16;
-      if (row >= a.M) continue;
-      float v[4];
-      if constexpr (SWIGLU) {
+    for (int j = 0; j < NJ; ++j) {
+      const int64_t col = cbase + 16 * j + 4 * g4;
+      if (col >= a.N) continue;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int64_t row = rbase + 16 * i + l16;
+        if (row >= a.M) continue;
+        float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float g = acc[i][j][e] * sc[e];
-          const float u = acc[i][j + 4][e] * su[e];
+          const float g = acc[i][j][e] * sc[j][e];
+          const float u = acc[i][j + 4][e] * su[j][e];
           // silu(g) = g / (1 + exp(-g)) from the hardware 2^x and reciprocal
           const float ex = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
           v[e] = g * __builtin_amdgcn_rcpf(1.0f + ex) * u;
         }
-      } else {
-        float r4[4] = {0.f, 0.f, 0.f, 0.f};
-        if (a.flags & GEMM_RESID) {
-          if (vec && col + 3 < a.N) {
-            OutT<TC>::load4(a.resid, row * a.ldc + col, r4);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (col + e < a.N) r4[e] = OutT<TC>::load(a.resid, row * a.ldc + col + e);
-          }
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = epilogue(a.flags, acc[i][j][e] * sc[e], bi[e], r4[e]);
+        put4(row, col, v);
       }
-      put4(row, col, v);
+    }
+  } else {
+    const bool res = (a.flags & GEMM_RESID) != 0;
+    // residual of tile column j, rows i: 4 elements each
+    auto fetch = [&](int j, float (&r)[NI][4]) {
+      const int64_t col = cbase + 16 * j + 4 * g4;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int64_t row = rbase + 16 * i + l16;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[i][e] = 0.f;
+        if (!res || row >= a.M || col >= a.N) continue;
+        if (vec && col + 3 < a.N) {
+          OutT<TC>::load4(a.resid, row * a.ldc + col, r[i]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (col + e < a.N) r[i][e] = OutT<TC>::load(a.resid, row * a.ldc + col + e);
+        }
+      }
+    };
+    float rc[NI][4], rn[NI][4];
+    fetch(0, rc);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      if (j + 1 < NJ) fetch(j + 1, rn);
+      const int64_t col = cbase + 16 * j + 4 * g4;
+      if (col < a.N) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          const int64_t row = rbase + 16 * i + l16;
+          if (row >= a.M) continue;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = epilogue(a.flags, acc[i][j][e] * sc[j][e], bi[j][e], rc[i][e]);
+          put4(row, col, v);
+        }
+      }
+      if (j + 1 < NJ) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) rc[i][e] = rn[i][e];
+      }
+    }
+  }
+}
+
+// Epilogue of the rotary-embedding kernels: columns below rope_nq + rope_nk
+// are heads of 128 (q heads, then k heads), and a wave's 128 columns are one
+// head (cbase is a multiple of 128), so lane (g, i) holds frequency
+// 16 j + 4 g + e of both halves: x0 in tile j, x1 in tile j + 4.  Per element,
+// as the traced NumPy code evaluates it:
+//   x0, x1 = bf16(product * scale)                     (the projection's cast)
+//   out0 = bf16(x0 * cos - x1 * sin), out1 = bf16(x0 * sin + x1 * cos)
+// with every product and sum rounded to fp32 separately (no fused
+// multiply-add).  The rotated head goes to rope_q / rope_k; C keeps only the
+// remaining (value) columns.
+template <int NI>
+__device__ __forceinline__ void gemm_epilogue_rope(const GemmArgs &a, const f32x4 (&acc)[NI][8], int64_t rbase,
+                                                   int64_t cbase, int lane) {
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const bool isq = cbase < a.rope_nq;
+  uint16_t *dst = reinterpret_cast<uint16_t *>(isq ? a.rope_q : a.rope_k);
+  const int64_t ldd = isq ? a.rope_nq : a.rope_nk;
+  const int64_t c0 = isq ? cbase : cbase - a.rope_nq;
+  const bool scaled = (a.flags & GEMM_SCALE) != 0;
+  // table row offsets of the lane's rows (rows past M read row 0: in bounds, unused)
+  int64_t toff[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int64_t row = rbase + 16 * i + l16;
+    toff[i] = (row < a.M ? (int64_t)((int32_t)row % a.rope_seq) : 0) * a.rope_ts + 4 * g4;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int d = 16 * j + 4 * g4;
+    // one batch of loads per tile column: its scales and the 2 x NI table vectors
+    float s0[4], s1[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      s0[e] = scaled ? a.scale0[cbase + d + e] : 1.f;
+      s1[e] = scaled ? a.scale0[cbase + 64 + d + e] : 1.f;
+    }
+    float4 c[NI], s[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      c[i] = *reinterpret_cast<const float4 *>(a.rope_cos + toff[i] + 16 * j);
+      s[i] = *reinterpret_cast<const float4 *>(a.rope_sin + toff[i] + 16 * j);
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int64_t row = rbase + 16 * i + l16;
+      if (row >= a.M) continue;
+      const float cv[4] = {c[i].x, c[i].y, c[i].z, c[i].w}, sv[4] = {s[i].x, s[i].y, s[i].z, s[i].w};
+      float y0[4], y1[4];
+      {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x0 = bf16_to_f32(f32_to_bf16(acc[i][j][e] * s0[e]));
+          const float x1 = bf16_to_f32(f32_to_bf16(acc[i][j + 4][e] * s1[e]));
+          y0[e] = x0 * cv[e] - x1 * sv[e];
+          y1[e] = x0 * sv[e] + x1 * cv[e];
+        }
+      }
+      OutT<bf16>::store4(dst, row * ldd + c0 + d, y0);
+      OutT<bf16>::store4(dst, row * ldd + c0 + 64 + d, y1);
     }
   }
 }
@@ -853,8 +965,9 @@ __device__ __forceinline__ void dma16_asm(i32x4_t r, uint32_t lds, uint32_t off)
                :: "v"(off), "s"(r), "s"(m) : "memory", "m0");
 }
 
-template <bool NT, bool FP8, bool SWIGLU, typename TC>
+template <bool NT, bool FP8, bool SWIGLU, typename TC, bool ROPE = false>
 __device__ __forceinline__ void gemm_pp_body(const GemmArgs &a) {
+  static_assert(!ROPE || (!SWIGLU && sizeof(TC) == 2), "the rotary epilogue writes bf16 projections");
   static_assert(NT || !FP8, "fp8 NN weights use the 4-wave kernel");
   constexpr int BMODE = (NT && FP8) ? B_T8 : NT ? B_T16 : B_NN16;
   constexpr int HB = BMODE == B_T8 ? 8192 : 16384;  // B bytes per half-tile stage
@@ -1098,6 +1211,12 @@ __device__ __forceinline__ void gemm_pp_body(const GemmArgs &a) {
   else
     run(Int<1>{});
   wait_vmem();
+  if constexpr (ROPE) {
+    if (n0 + bw0 < (int64_t)a.rope_nq + a.rope_nk) {
+      gemm_epilogue_rope<4>(a, acc, m0 + arow0, n0 + bw0, lane);
+      return;
+    }
+  }
   gemm_epilogue16<SWIGLU, TC, 4>(a, acc, m0 + arow0, n0 + bw0, lane);
 }
 
@@ -1131,3 +1250,13 @@ NK_GEMM_PP(true, false, true, bf16, nk_gemm8_swiglu_nt_bf16_bf16)
 NK_GEMM_PP(true, true, false, bf16, nk_gemm8_nt_e4m3_bf16)
 NK_GEMM_PP(true, true, false, float, nk_gemm8_nt_e4m3_f32)
 NK_GEMM_PP(true, true, true, bf16, nk_gemm8_swiglu_nt_e4m3_bf16)
+
+// fused QKV projection with the rotary embedding of q and k
+#define NK_GEMM_ROPE(NT, FP8, name)                                                      \
+  extern "C" __global__ __launch_bounds__(512, 1) void name(GemmArgs a) {                \
+    gemm_pp_body<NT, FP8, false, bf16, true>(a);                                         \
+  }
+
+NK_GEMM_ROPE(false, false, nk_gemm8_nn_bf16_bf16_rope)
+NK_GEMM_ROPE(true, false, nk_gemm8_nt_bf16_bf16_rope)
+NK_GEMM_ROPE(true, true, nk_gemm8_nt_e4m3_bf16_rope)

@@ -224,7 +224,25 @@ class GemmArgs(ctypes.Structure):
         ("lda", ctypes.c_int64), ("ldb", ctypes.c_int64), ("ldc", ctypes.c_int64),
         ("tiles_m", ctypes.c_int32), ("tiles_n", ctypes.c_int32),
         ("flags", ctypes.c_int32), ("group_m", ctypes.c_int32),
+        ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p),
+        ("rope_q", ctypes.c_void_p), ("rope_k", ctypes.c_void_p),
+        ("rope_ts", ctypes.c_int64), ("rope_seq", ctypes.c_int32),
+        ("rope_nq", ctypes.c_int32), ("rope_nk", ctypes.c_int32), ("rope_pad", ctypes.c_int32),
     ]
+
+
+class GemmRope:
+    """Rotary embedding folded into a QKV projection's epilogue: columns
+    0 .. nq-1 (q heads) and nq .. nq+nk-1 (k heads) of the product, heads of
+    128, are rotated by fp32 tables (position, 64) with row stride
+    ``table_stride`` (row m at position m % seq) and written to q_ptr (M x nq)
+    and k_ptr (M x nk), bf16; C receives only the columns after them."""
+
+    HEAD_DIM = 128
+
+    def __init__(self, cos_ptr, sin_ptr, q_ptr, k_ptr, table_stride, seq, nq, nk):
+        self.cos_ptr, self.sin_ptr, self.q_ptr, self.k_ptr = cos_ptr, sin_ptr, q_ptr, k_ptr
+        self.table_stride, self.seq, self.nq, self.nk = int(table_stride), int(seq), int(nq), int(nk)
 
 
 GEMM_BIAS = 1
@@ -241,7 +259,8 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
          b_dtype, c_dtype, lda: int = None, ldb: int = None, ldc: int = None,
          bias_ptr: int = 0, scale_ptr: int = 0, resid_ptr: int = 0,
          up_ptr: int = 0, up_scale_ptr: int = 0, pingpong: bool = None,
-         round_before_bias: bool = False, round_before_resid: bool = False) -> Launch:
+         round_before_bias: bool = False, round_before_resid: bool = False,
+         rope: GemmRope = None) -> Launch:
     """C[M, N] = A[M, K] @ B (+ epilogue) on bf16 MFMA, fp32 accumulation.
 
     ``layout`` "nn": B is K x N row-major (ldb >= N); "nt": B is N x K
@@ -254,7 +273,9 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
     bf16 before that add (the cast points of ``(x @ w).astype(bf16) + r``).
     ``pingpong`` selects the 8-wave kernel (two waves per SIMD alternating
     between MFMAs and fragment loads; the default where it exists, i.e. for
-    every layout except fp8 NN weights) or the 4-wave kernel.
+    every layout except fp8 NN weights) or the 4-wave kernel.  ``rope``
+    (:class:`GemmRope`) selects the 8-wave kernel whose epilogue applies the
+    rotary embedding to the q / k columns.
     """
     if layout not in ("nn", "nt"):
         raise LaunchError(f"unknown GEMM layout {layout}")
@@ -309,6 +330,24 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
     args = GemmArgs(a_ptr, b_ptr, up_ptr or None, c_ptr, bias_ptr or None, scale_ptr or None,
                     up_scale_ptr or None, resid_ptr or None, M, N, K, lda, ldb, ldc,
                     tiles_m, tiles_n, flags, 0)
+    if rope is not None:
+        hd = GemmRope.HEAD_DIM
+        if swiglu or bias_ptr or resid_ptr or c_dtype != dt.bfloat16 or pingpong is False:
+            raise LaunchError("the rotary epilogue is a plain bf16 projection on the 8-wave kernel")
+        if rope.nq % hd or rope.nk % hd or rope.nq + rope.nk <= 0 or rope.nq + rope.nk > N:
+            raise LaunchError(f"rotated columns must be whole heads of {hd} within N, got "
+                              f"{rope.nq} + {rope.nk} of {N}")
+        if rope.seq <= 0 or M % rope.seq:
+            raise LaunchError(f"rows ({M}) must be whole sequences of {rope.seq} positions")
+        if rope.table_stride % 4 or rope.table_stride < hd // 2:
+            raise LaunchError("rope tables need a row stride that is a multiple of 4 and covers 64")
+        if any(p % 16 for p in (rope.cos_ptr, rope.sin_ptr)) or any(
+                p % 8 for p in (rope.q_ptr, rope.k_ptr)) or not (rope.q_ptr and rope.k_ptr):
+            raise LaunchError("rope tables must be 16-byte and outputs 8-byte aligned")
+        args.rope_cos, args.rope_sin = rope.cos_ptr, rope.sin_ptr
+        args.rope_q, args.rope_k = rope.q_ptr, rope.k_ptr
+        args.rope_ts, args.rope_seq = rope.table_stride, rope.seq
+        args.rope_nq, args.rope_nk = rope.nq, rope.nk
     btag = "e4m3" if fp8 else "bf16"
     ctag = "bf16" if c_dtype == dt.bfloat16 else "f32"
     has_pp = not (fp8 and layout == "nn")
@@ -320,7 +359,7 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
     if swiglu:
         symbol = f"{prefix}_swiglu_{layout}_{btag}_bf16"
     else:
-        symbol = f"{prefix}_{layout}_{btag}_{ctag}"
+        symbol = f"{prefix}_{layout}_{btag}_{ctag}" + ("_rope" if rope is not None else "")
     n_mm = 2 if swiglu else 1
     nbytes = M * K * 2 + n_mm * N * K * b_dtype.itemsize + M * N * c_dtype.itemsize
     return Launch("gemm", symbol, (tiles_m * tiles_n, 1, 1), (512 if pingpong else 256, 1, 1), args,

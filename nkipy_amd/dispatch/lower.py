@@ -53,6 +53,7 @@ class Lowering:
         self.matches = []
         self.covered: Dict[int, object] = {}  # id(node) -> match
         self.dot_contig: Set[int] = set()  # dots that read contiguous operands
+        self.match_alias: Dict[int, Value] = {}  # value inside a match -> equal output
 
     # ------------------------------------------------------------------
     def n_users(self, v: Value) -> int:
@@ -81,6 +82,13 @@ class Lowering:
                 self.matches.append(m)
                 for nid in m.nodes:
                     self.covered[nid] = m
+        self.match_alias = self._match_aliases()
+        for pat in self.patterns:
+            # merges of claimed matches (e.g. RoPE into its QKV projection)
+            refine = getattr(pat, "refine", None)
+            if refine is not None:
+                refine(self)
+        self.match_alias = self._match_aliases()
         # 2. materialisation
         for r in self.g.results:
             self.need(r)
@@ -111,6 +119,26 @@ class Lowering:
         self._settle_programs()
         # 3. storage and 4. steps
         return self._build_plan()
+
+    def _match_aliases(self) -> Dict[int, Value]:
+        """Values inside a match that equal one of its outputs bit for bit
+        (the output is a same-dtype copy / convert of them, e.g. a no-op
+        ``astype`` the GEMM epilogue absorbed).  Views look through such
+        copies, so another match may read the inner value; it shares the
+        output's storage, which the match writes."""
+        alias: Dict[int, Value] = {}
+        for m in self.matches:
+            outs = {v.id for v in m.outputs}
+            for o in m.outputs:
+                cur = o
+                while (cur.node is not None and id(cur.node) in m.nodes
+                       and cur.node.op in ("copy", "convert") and cur.node.inputs[0].dtype == cur.dtype):
+                    src = cur.node.inputs[0]
+                    if src.id in outs or src.node is None or id(src.node) not in m.nodes:
+                        break
+                    alias[src.id] = o
+                    cur = src
+        return alias
 
     def _decide(self, n: Node):
         op = n.op
@@ -205,7 +233,7 @@ class Lowering:
 
         for n in self.live:
             v = n.out
-            if v.id in self.mat and v.id not in slots:
+            if v.id in self.mat and v.id not in slots and v.id not in self.match_alias:
                 if n.op == "constant":
                     payload = n.attrs["value"]
                     idx = plan.add_buffer(v.nbytes, "const", f"const{v.id}", payload)
@@ -214,6 +242,9 @@ class Lowering:
                 else:
                     idx = plan.add_buffer(v.nbytes, "temp", f"t{v.id}")
                 slots[v.id] = Slot(idx)
+        for vid, o in self.match_alias.items():
+            if vid in self.mat:
+                slots[vid] = slots[o.id]
         for n in self.live:
             v = n.out
             if v.id in self.alias_reshape and v.id not in slots:

@@ -479,13 +479,16 @@ def default_patterns():
 
 
 def _build_default_patterns():
-    from nkipy_amd.dispatch.patterns_attention import AttentionPattern, DecodeAttentionPattern, RopePattern
+    from nkipy_amd.dispatch.patterns_attention import (
+        AttentionPattern, DecodeAttentionPattern, QkvRopeFusion, RopePattern,
+    )
     from nkipy_amd.dispatch.patterns_gemm import GemmPattern, SwigluPattern
     from nkipy_amd.dispatch.patterns_linattn import LinearAttentionPattern
 
     # larger structures first: they contain matmuls / softmaxes that smaller
     # patterns would claim; GEMMs before RMSNorm so that a residual add
-    # after a projection goes into the GEMM epilogue
+    # after a projection goes into the GEMM epilogue; the RoPE of q / k then
+    # folds into its QKV projection
     return [LinearAttentionPattern(), DecodeAttentionPattern(), AttentionPattern(), RopePattern(), SwigluPattern(),
-            GemmPattern(), SoftmaxPattern(), RmsNormPattern()]
+            GemmPattern(), SoftmaxPattern(), RmsNormPattern(), QkvRopeFusion()]
 

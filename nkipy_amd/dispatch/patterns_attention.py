@@ -37,7 +37,7 @@ from nkipy_amd.dispatch import launchers as LA
 from nkipy_amd.dispatch.patterns import (
     LaunchStep, Match, SoftmaxPattern, _users_of, op_of, scalar_value,
 )
-from nkipy_amd.dispatch.views import View, resolve
+from nkipy_amd.dispatch.views import View, _is_view_node, resolve
 
 MASK_LIMIT = -1.0e4
 
@@ -191,6 +191,150 @@ class RopePattern:
             if vw.base is not c0.base and vw.base is not s0.base:
                 nodes += _owned(L, vw, inside)
         return RopeMatch(nodes, x0, x_half, c0, s0, roles, out)
+
+
+# ---------------------------------------------------------------------------
+# RoPE folded into the QKV projection
+# ---------------------------------------------------------------------------
+class QkvRopeMatch(Match):
+    """A bf16 QKV projection whose q and k heads (128 wide, columns 0 ..
+    nq + nk - 1) feed only the two RoPE matches: one GEMM launch rotates them
+    in its epilogue (csrc/kernels/gemm.hip, ``gemm_epilogue_rope``) and writes
+    the RoPE outputs directly; the projection value keeps its remaining (v)
+    columns.  Emitted where the GEMM was."""
+
+    name = "gemm_rope"
+
+    def __init__(self, gm, rq: RopeMatch, rk: RopeMatch, last: Node):
+        ins = list(dict.fromkeys(list(gm.inputs) + [rq.cos.base, rq.sin.base]))
+        super().__init__(gm.node_list + rq.node_list + rk.node_list, ins, [gm.out, rq.out, rk.out])
+        self.gm, self.rq, self.rk = gm, rq, rk
+        self.last = last
+
+    def steps(self, plan):
+        gm, rq, rk = self.gm, self.rq, self.rk
+        x, w, out = gm.x, gm.w, gm.out
+        K = x.shape[-1]
+        M = x.size // K
+        N = out.shape[-1]
+        ldb = w.value.shape[1]
+        (_, S, Hq), _, _, t_ss = rq.roles
+        Hk = rk.roles[0][2]
+        hd = LA.GemmRope.HEAD_DIM
+        cos, sin = rq.cos, rq.sin
+
+        def make(addr):
+            rope = LA.GemmRope(addr(cos.base) + 4 * cos.offset, addr(sin.base) + 4 * sin.offset,
+                               addr(rq.out), addr(rk.out), t_ss, S, Hq * hd, Hk * hd)
+            return LA.gemm(addr(x), addr(w.value), addr(out), M, N, K, layout=w.layout,
+                           b_dtype=w.value.dtype, c_dtype=out.dtype, ldb=ldb,
+                           scale_ptr=addr(w.scale) if w.scale is not None else 0, rope=rope)
+
+        desc = (f"gemm {w.layout} M={M} N={N} K={K} {dt.name(w.value.dtype)} -> bf16 "
+                f"+rope q {Hq}x{hd} k {Hk}x{hd}")
+        return [LaunchStep("gemm_rope", desc, self.inputs, self.outputs, make)]
+
+
+def _first_column(vw: View, n_cols: int) -> int:
+    """Smallest column of a row-major (.., n_cols) base that ``vw`` reads
+    (0 when its columns may wrap into the next row)."""
+    span = sum((n - 1) * s for d in vw.dims for n, s in d if n > 1 and s % n_cols)
+    c = vw.offset % n_cols
+    return c if c + span < n_cols else 0
+
+
+class QkvRopeFusion:
+    """Merges a QKV :class:`GemmMatch` with the RoPE matches of its q and k
+    heads (examples/models/qwen3/kernels/attention.py:44-66, tests/kernels/
+    llama_decoder_dynamo.py:150-178: split of the fused projection into
+    heads, then the split-half rotation).  Runs after every pattern has
+    claimed its nodes; finds nothing on its own."""
+
+    def find(self, L):
+        return iter(())
+
+    def refine(self, L):
+        from nkipy_amd.dispatch.patterns_gemm import GemmMatch
+
+        ropes = {}
+        for m in L.matches:
+            if isinstance(m, RopeMatch):
+                base = L.match_alias.get(m.x.base.id, m.x.base)
+                ropes.setdefault(base.id, []).append(m)
+        for gm in [m for m in L.matches if isinstance(m, GemmMatch)]:
+            rs = ropes.get(gm.out.id, [])
+            if len(rs) != 2:
+                continue
+            rq, rk = sorted(rs, key=lambda r: r.x.offset)
+            fused = self._fuse(L, gm, rq, rk)
+            if fused is None:
+                continue
+            for m in (gm, rq, rk):
+                L.matches.remove(m)
+            L.matches.append(fused)
+            for nid in fused.nodes:
+                L.covered[nid] = fused
+
+    @staticmethod
+    def _fuse(L, gm, rq, rk) -> Optional[QkvRopeMatch]:
+        hd = LA.GemmRope.HEAD_DIM
+        out, x, w = gm.out, gm.x, gm.w
+        if gm.up is not None or gm.bias is not None or gm.resid is not None or out.dtype != dt.bfloat16:
+            return None
+        if w.value.dtype == dt.float8_e4m3fn and w.layout == "nn":
+            return None  # no 8-wave kernel
+        if out.id in L.result_ids:
+            return None
+        K = x.shape[-1]
+        M, N = x.size // K, out.shape[-1]
+        col0 = 0
+        for r in (rq, rk):
+            (Bs, S, H), xs, os_, _ = r.roles
+            if r.out.shape[-1] != hd or r.x_half != hd // 2 or Bs * S != M:
+                return None
+            if xs[1] != N or (H > 1 and xs[2] != hd) or (Bs > 1 and xs[0] != S * N):
+                return None
+            if tuple(os_) != (S * H * hd, H * hd, hd) or r.x.offset != col0:
+                return None
+            col0 += H * hd
+        if col0 > N or rq.roles[0][1] != rk.roles[0][1] or rq.roles[3] != rk.roles[3]:
+            return None
+        # RopePattern fixed each table's layout (position stride roles[3],
+        # frequency contiguous); the views differ only in broadcast axes
+        for a, b in ((rq.cos, rk.cos), (rq.sin, rk.sin)):
+            if a.offset != b.offset:
+                return None
+            if a.base is not b.base:  # each rotation traced its own copy of the table
+                pa, pb = _const_payload(a.base), _const_payload(b.base)
+                if pa is None or pb is None or not np.array_equal(pa, pb):
+                    return None
+            base = a.base
+            if not (base.is_parameter or (base.node is not None and base.node.op == "constant")):
+                return None  # the tables must exist where the GEMM runs
+        # nothing but the two rotations may read the q / k columns
+        allowed = (id(rq), id(rk))
+        work, seen = [out], {out.id}
+        while work:
+            v = work.pop()
+            for u in L.users.get(v.id, ()):
+                m = L.covered.get(id(u))
+                if m is not None and id(m) in allowed:
+                    continue
+                if m is None and _is_view_node(u, True):
+                    if u.out.id in L.result_ids:  # a result copied out of these columns
+                        vw = resolve(u.out)
+                        if L.match_alias.get(vw.base.id, vw.base) is not out or _first_column(vw, N) < col0:
+                            return None
+                    if u.out.id not in seen:
+                        seen.add(u.out.id)
+                        work.append(u.out)
+                    continue
+                vw = resolve(v)
+                if L.match_alias.get(vw.base.id, vw.base) is not out or _first_column(vw, N) < col0:
+                    return None
+        order = {id(n): i for i, n in enumerate(L.live)}
+        return QkvRopeMatch(gm, rq, rk, gm.last if gm.last is not None else
+                            max(gm.node_list, key=lambda n: order[id(n)]))
 
 
 # ---------------------------------------------------------------------------

@@ -22,7 +22,7 @@ from oracle import numerics as N
 
 pytestmark = pytest.mark.gpu
 
-DECODER_KINDS = ["rmsnorm", "gemm", "rope", "rope", "attention", "gemm", "rmsnorm", "gemm_swiglu", "gemm"]
+DECODER_KINDS = ["rmsnorm", "gemm_rope", "attention", "gemm", "rmsnorm", "gemm_swiglu", "gemm"]
 
 
 def _close(got, ref, tol=2e-2, axis=None, rounded=None):

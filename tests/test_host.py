@@ -170,7 +170,9 @@ def _fp8(shape):
 
 
 def _kinds(fn, *args, **kw):
-    return lower(NKIPyKernel.trace(fn).specialize(*args, **kw)).kernel_kinds
+    plan = lower(NKIPyKernel.trace(fn).specialize(*args, **kw))
+    _assert_temps_written_before_read(plan)
+    return plan.kernel_kinds
 
 
 def test_lowering_softmax_and_rmsnorm():
@@ -207,7 +209,72 @@ def test_lowering_decoder_layer_fp8():
             _fp8((hid, hid)), one(hid), _bf16((hid,)), _fp8((F, hid)), one(F), _fp8((F, hid)), one(F),
             _fp8((hid, F)), one(hid)]
     assert _kinds(llama_decoder_layer_fp8, *args) == [
-        "rmsnorm", "gemm", "rope", "rope", "attention", "gemm", "rmsnorm", "gemm_swiglu", "gemm"]
+        "rmsnorm", "gemm_rope", "attention", "gemm", "rmsnorm", "gemm_swiglu", "gemm"]
+
+
+def _assert_temps_written_before_read(plan):
+    """Every temporary a step reads is written by an earlier step."""
+    written = set()
+    for st in plan.steps:
+        for v in st.inputs:
+            b = plan.slot(v).buffer
+            if plan.buffers[b].kind == "temp":
+                assert b in written, f"step {st.desc} reads temporary {b} ({v!r}) before any step writes it"
+        written.update(plan.slot(v).buffer for v in st.outputs)
+
+
+def test_lowering_value_inside_a_match_read_through_a_view():
+    """``(h @ w).astype(bf16)`` with bf16 operands: the GEMM absorbs the
+    no-op cast, and the RoPE views look through it to the product itself,
+    which must then share the GEMM output's storage."""
+    from nkipy_amd.dispatch.patterns import default_patterns
+    from nkipy_amd.dispatch.patterns_attention import QkvRopeFusion
+    from nkipy_amd.kernels.decoder import rope_kernel, rope_tables
+
+    B, S, H, D, hid = 1, 64, 2, 128, 128
+    cos, sin = rope_tables(D, S, 1e4)
+
+    def fn(h, w):
+        q = np.matmul(h, w).astype(h.dtype)
+        return rope_kernel(q.reshape(B, S, H, D), cos, sin).astype(h.dtype)
+
+    g = NKIPyKernel.trace(fn).specialize(_bf16((B, S, hid)), _bf16((hid, H * D)))
+    plain = lower(g, [p for p in default_patterns() if not isinstance(p, QkvRopeFusion)])
+    assert plain.kernel_kinds == ["gemm", "rope"]
+    _assert_temps_written_before_read(plain)
+
+
+def test_lowering_qkv_rope_fusion_only_when_qk_columns_are_private():
+    """RoPE folds into the QKV projection only when nothing else reads the
+    q / k columns the fused epilogue leaves unwritten."""
+    from nkipy_amd.kernels.decoder import rope_kernel, rope_tables
+
+    B, S, Hq, Hkv, D, hid = 2, 128, 4, 2, 128, 256
+    cos, sin = rope_tables(D, S, 1e4)
+    x, w = _bf16((B, S, hid)), _bf16((hid, (Hq + 2 * Hkv) * D))
+
+    def qkv_rope(extra):
+        def fn(h, w):
+            qkv = np.matmul(h, w).astype(h.dtype)
+            q, k, v = np.split(qkv, [Hq * D, (Hq + Hkv) * D], axis=-1)
+            qr = rope_kernel(q.reshape(B, S, Hq, D), cos, sin).astype(h.dtype)
+            kr = rope_kernel(k.reshape(B, S, Hkv, D), cos, sin).astype(h.dtype)
+            outs = [qr, kr, v.reshape(B, S, Hkv, D)]
+            if extra == "raw_k":
+                outs.append(k * 2.0)
+            elif extra == "qkv":
+                outs.append(qkv)
+            elif extra == "v_sum":
+                outs.append(np.sum(v.astype(np.float32), axis=-1))
+            return tuple(outs)
+        return fn
+
+    assert _kinds(qkv_rope(None), x, w)[0] == "gemm_rope"
+    _assert_temps_written_before_read(lower(NKIPyKernel.trace(qkv_rope(None)).specialize(x, w)))
+    assert _kinds(qkv_rope("v_sum"), x, w)[0] == "gemm_rope"   # v columns only
+    for extra in ("raw_k", "qkv"):
+        kinds = _kinds(qkv_rope(extra), x, w)
+        assert "gemm_rope" not in kinds and kinds.count("rope") == 2, (extra, kinds)
 
 
 def test_lowering_attention_variants_and_non_matches():
