@@ -101,8 +101,13 @@ take_along_axis = Op("take_along_axis")
 def _take_along_axis_hip(arr, indices, axis):
     c = ctx()
     v = val(arr)
-    ax = norm_axis(axis, v.ndim)[0]
     iv = _index_value(c, indices)
+    if axis is None:  # NumPy: along the flattened array, 1-D indices
+        if iv.ndim != 1:
+            raise ValueError("with axis=None the indices must be 1-D")
+        v = reshape(c, v, (v.size,))
+        axis = 0
+    ax = norm_axis(axis, v.ndim)[0]
     if iv.ndim != v.ndim:
         raise ValueError("indices and arr must have the same number of dimensions")
     # NumPy broadcasts the non-axis dimensions of indices against arr
@@ -121,10 +126,17 @@ put_along_axis = Op("put_along_axis")
 def _put_along_axis_hip(arr, indices, values, axis):
     c = ctx()
     v = val(arr)
-    ax = norm_axis(axis, v.ndim)[0]
     iv = _index_value(c, indices)
+    shape = v.shape
+    if axis is None:  # NumPy: into the flattened array, 1-D indices
+        if iv.ndim != 1:
+            raise ValueError("with axis=None the indices must be 1-D")
+        v = reshape(c, v, (v.size,))
+        axis = 0
+    ax = norm_axis(axis, v.ndim)[0]
     vals = convert(c, broadcast_to(c, val(values, v.dtype), iv.shape), v.dtype)
-    return wrap(c.build_op("put_along_axis", [v, iv, vals], v.shape, v.dtype, {"axis": ax}))
+    out = c.build_op("put_along_axis", [v, iv, vals], v.shape, v.dtype, {"axis": ax})
+    return wrap(reshape(c, out, shape) if out.shape != shape else out)
 
 
 dynamic_update_slice = Op("dynamic_update_slice")

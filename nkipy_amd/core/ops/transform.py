@@ -269,15 +269,47 @@ def _tile_hip(x, reps):
 pad = Op("pad")
 
 
+def _edge_pad(c, v, low, high):
+    """np.pad(mode="edge"): per axis, the first / last slice broadcast over
+    the padding, concatenated around the operand."""
+    for ax in range(v.ndim):
+        lo, hi = low[ax], high[ax]
+        if lo == 0 and hi == 0:
+            continue
+        n = v.shape[ax]
+
+        def edge(i, count, v=v, ax=ax):
+            start = [0] * v.ndim
+            limit = list(v.shape)
+            start[ax], limit[ax] = i, i + 1
+            one = tuple(b - a for a, b in zip(start, limit))
+            sl = c.build_op("slice", [v], one, v.dtype, {"start_indices": tuple(start),
+                                                         "limit_indices": tuple(limit),
+                                                         "strides": (1,) * v.ndim})
+            tgt = list(v.shape)
+            tgt[ax] = count
+            return _bcast(c, sl, tuple(tgt))
+
+        parts = ([edge(0, lo)] if lo else []) + [v] + ([edge(n - 1, hi)] if hi else [])
+        shape = list(v.shape)
+        shape[ax] = n + lo + hi
+        v = c.build_op("concatenate", parts, tuple(shape), v.dtype, {"dimension": ax})
+    return v
+
+
 @pad.impl("hip")
 def _pad_hip(x, pad_width, mode="constant", constant_values=0, **kw):
-    if mode != "constant":
+    if mode not in ("constant", "edge"):
         raise NotImplementedError(f"pad mode '{mode}' is not supported")
     c = ctx()
     v = val(x)
     pw = np.broadcast_to(np.asarray(pad_width, dtype=np.int64), (v.ndim, 2))
     low = tuple(int(a) for a in pw[:, 0])
     high = tuple(int(b) for b in pw[:, 1])
+    if mode == "edge":
+        if v.size == 0:
+            raise ValueError("edge padding of an empty array")
+        return wrap(_edge_pad(c, v, low, high))
     shape = tuple(s + a + b for s, a, b in zip(v.shape, low, high))
     pv = c.constant(constant_values, v.dtype)
     return wrap(c.build_op("pad", [v, pv], shape, v.dtype,

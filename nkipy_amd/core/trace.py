@@ -67,6 +67,19 @@ def is_array_arg(a) -> bool:
     return hasattr(a, "shape") and hasattr(a, "dtype") and hasattr(a, "tensor_ref")
 
 
+def kernel_signature(func, n_args: int, kwargs) -> inspect.Signature:
+    """The kernel function's signature.  ufuncs and builtins passed as the
+    kernel (np.matmul, np.where, ...) have none that ``inspect`` can read:
+    they get positional parameters arg0, arg1, ... and keyword-only ones
+    for the given keywords."""
+    try:
+        return inspect.signature(func)
+    except (TypeError, ValueError):
+        P = inspect.Parameter
+        return inspect.Signature([P(f"arg{i}", P.POSITIONAL_ONLY) for i in range(n_args)]
+                                 + [P(k, P.KEYWORD_ONLY) for k in kwargs])
+
+
 def arg_shape_dtype(a):
     if isinstance(a, np.ndarray):
         return tuple(a.shape), a.dtype
@@ -117,7 +130,7 @@ class NKIPyKernel:
         graph = Graph(name=self.func.__name__)
         ctx = HIPTraceContext(graph)
         with tracing(ctx):
-            sig = inspect.signature(self.func)
+            sig = kernel_signature(self.func, len(args), kwargs)
             bound = sig.bind(*args, **kwargs)
             bound.apply_defaults()
             call_args, call_kwargs, params = [], {}, []

@@ -11,12 +11,12 @@ the ``BenchmarkResult`` of ``DeviceKernel.benchmark``.
 
 from __future__ import annotations
 
-import inspect
 import os
 from typing import Dict, Optional, Tuple
 
 import numpy as np
 
+from nkipy_amd.core.trace import kernel_signature
 from nkipy_amd.runtime.device_kernel import DeviceKernel
 from nkipy_amd.runtime.device_tensor import DeviceTensor
 
@@ -50,7 +50,7 @@ class BaremetalExecutor:
 
     def _prepare_io_tensors(self, ck: CompiledKernel, dk: DeviceKernel, *args,
                             **kwargs) -> Tuple[Dict[str, DeviceTensor], Dict[str, DeviceTensor], Dict[str, np.ndarray]]:
-        sig = inspect.signature(ck.traced_kernel.func)
+        sig = kernel_signature(ck.traced_kernel.func, len(args), kwargs)
         bound = sig.bind(*args, **kwargs)
         bound.apply_defaults()
         originals = {n: a for n, a in bound.arguments.items() if isinstance(a, np.ndarray)}

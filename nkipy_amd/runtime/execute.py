@@ -10,11 +10,9 @@ left out of the return value.  Returns one array, a tuple, or None.
 
 from __future__ import annotations
 
-import inspect
-
 import numpy as np
 
-from nkipy_amd.core.trace import _sanitize_array_dtype
+from nkipy_amd.core.trace import _sanitize_array_dtype, kernel_signature
 from nkipy_amd.runtime.device_kernel import DeviceKernel
 from nkipy_amd.runtime.device_tensor import DeviceTensor
 
@@ -29,7 +27,7 @@ def baremetal_run_traced_kernel(kernel, *args, artifacts_dir=None, save_trace=Fa
                                        additional_compiler_args=additional_compiler_args,
                                        build_dir=artifacts_dir)
     graph = dk.graph
-    sig = inspect.signature(kernel.func if hasattr(kernel, "func") else kernel)
+    sig = kernel_signature(kernel.func if hasattr(kernel, "func") else kernel, len(args), kwargs)
     bound = sig.bind(*args, **kwargs)
     bound.apply_defaults()
     arrays = {}

@@ -72,3 +72,31 @@ def assert_rel(got, ref, name: str, tol: float):
     RECORDS.append({"check": name, "n": int(err.size), "max_abs": float(err.max()), "max_rel": rel,
                     "worst_of_bar": rel / tol})
     assert rel <= tol, f"{name}: max rel err {rel:.3e} > {tol:.1e}"
+
+
+def assert_matches_numpy(got, ref, what: str):
+    """A kernel run against the same function run by NumPy (tuples item by
+    item).  fp32: |got - ref| <= 1e-4 |ref| + 1e-4 max(1, RMS(ref)); fp16:
+    1e-2 on both parts; integers and booleans exactly."""
+    if isinstance(ref, (tuple, list)):
+        assert isinstance(got, (tuple, list)) and len(got) == len(ref), what
+        for i, (g, r) in enumerate(zip(got, ref)):
+            assert_matches_numpy(g, r, f"{what}[{i}]")
+        return
+    ref = np.asarray(ref)
+    got = np.asarray(got)
+    assert got.shape == ref.shape, (what, got.shape, ref.shape)
+    if not np.issubdtype(ref.dtype, np.floating):
+        np.testing.assert_array_equal(got.astype(np.int64), ref.astype(np.int64), err_msg=what)
+        return
+    tol = 1e-2 if ref.dtype == np.float16 else 1e-4
+    r = ref.astype(np.float64)
+    g = got.astype(np.float64)
+    assert np.array_equal(np.isnan(g), np.isnan(r)), f"{what}: NaN positions differ"
+    fin = ~np.isnan(r)
+    r, g = r[fin], g[fin]
+    scale = max(1.0, float(np.sqrt(np.mean(r * r)))) if r.size else 1.0
+    err = np.abs(g - r)
+    bound = tol * np.abs(r) + tol * scale
+    bad = err > bound
+    assert not bad.any(), f"{what}: {int(bad.sum())} of {r.size} out of tolerance, max abs {err.max():.3e}"
