@@ -8,8 +8,8 @@
 // examples/models/qwen3/kernels/attention.py:109-140): np.repeat of the KV
 // heads, q @ k^T scaled, causal mask added, softmax over keys, @ v.
 //
-// Work split: one workgroup (4 waves) per (b, h, block of 128 queries); each
-// wave owns 32 queries; two workgroups share a CU.  The kernel computes
+// Work split: one workgroup of NW waves (4 or 8) per (b, h, block of 32 NW
+// queries); each wave owns 32 queries; two workgroups share a CU.  The kernel computes
 // S^T = K Q^T and O^T = V^T P^T with v_mfma_f32_32x32x16_bf16 so that every
 // lane owns one query column: the running max / sum of the online softmax
 // are lane-local (the two lane halves holding the same query combine with
@@ -44,10 +44,7 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef __attribute__((address_space(3))) void lds_void;
 
-#define AQ 128  // queries per workgroup
-#define AK 64   // keys per block
 #define AD 128  // head dim
-#define TILE_BYTES (AK * AD * 2)
 
 struct AttnArgs {
   const uint16_t *q;
@@ -84,7 +81,21 @@ template <bool B> struct Flag {
   static constexpr bool value = B;
 };
 
-extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(AttnArgs a) {
+// NW waves (32 queries each) share one workgroup's K / V tiles: AQ = 32 NW
+// queries per workgroup, two workgroups per CU (64 KiB of LDS each), so NW
+// = 8 puts four waves on every SIMD (at most 128 registers each) and halves
+// the K / V traffic per query.
+// AKB keys per block (64, or 32: one 32 x 32 score tile, half the score
+// registers and LDS, which lets three workgroups of four waves share a CU).
+// PIPE: scores of block j + 1 computed while block j's softmax runs (two
+// score sets live); without it a wave computes a block's scores, then its
+// softmax, and the other waves on the SIMD fill the gaps.
+template <int NW, int AKB, bool PIPE>
+__device__ __forceinline__ void attention_causal_body(const AttnArgs &a) {
+  constexpr int AQW = 32 * NW;  // queries per workgroup
+  constexpr int AK = AKB;
+  constexpr int KT = AK / 32;   // 32-key score tiles per block
+  constexpr int TILE_BYTES = AK * AD * 2;
   __shared__ __attribute__((aligned(1024))) uint8_t K0[TILE_BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t K1[TILE_BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t V0[TILE_BYTES];
@@ -100,7 +111,7 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
   // and blocks that share one K / V head on one XCD, whose L2 then serves
   // the K / V re-reads.  Within a KV head, the longest (last) query blocks
   // go first.
-  const int nqb = a.S / AQ;
+  const int nqb = a.S / AQW;
   const int rep = a.Hq / a.Hkv;
   const int per_kv = rep * nqb;
   const int nwg = a.B * a.Hkv * per_kv;  // the grid size
@@ -110,7 +121,7 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
   const int qb = nqb - 1 - within / rep;
   const int g = bg % a.Hkv, b = bg / a.Hkv;
   const int h = g * rep + within % rep;
-  const int q0 = qb * AQ;
+  const int q0 = qb * AQW;
 
   const uint16_t *qp = a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh;
   const uint16_t *kp = a.k + (int64_t)b * a.k_sb + (int64_t)g * a.k_sh;
@@ -135,59 +146,62 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
   float m_run = -INFINITY, l_run = 0.f;
   const float sl2 = a.scale * 1.44269504088896340736f;  // scale * log2(e)
 
-  const int kend = a.causal ? (q0 + AQ) : a.S;
+  const int kend = a.causal ? (q0 + AQW) : a.S;
   const int nkb = kend / AK;
 
-  // DMA plan: a tile pair is 32 moves of 1 KiB (4 rows of 256 bytes); wave w
-  // does moves m = 4 j + w: j < 4 K rows, j >= 4 V rows.  The chunk a lane
-  // fetches is the same for every j (the swizzles only see row & 15).
+  // DMA plan: a tile is AK / 4 moves of 1 KiB (4 rows of 256 bytes); wave w
+  // does the K and V moves m = NW j + w (rows 4 m ..).  The chunk a lane
+  // fetches is the same for every j (the swizzles only see row & 15, and
+  // 4 NW j is a multiple of 16).
+  constexpr int NM = AK / 4 / NW;  // K (and V) moves per wave
+  static_assert(NM >= 1 && NM * NW * 4 == AK, "moves per wave");
   const int kchunk = (lane & 15) ^ kswz(wave * 4 + (lane >> 4));
   const int vchunk = (lane & 15) ^ vswz(wave * 4 + (lane >> 4));
-  uint32_t kbase[4], vbase[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int row = (j * 4 + wave) * 4 + (lane >> 4);
-    kbase[j] = (uint32_t)(((int64_t)row * a.k_ss + kchunk * 8) * 2);
-    vbase[j] = (uint32_t)(((int64_t)row * a.v_ss + vchunk * 8) * 2);
-  }
+  // move j of this wave: rows 4 (NW j + wave) + lane / 16, i.e. the j = 0
+  // source plus j times a uniform stride
+  const int row0 = wave * 4 + (lane >> 4);
+  const uint32_t kbase = (uint32_t)(((int64_t)row0 * a.k_ss + kchunk * 8) * 2);
+  const uint32_t vbase = (uint32_t)(((int64_t)row0 * a.v_ss + vchunk * 8) * 2);
+  const uint32_t kjs = (uint32_t)(NW * 4 * a.k_ss * 2), vjs = (uint32_t)(NW * 4 * a.v_ss * 2);
   auto load_k = [&](uint8_t *dst, int kb) {
     const uint32_t kst = (uint32_t)((int64_t)kb * AK * a.k_ss * 2);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dma16(rk, dst + (j * 4 + wave) * 1024, kbase[j] + kst);
+    for (int j = 0; j < NM; ++j) dma16(rk, dst + (j * NW + wave) * 1024, kbase + j * kjs + kst);
   };
   auto load_v = [&](uint8_t *dst, int kb) {
     const uint32_t vst = (uint32_t)((int64_t)kb * AK * a.v_ss * 2);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dma16(rv, dst + (j * 4 + wave) * 1024, vbase[j] + vst);
+    for (int j = 0; j < NM; ++j) dma16(rv, dst + (j * NW + wave) * 1024, vbase + j * vjs + vst);
   };
 
-  // Per-lane LDS byte offsets, fixed for the whole loop (the swizzles only
-  // see lane bits), so every fragment read is lane offset + immediate.
-  // K fragment (row kt*32 + l32, chunk 2 kk + lhi): kt*8192 + koff[kk].
-  int koff[AD / 16];
-#pragma unroll
-  for (int kk = 0; kk < AD / 16; ++kk) koff[kk] = l32 * 256 + (((kk * 2 + lhi) ^ kswz(l32)) << 4);
+  // Per-lane LDS byte offsets (the swizzles only see lane bits).
+  // K fragment (row kt*32 + l32, chunk 2 kk + lhi): kt*8192 + koff(kk), with
+  // chunk (2 kk + lhi) ^ (l32 & 15) = (2 kk ^ (l32 & 14)) + (lhi ^ (l32 & 1)):
+  // one lane base plus kk * 32 XOR a lane constant (no table of offsets).
+  const int klb = l32 * 256 + ((lhi ^ (l32 & 1)) << 4);
+  const int kx = (l32 & 14) << 4;
+  auto koff = [&](int kk) __attribute__((always_inline)) { return klb + ((kk << 5) ^ kx); };
   // V^T transpose read (group g = lane/16, i = lane%16): source row
   // 16 j + 8 si + 4 (g/2) + i/4, columns dt*32 + 16 (g%2) + 4 (i%4):
-  // (16 j + 8 si) * 256 + voff[dt].
-  int voff[4];
+  // (16 j + 8 si) * 256 + voff(dt).
+  int vlb, vx;
   {
     const int grp = lane >> 4, gi = lane & 15;
     const int c0 = (grp & 1) * 2 + ((gi & 3) >> 1), vsh = (gi >> 2) & 3;
-    const int lb = (4 * (grp >> 1) + (gi >> 2)) * 256 + (c0 << 4) + (gi & 1) * 8;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) voff[dt] = lb + ((dt ^ vsh) << 6);
+    vlb = (4 * (grp >> 1) + (gi >> 2)) * 256 + (c0 << 4) + (gi & 1) * 8;
+    vx = vsh << 6;
   }
+  auto voff = [&](int dt) __attribute__((always_inline)) { return vlb + ((dt << 6) ^ vx); };
 
   // S^T = K Q^T for one 64-key block (keys kt*32 + row, this lane's query)
-  auto qk = [&](const uint8_t *Kt, f32x16 (&s)[2]) __attribute__((always_inline)) {
+  auto qk = [&](const uint8_t *Kt, f32x16 (&s)[KT]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
+    for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[kt][r] = 0.f;
 #pragma unroll
       for (int kk = 0; kk < AD / 16; ++kk) {
-        const bf16x8_t kf = *reinterpret_cast<const bf16x8_t *>(Kt + kt * 8192 + koff[kk]);
+        const bf16x8_t kf = *reinterpret_cast<const bf16x8_t *>(Kt + kt * 8192 + koff(kk));
         s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[kt], 0, 0, 0);
       }
     }
@@ -197,13 +211,13 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
   // are the final pair of a row of blocks: under a causal mask they may
   // cross the diagonal of this wave's queries; every other block lies below
   // it for all four waves and runs without mask code.
-  auto finish = [&](f32x16 (&s)[2], const uint8_t *Vt, int key0, auto diag_flag) __attribute__((always_inline)) {
+  auto finish = [&](f32x16 (&s)[KT], const uint8_t *Vt, int key0, auto diag_flag) __attribute__((always_inline)) {
     constexpr bool DIAG = decltype(diag_flag)::value;
     // block max of the raw scores (the scale is positive, so it commutes
     // with the max), as a tree
-    float mx[8];
+    float mx[4 * KT];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4 * KT; ++i) {
       if constexpr (DIAG) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -215,8 +229,8 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
       const int kt = i >> 2, r0 = (i & 3) * 4;
       mx[i] = fmaxf(fmaxf(s[kt][r0], s[kt][r0 + 1]), fmaxf(s[kt][r0 + 2], s[kt][r0 + 3]));
     }
-    float bmax = fmaxf(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])),
-                       fmaxf(fmaxf(mx[4], mx[5]), fmaxf(mx[6], mx[7])));
+    float bmax = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+    if constexpr (KT == 2) bmax = fmaxf(bmax, fmaxf(fmaxf(mx[4], mx[5]), fmaxf(mx[6], mx[7])));
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
     // Running max m_run in log2 units, kept stale: it moves only when some
     // row's block max exceeds it by more than 8, so every P stays <= 2^8 and
@@ -227,7 +241,9 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
     const float m_new = moved ? fmaxf(m_run, m_blk) : m_run;
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first block, 1 if unmoved
     m_run = m_new;
-    float ps[4] = {0.f, 0.f, 0.f, 0.f};
+    float ps[AK / 16];
+#pragma unroll
+    for (int j = 0; j < AK / 16; ++j) ps[j] = 0.f;
     bf16x8_t pf[AK / 16];
 #pragma unroll
     for (int j = 0; j < AK / 16; ++j)
@@ -238,7 +254,8 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
         ps[j] += p;
         pf[j][e] = (__bf16)p;
       }
-    float bsum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+    float bsum = ps[0] + ps[1];
+    if constexpr (KT == 2) bsum = bsum + (ps[2] + ps[3]);
     bsum += __shfl_xor(bsum, 32, 64);
     l_run = fmaf(l_run, alpha, bsum);
     if (moved) {
@@ -260,7 +277,7 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
 #pragma unroll
         for (int si = 0; si < 2; ++si)
           v[si] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_s16x4 *)(Vt + (16 * j + 8 * si) * 256 + voff[dt]));
+              (lds_s16x4 *)(Vt + (16 * j + 8 * si) * 256 + voff(dt)));
         const bf16x8_t vf = __builtin_shufflevector(__builtin_bit_cast(bf16x4_t, v[0]),
                                                     __builtin_bit_cast(bf16x4_t, v[1]), 0, 1, 2, 3, 4, 5, 6, 7);
         acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[j], acc_o[dt], 0, 0, 0);
@@ -272,14 +289,54 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
   // V tile in V[j & 1]; the step for block j computes the scores of block
   // j + 1 while it runs block j's softmax and PV, and streams in K_{j+2} and
   // V_{j+1} meanwhile (K runs one tile ahead of V).  The buffers a step
-  // overwrites were last read before the previous step's barrier.
-  f32x16 sa[2], sb[2];
-  auto step = [&](int j, f32x16 (&cur)[2], f32x16 (&nxt)[2], uint8_t *kdst, uint8_t *vdst, const uint8_t *knext,
-                  const uint8_t *vcur) __attribute__((always_inline)) {
+  // overwrites were last read before the previous step's barrier.  Loads
+  // past the blocks a workgroup needs read in-range rows it ignores, or zeros
+  // past the end of the sequence.
+  // Blocks 0 .. nd-1 lie below the diagonal of every wave (causal: the keys
+  // before the workgroup's first query); the last blocks are the
+  // diagonal blocks (AQW / AK of them), masked per key and skipped by the
+  // waves whose queries all precede them (every wave still takes part in the loads and
+  // barriers).  nd and the number of diagonal blocks are even.
+  constexpr int NDIAG = AQW / AK;  // diagonal blocks (even)
+  static_assert(NDIAG % 2 == 0, "diagonal blocks come in pairs");
+  const int nd = a.causal ? q0 / AK : nkb - NDIAG;
+  auto needed = [&](int j) { return !a.causal || j * AK <= wq0 + 31; };
+  if constexpr (!PIPE) {
+    f32x16 sc[KT];
+    auto step1 = [&](int j, const uint8_t *kc, const uint8_t *vc, uint8_t *kn, uint8_t *vn, auto diag_flag)
+        __attribute__((always_inline)) {
+      constexpr bool DIAG = decltype(diag_flag)::value;
+      load_k(kn, j + 1);
+      load_v(vn, j + 1);
+      if (!DIAG || needed(j)) {
+        qk(kc, sc);
+        finish(sc, vc, j * AK, diag_flag);
+      }
+      wait_vmem();
+      __syncthreads();
+    };
+    load_k(K0, 0);
+    load_v(V0, 0);
+    wait_vmem();
+    __syncthreads();
+    for (int kb = 0; kb < nd; kb += 2) {
+      step1(kb, K0, V0, K1, V1, Flag<false>{});
+      step1(kb + 1, K1, V1, K0, V0, Flag<false>{});
+    }
+#pragma unroll
+    for (int t = 0; t < NDIAG; t += 2) {
+      step1(nd + t, K0, V0, K1, V1, Flag<true>{});
+      step1(nd + t + 1, K1, V1, K0, V0, Flag<true>{});
+    }
+  } else {
+  f32x16 sa[KT], sb[KT];
+  auto step = [&](int j, f32x16 (&cur)[KT], f32x16 (&nxt)[KT], uint8_t *kdst, uint8_t *vdst, const uint8_t *knext,
+                  const uint8_t *vcur, auto diag_flag) __attribute__((always_inline)) {
+    constexpr bool DIAG = decltype(diag_flag)::value;
     load_k(kdst, j + 2);
     load_v(vdst, j + 1);
-    qk(knext, nxt);
-    finish(cur, vcur, j * AK, Flag<false>{});
+    if (!DIAG || (j + 1 < nkb && needed(j + 1))) qk(knext, nxt);
+    if (!DIAG || needed(j)) finish(cur, vcur, j * AK, diag_flag);
     wait_vmem();
     __syncthreads();
   };
@@ -290,20 +347,16 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
   __syncthreads();
   qk(K0, sa);
   __syncthreads();
-  // Blocks 0 .. nkb-3 lie below the diagonal of every wave; nkb is even.
-  int kb = 0;
-  for (; kb < nkb - 2; kb += 2) {
-    step(kb, sa, sb, K0, V1, K1, V0);
-    step(kb + 1, sb, sa, K1, V0, K0, V1);
+  for (int kb = 0; kb < nd; kb += 2) {
+    step(kb, sa, sb, K0, V1, K1, V0, Flag<false>{});
+    step(kb + 1, sb, sa, K1, V0, K0, V1, Flag<false>{});
   }
-  // final pair: blocks nkb-2 (scores in sa, V in V0) and nkb-1 (K in K1)
-  load_v(V1, nkb - 1);
-  const bool need_last = !a.causal || (nkb - 1) * AK <= wq0 + 31;
-  if (need_last) qk(K1, sb);
-  finish(sa, V0, (nkb - 2) * AK, Flag<true>{});
-  wait_vmem();
-  __syncthreads();
-  if (need_last) finish(sb, V1, (nkb - 1) * AK, Flag<true>{});
+#pragma unroll
+  for (int t = 0; t < NDIAG; t += 2) {
+    step(nd + t, sa, sb, K0, V1, K1, V0, Flag<true>{});
+    step(nd + t + 1, sb, sa, K1, V0, K0, V1, Flag<true>{});
+  }
+  }
 
   // normalise and store: lane holds d = t*32 + (r>>2)*8 + lhi*4 + (r&3) of its query
   const float inv_l = 1.0f / l_run;
@@ -316,6 +369,17 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(At
       const uint32_t w1 = pack_bf16x2(acc_o[t][gq * 4 + 2] * inv_l, acc_o[t][gq * 4 + 3] * inv_l);
       *reinterpret_cast<uint2 *>(orow + t * 32 + gq * 8 + lhi * 4) = make_uint2(w0, w1);
     }
+}
+
+// (launch bounds: threads per workgroup, minimum waves per SIMD)
+extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(AttnArgs a) {
+  attention_causal_body<4, 64, true>(a);
+}
+extern "C" __global__ __launch_bounds__(512, 2) void nk_attention_causal_d128_w8(AttnArgs a) {
+  attention_causal_body<8, 64, true>(a);
+}
+extern "C" __global__ __launch_bounds__(256, 3) void nk_attention_causal_d128_k32(AttnArgs a) {
+  attention_causal_body<4, 32, false>(a);
 }
 
 // ---------------------------------------------------------------------------

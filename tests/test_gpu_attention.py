@@ -21,14 +21,14 @@ def _close(got, ref, tol=2e-2, axis=-1):
     assert_close(got, ref, name, rtol=tol, axis=axis)
 
 
-def _run(gpu, q, k, v):
+def _run(gpu, q, k, v, **variant):
     B, S, Hq, D = q.shape
     Hkv = k.shape[2]
     t = [DeviceTensor.from_numpy(dt.to_bf16(a)) for a in (q, k, v)]
     o = DeviceTensor.empty(q.shape, dt.bfloat16)
     st = {"q": (S * Hq * D, Hq * D, D), "k": (S * Hkv * D, Hkv * D, D),
           "v": (S * Hkv * D, Hkv * D, D), "o": (S * Hq * D, Hq * D, D)}
-    LA.attention(t[0].ptr, t[1].ptr, t[2].ptr, o.ptr, B, S, Hq, Hkv, D, 1 / np.sqrt(D), st).run(gpu)
+    LA.attention(t[0].ptr, t[1].ptr, t[2].ptr, o.ptr, B, S, Hq, Hkv, D, 1 / np.sqrt(D), st, **variant).run(gpu)
     gpu.sync()
     return dt.to_float32(o.numpy())
 
@@ -41,6 +41,22 @@ def test_attention_small(gpu, shape):
     k = N.bf16_round(rng.standard_normal((B, S, Hkv, 128)))
     v = N.bf16_round(rng.standard_normal((B, S, Hkv, 128)))
     _close(_run(gpu, q, k, v), K.causal_gqa_attention(q, k, v))
+
+
+@pytest.mark.parametrize("waves,key_block", [(4, 64), (8, 64), (4, 32)])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", [(1, 256, 4, 1), (2, 512, 8, 2), (1, 768, 2, 2)])
+def test_attention_variants(gpu, waves, key_block, causal, shape):
+    """Every kernel variant (waves per workgroup, keys per block), masked and
+    unmasked, including the diagonal blocks a workgroup's waves skip."""
+    B, S, Hq, Hkv = shape
+    print(f"attention variant waves={waves} key_block={key_block} causal={causal} shape={shape}", flush=True)
+    rng = np.random.default_rng(S + Hq + waves + key_block)
+    q = N.bf16_round(rng.standard_normal((B, S, Hq, 128)))
+    k = N.bf16_round(rng.standard_normal((B, S, Hkv, 128)))
+    v = N.bf16_round(rng.standard_normal((B, S, Hkv, 128)))
+    got = _run(gpu, q, k, v, causal=causal, waves=waves, key_block=key_block)
+    _close(got, K.causal_gqa_attention(q, k, v, causal=causal))
 
 
 def test_attention_config_sampled(gpu):
