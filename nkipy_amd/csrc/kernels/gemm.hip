@@ -965,6 +965,14 @@ __device__ __forceinline__ void dma16_asm(i32x4_t r, uint32_t lds, uint32_t off)
                :: "v"(off), "s"(r), "s"(m) : "memory", "m0");
 }
 
+// the same move with a uniform (SGPR) part of the offset: voff + soff
+__device__ __forceinline__ void dma16_asm_so(i32x4_t r, uint32_t lds, uint32_t voff, uint32_t soff) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
+  const uint32_t so = __builtin_amdgcn_readfirstlane(soff);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %3 offen lds"
+               :: "v"(voff), "s"(r), "s"(m), "s"(so) : "memory", "m0");
+}
+
 template <bool NT, bool FP8, bool SWIGLU, typename TC, bool ROPE = false>
 __device__ __forceinline__ void gemm_pp_body(const GemmArgs &a) {
   static_assert(!ROPE || (!SWIGLU && sizeof(TC) == 2), "the rotary epilogue writes bf16 projections");
@@ -1220,6 +1228,199 @@ __device__ __forceinline__ void gemm_pp_body(const GemmArgs &a) {
   gemm_epilogue16<SWIGLU, TC, 4>(a, acc, m0 + arow0, n0 + bw0, lane);
 }
 
+// ---------------------------------------------------------------------------
+// 8-wave kernel with 64-deep K stages (fp8 NT weights)
+// ---------------------------------------------------------------------------
+// The ping-pong of gemm_pp_body (phases of 32 k, group 0 and group 1
+// alternating between MFMAs and fragment reads), but LDS holds a ring of
+// three stages of 64 k: A 256 rows x 128 bytes and fp8 B^T 256 rows x 64
+// bytes (48 KiB, 144 KiB for the ring).  Each global -> LDS move then reads
+// whole 128-byte A lines and 64-byte B row segments: half as many requests
+// as 32-deep stages, whose 64- and 32-byte segments kept the texture address
+// unit stalled on the L1 cache for a third of the kernel.
+//   A stage:  row r, logical 16-byte chunk c (k 8c..8c+7) at slot c ^ ((r >> 1) & 7)
+//   B stage:  row r, logical chunk c (k 16c..16c+15) at slot c ^ ((r >> 2) & 3)
+// A fragment read (16 rows x one chunk per 16 lanes) and a B read (16 rows
+// x one chunk x two halves per 32 lanes) each cover distinct 16- / 8-byte
+// groups of a 256-byte LDS row of banks.
+// Stage t (phases 2t, 2t + 1) is read by group 0 in the slots before its
+// phases and by group 1 in the first slot of each; it is refilled with
+// block t + 3 in the second slot of phase 2t + 1.
+__device__ __forceinline__ int swz_a64(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int swz_b64(int r) { return (r >> 2) & 3; }
+
+template <bool SWIGLU, typename TC, bool ROPE = false>
+__device__ __forceinline__ void gemm_pp64_body(const GemmArgs &a) {
+  static_assert(!ROPE || (!SWIGLU && sizeof(TC) == 2), "the rotary epilogue writes bf16 projections");
+  constexpr int R2 = 3;                         // ring stages
+  constexpr int KB = 64;                        // k per stage
+  constexpr int SA = 32768, SS = SA + 16384;    // A bytes, stage bytes
+  constexpr int NAM = 4, NBM = 2;               // A / B moves per wave per stage
+  constexpr int ND = NAM + NBM;
+
+  int tm, tn;
+  gemm_tile(a, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM;
+  const int64_t n0 = (int64_t)tn * (SWIGLU ? BN / 2 : BN);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2, wi = wave & 3;
+  const int wm = wi >> 1, wn = wi & 1;
+  const int arow0 = 128 * grp + 64 * wm;
+
+  f32x4 acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.f;
+
+  const i32x4_t ra = rsrc_words(a.A, a.M * a.lda * 2);
+  const i32x4_t rb0 = rsrc_words(a.B0, a.N * a.ldb);
+  const i32x4_t rb1 = rsrc_words(SWIGLU ? a.B1 : a.B0, a.N * a.ldb);
+
+  // A move m = 8 j + wave (j < 4): rows 8 m .. 8 m + 7; lane l fills slot
+  // l & 7 of row 8 m + l / 8 with logical chunk (l & 7) ^ swz_a64(row), and
+  // swz_a64(row) = (4 m + l / 16) & 7 = (4 wave + l / 16) & 7 for every j.
+  const int ac = (lane & 7) ^ ((4 * wave + (lane >> 4)) & 7);
+  const uint32_t abase = (uint32_t)(((m0 + 8 * wave + (lane >> 3)) * a.lda + ac * 8) * 2);
+  const uint32_t astr = (uint32_t)(64 * a.lda * 2);
+  // B move m = 8 j + wave (j < 2): tile rows 16 m .. 16 m + 15; lane l fills
+  // slot l & 3 of row 16 m + l / 4 with logical chunk (l & 3) ^ swz_b64(row),
+  // swz_b64(row) = (l / 16) & 3.  Tile row r is weight row n0 + r (SwiGLU:
+  // rows 128.. are the up weight's rows n0 + r - 128, i.e. move j = 1).
+  const int bc = (lane & 3) ^ ((lane >> 4) & 3);
+  const uint32_t bbase = (uint32_t)((n0 + 16 * wave + (lane >> 2)) * a.ldb + bc * 16);
+  const uint32_t bstr = SWIGLU ? 0u : (uint32_t)(128 * a.ldb);
+  // per-lane offset (the base, or OOB for a chunk past K: OOB plus the
+  // uniform part stays past the end) plus a uniform per-move part
+  auto issue = [&](uint8_t *St, int64_t k0) __attribute__((always_inline)) {
+    const uint32_t kk0 = (uint32_t)k0;
+    const uint32_t va = k0 + ac * 8 < a.K ? abase : OOB;
+    const uint32_t vb = k0 + bc * 16 < a.K ? bbase : OOB;
+    const uint32_t la = lds_addr(St), lb = la + SA;
+#pragma unroll
+    for (int j = 0; j < NAM; ++j) dma16_asm_so(ra, la + (j * 8 + wave) * 1024, va, j * astr + kk0 * 2);
+#pragma unroll
+    for (int j = 0; j < NBM; ++j)
+      dma16_asm_so((SWIGLU && j) ? rb1 : rb0, lb + (j * 8 + wave) * 1024, vb, j * bstr + kk0);
+  };
+
+  // fragment offsets of phase half h: A tile i = rows arow0 + 16 i + l16
+  // (swz_a64 of those rows = (l16 >> 1) & 7), B tile j = rows bw0 + brel[j]
+  // + l16 (swz_b64 = (l16 >> 2) & 3)
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int bw0 = SWIGLU ? wn * 64 : wn * 128;
+  constexpr int brel[8] = {0, 16, 32, 48, SWIGLU ? 128 : 64, SWIGLU ? 144 : 80, SWIGLU ? 160 : 96,
+                           SWIGLU ? 176 : 112};
+  // half 1 reads logical chunks 4 + g (A) and 2 + g / 2 (B): slot XOR 4 / 2,
+  // i.e. offset bit 6 / bit 5 (the row and lane parts sit in other bits)
+  const uint32_t aoff0 = (arow0 + l16) * 128 + ((g4 ^ swz_a64(l16)) << 4);
+  const uint32_t boff0 = SA + (bw0 + l16) * 64 + (((g4 >> 1) ^ swz_b64(l16)) << 4) + 8 * (g4 & 1);
+
+  // One LDS base per operand and call, kept opaque so that it is formed at
+  // the read (stage bases past 64 KiB do not fit the reads' immediate
+  // offsets; hoisted per-stage, per-tile addresses would not fit the
+  // register budget); the tile offsets are immediates.
+  typedef __attribute__((address_space(3))) const uint8_t lds_u8;
+  typedef __attribute__((address_space(3))) const bf16x8_t lds_bf16x8;
+  typedef __attribute__((address_space(3))) const unsigned long long lds_u64;
+  bf16x8_t af[4], bf[8];
+  auto load = [&](const uint8_t *St, auto htag) __attribute__((always_inline)) {
+    constexpr int H = decltype(htag)::value;
+    lds_u8 *pa = (lds_u8 *)St + (H ? (aoff0 ^ 64u) : aoff0);
+    lds_u8 *pb = (lds_u8 *)St + (H ? (boff0 ^ 32u) : boff0);
+    asm volatile("" : "+v"(pa), "+v"(pb));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<lds_bf16x8 *>(pa + i * 2048);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const unsigned long long q = *reinterpret_cast<lds_u64 *>(pb + brel[j] * 64);
+      const uint4 w = e4m3x8_to_bf16x8(make_uint2((uint32_t)q, (uint32_t)(q >> 32)));
+      bf[j] = *reinterpret_cast<const bf16x8_t *>(&w);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  };
+  auto compute = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
+  };
+  auto slot_end = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    barrier_no_fence();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  __shared__ __attribute__((aligned(1024))) uint8_t SG0[SS], SG1[SS], SG2[SS];
+  auto st = [&](auto stag) __attribute__((always_inline)) -> uint8_t * {
+    constexpr int S = decltype(stag)::value;
+    if constexpr (S == 0) return SG0; else if constexpr (S == 1) return SG1; else return SG2;
+  };
+
+  const int nblk = (int)((a.K + KB - 1) / KB);
+  issue(SG0, 0);
+  issue(SG1, KB);
+  issue(SG2, 2 * KB);
+  wait_vmem_but<ND * 2>();  // block 0 landed
+  slot_end();
+  if (grp == 0) load(SG0, Int<0>{});
+  slot_end();
+  // phase (block t, half H) in stage S = t mod 3; G = this wave's group
+  auto phase = [&](auto stag, auto htag, int t, auto gtag) __attribute__((always_inline)) {
+    constexpr int S = decltype(stag)::value;
+    constexpr int H = decltype(htag)::value;
+    constexpr int G = decltype(gtag)::value;
+    uint8_t *Sc = st(Int<S>{});
+    if (G == 0) compute(); else load(Sc, Int<H>{});
+    if (H == 1) wait_vmem_but<ND * (R2 - 2)>();  // block t + 1 landed
+    slot_end();
+    // group 0 reads the next phase (past the last block it reads a stage
+    // nothing will consume); after the second half every wave refills S
+    if (G == 0) {
+      if constexpr (H == 0) load(Sc, Int<1>{}); else load(st(Int<(S + 1) % R2>{}), Int<0>{});
+    }
+    if (H == 1) issue(Sc, (int64_t)(t + R2) * KB);
+    if (G == 1) compute();
+    slot_end();
+  };
+  auto run = [&](auto gtag) __attribute__((always_inline)) {
+    int t = 0;
+    for (; t + R2 <= nblk; t += R2) {
+      phase(Int<0>{}, Int<0>{}, t, gtag);
+      phase(Int<0>{}, Int<1>{}, t, gtag);
+      phase(Int<1>{}, Int<0>{}, t + 1, gtag);
+      phase(Int<1>{}, Int<1>{}, t + 1, gtag);
+      phase(Int<2>{}, Int<0>{}, t + 2, gtag);
+      phase(Int<2>{}, Int<1>{}, t + 2, gtag);
+    }
+    if (t < nblk) {
+      phase(Int<0>{}, Int<0>{}, t, gtag);
+      phase(Int<0>{}, Int<1>{}, t, gtag);
+    }
+    if (t + 1 < nblk) {
+      phase(Int<1>{}, Int<0>{}, t + 1, gtag);
+      phase(Int<1>{}, Int<1>{}, t + 1, gtag);
+    }
+  };
+  if (grp == 0)
+    run(Int<0>{});
+  else
+    run(Int<1>{});
+  wait_vmem();
+  if constexpr (ROPE) {
+    if (n0 + bw0 < (int64_t)a.rope_nq + a.rope_nk) {
+      gemm_epilogue_rope<4>(a, acc, m0 + arow0, n0 + bw0, lane);
+      return;
+    }
+  }
+  gemm_epilogue16<SWIGLU, TC, 4>(a, acc, m0 + arow0, n0 + bw0, lane);
+}
+
 #define NK_GEMM(NT, FP8, SW, TC, name)                                                   \
   extern "C" __global__ __launch_bounds__(NTHREADS, 1) void name(GemmArgs a) {           \
     gemm_body<NT, FP8, SW, TC>(a);                                                       \
@@ -1256,6 +1457,16 @@ NK_GEMM_PP(true, true, true, bf16, nk_gemm8_swiglu_nt_e4m3_bf16)
   extern "C" __global__ __launch_bounds__(512, 1) void name(GemmArgs a) {                \
     gemm_pp_body<NT, FP8, false, bf16, true>(a);                                         \
   }
+
+#define NK_GEMM_K64(SW, TC, ROPE, name)                                                  \
+  extern "C" __global__ __launch_bounds__(512, 1) void name(GemmArgs a) {                \
+    gemm_pp64_body<SW, TC, ROPE>(a);                                                     \
+  }
+
+NK_GEMM_K64(false, bf16, false, nk_gemm8k_nt_e4m3_bf16)
+NK_GEMM_K64(false, float, false, nk_gemm8k_nt_e4m3_f32)
+NK_GEMM_K64(true, bf16, false, nk_gemm8k_swiglu_nt_e4m3_bf16)
+NK_GEMM_K64(false, bf16, true, nk_gemm8k_nt_e4m3_bf16_rope)
 
 NK_GEMM_ROPE(false, false, nk_gemm8_nn_bf16_bf16_rope)
 NK_GEMM_ROPE(true, false, nk_gemm8_nt_bf16_bf16_rope)

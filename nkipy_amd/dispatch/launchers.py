@@ -260,7 +260,7 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
          bias_ptr: int = 0, scale_ptr: int = 0, resid_ptr: int = 0,
          up_ptr: int = 0, up_scale_ptr: int = 0, pingpong: bool = None,
          round_before_bias: bool = False, round_before_resid: bool = False,
-         rope: GemmRope = None) -> Launch:
+         rope: GemmRope = None, stage64: bool = None) -> Launch:
     """C[M, N] = A[M, K] @ B (+ epilogue) on bf16 MFMA, fp32 accumulation.
 
     ``layout`` "nn": B is K x N row-major (ldb >= N); "nt": B is N x K
@@ -275,7 +275,9 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
     between MFMAs and fragment loads; the default where it exists, i.e. for
     every layout except fp8 NN weights) or the 4-wave kernel.  ``rope``
     (:class:`GemmRope`) selects the 8-wave kernel whose epilogue applies the
-    rotary embedding to the q / k columns.
+    rotary embedding to the q / k columns.  ``stage64`` (default: wherever
+    it exists, i.e. fp8 NT weights on the 8-wave kernel) selects 64-deep K
+    stages in LDS (whole 128-byte lines per global read).
     """
     if layout not in ("nn", "nt"):
         raise LaunchError(f"unknown GEMM layout {layout}")
@@ -355,7 +357,11 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
         pingpong = has_pp
     if pingpong and not has_pp:
         raise LaunchError("the 8-wave GEMM has no fp8 NN variant")
-    prefix = "nk_gemm8" if pingpong else "nk_gemm"
+    if stage64 is None:  # the default wherever it exists: half the global read requests
+        stage64 = bool(pingpong and fp8 and layout == "nt")
+    if stage64 and not (pingpong and fp8 and layout == "nt"):
+        raise LaunchError("64-deep K stages exist for fp8 NT weights on the 8-wave kernel")
+    prefix = ("nk_gemm8k" if stage64 else "nk_gemm8") if pingpong else "nk_gemm"
     if swiglu:
         symbol = f"{prefix}_swiglu_{layout}_{btag}_bf16"
     else:

@@ -37,6 +37,12 @@ SHAPES = [(256, 256, 64), (512, 768, 320), (300, 520, 136), (64, 40, 16), (1000,
 
 # pp: the 8-wave kernel (default) and the 4-wave kernel
 PP = [True, False]
+# fp8 NT weights also have the 8-wave kernel with 64-deep K stages
+PP8 = [True, False, "k64"]
+
+
+def _kern(pp):
+    return {"pingpong": pp is not False, "stage64": pp == "k64" if pp is not False else None}
 
 
 @pytest.mark.parametrize("pp", PP)
@@ -90,7 +96,7 @@ def test_gemm_swiglu(gpu, layout, pp):
     _close(dt.to_float32(hd.numpy()), ref)
 
 
-@pytest.mark.parametrize("pp", PP)
+@pytest.mark.parametrize("pp", PP8)
 def test_gemm_fp8_nt_scales_bias_residual(gpu, pp):
     M, Nn, Kk = 384, 512, 448
     rng = np.random.default_rng(11)
@@ -109,11 +115,11 @@ def test_gemm_fp8_nt_scales_bias_residual(gpu, pp):
     cd = DeviceTensor.empty((M, Nn), dt.bfloat16)
     _run(gpu, LA.gemm(xd.ptr, wd.ptr, cd.ptr, M, Nn, Kk, layout="nt", b_dtype=dt.float8_e4m3fn,
                       c_dtype=dt.bfloat16, scale_ptr=sd.ptr, bias_ptr=bd.ptr, resid_ptr=rd.ptr,
-                      pingpong=pp))
+                      **_kern(pp)))
     _close(dt.to_float32(cd.numpy()), ref)
 
 
-@pytest.mark.parametrize("pp", PP)
+@pytest.mark.parametrize("pp", PP8)
 @pytest.mark.parametrize("Kk", [16, 64, 128, 192, 208, 576])
 def test_gemm_fp8_nt_k_tiles(gpu, Kk, pp):
     """fp8 NT weights stream through an LDS ring (three stages in the 4-wave
@@ -131,11 +137,11 @@ def test_gemm_fp8_nt_k_tiles(gpu, Kk, pp):
     sd = DeviceTensor.from_numpy(scale.astype(np.float32))
     cd = DeviceTensor.empty((M, Nn), dt.float32)
     _run(gpu, LA.gemm(xd.ptr, wd.ptr, cd.ptr, M, Nn, Kk, layout="nt", b_dtype=dt.float8_e4m3fn,
-                      c_dtype=dt.float32, scale_ptr=sd.ptr, pingpong=pp))
+                      c_dtype=dt.float32, scale_ptr=sd.ptr, **_kern(pp)))
     np.testing.assert_allclose(cd.numpy(), ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
 
 
-@pytest.mark.parametrize("pp", PP)
+@pytest.mark.parametrize("pp", PP8)
 def test_gemm_fp8_swiglu_nt(gpu, pp):
     M, F, Kk = 256, 256, 512
     rng = np.random.default_rng(12)
@@ -152,8 +158,46 @@ def test_gemm_fp8_swiglu_nt(gpu, pp):
     hd = DeviceTensor.empty((M, F), dt.bfloat16)
     _run(gpu, LA.gemm(t[0].ptr, t[1].ptr, hd.ptr, M, F, Kk, layout="nt", b_dtype=dt.float8_e4m3fn,
                       c_dtype=dt.bfloat16, scale_ptr=t[3].ptr, up_ptr=t[2].ptr, up_scale_ptr=t[4].ptr,
-                      pingpong=pp))
+                      **_kern(pp)))
     _close(dt.to_float32(hd.numpy()), ref)
+
+
+@pytest.mark.parametrize("shape", [(256, 256, 64), (300, 520, 208), (520, 272, 576), (64, 40, 16),
+                                   (1000, 768, 1000 // 16 * 16)])
+@pytest.mark.parametrize("variant", ["plain", "f32", "swiglu", "bias_resid"])
+def test_gemm_fp8_stage64_bit_exact(gpu, shape, variant):
+    """The 64-deep-stage kernel accumulates over k in the same order as the
+    32-deep one: outputs equal bit for bit, edge tiles and K tails included."""
+    M, Nn, Kk = shape
+    print(f"gemm fp8 stage64 {variant} M={M} N={Nn} K={Kk}", flush=True)
+    rng = np.random.default_rng(M + Nn + Kk)
+    x = _bf16(rng, (M, Kk))
+    w = (rng.standard_normal((Nn, Kk)) * 0.02).astype(np.float32)
+    codes, scale = N.quantize_per_channel_e4m3fn(w, axis=1)
+    xd = DeviceTensor.from_numpy(dt.to_bf16(x))
+    wd = DeviceTensor.from_numpy(codes.view(dt.float8_e4m3fn))
+    sd = DeviceTensor.from_numpy(scale.astype(np.float32))
+    kw = {"scale_ptr": sd.ptr}
+    keep = []
+    out_dt = dt.float32 if variant == "f32" else dt.bfloat16
+    n_out = Nn
+    if variant == "swiglu":
+        wu = (rng.standard_normal((Nn, Kk)) * 0.02).astype(np.float32)
+        cu, su = N.quantize_per_channel_e4m3fn(wu, axis=1)
+        keep = [DeviceTensor.from_numpy(cu.view(dt.float8_e4m3fn)), DeviceTensor.from_numpy(su.astype(np.float32))]
+        kw.update(up_ptr=keep[0].ptr, up_scale_ptr=keep[1].ptr)
+    if variant == "bias_resid":
+        keep = [DeviceTensor.from_numpy(dt.to_bf16(N.bf16_round(rng.standard_normal(Nn) * 0.1))),
+                DeviceTensor.from_numpy(dt.to_bf16(N.bf16_round(rng.standard_normal((M, Nn))))),]
+        kw.update(bias_ptr=keep[0].ptr, resid_ptr=keep[1].ptr, round_before_resid=True)
+    outs = []
+    for k64 in (False, True):
+        cd = DeviceTensor.empty((M, n_out), out_dt)
+        _run(gpu, LA.gemm(xd.ptr, wd.ptr, cd.ptr, M, Nn, Kk, layout="nt", b_dtype=dt.float8_e4m3fn,
+                          c_dtype=out_dt, stage64=k64, **kw))
+        outs.append(cd.numpy())
+    a, b = (dt.to_float32(o) if out_dt == dt.bfloat16 else o for o in outs)
+    np.testing.assert_array_equal(b, a)
 
 
 def test_fp8_decode_all_codes(gpu):
