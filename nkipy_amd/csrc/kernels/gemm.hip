@@ -52,6 +52,9 @@ enum {
   GEMM_VEC = 8,       // C / residual rows allow aligned 4-element vector access
   GEMM_RND_BIAS = 16, // round the (scaled) product to bf16 before the bias add
   GEMM_RND_RESID = 32,// round to bf16 before the residual add
+  GEMM_ROWS16 = 64,   // bf16 C / residual rows take aligned 16-byte chunks (N, ldc
+                      // multiples of 8) and a residual is added to a rounded value:
+                      // the 8-wave kernels may stage the output tile through LDS
 };
 // The rounding flags keep the cast points of the traced NumPy code: e.g.
 // ``z + (x @ w).astype(bf16)`` rounds the product before the add.
@@ -879,6 +882,78 @@ __device__ __forceinline__ void gemm_epilogue16(const GemmArgs &a, const f32x4 (
   }
 }
 
+// Epilogue through LDS (bf16 C, flag GEMM_ROWS16, the LDS ring idle): each
+// wave writes its converted values (scale, bias, SwiGLU; with a residual,
+// the value rounded to bf16 before the add, which is what is stored) into a
+// row-major tile T of 256 rows (padded by 16 bytes against bank conflicts);
+// then all 512 threads walk T in 16-byte chunks along the rows, add the
+// residual and store, so every global access covers whole cache lines
+// (the per-lane 8-byte stores of gemm_epilogue16 cover 32-byte row pieces,
+// four times as many requests).  Same arithmetic as gemm_epilogue16.
+template <bool SWIGLU, int NI>
+__device__ __forceinline__ void gemm_epilogue_lds(const GemmArgs &a, const f32x4 (&acc)[NI][8], int64_t m0,
+                                                  int64_t n0, int arow0, int bw0, int lane, uint8_t *T) {
+  constexpr int OC = SWIGLU ? 128 : 256;  // output columns of the tile
+  constexpr int TS = OC * 2 + 16;         // T row stride in bytes
+  constexpr int NJ = SWIGLU ? 4 : 8;
+  const int l16 = lane & 15, g4 = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int ct = bw0 + 16 * j + 4 * g4;
+    const int64_t col = n0 + ct;
+    float sc[4], su[4], bi[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool in = col + e < a.N;
+      sc[e] = ((a.flags & GEMM_SCALE) && in) ? a.scale0[col + e] : 1.f;
+      su[e] = (SWIGLU && (a.flags & GEMM_SCALE) && in) ? a.scale1[col + e] : 1.f;
+      bi[e] = (!SWIGLU && (a.flags & GEMM_BIAS) && in)
+                  ? bf16_to_f32(reinterpret_cast<const uint16_t *>(a.bias)[col + e]) : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (SWIGLU) {
+          const float g = acc[i][j][e] * sc[e];
+          const float u = acc[i][j + 4][e] * su[e];
+          const float ex = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+          v[e] = g * __builtin_amdgcn_rcpf(1.0f + ex) * u;
+        } else {
+          float prod = acc[i][j][e] * sc[e];
+          if (a.flags & GEMM_RND_BIAS) prod = bf16_to_f32(f32_to_bf16(prod));
+          v[e] = prod + bi[e];
+        }
+      }
+      const int rt = arow0 + 16 * i + l16;
+      *reinterpret_cast<uint2 *>(T + rt * TS + ct * 2) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    }
+  }
+  barrier_no_fence();
+  constexpr int CPR = OC / 8;  // 16-byte chunks per row
+  const bool res = (a.flags & GEMM_RESID) != 0;
+  for (int k = threadIdx.x; k < 256 * CPR; k += 512) {
+    const int rt = k / CPR, ch = k % CPR;
+    const int64_t row = m0 + rt, col = n0 + ch * 8;
+    if (row >= a.M || col >= a.N) continue;
+    uint4 w = *reinterpret_cast<const uint4 *>(T + rt * TS + ch * 16);
+    if (res) {
+      const uint4 r = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.resid) + row * a.ldc + col);
+      const uint32_t wv[4] = {w.x, w.y, w.z, w.w}, rv[4] = {r.x, r.y, r.z, r.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float lo = __uint_as_float(wv[q] << 16) + __uint_as_float(rv[q] << 16);
+        const float hi = __uint_as_float(wv[q] & 0xffff0000u) + __uint_as_float(rv[q] & 0xffff0000u);
+        o[q] = pack_bf16x2(lo, hi);
+      }
+      w = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.C) + row * a.ldc + col) = w;
+  }
+}
+
 // Epilogue of the rotary-embedding kernels: columns below rope_nq + rope_nk
 // are heads of 128 (q heads, then k heads), and a wave's 128 columns are one
 // head (cbase is a multiple of 128), so lane (g, i) holds frequency
@@ -1249,8 +1324,12 @@ __device__ __forceinline__ void gemm_pp_body(const GemmArgs &a) {
 __device__ __forceinline__ int swz_a64(int r) { return (r >> 1) & 7; }
 __device__ __forceinline__ int swz_b64(int r) { return (r >> 2) & 3; }
 
-template <bool SWIGLU, typename TC, bool ROPE = false>
+// R16: the kernel stages its bf16 output through LDS (gemm_epilogue_lds;
+// launched when the flag GEMM_ROWS16 holds).  A separate kernel, so that
+// one epilogue's live values do not add to the other's register pressure.
+template <bool SWIGLU, typename TC, bool ROPE = false, bool R16 = false>
 __device__ __forceinline__ void gemm_pp64_body(const GemmArgs &a) {
+  static_assert(!R16 || (sizeof(TC) == 2 && !ROPE), "the staged epilogue writes bf16");
   static_assert(!ROPE || (!SWIGLU && sizeof(TC) == 2), "the rotary epilogue writes bf16 projections");
   constexpr int R2 = 3;                         // ring stages
   constexpr int KB = 64;                        // k per stage
@@ -1356,7 +1435,10 @@ __device__ __forceinline__ void gemm_pp64_body(const GemmArgs &a) {
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  __shared__ __attribute__((aligned(1024))) uint8_t SG0[SS], SG1[SS], SG2[SS];
+  // one ring (the DMA is inline asm, which the compiler does not track, and
+  // the fragment reads go through opaque bases), reused by the epilogue
+  __shared__ __attribute__((aligned(1024))) uint8_t RING[R2 * SS];
+  uint8_t *const SG0 = RING, *const SG1 = RING + SS, *const SG2 = RING + 2 * SS;
   auto st = [&](auto stag) __attribute__((always_inline)) -> uint8_t * {
     constexpr int S = decltype(stag)::value;
     if constexpr (S == 0) return SG0; else if constexpr (S == 1) return SG1; else return SG2;
@@ -1417,6 +1499,10 @@ __device__ __forceinline__ void gemm_pp64_body(const GemmArgs &a) {
       gemm_epilogue_rope<4>(a, acc, m0 + arow0, n0 + bw0, lane);
       return;
     }
+  } else if constexpr (R16) {
+    barrier_no_fence();  // every wave's DMA has landed and its fragment reads are done: the ring is idle
+    gemm_epilogue_lds<SWIGLU, 4>(a, acc, m0, n0, arow0, bw0, lane, RING);
+    return;
   }
   gemm_epilogue16<SWIGLU, TC, 4>(a, acc, m0 + arow0, n0 + bw0, lane);
 }
@@ -1458,15 +1544,16 @@ NK_GEMM_PP(true, true, true, bf16, nk_gemm8_swiglu_nt_e4m3_bf16)
     gemm_pp_body<NT, FP8, false, bf16, true>(a);                                         \
   }
 
-#define NK_GEMM_K64(SW, TC, ROPE, name)                                                  \
+#define NK_GEMM_K64(SW, TC, ROPE, R16, name)                                             \
   extern "C" __global__ __launch_bounds__(512, 1) void name(GemmArgs a) {                \
-    gemm_pp64_body<SW, TC, ROPE>(a);                                                     \
+    gemm_pp64_body<SW, TC, ROPE, R16>(a);                                                \
   }
 
-NK_GEMM_K64(false, bf16, false, nk_gemm8k_nt_e4m3_bf16)
-NK_GEMM_K64(false, float, false, nk_gemm8k_nt_e4m3_f32)
-NK_GEMM_K64(true, bf16, false, nk_gemm8k_swiglu_nt_e4m3_bf16)
-NK_GEMM_K64(false, bf16, true, nk_gemm8k_nt_e4m3_bf16_rope)
+NK_GEMM_K64(false, bf16, false, false, nk_gemm8k_nt_e4m3_bf16)
+NK_GEMM_K64(false, float, false, false, nk_gemm8k_nt_e4m3_f32)
+NK_GEMM_K64(true, bf16, false, false, nk_gemm8k_swiglu_nt_e4m3_bf16)
+NK_GEMM_K64(false, bf16, true, false, nk_gemm8k_nt_e4m3_bf16_rope)
+NK_GEMM_K64(false, bf16, false, true, nk_gemm8k_nt_e4m3_bf16_r16)
 
 NK_GEMM_ROPE(false, false, nk_gemm8_nn_bf16_bf16_rope)
 NK_GEMM_ROPE(true, false, nk_gemm8_nt_bf16_bf16_rope)

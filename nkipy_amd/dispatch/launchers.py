@@ -251,6 +251,7 @@ GEMM_RESID = 4
 GEMM_VEC = 8
 GEMM_RND_BIAS = 16
 GEMM_RND_RESID = 32
+GEMM_ROWS16 = 64
 GEMM_BM = 256
 GEMM_BN = 256
 
@@ -329,6 +330,11 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
     vbytes = 4 * c_dtype.itemsize
     if ldc % 4 == 0 and c_ptr % vbytes == 0 and (not resid_ptr or resid_ptr % vbytes == 0):
         flags |= GEMM_VEC
+    # bf16 rows in aligned 16-byte chunks, a residual (if any) added to the
+    # bf16-rounded value: the output tile may be staged through LDS
+    if c_dtype == dt.bfloat16 and N % 8 == 0 and ldc % 8 == 0 and c_ptr % 16 == 0 and (
+            not resid_ptr or (round_before_resid and resid_ptr % 16 == 0)):
+        flags |= GEMM_ROWS16
     args = GemmArgs(a_ptr, b_ptr, up_ptr or None, c_ptr, bias_ptr or None, scale_ptr or None,
                     up_scale_ptr or None, resid_ptr or None, M, N, K, lda, ldb, ldc,
                     tiles_m, tiles_n, flags, 0)
@@ -366,6 +372,8 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
         symbol = f"{prefix}_swiglu_{layout}_{btag}_bf16"
     else:
         symbol = f"{prefix}_{layout}_{btag}_{ctag}" + ("_rope" if rope is not None else "")
+    if stage64 and rope is None and not swiglu and (flags & GEMM_ROWS16):
+        symbol += "_r16"  # the output tile staged through LDS
     n_mm = 2 if swiglu else 1
     nbytes = M * K * 2 + n_mm * N * K * b_dtype.itemsize + M * N * c_dtype.itemsize
     return Launch("gemm", symbol, (tiles_m * tiles_n, 1, 1), (512 if pingpong else 256, 1, 1), args,
