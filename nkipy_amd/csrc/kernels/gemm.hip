@@ -897,6 +897,10 @@ __device__ __forceinline__ void gemm_epilogue_lds(const GemmArgs &a, const f32x4
   constexpr int TS = OC * 2 + 16;         // T row stride in bytes
   constexpr int NJ = SWIGLU ? 4 : 8;
   const int l16 = lane & 15, g4 = lane >> 4;
+  // this lane's first T element (row arow0 + l16, column bw0 + 4 g4); tile
+  // (i, j) is at + i * 16 rows + j * 16 columns, immediates off one base
+  uint8_t *tb = T + (arow0 + l16) * TS + (bw0 + 4 * g4) * 2;
+  asm volatile("" : "+v"(tb));
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int ct = bw0 + 16 * j + 4 * g4;
@@ -926,8 +930,7 @@ __device__ __forceinline__ void gemm_epilogue_lds(const GemmArgs &a, const f32x4
           v[e] = prod + bi[e];
         }
       }
-      const int rt = arow0 + 16 * i + l16;
-      *reinterpret_cast<uint2 *>(T + rt * TS + ct * 2) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+      *reinterpret_cast<uint2 *>(tb + 16 * i * TS + 32 * j) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
     }
   }
   barrier_no_fence();
