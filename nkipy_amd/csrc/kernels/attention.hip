@@ -371,7 +371,341 @@ __device__ __forceinline__ void attention_causal_body(const AttnArgs &a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Software-pipelined variant.  Same operand layouts as above (S^T = K Q^T and
+// O^T = V^T P^T on 32x32x16 MFMAs, one query column per lane, the same K / V
+// swizzles), 32-key blocks, and rings of four LDS slots for K and for V.
+//
+// Iteration j issues, in one basic block, the score MFMAs of block j + 1 and
+// the P V MFMAs of block j - 1, interleaved with the softmax of block j on
+// the VALU: the matrix pipe stays fed while the wave evaluates its
+// exponentials, instead of the two phases following each other.  K of block
+// j + 4 and V of block j + 2 move into the slots freed by the previous
+// iteration, so each DMA has three iterations to land; one barrier per block.
+//
+// Softmax offset: p = 2^(s c - m) with c = scale log2(e) and a per-query
+// offset m that is not the running max.  m starts at the first block's max
+// and is raised (O and l rescaled, the block recomputed) only when some lane's
+// sum over its 16 scores of a block exceeds 2^16; otherwise no max is taken,
+// so the common block costs one fma, one exp, one add and half a convert per
+// score.  Every p stays below 2^16: nothing overflows, and since the output
+// is a ratio of sums of the same p, the offset does not change it.
+// ---------------------------------------------------------------------------
+#ifndef ATT_SP_SCHED
+#define ATT_SP_SCHED 1
+#endif
+
+template <int N> struct SlotTag {
+  static constexpr int value = N;
+};
+
+// LDS DMA issued from inline asm: the compiler does not model it, so it adds
+// no waits of its own before the reads of other ring slots (its alias
+// analysis cannot separate slots of one array); every wait is explicit.
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4_t rsrc_words(const void *p, int64_t bytes) {
+  const uint64_t ad = (uint64_t)p;
+  i32x4_t r;
+  r[0] = (int)(uint32_t)ad;
+  r[1] = (int)(uint32_t)(ad >> 32) & 0xffff;
+  r[2] = (int)bytes;
+  r[3] = 0x00020000;  // raw, untyped
+  return r;
+}
+// LDS byte address of a shared-memory array
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) { return (uint32_t)(uintptr_t)(lds_void *)p; }
+// lane l of the wave fills LDS byte address lds + 16 l from byte offset off
+// of the resource
+__device__ __forceinline__ void dma16_asm(i32x4_t r, uint32_t lds, uint32_t off) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :: "v"(off), "s"(r), "s"(m) : "memory", "m0");
+}
+
+template <int NW>
+__device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
+  constexpr int AQW = 32 * NW;  // queries per workgroup
+  constexpr int TB = 32 * AD * 2;  // one 32-key K or V tile
+  // one array per operand: a slot is a constant offset, so one address
+  // register per fragment serves all four slots
+  __shared__ __attribute__((aligned(1024))) uint8_t KR[4 * TB];
+  __shared__ __attribute__((aligned(1024))) uint8_t VR[4 * TB];
+  auto kslot = [&](auto t) __attribute__((always_inline)) -> uint8_t * {
+    return KR + (decltype(t)::value & 3) * TB;
+  };
+  auto vslot = [&](auto t) __attribute__((always_inline)) -> uint8_t * {
+    return VR + (decltype(t)::value & 3) * TB;
+  };
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l32 = lane & 31, lhi = lane >> 5;
+
+  // work item order as in attention_causal_body: contiguous ranges per XCD,
+  // longest query blocks of a KV head first
+  const int nqb = a.S / AQW;
+  const int rep = a.Hq / a.Hkv;
+  const int per_kv = rep * nqb;
+  const int nwg = a.B * a.Hkv * per_kv;
+  int w = blockIdx.x;
+  if ((nwg & 7) == 0) w = (w & 7) * (nwg >> 3) + (w >> 3);
+  const int bg = w / per_kv, within = w % per_kv;
+  const int qb = nqb - 1 - within / rep;
+  const int g = bg % a.Hkv, b = bg / a.Hkv;
+  const int h = g * rep + within % rep;
+  const int q0 = qb * AQW;
+
+  const uint16_t *qp = a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh;
+  const uint16_t *kp = a.k + (int64_t)b * a.k_sb + (int64_t)g * a.k_sh;
+  const uint16_t *vp = a.v + (int64_t)b * a.v_sb + (int64_t)g * a.v_sh;
+  uint16_t *op = a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
+  const i32x4_t rk = rsrc_words(kp, (int64_t)a.S * a.k_ss * 2);
+  const i32x4_t rv = rsrc_words(vp, (int64_t)a.S * a.v_ss * 2);
+
+  const int wq0 = q0 + wave * 32;
+  const int qrow = wq0 + l32;
+  bf16x8_t qf[AD / 16];
+#pragma unroll
+  for (int kk = 0; kk < AD / 16; ++kk)
+    qf[kk] = *reinterpret_cast<const bf16x8_t *>(qp + (int64_t)qrow * a.q_ss + kk * 16 + lhi * 8);
+
+  f32x16 acc_o[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_o[t][r] = 0.f;
+  // m: the softmax offset in log2 units, finite so that masked scores (-inf)
+  // give p = 0 and the first block (p = inf) always takes the recompute path
+  float m_run = -1e30f, l_run = 0.f;
+  const float sl2 = a.scale * 1.44269504088896340736f;
+
+  // key blocks: the workgroup's (the last wave's causal extent) and this wave's
+  const int nb_wg = a.causal ? (q0 + AQW) / 32 : a.S / 32;
+  const int nb_w = a.causal ? wq0 / 32 + 1 : a.S / 32;
+  // iterations 1 .. U-1 run for every wave with no mask: causal, block j + 1
+  // lies below the first wave's diagonal block q0 / 32
+  const int U = a.causal ? q0 / 32 : nb_wg - 1;
+  const int NIT = nb_wg + 1;  // iteration nb_wg adds the last block's P V
+
+  // DMA plan (as in attention_causal_body): a tile is 8 moves of 1 KiB
+  constexpr int NM = 32 / 4 / NW;
+  static_assert(NM >= 1 && NM * NW * 4 == 32, "moves per wave");
+  const int kchunk = (lane & 15) ^ kswz(wave * 4 + (lane >> 4));
+  const int vchunk = (lane & 15) ^ vswz(wave * 4 + (lane >> 4));
+  const int row0 = wave * 4 + (lane >> 4);
+  const uint32_t kbase = (uint32_t)(((int64_t)row0 * a.k_ss + kchunk * 8) * 2);
+  const uint32_t vbase = (uint32_t)(((int64_t)row0 * a.v_ss + vchunk * 8) * 2);
+  const uint32_t kjs = (uint32_t)(NW * 4 * a.k_ss * 2), vjs = (uint32_t)(NW * 4 * a.v_ss * 2);
+  const uint32_t k_lds = lds_addr(KR) + wave * 1024, v_lds = lds_addr(VR) + wave * 1024;
+  auto load_k = [&](auto sl, int kb) __attribute__((always_inline)) {
+    const uint32_t kst = (uint32_t)((int64_t)kb * 32 * a.k_ss * 2);
+#pragma unroll
+    for (int j = 0; j < NM; ++j)
+      dma16_asm(rk, k_lds + (decltype(sl)::value & 3) * TB + j * NW * 1024, kbase + j * kjs + kst);
+  };
+  auto load_v = [&](auto sl, int kb) __attribute__((always_inline)) {
+    const uint32_t vst = (uint32_t)((int64_t)kb * 32 * a.v_ss * 2);
+#pragma unroll
+    for (int j = 0; j < NM; ++j)
+      dma16_asm(rv, v_lds + (decltype(sl)::value & 3) * TB + j * NW * 1024, vbase + j * vjs + vst);
+  };
+  // wait until at most n of this wave's DMA moves are outstanding (the Q
+  // loads were issued before every move, so they are done by then too)
+  auto wait_moves = [&](auto ntag) __attribute__((always_inline)) {
+    constexpr int n = decltype(ntag)::value;
+    static_assert(n < 16, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | n);
+  };
+
+  const int klb = l32 * 256 + ((lhi ^ (l32 & 1)) << 4);
+  const int kx = (l32 & 14) << 4;
+  auto koff = [&](int kk) __attribute__((always_inline)) { return klb + ((kk << 5) ^ kx); };
+  int vlb, vx;
+  {
+    const int grp = lane >> 4, gi = lane & 15;
+    const int c0 = (grp & 1) * 2 + ((gi & 3) >> 1), vsh = (gi >> 2) & 3;
+    vlb = (4 * (grp >> 1) + (gi >> 2)) * 256 + (c0 << 4) + (gi & 1) * 8;
+    vx = vsh << 6;
+  }
+  auto voff = [&](int dt) __attribute__((always_inline)) { return vlb + ((dt << 6) ^ vx); };
+
+  // scores of one block: S^T = K Q^T
+  auto qk = [&](const uint8_t *Kt, f32x16 &s) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < AD / 16; ++kk) {
+      const bf16x8_t kf = *reinterpret_cast<const bf16x8_t *>(Kt + koff(kk));
+      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s, 0, 0, 0);
+    }
+  };
+  // O^T += V^T P^T for one block (P as two 16-key bf16 fragments)
+  auto pv = [&](const uint8_t *Vt, const bf16x8_t (&pf)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        s16x4 v[2];
+#pragma unroll
+        for (int si = 0; si < 2; ++si)
+          v[si] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(Vt + (16 * j + 8 * si) * 256 + voff(dt)));
+        const bf16x8_t vf = __builtin_shufflevector(__builtin_bit_cast(bf16x4_t, v[0]),
+                                                    __builtin_bit_cast(bf16x4_t, v[1]), 0, 1, 2, 3, 4, 5, 6, 7);
+        acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[j], acc_o[dt], 0, 0, 0);
+      }
+  };
+  // p = 2^(s c - m) of one block -> bf16 fragments; returns this lane's sum
+  auto expblock = [&](const f32x16 &s, bf16x8_t (&pf)[2]) __attribute__((always_inline)) {
+    float ps0 = 0.f, ps1 = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * j + e], sl2, -m_run));
+        if (e & 1) ps1 += p; else ps0 += p;
+        pf[j][e] = (__bf16)p;
+      }
+    return ps0 + ps1;
+  };
+  // the softmax of one block (scores s, key block kb); with MASK, keys past
+  // klim (the query itself when causal, else the last key) get p = 0
+  const int klim = a.causal ? qrow : a.S - 1;
+  auto softmax = [&](f32x16 &s, bf16x8_t (&pf)[2], int kb, auto masktag) __attribute__((always_inline)) {
+    if constexpr (decltype(masktag)::value) {
+      // element r holds key kb * 32 + 4 lhi + (8 (r / 4) + r % 4)
+      const int t = klim - kb * 32 - lhi * 4;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = ((r >> 2) * 8 + (r & 3)) > t ? -INFINITY : s[r];
+    }
+    float ls = expblock(s, pf);
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(ls <= 65536.f)) != 0, 0)) {
+      // raise m to the block max of the lane pair holding this query, rescale
+      // what has been accumulated, recompute the block
+      float bm = s[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) bm = fmaxf(bm, s[r]);
+      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+      const float m_new = fmaxf(m_run, bm * sl2);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_o[t][r] *= alpha;
+      l_run *= alpha;
+      ls = expblock(s, pf);
+    }
+    l_run += ls;
+  };
+
+  f32x16 sA, sB;
+  bf16x8_t pA[2], pB[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      pA[j][e] = (__bf16)0.f;
+      pB[j][e] = (__bf16)0.f;
+    }
+
+  // Iteration j (SL = j mod 4).  Register sets alternate with the parity of
+  // j: s_cur holds block j's scores, s_nxt receives block j + 1's; p_cur
+  // receives block j's P, p_prev holds block j - 1's.
+  auto iter = [&](auto sl, auto gen, int j, f32x16 &s_cur, f32x16 &s_nxt, bf16x8_t (&p_prev)[2],
+                  bf16x8_t (&p_cur)[2]) __attribute__((always_inline)) {
+    constexpr int SL = decltype(sl)::value;
+    constexpr bool GEN = decltype(gen)::value;
+    load_k(SlotTag<SL>{}, j + 4);
+    load_v(SlotTag<SL + 2>{}, j + 2);
+    const uint8_t *kn = kslot(SlotTag<SL + 1>{});
+    const uint8_t *vp_ = vslot(SlotTag<SL + 3>{});
+    if constexpr (!GEN) {
+      pv(vp_, p_prev);
+      qk(kn, s_nxt);
+      softmax(s_cur, p_cur, j, Flag<false>{});
+#if ATT_SP_SCHED
+      // order within the block: every LDS fragment read first, a few VALU
+      // ops while they land, then each MFMA followed by VALU work
+      __builtin_amdgcn_sched_group_barrier(0x100, 24, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+      }
+#endif
+    } else if (j <= nb_w) {
+      // the same body with the mask; blocks past this wave's last come out
+      // as p = 0 (their scores, computed anyway, are discarded)
+      qk(kn, s_nxt);
+      pv(vp_, p_prev);
+      softmax(s_cur, p_cur, j, Flag<true>{});
+    }
+    wait_moves(SlotTag<4 * NM>{});
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  // V slot 3 stands for block -1 in iteration 0 (P = 0 there): zero it so
+  // that product is exactly zero
+  {
+    uint4 *z = reinterpret_cast<uint4 *>(vslot(SlotTag<3>{}));
+    for (int i = threadIdx.x; i < TB / 16; i += 64 * NW) z[i] = make_uint4(0, 0, 0, 0);
+  }
+  // prologue: K of blocks 0..3 and V of blocks 0, 1 (in the order that lets
+  // each iteration's wait leave exactly the last two iterations' moves
+  // outstanding), then the scores of block 0
+  load_k(SlotTag<0>{}, 0);
+  load_k(SlotTag<1>{}, 1);
+  load_k(SlotTag<2>{}, 2);
+  load_v(SlotTag<0>{}, 0);
+  load_k(SlotTag<3>{}, 3);
+  load_v(SlotTag<1>{}, 1);
+  wait_moves(SlotTag<4 * NM>{});
+  __builtin_amdgcn_s_barrier();
+  qk(kslot(SlotTag<0>{}), sA);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): K0 reads done before its slot is refilled
+  __builtin_amdgcn_s_barrier();
+  iter(SlotTag<0>{}, Flag<true>{}, 0, sA, sB, pB, pA);
+  int j = 1;
+  for (; j + 4 <= U; j += 4) {
+    iter(SlotTag<1>{}, Flag<false>{}, j, sB, sA, pA, pB);
+    iter(SlotTag<2>{}, Flag<false>{}, j + 1, sA, sB, pB, pA);
+    iter(SlotTag<3>{}, Flag<false>{}, j + 2, sB, sA, pA, pB);
+    iter(SlotTag<0>{}, Flag<false>{}, j + 3, sA, sB, pB, pA);
+  }
+  // the rest, straight-line (j = 1 mod 4 here): fewer than four uniform
+  // iterations, the diagonal blocks and the last P V, at most NW + 4 in all,
+  // with the masked body
+  static_assert(NW == 4, "tail length");
+  if (j < NIT) iter(SlotTag<1>{}, Flag<true>{}, j, sB, sA, pA, pB);
+  if (j + 1 < NIT) iter(SlotTag<2>{}, Flag<true>{}, j + 1, sA, sB, pB, pA);
+  if (j + 2 < NIT) iter(SlotTag<3>{}, Flag<true>{}, j + 2, sB, sA, pA, pB);
+  if (j + 3 < NIT) iter(SlotTag<0>{}, Flag<true>{}, j + 3, sA, sB, pB, pA);
+  if (j + 4 < NIT) iter(SlotTag<1>{}, Flag<true>{}, j + 4, sB, sA, pA, pB);
+  if (j + 5 < NIT) iter(SlotTag<2>{}, Flag<true>{}, j + 5, sA, sB, pB, pA);
+  if (j + 6 < NIT) iter(SlotTag<3>{}, Flag<true>{}, j + 6, sB, sA, pA, pB);
+  if (j + 7 < NIT) iter(SlotTag<0>{}, Flag<true>{}, j + 7, sA, sB, pB, pA);
+  wait_moves(SlotTag<0>{});  // no LDS DMA outlives the workgroup
+
+  // normalise and store
+  const float inv_l = 1.0f / (l_run + __shfl_xor(l_run, 32, 64));
+  uint16_t *orow = op + (int64_t)qrow * a.o_ss;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const uint32_t w0 = pack_bf16x2(acc_o[t][gq * 4 + 0] * inv_l, acc_o[t][gq * 4 + 1] * inv_l);
+      const uint32_t w1 = pack_bf16x2(acc_o[t][gq * 4 + 2] * inv_l, acc_o[t][gq * 4 + 3] * inv_l);
+      *reinterpret_cast<uint2 *>(orow + t * 32 + gq * 8 + lhi * 4) = make_uint2(w0, w1);
+    }
+}
+
 // (launch bounds: threads per workgroup, minimum waves per SIMD)
+extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128_sp(AttnArgs a) {
+  attention_sp_body<4>(a);
+}
 extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(AttnArgs a) {
   attention_causal_body<4, 64, true>(a);
 }

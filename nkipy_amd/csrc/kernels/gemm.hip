@@ -1412,8 +1412,13 @@ __device__ __forceinline__ void gemm_pp64_body(const GemmArgs &a) {
   bf16x8_t af[4], bf[8];
   auto load = [&](const uint8_t *St, auto htag) __attribute__((always_inline)) {
     constexpr int H = decltype(htag)::value;
-    lds_u8 *pa = (lds_u8 *)St + (H ? (aoff0 ^ 64u) : aoff0);
-    lds_u8 *pb = (lds_u8 *)St + (H ? (boff0 ^ 32u) : boff0);
+    // the lane offsets pass through an empty asm first, so that stage base
+    // plus offset is formed here and not hoisted out of the loop (six
+    // loop-invariant sums would otherwise stay live across it)
+    uint32_t ao = H ? (aoff0 ^ 64u) : aoff0, bo = H ? (boff0 ^ 32u) : boff0;
+    asm volatile("" : "+v"(ao), "+v"(bo));
+    lds_u8 *pa = (lds_u8 *)St + ao;
+    lds_u8 *pb = (lds_u8 *)St + bo;
     asm volatile("" : "+v"(pa), "+v"(pb));
 #pragma unroll
     for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<lds_bf16x8 *>(pa + i * 2048);
@@ -1557,6 +1562,7 @@ NK_GEMM_K64(false, float, false, false, nk_gemm8k_nt_e4m3_f32)
 NK_GEMM_K64(true, bf16, false, false, nk_gemm8k_swiglu_nt_e4m3_bf16)
 NK_GEMM_K64(false, bf16, true, false, nk_gemm8k_nt_e4m3_bf16_rope)
 NK_GEMM_K64(false, bf16, false, true, nk_gemm8k_nt_e4m3_bf16_r16)
+NK_GEMM_K64(true, bf16, false, true, nk_gemm8k_swiglu_nt_e4m3_bf16_r16)
 
 NK_GEMM_ROPE(false, false, nk_gemm8_nn_bf16_bf16_rope)
 NK_GEMM_ROPE(true, false, nk_gemm8_nt_bf16_bf16_rope)

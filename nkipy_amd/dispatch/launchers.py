@@ -261,7 +261,7 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
          bias_ptr: int = 0, scale_ptr: int = 0, resid_ptr: int = 0,
          up_ptr: int = 0, up_scale_ptr: int = 0, pingpong: bool = None,
          round_before_bias: bool = False, round_before_resid: bool = False,
-         rope: GemmRope = None, stage64: bool = None) -> Launch:
+         rope: GemmRope = None, stage64: bool = None, staged: bool = None) -> Launch:
     """C[M, N] = A[M, K] @ B (+ epilogue) on bf16 MFMA, fp32 accumulation.
 
     ``layout`` "nn": B is K x N row-major (ldb >= N); "nt": B is N x K
@@ -278,7 +278,10 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
     (:class:`GemmRope`) selects the 8-wave kernel whose epilogue applies the
     rotary embedding to the q / k columns.  ``stage64`` (default: wherever
     it exists, i.e. fp8 NT weights on the 8-wave kernel) selects 64-deep K
-    stages in LDS (whole 128-byte lines per global read).
+    stages in LDS (whole 128-byte lines per global read).  ``staged``
+    (default: wherever it applies, i.e. 64-deep stages without the rotary
+    epilogue and a bf16 output in aligned 16-byte row chunks) writes the
+    output tile through LDS so that every global store covers whole lines.
     """
     if layout not in ("nn", "nt"):
         raise LaunchError(f"unknown GEMM layout {layout}")
@@ -372,7 +375,13 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
         symbol = f"{prefix}_swiglu_{layout}_{btag}_bf16"
     else:
         symbol = f"{prefix}_{layout}_{btag}_{ctag}" + ("_rope" if rope is not None else "")
-    if stage64 and rope is None and not swiglu and (flags & GEMM_ROWS16):
+    can_stage = bool(stage64 and rope is None and (flags & GEMM_ROWS16))
+    if staged is None:
+        staged = can_stage
+    if staged and not can_stage:
+        raise LaunchError("the staged epilogue needs 64-deep stages, no rotary epilogue and a bf16 output "
+                          "in aligned 16-byte row chunks (a residual added after the bf16 rounding)")
+    if staged:
         symbol += "_r16"  # the output tile staged through LDS
     n_mm = 2 if swiglu else 1
     nbytes = M * K * 2 + n_mm * N * K * b_dtype.itemsize + M * N * c_dtype.itemsize
@@ -485,13 +494,14 @@ class AttnArgs(ctypes.Structure):
 
 def attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, B: int, S: int, Hq: int, Hkv: int,
               D: int, scale: float, strides: dict, causal: bool = True, waves: int = None,
-              key_block: int = None) -> Launch:
+              key_block: int = None, ring: bool = None) -> Launch:
     """Flash-style attention over bf16 q (B, S, Hq, D), k / v (B, S, Hkv, D) and
     o (B, S, Hq, D), each addressed by element strides {"q": (sb, ss, sh), ...}
     with the head dim contiguous.  KV head of query head h is h // (Hq // Hkv).
     ``waves`` (4 or 8) waves of 32 queries share a workgroup's K / V tiles;
     ``key_block`` (64 or 32) keys per step.  Variants: (4, 64), (8, 64) and
-    (4, 32), the last with three workgroups per CU."""
+    (4, 32), the last with three workgroups per CU; ``ring`` selects the
+    software-pipelined (4, 32) kernel over a four-slot K / V ring."""
     if D != 128:
         raise LaunchError(f"attention kernel is built for head_dim 128, got {D}")
     if S % 128 or S <= 0:
@@ -518,7 +528,12 @@ def attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, B: int, S: int, Hq
     # (4, 64) and 326 us for (8, 64)
     waves = 4 if waves is None else waves
     key_block = 32 if key_block is None else key_block
-    suffix = {(4, 64): "", (8, 64): "_w8", (4, 32): "_k32"}.get((waves, key_block))
+    # default: the ring kernel (4 waves, 32-key blocks, software pipelined
+    # over a four-slot K / V ring); explicit (waves, key_block) pick the others
+    ring = (waves, key_block) == (4, 32) if ring is None else ring
+    if ring and (waves, key_block) != (4, 32):
+        raise LaunchError("the ring attention kernel runs 4 waves over 32-key blocks")
+    suffix = "_sp" if ring else {(4, 64): "", (8, 64): "_w8", (4, 32): "_k32"}.get((waves, key_block))
     if suffix is None:
         raise LaunchError(f"no attention variant with {waves} waves and {key_block}-key blocks")
     if S % (32 * waves):

@@ -43,19 +43,43 @@ def test_attention_small(gpu, shape):
     _close(_run(gpu, q, k, v), K.causal_gqa_attention(q, k, v))
 
 
-@pytest.mark.parametrize("waves,key_block", [(4, 64), (8, 64), (4, 32)])
+@pytest.mark.parametrize("waves,key_block,ring", [(4, 64, False), (8, 64, False), (4, 32, False), (4, 32, True)])
 @pytest.mark.parametrize("causal", [True, False])
-@pytest.mark.parametrize("shape", [(1, 256, 4, 1), (2, 512, 8, 2), (1, 768, 2, 2)])
-def test_attention_variants(gpu, waves, key_block, causal, shape):
-    """Every kernel variant (waves per workgroup, keys per block), masked and
-    unmasked, including the diagonal blocks a workgroup's waves skip."""
+@pytest.mark.parametrize("shape", [(1, 128, 1, 1), (1, 256, 4, 1), (2, 512, 8, 2), (1, 768, 2, 2),
+                                   (1, 1152, 2, 1)])
+def test_attention_variants(gpu, waves, key_block, ring, causal, shape):
+    """Every kernel variant (waves per workgroup, keys per block, the
+    four-slot ring), masked and unmasked, including the diagonal blocks a
+    workgroup's waves skip and sequences whose block counts leave every
+    remainder of the ring kernel's four-way unrolled loop."""
     B, S, Hq, Hkv = shape
-    print(f"attention variant waves={waves} key_block={key_block} causal={causal} shape={shape}", flush=True)
+    if S % (32 * waves):
+        pytest.skip(f"{waves} waves take query blocks of {32 * waves}")
+    print(f"attention variant waves={waves} key_block={key_block} ring={ring} causal={causal} shape={shape}",
+          flush=True)
     rng = np.random.default_rng(S + Hq + waves + key_block)
     q = N.bf16_round(rng.standard_normal((B, S, Hq, 128)))
     k = N.bf16_round(rng.standard_normal((B, S, Hkv, 128)))
     v = N.bf16_round(rng.standard_normal((B, S, Hkv, 128)))
-    got = _run(gpu, q, k, v, causal=causal, waves=waves, key_block=key_block)
+    got = _run(gpu, q, k, v, causal=causal, waves=waves, key_block=key_block, ring=ring)
+    _close(got, K.causal_gqa_attention(q, k, v, causal=causal))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_ring_offset_raised(gpu, causal):
+    """Scores that grow along the keys (q . k rises with the key index) make
+    later blocks exceed the first block's offset by far more than 2^16, so the
+    ring kernel's recompute path (offset raised, O and l rescaled) runs on
+    many blocks; the result still matches the float64 softmax."""
+    B, S, Hq, Hkv = 1, 512, 2, 1
+    rng = np.random.default_rng(7)
+    q = np.abs(rng.standard_normal((B, S, Hq, 128))) * 0.3 + 0.2
+    ramp = np.linspace(0.0, 8.0, S)[None, :, None, None]
+    k = (np.abs(rng.standard_normal((B, S, Hkv, 128))) * 0.3 + 0.2) * ramp
+    q, k = N.bf16_round(q), N.bf16_round(k)
+    v = N.bf16_round(rng.standard_normal((B, S, Hkv, 128)))
+    print(f"ring offset raised causal={causal}", flush=True)
+    got = _run(gpu, q, k, v, causal=causal, ring=True)
     _close(got, K.causal_gqa_attention(q, k, v, causal=causal))
 
 

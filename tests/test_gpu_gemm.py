@@ -191,13 +191,16 @@ def test_gemm_fp8_stage64_bit_exact(gpu, shape, variant):
                 DeviceTensor.from_numpy(dt.to_bf16(N.bf16_round(rng.standard_normal((M, Nn))))),]
         kw.update(bias_ptr=keep[0].ptr, resid_ptr=keep[1].ptr, round_before_resid=True)
     outs = []
-    for k64 in (False, True):
+    # 32-deep kernel; 64-deep with the direct epilogue; 64-deep with the
+    # output staged through LDS (where the output allows it)
+    runs = [(False, None), (True, False)] + ([(True, True)] if out_dt == dt.bfloat16 else [])
+    for k64, staged in runs:
         cd = DeviceTensor.empty((M, n_out), out_dt)
         _run(gpu, LA.gemm(xd.ptr, wd.ptr, cd.ptr, M, Nn, Kk, layout="nt", b_dtype=dt.float8_e4m3fn,
-                          c_dtype=out_dt, stage64=k64, **kw))
-        outs.append(cd.numpy())
-    a, b = (dt.to_float32(o) if out_dt == dt.bfloat16 else o for o in outs)
-    np.testing.assert_array_equal(b, a)
+                          c_dtype=out_dt, stage64=k64, staged=staged, **kw))
+        outs.append(dt.to_float32(cd.numpy()) if out_dt == dt.bfloat16 else cd.numpy())
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])
 
 
 def test_fp8_decode_all_codes(gpu):
