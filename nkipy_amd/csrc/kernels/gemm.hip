@@ -1021,6 +1021,92 @@ __device__ __forceinline__ void gemm_epilogue_rope(const GemmArgs &a, const f32x
   }
 }
 
+// The rotary epilogue staged through LDS (the ring idle): each wave writes
+// its head -- rotated as in gemm_epilogue_rope for q / k heads, the scaled
+// projection for value columns -- as bf16 into a row-major tile T (256 rows,
+// padded by 16 bytes), then all 512 threads move 16-byte row chunks to
+// rope_q, rope_k or C by column, so every global store covers whole lines.
+// Same arithmetic as gemm_epilogue_rope / gemm_epilogue16.
+template <int NI>
+__device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmArgs &a, const f32x4 (&acc)[NI][8], int64_t m0,
+                                                       int64_t n0, int arow0, int bw0, int lane, uint8_t *T) {
+  constexpr int TS = 256 * 2 + 16;  // T row stride in bytes
+  const int l16 = lane & 15, g4 = lane >> 4;
+  uint8_t *tb = T + (arow0 + l16) * TS + (bw0 + 4 * g4) * 2;
+  asm volatile("" : "+v"(tb));
+  const int64_t cbase = n0 + bw0;  // this wave's 128 columns: one head
+  const bool scaled = (a.flags & GEMM_SCALE) != 0;
+  if (cbase < (int64_t)a.rope_nq + a.rope_nk) {
+    int64_t toff[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int64_t row = m0 + arow0 + 16 * i + l16;
+      toff[i] = (row < a.M ? (int64_t)((int32_t)row % a.rope_seq) : 0) * a.rope_ts + 4 * g4;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = 16 * j + 4 * g4;
+      float s0[4], s1[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s0[e] = scaled ? a.scale0[cbase + d + e] : 1.f;
+        s1[e] = scaled ? a.scale0[cbase + 64 + d + e] : 1.f;
+      }
+      float4 c[NI], sn[NI];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        c[i] = *reinterpret_cast<const float4 *>(a.rope_cos + toff[i] + 16 * j);
+        sn[i] = *reinterpret_cast<const float4 *>(a.rope_sin + toff[i] + 16 * j);
+      }
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const float cv[4] = {c[i].x, c[i].y, c[i].z, c[i].w}, sv[4] = {sn[i].x, sn[i].y, sn[i].z, sn[i].w};
+        float y0[4], y1[4];
+        {
+#pragma clang fp contract(off)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float x0 = bf16_to_f32(f32_to_bf16(acc[i][j][e] * s0[e]));
+            const float x1 = bf16_to_f32(f32_to_bf16(acc[i][j + 4][e] * s1[e]));
+            y0[e] = x0 * cv[e] - x1 * sv[e];
+            y1[e] = x0 * sv[e] + x1 * cv[e];
+          }
+        }
+        *reinterpret_cast<uint2 *>(tb + 16 * i * TS + 32 * j) =
+            make_uint2(pack_bf16x2(y0[0], y0[1]), pack_bf16x2(y0[2], y0[3]));
+        *reinterpret_cast<uint2 *>(tb + 16 * i * TS + 32 * (j + 4)) =
+            make_uint2(pack_bf16x2(y1[0], y1[1]), pack_bf16x2(y1[2], y1[3]));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t col = cbase + 16 * j + 4 * g4;
+      float sc[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sc[e] = (scaled && col + e < a.N) ? a.scale0[col + e] : 1.f;
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        *reinterpret_cast<uint2 *>(tb + 16 * i * TS + 32 * j) =
+            make_uint2(pack_bf16x2(acc[i][j][0] * sc[0], acc[i][j][1] * sc[1]),
+                       pack_bf16x2(acc[i][j][2] * sc[2], acc[i][j][3] * sc[3]));
+    }
+  }
+  barrier_no_fence();
+  constexpr int CPR = 32;  // 16-byte chunks per tile row
+  const int64_t nrot = (int64_t)a.rope_nq + a.rope_nk;
+  for (int k = threadIdx.x; k < 256 * CPR; k += 512) {
+    const int rt = k / CPR, ch = k % CPR;
+    const int64_t row = m0 + rt, col = n0 + ch * 8;
+    if (row >= a.M || col >= a.N) continue;
+    const uint4 w = *reinterpret_cast<const uint4 *>(T + rt * TS + ch * 16);
+    uint16_t *dst = col < a.rope_nq ? reinterpret_cast<uint16_t *>(a.rope_q) + row * a.rope_nq + col
+                    : col < nrot   ? reinterpret_cast<uint16_t *>(a.rope_k) + row * a.rope_nk + (col - a.rope_nq)
+                                   : reinterpret_cast<uint16_t *>(a.C) + row * a.ldc + col;
+    *reinterpret_cast<uint4 *>(dst) = w;
+  }
+}
+
 // LDS DMA issued as inline asm: the compiler's wait insertion does not model
 // it, so it adds no waits of its own for it; every ordering is explicit
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
@@ -1332,7 +1418,7 @@ __device__ __forceinline__ int swz_b64(int r) { return (r >> 2) & 3; }
 // one epilogue's live values do not add to the other's register pressure.
 template <bool SWIGLU, typename TC, bool ROPE = false, bool R16 = false>
 __device__ __forceinline__ void gemm_pp64_body(const GemmArgs &a) {
-  static_assert(!R16 || (sizeof(TC) == 2 && !ROPE), "the staged epilogue writes bf16");
+  static_assert(!R16 || sizeof(TC) == 2, "the staged epilogue writes bf16");
   static_assert(!ROPE || (!SWIGLU && sizeof(TC) == 2), "the rotary epilogue writes bf16 projections");
   constexpr int R2 = 3;                         // ring stages
   constexpr int KB = 64;                        // k per stage
@@ -1502,7 +1588,11 @@ __device__ __forceinline__ void gemm_pp64_body(const GemmArgs &a) {
   else
     run(Int<1>{});
   wait_vmem();
-  if constexpr (ROPE) {
+  if constexpr (ROPE && R16) {
+    barrier_no_fence();  // the ring is idle
+    gemm_epilogue_rope_lds<4>(a, acc, m0, n0, arow0, bw0, lane, RING);
+    return;
+  } else if constexpr (ROPE) {
     if (n0 + bw0 < (int64_t)a.rope_nq + a.rope_nk) {
       gemm_epilogue_rope<4>(a, acc, m0 + arow0, n0 + bw0, lane);
       return;
@@ -1563,6 +1653,7 @@ NK_GEMM_K64(true, bf16, false, false, nk_gemm8k_swiglu_nt_e4m3_bf16)
 NK_GEMM_K64(false, bf16, true, false, nk_gemm8k_nt_e4m3_bf16_rope)
 NK_GEMM_K64(false, bf16, false, true, nk_gemm8k_nt_e4m3_bf16_r16)
 NK_GEMM_K64(true, bf16, false, true, nk_gemm8k_swiglu_nt_e4m3_bf16_r16)
+NK_GEMM_K64(false, bf16, true, true, nk_gemm8k_nt_e4m3_bf16_rope_r16)
 
 NK_GEMM_ROPE(false, false, nk_gemm8_nn_bf16_bf16_rope)
 NK_GEMM_ROPE(true, false, nk_gemm8_nt_bf16_bf16_rope)

@@ -279,9 +279,9 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
     rotary embedding to the q / k columns.  ``stage64`` (default: wherever
     it exists, i.e. fp8 NT weights on the 8-wave kernel) selects 64-deep K
     stages in LDS (whole 128-byte lines per global read).  ``staged``
-    (default: wherever it applies, i.e. 64-deep stages without the rotary
-    epilogue and a bf16 output in aligned 16-byte row chunks) writes the
-    output tile through LDS so that every global store covers whole lines.
+    (default: wherever it applies, i.e. 64-deep stages and a bf16 output in
+    aligned 16-byte row chunks) writes the output tile through LDS so that
+    every global store covers whole lines.
     """
     if layout not in ("nn", "nt"):
         raise LaunchError(f"unknown GEMM layout {layout}")
@@ -375,12 +375,13 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
         symbol = f"{prefix}_swiglu_{layout}_{btag}_bf16"
     else:
         symbol = f"{prefix}_{layout}_{btag}_{ctag}" + ("_rope" if rope is not None else "")
-    can_stage = bool(stage64 and rope is None and (flags & GEMM_ROWS16))
+    can_stage = bool(stage64 and (flags & GEMM_ROWS16) and (
+        rope is None or (rope.q_ptr % 16 == 0 and rope.k_ptr % 16 == 0)))
     if staged is None:
         staged = can_stage
     if staged and not can_stage:
-        raise LaunchError("the staged epilogue needs 64-deep stages, no rotary epilogue and a bf16 output "
-                          "in aligned 16-byte row chunks (a residual added after the bf16 rounding)")
+        raise LaunchError("the staged epilogue needs 64-deep stages and a bf16 output in aligned 16-byte row "
+                          "chunks (a residual added after the bf16 rounding; 16-byte aligned rotary outputs)")
     if staged:
         symbol += "_r16"  # the output tile staged through LDS
     n_mm = 2 if swiglu else 1

@@ -290,3 +290,33 @@ def test_traced_residual_keeps_cast_points(gpu):
     # without the rounding of the product, most elements would be off
     unrounded = N.bf16_round(z + p)
     assert np.mean(unrounded != ref) > 0.2
+
+
+@pytest.mark.parametrize("M,seq,nq,nk,nv,K", [(300, 100, 1024, 128, 128, 512), (256, 64, 128, 128, 256, 256),
+                                             (520, 130, 384, 256, 128, 192)])
+def test_gemm_rope_staged_bit_exact(gpu, M, seq, nq, nk, nv, K):
+    """The rotary epilogue staged through LDS equals the direct one bit for
+    bit, on tiles that mix q / k or k / v heads, on edge rows and columns."""
+    print(f"gemm rope staged M={M} seq={seq} nq={nq} nk={nk} nv={nv} K={K}", flush=True)
+    NC = nq + nk + nv
+    rng = np.random.default_rng(M + NC + K)
+    x = _bf16(rng, (M, K))
+    w = (rng.standard_normal((NC, K)) * 0.02).astype(np.float32)
+    codes, scale = N.quantize_per_channel_e4m3fn(w, axis=1)
+    ang = np.arange(seq)[:, None] * (5.0e5 ** (-np.arange(64) / 64.0))[None, :]
+    cos = DeviceTensor.from_numpy(np.cos(ang).astype(np.float32))
+    sin = DeviceTensor.from_numpy(np.sin(ang).astype(np.float32))
+    xd = DeviceTensor.from_numpy(dt.to_bf16(x))
+    wd = DeviceTensor.from_numpy(codes.view(dt.float8_e4m3fn))
+    sd = DeviceTensor.from_numpy(scale.astype(np.float32))
+    outs = []
+    for staged in (False, True):
+        q = DeviceTensor.empty((M, nq), dt.bfloat16)
+        k = DeviceTensor.empty((M, nk), dt.bfloat16)
+        c = DeviceTensor.from_numpy(np.zeros((M, NC), dtype=dt.bfloat16))
+        rope = LA.GemmRope(cos.ptr, sin.ptr, q.ptr, k.ptr, 64, seq, nq, nk)
+        _run(gpu, LA.gemm(xd.ptr, wd.ptr, c.ptr, M, NC, K, layout="nt", b_dtype=dt.float8_e4m3fn,
+                          c_dtype=dt.bfloat16, scale_ptr=sd.ptr, rope=rope, staged=staged))
+        outs.append([dt.to_float32(t.numpy()) for t in (q, k)] + [dt.to_float32(c.numpy())[:, nq + nk:]])
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(b, a)
