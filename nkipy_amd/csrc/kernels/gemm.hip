@@ -890,6 +890,22 @@ __device__ __forceinline__ void gemm_epilogue16(const GemmArgs &a, const f32x4 (
 // residual and store, so every global access covers whole cache lines
 // (the per-lane 8-byte stores of gemm_epilogue16 cover 32-byte row pieces,
 // four times as many requests).  Same arithmetic as gemm_epilogue16.
+typedef __attribute__((address_space(3))) uint8_t lds_b;
+typedef unsigned lds_u32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned lds_u32x4_t __attribute__((ext_vector_type(4)));
+// 8-byte store / 16-byte load through an LDS-typed pointer (ds_write_b64 /
+// ds_read_b128 rather than the flat forms a generic pointer would give)
+__device__ __forceinline__ void lds_st8(lds_b *p, uint32_t lo, uint32_t hi) {
+  lds_u32x2_t v;
+  v.x = lo;
+  v.y = hi;
+  *reinterpret_cast<__attribute__((address_space(3))) lds_u32x2_t *>(p) = v;
+}
+__device__ __forceinline__ uint4 lds_ld16(const lds_b *p) {
+  const lds_u32x4_t v = *reinterpret_cast<const __attribute__((address_space(3))) lds_u32x4_t *>(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 template <bool SWIGLU, int NI>
 __device__ __forceinline__ void gemm_epilogue_lds(const GemmArgs &a, const f32x4 (&acc)[NI][8], int64_t m0,
                                                   int64_t n0, int arow0, int bw0, int lane, uint8_t *T) {
@@ -899,7 +915,9 @@ __device__ __forceinline__ void gemm_epilogue_lds(const GemmArgs &a, const f32x4
   const int l16 = lane & 15, g4 = lane >> 4;
   // this lane's first T element (row arow0 + l16, column bw0 + 4 g4); tile
   // (i, j) is at + i * 16 rows + j * 16 columns, immediates off one base
-  uint8_t *tb = T + (arow0 + l16) * TS + (bw0 + 4 * g4) * 2;
+  // (an LDS-typed pointer, so the accesses are ds_* and not flat)
+  lds_b *const TL = (lds_b *)T;
+  lds_b *tb = TL + (arow0 + l16) * TS + (bw0 + 4 * g4) * 2;
   asm volatile("" : "+v"(tb));
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
@@ -930,20 +948,38 @@ __device__ __forceinline__ void gemm_epilogue_lds(const GemmArgs &a, const f32x4
           v[e] = prod + bi[e];
         }
       }
-      *reinterpret_cast<uint2 *>(tb + 16 * i * TS + 32 * j) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+      lds_st8(tb + 16 * i * TS + 32 * j, pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
     }
   }
   barrier_no_fence();
-  constexpr int CPR = OC / 8;  // 16-byte chunks per row
+  // every read (the tile's chunks from LDS, the residual's from memory) is
+  // issued before the first store: a store may alias the residual (C may be
+  // the residual buffer), so reads interleaved with the stores would each
+  // wait a full memory latency.  Each thread reads only the residual chunks
+  // it writes, so reading them all first is exact.
+  constexpr int CPR = OC / 8;           // 16-byte chunks per row
+  constexpr int NIT = 256 * CPR / 512;  // chunks per thread
   const bool res = (a.flags & GEMM_RESID) != 0;
-  for (int k = threadIdx.x; k < 256 * CPR; k += 512) {
+  uint4 w[NIT], r[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int k = threadIdx.x + 512 * it;
+    const int rt = k / CPR, ch = k % CPR;
+    const int64_t row = m0 + rt, col = n0 + ch * 8;
+    w[it] = lds_ld16(TL + rt * TS + ch * 16);
+    r[it] = make_uint4(0, 0, 0, 0);
+    if (res && row < a.M && col < a.N)
+      r[it] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.resid) + row * a.ldc + col);
+  }
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int k = threadIdx.x + 512 * it;
     const int rt = k / CPR, ch = k % CPR;
     const int64_t row = m0 + rt, col = n0 + ch * 8;
     if (row >= a.M || col >= a.N) continue;
-    uint4 w = *reinterpret_cast<const uint4 *>(T + rt * TS + ch * 16);
+    uint4 v = w[it];
     if (res) {
-      const uint4 r = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.resid) + row * a.ldc + col);
-      const uint32_t wv[4] = {w.x, w.y, w.z, w.w}, rv[4] = {r.x, r.y, r.z, r.w};
+      const uint32_t wv[4] = {v.x, v.y, v.z, v.w}, rv[4] = {r[it].x, r[it].y, r[it].z, r[it].w};
       uint32_t o[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -951,9 +987,9 @@ __device__ __forceinline__ void gemm_epilogue_lds(const GemmArgs &a, const f32x4
         const float hi = __uint_as_float(wv[q] & 0xffff0000u) + __uint_as_float(rv[q] & 0xffff0000u);
         o[q] = pack_bf16x2(lo, hi);
       }
-      w = make_uint4(o[0], o[1], o[2], o[3]);
+      v = make_uint4(o[0], o[1], o[2], o[3]);
     }
-    *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.C) + row * a.ldc + col) = w;
+    *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.C) + row * a.ldc + col) = v;
   }
 }
 
@@ -1032,7 +1068,8 @@ __device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmArgs &a, const 
                                                        int64_t n0, int arow0, int bw0, int lane, uint8_t *T) {
   constexpr int TS = 256 * 2 + 16;  // T row stride in bytes
   const int l16 = lane & 15, g4 = lane >> 4;
-  uint8_t *tb = T + (arow0 + l16) * TS + (bw0 + 4 * g4) * 2;
+  lds_b *const TL = (lds_b *)T;  // ds_* accesses, not flat
+  lds_b *tb = TL + (arow0 + l16) * TS + (bw0 + 4 * g4) * 2;
   asm volatile("" : "+v"(tb));
   const int64_t cbase = n0 + bw0;  // this wave's 128 columns: one head
   const bool scaled = (a.flags & GEMM_SCALE) != 0;
@@ -1072,10 +1109,8 @@ __device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmArgs &a, const 
             y1[e] = x0 * sv[e] + x1 * cv[e];
           }
         }
-        *reinterpret_cast<uint2 *>(tb + 16 * i * TS + 32 * j) =
-            make_uint2(pack_bf16x2(y0[0], y0[1]), pack_bf16x2(y0[2], y0[3]));
-        *reinterpret_cast<uint2 *>(tb + 16 * i * TS + 32 * (j + 4)) =
-            make_uint2(pack_bf16x2(y1[0], y1[1]), pack_bf16x2(y1[2], y1[3]));
+        lds_st8(tb + 16 * i * TS + 32 * j, pack_bf16x2(y0[0], y0[1]), pack_bf16x2(y0[2], y0[3]));
+        lds_st8(tb + 16 * i * TS + 32 * (j + 4), pack_bf16x2(y1[0], y1[1]), pack_bf16x2(y1[2], y1[3]));
       }
     }
   } else {
@@ -1087,19 +1122,27 @@ __device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmArgs &a, const 
       for (int e = 0; e < 4; ++e) sc[e] = (scaled && col + e < a.N) ? a.scale0[col + e] : 1.f;
 #pragma unroll
       for (int i = 0; i < NI; ++i)
-        *reinterpret_cast<uint2 *>(tb + 16 * i * TS + 32 * j) =
-            make_uint2(pack_bf16x2(acc[i][j][0] * sc[0], acc[i][j][1] * sc[1]),
-                       pack_bf16x2(acc[i][j][2] * sc[2], acc[i][j][3] * sc[3]));
+        lds_st8(tb + 16 * i * TS + 32 * j, pack_bf16x2(acc[i][j][0] * sc[0], acc[i][j][1] * sc[1]),
+                pack_bf16x2(acc[i][j][2] * sc[2], acc[i][j][3] * sc[3]));
     }
   }
   barrier_no_fence();
-  constexpr int CPR = 32;  // 16-byte chunks per tile row
+  constexpr int CPR = 32;               // 16-byte chunks per tile row
+  constexpr int NIT = 256 * CPR / 512;  // chunks per thread
   const int64_t nrot = (int64_t)a.rope_nq + a.rope_nk;
-  for (int k = threadIdx.x; k < 256 * CPR; k += 512) {
+  uint4 wt[NIT];  // every LDS read issued before the first store
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int k = threadIdx.x + 512 * it;
+    wt[it] = lds_ld16(TL + (k / CPR) * TS + (k % CPR) * 16);
+  }
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int k = threadIdx.x + 512 * it;
     const int rt = k / CPR, ch = k % CPR;
     const int64_t row = m0 + rt, col = n0 + ch * 8;
     if (row >= a.M || col >= a.N) continue;
-    const uint4 w = *reinterpret_cast<const uint4 *>(T + rt * TS + ch * 16);
+    const uint4 w = wt[it];
     uint16_t *dst = col < a.rope_nq ? reinterpret_cast<uint16_t *>(a.rope_q) + row * a.rope_nq + col
                     : col < nrot   ? reinterpret_cast<uint16_t *>(a.rope_k) + row * a.rope_nk + (col - a.rope_nq)
                                    : reinterpret_cast<uint16_t *>(a.C) + row * a.ldc + col;
