@@ -394,6 +394,9 @@ __device__ __forceinline__ void attention_causal_body(const AttnArgs &a) {
 #ifndef ATT_SP_SCHED
 #define ATT_SP_SCHED 1
 #endif
+#ifndef ATT_SP_DMA_LATE
+#define ATT_SP_DMA_LATE 1
+#endif
 
 template <int N> struct SlotTag {
   static constexpr int value = N;
@@ -615,8 +618,10 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
                   bf16x8_t (&p_cur)[2]) __attribute__((always_inline)) {
     constexpr int SL = decltype(sl)::value;
     constexpr bool GEN = decltype(gen)::value;
+#if !ATT_SP_DMA_LATE
     load_k(SlotTag<SL>{}, j + 4);
     load_v(SlotTag<SL + 2>{}, j + 2);
+#endif
     const uint8_t *kn = kslot(SlotTag<SL + 1>{});
     const uint8_t *vp_ = vslot(SlotTag<SL + 3>{});
     if constexpr (!GEN) {
@@ -641,6 +646,12 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
       pv(vp_, p_prev);
       softmax(s_cur, p_cur, j, Flag<true>{});
     }
+#if ATT_SP_DMA_LATE
+    // after the block's MFMAs: a vector memory instruction that waits at
+    // issue then holds up no MFMA of this wave
+    load_k(SlotTag<SL>{}, j + 4);
+    load_v(SlotTag<SL + 2>{}, j + 2);
+#endif
     wait_moves(SlotTag<4 * NM>{});
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -678,7 +689,7 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
   // the rest, straight-line (j = 1 mod 4 here): fewer than four uniform
   // iterations, the diagonal blocks and the last P V, at most NW + 4 in all,
   // with the masked body
-  static_assert(NW == 4, "tail length");
+  static_assert(NW == 4 || NW == 8, "tail length");
   if (j < NIT) iter(SlotTag<1>{}, Flag<true>{}, j, sB, sA, pA, pB);
   if (j + 1 < NIT) iter(SlotTag<2>{}, Flag<true>{}, j + 1, sA, sB, pB, pA);
   if (j + 2 < NIT) iter(SlotTag<3>{}, Flag<true>{}, j + 2, sB, sA, pA, pB);
@@ -687,6 +698,12 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
   if (j + 5 < NIT) iter(SlotTag<2>{}, Flag<true>{}, j + 5, sA, sB, pB, pA);
   if (j + 6 < NIT) iter(SlotTag<3>{}, Flag<true>{}, j + 6, sB, sA, pA, pB);
   if (j + 7 < NIT) iter(SlotTag<0>{}, Flag<true>{}, j + 7, sA, sB, pB, pA);
+  if constexpr (NW == 8) {
+    if (j + 8 < NIT) iter(SlotTag<1>{}, Flag<true>{}, j + 8, sB, sA, pA, pB);
+    if (j + 9 < NIT) iter(SlotTag<2>{}, Flag<true>{}, j + 9, sA, sB, pB, pA);
+    if (j + 10 < NIT) iter(SlotTag<3>{}, Flag<true>{}, j + 10, sB, sA, pA, pB);
+    if (j + 11 < NIT) iter(SlotTag<0>{}, Flag<true>{}, j + 11, sA, sB, pB, pA);
+  }
   wait_moves(SlotTag<0>{});  // no LDS DMA outlives the workgroup
 
   // normalise and store
@@ -705,6 +722,9 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
 // (launch bounds: threads per workgroup, minimum waves per SIMD)
 extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128_sp(AttnArgs a) {
   attention_sp_body<4>(a);
+}
+extern "C" __global__ __launch_bounds__(512, 1) void nk_attention_causal_d128_sp8(AttnArgs a) {
+  attention_sp_body<8>(a);
 }
 extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128(AttnArgs a) {
   attention_causal_body<4, 64, true>(a);

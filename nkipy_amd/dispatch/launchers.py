@@ -532,9 +532,10 @@ def attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, B: int, S: int, Hq
     # default: the ring kernel (4 waves, 32-key blocks, software pipelined
     # over a four-slot K / V ring); explicit (waves, key_block) pick the others
     ring = (waves, key_block) == (4, 32) if ring is None else ring
-    if ring and (waves, key_block) != (4, 32):
-        raise LaunchError("the ring attention kernel runs 4 waves over 32-key blocks")
-    suffix = "_sp" if ring else {(4, 64): "", (8, 64): "_w8", (4, 32): "_k32"}.get((waves, key_block))
+    if ring and (waves, key_block) not in ((4, 32), (8, 32)):
+        raise LaunchError("the ring attention kernels run 4 or 8 waves over 32-key blocks")
+    suffix = {4: "_sp", 8: "_sp8"}[waves] if ring else {(4, 64): "", (8, 64): "_w8", (4, 32): "_k32"}.get(
+        (waves, key_block))
     if suffix is None:
         raise LaunchError(f"no attention variant with {waves} waves and {key_block}-key blocks")
     if S % (32 * waves):

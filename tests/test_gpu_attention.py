@@ -43,7 +43,8 @@ def test_attention_small(gpu, shape):
     _close(_run(gpu, q, k, v), K.causal_gqa_attention(q, k, v))
 
 
-@pytest.mark.parametrize("waves,key_block,ring", [(4, 64, False), (8, 64, False), (4, 32, False), (4, 32, True)])
+@pytest.mark.parametrize("waves,key_block,ring", [(4, 64, False), (8, 64, False), (4, 32, False), (4, 32, True),
+                                                   (8, 32, True)])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("shape", [(1, 128, 1, 1), (1, 256, 4, 1), (2, 512, 8, 2), (1, 768, 2, 2),
                                    (1, 1152, 2, 1)])
