@@ -509,6 +509,9 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_state_c64_d128(L
   // thread -> k and v chunks tid + 512 i (row / 16, 8 columns at 8 (% 16)).
   // Buffer loads: one per-lane 32-bit offset, the chunk offset in a scalar
   // register and move i as an immediate (no 64-bit addresses held live).
+  // Each load instruction covers 64 x 16 contiguous bytes, so the loads
+  // stream (nontemporal): 172 -> 166 us per linear-attention step at
+  // (64, 8192, 128).
   const int64_t rbytes = (int64_t)a.rchunks * LC * LD * 2;
   const __amdgpu_buffer_rsrc_t rk =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.k + base), (short)0, (int)rbytes, 0x00020000);
@@ -517,7 +520,7 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_state_c64_d128(L
   const uint32_t loff = (uint32_t)((tid >> 4) * LD + (tid & 15) * 8) * 2;
   typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
   auto ld16 = [&](__amdgpu_buffer_rsrc_t r, uint32_t off, int c) __attribute__((always_inline)) {
-    const u32x4v q = __builtin_amdgcn_raw_buffer_load_b128(r, off, c * (LC * LD * 2), 0);
+    const u32x4v q = __builtin_amdgcn_raw_buffer_load_b128(r, off, c * (LC * LD * 2), 2);  // streaming
     return make_uint4(q[0], q[1], q[2], q[3]);
   };
   auto load = [&](uint4 (&kr)[2], uint4 (&vr)[2], int c) __attribute__((always_inline)) {
