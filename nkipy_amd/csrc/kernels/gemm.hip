@@ -1648,6 +1648,199 @@ __device__ __forceinline__ void gemm_pp64_body(const GemmArgs &a) {
   gemm_epilogue16<SWIGLU, TC, 4>(a, acc, m0 + arow0, n0 + bw0, lane);
 }
 
+// ---------------------------------------------------------------------------
+// 8-wave kernel with 64-deep A stages (bf16 K x N weights)
+// ---------------------------------------------------------------------------
+// The ping-pong of gemm_pp_body for NN bf16 weights, with A in the 64-deep
+// ring of gemm_pp64_body (three 64-k blocks, 256 rows x 128 bytes, 96 KiB)
+// and B in a ring of four 32-k phases in the NN layout of gemm_pp_body
+// (32 k rows x 256 columns, 64 KiB; 160 KiB in all).  A moves read whole
+// 128-byte lines of 8 rows instead of 64-byte halves of 16 rows; B moves
+// read 256-byte runs of k rows as before.  Phase q (block t = q / 2, half
+// H = q mod 2) reads A stage t mod 3 and B stage q mod 4, the fragments and
+// MFMA order of the 32-deep kernel (bit-identical results).  After phase q
+// each wave refills B stage q mod 4 with phase q + 4 and, after the second
+// half, A stage t mod 3 with block t + 3.
+template <bool SWIGLU, typename TC, bool R16 = false>
+__device__ __forceinline__ void gemm_nn64_body(const GemmArgs &a) {
+  static_assert(!R16 || sizeof(TC) == 2, "the staged epilogue writes bf16");
+  constexpr int RA = 3;                       // A ring stages (one block each)
+  constexpr int KB = 64, KP = 32;             // k per block, per phase
+  constexpr int SA = 32768, SP = 16384;       // A stage bytes, B stage bytes (one phase)
+  constexpr int BOFF = RA * SA;               // the B ring follows the A ring
+  constexpr int NAM = 4, NBM = 2;             // moves per wave: A per block, B per phase
+
+  int tm, tn;
+  gemm_tile(a, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM;
+  const int64_t n0 = (int64_t)tn * (SWIGLU ? BN / 2 : BN);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2, wi = wave & 3;
+  const int wm = wi >> 1, wn = wi & 1;
+  const int arow0 = 128 * grp + 64 * wm;
+
+  f32x4 acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.f;
+
+  const i32x4_t ra = rsrc_words(a.A, a.M * a.lda * 2);
+  const i32x4_t rb0 = rsrc_words(a.B0, a.K * a.ldb * 2);
+  const i32x4_t rb1 = rsrc_words(SWIGLU ? a.B1 : a.B0, a.K * a.ldb * 2);
+
+  // A move m = 8 j + wave (j < 4): rows 8 m .. 8 m + 7, lane l fills slot
+  // l & 7 of row 8 m + l / 8 with logical chunk (l & 7) ^ swz_a64(row) =
+  // (l & 7) ^ ((4 wave + l / 16) & 7).
+  const int ac = (lane & 7) ^ ((4 * wave + (lane >> 4)) & 7);
+  const uint32_t abase = (uint32_t)(((m0 + 8 * wave + (lane >> 3)) * a.lda + ac * 8) * 2);
+  const uint32_t astr = (uint32_t)(64 * a.lda * 2);
+  // B move j (j < 2) of wave w: column half j, k rows 4 w + l / 16 of the
+  // phase; lane slot l % 16 holds logical chunk (l % 16) ^ nnswz(k) (8
+  // columns each).  k rows past K lie past the buffer's end and read zeros;
+  // chunks past N are sent out of range.  SwiGLU: half 1 is the up weight's
+  // columns n0 ...
+  const int kq = lane >> 4;
+  const int lc = (lane & 15) ^ nnswz(kq);
+  const uint32_t bbase = (uint32_t)(((int64_t)(4 * wave + kq) * a.ldb + n0 + lc * 8) * 2);
+  const uint32_t bb0 = n0 + lc * 8 < a.N ? bbase : OOB;
+  const uint32_t bb1 = n0 + (SWIGLU ? 0 : 128) + lc * 8 < a.N ? bbase + (SWIGLU ? 0u : 256u) : OOB;
+  auto issue_a = [&](const uint8_t *St, int64_t k0) __attribute__((always_inline)) {
+    const uint32_t va = k0 + ac * 8 < a.K ? abase : OOB;
+    const uint32_t la = lds_addr(St);
+#pragma unroll
+    for (int j = 0; j < NAM; ++j) dma16_asm_so(ra, la + (j * 8 + wave) * 1024, va, j * astr + (uint32_t)k0 * 2);
+  };
+  auto issue_b = [&](const uint8_t *St, int64_t k0) __attribute__((always_inline)) {
+    const uint32_t lb = lds_addr(St);
+    const uint32_t kofs = (uint32_t)k0 * (uint32_t)(a.ldb * 2);
+    dma16_asm_so(rb0, lb + wave * 1024, bb0, kofs);
+    dma16_asm_so(SWIGLU ? rb1 : rb0, lb + (8 + wave) * 1024, bb1, kofs);
+  };
+
+  // Per-lane fragment offsets.  A (64-deep stage, phase half H): tile i =
+  // rows arow0 + 16 i + l16, chunk g ^ swz_a64 (half 1: slot XOR 4, offset
+  // bit 6).  B (ds_read_b64_tr_b16): per B tile j, lane (g, i) reads k rows
+  // 8 g + 4 s + i / 4 (s immediate) and columns c + 4 (i % 4) of column half
+  // (bw0 + brel[j]) / 128.
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int bw0 = SWIGLU ? wn * 64 : wn * 128;
+  constexpr int brel[8] = {0, 16, 32, 48, SWIGLU ? 128 : 64, SWIGLU ? 144 : 80, SWIGLU ? 160 : 96,
+                           SWIGLU ? 176 : 112};
+  const uint32_t aoff0 = (arow0 + l16) * 128 + ((g4 ^ swz_a64(l16)) << 4);
+  uint32_t nnoff[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int br = bw0 + brel[j];
+    const int half = br >> 7, c = br & 127;
+    const int nl = c + 4 * (l16 & 3);
+    const int k = 8 * g4 + (l16 >> 2);
+    nnoff[j] = half * 8192 + k * 256 + (((nl >> 3) ^ nnswz(k)) << 4) + (nl & 7) * 2;
+  }
+
+  typedef __attribute__((address_space(3))) const uint8_t lds_u8;
+  typedef __attribute__((address_space(3))) const bf16x8_t lds_bf16x8;
+  bf16x8_t af[4], bf[8];
+  auto load = [&](const uint8_t *Sa, const uint8_t *Sb, auto htag) __attribute__((always_inline)) {
+    constexpr int H = decltype(htag)::value;
+    uint32_t ao = H ? (aoff0 ^ 64u) : aoff0;
+    asm volatile("" : "+v"(ao));
+    lds_u8 *pa = (lds_u8 *)Sa + ao;
+    asm volatile("" : "+v"(pa));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<lds_bf16x8 *>(pa + i * 2048);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      s16x4 v[2];
+#pragma unroll
+      for (int sidx = 0; sidx < 2; ++sidx)
+        v[sidx] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)((lds_u8 *)Sb + nnoff[j] + 4 * sidx * 256));
+      bf[j] = __builtin_shufflevector(__builtin_bit_cast(__attribute__((ext_vector_type(4))) __bf16, v[0]),
+                                      __builtin_bit_cast(__attribute__((ext_vector_type(4))) __bf16, v[1]),
+                                      0, 1, 2, 3, 4, 5, 6, 7);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  };
+  auto compute = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
+  };
+  auto slot_end = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    barrier_no_fence();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // one array for both rings, reused by the epilogue
+  __shared__ __attribute__((aligned(1024))) uint8_t RING[RA * SA + 4 * SP];
+  uint8_t *const RB = RING + BOFF;
+
+  // Per wave, in issue order: A0, B0, A1, B1, B2, A2, B3, then after phase
+  // q the moves X_q = B(q + 4), preceded after a second half (q = 2t + 1) by
+  // A(t + 3).  vmcnt counts in issue order, so "phase q + 1 landed" (waited
+  // for in phase q, before X_q) leaves X_{q-2} and X_{q-1} outstanding:
+  // NAM + 2 NBM moves.
+  const int nblk = (int)((a.K + KB - 1) / KB);
+  issue_a(RING, 0);
+  issue_b(RB, 0);
+  issue_a(RING + SA, KB);
+  issue_b(RB + SP, KP);
+  issue_b(RB + 2 * SP, 2 * KP);
+  issue_a(RING + 2 * SA, 2 * KB);
+  issue_b(RB + 3 * SP, 3 * KP);
+  wait_vmem_but<2 * NAM + 3 * NBM>();  // A0, B0 landed
+  slot_end();
+  if (grp == 0) load(RING, RB, Int<0>{});
+  slot_end();
+  // phase (block t, half H) in A stage sa = t mod 3 and B stage sq = (2 t +
+  // H) mod 4; G = this wave's group
+  auto phase = [&](int sa, int sq, auto htag, int t, auto gtag) __attribute__((always_inline)) {
+    constexpr int H = decltype(htag)::value;
+    constexpr int G = decltype(gtag)::value;
+    const uint8_t *Sa = RING + sa * SA, *Sb = RB + sq * SP;
+    if (G == 0) compute(); else load(Sa, Sb, Int<H>{});
+    wait_vmem_but<NAM + 2 * NBM>();  // phase 2 t + H + 1 landed
+    slot_end();
+    // group 0 reads the next phase (past the last block it reads a stage
+    // nothing will consume); then every wave refills
+    if (G == 0) {
+      const uint8_t *Sb1 = RB + ((sq + 1) & 3) * SP;
+      if constexpr (H == 0) load(Sa, Sb1, Int<1>{}); else load(RING + (sa == RA - 1 ? 0 : sa + 1) * SA, Sb1, Int<0>{});
+    }
+    if (H == 1) issue_a(Sa, (int64_t)(t + RA) * KB);
+    issue_b(Sb, (int64_t)(2 * t + H + 4) * KP);
+    if (G == 1) compute();
+    slot_end();
+  };
+  auto run = [&](auto gtag) __attribute__((always_inline)) {
+    int sa = 0, sq = 0;
+    for (int t = 0; t < nblk; ++t) {
+      phase(sa, sq, Int<0>{}, t, gtag);
+      phase(sa, sq + 1, Int<1>{}, t, gtag);
+      sa = sa == RA - 1 ? 0 : sa + 1;
+      sq ^= 2;
+    }
+  };
+  if (grp == 0)
+    run(Int<0>{});
+  else
+    run(Int<1>{});
+  wait_vmem();
+  if constexpr (R16) {
+    barrier_no_fence();  // every wave's DMA has landed and its fragment reads are done: the ring is idle
+    gemm_epilogue_lds<SWIGLU, 4>(a, acc, m0, n0, arow0, bw0, lane, RING);
+    return;
+  }
+  gemm_epilogue16<SWIGLU, TC, 4>(a, acc, m0 + arow0, n0 + bw0, lane);
+}
+
 #define NK_GEMM(NT, FP8, SW, TC, name)                                                   \
   extern "C" __global__ __launch_bounds__(NTHREADS, 1) void name(GemmArgs a) {           \
     gemm_body<NT, FP8, SW, TC>(a);                                                       \
@@ -1697,6 +1890,17 @@ NK_GEMM_K64(false, bf16, true, false, nk_gemm8k_nt_e4m3_bf16_rope)
 NK_GEMM_K64(false, bf16, false, true, nk_gemm8k_nt_e4m3_bf16_r16)
 NK_GEMM_K64(true, bf16, false, true, nk_gemm8k_swiglu_nt_e4m3_bf16_r16)
 NK_GEMM_K64(false, bf16, true, true, nk_gemm8k_nt_e4m3_bf16_rope_r16)
+
+#define NK_GEMM_NN64(SW, TC, R16, name)                                                  \
+  extern "C" __global__ __launch_bounds__(512, 1) void name(GemmArgs a) {                \
+    gemm_nn64_body<SW, TC, R16>(a);                                                      \
+  }
+
+NK_GEMM_NN64(false, bf16, false, nk_gemm8k_nn_bf16_bf16)
+NK_GEMM_NN64(false, float, false, nk_gemm8k_nn_bf16_f32)
+NK_GEMM_NN64(true, bf16, false, nk_gemm8k_swiglu_nn_bf16_bf16)
+NK_GEMM_NN64(false, bf16, true, nk_gemm8k_nn_bf16_bf16_r16)
+NK_GEMM_NN64(true, bf16, true, nk_gemm8k_swiglu_nn_bf16_bf16_r16)
 
 NK_GEMM_ROPE(false, false, nk_gemm8_nn_bf16_bf16_rope)
 NK_GEMM_ROPE(true, false, nk_gemm8_nt_bf16_bf16_rope)

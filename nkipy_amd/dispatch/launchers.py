@@ -277,8 +277,9 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
     every layout except fp8 NN weights) or the 4-wave kernel.  ``rope``
     (:class:`GemmRope`) selects the 8-wave kernel whose epilogue applies the
     rotary embedding to the q / k columns.  ``stage64`` (default: wherever
-    it exists, i.e. fp8 NT weights on the 8-wave kernel) selects 64-deep K
-    stages in LDS (whole 128-byte lines per global read).  ``staged``
+    it exists, i.e. on the 8-wave kernel for fp8 NT weights and for bf16 NN
+    weights without a rotary epilogue) selects 64-deep A stages in LDS
+    (whole 128-byte lines per global read).  ``staged``
     (default: wherever it applies, i.e. 64-deep stages and a bf16 output in
     aligned 16-byte row chunks) writes the output tile through LDS so that
     every global store covers whole lines.
@@ -366,10 +367,12 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
         pingpong = has_pp
     if pingpong and not has_pp:
         raise LaunchError("the 8-wave GEMM has no fp8 NN variant")
-    if stage64 is None:  # the default wherever it exists: half the global read requests
-        stage64 = bool(pingpong and fp8 and layout == "nt")
-    if stage64 and not (pingpong and fp8 and layout == "nt"):
-        raise LaunchError("64-deep K stages exist for fp8 NT weights on the 8-wave kernel")
+    has_k64 = bool(pingpong and ((fp8 and layout == "nt") or (not fp8 and layout == "nn" and rope is None)))
+    if stage64 is None:  # the default wherever it exists: whole-line global reads
+        stage64 = has_k64
+    if stage64 and not has_k64:
+        raise LaunchError("64-deep K stages exist on the 8-wave kernel for fp8 NT weights and for bf16 NN "
+                          "weights without a rotary epilogue")
     prefix = ("nk_gemm8k" if stage64 else "nk_gemm8") if pingpong else "nk_gemm"
     if swiglu:
         symbol = f"{prefix}_swiglu_{layout}_{btag}_bf16"

@@ -203,6 +203,55 @@ def test_gemm_fp8_stage64_bit_exact(gpu, shape, variant):
         np.testing.assert_array_equal(o, outs[0])
 
 
+
+@pytest.mark.parametrize("shape", [(256, 256, 64), (300, 520, 136), (520, 272, 600), (64, 40, 16),
+                                   (1000, 768, 1000), (256, 512, 4128)])
+@pytest.mark.parametrize("variant", ["plain", "f32", "swiglu", "bias_resid"])
+def test_gemm_bf16_nn_stage64_bit_exact(gpu, shape, variant):
+    """bf16 K x N weights: the kernel with 64-deep A stages reads the same
+    fragments in the same MFMA order as the 32-deep one, so outputs equal
+    bit for bit (edge tiles, K tails of 8 / 24 / 32 past a 64-k block, and
+    the output staged through LDS included); the 32-deep output also meets
+    the bf16 bar against NumPy."""
+    M, Nn, Kk = shape
+    print(f"gemm bf16 nn stage64 {variant} M={M} N={Nn} K={Kk}", flush=True)
+    rng = np.random.default_rng(M * 7 + Nn + Kk)
+    x = _bf16(rng, (M, Kk))
+    w = _bf16(rng, (Kk, Nn), 0.05)
+    xd = DeviceTensor.from_numpy(dt.to_bf16(x))
+    wd = DeviceTensor.from_numpy(dt.to_bf16(w))
+    kw, keep = {}, []
+    out_dt = dt.float32 if variant == "f32" else dt.bfloat16
+    ref = x.astype(np.float64) @ w.astype(np.float64)
+    if variant == "swiglu":
+        # fused gate_up weight (K, 2N): up is a column offset, ldb = 2N
+        wu = _bf16(rng, (Kk, Nn), 0.05)
+        wd = DeviceTensor.from_numpy(dt.to_bf16(np.concatenate([w, wu], axis=1)))
+        kw.update(up_ptr=wd.ptr + Nn * 2, ldb=2 * Nn)
+        ref = K.silu(ref) * (x.astype(np.float64) @ wu.astype(np.float64))
+    if variant == "bias_resid":
+        bias = N.bf16_round(rng.standard_normal(Nn) * 0.1)
+        res = N.bf16_round(rng.standard_normal((M, Nn)))
+        keep = [DeviceTensor.from_numpy(dt.to_bf16(bias)), DeviceTensor.from_numpy(dt.to_bf16(res))]
+        kw.update(bias_ptr=keep[0].ptr, resid_ptr=keep[1].ptr, round_before_resid=True)
+        ref = N.bf16_round(ref + bias) + res
+    outs = []
+    runs = [(False, None), (True, False)] + ([(True, True)] if out_dt == dt.bfloat16 else [])
+    for k64, staged in runs:
+        cd = DeviceTensor.empty((M, Nn), out_dt)
+        launch = LA.gemm(xd.ptr, wd.ptr, cd.ptr, M, Nn, Kk, layout="nn", b_dtype=dt.bfloat16,
+                         c_dtype=out_dt, stage64=k64, staged=staged, **kw)
+        assert launch.symbol.startswith("nk_gemm8k_" if k64 else "nk_gemm8_")
+        _run(gpu, launch)
+        outs.append(dt.to_float32(cd.numpy()) if out_dt == dt.bfloat16 else cd.numpy())
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])
+    if out_dt == dt.float32:
+        np.testing.assert_allclose(outs[0], ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
+    else:
+        _close(outs[0], ref)
+
+
 def test_fp8_decode_all_codes(gpu):
     """The fp8 -> bf16 decode used by the GEMM staging, on every E4M3FN code
     (zeros, subnormals, normals, +-448, NaN) against the oracle's table."""
