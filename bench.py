@@ -626,6 +626,12 @@ def summarize(d, traffic_json=None):
                 parts.append(f"mfma_busy={mean['SQ_VALU_MFMA_BUSY_CYCLES'] / (4 * CUS * gui):.3f}")
             if "SQ_BUSY_CU_CYCLES" in mean and gui:
                 parts.append(f"cu_busy={mean['SQ_BUSY_CU_CYCLES'] / (CUS * gui):.3f}")
+            # wave-state counters as fractions of the waves' lifetime
+            # (SQ_WAVE_CYCLES, same units): where the waves spend their time
+            if mean.get("SQ_WAVE_CYCLES"):
+                for c in names:
+                    if c.startswith(("SQ_WAIT", "SQ_ACTIVE_INST")):
+                        parts.append(f"{c[3:].lower()}={mean[c] / mean['SQ_WAVE_CYCLES']:.3f}")
             for c in names:
                 parts.append(f"{c}={mean[c]:.6g}")
             key = f"{secs[sid][0]}/{label}"
