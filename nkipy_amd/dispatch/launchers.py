@@ -416,9 +416,10 @@ LINATTN_D = 128
 LINATTN_TARGET_WGS = 256
 
 
-def linear_attention_split(BH: int, T: int):
+def linear_attention_split(BH: int, T: int, ranges_per_segment: int = None):
     """(segments per sequence, chunks per partial-sum range, ranges) for the
-    linear-attention scan of BH sequences of length T."""
+    linear-attention scan of BH sequences of length T; ``ranges_per_segment``
+    (1, 2 or 4) overrides the partial-sum range policy."""
     nchunks = T // LINATTN_CHUNK
     nseg = 1
     while (BH * nseg < LINATTN_TARGET_WGS and nchunks % (2 * nseg) == 0
@@ -430,7 +431,11 @@ def linear_attention_split(BH: int, T: int):
     # prefetch, so fewer, longer ranges beat a second round of workgroups
     # (and halve the partial-state traffic); else halves or quarters.
     wgs = BH * (nseg - 1)
-    if cs % 4 or 4 * wgs >= 3 * LINATTN_TARGET_WGS:
+    if ranges_per_segment is not None:
+        if ranges_per_segment not in (1, 2, 4) or cs % ranges_per_segment:
+            raise LaunchError(f"{ranges_per_segment} ranges per segment of {cs} chunks")
+        rchunks = cs // ranges_per_segment
+    elif cs % 4 or 4 * wgs >= 3 * LINATTN_TARGET_WGS:
         rchunks = cs
     elif 2 * wgs >= LINATTN_TARGET_WGS:
         rchunks = cs // 2
@@ -440,15 +445,16 @@ def linear_attention_split(BH: int, T: int):
     return nseg, rchunks, nranges
 
 
-def linear_attention_workspace_bytes(BH: int, T: int) -> int:
+def linear_attention_workspace_bytes(BH: int, T: int, ranges_per_segment: int = None) -> int:
     """Device workspace (fp32 partial prefix states) the launch needs; 0 if
     the sequences run unsegmented."""
-    _, _, nranges = linear_attention_split(BH, T)
+    _, _, nranges = linear_attention_split(BH, T, ranges_per_segment)
     return BH * nranges * (LINATTN_D + 1) * LINATTN_D * 4
 
 
 def linear_attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, BH: int, T: int,
-                     D: int = 128, Dv: int = 128, chunk: int = 64, part_ptr: int = 0) -> List[Launch]:
+                     D: int = 128, Dv: int = 128, chunk: int = 64, part_ptr: int = 0,
+                     ranges_per_segment: int = None) -> List[Launch]:
     """o = causal linear attention with phi = elu + 1 over (BH, T, D) bf16
     sequences, chunk 64, head dims 128 (the compiled variant).
 
@@ -463,12 +469,12 @@ def linear_attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, BH: int, T:
         raise LaunchError(f"linear attention needs T a positive multiple of {chunk}, got T={T}")
     if any(p % 16 for p in (q_ptr, k_ptr, v_ptr, o_ptr)):
         raise LaunchError("linear attention operands must be 16-byte aligned")
-    nseg, rchunks, nranges = linear_attention_split(BH, T)
+    nseg, rchunks, nranges = linear_attention_split(BH, T, ranges_per_segment)
     if BH * nseg >= 2**31 or BH * max(nranges, 1) >= 2**31:
         raise LaunchError("linear attention grid too large")
     if nranges and not part_ptr:
         raise LaunchError(f"linear attention of {BH} x {T} runs in {nseg} segments and needs a "
-                          f"workspace of {linear_attention_workspace_bytes(BH, T)} bytes")
+                          f"workspace of {linear_attention_workspace_bytes(BH, T, ranges_per_segment)} bytes")
     if part_ptr % 16:
         raise LaunchError("linear attention workspace must be 16-byte aligned")
     n = T // chunk

@@ -22,14 +22,14 @@ def _qkv(B, H, T, D, seed):
     return [N.bf16_round(rng.standard_normal((B, H, T, D)) / np.sqrt(D)) for _ in range(3)]
 
 
-def _run(gpu, q, k, v):
+def _run(gpu, q, k, v, rps=None):
     B, H, T, D = q.shape
     t = [DeviceTensor.from_numpy(dt.to_bf16(a)) for a in (q, k, v)]
     o = DeviceTensor.empty((B, H, T, D), dt.bfloat16)
-    ws_bytes = LA.linear_attention_workspace_bytes(B * H, T)
+    ws_bytes = LA.linear_attention_workspace_bytes(B * H, T, rps)
     ws = DeviceTensor.empty((max(ws_bytes, 16),), dt.uint8) if ws_bytes else None
     for launch in LA.linear_attention(t[0].ptr, t[1].ptr, t[2].ptr, o.ptr, B * H, T,
-                                      part_ptr=ws.ptr if ws is not None else 0):
+                                      part_ptr=ws.ptr if ws is not None else 0, ranges_per_segment=rps):
         launch.run(gpu)
     gpu.sync()
     return dt.to_float32(o.numpy())
@@ -47,15 +47,25 @@ def test_linattn_matches_quadratic_form(gpu, shape):
     _close(got, K.linear_attention_quadratic_f64(q, k, v))
 
 
-@pytest.mark.parametrize("shape", [(1, 2, 1024, 128), (1, 1, 4096, 128)])
-def test_linattn_segmented_matches_quadratic_form(gpu, shape):
+@pytest.mark.parametrize("rps", [None, 1, 2, 4])
+@pytest.mark.parametrize("shape", [(1, 2, 1024, 128), (1, 1, 4096, 128), (40, 2, 2048, 128)])
+def test_linattn_segmented_matches_quadratic_form(gpu, shape, rps):
     """Few sequences: the scan is cut into segments whose prefix states come
-    from the partial-sum kernel (segments, ranges as chosen by the launcher)."""
+    from the partial-sum kernel (segments as chosen by the launcher; partial
+    sums over whole segments, halves or quarters, so that a segment starts
+    from the sum of up to 4 (nseg - 1) ranges)."""
     B, H, T, D = shape
-    assert LA.linear_attention_split(B * H, T)[0] > 1
+    nseg, rchunks, nranges = LA.linear_attention_split(B * H, T, rps)
+    assert nseg > 1
+    print(f"linattn segmented shape={shape} ranges/segment={rps} nseg={nseg} rchunks={rchunks} "
+          f"ranges={nranges}", flush=True)
     q, k, v = _qkv(*shape, seed=sum(shape))
-    got = _run(gpu, q, k, v)
-    _close(got, K.linear_attention_quadratic_f64(q, k, v))
+    got = _run(gpu, q, k, v, rps)
+    if B * H > 8:  # the float64 quadratic form on a sample of heads
+        idx = (slice(0, B, B - 1), slice(0, 1))  # first and last batch, head 0
+        _close(got[idx], K.linear_attention_quadratic_f64(q[idx], k[idx], v[idx]))
+    else:
+        _close(got, K.linear_attention_quadratic_f64(q, k, v))
 
 
 def test_linattn_first_position_is_v0(gpu):
