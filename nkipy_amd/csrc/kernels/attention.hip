@@ -391,13 +391,6 @@ __device__ __forceinline__ void attention_causal_body(const AttnArgs &a) {
 // score.  Every p stays below 2^16: nothing overflows, and since the output
 // is a ratio of sums of the same p, the offset does not change it.
 // ---------------------------------------------------------------------------
-#ifndef ATT_SP_SCHED
-#define ATT_SP_SCHED 1
-#endif
-#ifndef ATT_SP_DMA_LATE
-#define ATT_SP_DMA_LATE 1
-#endif
-
 template <int N> struct SlotTag {
   static constexpr int value = N;
 };
@@ -618,19 +611,15 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
                   bf16x8_t (&p_cur)[2]) __attribute__((always_inline)) {
     constexpr int SL = decltype(sl)::value;
     constexpr bool GEN = decltype(gen)::value;
-#if !ATT_SP_DMA_LATE
-    load_k(SlotTag<SL>{}, j + 4);
-    load_v(SlotTag<SL + 2>{}, j + 2);
-#endif
     const uint8_t *kn = kslot(SlotTag<SL + 1>{});
     const uint8_t *vp_ = vslot(SlotTag<SL + 3>{});
     if constexpr (!GEN) {
       pv(vp_, p_prev);
       qk(kn, s_nxt);
       softmax(s_cur, p_cur, j, Flag<false>{});
-#if ATT_SP_SCHED
       // order within the block: every LDS fragment read first, a few VALU
-      // ops while they land, then each MFMA followed by VALU work
+      // ops while they land, then each MFMA followed by VALU work (other
+      // orders measured within 1%)
       __builtin_amdgcn_sched_group_barrier(0x100, 24, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
 #pragma unroll
@@ -638,7 +627,6 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
       }
-#endif
     } else if (j <= nb_w) {
       // the same body with the mask; blocks past this wave's last come out
       // as p = 0 (their scores, computed anyway, are discarded)
@@ -646,12 +634,10 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
       pv(vp_, p_prev);
       softmax(s_cur, p_cur, j, Flag<true>{});
     }
-#if ATT_SP_DMA_LATE
     // after the block's MFMAs: a vector memory instruction that waits at
     // issue then holds up no MFMA of this wave
     load_k(SlotTag<SL>{}, j + 4);
     load_v(SlotTag<SL + 2>{}, j + 2);
-#endif
     wait_moves(SlotTag<4 * NM>{});
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
