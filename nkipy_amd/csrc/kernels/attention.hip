@@ -457,6 +457,9 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
   uint16_t *op = a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
   const i32x4_t rk = rsrc_words(kp, (int64_t)a.S * a.k_ss * 2);
   const i32x4_t rv = rsrc_words(vp, (int64_t)a.S * a.v_ss * 2);
+  // a resource of no bytes: moves of blocks past the workgroup's last write
+  // zeros and read no memory
+  const i32x4_t rnone = rsrc_words(kp, 0);
 
   const int wq0 = q0 + wave * 32;
   const int qrow = wq0 + l32;
@@ -495,15 +498,17 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
   const uint32_t k_lds = lds_addr(KR) + wave * 1024, v_lds = lds_addr(VR) + wave * 1024;
   auto load_k = [&](auto sl, int kb) __attribute__((always_inline)) {
     const uint32_t kst = (uint32_t)((int64_t)kb * 32 * a.k_ss * 2);
+    const i32x4_t r = kb < nb_wg ? rk : rnone;
 #pragma unroll
     for (int j = 0; j < NM; ++j)
-      dma16_asm(rk, k_lds + (decltype(sl)::value & 3) * TB + j * NW * 1024, kbase + j * kjs + kst);
+      dma16_asm(r, k_lds + (decltype(sl)::value & 3) * TB + j * NW * 1024, kbase + j * kjs + kst);
   };
   auto load_v = [&](auto sl, int kb) __attribute__((always_inline)) {
     const uint32_t vst = (uint32_t)((int64_t)kb * 32 * a.v_ss * 2);
+    const i32x4_t r = kb < nb_wg ? rv : rnone;
 #pragma unroll
     for (int j = 0; j < NM; ++j)
-      dma16_asm(rv, v_lds + (decltype(sl)::value & 3) * TB + j * NW * 1024, vbase + j * vjs + vst);
+      dma16_asm(r, v_lds + (decltype(sl)::value & 3) * TB + j * NW * 1024, vbase + j * vjs + vst);
   };
   // wait until at most n of this wave's DMA moves are outstanding (the Q
   // loads were issued before every move, so they are done by then too)
@@ -629,27 +634,25 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
       }
     } else if (j <= nb_w) {
       // the same body with the mask; blocks past this wave's last come out
-      // as p = 0 (their scores, computed anyway, are discarded)
-      qk(kn, s_nxt);
-      pv(vp_, p_prev);
+      // as p = 0 (their scores are discarded); no scores past the
+      // workgroup's last block, no P V before block 0
+      if (j + 1 < nb_wg) qk(kn, s_nxt);
+      if (j > 0) pv(vp_, p_prev);
       softmax(s_cur, p_cur, j, Flag<true>{});
     }
     // after the block's MFMAs: a vector memory instruction that waits at
-    // issue then holds up no MFMA of this wave
-    load_k(SlotTag<SL>{}, j + 4);
-    load_v(SlotTag<SL + 2>{}, j + 2);
+    // issue then holds up no MFMA of this wave; the last iteration moves
+    // nothing
+    if (j < nb_wg) {
+      load_k(SlotTag<SL>{}, j + 4);
+      load_v(SlotTag<SL + 2>{}, j + 2);
+    }
     wait_moves(SlotTag<4 * NM>{});
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
 
-  // V slot 3 stands for block -1 in iteration 0 (P = 0 there): zero it so
-  // that product is exactly zero
-  {
-    uint4 *z = reinterpret_cast<uint4 *>(vslot(SlotTag<3>{}));
-    for (int i = threadIdx.x; i < TB / 16; i += 64 * NW) z[i] = make_uint4(0, 0, 0, 0);
-  }
   // prologue: K of blocks 0..3 and V of blocks 0, 1 (in the order that lets
   // each iteration's wait leave exactly the last two iterations' moves
   // outstanding), then the scores of block 0
