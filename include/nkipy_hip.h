@@ -112,6 +112,16 @@ int nkh_event_destroy(void *event);
 int nkh_event_record(void *event);
 int nkh_event_elapsed_ms(void *start, void *stop, float *ms_out);
 
+/* Named profiler ranges around a stretch of host calls (roctx ranges,
+ * shown by `rocprofv3 --marker-trace`).  They stand where the reference
+ * brackets one execution with nrt_profile_start / nrt_profile_stop
+ * (spike/src/model.cpp:97-103).  The roctx library is opened on first use;
+ * where it is absent both calls succeed and record nothing, and *available
+ * (if not null) reports 0.  Ranges nest per thread; a pop without a push
+ * returns NKH_ERR_INVALID. */
+int nkh_profile_range_push(const char *name, int *available);
+int nkh_profile_range_pop(void);
+
 /* Batched launch: run `count` launches back to back on the runtime stream
  * with one host call.  Launch i uses functions[i], grids[3i..3i+2],
  * blocks[3i..3i+2], shared[i] and the kernarg block at

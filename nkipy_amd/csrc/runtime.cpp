@@ -13,6 +13,7 @@
 //   * a registry of loaded modules, unloaded at shutdown;
 //   * thread-local last-error text.
 
+#include <dlfcn.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -91,6 +92,35 @@ int check_range(const void *p, size_t n, const char *what) {
     return set_error(NKH_ERR_BOUNDS, buf);
   }
   return NKH_OK;
+}
+
+// roctx, opened on first use (the library is part of the ROCm profiler SDK;
+// without it profiler ranges are no-ops)
+struct Roctx {
+  std::once_flag once;
+  int (*push)(const char *) = nullptr;
+  int (*pop)() = nullptr;
+};
+Roctx g_roctx;
+thread_local int g_range_depth = 0;
+
+void open_roctx() {
+  std::call_once(g_roctx.once, [] {
+    const char *names[] = {"librocprofiler-sdk-roctx.so.1", "librocprofiler-sdk-roctx.so",
+                           "libroctx64.so.4", "libroctx64.so"};
+    for (const char *n : names) {
+      void *h = dlopen(n, RTLD_NOW | RTLD_LOCAL);
+      if (!h) continue;
+      auto push = reinterpret_cast<int (*)(const char *)>(dlsym(h, "roctxRangePushA"));
+      auto pop = reinterpret_cast<int (*)()>(dlsym(h, "roctxRangePop"));
+      if (push && pop) {
+        g_roctx.push = push;
+        g_roctx.pop = pop;
+        return;
+      }
+      dlclose(h);
+    }
+  });
 }
 
 }  // namespace
@@ -372,6 +402,23 @@ int nkh_launch(void *function, unsigned gx, unsigned gy, unsigned gz,
   if (rc) return rc;
   return launch_locked(function, gx, gy, gz, bx, by, bz, shared_bytes, kernarg,
                        kernarg_bytes);
+}
+
+int nkh_profile_range_push(const char *name, int *available) {
+  if (!name) return set_error(NKH_ERR_INVALID, "range name is null");
+  open_roctx();
+  if (available) *available = g_roctx.push != nullptr;
+  if (g_roctx.push) g_roctx.push(name);
+  ++g_range_depth;
+  return NKH_OK;
+}
+
+int nkh_profile_range_pop(void) {
+  if (g_range_depth <= 0)
+    return set_error(NKH_ERR_INVALID, "profiler range pop without a push");
+  --g_range_depth;
+  if (g_roctx.pop) g_roctx.pop();
+  return NKH_OK;
 }
 
 int nkh_launch_batch(int count, void *const *functions, const unsigned *grids,

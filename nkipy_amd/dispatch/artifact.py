@@ -57,12 +57,21 @@ class NotRelocatable(ValueError):
 _digest_cache: Dict[str, str] = {}
 
 
+def lowering_sources() -> List[Path]:
+    """The files whose content decides a plan's launches and argument blocks:
+    the lowering itself, plus the dtype table (item sizes and the dtype codes
+    packed into argument blocks) and the IR the patterns match on."""
+    pkg = Path(__file__).resolve().parent
+    core = pkg.parent / "core"
+    return sorted(pkg.glob("*.py")) + [core / "dtypes.py", core / "backend" / "ir.py"]
+
+
 def lowering_digest() -> str:
     """Digest of the lowering code: a change to it invalidates artefacts."""
     key = "__lowering__"
     if key not in _digest_cache:
         h = hashlib.sha256()
-        for p in sorted(Path(__file__).resolve().parent.glob("*.py")):
+        for p in lowering_sources():
             h.update(p.name.encode())
             h.update(p.read_bytes())
         _digest_cache[key] = h.hexdigest()[:16]
@@ -218,8 +227,14 @@ class RelocatablePlan:
             if b.kind == "const" and b.data is not None:
                 raw = np.ascontiguousarray(dt.numpy_storage(np.ascontiguousarray(b.data))).reshape(-1).view(np.uint8)
                 fname = f"{path.stem}.const{b.index}.npy"
-                np.save(path.parent / fname, raw, allow_pickle=False)
+                # written under a temporary name and renamed, like the JSON:
+                # a concurrent reader sees the old payload or the new one
+                part = path.parent / (fname + f".{os.getpid()}.tmp")
+                with open(part, "wb") as f:
+                    np.save(f, raw, allow_pickle=False)
+                os.replace(part, path.parent / fname)
                 e["data"] = fname
+                e["sha256"] = hashlib.sha256(raw.tobytes()).hexdigest()
             bufs.append(e)
         doc = {
             "format": FORMAT, "backend": BACKEND_ID, "lowering": self.lowering, "modules": self.modules,
@@ -231,7 +246,7 @@ class RelocatablePlan:
                           "relocs": [list(x) for x in r.relocs], "bytes": r.bytes, "flops": r.flops}
                          for r in self.records],
         }
-        tmp = path.with_suffix(path.suffix + ".tmp")
+        tmp = path.with_suffix(path.suffix + f".{os.getpid()}.tmp")
         tmp.write_text(json.dumps(doc, indent=1))
         os.replace(tmp, path)
 
@@ -246,6 +261,9 @@ class RelocatablePlan:
             data = None
             if e.get("data"):
                 data = np.load(path.parent / e["data"], allow_pickle=False)
+                want = e.get("sha256")
+                if want is not None and hashlib.sha256(np.ascontiguousarray(data).tobytes()).hexdigest() != want:
+                    raise NotRelocatable(f"{path}: constant payload {e['data']} does not match its checksum")
             bufs.append(BufferSpec(int(e["index"]), int(e["nbytes"]), e["kind"], e["name"], data))
         records = [LaunchRecord(r["kind"], r["module"], r["symbol"], tuple(r["grid"]), tuple(r["block"]),
                                 int(r["shared"]), bytes.fromhex(r["args"]), [tuple(x) for x in r["relocs"]],

@@ -300,17 +300,81 @@ class DeviceKernel:
                     shape, dtype = self._out_specs[on]
                     st = self._staging[on] = DeviceTensor.empty(shape, dtype, name=on)
                 run_outputs[on] = st
-            self.executor.run(self._io_ptrs(inputs, run_outputs))
+            self._execute(self._io_ptrs(inputs, run_outputs), save_trace, ntff_name)
             rt = get_runtime()
             for on in staged:
                 rt.d2d(outputs[on].ptr, run_outputs[on].ptr, outputs[on].nbytes)
         else:
-            self.executor.run(self._io_ptrs(inputs, outputs))
+            self._execute(self._io_ptrs(inputs, outputs), save_trace, ntff_name)
         if sync:
             get_runtime().sync()
         if auto:
             return outputs
         return None
+
+    def trace_path(self, ntff_name: Optional[str] = None) -> str:
+        """Where ``save_trace`` writes: ``ntff_name``, else beside the compiled
+        artefact with its suffix replaced (spike_model.py:250-251)."""
+        if ntff_name:
+            return str(ntff_name)
+        if self.neff_path:
+            return os.path.splitext(str(self.neff_path))[0] + ".ntff"
+        return f"{self.name}.ntff"
+
+    def _execute(self, io_ptrs: Dict[str, int], save_trace: bool, ntff_name: Optional[str]):
+        if not save_trace:
+            self.executor.run(io_ptrs)
+            return
+        self._run_profiled(io_ptrs, self.trace_path(ntff_name))
+
+    def _run_profiled(self, io_ptrs: Dict[str, int], path: str):
+        """One execution with every launch bracketed by events, inside a
+        roctx range named after the kernel: the profile the reference takes
+        between nrt_profile_start / nrt_profile_stop (spike/src/model.cpp:
+        97-103).  Writes a Chrome trace-event JSON document (one complete
+        event per launch, microseconds, back to back on the runtime stream)
+        to ``path`` and returns it."""
+        from nkipy_amd.runtime.hip import profile_range
+
+        rt = get_runtime()
+        bound = self.executor.bind(io_ptrs)
+        n = len(bound.launches)
+        evs = [rt.event() for _ in range(n + 1)]
+        try:
+            rt.sync()
+            with profile_range(f"nkipy:{self.name}") as have_roctx:
+                evs[0].record()
+                for i in range(n):
+                    bound.run_range(i, i + 1)
+                    evs[i + 1].record()
+                rt.sync()
+            durs = [evs[i].elapsed_ms(evs[i + 1]) * 1e3 for i in range(n)]
+        finally:
+            for e in evs:
+                e.destroy()
+        events, t = [], 0.0
+        for l, d in zip(bound.launches, durs):
+            args = {"module": l.module, "grid": list(l.grid), "block": list(l.block), "lds_bytes": l.shared}
+            if l.bytes:
+                args["bytes"] = int(l.bytes)
+                args["GB_per_s"] = l.bytes / (d * 1e3) if d > 0 else None
+            if l.flops:
+                args["flops"] = int(l.flops)
+                args["TFLOP_per_s"] = l.flops / (d * 1e6) if d > 0 else None
+            events.append({"name": l.symbol, "cat": "kernel", "ph": "X", "ts": round(t, 3),
+                           "dur": round(d, 3), "pid": 0, "tid": 0, "args": args})
+            t += d
+        doc = {"traceEvents": events, "displayTimeUnit": "ns",
+               "otherData": {"kernel": self.name, "device": rt.device, "steps": list(self.plan.kernel_kinds),
+                             "total_us": round(t, 3), "roctx_range": have_roctx}}
+        d = os.path.dirname(os.path.abspath(path))
+        os.makedirs(d, exist_ok=True)
+        tmp = f"{path}.{os.getpid()}.tmp"
+        with open(tmp, "w") as f:
+            json.dump(doc, f, indent=1)
+        os.replace(tmp, path)
+        logger.info(f"wrote execution trace of {self.name} to {path}")
+        return doc
 
     def benchmark(self, inputs, outputs=None, warmup_iter=5, benchmark_iter=5, mode: str = "device"):
         if mode not in ("device", "host"):
@@ -348,4 +412,4 @@ class DeviceKernel:
         return _make_benchmark_result(durations, warmup_iter)
 
     def __repr__(self):
-        return f"DeviceKernel('{self.name}', steps={[s.kind for s in self.plan.steps]})"
+        return f"DeviceKernel('{self.name}', steps={list(self.plan.kernel_kinds)})"

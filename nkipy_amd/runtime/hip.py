@@ -16,6 +16,7 @@ reference's Spike/NRT stack:
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import json
 import os
@@ -96,6 +97,8 @@ def _bind(lib):
             ctypes.c_int,
         ),
     }
+    sigs["nkh_profile_range_push"] = ([ctypes.c_char_p, c_int_p], ctypes.c_int)
+    sigs["nkh_profile_range_pop"] = ([], ctypes.c_int)
     i64 = ctypes.c_int64
     sigs["nkh_linear_attention_workspace_size"] = ([i64, i64, ctypes.POINTER(sz)], ctypes.c_int)
     sigs["nkh_linear_attention"] = ([vp, vp, vp, vp, i64, i64, vp, sz], ctypes.c_int)
@@ -116,7 +119,7 @@ EXPORTED_SYMBOLS = (
     "nkh_launch", "nkh_sync", "nkh_time_launch", "nkh_event_create",
     "nkh_event_destroy", "nkh_event_record", "nkh_event_elapsed_ms",
     "nkh_launch_batch", "nkh_linear_attention_workspace_size", "nkh_linear_attention",
-    "nkh_linear_attention_noalloc",
+    "nkh_linear_attention_noalloc", "nkh_profile_range_push", "nkh_profile_range_pop",
 )
 
 _lib = None
@@ -362,6 +365,19 @@ class HipRuntime:
     def event(self) -> "Event":
         self._live()
         return Event(self)
+
+
+@contextlib.contextmanager
+def profile_range(name: str):
+    """A named roctx range around the enclosed host calls (``rocprofv3
+    --marker-trace`` shows it); yields whether a roctx library was found."""
+    lib = load_library()
+    avail = ctypes.c_int(0)
+    _check(lib.nkh_profile_range_push(name.encode(), ctypes.byref(avail)), "profile_range_push")
+    try:
+        yield bool(avail.value)
+    finally:
+        _check(lib.nkh_profile_range_pop(), "profile_range_pop")
 
 
 class Event:

@@ -114,3 +114,51 @@ def test_unrelocatable_launch_is_not_cached(tmp_path, monkeypatch):
     assert not artifact.write_artifact(plan, g, str(path))
     assert json.loads(path.read_text())["relocatable"] is False
     assert artifact.try_load(str(path), g) is None
+
+
+def test_digest_covers_dtype_table_and_ir(tmp_path, monkeypatch):
+    """A change to the dtype table or the IR (both shape the argument blocks)
+    makes a saved artefact stale, like a change to the lowering code."""
+    from pathlib import Path
+
+    srcs = artifact.lowering_sources()
+    names = {(p.parent.name, p.name) for p in srcs}
+    assert ("core", "dtypes.py") in names and ("backend", "ir.py") in names
+    fn, args, kw = _kernels()[0]
+    g = NKIPyKernel.trace(fn).specialize(*args, **kw)
+    path = tmp_path / "plan.json"
+    assert artifact.write_artifact(lower(g), g, str(path))
+    assert artifact.try_load(str(path), g) is not None
+    # a copy of the digested files with an edited dtype table
+    copies = []
+    for i, p in enumerate(srcs):
+        c = tmp_path / "src" / str(i) / p.name
+        c.parent.mkdir(parents=True)
+        data = p.read_bytes()
+        if p.name == "dtypes.py" and p.parent.name == "core":
+            data += b"\n# edited\n"
+        c.write_bytes(data)
+        copies.append(Path(c))
+    monkeypatch.setattr(artifact, "lowering_sources", lambda: copies)
+    monkeypatch.setattr(artifact, "_digest_cache", {})
+    assert artifact.try_load(str(path), g) is None
+
+
+def test_constant_payloads_are_checked_on_load(tmp_path):
+    """Payloads are renamed into place after a full write and carry a
+    checksum: a truncated or replaced payload is not loaded."""
+    fn, args, kw = _kernels()[4]
+    g = NKIPyKernel.trace(fn).specialize(*args, **kw)
+    path = tmp_path / "plan.json"
+    assert artifact.write_artifact(lower(g), g, str(path))
+    assert not list(tmp_path.glob("*.tmp"))
+    doc = json.loads(path.read_text())
+    payloads = [b for b in doc["buffers"] if b["data"]]
+    assert payloads and all(len(b["sha256"]) == 64 for b in payloads)
+    assert artifact.try_load(str(path), g) is not None
+    victim = tmp_path / payloads[0]["data"]
+    raw = np.load(victim, allow_pickle=False)
+    np.save(victim, raw ^ np.uint8(1), allow_pickle=False)
+    assert artifact.try_load(str(path), g) is None
+    with pytest.raises(artifact.NotRelocatable):
+        RelocatablePlan.load(str(path))

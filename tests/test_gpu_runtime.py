@@ -2,6 +2,7 @@
 objects, unknown symbols, argument-size mismatch) and basic device I/O."""
 
 import ctypes
+import os
 
 import numpy as np
 import pytest
@@ -115,3 +116,33 @@ def test_reset_runtime_invalidates_loaded_kernels(gpu):
     dk2 = DeviceKernel.compile_and_load(kern, x, name="reset_probe")
     assert dk2 is not dk and dk2.executor.rt is get_runtime()
     np.testing.assert_array_equal(dk2(fresh)["output0"].numpy(), x * 2 + 1)
+
+
+def test_save_trace_writes_one_event_per_launch(gpu, tmp_path):
+    """save_trace=True profiles one execution (the reference's
+    nrt_profile_start / nrt_profile_stop window, spike/src/model.cpp:97-103)
+    and writes its trace beside the artefact or at ntff_name."""
+    import json
+
+    from nkipy_amd.kernels import residual_rmsnorm_kernel
+    from nkipy_amd.runtime import DeviceKernel
+
+    rng = np.random.default_rng(3)
+    x = dt.to_bf16(rng.standard_normal((256, 4096)).astype(np.float32))
+    w = dt.to_bf16(rng.uniform(0.5, 1.5, 4096).astype(np.float32))
+    dk = DeviceKernel.compile_and_load(residual_rmsnorm_kernel, x, x, w, 1e-6, build_dir=str(tmp_path))
+    assert repr(dk).startswith("DeviceKernel(")
+    ins = {n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(list(dk.input_tensors_info), (x, x, w))}
+    plain = dk(ins)
+    dest = tmp_path / "prof" / "rms.ntff"
+    traced = dk(ins, save_trace=True, ntff_name=str(dest))
+    for k in plain:  # the profiled execution computes the same result
+        np.testing.assert_array_equal(dt.numpy_storage(traced[k].numpy()), dt.numpy_storage(plain[k].numpy()))
+    doc = json.loads(dest.read_text())
+    evs = doc["traceEvents"]
+    assert len(evs) == len(dk.plan.kernel_kinds) == 1
+    assert evs[0]["name"].startswith("nk_rmsnorm") and evs[0]["dur"] > 0 and evs[0]["args"]["bytes"] > 0
+    assert doc["otherData"]["steps"] == ["rmsnorm"]
+    # default location: beside the compiled artefact
+    dk(ins, save_trace=True)
+    assert os.path.exists(dk.trace_path())

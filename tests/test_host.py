@@ -390,3 +390,15 @@ def test_c_abi_linear_attention_workspace_matches_launcher():
     for bh, t in ((0, 64), (4, 100), (4, 0), (-1, 64)):
         assert lib.nkh_linear_attention_workspace_size(bh, t, ctypes.byref(size)) == 2
         assert b"multiple of 64" in lib.nkh_last_error()
+
+
+def test_profile_ranges_need_no_device_and_reject_unbalanced_pops():
+    from nkipy_amd.runtime.hip import SpikeError, load_library, profile_range
+
+    with profile_range("outer") as have:
+        assert have in (True, False)
+        with profile_range("inner"):
+            pass
+    lib = load_library()
+    assert lib.nkh_profile_range_pop() != 0
+    assert b"without a push" in lib.nkh_last_error()
