@@ -12,13 +12,19 @@ each with its own roofline, CPU baseline and parity record:
   4  chunked causal linear attention, q, k, v bf16 (4, 16, 8192, 128)
   5  Llama-style decoder layer with fp8 weights, x bf16 (8, 2048, 4096),
      32 / 8 heads, FFN 14336 -- reported as its latency per layer
+  6  Qwen3 prefill attention: q bf16 (1, 2048, 32, 128) against a bf16 KV
+     cache of 4096 rows (8 KV heads), scores rounded to bf16, mask rows
+     [:2048, :4096], bf16 softmax (an extra line beside the five
+     configurations)
 
 Timing: inputs are resident in HBM; bandwidth-bound steps rotate over
 buffer sets whose total exceeds the 256 MB Infinity Cache; every timed
 region follows 50 ms of untimed load of the same work (the part ramps its
 clocks) and is bracketed by HIP events on the runtime stream.  Per-kernel
-times inside multi-kernel steps come from HIP events recorded between the
-launches of whole steps.
+times inside multi-kernel steps come from each launch run back to back with
+itself over the rotating buffer sets (events around the whole run only, so
+no marker sits between two launches of one kernel), after one whole step
+has produced every intermediate.
 
 ``cpu_baseline`` of each workload is the oracle's NumPy form of the same
 kernel (the reference's CPU path) timed on the host on a bounded sample;
@@ -30,7 +36,7 @@ run of this script can be split per workload and per launch position;
 ``python bench.py --summarize DIR`` prints those summaries (no GPU needed).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--configs 1,2,3,4,5] [--mark-sections] [--calibrate-copy]
+                       [--configs 1,2,3,4,5,6] [--mark-sections] [--calibrate-copy]
        python bench.py --summarize DIR [--traffic-json PATH]
 """
 
@@ -65,6 +71,7 @@ LA_B, LA_H, LA_T, LA_D = 4, 16, 8192, 128
 DEC_B, DEC_S, DEC_HQ, DEC_HKV, DEC_D, DEC_F = 8, 2048, 32, 8, 128, 14336
 DEC_HID = DEC_HQ * DEC_D
 DEC_M = DEC_B * DEC_S
+QP_B, QP_S, QP_MAXS, QP_HQ, QP_HKV = 1, 2048, 4096, 32, 8
 
 
 def _linattn_prefix_bytes():
@@ -94,6 +101,7 @@ def sections():
             ("mlp_norm", "hbm", norm_bytes),
             ("gate_up_swiglu", "mfma", 2 * 2 * DEC_M * DEC_HID * DEC_F),
             ("down_proj_residual", "mfma", 2 * DEC_M * DEC_F * DEC_HID)]),
+        6: ("qwen3_prefill_attention", [("attention", "mfma", 4 * QP_B * QP_HQ * QP_S * QP_S * DEC_D // 2)]),
         9: ("copy_calibration", [("copy16", "hbm", 2 * 2**30)]),
     }
 
@@ -167,23 +175,30 @@ def _time_steps(bounds, steps, warmup, rt):
 
 
 def _time_in_step(bounds, reps, rt):
-    """Mean microseconds of each launch of a step: HIP events between the
-    launches of whole steps, over rotating buffer sets."""
+    """Mean microseconds of each launch of a step.  One whole step per buffer
+    set first produces every intermediate; then launch i runs ``reps`` times
+    back to back over the sets, with HIP events around that run only (an
+    event between two launches adds a marker's latency to the shorter
+    kernels).  A launch that writes over its own input reads its previous
+    result: the kernels' work does not depend on the values."""
     n = len(bounds[0].launches)
-    sums = [0.0] * n
-    evs = [rt.event() for _ in range(n + 1)]
-    for r in range(reps):
-        b = bounds[r % len(bounds)]
-        evs[0].record()
-        for i in range(n):
-            b.run_range(i, i + 1)
-            evs[i + 1].record()
+    for b in bounds:
+        b.run()
+    rt.sync()
+    out = []
+    e0, e1 = rt.event(), rt.event()
+    for i in range(n):
+        for r in range(2):
+            bounds[r % len(bounds)].run_range(i, i + 1)
+        e0.record()
+        for r in range(reps):
+            bounds[r % len(bounds)].run_range(i, i + 1)
+        e1.record()
         rt.sync()
-        for i in range(n):
-            sums[i] += evs[i].elapsed_ms(evs[i + 1])
-    for e in evs:
-        e.destroy()
-    return [s / reps * 1e3 for s in sums]
+        out.append(e0.elapsed_ms(e1) / reps * 1e3)
+    e0.destroy()
+    e1.destroy()
+    return out
 
 
 def _shape_of(launch):
@@ -515,7 +530,66 @@ def bench_decoder(a, rt, mk):
                  "sample": f"1 of {B} sequences ({S} tokens, fp32 NumPy with OpenBLAS matmuls, weights "
                            f"dequantized per call like the NumPy kernel), one run ({t:.2f} s); host has "
                            f"{_host_cores()} cores"},
-                _parity(dt.to_float32(outs[0].numpy()[0:1]), ref, atol=np.inf))
+                _decoder_parity(dt.to_float32(outs[0].numpy()[0:1]), ref))
+
+    return entry, cpu
+
+
+def _decoder_parity(got, ref):
+    """End to end through eight bf16 cast points: the floor 2e-2 x RMS, and
+    (recorded beside it) the reference's absolute tolerance 1e-2
+    (tests/utils.py:19-25) with the bf16 rtol 2e-2."""
+    par = _parity(got, ref, atol=np.inf)
+    tight = _parity(got, ref, atol=1e-2)
+    par["atol_1e-2"] = {"bar": tight["bar"], "worst_of_bar": tight["worst_of_bar"], "ok": tight["ok"]}
+    return par
+
+
+def bench_qwen3_prefill(a, rt, mk):
+    from nkipy_amd.core import dtypes as dt
+    from nkipy_amd.kernels.qwen3 import prefill_attention_kernel
+    from nkipy_amd.runtime import DeviceKernel, DeviceTensor
+
+    B, S, MAXS, Hq, Hkv, D = QP_B, QP_S, QP_MAXS, QP_HQ, QP_HKV, DEC_D
+    rng = np.random.default_rng(42)
+    q = dt.round_to_bf16(rng.standard_normal((B, S, Hq, D), dtype=np.float32))
+    ck = dt.round_to_bf16(rng.standard_normal((B, MAXS, Hkv, D), dtype=np.float32))
+    cv = dt.round_to_bf16(rng.standard_normal((B, MAXS, Hkv, D), dtype=np.float32))
+    args = [dt.to_bf16(v) for v in (q, ck, cv)]
+    dk = DeviceKernel.compile_and_load(prefill_attention_kernel, *args, name="qwen3_prefill_attention")
+    if dk.plan.kernel_kinds != ["attention"]:
+        raise RuntimeError(f"Qwen3 prefill attention did not lower to one kernel: {dk.plan.kernel_kinds}")
+    names = list(dk.input_tensors_info)
+    sets = [[DeviceTensor.from_numpy(v, name=n) for n, v in zip(names, args)]
+            + [DeviceTensor.empty((B, S, Hq, D), dt.bfloat16, name="output0")] for _ in range(3)]
+    bounds = [dk.executor.bind({**{n: t.ptr for n, t in zip(names, s[:3])}, "output0": s[3].ptr}) for s in sets]
+    steps, warm = max(10, a.steps // 10), max(2, a.warmup // 5)
+    mk.mark(6)
+    ms = _time_steps(bounds, steps, warm, rt)
+    recs = _kernel_records(6, bounds[0].launches, [ms * 1e3])
+    entry = {"config": 6, "workload": "qwen3_prefill_attention",
+             "shape": {"batch": B, "seq": S, "cache_rows": MAXS, "heads": Hq, "kv_heads": Hkv, "head_dim": D},
+             "dtype": "bf16 (scores rounded to bf16 after the product and the divide by sqrt(d))",
+             "us_per_step": round(ms * 1e3, 2), "roofline": _roofline(6, recs[0]), "kernels": recs,
+             "note": "causal flops (keys 0..s for query s); cache rows past S are masked and not read"}
+
+    def cpu():
+        from oracle import kernels as K
+
+        rows = np.arange(0, S, 64)  # 32 query rows, across the causal range
+        K.qwen3_prefill_attention(q, ck, cv, rows=rows[:1])
+        t, ts, ref = _timed(lambda: K.qwen3_prefill_attention(q, ck, cv, rows=rows), 3)
+        f = sum(4 * Hq * (int(r) + 1) * D for r in rows) * B
+        got = dt.to_float32(sets[0][3].numpy())[:, rows]
+        par = _parity(got, ref)
+        rms = np.sqrt(np.mean(np.asarray(ref, np.float64) ** 2, axis=-1, keepdims=True))
+        par["worst_of_bar_per_row_rms"] = round(float(np.max(
+            np.abs(got - ref) / (2e-2 * np.abs(ref) + np.minimum(1e-2, 2e-2 * rms)))), 4)
+        return ({"value": round(f / t / 1e12, 4), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+                 "sample": f"{len(rows)} of {S} query rows, all heads (NumPy op-by-op bf16 emulation over "
+                           f"the {MAXS}-row cache), median of {len(ts)} runs ({sum(ts):.2f} s); host has "
+                           f"{_host_cores()} cores",
+                 "ms_full_equiv": round(t * S / len(rows) * 1e3, 1)}, par)
 
     return entry, cpu
 
@@ -669,7 +743,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--configs", default="1,2,3,4,5")
+    ap.add_argument("--configs", default="1,2,3,4,5,6")
     ap.add_argument("--mark-sections", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 1 GiB streaming copy (calibrates HBM traffic counters)")
@@ -696,7 +770,8 @@ def main():
     if a.calibrate_copy:
         calibrate_copy(rt, mk)
 
-    benches = {1: bench_softmax, 2: bench_rmsnorm, 3: bench_swiglu, 4: bench_linattn, 5: bench_decoder}
+    benches = {1: bench_softmax, 2: bench_rmsnorm, 3: bench_swiglu, 4: bench_linattn, 5: bench_decoder,
+               6: bench_qwen3_prefill}
     entries, legs = {}, {}
     for cid in sorted(want):
         e, leg = benches[cid](a, rt, mk)
@@ -740,6 +815,7 @@ def main():
         "cpu_baseline": head["cpu_baseline"],
         "parity_ok": head["parity"]["ok"] if head["parity"] else None,
         "decoder_layer_fp8_us": entries[5]["value"] if 5 in entries else None,
+        "qwen3_prefill_attention_us": entries[6]["us_per_step"] if 6 in entries else None,
         "configs": [entries[c] for c in sorted(entries)],
     }
     print(json.dumps(line), flush=True)

@@ -58,7 +58,13 @@ struct AttnArgs {
   int32_t B, S, Hq, Hkv;
   float scale;
   int32_t causal;
+  // score cast points of the *_xf kernels (ATT_* flags): the product rounded
+  // to bf16, divided by `div` (rdiv = RN(1 / div)) instead of multiplied by
+  // `scale`, the scaled score rounded to bf16
+  float div, rdiv;
+  int32_t flags;
 };
+enum { ATT_RND_PROD = 1, ATT_RND_SCORE = 2, ATT_DIVIDE = 8 };
 
 // K tile row (key) r: 16-byte chunk c stored at c ^ (r & 15): the 32 rows of
 // a K fragment read hit 16 distinct bank slots (two per cycle's worth).
@@ -418,7 +424,11 @@ __device__ __forceinline__ void dma16_asm(i32x4_t r, uint32_t lds, uint32_t off)
                :: "v"(off), "s"(r), "s"(m) : "memory", "m0");
 }
 
-template <int NW>
+// XF: each score first takes the cast points the traced code applies
+// before its softmax (the Qwen3 prefill form, examples/models/qwen3/kernels/
+// attention.py:119-120: (q @ k^T) in bf16, divided by sqrt(d) in fp32, cast
+// to bf16), then enters the softmax with a unit scale.
+template <int NW, bool XF = false>
 __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
   constexpr int AQW = 32 * NW;  // queries per workgroup
   constexpr int TB = 32 * AD * 2;  // one 32-key K or V tile
@@ -476,7 +486,7 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
   // m: the softmax offset in log2 units, finite so that masked scores (-inf)
   // give p = 0 and the first block (p = inf) always takes the recompute path
   float m_run = -1e30f, l_run = 0.f;
-  const float sl2 = a.scale * 1.44269504088896340736f;
+  const float sl2 = XF ? 1.44269504088896340736f : a.scale * 1.44269504088896340736f;
 
   // key blocks: the workgroup's (the last wave's causal extent) and this wave's
   const int nb_wg = a.causal ? (q0 + AQW) / 32 : a.S / 32;
@@ -572,6 +582,24 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
   // klim (the query itself when causal, else the last key) get p = 0
   const int klim = a.causal ? qrow : a.S - 1;
   auto softmax = [&](f32x16 &s, bf16x8_t (&pf)[2], int kb, auto masktag) __attribute__((always_inline)) {
+    if constexpr (XF) {
+      // uniform branches: every lane takes the same cast points
+      if (a.flags & ATT_RND_PROD) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = bf16_to_f32(f32_to_bf16(s[r]));
+      }
+      if (a.flags & ATT_DIVIDE) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = div_rn(s[r], a.div, a.rdiv);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] *= a.scale;
+      }
+      if (a.flags & ATT_RND_SCORE) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = bf16_to_f32(f32_to_bf16(s[r]));
+      }
+    }
     if constexpr (decltype(masktag)::value) {
       // element r holds key kb * 32 + 4 lhi + (8 (r / 4) + r % 4)
       const int t = klim - kb * 32 - lhi * 4;
@@ -711,6 +739,9 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
 // (launch bounds: threads per workgroup, minimum waves per SIMD)
 extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128_sp(AttnArgs a) {
   attention_sp_body<4>(a);
+}
+extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128_sp_xf(AttnArgs a) {
+  attention_sp_body<4, true>(a);
 }
 extern "C" __global__ __launch_bounds__(512, 1) void nk_attention_causal_d128_sp8(AttnArgs a) {
   attention_sp_body<8>(a);

@@ -499,19 +499,32 @@ class AttnArgs(ctypes.Structure):
                 ("o", ctypes.c_void_p)] + \
         [(f"{t}_{s}", ctypes.c_int64) for t in "qkvo" for s in ("sb", "ss", "sh")] + \
         [("B", ctypes.c_int32), ("S", ctypes.c_int32), ("Hq", ctypes.c_int32),
-         ("Hkv", ctypes.c_int32), ("scale", ctypes.c_float), ("causal", ctypes.c_int32)]
+         ("Hkv", ctypes.c_int32), ("scale", ctypes.c_float), ("causal", ctypes.c_int32),
+         ("div", ctypes.c_float), ("rdiv", ctypes.c_float), ("flags", ctypes.c_int32)]
+
+
+# score cast points of the traced code before its softmax (the values of the
+# decode kernel's DEC_* flags)
+ATT_RND_PROD, ATT_RND_SCORE, ATT_DIVIDE = 1, 2, 8
 
 
 def attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, B: int, S: int, Hq: int, Hkv: int,
               D: int, scale: float, strides: dict, causal: bool = True, waves: int = None,
-              key_block: int = None, ring: bool = None) -> Launch:
+              key_block: int = None, ring: bool = None, score_flags: int = 0,
+              divisor: float = None) -> Launch:
     """Flash-style attention over bf16 q (B, S, Hq, D), k / v (B, S, Hkv, D) and
     o (B, S, Hq, D), each addressed by element strides {"q": (sb, ss, sh), ...}
     with the head dim contiguous.  KV head of query head h is h // (Hq // Hkv).
     ``waves`` (4 or 8) waves of 32 queries share a workgroup's K / V tiles;
     ``key_block`` (64 or 32) keys per step.  Variants: (4, 64), (8, 64) and
     (4, 32), the last with three workgroups per CU; ``ring`` selects the
-    software-pipelined (4, 32) kernel over a four-slot K / V ring."""
+    software-pipelined (4, 32) kernel over a four-slot K / V ring.
+
+    ``score_flags`` (ATT_*) give each score the traced code's cast points
+    before the softmax: ATT_RND_PROD rounds q.k to bf16, ATT_DIVIDE divides
+    by ``divisor`` (fp32, correctly rounded quotient) instead of multiplying
+    by ``scale``, ATT_RND_SCORE rounds the scaled score to bf16.  Any flag
+    selects the ring kernel's score-transform variant (4 waves)."""
     if D != 128:
         raise LaunchError(f"attention kernel is built for head_dim 128, got {D}")
     if S % 128 or S <= 0:
@@ -529,10 +542,22 @@ def attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, B: int, S: int, Hq
         raise LaunchError("attention kernel needs a positive score scale")
     if S * max(strides["k"][1], strides["v"][1], 128) * 2 >= 2**31:
         raise LaunchError("attention K / V rows of one sequence must span less than 2 GiB")
+    if score_flags & ~(ATT_RND_PROD | ATT_RND_SCORE | ATT_DIVIDE):
+        raise LaunchError(f"unknown attention score flags {score_flags:#x}")
     vals = [q_ptr, k_ptr, v_ptr, o_ptr]
     for name in "qkvo":
         vals += list(strides[name])
-    args = AttnArgs(*vals, B, S, Hq, Hkv, float(scale), 1 if causal else 0)
+    div = np.float32(1.0)
+    if score_flags & ATT_DIVIDE:
+        div = np.float32(divisor if divisor is not None else 1.0 / scale)
+        if not (np.isfinite(div) and div > 0):
+            raise LaunchError("attention score divisor must be finite and positive")
+    args = AttnArgs(*vals, B, S, Hq, Hkv, float(scale), 1 if causal else 0, float(div),
+                    float(np.float32(1.0) / np.float32(div)), int(score_flags))
+    if score_flags:
+        if (waves or 4, key_block or 32, True if ring is None else ring) != (4, 32, True):
+            raise LaunchError("attention score cast points exist on the 4-wave ring kernel only")
+        waves, key_block, ring = 4, 32, True
     # default: 4 waves, 32-key blocks (three workgroups per CU); measured at
     # (8, 2048, 32 / 8 heads) 319.5 us mean of eight runs against 328 us for
     # (4, 64) and 326 us for (8, 64)
@@ -553,7 +578,7 @@ def attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, B: int, S: int, Hq
     if nblocks >= 2**31:
         raise LaunchError("attention grid too large")
     flops = 4 * B * Hq * S * S * D // (2 if causal else 1)
-    sym = "nk_attention_causal_d128" + suffix
+    sym = "nk_attention_causal_d128" + suffix + ("_xf" if score_flags else "")
     return Launch("attention", sym, (nblocks, 1, 1), (64 * waves, 1, 1), args,
                   bytes=(2 * B * S * Hq * D + 2 * B * S * Hkv * D) * 2, flops=flops)
 

@@ -343,11 +343,14 @@ class QkvRopeFusion:
 class AttentionMatch(Match):
     name = "attention"
 
-    def __init__(self, nodes, q: View, k: View, v: View, out: Value, dims, scale, causal, o_str):
+    def __init__(self, nodes, q: View, k: View, v: View, out: Value, dims, scale, causal, o_str,
+                 score_flags: int = 0, divisor: float = None, keys: int = None):
         ins = list(dict.fromkeys([q.base, k.base, v.base]))
         super().__init__(nodes, ins, [out])
         self.q, self.k, self.v, self.out = q, k, v, out
         self.dims, self.scale, self.causal, self.o_str = dims, scale, causal, o_str
+        self.score_flags, self.divisor = score_flags, divisor
+        self.keys = keys if keys is not None else dims[1]
 
     def steps(self, plan):
         q, k, v, out = self.q, self.k, self.v, self.out
@@ -356,9 +359,14 @@ class AttentionMatch(Match):
         def make(addr):
             return LA.attention(addr(q.base) + 2 * q.offset, addr(k.base) + 2 * k.offset,
                                 addr(v.base) + 2 * v.offset, addr(out), B, S, Hq, Hkv, D,
-                                self.scale, dict(strides, o=self.o_str), causal=self.causal)
+                                self.scale, dict(strides, o=self.o_str), causal=self.causal,
+                                score_flags=self.score_flags, divisor=self.divisor)
 
         desc = f"{'causal ' if self.causal else ''}attention B={B} S={S} Hq={Hq} Hkv={Hkv} D={D}"
+        if self.keys != S:
+            desc += f" keys<{S} of {self.keys}"
+        if self.score_flags:
+            desc += f" score_flags={self.score_flags}"
         return [LaunchStep("attention", desc, self.inputs, self.outputs, make)]
 
 
@@ -370,6 +378,19 @@ def _qk_dot(n: Node) -> bool:
 
 
 class AttentionPattern:
+    """Prefill attention in two traced forms:
+
+    * fp32 scores (tests/kernels/llama_decoder_dynamo.py:180-288): the
+      product (bf16 operands, fp32 result) scaled, plus an (S, S) causal
+      mask, fp32 softmax;
+    * bf16 scores over a KV cache (examples/models/qwen3/kernels/
+      attention.py:109-140): the product rounded to bf16, divided by sqrt(d)
+      in fp32, rounded to bf16, plus the mask rows [:S, :MAXS] of a constant
+      (MAXS, MAXS) triu mask (cast to bf16), softmax in bf16, @ v over all
+      MAXS cache rows.  Keys at S and beyond are masked for every query, so
+      the kernel reads the first S cache rows only; the cast points of the
+      score go to the kernel as ATT_* flags."""
+
     def find(self, L):
         for n in L.live:
             if id(n) in L.covered or not _qk_dot(n):
@@ -379,36 +400,65 @@ class AttentionPattern:
                 yield m
 
     @staticmethod
-    def _scaled(v: Value):
-        """v = dot * c | c * dot | dot / c -> (dot node, scale, nodes)."""
-        if op_of(v) == "dot":
-            return v.node, 1.0, []
-        if op_of(v) == "multiply":
-            for d, c in (v.node.inputs, v.node.inputs[::-1]):
-                cv, cn = scalar_value(c)
-                if cv is not None and op_of(d) == "dot":
-                    return d.node, cv, [v.node] + cn
-        if op_of(v) == "divide":
-            d, c = v.node.inputs
-            cv, cn = scalar_value(c)
-            if cv is not None and cv != 0 and op_of(d) == "dot":
-                return d.node, 1.0 / cv, [v.node] + cn
-        return None
-
-    @staticmethod
-    def _mask(v: Value, S: int):
-        """An additive causal mask over (b, h, s, t) -> view, or None."""
+    def _mask(v: Value, S: int, Sk: int):
+        """An additive causal mask over (b, h, s, t), t < Sk -> (view, cast
+        node or None), or None.  Its base is a constant, or a constant cast
+        to a float type (which keeps zeros and values <= MASK_LIMIT)."""
         mv = resolve(v, widen_ok=False)
-        payload = _const_payload(mv.base)
-        if payload is None or mv.shape[-2:] != (S, S):
+        cast, base = None, mv.base
+        if op_of(base) == "convert" and op_of(base.node.inputs[0]) == "constant" and \
+                base.dtype in (dt.float32, dt.bfloat16, dt.float16):
+            cast, base = base.node, base.node.inputs[0]
+        payload = _const_payload(base)
+        if payload is None or mv.shape[-2:] != (S, Sk) or Sk < S:
             return None
         if mv.simple(0) != 0 or mv.simple(1) != 0:
             return None
-        m = mv.materialize_check(payload.reshape(mv.base.shape))[0, 0]
-        lower = np.tril(np.ones((S, S), bool))
+        m = mv.materialize_check(payload.reshape(base.shape))[0, 0]
+        lower = np.tril(np.ones((S, Sk), bool))
         if np.any(m[lower] != 0) or np.any(m[~lower] > MASK_LIMIT):
             return None
-        return mv
+        return mv, cast
+
+    @staticmethod
+    def _score_chain(v: Value):
+        """The score before the mask -> (dot node, scale, divisor, flags,
+        nodes): [convert bf16] <- (multiply | divide by a scalar) <-
+        [convert f32] <- dot, or the fp32 form without casts."""
+        flags, nodes = 0, []
+        if op_of(v) == "convert" and v.dtype == dt.bfloat16 and v.node.inputs[0].dtype == dt.float32:
+            flags |= LA.ATT_RND_SCORE
+            nodes.append(v.node)
+            v = v.node.inputs[0]
+        if v.dtype != dt.float32:
+            return None
+        scale, divisor = 1.0, None
+        if op_of(v) in ("multiply", "divide"):
+            a, c = v.node.inputs
+            if op_of(v) == "multiply" and scalar_value(a)[0] is not None:
+                a, c = c, a
+            cv, cn = scalar_value(c)
+            if cv is None or not cv > 0:
+                return None
+            if op_of(v) == "divide":
+                scale, divisor = 1.0 / cv, float(cv)
+            else:
+                scale = float(cv)
+            nodes += [v.node] + cn
+            v = a
+        if op_of(v) == "convert" and v.dtype == dt.float32 and v.node.inputs[0].dtype == dt.bfloat16:
+            nodes.append(v.node)
+            v = v.node.inputs[0]
+        if op_of(v) != "dot" or not _qk_dot(v.node):
+            return None
+        d1 = v.node
+        if d1.out.dtype == dt.bfloat16:
+            flags |= LA.ATT_RND_PROD
+        elif d1.out.dtype != dt.float32:
+            return None
+        if flags and divisor is not None:
+            flags |= LA.ATT_DIVIDE
+        return d1, scale, divisor, flags, nodes
 
     def _match(self, L, n2: Node):
         p_val, kv_op = n2.inputs
@@ -416,32 +466,34 @@ class AttentionPattern:
         while op_of(p_val) in ("convert", "copy") and p_val.dtype == dt.float32:
             nodes.append(p_val.node)
             p_val = p_val.node.inputs[0]
-        if op_of(p_val) != "divide" or p_val.dtype != dt.float32:
+        if op_of(p_val) != "divide" or p_val.dtype not in (dt.float32, dt.bfloat16):
             return None
         st = SoftmaxPattern.structure(L, p_val.node)
         if st is None:
             return None
         X, smx = st
         nodes += smx
-        causal, mask_nodes = False, []
-        sc = self._scaled(X)
+        Sq, Sk = X.shape[-2], X.shape[-1]
+        causal, mask_nodes = False, None
+        sc = self._score_chain(X)
         if sc is None and op_of(X) == "add":
             for a, b in (X.node.inputs, X.node.inputs[::-1]):
-                sc = self._scaled(a)
+                sc = self._score_chain(a)
                 if sc is None:
                     continue
-                mv = self._mask(b, a.shape[-1])
-                if mv is None:
+                mk = self._mask(b, Sq, Sk)
+                if mk is None:
                     sc = None
                     continue
                 causal = True
                 nodes.append(X.node)
-                mask_nodes = (mv, b)
+                mask_nodes = mk
                 break
         if sc is None:
             return None
-        d1, scale, snodes = sc
-        if not _qk_dot(d1) or d1.out.dtype != dt.float32:
+        d1, scale, divisor, score_flags, snodes = sc
+        # a bf16 softmax runs on bf16 scores: the score must have been cast
+        if p_val.dtype == dt.bfloat16 and not score_flags & LA.ATT_RND_SCORE:
             return None
         nodes += [d1] + snodes
         q = _bf16_view(d1.inputs[0])
@@ -450,7 +502,10 @@ class AttentionPattern:
         if q is None or k is None or v is None:
             return None
         B, Hq, S, D = q.shape
-        if k.shape != (B, Hq, D, S) or v.shape != (B, Hq, S, D) or n2.out.shape != (B, Hq, S, D):
+        # keys past the queries exist only under a causal mask, which hides them
+        if Sk != S and not causal:
+            return None
+        if k.shape != (B, Hq, D, Sk) or v.shape != (B, Hq, Sk, D) or n2.out.shape != (B, Hq, S, D):
             return None
         qs = [q.simple(0), q.simple(2), q.simple(1)]
         kg, vg = k.grouped(1), v.grouped(1)
@@ -490,16 +545,27 @@ class AttentionPattern:
         try:
             LA.attention(16, 16, 16, 16, B, S, Hq, Hkv, D, scale,
                          {"q": qs, "k": (ks[0], ks[1], kg[1]), "v": (vs[0], vs[1], vg[1]), "o": o_str},
-                         causal=causal)
+                         causal=causal, score_flags=score_flags, divisor=divisor)
         except LA.LaunchError:
             return None
         if any((vw.offset * 2) % 16 for vw in (q, k, v)):
             return None
         if mask_nodes:
-            mv, b = mask_nodes
-            nodes += _owned(L, mv, {id(x) for x in nodes})
+            mv, cast = mask_nodes
+            inside = {id(x) for x in nodes}
+            chain = _owned(L, mv, inside)
+            nodes += chain
+            if cast is not None and chain:  # the cast and its constant, if only this mask reads them
+                own = inside | {id(x) for x in chain}
+                cnode = cast.inputs[0].node
+                if cast.out.id not in L.result_ids and all(id(u) in own for u in _users_of(L, cast.out)):
+                    nodes.append(cast)
+                    own.add(id(cast))
+                    if cnode.out.id not in L.result_ids and all(id(u) in own for u in _users_of(L, cnode.out)):
+                        nodes.append(cnode)
         strides = {"q": tuple(qs), "k": (ks[0], ks[1], kg[1]), "v": (vs[0], vs[1], vg[1])}
-        return AttentionMatch(nodes, q, k, v, out, (B, S, Hq, Hkv, D, strides), scale, causal, o_str)
+        return AttentionMatch(nodes, q, k, v, out, (B, S, Hq, Hkv, D, strides), scale, causal, o_str,
+                              score_flags, divisor, Sk)
 
 
 # ---------------------------------------------------------------------------

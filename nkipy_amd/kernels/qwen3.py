@@ -53,7 +53,6 @@ def qwen3_attention_kernel(x, qkv_weight, q_norm_weight, k_norm_weight, norm_eps
     position start_pos (an int32 array of shape (1,))."""
     prefill = start_pos is None
     B, S, _ = x.shape
-    n_rep = n_heads // n_kv_heads
     q_end = n_heads * head_dim
     k_end = q_end + n_kv_heads * head_dim
     xq, xk, xv = np.split(np.matmul(x, qkv_weight), [q_end, k_end], axis=x.ndim - 1)
@@ -80,22 +79,40 @@ def qwen3_attention_kernel(x, qkv_weight, q_norm_weight, k_norm_weight, norm_eps
         cache_k[:, start_pos] = xk
         cache_v[:, start_pos] = xv
 
+    out = cached_attention(xq, cache_k, cache_v, start_pos).reshape(B, S, -1)
+    return np.matmul(out, o_weight)
+
+
+def cached_attention(xq, cache_k, cache_v, start_pos=None):
+    """Attention of the queries xq (B, S, Hq, D) over the whole KV cache
+    (B, MAXS, Hkv, D), as examples/models/qwen3/kernels/attention.py:107-143
+    computes it: GQA by ``np.repeat``, scores (q @ k^T) / sqrt(D) cast to the
+    activation dtype, plus the mask rows of the current positions (rows
+    0..S-1 for prefill, row start_pos for one decode token) of a constant
+    (MAXS, MAXS) triu mask, softmax, @ values -> (B, S, Hq, D)."""
+    B, S, n_heads, head_dim = xq.shape
+    max_seq, n_kv_heads = cache_k.shape[1], cache_k.shape[2]
+    n_rep = n_heads // n_kv_heads
     keys = np.repeat(cache_k, n_rep, axis=2) if n_rep > 1 else cache_k
     values = np.repeat(cache_v, n_rep, axis=2) if n_rep > 1 else cache_v
     q = xq.transpose(0, 2, 1, 3)
     k = keys.transpose(0, 2, 1, 3)
     v = values.transpose(0, 2, 1, 3)
     scores = (q @ k.transpose(0, 1, 3, 2)) / np.float32(np.sqrt(head_dim))
-    scores = scores.astype(x.dtype)
+    scores = scores.astype(xq.dtype)
     mask = tensor_apis.constant(np.triu(np.ones((max_seq, max_seq)) * MASK_VALUE, k=1).astype(np.float32))
     mask = mask.astype(scores.dtype)
-    if prefill:
+    if start_pos is None:
         scores = scores + np.expand_dims(mask[:S, :max_seq], axis=[0, 1])
     else:
         scores = scores + np.expand_dims(mask[start_pos, :max_seq], axis=[0, 1])
     out = softmax_kernel(scores) @ v
-    out = out.transpose(0, 2, 1, 3).reshape(B, S, -1)
-    return np.matmul(out, o_weight)
+    return out.transpose(0, 2, 1, 3)
+
+
+def prefill_attention_kernel(xq, cache_k, cache_v):
+    """The prefill half of :func:`cached_attention` as a kernel of its own."""
+    return cached_attention(xq, cache_k, cache_v)
 
 
 def greedy_sampling(h, norm_weight, lm_head_weight, norm_eps):

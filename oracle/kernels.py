@@ -412,3 +412,51 @@ def decode_attention(q, cache_k, cache_v, pos, round_prod=False, round_score=Fal
                 p = r(p)
             out[b, h] = (p.astype(np.float64) @ v.astype(np.float64)).astype(np.float32)
     return out
+
+
+# ---------------------------------------------------------------------------
+# Qwen3 prefill attention over a KV cache -- examples/models/qwen3/kernels/
+# attention.py:107-140 with bf16 activations (start_pos None): keys / values
+# are the whole cache (B, MAXS, Hkv, D) with np.repeat GQA; the product q k^T
+# of bf16 operands is a bf16 array; ``/ np.float32(sqrt(D))`` promotes it to
+# fp32, ``.astype(bf16)`` rounds the score; the mask rows [:S, :MAXS] of
+# triu(ones * -1e5, k=1) cast to bf16 are added in bf16; the softmax
+# (kernels/softmax.py:4-6) runs op by op in bf16 (max, subtract, exp, sum,
+# divide, each result rounded); the bf16 weights @ values give bf16.
+# Products accumulate in float64 and are rounded once (to fp32, then to the
+# array's dtype); the bf16 sum accumulates in fp32 and is rounded once.
+# ---------------------------------------------------------------------------
+
+
+def qwen3_prefill_attention(q, cache_k, cache_v, rows=None, round_prod=True, round_score=True,
+                            softmax_bf16=True):
+    """q (B, S, Hq, D), caches (B, MAXS, Hkv, D), bf16 values in fp32 arrays
+    -> (B, len(rows), Hq, D) fp32 holding the bf16 output values of the
+    query positions ``rows`` (all S by default).  The flags drop single cast
+    points (used to show that each one matters)."""
+    q = np.asarray(q, np.float32)
+    B, S, Hq, D = q.shape
+    MAXS, Hkv = cache_k.shape[1], cache_k.shape[2]
+    rep = Hq // Hkv
+    rows = np.arange(S) if rows is None else np.asarray(rows)
+    r = bf16_round
+    keep = r if softmax_bf16 else (lambda a: a)
+    mask = r(np.triu(np.ones((MAXS, MAXS)) * -100000, k=1).astype(np.float32))[rows, :MAXS]
+    out = np.zeros((B, len(rows), Hq, D), np.float32)
+    for b in range(B):
+        for h in range(Hq):
+            k = np.asarray(cache_k[b, :, h // rep], np.float64)
+            v = np.asarray(cache_v[b, :, h // rep], np.float64)
+            s = (q[b, rows, h].astype(np.float64) @ k.T).astype(np.float32)
+            if round_prod:
+                s = r(s)
+            s = s / np.float32(np.sqrt(D))
+            if round_score:
+                s = r(s)
+            s = r(s + mask) if round_score else s + mask
+            d = keep(s - s.max(-1, keepdims=True))
+            e = keep(np.exp(d))
+            tot = keep(e.sum(-1, keepdims=True, dtype=np.float32))
+            p = keep(e / tot)
+            out[b, :, h] = r((p.astype(np.float64) @ v).astype(np.float32))
+    return out

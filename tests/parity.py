@@ -63,6 +63,16 @@ def assert_close(got, ref, name: str, rtol: float = 2e-2, atol: float = 1e-2, fl
     return rec
 
 
+def record_close(got, ref, name: str, **kw) -> float:
+    """``assert_close``'s measurement without its assertion: records the
+    check and returns its worst error as a fraction of the bar."""
+    try:
+        assert_close(got, ref, name, **kw)
+    except AssertionError:
+        pass
+    return RECORDS[-1]["worst_of_bar"]
+
+
 def assert_rel(got, ref, name: str, tol: float):
     """fp32 bar: max |got - ref| / |ref| <= tol."""
     got = np.asarray(got, np.float64)

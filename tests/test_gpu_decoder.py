@@ -6,7 +6,7 @@ import os
 
 import numpy as np
 import pytest
-from parity import assert_close
+from parity import assert_close, record_close
 import torch
 
 from nkipy_amd.core import dtypes as dt
@@ -90,6 +90,14 @@ def _check_blocks(x, w, a, z, act, y, ref, Hq):
     # above meets the tight bar on its own)
     name = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0] + " [end to end]"
     assert_close(y, ref["y"], name, atol=np.inf)
+    # Recorded, not asserted: the reference's absolute tolerance (tests/
+    # utils.py:19-25: atol 1e-2) with the bf16 rtol 2e-2.  End to end, a
+    # change of summation order alone exceeds it (the oracle against itself
+    # with fp64 products, test_oracle.py::
+    # test_decoder_end_to_end_sensitivity_to_summation_order): a third of the
+    # bf16 SwiGLU activations move by one rounding step and the down
+    # projection sums 14336 of them.
+    record_close(y, ref["y"], name + " [atol 1e-2, recorded]", atol=1e-2, floor=np.inf)
 
 
 @pytest.mark.parametrize("shape", [(1, 128, 1, 1), (2, 256, 4, 2), (1, 384, 4, 4)])

@@ -402,3 +402,33 @@ def test_profile_ranges_need_no_device_and_reject_unbalanced_pops():
     lib = load_library()
     assert lib.nkh_profile_range_pop() != 0
     assert b"without a push" in lib.nkh_last_error()
+
+
+def test_lowering_qwen3_prefill_attention_is_one_launch():
+    """The Qwen3 prefill form (bf16 scores over the whole cache, mask rows
+    [:S, :MAXS], bf16 softmax) lowers to one attention launch with the score
+    cast points as flags; keys past S are not read."""
+    from nkipy_amd.kernels.qwen3 import prefill_attention_kernel, qwen3_attention_kernel
+
+    B, S, MAXS, Hq, Hkv, D = 1, 2048, 4096, 32, 8, 128
+    g = NKIPyKernel.trace(prefill_attention_kernel).specialize(
+        _bf16((B, S, Hq, D)), _bf16((B, MAXS, Hkv, D)), _bf16((B, MAXS, Hkv, D)))
+    plan = lower(g)
+    assert plan.kernel_kinds == ["attention"]
+    ((launch,),) = [st.launches(lambda v: 1 << 40) for st in plan.steps]
+    assert launch.symbol == "nk_attention_causal_d128_sp_xf"
+    a = launch.args
+    assert a.flags == LA.ATT_RND_PROD | LA.ATT_RND_SCORE | LA.ATT_DIVIDE and a.S == S and a.causal == 1
+    assert np.float32(a.div) == np.float32(np.sqrt(D))
+    # the whole layer: no score matrix, no generic products or softmax
+    hid = 512
+    kinds = _kinds(qwen3_attention_kernel, _bf16((2, 256, hid)), _bf16((hid, 8 * D)), _bf16((D,)), _bf16((D,)),
+                   1e-6, 4, D, 2, _bf16((2, 512, 2, D)), _bf16((2, 512, 2, D)), None, _bf16((4 * D, hid)))
+    assert "attention" in kinds and "dot" not in kinds and "softmax" not in kinds, kinds
+    # fp32 scores (the Llama form) keep the plain kernel
+    from nkipy_amd.kernels import causal_gqa_attention_kernel
+
+    q = _bf16((1, 256, 8, 128))
+    g = NKIPyKernel.trace(causal_gqa_attention_kernel).specialize(q, q, q)
+    ((launch,),) = [st.launches(lambda v: 1 << 40) for st in lower(g).steps]
+    assert launch.symbol == "nk_attention_causal_d128_sp" and launch.args.flags == 0
