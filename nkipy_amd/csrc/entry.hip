@@ -79,7 +79,7 @@ int launch_linattn(const void *q, const void *k, const void *v, void *o, int64_t
   const LinAttnSplit s = linattn_split(BH, T);
   if (s.nranges) {
     LinAttnStateArgs sa{static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v), part, BH, T,
-                        (int32_t)s.nranges, (int32_t)s.rchunks};
+                        (int32_t)s.nranges, (int32_t)s.rchunks, nullptr};
     void *args[] = {&sa};
     hipError_t e = hipLaunchKernel(reinterpret_cast<const void *>(&nk_linattn_state_c64_d128),
                                    dim3((unsigned)(BH * s.nranges)), dim3(512), args, 0, stream);
@@ -87,7 +87,7 @@ int launch_linattn(const void *q, const void *k, const void *v, void *o, int64_t
   }
   LinAttnArgs a{static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k),
                 static_cast<const uint16_t *>(v), static_cast<uint16_t *>(o),
-                s.nranges ? part : nullptr, BH, T, (int32_t)s.nseg, (int32_t)s.rchunks};
+                s.nranges ? part : nullptr, BH, T, (int32_t)s.nseg, (int32_t)s.rchunks, nullptr};
   void *args[] = {&a};
   hipError_t e = hipLaunchKernel(reinterpret_cast<const void *>(&nk_linattn_c64_d128),
                                  dim3((unsigned)(BH * s.nseg)), dim3(512), args, 0, stream);

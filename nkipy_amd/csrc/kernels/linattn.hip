@@ -55,7 +55,12 @@
 // normaliser share one power-of-two scale (exact) and the quotient is
 // unchanged; the copies stay finite while |S|, z and A are below 2^24
 // (e.g. v of mean 8 over 2^21 tokens).  V and phi(K) enter as fp16 inputs:
-// |v| and k must stay below 65504.
+// |v| and k must stay below 65504.  At the small end, V and S / 256 go
+// subnormal in fp16 when a sequence's |v| is tiny (max |v| below ~1e-4:
+// the output then loses relative precision, while the fp32 recurrence does
+// not).  The scan therefore reports each sequence's max |v| (bf16 bits,
+// `vmax`) so that the caller can reject sequences outside the window
+// instead of returning a silently degraded result.
 
 #include "common.h"
 
@@ -82,6 +87,11 @@ struct LinAttnArgs {
   int64_t T;          // sequence length (multiple of 64 * nseg)
   int32_t nseg;       // sequence segments per head, run concurrently
   int32_t rchunks;    // chunks per partial-sum range (divides T / 64 / nseg)
+  // max |v| of each sequence as bf16 bits (BH words), or null: written by
+  // the single workgroup of a sequence (nseg == 1) or combined by atomic
+  // max over its segments (nseg > 1, after nk_linattn_state_c64_d128 has
+  // cleared the word)
+  uint32_t *vmax;
 };
 
 // Partial state sums over ranges of rchunks chunks: for head bh and range r,
@@ -97,6 +107,7 @@ struct LinAttnStateArgs {
   int64_t T;
   int32_t nranges;  // R
   int32_t rchunks;
+  uint32_t *vmax;   // cleared (BH words) for the scan's atomic max, or null
 };
 
 // Byte offsets in the LDS tiles, bank-conflict free for every access below
@@ -198,6 +209,7 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
   // A operand reads z in lanes l16 == 0 and zeros elsewhere
   __shared__ __attribute__((aligned(16))) uint8_t Z0[LD * 4];
   __shared__ __attribute__((aligned(16))) uint8_t Z1[LD * 4];
+  __shared__ uint32_t vred[512];  // per-thread max |v| bits (with a.vmax)
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -247,8 +259,24 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
 #pragma unroll
     for (int st = 0; st < 4; ++st) qf[st] = __builtin_bit_cast(f16x8_t, phi8(r.x[st]));
   };
+  // max |v| bits of this thread's v elements, kept in its own LDS word
+  // (an atomic max without return: no register stays live across the loop):
+  // two bf16 per 32-bit lane of a packed 16-bit integer max, since
+  // magnitudes compare as integers
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
   // phi(K) and V of the next chunk into LDS
   auto stage_in = [&](const Raw &r, const Stage &s) {
+    if (a.vmax) {
+      u16x2 m = __builtin_bit_cast(u16x2, r.v[0].x & 0x7fff7fffu);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        if (i) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, r.v[i].x & 0x7fff7fffu));
+        m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, r.v[i].y & 0x7fff7fffu));
+        m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, r.v[i].z & 0x7fff7fffu));
+        m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, r.v[i].w & 0x7fff7fffu));
+      }
+      atomicMax(&vred[tid], (uint32_t)(m[0] > m[1] ? m[0] : m[1]));
+    }
     if (!qwave) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -439,6 +467,7 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
   };
 
   const Stage s0{K0, V0, ST0, Z0}, s1{K1, V1, ST1, Z1};
+  vred[tid] = 0u;  // before the first stage_in, in this thread's own word
   if (!qwave) write_state(s0, wave - 4);  // initial S^T and z / 256
   if (tid < 32) *reinterpret_cast<uint4 *>((tid < 16 ? Z0 : Z1) + LD * 2 + 16 * (tid & 15)) = make_uint4(0, 0, 0, 0);
   Raw ra{}, rb{};
@@ -471,6 +500,27 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_c64_d128(LinAttn
     case 3: run(Int<3>{}); break;
     default: run(Int<4>{}); break;
   }
+  if (a.vmax) {
+    // the workgroup's max |v| (every v of the segment passed stage_in)
+    __shared__ uint32_t red[8];
+    __syncthreads();
+    uint32_t m = vred[tid];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const uint32_t o = (uint32_t)__shfl_xor((int)m, off, 64);
+      m = o > m ? o : m;
+    }
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    if (tid == 0) {
+#pragma unroll
+      for (int w = 1; w < 8; ++w) m = red[w] > m ? red[w] : m;
+      if (a.nseg == 1)
+        a.vmax[bh] = m;
+      else
+        atomicMax(a.vmax + bh, m);
+    }
+  }
 }
 
 // Partial states of ranges of rchunks chunks (the prefix of later segments):
@@ -494,6 +544,7 @@ extern "C" __global__ __launch_bounds__(512, 1) void nk_linattn_state_c64_d128(L
   const int64_t rr = unit % a.nranges;
   const int64_t bh = unit / a.nranges;
   const int64_t base = bh * a.T * LD + rr * a.rchunks * LC * LD;
+  if (a.vmax && rr == 0 && tid == 0) a.vmax[bh] = 0u;
 
   f32x16 S[2], Z;
 #pragma unroll

@@ -135,7 +135,7 @@ class RelocatablePlan:
     kernel's I/O contract; drop-in for :class:`Plan` in an executor."""
 
     def __init__(self, *, name, buffers, input_buffers, output_buffers, alias_outputs, steps, records, io,
-                 modules, lowering):
+                 modules, lowering, checks=()):
         self.name = name
         self.buffers: List[BufferSpec] = buffers
         self.input_buffers: Dict[str, int] = input_buffers
@@ -146,6 +146,7 @@ class RelocatablePlan:
         self.io: dict = io
         self.modules: Dict[str, Optional[str]] = modules
         self.lowering = lowering
+        self.checks: List[dict] = [dict(c) for c in checks]
 
     # -- Plan-like surface ---------------------------------------------
     @property
@@ -202,7 +203,8 @@ class RelocatablePlan:
         return cls(name=plan.graph.name, buffers=list(plan.buffers), input_buffers=dict(plan.input_buffers),
                    output_buffers=dict(plan.output_buffers), alias_outputs=dict(plan.alias_outputs),
                    steps=[{"kind": s["kind"], "desc": s["desc"]} for s in plan.describe()["steps"]],
-                   records=records, io=io, modules=modules, lowering=lowering_digest())
+                   records=records, io=io, modules=modules, lowering=lowering_digest(),
+                   checks=list(getattr(plan, "checks", ())))
 
     # -- binding ---------------------------------------------------------
     def blobs(self, bases: Dict[int, int]) -> List[bytes]:
@@ -240,7 +242,7 @@ class RelocatablePlan:
             "format": FORMAT, "backend": BACKEND_ID, "lowering": self.lowering, "modules": self.modules,
             "name": self.name, "io": self.io, "buffers": bufs,
             "input_buffers": self.input_buffers, "output_buffers": self.output_buffers,
-            "alias_outputs": self.alias_outputs, "steps": self.step_info,
+            "alias_outputs": self.alias_outputs, "steps": self.step_info, "checks": self.checks,
             "launches": [{"kind": r.kind, "module": r.module, "symbol": r.symbol, "grid": list(r.grid),
                           "block": list(r.block), "shared": r.shared, "args": r.blob.hex(),
                           "relocs": [list(x) for x in r.relocs], "bytes": r.bytes, "flops": r.flops}
@@ -271,7 +273,7 @@ class RelocatablePlan:
         return cls(name=doc["name"], buffers=bufs, input_buffers={k: int(v) for k, v in doc["input_buffers"].items()},
                    output_buffers={k: int(v) for k, v in doc["output_buffers"].items()},
                    alias_outputs=dict(doc["alias_outputs"]), steps=doc["steps"], records=records, io=doc["io"],
-                   modules=doc["modules"], lowering=doc["lowering"])
+                   modules=doc["modules"], lowering=doc["lowering"], checks=doc.get("checks", []))
 
 
 def io_contract(graph) -> dict:

@@ -399,13 +399,14 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
 class LinAttnArgs(ctypes.Structure):
     _fields_ = [("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
                 ("o", ctypes.c_void_p), ("part", ctypes.c_void_p), ("BH", ctypes.c_int64),
-                ("T", ctypes.c_int64), ("nseg", ctypes.c_int32), ("rchunks", ctypes.c_int32)]
+                ("T", ctypes.c_int64), ("nseg", ctypes.c_int32), ("rchunks", ctypes.c_int32),
+                ("vmax", ctypes.c_void_p)]
 
 
 class LinAttnStateArgs(ctypes.Structure):
     _fields_ = [("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("part", ctypes.c_void_p),
                 ("BH", ctypes.c_int64), ("T", ctypes.c_int64), ("nranges", ctypes.c_int32),
-                ("rchunks", ctypes.c_int32)]
+                ("rchunks", ctypes.c_int32), ("vmax", ctypes.c_void_p)]
 
 
 LINATTN_CHUNK = 64
@@ -452,16 +453,26 @@ def linear_attention_workspace_bytes(BH: int, T: int, ranges_per_segment: int = 
     return BH * nranges * (LINATTN_D + 1) * LINATTN_D * 4
 
 
+# The fp16 operand window of the kernel (csrc/kernels/linattn.hip): a
+# sequence whose largest |v| is below 2^-13 has its V and S / 256 operands
+# in the fp16 subnormal range (relative precision lost); 65536 and above
+# overflow fp16.  bf16 bit patterns of those bounds:
+LINATTN_VMAX_LOW_BITS = 0x3900   # 2^-13
+LINATTN_VMAX_HIGH_BITS = 0x4780  # 65536 (the first bf16 value fp16 cannot hold)
+
+
 def linear_attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, BH: int, T: int,
                      D: int = 128, Dv: int = 128, chunk: int = 64, part_ptr: int = 0,
-                     ranges_per_segment: int = None) -> List[Launch]:
+                     ranges_per_segment: int = None, vmax_ptr: int = 0) -> List[Launch]:
     """o = causal linear attention with phi = elu + 1 over (BH, T, D) bf16
     sequences, chunk 64, head dims 128 (the compiled variant).
 
     Returns the launches in order: when the sequences are cut into segments,
     a partial-sum kernel writes the prefix states into ``part_ptr`` (a
     workspace of :func:`linear_attention_workspace_bytes` bytes) before the
-    scan reads them."""
+    scan reads them.  With ``vmax_ptr`` (BH uint32 words) the scan writes
+    each sequence's max |v| as bf16 bits there, for
+    :func:`check_linear_attention_vmax` after the launches complete."""
     if (D, Dv, chunk) != (LINATTN_D, LINATTN_D, LINATTN_CHUNK):
         raise LaunchError(f"linear attention kernel is built for d = d_v = 128, chunk 64; "
                           f"got d={D}, d_v={Dv}, chunk={chunk}")
@@ -477,18 +488,49 @@ def linear_attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, BH: int, T:
                           f"workspace of {linear_attention_workspace_bytes(BH, T, ranges_per_segment)} bytes")
     if part_ptr % 16:
         raise LaunchError("linear attention workspace must be 16-byte aligned")
+    if vmax_ptr % 4:
+        raise LaunchError("linear attention max |v| words must be 4-byte aligned")
     n = T // chunk
     flops_chunk = 2 * chunk * chunk * D + 2 * chunk * D * Dv + 2 * chunk * chunk * Dv + 2 * D * Dv * chunk
     launches = []
     if nranges:
         launches.append(Launch("linattn", "nk_linattn_state_c64_d128", (BH * nranges, 1, 1),
-                               (512, 1, 1), LinAttnStateArgs(k_ptr, v_ptr, part_ptr, BH, T, nranges, rchunks),
+                               (512, 1, 1),
+                               LinAttnStateArgs(k_ptr, v_ptr, part_ptr, BH, T, nranges, rchunks, vmax_ptr or None),
                                bytes=2 * BH * nranges * rchunks * chunk * D * 2,
                                flops=BH * nranges * rchunks * 2 * chunk * D * Dv))
     launches.append(Launch("linattn", "nk_linattn_c64_d128", (BH * nseg, 1, 1), (512, 1, 1),
-                           LinAttnArgs(q_ptr, k_ptr, v_ptr, o_ptr, part_ptr or None, BH, T, nseg, rchunks),
+                           LinAttnArgs(q_ptr, k_ptr, v_ptr, o_ptr, part_ptr or None, BH, T, nseg, rchunks,
+                                       vmax_ptr or None),
                            bytes=4 * BH * T * D * 2, flops=BH * n * flops_chunk))
     return launches
+
+
+class LinearAttentionRangeError(ValueError):
+    """Values of v outside the fp16 operand window of the linear-attention
+    kernel: the result is not within the kernel's accuracy."""
+
+
+def check_linear_attention_vmax(words: np.ndarray, what: str = "linear attention"):
+    """Raise LinearAttentionRangeError naming the sequences whose max |v|
+    (bf16 bits, as the scan reports them) lies outside the kernel's fp16
+    operand window.  All-zero sequences are exact (o = 0) and pass."""
+    bits = np.asarray(words, np.uint32)
+    low = np.nonzero((bits > 0) & (bits < LINATTN_VMAX_LOW_BITS))[0]
+    high = np.nonzero(bits >= LINATTN_VMAX_HIGH_BITS)[0]
+    if not len(low) and not len(high):
+        return
+    val = lambda b: float(np.array([int(b) << 16], np.uint32).view(np.float32)[0])
+    parts = []
+    if len(low):
+        parts.append(f"{len(low)} sequence(s) (first: {int(low[0])}, max |v| {val(bits[low[0]]):.3g}) have max |v| "
+                     f"below 2^-13, where v and the running state go subnormal in the kernel's fp16 operands")
+    if len(high):
+        parts.append(f"{len(high)} sequence(s) (first: {int(high[0])}, max |v| {val(bits[high[0]]):.3g}) have |v| "
+                     f"of 65536 or more (or non-finite), beyond fp16")
+    raise LinearAttentionRangeError(
+        f"{what}: " + "; ".join(parts) + ". The output is linear in v: scale v by a power of two "
+        "into the window and the output back.")
 
 
 # ---------------------------------------------------------------------------

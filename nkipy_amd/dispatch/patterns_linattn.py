@@ -107,10 +107,15 @@ class LinearAttentionMatch(Match):
         # segmented scans take their prefix states from a workspace temporary
         ws_bytes = LA.linear_attention_workspace_bytes(B * H, T)
         ws = Slot(plan.add_buffer(ws_bytes, "temp", "linear_attention.prefix")) if ws_bytes else None
+        # each sequence's max |v|, checked against the kernel's fp16 operand
+        # window after the execution (a silent precision loss becomes an error)
+        vm = Slot(plan.add_buffer(4 * B * H, "temp", "linear_attention.vmax"))
+        plan.checks.append({"kind": "linattn_vmax", "buffer": vm.buffer, "offset": 0, "count": B * H,
+                            "desc": f"linear attention over {B}x{H} sequences of {T}"})
 
         def make(addr):
             return LA.linear_attention(addr(q), addr(k), addr(v), addr(out), B * H, T, D, v.shape[-1], 64,
-                                       part_ptr=addr(ws) if ws is not None else 0)
+                                       part_ptr=addr(ws) if ws is not None else 0, vmax_ptr=addr(vm))
 
         return [LaunchStep("linear_attention", f"chunked causal linear attention B*H={B * H} T={T} d={D}",
                            self.inputs, self.outputs, make)]

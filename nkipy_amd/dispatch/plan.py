@@ -76,6 +76,9 @@ class Plan:
     output_buffers: Dict[str, int] = field(default_factory=dict)
     # output name -> input name whose buffer it must reuse (aliasing)
     alias_outputs: Dict[str, str] = field(default_factory=dict)
+    # host-side checks of words the kernels leave in temporaries, run after
+    # an execution completes: {"kind", "buffer", "offset", "count", "desc"}
+    checks: List[dict] = field(default_factory=list)
 
     def add_buffer(self, nbytes: int, kind: str, name: str = "", data=None) -> int:
         b = BufferSpec(len(self.buffers), int(nbytes), kind, name, data)
@@ -179,6 +182,16 @@ class BoundPlan:
         )
 
 
+def _check_linattn_vmax(words, desc):
+    from nkipy_amd.dispatch.launchers import check_linear_attention_vmax
+
+    check_linear_attention_vmax(words, desc or "linear attention")
+
+
+# check kind -> function(words, description) raising on a failed check
+CHECKS: Dict[str, Callable] = {"linattn_vmax": _check_linattn_vmax}
+
+
 class PlanExecutor:
     """Owns a plan's temporaries and constants and runs it on bound I/O.
 
@@ -259,6 +272,17 @@ class PlanExecutor:
 
     def run(self, io_ptrs: Dict[str, int]):
         self.bind(io_ptrs).run()
+
+    def run_checks(self):
+        """The plan's host-side checks (:data:`CHECKS`) over what the last
+        completed execution left in their temporaries; the caller has
+        synchronised."""
+        for c in getattr(self.plan, "checks", ()):
+            buf = self._owned[c["buffer"]]
+            count = int(c["count"])
+            words = np.empty(count, np.uint32)
+            self.rt.d2h(words.ctypes.data, buf.ptr + int(c["offset"]), 4 * count)
+            CHECKS[c["kind"]](words, c.get("desc", ""))
 
     def forget(self):
         """Drop every bound launch list and owned buffer without touching the

@@ -1,5 +1,6 @@
 """Device runtime: tensors, loaded kernels and the jit entry points."""
 
+from nkipy_amd.dispatch.launchers import LinearAttentionRangeError
 from nkipy_amd.runtime.baremetal_executor import BaremetalExecutor, CompiledKernel
 from nkipy_amd.runtime.decorators import baremetal_jit
 from nkipy_amd.runtime.device_kernel import BenchmarkResult, DeviceKernel
@@ -10,6 +11,6 @@ from nkipy_amd.runtime.utils import is_gpu_available, is_neuron_compatible
 
 __all__ = [
     "BaremetalExecutor", "CompiledKernel", "baremetal_jit", "baremetal_run_traced_kernel", "BenchmarkResult", "DeviceKernel",
-    "DeviceTensor", "HipError", "NrtError", "SpikeError", "SpikeRuntimeError",
+    "DeviceTensor", "HipError", "LinearAttentionRangeError", "NrtError", "SpikeError", "SpikeRuntimeError",
     "is_gpu_available", "is_neuron_compatible",
 ]

@@ -308,6 +308,9 @@ class DeviceKernel:
             self._execute(self._io_ptrs(inputs, outputs), save_trace, ntff_name)
         if sync:
             get_runtime().sync()
+            # words the kernels left for the host (e.g. the linear-attention
+            # operand range), checked once the execution is complete
+            self.executor.run_checks()
         if auto:
             return outputs
         return None

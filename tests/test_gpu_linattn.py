@@ -162,3 +162,52 @@ def test_c_abi_linear_attention_rejects_missing_workspace(gpu):
     q, k, v = _qkv(1, 1, 4096, 128, seed=5)
     rc, msg = _c_abi_run(gpu, q, k, v, workspace=False)
     assert rc == 2 and b"workspace" in msg
+
+
+@pytest.mark.parametrize("T", [512, 1024])  # one segment per sequence; two segments (atomic max)
+def test_linattn_operand_window_guard(gpu, T):
+    """v of std 3e-6 has its max |v| below 2^-13, where the kernel's fp16
+    operands (V, S / 256) are subnormal: the traced kernel runs, reports each
+    sequence's max |v| exactly, and the call raises.  The output it leaves
+    follows the CPU model of the fp16 path (tests/linattn_model.py) and is
+    outside the bar against the oracle's fp32 recurrence, which is what the
+    guard prevents from passing silently.  At std 2e-4 the same kernel runs
+    without error and matches the oracle."""
+    from linattn_model import linear_attention_fp16
+
+    from nkipy_amd.kernels import chunked_linear_attention_kernel
+    from nkipy_amd.runtime import DeviceKernel
+
+    B, H, D = 1, 4, 128
+    nseg = LA.linear_attention_split(B * H, T)[0]
+    print(f"linattn window guard T={T} nseg={nseg}", flush=True)
+    rng = np.random.default_rng(T)
+    q, k = (N.bf16_round(rng.standard_normal((B, H, T, D)) / np.sqrt(D)) for _ in range(2))
+    base = rng.standard_normal((B, H, T, D))
+    for sigma, inside in ((2e-4, True), (3e-6, False)):
+        v = N.bf16_round(base * sigma)
+        args = [dt.to_bf16(a) for a in (q, k, v)]
+        dk = DeviceKernel.compile_and_load(chunked_linear_attention_kernel, *args, name=f"la_guard_{T}")
+        ins = {n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(("q", "k", "v"), args)}
+        outs = {"output0": DeviceTensor.empty((B, H, T, D), dt.bfloat16, name="output0")}
+        if inside:
+            dk(ins, outs)
+        else:
+            with pytest.raises(LA.LinearAttentionRangeError, match="below 2\\^-13"):
+                dk(ins, outs)
+        (chk,) = dk.plan.checks
+        words = np.empty(B * H, np.uint32)
+        gpu.d2h(words.ctypes.data, dk.executor._owned[chk["buffer"]].ptr, 4 * B * H)
+        want = N.bf16_bits(np.abs(v).reshape(B * H, -1).max(axis=1)).astype(np.uint32)
+        np.testing.assert_array_equal(words, want)
+        got = dt.to_float32(outs["output0"].numpy())
+        ref = K.linear_attention_chunked(q, k, v)
+        if inside:
+            _close(got, ref)
+        else:
+            model = np.stack([linear_attention_fp16(q[0, h], k[0, h], v[0, h]) for h in range(H)])[None]
+            _close(got, model)
+            name = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0] + " [vs oracle, recorded]"
+            from parity import record_close
+
+            assert record_close(got, ref, name, axis=-1) > 1.0
