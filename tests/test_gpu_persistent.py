@@ -139,3 +139,113 @@ def test_baremetal_executor_runs_compiled_artifact(gpu, tmp_path):
         assert res.iterations == 3 and res.mean_ms > 0
     with pytest.raises(FileNotFoundError):
         CompiledKernel(tk, str(tmp_path / "missing.neff"))
+
+
+def test_bf16_decode_loop_fused_generic_and_reloaded(gpu, tmp_path):
+    """The bf16 form: prefill on the fused Qwen3 prefill attention, three
+    decode steps on the fused decode-attention kernel with the caches
+    aliased in place, against the same graphs lowered onto the generic
+    kernels (which follow every traced cast point op by op); then the decode
+    artefact reloaded by graph hash (no lowering: relocated argument blocks,
+    the runtime position read through a relocated address) replays the last
+    step bit for bit."""
+    import os
+
+    from parity import assert_close
+
+    from nkipy_amd.core import dtypes as dt
+    from nkipy_amd.core.trace import NKIPyKernel
+    from nkipy_amd.dispatch.artifact import RelocatablePlan
+    from nkipy_amd.dispatch.lower import lower
+    from nkipy_amd.dispatch.patterns import default_patterns
+    from nkipy_amd.dispatch.patterns_attention import AttentionPattern, DecodeAttentionPattern
+    from nkipy_amd.kernels.qwen3 import qwen3_attention_kernel
+    from nkipy_amd.runtime import device_kernel as dkm
+    from oracle import numerics as N
+
+    Bb, Sb, MAXSb, Hb, Db, HKVb = 2, 128, 256, 4, 128, 2
+    HIDb = Hb * Db
+
+    def pre(x, qkv_weight, q_norm_weight, k_norm_weight, cache_k, cache_v, o_weight):
+        return qwen3_attention_kernel(x, qkv_weight, q_norm_weight, k_norm_weight, EPS, Hb, Db, HKVb,
+                                      cache_k, cache_v, None, o_weight)
+
+    def dec(x, qkv_weight, q_norm_weight, k_norm_weight, cache_k, cache_v, start_pos, o_weight):
+        return qwen3_attention_kernel(x, qkv_weight, q_norm_weight, k_norm_weight, EPS, Hb, Db, HKVb,
+                                      cache_k, cache_v, start_pos, o_weight)
+
+    rng = np.random.default_rng(17)
+    bf = lambda a: dt.to_bf16(N.bf16_round(a))
+    w = {"qkv_weight": bf(rng.standard_normal((HIDb, (Hb + 2 * HKVb) * Db)) * 0.05),
+         "q_norm_weight": bf(rng.uniform(0.5, 1.5, Db)), "k_norm_weight": bf(rng.uniform(0.5, 1.5, Db)),
+         "o_weight": bf(rng.standard_normal((Hb * Db, HIDb)) * 0.05)}
+    x0 = bf(rng.standard_normal((Bb, Sb, HIDb)))
+    toks = [bf(rng.standard_normal((Bb, 1, HIDb))) for _ in range(3)]
+    zeros = bf(np.zeros((Bb, MAXSb, HKVb, Db)))
+    pos0 = np.array([Sb], np.int32)
+    gp = NKIPyKernel.trace(pre).specialize(x0, w["qkv_weight"], w["q_norm_weight"], w["k_norm_weight"],
+                                           zeros, zeros, w["o_weight"])
+    gd = NKIPyKernel.trace(dec).specialize(toks[0], w["qkv_weight"], w["q_norm_weight"], w["k_norm_weight"],
+                                           zeros, zeros, pos0, w["o_weight"])
+    generic = [p for p in default_patterns() if not isinstance(p, (AttentionPattern, DecodeAttentionPattern))]
+    build = str(tmp_path / "build")
+    kinds = {}
+    results = {}
+    for mode in ("fused", "generic"):
+        if mode == "fused":
+            kp = DeviceKernel.compile_and_load(pre, x0, w["qkv_weight"], w["q_norm_weight"], w["k_norm_weight"],
+                                               zeros, zeros, w["o_weight"], build_dir=build)
+            kd = DeviceKernel.compile_and_load(dec, toks[0], w["qkv_weight"], w["q_norm_weight"],
+                                               w["k_norm_weight"], zeros, zeros, pos0, w["o_weight"],
+                                               build_dir=build)
+        else:
+            kp = DeviceKernel(gp, lower(gp, generic), "pre_generic")
+            kd = DeviceKernel(gd, lower(gd, generic), "dec_generic")
+        kinds[mode] = (kp.plan.kernel_kinds, kd.plan.kernel_kinds)
+        dw = {k: DeviceTensor.from_numpy(v, name=k) for k, v in w.items()}
+        ck = DeviceTensor.from_numpy(zeros, name="cache_k")
+        cv = DeviceTensor.from_numpy(zeros, name="cache_v")
+        hs = DeviceTensor.from_numpy(x0, name="hidden_states")
+        kp(inputs=_layer_inputs(dw, hs, ck, cv), outputs={"output0": hs, "cache_k": ck, "cache_v": cv})
+        outs = [hs.numpy()]
+        tok = DeviceTensor.from_numpy(toks[0], name="x")
+        pos = DeviceTensor.from_numpy(pos0, name="start_pos")
+        for i, t in enumerate(toks):
+            if i == len(toks) - 1:
+                before = (ck.numpy(), cv.numpy())
+            tok.write_from_numpy(t)
+            pos.write_from_numpy(np.array([Sb + i], np.int32))
+            kd(inputs=_layer_inputs(dw, tok, ck, cv, pos), outputs={"output0": tok, "cache_k": ck, "cache_v": cv})
+            outs.append(tok.numpy())
+        results[mode] = (outs, ck.numpy(), cv.numpy(), before, dw, kd)
+    assert "attention" in kinds["fused"][0] and "dot" not in kinds["fused"][0], kinds
+    assert "decode_attention" in kinds["fused"][1], kinds
+    assert "attention" not in kinds["generic"][0] and "decode_attention" not in kinds["generic"][1]
+    name = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    f_outs, f_ck, f_cv, before, dw, kd = results["fused"]
+    g_outs, g_ck, g_cv = results["generic"][:3]
+    for i, (a, b) in enumerate(zip(f_outs, g_outs)):
+        assert_close(dt.to_float32(a), dt.to_float32(b), f"{name} [step {i}]", axis=-1)
+    # prefill writes the caches from the same projection / norm / rotary
+    # kernels in both lowerings; later rows come from the decode steps
+    np.testing.assert_array_equal(dt.numpy_storage(f_ck)[:, :Sb], dt.numpy_storage(g_ck)[:, :Sb])
+    assert not dt.numpy_storage(f_ck)[:, Sb + len(toks):].any()
+
+    dkm._LOADED_KERNELS.clear()
+    real_lower = DeviceKernel._lower
+    DeviceKernel._lower = staticmethod(lambda g: (_ for _ in ()).throw(AssertionError("lowered again")))
+    try:
+        kd2 = DeviceKernel.compile_and_load(dec, toks[0], w["qkv_weight"], w["q_norm_weight"], w["k_norm_weight"],
+                                            zeros, zeros, pos0, w["o_weight"], build_dir=build)
+    finally:
+        DeviceKernel._lower = real_lower
+    assert isinstance(kd2.plan, RelocatablePlan) and kd2 is not kd
+    assert "decode_attention" in kd2.plan.kernel_kinds and repr(kd2).startswith("DeviceKernel(")
+    ck2 = DeviceTensor.from_numpy(before[0], name="cache_k")
+    cv2 = DeviceTensor.from_numpy(before[1], name="cache_v")
+    tok = DeviceTensor.from_numpy(toks[-1], name="x")
+    pos = DeviceTensor.from_numpy(np.array([Sb + len(toks) - 1], np.int32), name="start_pos")
+    out2 = kd2(inputs=_layer_inputs(dw, tok, ck2, cv2, pos))
+    np.testing.assert_array_equal(dt.numpy_storage(out2["output0"].numpy()), dt.numpy_storage(f_outs[-1]))
+    np.testing.assert_array_equal(dt.numpy_storage(out2["cache_k"].numpy()), dt.numpy_storage(f_ck))
+    np.testing.assert_array_equal(dt.numpy_storage(out2["cache_v"].numpy()), dt.numpy_storage(f_cv))
