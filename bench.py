@@ -107,6 +107,7 @@ def sections():
 
 
 MARK_BASE = 1000  # marker grid = MARK_BASE + workload id
+LAUNCH_MARK = 100  # marker grid = MARK_BASE + LAUNCH_MARK + launch index (back-to-back runs)
 CUS, XCDS = 256, 8  # MI355X
 
 
@@ -135,7 +136,7 @@ class Marker:
     def __init__(self, rt, enabled):
         self.rt, self.enabled = rt, enabled
         if enabled:
-            self.n = 4096 * (MARK_BASE + 16)
+            self.n = 4096 * (MARK_BASE + LAUNCH_MARK + 64)
             self.src, self.dst = rt.malloc(self.n), rt.malloc(self.n)
 
     def mark(self, sid):
@@ -143,6 +144,12 @@ class Marker:
             from nkipy_amd.dispatch.generic import copy16
 
             copy16(self.src, self.dst, 4096 * (MARK_BASE + sid)).run(self.rt)
+
+    def mark_launch(self, i):
+        """Before launch i of the current workload runs back to back with
+        itself: every dispatch up to the next marker is that launch."""
+        if self.enabled:
+            self.mark(LAUNCH_MARK + i)
 
 
 def _time_steps(bounds, steps, warmup, rt):
@@ -174,7 +181,7 @@ def _time_steps(bounds, steps, warmup, rt):
     return total / steps
 
 
-def _time_in_step(bounds, reps, rt):
+def _time_in_step(bounds, reps, rt, mk=None):
     """Mean microseconds of each launch of a step.  One whole step per buffer
     set first produces every intermediate; then launch i runs ``reps`` times
     back to back over the sets, with HIP events around that run only (an
@@ -188,6 +195,8 @@ def _time_in_step(bounds, reps, rt):
     out = []
     e0, e1 = rt.event(), rt.event()
     for i in range(n):
+        if mk is not None:
+            mk.mark_launch(i)
         for r in range(2):
             bounds[r % len(bounds)].run_range(i, i + 1)
         e0.record()
@@ -386,7 +395,7 @@ def bench_swiglu(a, rt, mk):
     steps, warm = max(5, a.steps // 20), max(2, a.warmup // 5)
     mk.mark(3)
     ms = _time_steps([bound], steps, warm, rt)
-    recs = _kernel_records(3, bound.launches, _time_in_step([bound], max(3, steps), rt))
+    recs = _kernel_records(3, bound.launches, _time_in_step([bound], max(3, steps), rt, mk))
     flops = sum(w for _, _, w in sections()[3][1])
     step_rec = {"label": "mlp", "kernel": " + ".join(l.symbol for l in bound.launches), "bound": "mfma"}
     entry = {"config": 3, "workload": "swiglu_mlp", "shape": {"M": MLP_M, "hidden": MLP_H, "ffn": MLP_F},
@@ -432,7 +441,7 @@ def bench_linattn(a, rt, mk):
     steps, warm = max(10, a.steps // 10), max(2, a.warmup // 5)
     mk.mark(4)
     ms = _time_steps(bounds, steps, warm, rt)
-    recs = _kernel_records(4, bounds[0].launches, _time_in_step(bounds, max(5, steps), rt))
+    recs = _kernel_records(4, bounds[0].launches, _time_in_step(bounds, max(5, steps), rt, mk))
     step_rec = {"label": "step", "kernel": " + ".join(l.symbol for l in bounds[0].launches), "bound": "hbm"}
     roof = _roofline(4, step_rec, us=ms * 1e3, work=work)
     t_pre, t_scan = _traffic("linear_attention/prefix_states"), _traffic("linear_attention/scan")
@@ -501,7 +510,7 @@ def bench_decoder(a, rt, mk):
     steps, warm = max(5, a.steps // 20), max(2, a.warmup // 5)
     mk.mark(5)
     ms = _time_steps(bounds, steps, warm, rt)
-    recs = _kernel_records(5, bounds[0].launches, _time_in_step(bounds, max(6, steps), rt))
+    recs = _kernel_records(5, bounds[0].launches, _time_in_step(bounds, max(6, steps), rt, mk))
     flops = sum(l.flops for l in bounds[0].launches)
     ach = flops / (ms * 1e-3) / 1e12
     roof = {"bound": "mfma", "kernel": "layer (9 kernels)", "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS,
@@ -618,18 +627,26 @@ def _label_dispatches(rows):
     """rows: dicts with name, wgs (workgroups), dispatch, sorted by dispatch.
     Yields (workload id, launch label, row) for the launches of the marked
     sections: a marker (nk_copy16 with MARK_BASE + id workgroups) opens a
-    section, whose launches are whole steps, labelled by position."""
+    section, whose launches are whole steps, labelled by position; a launch
+    marker (MARK_BASE + LAUNCH_MARK + i) within it is followed by launch i
+    run back to back with itself."""
     secs = sections()
-    cur, pos = None, 0
+    cur, pos, fixed = None, 0, None
     for r in rows:
         if r["name"].startswith("__amd"):
             continue  # runtime copies and fills
         if r["name"] == "nk_copy16" and (r["wgs"] - MARK_BASE) in secs:
-            cur, pos = r["wgs"] - MARK_BASE, 0
+            cur, pos, fixed = r["wgs"] - MARK_BASE, 0, None
+            continue
+        if r["name"] == "nk_copy16" and cur is not None and 0 <= r["wgs"] - MARK_BASE - LAUNCH_MARK < 64:
+            fixed = r["wgs"] - MARK_BASE - LAUNCH_MARK
             continue
         if cur is None:
             continue
         labels = secs[cur][1]
+        if fixed is not None:
+            yield cur, labels[fixed][0], r
+            continue
         yield cur, labels[pos % len(labels)][0], r
         pos += 1
 
