@@ -216,13 +216,19 @@ __device__ __forceinline__ void rmsnorm_reg_body(const RmsNormArgs &a) {
   const auto hr = buf_rsrc((flags & NK_RMS_WRITE_H) ? reinterpret_cast<T *>(a.h) + row * n : nullptr,
                            (flags & NK_RMS_WRITE_H) ? rb : 0);
   const int tid = threadIdx.x;
-  Raw8<T> xv[CHUNKS], rv_[CHUNKS];
+  Raw8<T> xv[CHUNKS], rv_[CHUNKS], wraw[CHUNKS];
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
     const uint32_t off = (c * BLOCK + tid) * 8 * sizeof(T);
     xv[c].template load_buf<RES>(xr, off);
     if (RES) rv_[c].template load_buf<RES>(rr_, off);
   }
+  // the weight (the same row for every workgroup, cache-resident) is
+  // fetched with the row, not after the reduction: no second memory round
+  // trip between the sum and the stores
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c)
+    if (flags & NK_RMS_W) wraw[c].template load_buf<false>(wr, (c * BLOCK + tid) * 8 * sizeof(T));
   float v[CHUNKS][8];
   float ss = 0.f;
 #pragma unroll
@@ -254,11 +260,7 @@ __device__ __forceinline__ void rmsnorm_reg_body(const RmsNormArgs &a) {
   for (int c = 0; c < CHUNKS; ++c) {
     const uint32_t off = (c * BLOCK + tid) * 8 * sizeof(T);
     float wv[8];
-    if (flags & NK_RMS_W) {
-      Raw8<T> wraw;
-      wraw.template load_buf<false>(wr, off);
-      decode8(wraw, wv);
-    }
+    if (flags & NK_RMS_W) decode8(wraw[c], wv);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       float q = (flags & NK_RMS_MUL_RECIP) ? v[c][j] * inv : div_rn(v[c][j], s, inv);
