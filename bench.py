@@ -101,7 +101,11 @@ def sections():
             ("mlp_norm", "hbm", norm_bytes),
             ("gate_up_swiglu", "mfma", 2 * 2 * DEC_M * DEC_HID * DEC_F),
             ("down_proj_residual", "mfma", 2 * DEC_M * DEC_F * DEC_HID)]),
-        6: ("qwen3_prefill_attention", [("attention", "mfma", 4 * QP_B * QP_HQ * QP_S * QP_S * DEC_D // 2)]),
+        # the bf16 softmax: row-max and row-sum passes over the scores (half
+        # the flops each, recomputed by the last pass), then the weighted values
+        6: ("qwen3_prefill_attention", [("rowmax", "mfma", 2 * QP_B * QP_HQ * QP_S * QP_S * DEC_D // 2),
+                                        ("rowsum", "mfma", 2 * QP_B * QP_HQ * QP_S * QP_S * DEC_D // 2),
+                                        ("attention", "mfma", 4 * QP_B * QP_HQ * QP_S * QP_S * DEC_D // 2)]),
         9: ("copy_calibration", [("copy16", "hbm", 2 * 2**30)]),
     }
 
@@ -572,14 +576,24 @@ def bench_qwen3_prefill(a, rt, mk):
     sets = [[DeviceTensor.from_numpy(v, name=n) for n, v in zip(names, args)]
             + [DeviceTensor.empty((B, S, Hq, D), dt.bfloat16, name="output0")] for _ in range(3)]
     bounds = [dk.executor.bind({**{n: t.ptr for n, t in zip(names, s[:3])}, "output0": s[3].ptr}) for s in sets]
+    if len(bounds[0].launches) != len(sections()[6][1]):
+        raise RuntimeError("Qwen3 prefill attention step has an unexpected launch count")
     steps, warm = max(10, a.steps // 10), max(2, a.warmup // 5)
     mk.mark(6)
     ms = _time_steps(bounds, steps, warm, rt)
-    recs = _kernel_records(6, bounds[0].launches, [ms * 1e3])
+    recs = _kernel_records(6, bounds[0].launches, _time_in_step(bounds, max(5, steps), rt, mk))
+    # the roofline of the whole step on the algorithmic (causal) flops: the
+    # score products of the row-max and row-sum passes are recomputed work,
+    # not counted
+    step_rec = {"label": "step", "kernel": " + ".join(l.symbol for l in bounds[0].launches), "bound": "mfma"}
+    roof = _roofline(6, step_rec, us=ms * 1e3, work=sections()[6][1][2][2])
+    tr = [_traffic(f"qwen3_prefill_attention/{lbl}") for lbl, _, _ in sections()[6][1]]
+    roof["traffic"] = sum(tr) if all(tr) else None
     entry = {"config": 6, "workload": "qwen3_prefill_attention",
              "shape": {"batch": B, "seq": S, "cache_rows": MAXS, "heads": Hq, "kv_heads": Hkv, "head_dim": D},
-             "dtype": "bf16 (scores rounded to bf16 after the product and the divide by sqrt(d))",
-             "us_per_step": round(ms * 1e3, 2), "roofline": _roofline(6, recs[0]), "kernels": recs,
+             "dtype": "bf16 (scores rounded to bf16 after the product and the divide by sqrt(d); "
+                      "bf16 softmax)",
+             "us_per_step": round(ms * 1e3, 2), "roofline": roof, "kernels": recs,
              "note": "causal flops (keys 0..s for query s); cache rows past S are masked and not read"}
 
     def cpu():

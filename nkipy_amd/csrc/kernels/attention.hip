@@ -63,8 +63,15 @@ struct AttnArgs {
   // `scale`, the scaled score rounded to bf16
   float div, rdiv;
   int32_t flags;
+  // the launches of the bf16 softmax (ATT_SOFTMAX_BF16) share per-query
+  // statistics over chunks of ckb 32-key blocks (at most nch chunks per
+  // row): for chunk c and row = (b * Hq + h) * S + query, the max score at
+  // rowstat[c * B * Hq * S + row] and the sum of the weights at
+  // rowstat[(nch + c) * B * Hq * S + row]
+  float *rowstat;
+  int32_t ckb, nch;
 };
-enum { ATT_RND_PROD = 1, ATT_RND_SCORE = 2, ATT_DIVIDE = 8 };
+enum { ATT_RND_PROD = 1, ATT_RND_SCORE = 2, ATT_SOFTMAX_BF16 = 4, ATT_DIVIDE = 8 };
 
 // K tile row (key) r: 16-byte chunk c stored at c ^ (r & 15): the 32 rows of
 // a K fragment read hit 16 distinct bank slots (two per cycle's worth).
@@ -424,12 +431,74 @@ __device__ __forceinline__ void dma16_asm(i32x4_t r, uint32_t lds, uint32_t off)
                :: "v"(off), "s"(r), "s"(m) : "memory", "m0");
 }
 
+// the score cast points of the flags (uniform branches: every lane takes the
+// same ones; the quotient of a finite score needs no infinity fallback in
+// the block form)
+__device__ __forceinline__ float cast_score(const AttnArgs &a, float x) {
+  if (a.flags & ATT_RND_PROD) x = bf16_to_f32(f32_to_bf16(x));
+  x = (a.flags & ATT_DIVIDE) ? div_rn(x, a.div, a.rdiv) : x * a.scale;
+  if (a.flags & ATT_RND_SCORE) x = bf16_to_f32(f32_to_bf16(x));
+  return x;
+}
+__device__ __forceinline__ void round_bf16x2(float &x0, float &x1);
+__device__ __forceinline__ void round_block(f32x16 &s) {
+#pragma unroll
+  for (int r = 0; r < 16; r += 2) {
+    float x0 = s[r], x1 = s[r + 1];
+    round_bf16x2(x0, x1);
+    s[r] = x0;
+    s[r + 1] = x1;
+  }
+}
+__device__ __forceinline__ void cast_block(const AttnArgs &a, f32x16 &s) {
+  if (a.flags & ATT_RND_PROD) round_block(s);
+  if (a.flags & ATT_DIVIDE) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = div_rn_finite(s[r], a.div, a.rdiv);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] *= a.scale;
+  }
+  if (a.flags & ATT_RND_SCORE) round_block(s);
+}
+// query block qb's key chunks (bf16 softmax statistics)
+__device__ __forceinline__ int stat_chunks(const AttnArgs &a, int qb) {
+  const int nb = a.causal ? (qb + 1) * 4 : a.S / 32;
+  return (nb + a.ckb - 1) / a.ckb;
+}
+
+// x0, x1 rounded to bf16 (round to nearest even) with one packed
+// conversion.  The compiler splits a packed conversion whose halves are
+// used apart into two single ones; an empty asm that takes the packed word
+// keeps it whole.  (The conversion itself stays the compiler's, so its
+// hazard checks cover it: an instruction written in asm that reads a
+// v_exp_f32 result gets no wait state from the compiler.)
+__device__ __forceinline__ void round_bf16x2(float &x0, float &x1) {
+  uint32_t w = pack_bf16x2(x0, x1);
+  asm("" : "+v"(w));
+  x0 = __uint_as_float(w << 16);
+  x1 = __uint_as_float(w & 0xffff0000u);
+}
+
 // XF: each score first takes the cast points the traced code applies
 // before its softmax (the Qwen3 prefill form, examples/models/qwen3/kernels/
 // attention.py:119-120: (q @ k^T) in bf16, divided by sqrt(d) in fp32, cast
 // to bf16), then enters the softmax with a unit scale.
-template <int NW, bool XF = false>
+//
+// SMX selects the softmax: false, online in fp32 with the offset described
+// above; true, the bf16 softmax of the traced code (examples/models/qwen3/
+// kernels/softmax.py:4-6 on bf16 scores) with every cast point, given each
+// query's max score m and weight sum l from the row statistics kernels
+// below: the weights p = bf16(e / l) with e = bf16(exp(bf16(s - m))) are
+// the P V operand, and o = bf16(sum p v): the traced code's arithmetic, up
+// to the order of the fp32 sums.  bf16(e / l) is formed as bf16(e RN(1 / l)):
+// e and l have 8-bit significands, so e / l is never a bf16 rounding
+// midpoint (a midpoint times l has a set bit below e's last) and lies at
+// least 2^-17 (relative) from one, beyond the 2^-23 the product can stray
+// from the correctly rounded quotient: both round to the same bf16 value.
+template <int NW, bool XF = false, bool SMX = false>
 __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
+  static_assert(!SMX || XF, "the bf16 softmax follows the score cast points");
   constexpr int AQW = 32 * NW;  // queries per workgroup
   constexpr int TB = 32 * AD * 2;  // one 32-key K or V tile
   // one array per operand: a slot is a constant offset, so one address
@@ -473,6 +542,23 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
 
   const int wq0 = q0 + wave * 32;
   const int qrow = wq0 + l32;
+  // SMX: this query's max score, bf16 weight sum and RN(1 / sum), from the
+  // statistics of its query block's key chunks (the sums added in chunk
+  // order)
+  float mx = 0.f, lb = 1.f, rlb = 1.f;
+  if constexpr (SMX) {
+    const int64_t nq = (int64_t)a.B * a.Hq * a.S;
+    const float *st = a.rowstat + ((int64_t)b * a.Hq + h) * a.S + qrow;
+    const int nc = stat_chunks(a, qb);
+    mx = st[0];
+    float tot = st[a.nch * nq];
+    for (int c = 1; c < nc; ++c) {
+      mx = fmaxf(mx, st[c * nq]);
+      tot += st[(a.nch + c) * nq];
+    }
+    lb = bf16_to_f32(f32_to_bf16(tot));
+    rlb = __frcp_rn(lb);
+  }
   bf16x8_t qf[AD / 16];
 #pragma unroll
   for (int kk = 0; kk < AD / 16; ++kk)
@@ -520,6 +606,9 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
     for (int j = 0; j < NM; ++j)
       dma16_asm(r, v_lds + (decltype(sl)::value & 3) * TB + j * NW * 1024, vbase + j * vjs + vst);
   };
+  // moves an iteration leaves outstanding at its end: the last two
+  // iterations' K and V tiles
+  constexpr int OUT = 4 * NM;
   // wait until at most n of this wave's DMA moves are outstanding (the Q
   // loads were issued before every move, so they are done by then too)
   auto wait_moves = [&](auto ntag) __attribute__((always_inline)) {
@@ -582,29 +671,29 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
   // klim (the query itself when causal, else the last key) get p = 0
   const int klim = a.causal ? qrow : a.S - 1;
   auto softmax = [&](f32x16 &s, bf16x8_t (&pf)[2], int kb, auto masktag) __attribute__((always_inline)) {
-    if constexpr (XF) {
-      // uniform branches: every lane takes the same cast points
-      if (a.flags & ATT_RND_PROD) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[r] = bf16_to_f32(f32_to_bf16(s[r]));
-      }
-      if (a.flags & ATT_DIVIDE) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[r] = div_rn(s[r], a.div, a.rdiv);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[r] *= a.scale;
-      }
-      if (a.flags & ATT_RND_SCORE) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[r] = bf16_to_f32(f32_to_bf16(s[r]));
-      }
-    }
+    if constexpr (XF) cast_block(a, s);
     if constexpr (decltype(masktag)::value) {
       // element r holds key kb * 32 + 4 lhi + (8 (r / 4) + r % 4)
       const int t = klim - kb * 32 - lhi * 4;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = ((r >> 2) * 8 + (r & 3)) > t ? -INFINITY : s[r];
+    }
+    if constexpr (SMX) {
+      // e = bf16(exp(bf16(s - m))) in pairs (one packed conversion per
+      // rounding); masked keys: s = -inf, d = -inf, e = 0.  The exponential
+      // is 2^(d RN(log2 e)), within a few ulp of e^d: the bf16 rounding of
+      // e moves only for e^d within those few ulp of a rounding boundary.
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        float d0 = s[r] - mx, d1 = s[r + 1] - mx;
+        round_bf16x2(d0, d1);
+        float e0 = __builtin_amdgcn_exp2f(d0 * 1.44269504088896340736f);
+        float e1 = __builtin_amdgcn_exp2f(d1 * 1.44269504088896340736f);
+        round_bf16x2(e0, e1);
+        pf[r >> 3][r & 7] = (__bf16)(e0 * rlb);
+        pf[r >> 3][(r & 7) + 1] = (__bf16)(e1 * rlb);
+      }
+      return;
     }
     float ls = expblock(s, pf);
     if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(ls <= 65536.f)) != 0, 0)) {
@@ -675,7 +764,7 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
       load_k(SlotTag<SL>{}, j + 4);
       load_v(SlotTag<SL + 2>{}, j + 2);
     }
-    wait_moves(SlotTag<4 * NM>{});
+    wait_moves(SlotTag<OUT>{});
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -690,7 +779,7 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
   load_v(SlotTag<0>{}, 0);
   load_k(SlotTag<3>{}, 3);
   load_v(SlotTag<1>{}, 1);
-  wait_moves(SlotTag<4 * NM>{});
+  wait_moves(SlotTag<OUT>{});
   __builtin_amdgcn_s_barrier();
   qk(kslot(SlotTag<0>{}), sA);
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): K0 reads done before its slot is refilled
@@ -723,8 +812,9 @@ __device__ __forceinline__ void attention_sp_body(const AttnArgs &a) {
   }
   wait_moves(SlotTag<0>{});  // no LDS DMA outlives the workgroup
 
-  // normalise and store
-  const float inv_l = 1.0f / (l_run + __shfl_xor(l_run, 32, 64));
+  // normalise (the weights of the bf16 softmax are normalised already) and
+  // store
+  const float inv_l = SMX ? 1.0f : 1.0f / (l_run + __shfl_xor(l_run, 32, 64));
   uint16_t *orow = op + (int64_t)qrow * a.o_ss;
 #pragma unroll
   for (int t = 0; t < 4; ++t)
@@ -742,6 +832,175 @@ extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128_sp
 }
 extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128_sp_xf(AttnArgs a) {
   attention_sp_body<4, true>(a);
+}
+extern "C" __global__ __launch_bounds__(256, 2) void nk_attention_causal_d128_sp_xf_bf16(AttnArgs a) {
+  attention_sp_body<4, true, true>(a);
+}
+
+// ---------------------------------------------------------------------------
+// Row statistics of the bf16 softmax (ATT_SOFTMAX_BF16).  Its weights need
+// each query's max score, then the sum of its weights, before any weight
+// can be formed: two passes over the scores before the weighted values.
+// They compute scores only: no V.  Each wave keeps its 32 queries' Q
+// fragments in registers; each 32-key K tile moves once per workgroup,
+// straight into a four-slot LDS ring (the K layout and moves of the ring
+// kernel) three tiles ahead of the one the four waves read.  The keys
+// of a query block are cut into chunks of a.ckb blocks, one workgroup per
+// (query block, chunk, query head): the longest causal query blocks no
+// longer set the length of the launch.  For each chunk and query,
+//   MAX  writes the max score: the cast points (bf16 rounding, a positive
+//        scale, a correctly rounded divide by a positive divisor) never
+//        decrease a score, so the max of the cast scores is the cast of the
+//        max of the raw ones, and the cast is applied once;
+//   SUM  writes the fp32 sum over the chunk of e = bf16(exp(bf16(s - m))),
+//        m the max over the query's chunks.
+// Layout of the statistics: AttnArgs::rowstat.  Work items of one (batch,
+// KV head) run longest query block first; items are spread over the XCDs
+// in contiguous ranges, as in the ring kernel.
+// ---------------------------------------------------------------------------
+template <bool SUM>
+__device__ __forceinline__ void attention_rowstat_body(const AttnArgs &a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l32 = lane & 31, lhi = lane >> 5;
+  const int nqb = a.S / 128, rep = a.Hq / a.Hkv;
+
+  int per_bg = 0;  // work items of one (batch, KV head)
+  for (int qb = 0; qb < nqb; ++qb) per_bg += stat_chunks(a, qb);
+  per_bg *= rep;
+  const int nwg = a.B * a.Hkv * per_bg;
+  int w = blockIdx.x;
+  if ((nwg & 7) == 0) w = (w & 7) * (nwg >> 3) + (w >> 3);
+  const int bg = w / per_bg;
+  if (bg >= a.B * a.Hkv) return;  // (the grid holds exactly nwg workgroups)
+  int idx = w % per_bg, qb = nqb - 1;
+  for (; qb > 0; --qb) {
+    const int n = stat_chunks(a, qb) * rep;
+    if (idx < n) break;
+    idx -= n;
+  }
+  const int c = idx / rep, g = bg % a.Hkv, b = bg / a.Hkv;
+  const int h = g * rep + idx % rep;
+  if (c >= stat_chunks(a, qb)) return;  // (likewise)
+
+  // this wave's blocks of the chunk: every one of the chunk's, up to the
+  // block holding its own queries (causal); never empty, as a causal
+  // chunk starts at or before the query block's first key block
+  const int wq0 = qb * 128 + wave * 32, qrow = wq0 + l32;
+  const int kb0 = c * a.ckb;
+  int kb1 = min(kb0 + a.ckb, a.causal ? (qb + 1) * 4 : a.S / 32);
+  if (a.causal) kb1 = min(kb1, wq0 / 32 + 1);
+
+  const int kb1_wg = min(kb0 + a.ckb, a.causal ? (qb + 1) * 4 : a.S / 32);  // the workgroup's blocks
+  const uint16_t *qp = a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh;
+  const uint16_t *kp = a.k + (int64_t)b * a.k_sb + (int64_t)g * a.k_sh;
+  const i32x4_t rk = rsrc_words(kp, (int64_t)a.S * a.k_ss * 2);
+  const i32x4_t rnone = rsrc_words(kp, 0);  // moves of no bytes: zeros, no memory read
+  constexpr int TB = 32 * AD * 2;  // one K tile
+  __shared__ __attribute__((aligned(1024))) uint8_t KT[4 * TB];
+  const int64_t nq = (int64_t)a.B * a.Hq * a.S;
+  float *st = a.rowstat + ((int64_t)b * a.Hq + h) * a.S + qrow;
+  bf16x8_t qf[AD / 16];  // loaded once the first moves are out
+  float mx = 0.f;        // SUM: the query's max score, likewise
+
+  // tile moves (two 1 KiB moves per wave): move j of wave w fills key rows
+  // 16 j + 4 w .. + 3, lane l the row's 16-byte position l % 16, which
+  // holds chunk (l % 16) ^ (row % 16): chunk c of row r sits at
+  // r * 256 + 16 (c ^ (r % 16))
+  const int row0 = wave * 4 + (lane >> 4);
+  const int tch = (lane & 15) ^ (row0 & 15);  // (row0 + 16 j has the same low bits)
+  const uint32_t tsrc = (uint32_t)(((int64_t)row0 * a.k_ss + tch * 8) * 2);
+  const uint32_t tjs = (uint32_t)((int64_t)16 * a.k_ss * 2), tstep = (uint32_t)((int64_t)32 * a.k_ss * 2);
+  const uint32_t tlds = lds_addr(KT) + wave * 1024;
+  auto move = [&](int t) __attribute__((always_inline)) {  // tile t of the chunk into slot t % 4
+    const int kb = kb0 + t;
+    const i32x4_t r = t < kb1_wg - kb0 ? rk : rnone;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dma16_asm(r, tlds + (t & 3) * TB + j * 4096, tsrc + j * tjs + kb * tstep);
+  };
+  // this lane's fragment kk of a tile: row l32, chunk 2 kk + lhi
+  auto koff = [&](int kk) __attribute__((always_inline)) { return l32 * 256 + 16 * ((2 * kk + lhi) ^ (l32 & 15)); };
+  float acc = SUM ? 0.f : -INFINITY;
+  auto block = [&](int kb, const uint8_t *Kt) __attribute__((always_inline)) {
+    f32x16 s;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < AD / 16; ++kk)
+      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8_t *>(Kt + koff(kk)), qf[kk], s,
+                                                  0, 0, 0);
+    if constexpr (SUM) cast_block(a, s);
+    if (a.causal && kb == wq0 / 32) {
+      // element r holds key kb * 32 + 4 lhi + (8 (r / 4) + r % 4)
+      const int t = qrow - kb * 32 - lhi * 4;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = ((r >> 2) * 8 + (r & 3)) > t ? -INFINITY : s[r];
+    }
+    if constexpr (SUM) {
+      float ps0 = 0.f, ps1 = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        float d0 = s[r] - mx, d1 = s[r + 1] - mx;
+        round_bf16x2(d0, d1);
+        float e0 = __builtin_amdgcn_exp2f(d0 * 1.44269504088896340736f);
+        float e1 = __builtin_amdgcn_exp2f(d1 * 1.44269504088896340736f);
+        round_bf16x2(e0, e1);
+        ps0 += e0;
+        ps1 += e1;
+      }
+      acc += ps0 + ps1;
+    } else {
+      float bm = s[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) bm = fmaxf(bm, s[r]);
+      acc = fmaxf(acc, bm);
+    }
+  };
+  // tile t = kb - kb0 lands in slot t % 4.  Step t moves tile t + 3 into
+  // the slot of tile t - 1 (every wave finished it before the last
+  // barrier), reads tile t, then waits until tile t + 1 has landed: each
+  // step issues two moves per wave (of no bytes past the chunk), so at most
+  // the four of tiles t + 2 and t + 3 may still be in flight.
+  const int nt = kb1_wg - kb0;
+  move(0);
+  move(1);
+  move(2);
+  // Q fragments (and the query's max score), all in hand before the loop:
+  // the compiler, which cannot count the moves, then adds no wait of its
+  // own inside the loop
+#pragma unroll
+  for (int kk = 0; kk < AD / 16; ++kk)
+    qf[kk] = *reinterpret_cast<const bf16x8_t *>(qp + (int64_t)qrow * a.q_ss + kk * 16 + lhi * 8);
+  if constexpr (SUM) {
+    const int nc = stat_chunks(a, qb);
+    mx = st[0];
+    for (int cc = 1; cc < nc; ++cc) mx = fmaxf(mx, st[cc * nq]);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the moves of tiles 0 - 2 as well
+#pragma unroll
+  for (int kk = 0; kk < AD / 16; ++kk) asm volatile("" ::"v"(qf[kk]));
+  asm volatile("" ::"v"(mx));
+  __syncthreads();
+  for (int t = 0; t < nt; ++t) {
+    move(t + 3);
+    if (kb0 + t < kb1) block(kb0 + t, KT + (t & 3) * TB);
+    __builtin_amdgcn_s_waitcnt(0x0F70 | 4);  // vmcnt(4): tile t + 1 done
+    __syncthreads();
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no move outlives the workgroup
+  if constexpr (SUM) {
+    acc += __shfl_xor(acc, 32, 64);
+    if (lhi == 0) st[(a.nch + c) * nq] = acc;
+  } else {
+    acc = fmaxf(acc, __shfl_xor(acc, 32, 64));
+    if (lhi == 0) st[c * nq] = cast_score(a, acc);
+  }
+}
+extern "C" __global__ __launch_bounds__(256) void nk_attention_rowmax_d128(AttnArgs a) {
+  attention_rowstat_body<false>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void nk_attention_rowsum_d128(AttnArgs a) {
+  attention_rowstat_body<true>(a);
 }
 extern "C" __global__ __launch_bounds__(512, 1) void nk_attention_causal_d128_sp8(AttnArgs a) {
   attention_sp_body<8>(a);

@@ -18,7 +18,12 @@
 // Arithmetic is fp32 whatever the storage type.  The register softmax takes
 // e^x from the hardware 2^t with the rounding error of t = x log2 e folded
 // back in (exp_acc, about two ulp), so fp32 softmax stays within 1e-5 of
-// NumPy; the loop fallback calls libm expf.
+// NumPy; the loop fallback calls libm expf.  When the traced softmax runs
+// in the 16-bit input type itself (SMX_ROUND_OPS: bf16 or fp16 x - max,
+// exp, sum and divide, as softmax_kernel computes on bf16 scores), each
+// of those results is rounded to that type as the traced code rounds it:
+// d = r(x - max), e = r(exp d), s = r(sum e) with an fp32 sum,
+// y = r(e / s).
 
 #include "common.h"
 
@@ -29,8 +34,21 @@ struct SoftmaxArgs {
   void *y;
   int64_t rows;
   int32_t n;
-  int32_t pad;
+  int32_t flags;
 };
+enum { SMX_ROUND_OPS = 1 };
+
+// x rounded to the storage type T (fp32: unchanged)
+template <typename T>
+__device__ __forceinline__ float round_as(float x) {
+  if constexpr (sizeof(T) == 4) {
+    return x;
+  } else {
+    T t;
+    Elt<T>::store(&t, 0, x);
+    return Elt<T>::load(&t, 0);
+  }
+}
 
 // Loads go through the cache; NTS selects streaming stores (2-byte and
 // mixed types).  With each thread's 8 elements contiguous, fp32 measured on
@@ -87,23 +105,26 @@ __device__ __forceinline__ void softmax_reg_body(const SoftmaxArgs &a) {
     m = fmaxf(m, mc);
   }
   m = block_max<BLOCK>(m, red);
+  // uniform: every thread rounds the same steps
+  const bool rnd = (a.flags & SMX_ROUND_OPS) != 0;
+  auto r = [&](float x) __attribute__((always_inline)) { return rnd ? round_as<TI>(x) : x; };
   float s = 0.f;
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
     float sc = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      v[c][j] = exp_acc(v[c][j] - m);
+      v[c][j] = r(exp_acc(r(v[c][j] - m)));
       sc += inside(c, j) ? v[c][j] : 0.f;
     }
     s += sc;
   }
-  s = block_sum<BLOCK>(s, red);
+  s = r(block_sum<BLOCK>(s, red));
   const float inv_s = 1.0f / s;
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[c][j] = div_rn_finite(v[c][j], s, inv_s);
+    for (int j = 0; j < 8; ++j) v[c][j] = r(div_rn_finite(v[c][j], s, inv_s));
     Raw8<TO> o;
     encode8(v[c], o);
     if constexpr (SPLIT) {
@@ -125,11 +146,13 @@ __device__ __forceinline__ void softmax_loop_body(const SoftmaxArgs &a) {
   float m = -INFINITY;
   for (int i = threadIdx.x; i < n; i += BLOCK) m = fmaxf(m, Elt<TI>::load(x, i));
   m = block_max<BLOCK>(m, red);
+  const bool rnd = (a.flags & SMX_ROUND_OPS) != 0;
+  auto r = [&](float v) { return rnd ? round_as<TI>(v) : v; };
   float s = 0.f;
-  for (int i = threadIdx.x; i < n; i += BLOCK) s += expf(Elt<TI>::load(x, i) - m);
-  s = block_sum<BLOCK>(s, red);
+  for (int i = threadIdx.x; i < n; i += BLOCK) s += r(expf(r(Elt<TI>::load(x, i) - m)));
+  s = r(block_sum<BLOCK>(s, red));
   for (int i = threadIdx.x; i < n; i += BLOCK)
-    Elt<TO>::store(y, i, expf(Elt<TI>::load(x, i) - m) / s);
+    Elt<TO>::store(y, i, r(r(expf(r(Elt<TI>::load(x, i) - m))) / s));
 }
 
 #define NK_SOFTMAX_REG(TI, TO, tin, ton, B, C)                                       \

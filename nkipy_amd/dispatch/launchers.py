@@ -11,6 +11,7 @@ field; the kernel manifest's ``kernarg_size`` is checked at launch.
 from __future__ import annotations
 
 import ctypes
+import functools
 from dataclasses import dataclass, field
 from typing import List, Tuple
 
@@ -69,8 +70,11 @@ class SoftmaxArgs(ctypes.Structure):
         ("y", ctypes.c_void_p),
         ("rows", ctypes.c_int64),
         ("n", ctypes.c_int32),
-        ("pad", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
     ]
+
+
+SMX_ROUND_OPS = 1
 
 
 # (block, chunks) register variants of softmax: a row of up to
@@ -96,8 +100,10 @@ def _row_variant(n: int, elem_bytes: int, ptr_align_ok: bool):
 
 
 def softmax_rows(x_ptr: int, y_ptr: int, rows: int, n: int, in_dtype, out_dtype,
-                 block_chunks=None) -> Launch:
-    """y[r, :] = softmax(x[r, :]) over rows of n contiguous elements."""
+                 block_chunks=None, round_ops: bool = False) -> Launch:
+    """y[r, :] = softmax(x[r, :]) over rows of n contiguous elements.
+    ``round_ops``: the softmax runs in the 16-bit input type (x - max, exp,
+    sum and divide each rounded to it, the sum accumulated in fp32)."""
     ti, to = dtype_tag(in_dtype), dtype_tag(out_dtype)
     if (ti, to) not in _SOFTMAX_TYPES:
         raise LaunchError(f"softmax has no {ti}->{to} variant")
@@ -111,7 +117,9 @@ def softmax_rows(x_ptr: int, y_ptr: int, rows: int, n: int, in_dtype, out_dtype,
         if n > block_chunks[0] * block_chunks[1] * 8 or tuple(block_chunks) not in _SOFTMAX_REG_VARIANTS:
             raise LaunchError(f"softmax variant {block_chunks} does not fit n={n}")
         var = tuple(block_chunks)
-    args = SoftmaxArgs(x_ptr, y_ptr, rows, n, 0)
+    if round_ops and dt.itemsize(in_dtype) != 2:
+        raise LaunchError("softmax steps round only to a 16-bit input type")
+    args = SoftmaxArgs(x_ptr, y_ptr, rows, n, SMX_ROUND_OPS if round_ops else 0)
     nbytes = rows * n * (dt.itemsize(in_dtype) + dt.itemsize(out_dtype))
     if var is None:
         return Launch("rowwise", f"nk_softmax_loop_{ti}_{to}", (rows, 1, 1), (256, 1, 1),
@@ -542,18 +550,48 @@ class AttnArgs(ctypes.Structure):
         [(f"{t}_{s}", ctypes.c_int64) for t in "qkvo" for s in ("sb", "ss", "sh")] + \
         [("B", ctypes.c_int32), ("S", ctypes.c_int32), ("Hq", ctypes.c_int32),
          ("Hkv", ctypes.c_int32), ("scale", ctypes.c_float), ("causal", ctypes.c_int32),
-         ("div", ctypes.c_float), ("rdiv", ctypes.c_float), ("flags", ctypes.c_int32)]
+         ("div", ctypes.c_float), ("rdiv", ctypes.c_float), ("flags", ctypes.c_int32),
+         ("rowstat", ctypes.c_void_p), ("ckb", ctypes.c_int32), ("nch", ctypes.c_int32)]
 
 
-# score cast points of the traced code before its softmax (the values of the
-# decode kernel's DEC_* flags)
-ATT_RND_PROD, ATT_RND_SCORE, ATT_DIVIDE = 1, 2, 8
+# score cast points of the traced code before its softmax, and its softmax in
+# bf16 (the values of the decode kernel's DEC_* flags)
+ATT_RND_PROD, ATT_RND_SCORE, ATT_SOFTMAX_BF16, ATT_DIVIDE = 1, 2, 4, 8
+
+
+@functools.lru_cache(maxsize=64)
+def divide_rounds_as_multiply(div: float) -> bool:
+    """Whether bf16(RN(s / div)) == bf16(RN(s * RN(1 / div))) for every
+    finite bf16 s, checked over all of them: then a score divided by ``div``
+    and rounded to bf16 needs no correctly rounded quotient, the product by
+    the reciprocal rounds to the same bf16 value."""
+    s = (np.arange(1 << 16, dtype=np.uint32) << 16).view(np.float32)
+    s = s[np.isfinite(s)]
+    d = np.float32(div)
+    with np.errstate(over="ignore", under="ignore"):
+        return bool(np.array_equal(dt.round_to_bf16(s / d), dt.round_to_bf16(s * (np.float32(1) / d))))
+
+
+def attention_stat_chunks(S: int, causal: bool = True):
+    """Key chunks of the bf16 softmax's row statistics: (32-key blocks per
+    chunk, most chunks of a query block, chunks summed over the S / 128
+    query blocks).  Chunks of 512 keys, or of S / 8 rounded up to 128 keys
+    when S passes 4096, so a row has at most 8."""
+    ckb = 4 * max(4, -(-S // 1024))
+    per_qb = [-(-((qb + 1) * 4 if causal else S // 32) // ckb) for qb in range(S // 128)]
+    return ckb, max(per_qb), sum(per_qb)
+
+
+def attention_rowstat_bytes(B: int, S: int, Hq: int, causal: bool = True) -> int:
+    """Workspace of the bf16 softmax (ATT_SOFTMAX_BF16): per query and key
+    chunk, the max score and the sum of the weights, as fp32."""
+    return 2 * 4 * attention_stat_chunks(S, causal)[1] * B * Hq * S
 
 
 def attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, B: int, S: int, Hq: int, Hkv: int,
               D: int, scale: float, strides: dict, causal: bool = True, waves: int = None,
               key_block: int = None, ring: bool = None, score_flags: int = 0,
-              divisor: float = None) -> Launch:
+              divisor: float = None, rowstat_ptr: int = 0):
     """Flash-style attention over bf16 q (B, S, Hq, D), k / v (B, S, Hkv, D) and
     o (B, S, Hq, D), each addressed by element strides {"q": (sb, ss, sh), ...}
     with the head dim contiguous.  KV head of query head h is h // (Hq // Hkv).
@@ -566,7 +604,16 @@ def attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, B: int, S: int, Hq
     before the softmax: ATT_RND_PROD rounds q.k to bf16, ATT_DIVIDE divides
     by ``divisor`` (fp32, correctly rounded quotient) instead of multiplying
     by ``scale``, ATT_RND_SCORE rounds the scaled score to bf16.  Any flag
-    selects the ring kernel's score-transform variant (4 waves)."""
+    selects the ring kernel's score-transform variant (4 waves).
+
+    ATT_SOFTMAX_BF16 (with ATT_RND_SCORE) runs the softmax with the bf16
+    cast points of the traced code (examples/models/qwen3/kernels/
+    softmax.py:4-6 on bf16 scores): d = bf16(s - max), e = bf16(exp d),
+    l = bf16(sum e), p = bf16(e / l), o = bf16(sum p v).  It takes three
+    launches over the keys (the row max and the row sum, each over key
+    chunks, then the weighted values) sharing a workspace of
+    ``attention_rowstat_bytes`` at ``rowstat_ptr``; the result is then a
+    list of three launches instead of one launch."""
     if D != 128:
         raise LaunchError(f"attention kernel is built for head_dim 128, got {D}")
     if S % 128 or S <= 0:
@@ -584,8 +631,14 @@ def attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, B: int, S: int, Hq
         raise LaunchError("attention kernel needs a positive score scale")
     if S * max(strides["k"][1], strides["v"][1], 128) * 2 >= 2**31:
         raise LaunchError("attention K / V rows of one sequence must span less than 2 GiB")
-    if score_flags & ~(ATT_RND_PROD | ATT_RND_SCORE | ATT_DIVIDE):
+    if score_flags & ~(ATT_RND_PROD | ATT_RND_SCORE | ATT_SOFTMAX_BF16 | ATT_DIVIDE):
         raise LaunchError(f"unknown attention score flags {score_flags:#x}")
+    smx_bf16 = bool(score_flags & ATT_SOFTMAX_BF16)
+    if smx_bf16:
+        if not score_flags & ATT_RND_SCORE:
+            raise LaunchError("the bf16 softmax runs on scores rounded to bf16 (ATT_RND_SCORE)")
+        if not rowstat_ptr or rowstat_ptr % 4:
+            raise LaunchError("the bf16 softmax needs a 4-byte aligned row statistics workspace")
     vals = [q_ptr, k_ptr, v_ptr, o_ptr]
     for name in "qkvo":
         vals += list(strides[name])
@@ -594,8 +647,14 @@ def attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, B: int, S: int, Hq
         div = np.float32(divisor if divisor is not None else 1.0 / scale)
         if not (np.isfinite(div) and div > 0):
             raise LaunchError("attention score divisor must be finite and positive")
+        # a quotient rounded to bf16 right away: the product by RN(1 / div)
+        # when it gives the same bf16 score for every bf16 product
+        if score_flags & ATT_RND_SCORE and divide_rounds_as_multiply(float(div)):
+            score_flags &= ~ATT_DIVIDE
+            scale = float(np.float32(1) / div)
+    ckb, nch, items_per_head = attention_stat_chunks(S, causal) if smx_bf16 else (0, 0, 0)
     args = AttnArgs(*vals, B, S, Hq, Hkv, float(scale), 1 if causal else 0, float(div),
-                    float(np.float32(1.0) / np.float32(div)), int(score_flags))
+                    float(np.float32(1.0) / np.float32(div)), int(score_flags), int(rowstat_ptr), ckb, nch)
     if score_flags:
         if (waves or 4, key_block or 32, True if ring is None else ring) != (4, 32, True):
             raise LaunchError("attention score cast points exist on the 4-wave ring kernel only")
@@ -621,6 +680,18 @@ def attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, B: int, S: int, Hq
         raise LaunchError("attention grid too large")
     flops = 4 * B * Hq * S * S * D // (2 if causal else 1)
     sym = "nk_attention_causal_d128" + suffix + ("_xf" if score_flags else "")
+    if smx_bf16:
+        qk_bytes = (B * S * Hq * D + B * S * Hkv * D) * 2
+        stat = 4 * nch * B * Hq * S
+        nstat = B * Hq * items_per_head
+        if nstat >= 2**31:
+            raise LaunchError("attention statistics grid too large")
+        return [Launch("attention", "nk_attention_rowmax_d128", (nstat, 1, 1), (256, 1, 1), args,
+                       bytes=qk_bytes + stat, flops=flops // 2),
+                Launch("attention", "nk_attention_rowsum_d128", (nstat, 1, 1), (256, 1, 1), args,
+                       bytes=qk_bytes + 2 * stat, flops=flops // 2),
+                Launch("attention", sym + "_bf16", (nblocks, 1, 1), (64 * waves, 1, 1), args,
+                       bytes=(2 * B * S * Hq * D + 2 * B * S * Hkv * D) * 2 + 2 * stat, flops=flops)]
     return Launch("attention", sym, (nblocks, 1, 1), (64 * waves, 1, 1), args,
                   bytes=(2 * B * S * Hq * D + 2 * B * S * Hkv * D) * 2, flops=flops)
 

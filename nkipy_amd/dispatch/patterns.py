@@ -167,9 +167,9 @@ def _fold_output_convert(L, out: Value, allowed) -> Tuple[Value, List[Node]]:
 class SoftmaxMatch(Match):
     name = "softmax"
 
-    def __init__(self, nodes, x: Value, y: Value):
+    def __init__(self, nodes, x: Value, y: Value, round_ops: bool = False):
         super().__init__(nodes, [x], [y])
-        self.x, self.y = x, y
+        self.x, self.y, self.round_ops = x, y, round_ops
 
     def steps(self, plan):
         x, y = self.x, self.y
@@ -177,15 +177,18 @@ class SoftmaxMatch(Match):
         rows = x.size // n
 
         def make(addr):
-            return LA.softmax_rows(addr(x), addr(y), rows, n, x.dtype, y.dtype)
+            return LA.softmax_rows(addr(x), addr(y), rows, n, x.dtype, y.dtype, round_ops=self.round_ops)
 
-        return [LaunchStep("softmax", f"row softmax {rows}x{n} {dt.name(x.dtype)}->{dt.name(y.dtype)}",
-                           [x], [y], make)]
+        desc = f"row softmax {rows}x{n} {dt.name(x.dtype)}->{dt.name(y.dtype)}"
+        if self.round_ops:
+            desc += f" (steps in {dt.name(x.dtype)})"
+        return [LaunchStep("softmax", desc, [x], [y], make)]
 
 
 class SoftmaxPattern:
     """exp(x - max(x, -1)) / sum(exp(x - max(x, -1)), -1), optionally with an
-    fp32 upcast of a bf16/f16 input and a cast of the result."""
+    fp32 upcast of a bf16/f16 input and a cast of the result.  Steps traced
+    in the 16-bit input type itself are rounded to it as traced."""
 
     def find(self, L):
         for n in L.live:
@@ -228,6 +231,14 @@ class SoftmaxPattern:
             return None
         X, nodes = st
         sub, rm = nodes[3], nodes[4]
+        # the type the steps run in: fp32 throughout, or x's 16-bit type for
+        # x - max, exp, the sum and the divide alike
+        step_types = {sub.out.dtype, nodes[2].out.dtype, nodes[1].out.dtype, n.out.dtype}
+        if len(step_types) != 1:
+            return None
+        round_ops = sub.out.dtype in (dt.bfloat16, dt.float16)
+        if round_ops and X.dtype != sub.out.dtype:
+            return None
         x_in = X
         if op_of(X) == "convert" and X.dtype == dt.float32 and \
                 X.node.inputs[0].dtype in (dt.bfloat16, dt.float16) and X.id not in L.result_ids and \
@@ -242,7 +253,7 @@ class SoftmaxPattern:
             return None
         if (LA.dtype_tag(x_in.dtype), LA.dtype_tag(out.dtype)) not in LA._SOFTMAX_TYPES:
             return None
-        return SoftmaxMatch(nodes, x_in, out)
+        return SoftmaxMatch(nodes, x_in, out, round_ops)
 
 
 # ---------------------------------------------------------------------------

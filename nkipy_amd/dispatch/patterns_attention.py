@@ -37,6 +37,7 @@ from nkipy_amd.dispatch import launchers as LA
 from nkipy_amd.dispatch.patterns import (
     LaunchStep, Match, SoftmaxPattern, _users_of, op_of, scalar_value,
 )
+from nkipy_amd.dispatch.plan import Slot
 from nkipy_amd.dispatch.views import View, _is_view_node, resolve
 
 MASK_LIMIT = -1.0e4
@@ -356,11 +357,19 @@ class AttentionMatch(Match):
         q, k, v, out = self.q, self.k, self.v, self.out
         B, S, Hq, Hkv, D, strides = self.dims
 
+        # the bf16 softmax takes each query's max score and weight sum from
+        # passes of its own
+        rm = None
+        if self.score_flags & LA.ATT_SOFTMAX_BF16:
+            rm = Slot(plan.add_buffer(LA.attention_rowstat_bytes(B, S, Hq, self.causal), "temp",
+                                      "attention.rowstat"))
+
         def make(addr):
             return LA.attention(addr(q.base) + 2 * q.offset, addr(k.base) + 2 * k.offset,
                                 addr(v.base) + 2 * v.offset, addr(out), B, S, Hq, Hkv, D,
                                 self.scale, dict(strides, o=self.o_str), causal=self.causal,
-                                score_flags=self.score_flags, divisor=self.divisor)
+                                score_flags=self.score_flags, divisor=self.divisor,
+                                rowstat_ptr=addr(rm) if rm is not None else 0)
 
         desc = f"{'causal ' if self.causal else ''}attention B={B} S={S} Hq={Hq} Hkv={Hkv} D={D}"
         if self.keys != S:
@@ -493,8 +502,10 @@ class AttentionPattern:
             return None
         d1, scale, divisor, score_flags, snodes = sc
         # a bf16 softmax runs on bf16 scores: the score must have been cast
-        if p_val.dtype == dt.bfloat16 and not score_flags & LA.ATT_RND_SCORE:
-            return None
+        if p_val.dtype == dt.bfloat16:
+            if not score_flags & LA.ATT_RND_SCORE:
+                return None
+            score_flags |= LA.ATT_SOFTMAX_BF16
         nodes += [d1] + snodes
         q = _bf16_view(d1.inputs[0])
         k = _bf16_view(d1.inputs[1])
@@ -545,7 +556,7 @@ class AttentionPattern:
         try:
             LA.attention(16, 16, 16, 16, B, S, Hq, Hkv, D, scale,
                          {"q": qs, "k": (ks[0], ks[1], kg[1]), "v": (vs[0], vs[1], vg[1]), "o": o_str},
-                         causal=causal, score_flags=score_flags, divisor=divisor)
+                         causal=causal, score_flags=score_flags, divisor=divisor, rowstat_ptr=16)
         except LA.LaunchError:
             return None
         if any((vw.offset * 2) % 16 for vw in (q, k, v)):

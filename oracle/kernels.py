@@ -23,6 +23,17 @@ def softmax_kernel(x):
     return exp_x / sum_x
 
 
+def softmax_steps_rounded(x, rnd=bf16_round):
+    """softmax_kernel evaluated in a 16-bit type op by op (the reference's
+    softmax on bf16 scores, examples/models/qwen3/kernels/softmax.py:4-6):
+    x - max, exp, the sum (accumulated in fp32) and the divide each rounded
+    by ``rnd``.  x holds values of that type as float32."""
+    x = np.asarray(x, np.float32)
+    e = rnd(np.exp(rnd(x - x.max(-1, keepdims=True))))
+    tot = rnd(e.sum(-1, keepdims=True, dtype=np.float32))
+    return rnd(e / tot)
+
+
 def softmax_f64(x):
     x = np.asarray(x, dtype=np.float64)
     out = np.empty_like(x)
@@ -429,11 +440,13 @@ def decode_attention(q, cache_k, cache_v, pos, round_prod=False, round_score=Fal
 
 
 def qwen3_prefill_attention(q, cache_k, cache_v, rows=None, round_prod=True, round_score=True,
-                            softmax_bf16=True):
+                            softmax_bf16=True, round_weights=True):
     """q (B, S, Hq, D), caches (B, MAXS, Hkv, D), bf16 values in fp32 arrays
     -> (B, len(rows), Hq, D) fp32 holding the bf16 output values of the
     query positions ``rows`` (all S by default).  The flags drop single cast
-    points (used to show that each one matters)."""
+    points (used to show that each one matters); ``round_weights=False``
+    keeps each weight e / sum(e) unrounded (the one cast point a flash
+    kernel, which divides after the weighted sum, does not take)."""
     q = np.asarray(q, np.float32)
     B, S, Hq, D = q.shape
     MAXS, Hkv = cache_k.shape[1], cache_k.shape[2]
@@ -457,6 +470,6 @@ def qwen3_prefill_attention(q, cache_k, cache_v, rows=None, round_prod=True, rou
             d = keep(s - s.max(-1, keepdims=True))
             e = keep(np.exp(d))
             tot = keep(e.sum(-1, keepdims=True, dtype=np.float32))
-            p = keep(e / tot)
+            p = keep(e / tot) if round_weights else e / tot
             out[b, :, h] = r((p.astype(np.float64) @ v).astype(np.float32))
     return out

@@ -181,8 +181,9 @@ def test_decoder_layer_small(gpu):
 
 
 def test_decoder_layer_config_sampled(gpu):
-    """hidden 4096, 32 / 8 heads, FFN 14336, batch 8 x 2048 tokens; positions
-    of two sequences checked against the oracle's per-position form."""
+    """hidden 4096, 32 / 8 heads, FFN 14336, batch 8 x 2048 tokens: the
+    first and last sequences checked at every position against the oracle's
+    layer, 12 positions of two more against its per-position form."""
     B, S, Hq, Hkv, F = 8, 2048, 32, 8, 14336
     hid = Hq * 128
     rng = np.random.default_rng(5)
@@ -194,7 +195,12 @@ def test_decoder_layer_config_sampled(gpu):
     names = ["x", "an", "wqkv", "sq", "wo", "so", "mn", "wg", "sg", "wu", "su", "wd", "sd"]
     out = dk({n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(names, args)})
     y, a, z, act = (out[f"output{i}"].numpy() for i in range(4))
-    rows = np.array([0, 1, 127, 128, 1029, 2047])
-    for b in (0, 7):
+    for b in (0, B - 1):
+        print(f"decoder config: sequence {b}, all {S} positions", flush=True)
+        got = [dt.to_float32(t[b:b + 1]) for t in (a, z, act, y)]
+        _check_blocks(x[b:b + 1], w, *got, K.decoder_layer_fp8(x[b:b + 1], w), Hq)
+    # 12 positions (tile and block edges, the diagonal blocks, the end)
+    rows = np.array([0, 1, 31, 32, 127, 128, 255, 511, 1029, 1535, 2046, 2047])
+    for b in (3, 5):
         got = [dt.to_float32(t[b, rows]) for t in (a, z, act, y)]
         _check_blocks(x[b, rows], w, *got, K.decoder_layer_fp8_rows(x[b], w, rows), Hq)

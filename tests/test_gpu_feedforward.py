@@ -62,9 +62,9 @@ def test_linear_nt(gpu):
     _close(y, x @ w.T)
 
 
-def test_swiglu_mlp_config_row_sample(gpu):
+def test_swiglu_mlp_config_all_rows(gpu):
     """Config: x (4096, 4096), W_gate / W_up (4096, 14336), W_down (14336, 4096).
-    Rows are independent, so the oracle is evaluated on a sample of rows."""
+    Every row is checked against the oracle."""
     M, H, F = 4096, 4096, 14336
     x, wg, wu, wd = _inputs(M, H, F)
     args = [dt.to_bf16(a) for a in (x, wg, wu, wd)]
@@ -72,6 +72,4 @@ def test_swiglu_mlp_config_row_sample(gpu):
     assert k.plan.kernel_kinds == ["gemm_swiglu", "gemm"]
     ins = {n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(("x", "w_gate", "w_up", "w_down"), args)}
     out = k(ins)["output0"].numpy()
-    rows = np.random.default_rng(0).choice(M, 48, replace=False)
-    ref = K.swiglu_mlp(x[rows], wg, wu, wd, round_h=N.bf16_round)
-    _close(dt.to_float32(out[rows]), ref)
+    _close(dt.to_float32(out), K.swiglu_mlp(x, wg, wu, wd, round_h=N.bf16_round))

@@ -1,6 +1,6 @@
 """GPU parity of the chunked causal linear-attention kernel (K3) against the
 oracle: the float64 quadratic form on small shapes, the fp32 chunked
-recurrence on sampled heads of the full configuration."""
+recurrence on every head of the full configuration."""
 
 import os
 
@@ -74,19 +74,17 @@ def test_linattn_first_position_is_v0(gpu):
     np.testing.assert_allclose(got[0, 0, 0], v[0, 0, 0], rtol=1e-2, atol=1e-3)
 
 
-def test_linattn_config_sampled_heads(gpu):
-    """Config: B=4, H=16, T=8192, d=128; the oracle is run on 3 of the 64 heads."""
+def test_linattn_config_all_heads(gpu):
+    """Config: B=4, H=16, T=8192, d=128; every head against the oracle."""
     B, H, T, D = 4, 16, 8192, 128
     q, k, v = _qkv(B, H, T, D, seed=42)
     got = _run(gpu, q, k, v)
-    for b, h in [(0, 0), (1, 7), (3, 15)]:
-        ref = K.linear_attention_chunked(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1])
-        _close(got[b:b + 1, h:h + 1], ref)
+    _close(got, K.linear_attention_chunked(q, k, v))
 
 
 def test_traced_kernel_config_fused(gpu):
     """The NumPy kernel traced at the config shape lowers to the fused kernel
-    and matches the oracle's chunked recurrence on sampled heads."""
+    and matches the oracle's chunked recurrence on every head."""
     from nkipy_amd.kernels import chunked_linear_attention_kernel
     from nkipy_amd.runtime import DeviceKernel, DeviceTensor
 
@@ -97,9 +95,7 @@ def test_traced_kernel_config_fused(gpu):
     assert dk.plan.kernel_kinds == ["linear_attention"]
     ins = {n: DeviceTensor.from_numpy(a, name=n) for n, a in zip("qkv", args)}
     got = dt.to_float32(dk(ins)["output0"].numpy())
-    for b, h in [(0, 3), (2, 11)]:
-        ref = K.linear_attention_chunked(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1])
-        _close(got[b:b + 1, h:h + 1], ref)
+    _close(got, K.linear_attention_chunked(q, k, v))
 
 
 def test_traced_kernel_fp32_generic_path(gpu):

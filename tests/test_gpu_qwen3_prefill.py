@@ -4,10 +4,11 @@ bf16 KV cache of MAXS rows, scores rounded to bf16 after the product and
 after the divide by sqrt(d), mask rows [:S, :MAXS] of a constant triu mask,
 bf16 softmax, @ values.
 
-* The traced kernel lowers to one attention launch (no score matrix in
-  memory) and matches the oracle's op-by-op bf16 form on sampled query
-  rows at the bf16 bar; cache rows past S hold stale values, which the mask
-  hides.
+* The traced kernel lowers to one attention step (three launches over the
+  keys: row max, row sum, weighted values; no score matrix in memory) and
+  matches the oracle's op-by-op bf16 form on every query row at the bf16
+  bar, bit for bit on at least 99.8% of the outputs; cache rows past S
+  hold stale values, which the mask hides.
 * The whole bf16 Qwen3 attention layer (projection, q / k RMSNorm, RoPE,
   cache write, attention, output projection) lowered with the fused
   attention equals the same graph lowered onto the generic dot / softmax
@@ -18,7 +19,7 @@ import os
 
 import numpy as np
 import pytest
-from parity import assert_close
+from parity import assert_close, ulp_bf16
 
 from nkipy_amd.core import dtypes as dt
 from nkipy_amd.core.trace import NKIPyKernel
@@ -51,9 +52,18 @@ def test_prefill_attention_matches_oracle(gpu, B, S, MAXS, Hq, Hkv):
     ins = {n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(dk.input_tensors_info, args)}
     out = dt.to_float32(dk(ins)["output0"].numpy())
     assert out.shape == (B, S, Hq, D)
-    rows = np.unique(np.concatenate([[0, 1, 31, 32, S // 2, S - 2, S - 1], rng.integers(0, S, 16)]))
-    ref = K.qwen3_prefill_attention(q, ck, cv, rows=rows)
-    assert_close(out[:, rows], ref, _name(), axis=-1)
+    for r0 in range(0, S, 256):  # every query row, 256 at a time
+        rows = np.arange(r0, min(S, r0 + 256))
+        ref = K.qwen3_prefill_attention(q, ck, cv, rows=rows)
+        assert_close(out[:, rows], ref, _name(), axis=-1)
+        d = np.abs(out[:, rows] - ref)
+        ulp = ulp_bf16(ref)
+        print(f"rows {r0}..: identical {np.mean(d == 0):.5f}, max {np.max(d / ulp):.2f} ulp, "
+              f"over 1 ulp {np.mean(d > ulp):.2e}", flush=True)
+        # every cast point is the traced code's: what differs is the order of
+        # the fp32 sums (q.k, the weight sum, p.v), which moves a rounding
+        # across a bf16 boundary now and then
+        assert np.mean(d == 0) >= 0.998
 
 
 def test_prefill_attention_ignores_cache_rows_past_s(gpu):

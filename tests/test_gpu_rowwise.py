@@ -6,6 +6,7 @@ import os
 
 import numpy as np
 import pytest
+from parity import ulp_bf16
 
 from nkipy_amd.core import dtypes as dt
 from nkipy_amd.kernels import residual_rmsnorm_kernel, rmsnorm_kernel, softmax_kernel, softmax_upcast_kernel
@@ -72,6 +73,25 @@ def test_softmax_bf16_upcast(gpu):
     ref = N.bf16_round(K.softmax_kernel(xf))
     np.testing.assert_allclose(dt.to_float32(y), ref, rtol=2e-2, atol=1e-6)
     assert _kinds(softmax_upcast_kernel, dt.to_bf16(xf)) == ["softmax"]
+
+
+@pytest.mark.parametrize("shape", [(64, 1024), (2048, 4096), (5, 8192), (3, 100), (33, 4088)])
+def test_softmax_bf16_steps(gpu, shape):
+    """softmax_kernel on bf16 x runs each step in bf16 (x - max, exp, sum,
+    divide): the kernel rounds the same steps, so the output equals the
+    op-by-op oracle except where an fp32 exp or sum lands on the other side
+    of a bf16 rounding boundary (one step at most)."""
+    rng = np.random.default_rng(shape[1])
+    xf = N.bf16_round(rng.standard_normal(shape) * 4)
+    kinds = DeviceKernel.compile_and_load(softmax_kernel, dt.to_bf16(xf)).plan.kernel_kinds
+    assert kinds == ["softmax"]
+    y = dt.to_float32(baremetal_jit(softmax_kernel)(dt.to_bf16(xf)))
+    ref = K.softmax_steps_rounded(xf)
+    d = np.abs(y - ref)
+    same = float(np.mean(d == 0))
+    print(f"softmax bf16 steps {shape}: identical {same:.6f}, max {np.max(d / ulp_bf16(ref)):.2f} ulp", flush=True)
+    assert same >= 0.999
+    assert np.all(d <= ulp_bf16(ref))
 
 
 def _bf16_inputs(shape, seed=42):

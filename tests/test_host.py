@@ -404,10 +404,31 @@ def test_profile_ranges_need_no_device_and_reject_unbalanced_pops():
     assert b"without a push" in lib.nkh_last_error()
 
 
-def test_lowering_qwen3_prefill_attention_is_one_launch():
+def test_divide_rounds_as_multiply_is_checked_per_divisor():
+    """A score divided by c and rounded to bf16 equals the product by
+    RN(1 / c) rounded to bf16 for every bf16 score when c = sqrt(128), not
+    when c sits next to a ratio of a bf16 significand and a rounding
+    midpoint; the launcher keeps the correctly rounded divide then."""
+    rng = np.random.default_rng(0)
+    s = dt.round_to_bf16(rng.standard_normal(1 << 16).astype(np.float32) * 30)
+    for c, same in ((float(np.sqrt(128)), True), (3.0188679695129395, False)):
+        assert LA.divide_rounds_as_multiply(c) is same
+        if same:  # spot check of the claim on random scores
+            np.testing.assert_array_equal(dt.round_to_bf16(s / np.float32(c)),
+                                          dt.round_to_bf16(s * (np.float32(1) / np.float32(c))))
+        st = {"q": (8 * 128, 128, 8 * 128), "k": (8 * 128, 128, 0), "v": (8 * 128, 128, 0), "o": (8 * 128, 128, 8 * 128)}
+        (_, _, l) = LA.attention(1 << 20, 1 << 20, 1 << 20, 1 << 20, 1, 256, 1, 1, 128, 1 / c, st,
+                                 score_flags=LA.ATT_RND_PROD | LA.ATT_RND_SCORE | LA.ATT_DIVIDE | LA.ATT_SOFTMAX_BF16,
+                                 divisor=c, rowstat_ptr=1 << 20)
+        assert bool(l.args.flags & LA.ATT_DIVIDE) is not same
+
+
+def test_lowering_qwen3_prefill_attention_is_one_step():
     """The Qwen3 prefill form (bf16 scores over the whole cache, mask rows
-    [:S, :MAXS], bf16 softmax) lowers to one attention launch with the score
-    cast points as flags; keys past S are not read."""
+    [:S, :MAXS], bf16 softmax) lowers to one attention step with the score
+    cast points and the bf16 softmax as flags: row-max, row-sum and
+    weighted-value launches sharing one workspace of two statistics per
+    query; keys past S are not read."""
     from nkipy_amd.kernels.qwen3 import prefill_attention_kernel, qwen3_attention_kernel
 
     B, S, MAXS, Hq, Hkv, D = 1, 2048, 4096, 32, 8, 128
@@ -415,11 +436,22 @@ def test_lowering_qwen3_prefill_attention_is_one_launch():
         _bf16((B, S, Hq, D)), _bf16((B, MAXS, Hkv, D)), _bf16((B, MAXS, Hkv, D)))
     plan = lower(g)
     assert plan.kernel_kinds == ["attention"]
-    ((launch,),) = [st.launches(lambda v: 1 << 40) for st in plan.steps]
-    assert launch.symbol == "nk_attention_causal_d128_sp_xf"
-    a = launch.args
-    assert a.flags == LA.ATT_RND_PROD | LA.ATT_RND_SCORE | LA.ATT_DIVIDE and a.S == S and a.causal == 1
-    assert np.float32(a.div) == np.float32(np.sqrt(D))
+    ((rmax, rsum, smx),) = [st.launches(lambda v: 1 << 40) for st in plan.steps]
+    assert [l.symbol for l in (rmax, rsum, smx)] == [
+        "nk_attention_rowmax_d128", "nk_attention_rowsum_d128", "nk_attention_causal_d128_sp_xf_bf16"]
+    assert rmax.args is smx.args and rsum.args is smx.args
+    a = smx.args
+    # the divide by sqrt(128) rounds to bf16 as the product by its reciprocal
+    # does, for every bf16 score: the kernels multiply
+    assert a.flags == LA.ATT_RND_PROD | LA.ATT_RND_SCORE | LA.ATT_SOFTMAX_BF16
+    assert np.float32(a.scale) == np.float32(1) / np.float32(np.sqrt(D))
+    assert a.S == S and a.causal == 1 and a.rowstat == 1 << 40
+    # 512-key chunks: query block qb (128 queries, causal) has ceil((qb + 1) / 4)
+    assert (a.ckb, a.nch) == (16, 4)
+    assert rmax.grid[0] == rsum.grid[0] == Hq * sum(-(-(qb + 1) // 4) for qb in range(S // 128))
+    assert smx.grid[0] == Hq * S // 128
+    temps = [b for b in plan.buffers if b.kind == "temp"]
+    assert [t.nbytes for t in temps] == [LA.attention_rowstat_bytes(B, S, Hq)]
     # the whole layer: no score matrix, no generic products or softmax
     hid = 512
     kinds = _kinds(qwen3_attention_kernel, _bf16((2, 256, hid)), _bf16((hid, 8 * D)), _bf16((D,)), _bf16((D,)),

@@ -349,6 +349,22 @@ def _torch_bf16_attention(q, cache_k, cache_v, rows):
     return (p @ vals).transpose(1, 2).float().numpy()
 
 
+def test_softmax_steps_rounded_matches_torch_bf16_ops():
+    """The 16-bit softmax oracle equals torch's op-by-op bf16 evaluation of
+    exp(x - max) / sum bit for bit (rows of 1 .. 4096, a row with ties)."""
+    rng = np.random.default_rng(31)
+    for n in (1, 7, 256, 4096):
+        x = N.bf16_round(rng.standard_normal((16, n)) * 4)
+        x[0] = 1.5  # all equal
+        t = torch.tensor(x).to(torch.bfloat16)
+        e = torch.exp(t - t.amax(-1, keepdim=True))
+        ref = (e / e.sum(-1, keepdim=True)).float().numpy()
+        np.testing.assert_array_equal(K.softmax_steps_rounded(x), ref)
+    # the steps matter: fp32 steps rounded once differ on most elements
+    x = N.bf16_round(rng.standard_normal((16, 4096)) * 4)
+    assert np.mean(N.bf16_round(K.softmax_kernel(x)) == K.softmax_steps_rounded(x)) < 0.8
+
+
 def test_qwen3_prefill_cast_points_match_torch_bf16_ops():
     """Every cast point of the prefill oracle is pinned: with all of them the
     oracle equals torch's op-by-op bf16 evaluation bit for bit, and dropping
@@ -362,7 +378,7 @@ def test_qwen3_prefill_cast_points_match_torch_bf16_ops():
     ref = _torch_bf16_attention(q, ck, cv, rows)
     got = K.qwen3_prefill_attention(q, ck, cv)
     np.testing.assert_array_equal(got, ref)
-    for drop in ("round_prod", "round_score", "softmax_bf16"):
+    for drop in ("round_prod", "round_score", "softmax_bf16", "round_weights"):
         wrong = K.qwen3_prefill_attention(q, ck, cv, **{drop: False})
         assert np.mean(wrong == ref) < 0.8, drop
     # keys past S (stale cache rows) do not matter: the mask hides them
