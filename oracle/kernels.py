@@ -440,13 +440,14 @@ def decode_attention(q, cache_k, cache_v, pos, round_prod=False, round_score=Fal
 
 
 def qwen3_prefill_attention(q, cache_k, cache_v, rows=None, round_prod=True, round_score=True,
-                            softmax_bf16=True, round_weights=True):
+                            softmax_bf16=True, round_weights=True, causal=True):
     """q (B, S, Hq, D), caches (B, MAXS, Hkv, D), bf16 values in fp32 arrays
     -> (B, len(rows), Hq, D) fp32 holding the bf16 output values of the
     query positions ``rows`` (all S by default).  The flags drop single cast
     points (used to show that each one matters); ``round_weights=False``
     keeps each weight e / sum(e) unrounded (the one cast point a flash
-    kernel, which divides after the weighted sum, does not take)."""
+    kernel, which divides after the weighted sum, does not take);
+    ``causal=False`` drops the mask (every query sees every cache row)."""
     q = np.asarray(q, np.float32)
     B, S, Hq, D = q.shape
     MAXS, Hkv = cache_k.shape[1], cache_k.shape[2]
@@ -454,7 +455,10 @@ def qwen3_prefill_attention(q, cache_k, cache_v, rows=None, round_prod=True, rou
     rows = np.arange(S) if rows is None else np.asarray(rows)
     r = bf16_round
     keep = r if softmax_bf16 else (lambda a: a)
-    mask = r(np.triu(np.ones((MAXS, MAXS)) * -100000, k=1).astype(np.float32))[rows, :MAXS]
+    if causal:
+        mask = r(np.triu(np.ones((MAXS, MAXS)) * -100000, k=1).astype(np.float32))[rows, :MAXS]
+    else:
+        mask = np.zeros((len(rows), MAXS), np.float32)
     out = np.zeros((B, len(rows), Hq, D), np.float32)
     for b in range(B):
         for h in range(Hq):

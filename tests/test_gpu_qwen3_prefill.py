@@ -66,6 +66,66 @@ def test_prefill_attention_matches_oracle(gpu, B, S, MAXS, Hq, Hkv):
         assert np.mean(d == 0) >= 0.998
 
 
+def _check_rows(out, q, ck, cv, causal=True, step=256):
+    """Every query row against the op-by-op oracle at the bf16 bar, and
+    bit for bit on at least 99.8% of the outputs."""
+    S = q.shape[1]
+    for r0 in range(0, S, step):
+        rows = np.arange(r0, min(S, r0 + step))
+        ref = K.qwen3_prefill_attention(q, ck, cv, rows=rows, causal=causal)
+        assert_close(out[:, rows], ref, _name(), axis=-1)
+        same = np.mean(out[:, rows] == ref)
+        print(f"rows {r0}..: identical {same:.5f}", flush=True)
+        assert same >= 0.998
+
+
+def test_bf16_attention_unmasked_statistics_chunks(gpu):
+    """The bf16 score / bf16 softmax form without a mask (every query sees
+    every key, as an encoder's attention does): the statistics kernels run
+    over all S keys of every query block, in five 512-key chunks at S =
+    2560, and the result matches the op-by-op oracle."""
+    from nkipy_amd.kernels.softmax import softmax_kernel
+
+    def bf16_attention(xq, xk, xv):
+        B, S, Hq, D = xq.shape
+        rep = Hq // xk.shape[2]
+        q = xq.transpose(0, 2, 1, 3)
+        k = np.repeat(xk, rep, axis=2).transpose(0, 2, 1, 3)
+        v = np.repeat(xv, rep, axis=2).transpose(0, 2, 1, 3)
+        s = ((q @ k.transpose(0, 1, 3, 2)) / np.float32(np.sqrt(D))).astype(xq.dtype)
+        return (softmax_kernel(s) @ v).transpose(0, 2, 1, 3)
+
+    B, S, Hq, Hkv, D = 1, 2560, 4, 2, 128
+    rng = np.random.default_rng(29)
+    q, k, v = (N.bf16_round(rng.standard_normal((B, S, h, D))) for h in (Hq, Hkv, Hkv))
+    args = [dt.to_bf16(a) for a in (q, k, v)]
+    dk = DeviceKernel.compile_and_load(bf16_attention, *args, name="bf16_attention_unmasked")
+    assert dk.plan.kernel_kinds == ["attention"], dk.plan.kernel_kinds
+    (launches,) = [st.launches(lambda v: 1 << 40) for st in dk.plan.steps]
+    assert [l.args.causal for l in launches] == [0, 0, 0] and launches[0].args.nch == 5
+    ins = {n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(dk.input_tensors_info, args)}
+    out = dt.to_float32(dk(ins)["output0"].numpy())
+    _check_rows(out, q, k, v, causal=False, step=512)
+
+
+def test_prefill_attention_long_rows_many_chunks(gpu):
+    """S = 5120 causal: 640-key chunks (S / 8 rounded up to 128 keys), eight
+    for the last query blocks, against the op-by-op oracle."""
+    from nkipy_amd.kernels.qwen3 import prefill_attention_kernel
+
+    B, S, MAXS, Hq, Hkv, D = 1, 5120, 5120, 2, 1, 128
+    rng = np.random.default_rng(31)
+    q = N.bf16_round(rng.standard_normal((B, S, Hq, D)))
+    ck, cv = (N.bf16_round(rng.standard_normal((B, MAXS, Hkv, D))) for _ in range(2))
+    args = [dt.to_bf16(a) for a in (q, ck, cv)]
+    dk = DeviceKernel.compile_and_load(prefill_attention_kernel, *args, name="prefill_long")
+    (launches,) = [st.launches(lambda v: 1 << 40) for st in dk.plan.steps]
+    assert (launches[0].args.ckb, launches[0].args.nch) == (20, 8)
+    ins = {n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(dk.input_tensors_info, args)}
+    out = dt.to_float32(dk(ins)["output0"].numpy())
+    _check_rows(out, q, ck, cv, step=1024)
+
+
 def test_prefill_attention_ignores_cache_rows_past_s(gpu):
     """Rows S..MAXS-1 of the cache are masked for every query: values there
     (here large ones) change nothing, bit for bit."""

@@ -327,7 +327,7 @@ def test_decode_attention_is_a_row_of_causal_attention():
     assert np.abs(cast - exact).max() > 0
 
 
-def _torch_bf16_attention(q, cache_k, cache_v, rows):
+def _torch_bf16_attention(q, cache_k, cache_v, rows, causal=True):
     """The Qwen3 attention score / softmax / value chain evaluated op by op
     in torch bf16 on the CPU (an independent implementation of per-op bf16
     rounding): bf16 @ bf16 -> bf16, / fp32 scalar -> fp32, .to(bf16), + bf16
@@ -341,8 +341,9 @@ def _torch_bf16_attention(q, cache_k, cache_v, rows):
     vals = torch.repeat_interleave(torch.tensor(cache_v).to(bf), rep, dim=2).transpose(1, 2)
     sc = tq @ keys.transpose(2, 3).contiguous()
     sc = (sc / torch.tensor(np.float32(np.sqrt(D)))).to(bf)
-    mask = torch.tensor(np.triu(np.ones((MAXS, MAXS)) * -100000, k=1).astype(np.float32)).to(bf)
-    sc = sc + mask[torch.as_tensor(rows)][:, :MAXS]
+    if causal:
+        mask = torch.tensor(np.triu(np.ones((MAXS, MAXS)) * -100000, k=1).astype(np.float32)).to(bf)
+        sc = sc + mask[torch.as_tensor(rows)][:, :MAXS]
     e = torch.exp(sc - sc.amax(-1, keepdim=True))
     p = e / e.sum(-1, keepdim=True)
     assert sc.dtype == p.dtype == bf
@@ -389,6 +390,16 @@ def test_qwen3_prefill_cast_points_match_torch_bf16_ops():
     # selected rows equal the same rows of the full evaluation
     sel = np.array([0, 17, S - 1])
     np.testing.assert_array_equal(K.qwen3_prefill_attention(q, ck, cv, rows=sel), got[:, sel])
+    # without the mask (every cache row seen): torch's op-by-op evaluation
+    # again (up to its fp32 sum order: outputs one bf16 step apart now and
+    # then), and the causal form differs
+    qs = N.bf16_round(rng.standard_normal((B, MAXS, Hq, D)))
+    free = K.qwen3_prefill_attention(qs, ck, cv, causal=False)
+    tref = _torch_bf16_attention(qs, ck, cv, np.arange(MAXS), causal=False)
+    assert np.mean(free == tref) > 0.9999
+    step = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(tref), 2.0 ** -126))) - 7)
+    assert np.all(np.abs(free - tref) <= step)
+    assert np.mean(free == K.qwen3_prefill_attention(qs, ck, cv)) < 0.8
 
 
 def test_decode_attention_cast_points_match_torch_bf16_ops():
