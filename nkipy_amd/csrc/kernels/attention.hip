@@ -1026,15 +1026,34 @@ extern "C" __global__ __launch_bounds__(256, 3) void nk_attention_causal_d128_k3
 // exp, the fp32-accumulated sum, the quotient); the weighted sum of values
 // accumulates in fp32.
 //
-// One workgroup (4 waves) per (batch, KV head) serves its rep query heads,
-// so each K / V row is read from HBM once.  Scores of all keys stay in LDS
-// (rep x Smax fp32 <= 64 KiB); K tiles of 128 keys are staged with rows
-// padded to 272 bytes (conflict-free row reads), V tiles unpadded (read
-// along d).
+// One token's attention is little work spread over a long cache, so the
+// keys are cut into splits of DKS = 128 (the cache length fixes the grid;
+// splits past pos exit at once) and the step runs as four launches over a
+// workspace (DecodeAttnArgs::ws):
+//   scores   one workgroup per (batch, KV head, split): the split's K rows
+//            into LDS with 16-byte loads (rows padded to 272 bytes, so the
+//            row reads below are conflict free), thread = (key, half of the
+//            rep queries), fp32 dot products with q from LDS (broadcast
+//            reads), the cast points; the scores and each query's max over
+//            the split go to the workspace;
+//   rowstat  one workgroup per (batch, query head): the row's max m over
+//            the split maxima and the sum l of e = exp(s - m) (block
+//            reduction), each step rounded to bf16 with DEC_SOFTMAX_BF16;
+//   values   one workgroup per (batch, KV head, split): the split's V rows
+//            into LDS and its weights p = e / l (again each step rounded
+//            with DEC_SOFTMAX_BF16) from the scores, m and l; thread =
+//            (column, half of the queries), fp32 sum of p v over the
+//            split's keys, written per split;
+//   combine  one workgroup per (batch, query head): the splits' partial
+//            outputs added in split order, rounded to bf16.
+// Workspace (fp32), with nsplit = ceil(Smax / DKS) and rows r = b * Hq + h:
+//   scores            [r][Smax] at 0
+//   split maxima      [r][nsplit] after B * Hq * Smax
+//   partial outputs   [r][nsplit][128] after that
+//   row statistics    [r][2] (m, l) after that
 #define DQ_MAX 16       // query heads per KV head
-#define DKB 128         // keys per tile
+#define DKS 128         // keys per split
 #define DK_ROW 272      // padded K row (bytes)
-#define DSC_MAX 16384   // rep * Smax scores held in LDS
 
 enum { DEC_RND_PROD = 1, DEC_RND_SCORE = 2, DEC_SOFTMAX_BF16 = 4, DEC_DIVIDE = 8 };
 
@@ -1048,134 +1067,267 @@ struct DecodeAttnArgs {
   int32_t B, Smax, Hq, Hkv;
   float scale;  // multiplied in (divided by with DEC_DIVIDE)
   int32_t flags;
+  float *ws;    // workspace (see above)
+  int32_t nsplit;
 };
 
 __device__ __forceinline__ float bf16r(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
-extern "C" __global__ __launch_bounds__(256) void nk_decode_attention_d128(DecodeAttnArgs a) {
-  __shared__ __attribute__((aligned(16))) float qs[DQ_MAX][AD];
-  __shared__ __attribute__((aligned(16))) uint8_t kt[DKB * DK_ROW];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[DKB * AD];
-  __shared__ float sc[DSC_MAX];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int rep = a.Hq / a.Hkv;
-  const int b = blockIdx.x / a.Hkv, g = blockIdx.x % a.Hkv;
+// attended keys: pos + 1, pos clamped into the cache
+__device__ __forceinline__ int decode_keys(const DecodeAttnArgs &a) {
   int pos = *a.pos;
   pos = pos < 0 ? 0 : (pos >= a.Smax ? a.Smax - 1 : pos);
-  const int L = pos + 1;  // attended keys
-  const int ntiles = (L + DKB - 1) / DKB;
-  const uint16_t *kb = a.k + (int64_t)b * a.k_sb + (int64_t)g * a.k_sh;
-  const uint16_t *vb = a.v + (int64_t)b * a.v_sb + (int64_t)g * a.v_sh;
-  const bool rnd = (a.flags & DEC_SOFTMAX_BF16) != 0;
+  return pos + 1;
+}
 
-  // q of the rep heads as fp32
-  for (int i = tid; i < rep * AD; i += 256) {
-    const int qi = i / AD, d = i % AD;
-    qs[qi][d] = bf16_to_f32(a.q[(int64_t)b * a.q_sb + (int64_t)(g * rep + qi) * a.q_sh + d]);
-  }
+extern "C" __global__ __launch_bounds__(256) void nk_decode_scores_d128(DecodeAttnArgs a) {
+  __shared__ __attribute__((aligned(16))) float qs[DQ_MAX][AD];
+  __shared__ __attribute__((aligned(16))) uint8_t kt[DKS * DK_ROW];
+  __shared__ float smax[DQ_MAX][4];
 
-  // scores: thread -> key r of the tile, queries qi = half, half + 2, ...
-  const int r = tid & (DKB - 1), half = tid >> 7;
-  for (int t = 0; t < ntiles; ++t) {
-    __syncthreads();  // previous tile's reads done (and q staged)
-    for (int i = tid; i < DKB * 16; i += 256) {
-      const int row = i >> 4, c = i & 15;
-      const int key = t * DKB + row;
-      uint4 w = make_uint4(0, 0, 0, 0);
-      if (key < L) w = *reinterpret_cast<const uint4 *>(kb + (int64_t)key * a.k_ss + c * 8);
-      *reinterpret_cast<uint4 *>(kt + row * DK_ROW + c * 16) = w;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rep = a.Hq / a.Hkv;
+  const int sp = blockIdx.x % a.nsplit;
+  const int bg = blockIdx.x / a.nsplit;
+  const int b = bg / a.Hkv, g = bg % a.Hkv;
+  const int L = decode_keys(a);
+  const int k0 = sp * DKS;
+  if (k0 >= L) return;  // uniform: the whole workgroup
+  const int nk = min(DKS, L - k0);
+  const uint16_t *kb = a.k + (int64_t)b * a.k_sb + (int64_t)g * a.k_sh + (int64_t)k0 * a.k_ss;
+
+  // K rows of the split: 16-byte chunk c of row r by thread (r % 16) * 16 +
+  // c, rows r = that + 16 i; then q of the rep heads (thread -> 8 values
+  // of one head).  Every load is issued before the first store (one memory
+  // latency, not nine) and none sits behind a branch: rows past pos load
+  // the last attended row again and store zeros
+  {
+    const int c = tid & 15, r0 = tid >> 4;
+    uint4 w[DKS / 16];
+#pragma unroll
+    for (int i = 0; i < DKS / 16; ++i) {
+      const int row = min(r0 + 16 * i, nk - 1);
+      w[i] = *reinterpret_cast<const uint4 *>(kb + (int64_t)row * a.k_ss + c * 8);
     }
-    __syncthreads();
-    const int key = t * DKB + r;
-    if (key < L) {
-      float acc[DQ_MAX / 2];
+    const int qi = tid >> 4;  // 16 threads x 8 values per head, rep <= 16
+    const uint4 qw = *reinterpret_cast<const uint4 *>(a.q + (int64_t)b * a.q_sb +
+                                                      (int64_t)(g * rep + min(qi, rep - 1)) * a.q_sh + c * 8);
 #pragma unroll
-      for (int j = 0; j < DQ_MAX / 2; ++j) acc[j] = 0.f;
-      for (int c = 0; c < 16; ++c) {
-        const uint4 w = *reinterpret_cast<const uint4 *>(kt + r * DK_ROW + c * 16);
-        float kf[8];
-        kf[0] = __uint_as_float(w.x << 16); kf[1] = __uint_as_float(w.x & 0xffff0000u);
-        kf[2] = __uint_as_float(w.y << 16); kf[3] = __uint_as_float(w.y & 0xffff0000u);
-        kf[4] = __uint_as_float(w.z << 16); kf[5] = __uint_as_float(w.z & 0xffff0000u);
-        kf[6] = __uint_as_float(w.w << 16); kf[7] = __uint_as_float(w.w & 0xffff0000u);
+    for (int i = 0; i < DKS / 16; ++i)
+      *reinterpret_cast<uint4 *>(kt + (r0 + 16 * i) * DK_ROW + c * 16) =
+          r0 + 16 * i < nk ? w[i] : make_uint4(0, 0, 0, 0);
+    if (qi < rep) {
+      float *qd = &qs[qi][c * 8];
+      qd[0] = __uint_as_float(qw.x << 16); qd[1] = __uint_as_float(qw.x & 0xffff0000u);
+      qd[2] = __uint_as_float(qw.y << 16); qd[3] = __uint_as_float(qw.y & 0xffff0000u);
+      qd[4] = __uint_as_float(qw.z << 16); qd[5] = __uint_as_float(qw.z & 0xffff0000u);
+      qd[6] = __uint_as_float(qw.w << 16); qd[7] = __uint_as_float(qw.w & 0xffff0000u);
+    }
+  }
+  __syncthreads();
+
+  // thread -> key r of the split, queries qi = half, half + 2, ...
+  const int r = tid & (DKS - 1), half = tid >> 7;
+  float acc[DQ_MAX / 2];
 #pragma unroll
-        for (int j = 0; j < DQ_MAX / 2; ++j) {
-          const int qi = half + 2 * j;
-          if (qi < rep) {
+  for (int j = 0; j < DQ_MAX / 2; ++j) acc[j] = 0.f;
+  for (int c = 0; c < 16; ++c) {
+    const uint4 w = *reinterpret_cast<const uint4 *>(kt + r * DK_ROW + c * 16);
+    float kf[8];
+    kf[0] = __uint_as_float(w.x << 16); kf[1] = __uint_as_float(w.x & 0xffff0000u);
+    kf[2] = __uint_as_float(w.y << 16); kf[3] = __uint_as_float(w.y & 0xffff0000u);
+    kf[4] = __uint_as_float(w.z << 16); kf[5] = __uint_as_float(w.z & 0xffff0000u);
+    kf[6] = __uint_as_float(w.w << 16); kf[7] = __uint_as_float(w.w & 0xffff0000u);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[j] = fmaf(qs[qi][c * 8 + e], kf[e], acc[j]);
-          }
-        }
+    for (int j = 0; j < DQ_MAX / 2; ++j) {
+      const int qi = half + 2 * j;
+      if (qi < rep) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[j] = fmaf(qs[qi][c * 8 + e], kf[e], acc[j]);
       }
+    }
+  }
+  const int64_t row0 = (int64_t)b * a.Hq + g * rep;  // score row of query 0
+  float *sc = a.ws + row0 * a.Smax;
+  float *mx = a.ws + (int64_t)a.B * a.Hq * a.Smax + row0 * a.nsplit + sp;
 #pragma unroll
-      for (int j = 0; j < DQ_MAX / 2; ++j) {
-        const int qi = half + 2 * j;
-        if (qi < rep) {
-          float s = acc[j];
-          if (a.flags & DEC_RND_PROD) s = bf16r(s);
-          s = (a.flags & DEC_DIVIDE) ? s / a.scale : s * a.scale;
-          if (a.flags & DEC_RND_SCORE) s = bf16r(s);
-          sc[qi * a.Smax + key] = s;
+  for (int j = 0; j < DQ_MAX / 2; ++j) {
+    const int qi = half + 2 * j;
+    if (qi < rep) {  // uniform over the workgroup
+      float s = acc[j];
+      if (a.flags & DEC_RND_PROD) s = bf16r(s);
+      s = (a.flags & DEC_DIVIDE) ? s / a.scale : s * a.scale;
+      if (a.flags & DEC_RND_SCORE) s = bf16r(s);
+      if (r < nk) sc[(int64_t)qi * a.Smax + k0 + r] = s;
+      float m = r < nk ? s : -INFINITY;
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+      if (lane == 0) smax[qi][wave] = m;
+    }
+  }
+  __syncthreads();
+  // waves 0, 1 hold the even queries, waves 2, 3 the odd ones
+  if (tid < rep) {
+    const int w0 = (tid & 1) * 2;
+    mx[(int64_t)tid * a.nsplit] = fmaxf(smax[tid][w0], smax[tid][w0 + 1]);
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void nk_decode_rowstat_d128(DecodeAttnArgs a) {
+  __shared__ float red[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row = blockIdx.x;  // b * Hq + h
+  const int L = decode_keys(a);
+  const int nsp = (L + DKS - 1) / DKS;
+  const bool rnd = (a.flags & DEC_SOFTMAX_BF16) != 0;
+  const float *sc = a.ws + row * a.Smax;
+  const float *mx = a.ws + (int64_t)a.B * a.Hq * a.Smax + row * a.nsplit;
+  constexpr int U = 8;  // loads of a batch first (one latency a batch)
+  float m = -INFINITY;
+  for (int i0 = 0; i0 < nsp; i0 += U) {
+    float x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float y = mx[min(i0 + u, nsp - 1)];  // (in range: the max is unchanged)
+      x[u] = y;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) m = fmaxf(m, x[u]);
+  }
+  float sum = 0.f;
+  for (int j0 = 0; j0 < L; j0 += 256 * U) {
+    float x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) x[u] = sc[min(j0 + u * 256 + tid, L - 1)];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (j0 + u * 256 + tid < L) {
+        float d = x[u] - m;
+        if (rnd) d = bf16r(d);
+        float e = expf(d);
+        if (rnd) e = bf16r(e);
+        sum += e;
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  if (lane == 0) red[wave] = sum;
+  __syncthreads();
+  if (tid == 0) {
+    sum = (red[0] + red[1]) + (red[2] + red[3]);
+    if (rnd) sum = bf16r(sum);
+    float *rs = a.ws + (int64_t)a.B * a.Hq * (a.Smax + a.nsplit + (int64_t)a.nsplit * AD) + row * 2;
+    rs[0] = m;
+    rs[1] = sum;
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void nk_decode_values_d128(DecodeAttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t vt[DKS * AD];
+  __shared__ float ps[DQ_MAX][DKS];
+
+  const int tid = threadIdx.x;
+  const int rep = a.Hq / a.Hkv;
+  const int sp = blockIdx.x % a.nsplit;
+  const int bg = blockIdx.x / a.nsplit;
+  const int b = bg / a.Hkv, g = bg % a.Hkv;
+  const int L = decode_keys(a);
+  const int k0 = sp * DKS;
+  if (k0 >= L) return;
+  const int nk = min(DKS, L - k0);
+  const uint16_t *vb = a.v + (int64_t)b * a.v_sb + (int64_t)g * a.v_sh + (int64_t)k0 * a.v_ss;
+  const int64_t row0 = (int64_t)b * a.Hq + g * rep;
+  const float *pw = a.ws + row0 * a.Smax + k0;
+
+  // V rows as the K rows of the scores kernel, then this thread's scores
+  // (key kk, queries q0, q0 + 2, ...) and their rows' statistics: all loads
+  // first and none behind a branch (indexes clamped into range, results
+  // past pos or rep dropped)
+  {
+    const int c = tid & 15, r0 = tid >> 4;
+    uint4 w[DKS / 16];
+#pragma unroll
+    for (int i = 0; i < DKS / 16; ++i) {
+      const int row = min(r0 + 16 * i, nk - 1);
+      w[i] = *reinterpret_cast<const uint4 *>(vb + (int64_t)row * a.v_ss + c * 8);
+    }
+    const int kk = tid & (DKS - 1), q0 = tid >> 7;
+    const float *rs = a.ws + (int64_t)a.B * a.Hq * (a.Smax + a.nsplit + (int64_t)a.nsplit * AD) + row0 * 2;
+    float pv[DQ_MAX / 2], st[DQ_MAX / 2][2];
+#pragma unroll
+    for (int j = 0; j < DQ_MAX / 2; ++j) {
+      const int qc = min(q0 + 2 * j, rep - 1);
+      pv[j] = pw[(int64_t)qc * a.Smax + min(kk, nk - 1)];
+      st[j][0] = rs[qc * 2];
+      st[j][1] = rs[qc * 2 + 1];
+    }
+#pragma unroll
+    for (int i = 0; i < DKS / 16; ++i)
+      *reinterpret_cast<uint4 *>(vt + (r0 + 16 * i) * AD + c * 8) = r0 + 16 * i < nk ? w[i] : make_uint4(0, 0, 0, 0);
+    const bool rnd = (a.flags & DEC_SOFTMAX_BF16) != 0;
+#pragma unroll
+    for (int j = 0; j < DQ_MAX / 2; ++j) {
+      const int qi = q0 + 2 * j;
+      if (qi < rep) {
+        float p = 0.f;  // (keys past pos: weight 0, never added)
+        if (kk < nk) {
+          float d = pv[j] - st[j][0];
+          if (rnd) d = bf16r(d);
+          float e = expf(d);
+          if (rnd) e = bf16r(e);
+          p = e / st[j][1];
+          if (rnd) p = bf16r(p);
         }
+        ps[qi][kk] = p;
       }
     }
   }
   __syncthreads();
 
-  // softmax per query head (wave w: heads w, w + 4, ...)
-  for (int qi = wave; qi < rep; qi += 4) {
-    float *row = sc + qi * a.Smax;
-    float m = -INFINITY;
-    for (int j = lane; j < L; j += 64) m = fmaxf(m, row[j]);
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    float sum = 0.f;
-    for (int j = lane; j < L; j += 64) {
-      float d = row[j] - m;
-      if (rnd) d = bf16r(d);
-      float e = expf(d);
-      if (rnd) e = bf16r(e);
-      row[j] = e;
-      sum += e;
-    }
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-    if (rnd) sum = bf16r(sum);
-    for (int j = lane; j < L; j += 64) {
-      float p = row[j] / sum;
-      if (rnd) p = bf16r(p);
-      row[j] = p;
-    }
-  }
-
-  // o = P V: thread -> column d, queries qi = half, half + 2, ...
-  const int dcol = tid & (AD - 1);
+  // thread -> column d, queries qi = half, half + 2, ...
+  const int d = tid & (AD - 1), half = tid >> 7;
   float acc[DQ_MAX / 2];
 #pragma unroll
   for (int j = 0; j < DQ_MAX / 2; ++j) acc[j] = 0.f;
-  for (int t = 0; t < ntiles; ++t) {
-    __syncthreads();
-    for (int i = tid; i < DKB * 16; i += 256) {
-      const int row = i >> 4, c = i & 15;
-      const int key = t * DKB + row;
-      uint4 w = make_uint4(0, 0, 0, 0);
-      if (key < L) w = *reinterpret_cast<const uint4 *>(vb + (int64_t)key * a.v_ss + c * 8);
-      *reinterpret_cast<uint4 *>(vt + row * AD + c * 8) = w;
-    }
-    __syncthreads();
-    const int n = min(DKB, L - t * DKB);
-    for (int rr = 0; rr < n; ++rr) {
-      const float vv = bf16_to_f32(vt[rr * AD + dcol]);
+  // keys in order; past nk (a partial last split) the weights are 0 and
+  // not added, so the sum is that of the split's own keys
+  for (int k8 = 0; k8 < nk; k8 += 8) {
+    float vv[8];
 #pragma unroll
-      for (int j = 0; j < DQ_MAX / 2; ++j) {
-        const int qi = half + 2 * j;
-        if (qi < rep) acc[j] = fmaf(sc[qi * a.Smax + t * DKB + rr], vv, acc[j]);
+    for (int u = 0; u < 8; ++u) vv[u] = bf16_to_f32(vt[(k8 + u) * AD + d]);
+#pragma unroll
+    for (int j = 0; j < DQ_MAX / 2; ++j) {
+      const int qi = half + 2 * j;
+      if (qi < rep) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (k8 + u < nk) acc[j] = fmaf(ps[qi][k8 + u], vv[u], acc[j]);
       }
     }
   }
+  float *op = a.ws + (int64_t)a.B * a.Hq * (a.Smax + a.nsplit) + (row0 * a.nsplit + sp) * AD;
 #pragma unroll
   for (int j = 0; j < DQ_MAX / 2; ++j) {
     const int qi = half + 2 * j;
-    if (qi < rep) a.o[(int64_t)b * a.o_sb + (int64_t)(g * rep + qi) * a.o_sh + dcol] = f32_to_bf16(acc[j]);
+    if (qi < rep) op[(int64_t)qi * a.nsplit * AD + d] = acc[j];
   }
+}
+
+extern "C" __global__ __launch_bounds__(128) void nk_decode_combine_d128(DecodeAttnArgs a) {
+  const int d = threadIdx.x;
+  const int64_t row = blockIdx.x;  // b * Hq + h
+  const int b = (int)(row / a.Hq), h = (int)(row % a.Hq);
+  const int nsp = (decode_keys(a) + DKS - 1) / DKS;
+  const float *op = a.ws + (int64_t)a.B * a.Hq * (a.Smax + a.nsplit) + row * a.nsplit * AD + d;
+  float o = 0.f;
+  for (int i0 = 0; i0 < nsp; i0 += 8) {  // loads of a batch first, added in split order
+    float x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = op[(int64_t)min(i0 + u, nsp - 1) * AD];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (i0 + u < nsp) o += x[u];
+  }
+  a.o[(int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d] = f32_to_bf16(o);
 }

@@ -702,22 +702,38 @@ class DecodeAttnArgs(ctypes.Structure):
         [(f"{t}_{s}", ctypes.c_int64) for t, ss in (("q", "bh"), ("k", "bsh"), ("v", "bsh"), ("o", "bh"))
          for s in {"bh": ("sb", "sh"), "bsh": ("sb", "ss", "sh")}[ss]] + \
         [("B", ctypes.c_int32), ("Smax", ctypes.c_int32), ("Hq", ctypes.c_int32), ("Hkv", ctypes.c_int32),
-         ("scale", ctypes.c_float), ("flags", ctypes.c_int32)]
+         ("scale", ctypes.c_float), ("flags", ctypes.c_int32), ("ws", ctypes.c_void_p),
+         ("nsplit", ctypes.c_int32)]
 
 
 DEC_RND_PROD, DEC_RND_SCORE, DEC_SOFTMAX_BF16, DEC_DIVIDE = 1, 2, 4, 8
-DEC_MAX_REP, DEC_MAX_SCORES = 16, 16384
+DEC_MAX_REP = 16
+DEC_SPLIT = 128  # keys per split
+
+
+def decode_attention_workspace_bytes(B: int, Smax: int, Hq: int) -> int:
+    """Workspace of the decode step (fp32): the scores of every cache
+    position, each split's max, each split's partial output and the row's
+    max and weight sum, for every query head."""
+    nsplit = -(-Smax // DEC_SPLIT)
+    return 4 * B * Hq * (Smax + nsplit + nsplit * 128 + 2)
 
 
 def decode_attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, pos_ptr: int, B: int, Smax: int,
-                     Hq: int, Hkv: int, D: int, scale: float, strides: dict, flags: int = 0) -> Launch:
+                     Hq: int, Hkv: int, D: int, scale: float, strides: dict, flags: int = 0,
+                     ws_ptr: int = 0) -> List[Launch]:
     """One query token per sequence against a bf16 KV cache: q (B, Hq, D),
     k / v cache (B, Smax, Hkv, D) and o (B, Hq, D) through element strides
     {"q": (sb, sh), "k": (sb, ss, sh), "v": (sb, ss, sh), "o": (sb, sh)}
     with d contiguous; keys 0..pos attend, pos an int32 in device memory.
     ``flags``: DEC_RND_PROD / DEC_RND_SCORE round the product / the scaled
     score to bf16, DEC_SOFTMAX_BF16 rounds every softmax result to bf16,
-    DEC_DIVIDE divides by ``scale`` instead of multiplying."""
+    DEC_DIVIDE divides by ``scale`` instead of multiplying.
+
+    Four launches over splits of DEC_SPLIT cache positions (scores and
+    split maxima, each row's max and weight sum, per-split weighted values,
+    their sum in split order) sharing a workspace of
+    ``decode_attention_workspace_bytes`` at ``ws_ptr``."""
     if D != 128:
         raise LaunchError(f"decode attention kernel is built for head_dim 128, got {D}")
     if Hkv <= 0 or Hq % Hkv:
@@ -725,20 +741,30 @@ def decode_attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, pos_ptr: in
     rep = Hq // Hkv
     if rep > DEC_MAX_REP:
         raise LaunchError(f"decode attention serves at most {DEC_MAX_REP} query heads per KV head")
-    if Smax <= 0 or rep * Smax > DEC_MAX_SCORES:
-        raise LaunchError(f"decode attention keeps {rep} x {Smax} scores in LDS (at most {DEC_MAX_SCORES})")
+    if Smax <= 0 or Smax >= 2**31 - DEC_SPLIT:
+        raise LaunchError(f"decode attention cache length out of range: {Smax}")
+    if not ws_ptr or ws_ptr % 16:
+        raise LaunchError("decode attention needs a 16-byte aligned workspace")
     if any(int(x) % 8 for x in tuple(strides["k"]) + tuple(strides["v"])) or k_ptr % 16 or v_ptr % 16:
         raise LaunchError("decode attention K / V rows must be 16-byte aligned")
     if q_ptr % 2 or o_ptr % 2 or pos_ptr % 4 or not pos_ptr:
         raise LaunchError("decode attention operands are misaligned")
     if not scale > 0:
         raise LaunchError("decode attention needs a positive score scale")
-    if B * Hkv >= 2**31:
+    nsplit = -(-Smax // DEC_SPLIT)
+    if B * Hkv * nsplit >= 2**31 or B * Hq >= 2**31:
         raise LaunchError("decode attention grid too large")
     args = DecodeAttnArgs(q_ptr, k_ptr, v_ptr, o_ptr, pos_ptr, *strides["q"], *strides["k"], *strides["v"],
-                          *strides["o"], B, Smax, Hq, Hkv, float(scale), int(flags))
-    return Launch("attention", "nk_decode_attention_d128", (B * Hkv, 1, 1), (256, 1, 1), args,
-                  bytes=2 * B * Smax * Hkv * D * 2 + 2 * B * Hq * D * 2, flops=4 * B * Hq * Smax * D)
+                          *strides["o"], B, Smax, Hq, Hkv, float(scale), int(flags), int(ws_ptr), nsplit)
+    kv = B * Smax * Hkv * D * 2  # one cache's bytes (an upper bound: keys past pos are not read)
+    sc = 4 * B * Hq * Smax
+    return [Launch("attention", "nk_decode_scores_d128", (B * Hkv * nsplit, 1, 1), (256, 1, 1), args,
+                   bytes=kv + B * Hq * D * 2 + sc, flops=2 * B * Hq * Smax * D),
+            Launch("attention", "nk_decode_rowstat_d128", (B * Hq, 1, 1), (256, 1, 1), args, bytes=sc),
+            Launch("attention", "nk_decode_values_d128", (B * Hkv * nsplit, 1, 1), (256, 1, 1), args,
+                   bytes=kv + sc + 4 * B * Hq * nsplit * D, flops=2 * B * Hq * Smax * D),
+            Launch("attention", "nk_decode_combine_d128", (B * Hq, 1, 1), (128, 1, 1), args,
+                   bytes=4 * B * Hq * nsplit * D + B * Hq * D * 2)]
 
 
 # ---------------------------------------------------------------------------

@@ -594,11 +594,13 @@ class DecodeAttentionMatch(Match):
     def steps(self, plan):
         q, k, v, out, pos = self.q, self.k, self.v, self.out, self.pos
         B, Sk, Hq, Hkv, D, strides = self.dims
+        ws = Slot(plan.add_buffer(LA.decode_attention_workspace_bytes(B, Sk, Hq), "temp",
+                                  "decode_attention.workspace"))
 
         def make(addr):
             return LA.decode_attention(addr(q.base) + 2 * q.offset, addr(k.base) + 2 * k.offset,
                                        addr(v.base) + 2 * v.offset, addr(out), addr(pos), B, Sk, Hq, Hkv, D,
-                                       self.scale, dict(strides, o=self.o_str), self.flags)
+                                       self.scale, dict(strides, o=self.o_str), self.flags, ws_ptr=addr(ws))
 
         desc = f"decode attention B={B} cache={Sk} Hq={Hq} Hkv={Hkv} D={D} flags={self.flags}"
         return [LaunchStep("decode_attention", desc, self.inputs, self.outputs, make)]
@@ -760,7 +762,7 @@ class DecodeAttentionPattern:
         o_str = (cs[ps[0]], cs[ps[1]])
         strides = {"q": tuple(qs), "k": (ks[0], ks[1], kg[1]), "v": (vs[0], vs[1], vg[1])}
         try:
-            LA.decode_attention(16, 16, 16, 16, 16, B, Sk, Hq, Hkv, D, cv, dict(strides, o=o_str), flags)
+            LA.decode_attention(16, 16, 16, 16, 16, B, Sk, Hq, Hkv, D, cv, dict(strides, o=o_str), flags, ws_ptr=16)
         except LA.LaunchError:
             return None
         if any((vw.offset * 2) % 16 for vw in (k, v)):

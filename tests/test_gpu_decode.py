@@ -26,9 +26,13 @@ def _close(got, ref):
 
 
 @pytest.mark.parametrize("B,Smax,Hq,Hkv,pos", [(1, 128, 4, 1, 0), (2, 256, 8, 2, 100), (2, 300, 4, 2, 299),
-                                                (3, 1024, 16, 4, 1023), (1, 1024, 16, 1, 600)])
+                                                (3, 1024, 16, 4, 1023), (1, 1024, 16, 1, 600),
+                                                (1, 4096, 32, 8, 4095), (2, 5000, 8, 2, 4321),
+                                                (1, 8192, 4, 4, 129)])
 @pytest.mark.parametrize("casts", [True, False])
 def test_decode_attention_kernel(gpu, B, Smax, Hq, Hkv, pos, casts):
+    """Splits of 128 cache positions: one (pos 0), a partial last split
+    (300, 5000 rows; pos 4321), splits past pos left out (pos 129 of 8192)."""
     D = 128
     rng = np.random.default_rng(B * Smax + Hq + pos)
     q = N.bf16_round(rng.standard_normal((B, Hq, D)))
@@ -40,8 +44,10 @@ def test_decode_attention_kernel(gpu, B, Smax, Hq, Hkv, pos, casts):
     flags = (LA.DEC_RND_PROD | LA.DEC_RND_SCORE | LA.DEC_SOFTMAX_BF16) if casts else 0
     st = {"q": (Hq * D, D), "k": (Smax * Hkv * D, Hkv * D, D), "v": (Smax * Hkv * D, Hkv * D, D),
           "o": (Hq * D, D)}
-    LA.decode_attention(tq.ptr, tk.ptr, tv.ptr, to.ptr, tp.ptr, B, Smax, Hq, Hkv, D, float(np.sqrt(D)), st,
-                        flags | LA.DEC_DIVIDE).run(gpu)
+    ws = DeviceTensor.empty((LA.decode_attention_workspace_bytes(B, Smax, Hq),), dt.uint8)
+    for launch in LA.decode_attention(tq.ptr, tk.ptr, tv.ptr, to.ptr, tp.ptr, B, Smax, Hq, Hkv, D,
+                                      float(np.sqrt(D)), st, flags | LA.DEC_DIVIDE, ws_ptr=ws.ptr):
+        launch.run(gpu)
     gpu.sync()
     got = dt.to_float32(to.numpy())
     ref = K.decode_attention(q, ck, cv, pos, casts, casts, casts)
