@@ -1,0 +1,333 @@
+// Projections of a few rows (M <= 8, one decode token per sequence) on
+// gfx950: C[M, N] = A[M, K] @ B with the epilogues of the MFMA GEMM (gemm.hip).
+//
+// At such M the GEMM's 256-row tiles compute mostly padding and its grid
+// has N / 256 workgroups: a token's projection is weight streaming, bound by
+// HBM.  Here the K dimension is cut into ksplit ranges so that the grid
+// fills the part, and each workgroup streams its slice of the weights once:
+//   nk_gemv_{nn,nt}_{bf16,e4m3}[_swiglu]   partial sums over one K range
+//       into an fp32 workspace P[split][m][n] (a second array for the up
+//       weights of the SwiGLU form);
+//   nk_gemv_out_{bf16,f32}[_swiglu]        the splits added in split order,
+//       then the epilogue (per-column scale, bias, bf16 roundings, residual;
+//       or silu(g) u) as the GEMM's, and the store.
+// fp32 accumulation throughout; fp8 codes are decoded exactly (e4m3 fits in
+// fp32) and scaled in the epilogue, as in the GEMM.
+//
+// NN (B is K x N, row-major, ldb): a workgroup owns 256 columns and one K
+// range.  Thread t: column chunk t / 8 (8 columns), k lane t % 8 (rows
+// k0 + t % 8, + 8, ...); a wave's load of one row step covers 8 rows x 128
+// bytes (bf16) or 64 bytes (fp8).  The 8 k lanes of a chunk are added by a
+// fixed shuffle tree.
+// NT (B is N x K, row-major, ldb): a workgroup owns 4 waves x NT_ROWS rows
+// and one K range; the 64 lanes of a wave take 16-byte chunks of each row
+// in turn (1 KiB contiguous per load), the lanes are added by a fixed
+// shuffle tree.
+// A's rows of the K range sit in LDS as bf16 (M x KC <= 8 x 1024).
+// Kernels come for row counts up to MT = 1, 4 and 8 (accumulators sized to
+// MT; _m<MT> in the symbol).
+
+#include "common.h"
+
+using namespace nk;
+
+#define GV_MAX_M 8
+#define GV_MAX_KC 1024
+#define NT_ROWS 4
+
+enum {
+  GEMM_BIAS = 1, GEMM_SCALE = 2, GEMM_RESID = 4, GEMM_RND_BIAS = 16, GEMM_RND_RESID = 32,
+};
+
+struct GemvArgs {
+  const uint16_t *A;     // M x K bf16, row stride lda
+  const void *B0;        // weights (NN: K x N; NT: N x K), row stride ldb
+  const void *B1;        // up weights (SwiGLU), same layout
+  void *C;               // M x N, row stride ldc
+  const uint16_t *bias;  // N bf16
+  const float *scale0;   // N fp32 (fp8 weights)
+  const float *scale1;   // N fp32 (fp8 up weights)
+  const void *resid;     // M x N, C dtype, row stride ldc
+  float *ws;             // P0 [ksplit][M][N], then P1 (SwiGLU)
+  int64_t M, N, K, lda, ldb, ldc;
+  int32_t ksplit, kc;    // K ranges of kc (a multiple of 8, or of 16 for NT fp8)
+  int32_t flags, pad;
+};
+
+// 8 weights of one 16-byte (bf16) or 8-byte (fp8) load as fp32
+template <bool FP8> struct W8;
+template <> struct W8<false> {
+  typedef uint4 raw;
+  static __device__ __forceinline__ raw load(const void *p, int64_t e) {
+    return *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(p) + e);
+  }
+  static __device__ __forceinline__ void decode(const raw &w, float (&f)[8]) {
+    f[0] = __uint_as_float(w.x << 16); f[1] = __uint_as_float(w.x & 0xffff0000u);
+    f[2] = __uint_as_float(w.y << 16); f[3] = __uint_as_float(w.y & 0xffff0000u);
+    f[4] = __uint_as_float(w.z << 16); f[5] = __uint_as_float(w.z & 0xffff0000u);
+    f[6] = __uint_as_float(w.w << 16); f[7] = __uint_as_float(w.w & 0xffff0000u);
+  }
+};
+template <> struct W8<true> {
+  typedef uint2 raw;
+  static __device__ __forceinline__ raw load(const void *p, int64_t e) {
+    return *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint8_t *>(p) + e);
+  }
+  static __device__ __forceinline__ void decode(const raw &w, float (&f)[8]) {
+    const uint4 b = e4m3x8_to_bf16x8(w);  // exact
+    W8<false>::decode(b, f);
+  }
+};
+
+// A's rows m < MT, columns [k0, k0 + kc) into LDS as bf16: zeros past K and
+// for the rows past M, which the kernels then compute with (every
+// accumulator loop has a fixed trip count, so the accumulators stay in
+// registers) and do not store
+template <int MT>
+__device__ __forceinline__ void stage_a(const GemvArgs &a, uint16_t *xs, int64_t k0) {
+  const int per = a.kc / 8;  // 16-byte chunks per row
+  for (int i = threadIdx.x; i < MT * per; i += 256) {
+    const int m = i / per, c = i % per;
+    const int64_t k = k0 + 8 * c;
+    uint4 w = make_uint4(0, 0, 0, 0);
+    if (m < a.M && k < a.K) w = *reinterpret_cast<const uint4 *>(a.A + m * a.lda + k);
+    *reinterpret_cast<uint4 *>(xs + m * a.kc + 8 * c) = w;
+  }
+}
+
+template <bool FP8, bool SWIGLU, int MT>
+__device__ __forceinline__ void gemv_nn_body(const GemvArgs &a) {
+  __shared__ __attribute__((aligned(16))) uint16_t xs[GV_MAX_M * GV_MAX_KC];
+  const int tid = threadIdx.x;
+  const int ks = blockIdx.x % a.ksplit;
+  const int64_t n0 = (int64_t)(blockIdx.x / a.ksplit) * 256;
+  const int64_t k0 = (int64_t)ks * a.kc;
+  stage_a<MT>(a, xs, k0);
+  __syncthreads();
+
+  const int cc = tid >> 3, kl = tid & 7;
+  const int64_t col = n0 + 8 * cc;
+  const bool incol = col < a.N;  // N is a multiple of 8
+  const int64_t colc = incol ? col : 0;
+  const int M = (int)a.M;
+  float acc[SWIGLU ? 2 : 1][MT][8];
+#pragma unroll
+  for (int w = 0; w < (SWIGLU ? 2 : 1); ++w)
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[w][m][e] = 0.f;
+  const int kend = (int)min((int64_t)a.kc, a.K - k0);
+  // rows kl, kl + 8, ... of the range, two in flight
+  for (int kk = kl; kk < kend; kk += 16) {
+    const bool two = kk + 8 < kend;
+    const int64_t r0 = k0 + kk, r1 = two ? r0 + 8 : r0;
+    typename W8<FP8>::raw b0[2], b1[2];
+    b0[0] = W8<FP8>::load(a.B0, r0 * a.ldb + colc);
+    b0[1] = W8<FP8>::load(a.B0, r1 * a.ldb + colc);
+    if constexpr (SWIGLU) {
+      b1[0] = W8<FP8>::load(a.B1, r0 * a.ldb + colc);
+      b1[1] = W8<FP8>::load(a.B1, r1 * a.ldb + colc);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (h == 1 && !two) break;
+      const int kr = kk + 8 * h;
+      float f[8], fu[8];
+      W8<FP8>::decode(b0[h], f);
+      if constexpr (SWIGLU) W8<FP8>::decode(b1[h], fu);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const float xv = bf16_to_f32(xs[m * a.kc + kr]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          acc[0][m][e] = fmaf(xv, f[e], acc[0][m][e]);
+          if constexpr (SWIGLU) acc[1][m][e] = fmaf(xv, fu[e], acc[1][m][e]);
+        }
+      }
+    }
+  }
+  // the 8 k lanes of a chunk: lanes 8j .. 8j + 7 of the wave, a fixed tree
+#pragma unroll
+  for (int w = 0; w < (SWIGLU ? 2 : 1); ++w) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float v = acc[w][m][e];
+        v += __shfl_xor(v, 1, 64);
+        v += __shfl_xor(v, 2, 64);
+        v += __shfl_xor(v, 4, 64);
+        acc[w][m][e] = v;
+      }
+    }
+  }
+  if (kl == 0 && incol) {
+#pragma unroll
+    for (int w = 0; w < (SWIGLU ? 2 : 1); ++w) {
+      float *P = a.ws + (int64_t)w * a.ksplit * a.M * a.N + ((int64_t)ks * a.M) * a.N + col;
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        if (m < M) {
+          float4 *p = reinterpret_cast<float4 *>(P + m * a.N);
+          p[0] = make_float4(acc[w][m][0], acc[w][m][1], acc[w][m][2], acc[w][m][3]);
+          p[1] = make_float4(acc[w][m][4], acc[w][m][5], acc[w][m][6], acc[w][m][7]);
+        }
+      }
+    }
+  }
+}
+
+template <bool FP8, bool SWIGLU, int MT>
+__device__ __forceinline__ void gemv_nt_body(const GemvArgs &a) {
+  __shared__ __attribute__((aligned(16))) uint16_t xs[GV_MAX_M * GV_MAX_KC];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ks = blockIdx.x % a.ksplit;
+  const int64_t nb = (int64_t)(blockIdx.x / a.ksplit) * (4 * NT_ROWS) + wave * NT_ROWS;
+  const int64_t k0 = (int64_t)ks * a.kc;
+  stage_a<MT>(a, xs, k0);
+  __syncthreads();
+
+  constexpr int CK = FP8 ? 16 : 8;  // k per 16-byte chunk
+  const int M = (int)a.M;
+  float acc[SWIGLU ? 2 : 1][MT][NT_ROWS];
+#pragma unroll
+  for (int w = 0; w < (SWIGLU ? 2 : 1); ++w)
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int r = 0; r < NT_ROWS; ++r) acc[w][m][r] = 0.f;
+  const int kend = (int)min((int64_t)a.kc, a.K - k0);  // a multiple of CK
+  for (int kk = lane * CK; kk < kend; kk += 64 * CK) {
+    // this chunk of every row first (NT_ROWS loads per weight in flight)
+    uint4 raw0[NT_ROWS], raw1[NT_ROWS];
+#pragma unroll
+    for (int r = 0; r < NT_ROWS; ++r) {
+      const int64_t n = min(nb + r, a.N - 1);  // rows past N: loaded, never stored
+      const int64_t off = (n * a.ldb + k0 + kk) * (FP8 ? 1 : 2);
+      raw0[r] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint8_t *>(a.B0) + off);
+      if constexpr (SWIGLU) raw1[r] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint8_t *>(a.B1) + off);
+    }
+#pragma unroll
+    for (int h = 0; h < CK / 8; ++h) {
+      float xv[MT][8];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const uint4 xw = *reinterpret_cast<const uint4 *>(xs + m * a.kc + kk + 8 * h);
+        W8<false>::decode(xw, xv[m]);
+      }
+#pragma unroll
+      for (int r = 0; r < NT_ROWS; ++r) {
+        float f[8], fu[8];
+        if constexpr (FP8) {
+          const uint2 half = h ? make_uint2(raw0[r].z, raw0[r].w) : make_uint2(raw0[r].x, raw0[r].y);
+          W8<true>::decode(half, f);
+          if constexpr (SWIGLU) {
+            const uint2 hu = h ? make_uint2(raw1[r].z, raw1[r].w) : make_uint2(raw1[r].x, raw1[r].y);
+            W8<true>::decode(hu, fu);
+          }
+        } else {
+          W8<false>::decode(raw0[r], f);
+          if constexpr (SWIGLU) W8<false>::decode(raw1[r], fu);
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            acc[0][m][r] = fmaf(xv[m][e], f[e], acc[0][m][r]);
+            if constexpr (SWIGLU) acc[1][m][r] = fmaf(xv[m][e], fu[e], acc[1][m][r]);
+          }
+        }
+      }
+    }
+  }
+  // the 64 lanes: a fixed shuffle tree
+#pragma unroll
+  for (int w = 0; w < (SWIGLU ? 2 : 1); ++w)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+#pragma unroll
+      for (int r = 0; r < NT_ROWS; ++r) {
+        float v = acc[w][m][r];
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+        acc[w][m][r] = v;
+      }
+    }
+  if (lane == 0) {
+#pragma unroll
+    for (int w = 0; w < (SWIGLU ? 2 : 1); ++w) {
+      float *P = a.ws + (int64_t)w * a.ksplit * a.M * a.N + ((int64_t)ks * a.M) * a.N;
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+#pragma unroll
+        for (int r = 0; r < NT_ROWS; ++r)
+          if (m < M && nb + r < a.N) P[m * a.N + nb + r] = acc[w][m][r];
+      }
+    }
+  }
+}
+
+#define NK_GEMV_M(layout, wt, FP8, MT)                                                               \
+  extern "C" __global__ __launch_bounds__(256) void nk_gemv_##layout##_##wt##_m##MT(GemvArgs a) {    \
+    gemv_##layout##_body<FP8, false, MT>(a);                                                          \
+  }                                                                                                   \
+  extern "C" __global__ __launch_bounds__(256) void nk_gemv_##layout##_##wt##_swiglu_m##MT(GemvArgs a) { \
+    gemv_##layout##_body<FP8, true, MT>(a);                                                           \
+  }
+#define NK_GEMV(layout, wt, FP8) NK_GEMV_M(layout, wt, FP8, 1) NK_GEMV_M(layout, wt, FP8, 4) NK_GEMV_M(layout, wt, FP8, 8)
+NK_GEMV(nn, bf16, false)
+NK_GEMV(nn, e4m3, true)
+NK_GEMV(nt, bf16, false)
+NK_GEMV(nt, e4m3, true)
+
+// The splits added in split order, then the GEMM's epilogue: thread -> one
+// output (m, n)
+template <typename TC, bool SWIGLU>
+__device__ __forceinline__ void gemv_out_body(const GemvArgs &a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.M * a.N) return;
+  const int64_t m = i / a.N, n = i % a.N;
+  const int64_t plane = a.M * a.N;
+  float g = 0.f, u = 0.f;
+  for (int s0 = 0; s0 < a.ksplit; s0 += 8) {  // loads of a batch first
+    float x[8], y[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int s = min(s0 + j, a.ksplit - 1);
+      x[j] = a.ws[s * plane + i];
+      y[j] = SWIGLU ? a.ws[(a.ksplit + s) * plane + i] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (s0 + j < a.ksplit) {
+        g += x[j];
+        if constexpr (SWIGLU) u += y[j];
+      }
+  }
+  float v;
+  if constexpr (SWIGLU) {
+    if (a.flags & GEMM_SCALE) {
+      g *= a.scale0[n];
+      u *= a.scale1[n];
+    }
+    // silu(g) = g / (1 + exp(-g)) from the hardware 2^x and reciprocal, as
+    // the GEMM's epilogue computes it
+    const float ex = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+    v = g * __builtin_amdgcn_rcpf(1.0f + ex) * u;
+  } else {
+    float prod = (a.flags & GEMM_SCALE) ? g * a.scale0[n] : g;
+    const float bias = (a.flags & GEMM_BIAS) ? bf16_to_f32(a.bias[n]) : 0.f;
+    if (a.flags & GEMM_RND_BIAS) prod = bf16_to_f32(f32_to_bf16(prod));
+    v = prod + bias;
+    if (a.flags & GEMM_RND_RESID) v = bf16_to_f32(f32_to_bf16(v));
+    if (a.flags & GEMM_RESID) v += Elt<TC>::load(reinterpret_cast<const TC *>(a.resid), m * a.ldc + n);
+  }
+  Elt<TC>::store(reinterpret_cast<TC *>(a.C), m * a.ldc + n, v);
+}
+
+extern "C" __global__ __launch_bounds__(256) void nk_gemv_out_bf16(GemvArgs a) { gemv_out_body<bf16, false>(a); }
+extern "C" __global__ __launch_bounds__(256) void nk_gemv_out_f32(GemvArgs a) { gemv_out_body<float, false>(a); }
+extern "C" __global__ __launch_bounds__(256) void nk_gemv_out_bf16_swiglu(GemvArgs a) {
+  gemv_out_body<bf16, true>(a);
+}

@@ -402,6 +402,110 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
 
 
 # ---------------------------------------------------------------------------
+# Projections of a few rows (csrc/kernels/gemv.hip)
+# ---------------------------------------------------------------------------
+class GemvArgs(ctypes.Structure):
+    _fields_ = [
+        ("A", ctypes.c_void_p), ("B0", ctypes.c_void_p), ("B1", ctypes.c_void_p),
+        ("C", ctypes.c_void_p), ("bias", ctypes.c_void_p), ("scale0", ctypes.c_void_p),
+        ("scale1", ctypes.c_void_p), ("resid", ctypes.c_void_p), ("ws", ctypes.c_void_p),
+        ("M", ctypes.c_int64), ("N", ctypes.c_int64), ("K", ctypes.c_int64),
+        ("lda", ctypes.c_int64), ("ldb", ctypes.c_int64), ("ldc", ctypes.c_int64),
+        ("ksplit", ctypes.c_int32), ("kc", ctypes.c_int32), ("flags", ctypes.c_int32), ("pad", ctypes.c_int32),
+    ]
+
+
+GEMV_MAX_M = 8  # rows the split-K projection kernels take
+GEMV_MAX_KC = 1024
+GEMV_NT_ROWS = 16  # weight rows (output columns) per NT workgroup
+_GEMV_TARGET_WGS = 1024
+
+
+def gemv_split(M: int, N: int, K: int, layout: str, fp8: bool):
+    """(ksplit, kc): K ranges of kc (at most 1024, a multiple of 8, or of 16
+    for NT fp8 weights) so that the partial-sum grid has about 1024
+    workgroups."""
+    blocks = -(-N // 256) if layout == "nn" else -(-N // GEMV_NT_ROWS)
+    step = 16 if (fp8 and layout == "nt") else 8
+    ks = max(1, min(-(-_GEMV_TARGET_WGS // blocks), -(-K // step)))
+    kc = -(-(-(-K // ks)) // step) * step
+    if kc > GEMV_MAX_KC:
+        kc = GEMV_MAX_KC
+    return -(-K // kc), kc
+
+
+def gemv_workspace_bytes(M: int, N: int, K: int, layout: str, fp8: bool, swiglu: bool = False) -> int:
+    """fp32 partial sums of every K range (twice for the SwiGLU form)."""
+    ks, _ = gemv_split(M, N, K, layout, fp8)
+    return 4 * ks * M * N * (2 if swiglu else 1)
+
+
+def gemv(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: str, b_dtype, c_dtype,
+         ws_ptr: int, lda: int = None, ldb: int = None, ldc: int = None, bias_ptr: int = 0,
+         scale_ptr: int = 0, resid_ptr: int = 0, up_ptr: int = 0, up_scale_ptr: int = 0,
+         round_before_bias: bool = False, round_before_resid: bool = False) -> List[Launch]:
+    """The operation of :func:`gemm` (same operands and epilogues, no rotary
+    form) for M <= 8 rows: partial sums over K ranges into the workspace at
+    ``ws_ptr`` (``gemv_workspace_bytes``), then the splits added in order and
+    the epilogue.  Two launches."""
+    if layout not in ("nn", "nt"):
+        raise LaunchError(f"unknown GEMM layout {layout}")
+    b_dtype, c_dtype = dt.canonical(b_dtype), dt.canonical(c_dtype)
+    fp8 = b_dtype == dt.float8_e4m3fn
+    if not fp8 and b_dtype != dt.bfloat16:
+        raise LaunchError(f"GEMM weights must be bf16 or float8_e4m3fn, got {dt.name(b_dtype)}")
+    if c_dtype not in (dt.bfloat16, dt.float32):
+        raise LaunchError(f"GEMM output must be bf16 or float32, got {dt.name(c_dtype)}")
+    if not (0 < M <= GEMV_MAX_M) or N <= 0 or K <= 0:
+        raise LaunchError(f"the split-K projection takes 1..{GEMV_MAX_M} rows, got M={M} N={N} K={K}")
+    lda = K if lda is None else lda
+    ldb = (N if layout == "nn" else K) if ldb is None else ldb
+    ldc = N if ldc is None else ldc
+    swiglu = bool(up_ptr)
+    if K % 8 or lda % 8 or ldb % 8:
+        raise LaunchError("GEMM needs K, lda and ldb to be multiples of 8 (16-byte rows)")
+    if lda < K or ldc < N or (layout == "nn" and ldb < N) or (layout == "nt" and ldb < K):
+        raise LaunchError("GEMM leading dimension smaller than the matrix")
+    if layout == "nn" and N % 8:
+        raise LaunchError("NN GEMM needs N to be a multiple of 8")
+    if fp8 and layout == "nt" and (K % 16 or ldb % 16):
+        raise LaunchError("NT GEMM with fp8 weights needs K and ldb to be multiples of 16 (16-byte rows)")
+    balign = 8 if (fp8 and layout == "nn") else 16
+    for p, al in ((a_ptr, 16), (b_ptr, balign), (up_ptr, balign), (ws_ptr, 16)):
+        if p and p % al:
+            raise LaunchError("GEMM operand pointer is not aligned for 128-bit access")
+    if not ws_ptr:
+        raise LaunchError("the split-K projection needs a workspace")
+    if fp8 and not scale_ptr:
+        raise LaunchError("fp8 weights need per-column scales")
+    if swiglu and (fp8 != bool(up_scale_ptr)):
+        raise LaunchError("SwiGLU with fp8 weights needs scales for both weights")
+    if swiglu and (bias_ptr or resid_ptr or c_dtype != dt.bfloat16):
+        raise LaunchError("the SwiGLU epilogue writes bf16 without bias / residual")
+    ks, kc = gemv_split(M, N, K, layout, fp8)
+    blocks = -(-N // 256) if layout == "nn" else -(-N // GEMV_NT_ROWS)
+    if blocks * ks >= 2**31 or M * N >= 2**31:
+        raise LaunchError("GEMM grid too large")
+    flags = (GEMM_BIAS if bias_ptr else 0) | (GEMM_SCALE if scale_ptr else 0) | (GEMM_RESID if resid_ptr else 0)
+    if round_before_bias and bias_ptr:
+        flags |= GEMM_RND_BIAS
+    if round_before_resid and resid_ptr:
+        flags |= GEMM_RND_RESID
+    args = GemvArgs(a_ptr, b_ptr, up_ptr or None, c_ptr, bias_ptr or None, scale_ptr or None,
+                    up_scale_ptr or None, resid_ptr or None, ws_ptr, M, N, K, lda, ldb, ldc, ks, kc, flags, 0)
+    mt = 1 if M == 1 else (4 if M <= 4 else 8)
+    btag = "e4m3" if fp8 else "bf16"
+    sw = "_swiglu" if swiglu else ""
+    n_mm = 2 if swiglu else 1
+    ctag = "bf16" if c_dtype == dt.bfloat16 else "f32"
+    return [Launch("gemv", f"nk_gemv_{layout}_{btag}{sw}_m{mt}", (blocks * ks, 1, 1), (256, 1, 1), args,
+                   bytes=M * K * 2 + n_mm * N * K * b_dtype.itemsize + 4 * ks * M * N * n_mm,
+                   flops=2 * M * N * K * n_mm),
+            Launch("gemv", f"nk_gemv_out_{ctag}{sw}", (-(-M * N // 256), 1, 1), (256, 1, 1), args,
+                   bytes=4 * ks * M * N * n_mm + M * N * c_dtype.itemsize)]
+
+
+# ---------------------------------------------------------------------------
 # Chunked causal linear attention (csrc/kernels/linattn.hip)
 # ---------------------------------------------------------------------------
 class LinAttnArgs(ctypes.Structure):

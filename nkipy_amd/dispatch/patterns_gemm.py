@@ -29,6 +29,7 @@ from typing import List, Optional, Tuple
 from nkipy_amd.core import dtypes as dt
 from nkipy_amd.core.backend.ir import Node, Value
 from nkipy_amd.dispatch import launchers as LA
+from nkipy_amd.dispatch.plan import Slot
 from nkipy_amd.dispatch.patterns import (
     LaunchStep, Match, _users_of, col_broadcast, op_of, scalar_value, through_views,
 )
@@ -165,12 +166,29 @@ class GemmMatch(Match):
         bias, resid = self.bias, self.resid
         rnd_bias, rnd_resid = self.rnd
 
+        # a few rows (a decode token per sequence): the split-K projection,
+        # which streams the weights over the whole part
+        small = M <= LA.GEMV_MAX_M
+        ws = None
+        if small:
+            fp8 = w.value.dtype == dt.float8_e4m3fn
+            ws = Slot(plan.add_buffer(LA.gemv_workspace_bytes(M, N, K, w.layout, fp8, up is not None), "temp",
+                                      "gemv.partials"))
+
         def make(addr):
             up_ptr = 0
             up_scale = 0
             if up is not None:
                 up_ptr = addr(up.value) + off * up.value.dtype.itemsize
                 up_scale = addr(up.scale) if up.scale is not None else 0
+            if small:
+                return LA.gemv(addr(x), addr(w.value), addr(out), M, N, K, layout=w.layout,
+                               b_dtype=w.value.dtype, c_dtype=out.dtype, ldb=ldb, ws_ptr=addr(ws),
+                               bias_ptr=addr(bias) if bias is not None else 0,
+                               scale_ptr=addr(w.scale) if w.scale is not None else 0,
+                               resid_ptr=addr(resid) if resid is not None else 0,
+                               up_ptr=up_ptr, up_scale_ptr=up_scale,
+                               round_before_bias=rnd_bias, round_before_resid=rnd_resid)
             return LA.gemm(addr(x), addr(w.value), addr(out), M, N, K, layout=w.layout,
                            b_dtype=w.value.dtype, c_dtype=out.dtype, ldb=ldb,
                            bias_ptr=addr(bias) if bias is not None else 0,

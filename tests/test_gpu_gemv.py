@@ -1,0 +1,155 @@
+"""GPU parity of the split-K projection kernels (M <= 8 rows, the decode
+case) against NumPy float64 matmul on the same bf16 / fp8 values, across
+layouts, row counts, N and K tails and the GEMM's epilogues; and against the
+MFMA GEMM on the same operands; and the lowering of a decode-shaped
+projection onto them."""
+
+import os
+
+import numpy as np
+import pytest
+from parity import assert_close
+
+from nkipy_amd.core import dtypes as dt
+from nkipy_amd.dispatch import launchers as LA
+from nkipy_amd.runtime import DeviceTensor
+from oracle import kernels as K
+from oracle import numerics as N
+
+pytestmark = pytest.mark.gpu
+
+
+def _close(got, ref, **kw):
+    name = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    assert_close(got, ref, name, **kw)
+
+
+def _run(gpu, launches):
+    for launch in launches:
+        launch.run(gpu)
+    gpu.sync()
+
+
+def _weights(rng, layout, Nn, Kk, fp8):
+    """bf16 or fp8 weights (NN: K x N, NT: N x K) -> (device array, per-column
+    scales or None, float64 K x N matrix of their values)."""
+    shape = (Kk, Nn) if layout == "nn" else (Nn, Kk)
+    w = (rng.standard_normal(shape) * 0.05).astype(np.float32)
+    if not fp8:
+        wb = N.bf16_round(w)
+        mat = wb if layout == "nn" else wb.T
+        return dt.to_bf16(wb), None, mat.astype(np.float64)
+    axis = 0 if layout == "nn" else 1  # the input-feature axis
+    codes, scale = N.quantize_per_channel_e4m3fn(w, axis=axis)
+    deq = N.dequantize_e4m3fn(codes, scale, axis=axis).astype(np.float64)
+    return codes.view(dt.float8_e4m3fn), scale.reshape(-1).astype(np.float32), deq if layout == "nn" else deq.T
+
+
+CASES = [  # (layout, fp8, M, N, K): row counts 1 / 3 / 8, N and K tails
+    ("nn", False, 1, 6144, 4096), ("nn", False, 3, 264, 1000), ("nn", False, 8, 4096, 2048),
+    ("nn", True, 1, 512, 1032), ("nn", True, 5, 1000, 4096),
+    ("nt", False, 1, 4096, 4096), ("nt", False, 2, 100, 1000), ("nt", False, 8, 1000, 520),
+    ("nt", True, 1, 4096, 14336), ("nt", True, 4, 4104, 1008), ("nt", True, 7, 300, 2048),
+]
+
+
+@pytest.mark.parametrize("layout,fp8,M,Nn,Kk", CASES)
+@pytest.mark.parametrize("epi", ["plain", "f32", "bias_resid", "rounded"])
+def test_gemv_matches_float64(gpu, layout, fp8, M, Nn, Kk, epi):
+    rng = np.random.default_rng(M * 7 + Nn + Kk)
+    print(f"gemv {layout} fp8={fp8} M={M} N={Nn} K={Kk} {epi}", flush=True)
+    x = N.bf16_round(rng.standard_normal((M, Kk)))
+    wdev, scale, wmat = _weights(rng, layout, Nn, Kk, fp8)
+    prod = x.astype(np.float64) @ wmat
+    bias = N.bf16_round(rng.standard_normal(Nn) * 0.1)
+    res = N.bf16_round(rng.standard_normal((M, Nn)))
+    out = dt.float32 if epi == "f32" else dt.bfloat16
+    kw = {}
+    ref = prod
+    t = {"x": DeviceTensor.from_numpy(dt.to_bf16(x)), "w": DeviceTensor.from_numpy(wdev)}
+    if scale is not None:
+        t["s"] = DeviceTensor.from_numpy(scale)
+        kw["scale_ptr"] = t["s"].ptr
+    if epi in ("bias_resid", "rounded"):
+        t["b"] = DeviceTensor.from_numpy(dt.to_bf16(bias))
+        t["r"] = DeviceTensor.from_numpy(dt.to_bf16(res))
+        kw.update(bias_ptr=t["b"].ptr, resid_ptr=t["r"].ptr)
+        if epi == "rounded":  # ((x @ w).astype(bf16) + bias).astype(bf16) + r
+            kw.update(round_before_bias=True, round_before_resid=True)
+            ref = N.bf16_round(N.bf16_round(prod) + bias) + res
+        else:
+            ref = prod + bias + res
+    c = DeviceTensor.empty((M, Nn), out)
+    ws = DeviceTensor.empty((LA.gemv_workspace_bytes(M, Nn, Kk, layout, fp8),), dt.uint8)
+    _run(gpu, LA.gemv(t["x"].ptr, t["w"].ptr, c.ptr, M, Nn, Kk, layout=layout,
+                      b_dtype=dt.float8_e4m3fn if fp8 else dt.bfloat16, c_dtype=out, ws_ptr=ws.ptr, **kw))
+    got = c.numpy() if out == dt.float32 else dt.to_float32(c.numpy())
+    if out == dt.float32:  # fp32-accumulation level
+        np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
+    else:
+        _close(got, ref, axis=-1, rounded=N.bf16_round(prod) if epi == "rounded" else None)
+
+
+@pytest.mark.parametrize("layout,fp8,M,Nn,Kk", [("nn", False, 1, 14336, 4096), ("nt", True, 8, 2056, 4096),
+                                                ("nn", True, 3, 1024, 520), ("nt", False, 1, 700, 3000)])
+def test_gemv_swiglu(gpu, layout, fp8, M, Nn, Kk):
+    rng = np.random.default_rng(Nn + Kk)
+    x = N.bf16_round(rng.standard_normal((M, Kk)))
+    wg, sg, mg = _weights(rng, layout, Nn, Kk, fp8)
+    wu, su, mu = _weights(rng, layout, Nn, Kk, fp8)
+    ref = K.silu(x.astype(np.float64) @ mg) * (x.astype(np.float64) @ mu)
+    t = [DeviceTensor.from_numpy(v) for v in (dt.to_bf16(x), wg, wu)]
+    kw = {}
+    if fp8:
+        s = [DeviceTensor.from_numpy(v) for v in (sg, su)]
+        kw = {"scale_ptr": s[0].ptr, "up_scale_ptr": s[1].ptr}
+    h = DeviceTensor.empty((M, Nn), dt.bfloat16)
+    ws = DeviceTensor.empty((LA.gemv_workspace_bytes(M, Nn, Kk, layout, fp8, swiglu=True),), dt.uint8)
+    _run(gpu, LA.gemv(t[0].ptr, t[1].ptr, h.ptr, M, Nn, Kk, layout=layout,
+                      b_dtype=dt.float8_e4m3fn if fp8 else dt.bfloat16, c_dtype=dt.bfloat16, ws_ptr=ws.ptr,
+                      up_ptr=t[2].ptr, **kw))
+    _close(dt.to_float32(h.numpy()), ref, axis=-1)
+
+
+@pytest.mark.parametrize("layout,fp8", [("nn", False), ("nt", False), ("nt", True)])
+def test_gemv_against_mfma_gemm(gpu, layout, fp8):
+    """Same operands through the split-K kernels and the MFMA GEMM: fp32
+    results within the difference of two summation orders."""
+    M, Nn, Kk = 4, 2048, 4096
+    rng = np.random.default_rng(5)
+    x = N.bf16_round(rng.standard_normal((M, Kk)))
+    wdev, scale, _ = _weights(rng, layout, Nn, Kk, fp8)
+    t = [DeviceTensor.from_numpy(v) for v in (dt.to_bf16(x), wdev)]
+    kw = {}
+    if fp8:
+        sd = DeviceTensor.from_numpy(scale)
+        kw["scale_ptr"] = sd.ptr
+    bt = dt.float8_e4m3fn if fp8 else dt.bfloat16
+    c1, c2 = DeviceTensor.empty((M, Nn), dt.float32), DeviceTensor.empty((M, Nn), dt.float32)
+    ws = DeviceTensor.empty((LA.gemv_workspace_bytes(M, Nn, Kk, layout, fp8),), dt.uint8)
+    _run(gpu, LA.gemv(t[0].ptr, t[1].ptr, c1.ptr, M, Nn, Kk, layout=layout, b_dtype=bt, c_dtype=dt.float32,
+                      ws_ptr=ws.ptr, **kw))
+    _run(gpu, [LA.gemm(t[0].ptr, t[1].ptr, c2.ptr, M, Nn, Kk, layout=layout, b_dtype=bt, c_dtype=dt.float32,
+                       **kw)])
+    a, b = c1.numpy(), c2.numpy()
+    np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-5 * np.abs(b).max())
+
+
+def test_decode_projection_lowers_to_gemv(gpu):
+    """A traced decode-shaped projection (x (1, 1, 4096) @ W (4096, 6144),
+    bf16) lowers to the split-K kernels and matches float64."""
+    from nkipy_amd.runtime import DeviceKernel, baremetal_jit
+
+    def proj(x, w):
+        return np.matmul(x, w)
+
+    rng = np.random.default_rng(3)
+    x = N.bf16_round(rng.standard_normal((1, 1, 4096)))
+    w = N.bf16_round(rng.standard_normal((4096, 6144)) * 0.02)
+    args = [dt.to_bf16(a) for a in (x, w)]
+    dk = DeviceKernel.compile_and_load(proj, *args)
+    assert dk.plan.kernel_kinds == ["gemm"]
+    (step,) = dk.plan.steps
+    assert [l.symbol for l in step.launches(lambda v: 1 << 40)] == ["nk_gemv_nn_bf16_m1", "nk_gemv_out_bf16"]
+    got = dt.to_float32(baremetal_jit(proj)(*args))
+    _close(got, x.astype(np.float64) @ w.astype(np.float64), axis=-1)
