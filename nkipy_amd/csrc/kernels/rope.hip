@@ -84,3 +84,159 @@ extern "C" __global__ __launch_bounds__(256) void nk_rope_bf16(RopeArgs a) {
     *reinterpret_cast<uint4 *>(a.out + oo + a.half) = pack8(y1);
   }
 }
+
+// ---------------------------------------------------------------------------
+// Per-head RMSNorm and rotary embedding in bf16 steps: the prologue of
+// examples/models/qwen3/kernels/attention.py:79-97 (q / k RMSNorm over
+// head_dim, then rope.py:4-48 with the cos / sin tables cast to bf16 and
+// taken at the current positions), where every product, sum and difference
+// is a bf16 array:
+//
+//   y = bf16(h / sqrt(mean(h*h) + eps) * w)             (fp32 arithmetic)
+//   out[.., :D/2] = bf16(bf16(y0 * c) - bf16(y1 * s))
+//   out[.., D/2:] = bf16(bf16(y0 * s) + bf16(y1 * c))   y0 / y1 = halves of y
+//
+// One head row of D <= 128 elements per 16-lane DPP row of a wavefront:
+// lane l holds elements 8l .. 8l+7, so the sum of squares is formed exactly
+// as the RMSNorm row kernel forms it for a row of D elements (each lane's
+// eight squares in order, then the same four DPP steps within the 16 lanes,
+// lane 0's sum): the normalised values equal that kernel's bit for bit.
+// Lane l of the first half and lane l + D/16 of the second exchange their
+// values (one ds_bpermute each), then both apply the rotation to the same
+// eight frequencies.  Up to two targets (q and k heads) share the tables; a
+// workgroup (16 rows) serves one target, so their fields are uniform.
+// Tables are fp32 (rounded to bf16 as they are read: the traced astype) or
+// bf16, indexed [row * t_row + s * t_ss + f]; row is the runtime position
+// pos[0] (negative counts from the end, then clamped into the table, as the
+// gather kernel treats an index) or 0.
+// ---------------------------------------------------------------------------
+struct HeadRopeTarget {
+  const uint16_t *x;         // bf16 input rows, d contiguous
+  uint16_t *out;             // bf16 rotated rows
+  const uint16_t *w;         // bf16 norm weight (D elements) or null
+  int64_t x_sb, x_ss, x_sh;  // element strides of x over (b, s, h)
+  int64_t o_sb, o_ss, o_sh;  // element strides of out
+  int64_t x_half;            // element offset of the second half in an input row
+  int64_t rows;              // B * S * H
+  int64_t blocks;            // workgroups serving this target
+  float eps;
+  int32_t H, flags, pad;
+};
+
+struct HeadRopeArgs {
+  HeadRopeTarget t[2];
+  const void *cos_t;
+  const void *sin_t;
+  const int32_t *pos;  // runtime table row, or null
+  int64_t t_row;       // table elements per runtime row
+  int64_t t_ss;        // table element stride over s
+  int64_t t_rows;      // table rows (runtime row clamp)
+  int32_t S, D, tflags, pad;
+};
+
+enum { HR_NORM = 1, HR_MUL_RECIP = 2, HR_W = 4 };  // per target
+enum { HR_TABLE_F32 = 1 };
+
+__device__ __forceinline__ float rbf(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+extern "C" __global__ __launch_bounds__(256) void nk_head_rope_bf16(HeadRopeArgs a) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 15;
+  const bool t1 = (int64_t)blockIdx.x >= a.t[0].blocks;
+  // uniform per workgroup: scalar selects, no indexing of the argument array
+  const uint16_t *x = t1 ? a.t[1].x : a.t[0].x;
+  uint16_t *out = t1 ? a.t[1].out : a.t[0].out;
+  const uint16_t *w = t1 ? a.t[1].w : a.t[0].w;
+  const int64_t x_sb = t1 ? a.t[1].x_sb : a.t[0].x_sb, x_ss = t1 ? a.t[1].x_ss : a.t[0].x_ss;
+  const int64_t x_sh = t1 ? a.t[1].x_sh : a.t[0].x_sh, x_half = t1 ? a.t[1].x_half : a.t[0].x_half;
+  const int64_t o_sb = t1 ? a.t[1].o_sb : a.t[0].o_sb, o_ss = t1 ? a.t[1].o_ss : a.t[0].o_ss;
+  const int64_t o_sh = t1 ? a.t[1].o_sh : a.t[0].o_sh, nrows = t1 ? a.t[1].rows : a.t[0].rows;
+  const float eps = t1 ? a.t[1].eps : a.t[0].eps;
+  const int H = t1 ? a.t[1].H : a.t[0].H, flags = t1 ? a.t[1].flags : a.t[0].flags;
+  const int64_t row = ((int64_t)blockIdx.x - (t1 ? a.t[0].blocks : 0)) * 16 + (tid >> 4);
+
+  const int D = a.D, half = D >> 1, hl = D >> 4;  // hl: lanes per half row
+  const bool second = lane >= hl;
+  const bool live = row < nrows && lane < 2 * hl;
+  // rows < 2^31 (checked by the launcher): 32-bit index arithmetic
+  const uint32_t r = live ? (uint32_t)row : 0u;
+  const int h = (int)(r % (uint32_t)H);
+  const uint32_t bs = r / (uint32_t)H;
+  const int s = (int)(bs % (uint32_t)a.S);
+  const int64_t b = bs / (uint32_t)a.S;
+  const int f0 = live ? 8 * (second ? lane - hl : lane) : 0;  // first frequency of the lane
+  const int64_t col = (second ? half : 0) + f0;                // element of the row
+
+  // every load first: x chunk, weight chunk, table chunks
+  const uint4 xr = *reinterpret_cast<const uint4 *>(x + (live ? b * x_sb + s * x_ss + h * x_sh
+                                                                     + (second ? x_half : 0) + f0 : 0));
+  uint4 wr = make_uint4(0, 0, 0, 0);
+  if (flags & HR_W) wr = *reinterpret_cast<const uint4 *>(w + (live ? col : 0));
+  int64_t trow = 0;
+  if (a.pos != nullptr) {
+    int64_t j = a.pos[0];
+    if (j < 0) j += a.t_rows;
+    trow = j < 0 ? 0 : (j >= a.t_rows ? a.t_rows - 1 : j);
+  }
+  const int64_t to = trow * a.t_row + (int64_t)s * a.t_ss + f0;
+  float c[8], sn[8];
+  if (a.tflags & HR_TABLE_F32) {
+    const float4 *cp = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.cos_t) + to);
+    const float4 *sp = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.sin_t) + to);
+    const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+    const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      c[i] = rbf(cv[i]);
+      sn[i] = rbf(sv[i]);
+    }
+  } else {
+    unpack8(*reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.cos_t) + to), c);
+    unpack8(*reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.sin_t) + to), sn);
+  }
+
+  float v[8];
+  unpack8(xr, v);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = live ? v[j] : 0.f;
+  if (flags & HR_NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += v[j] * v[j];
+    ss = ss + dpp<0xB1>(ss);
+    ss = ss + dpp<0x4E>(ss);
+    ss = ss + dpp<0x124>(ss);
+    ss = ss + dpp<0x128>(ss);
+    ss = __shfl(ss, (tid & 63) & ~15);
+    const float ms = ss / (float)D;
+    const float sd = sqrtf(ms + eps);
+    const float inv = 1.0f / sd;
+    float wv[8];
+    unpack8(wr, wv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float q = (flags & HR_MUL_RECIP) ? v[j] * inv : div_rn(v[j], sd, inv);
+      if (flags & HR_W) q = q * wv[j];
+      v[j] = rbf(q);
+    }
+  }
+  // partner lane: the other half of the same frequencies
+  const int src = ((tid & 63) & ~15) + (second ? lane - hl : lane + hl);
+  float y[8];
+  {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float p = __shfl(v[j], src);
+      // first half: y0 c - y1 s; second half: y0 s + y1 c (own value y1)
+      const float own = rbf(v[j] * c[j]);
+      const float oth = rbf(p * sn[j]);
+      y[j] = rbf(second ? oth + own : own - oth);
+    }
+  }
+  if (live) {
+    const int64_t oo = b * o_sb + s * o_ss + h * o_sh + col;
+    *reinterpret_cast<uint4 *>(out + oo) = pack8(y);
+  }
+}

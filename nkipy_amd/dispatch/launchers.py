@@ -505,6 +505,91 @@ def gemv(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
                    bytes=4 * ks * M * N * n_mm + M * N * c_dtype.itemsize)]
 
 
+class HeadRopeTarget(ctypes.Structure):
+    _fields_ = [("x", ctypes.c_void_p), ("out", ctypes.c_void_p), ("w", ctypes.c_void_p)] + \
+        [(f"{t}_{s}", ctypes.c_int64) for t in "xo" for s in ("sb", "ss", "sh")] + \
+        [("x_half", ctypes.c_int64), ("rows", ctypes.c_int64), ("blocks", ctypes.c_int64),
+         ("eps", ctypes.c_float), ("H", ctypes.c_int32), ("flags", ctypes.c_int32), ("pad", ctypes.c_int32)]
+
+
+class HeadRopeArgs(ctypes.Structure):
+    _fields_ = [("t", HeadRopeTarget * 2), ("cos_t", ctypes.c_void_p), ("sin_t", ctypes.c_void_p),
+                ("pos", ctypes.c_void_p), ("t_row", ctypes.c_int64), ("t_ss", ctypes.c_int64),
+                ("t_rows", ctypes.c_int64), ("S", ctypes.c_int32), ("D", ctypes.c_int32),
+                ("tflags", ctypes.c_int32), ("pad", ctypes.c_int32)]
+
+
+HR_NORM, HR_MUL_RECIP, HR_W = 1, 2, 4
+HR_TABLE_F32 = 1
+
+
+@dataclass
+class HeadRopeSpec:
+    """One tensor of heads for :func:`head_rope`: bf16 rows of D elements at
+    ``x_ptr`` through element strides (b, s, h), the second half of a row
+    ``x_half`` elements after the first; rotated rows to ``out_ptr`` through
+    ``out_strides``.  ``norm``: RMSNorm each row first (``eps``, optional
+    bf16 weight at ``w_ptr``, ``mul_recip`` for the 1/sqrt form)."""
+    x_ptr: int
+    out_ptr: int
+    H: int
+    x_strides: tuple
+    out_strides: tuple
+    x_half: int
+    norm: bool = False
+    eps: float = 0.0
+    w_ptr: int = 0
+    mul_recip: bool = False
+
+
+def head_rope(targets, cos_ptr: int, sin_ptr: int, B: int, S: int, D: int, *, table_f32: bool,
+              pos_ptr: int = 0, table_row: int = 0, table_stride: int = 0, table_rows: int = 1) -> Launch:
+    """Per-head RMSNorm (optional) and split-half rotary embedding in bf16
+    steps of one or two tensors of heads (q and k) sharing cos / sin tables:
+    y = bf16(norm(x)); out = [bf16(bf16(y0 c) - bf16(y1 s)), bf16(bf16(y0 s)
+    + bf16(y1 c))].  Tables are read at element ``row * table_row + s *
+    table_stride + f`` (fp32 rounded to bf16 when ``table_f32``, else bf16),
+    with row the int32 at ``pos_ptr`` (negative from the end, clamped into
+    ``table_rows``) or 0."""
+    targets = list(targets)
+    if not 1 <= len(targets) <= 2:
+        raise LaunchError("head_rope takes one or two tensors of heads")
+    if D % 16 or not 16 <= D <= 128:
+        raise LaunchError(f"head_rope needs a head dim that is a multiple of 16 up to 128, got {D}")
+    half = D // 2
+    tw = 4 if table_f32 else 8  # table elements per 16 bytes
+    if any(int(v) % tw for v in (table_row, table_stride)) or any(p % 16 for p in (cos_ptr, sin_ptr)):
+        raise LaunchError("head_rope tables must keep 16-byte alignment")
+    if pos_ptr and (pos_ptr % 4 or table_rows < 1):
+        raise LaunchError("head_rope runtime position needs an aligned int32 and a table of rows")
+    args = HeadRopeArgs()
+    rows_all = 0
+    for i, t in enumerate(targets):
+        if any(int(v) % 8 for v in tuple(t.x_strides) + tuple(t.out_strides) + (t.x_half,)):
+            raise LaunchError("head_rope strides must keep 16-byte alignment")
+        if any(p % 16 for p in (t.x_ptr, t.out_ptr, t.w_ptr)):
+            raise LaunchError("head_rope operands must be 16-byte aligned")
+        rows = B * S * t.H
+        rows_all += rows
+        if rows <= 0:
+            raise LaunchError("head_rope needs at least one row")
+        flags = (HR_NORM if t.norm else 0) | (HR_MUL_RECIP if t.norm and t.mul_recip else 0) | \
+            (HR_W if t.norm and t.w_ptr else 0)
+        args.t[i] = HeadRopeTarget(t.x_ptr, t.out_ptr, t.w_ptr or None, *[int(v) for v in t.x_strides],
+                                   *[int(v) for v in t.out_strides], int(t.x_half), rows, -(-rows // 16),
+                                   float(t.eps), int(t.H), flags, 0)
+    if rows_all >= 2**31:
+        raise LaunchError("head_rope: too many rows for one launch")
+    args.cos_t, args.sin_t, args.pos = cos_ptr, sin_ptr, pos_ptr or None
+    args.t_row, args.t_ss, args.t_rows = int(table_row), int(table_stride), int(table_rows)
+    args.S, args.D, args.tflags = S, D, HR_TABLE_F32 if table_f32 else 0
+    blocks = sum(int(args.t[i].blocks) for i in range(len(targets)))
+    tb = 4 if table_f32 else 2
+    return Launch("rope", "nk_head_rope_bf16", (blocks, 1, 1), (256, 1, 1), args,
+                  bytes=2 * rows_all * D * 2 + 2 * S * half * tb,
+                  flops=rows_all * D * (6 + (4 if any(t.norm for t in targets) else 0)))
+
+
 # ---------------------------------------------------------------------------
 # Chunked causal linear attention (csrc/kernels/linattn.hip)
 # ---------------------------------------------------------------------------

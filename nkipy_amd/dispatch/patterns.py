@@ -491,7 +491,7 @@ def default_patterns():
 
 def _build_default_patterns():
     from nkipy_amd.dispatch.patterns_attention import (
-        AttentionPattern, DecodeAttentionPattern, QkvRopeFusion, RopePattern,
+        AttentionPattern, DecodeAttentionPattern, HeadRopePattern, QkvRopeFusion, RopePattern,
     )
     from nkipy_amd.dispatch.patterns_gemm import GemmPattern, SwigluPattern
     from nkipy_amd.dispatch.patterns_linattn import LinearAttentionPattern
@@ -500,6 +500,6 @@ def _build_default_patterns():
     # patterns would claim; GEMMs before RMSNorm so that a residual add
     # after a projection goes into the GEMM epilogue; the RoPE of q / k then
     # folds into its QKV projection
-    return [LinearAttentionPattern(), DecodeAttentionPattern(), AttentionPattern(), RopePattern(), SwigluPattern(),
-            GemmPattern(), SoftmaxPattern(), RmsNormPattern(), QkvRopeFusion()]
+    return [LinearAttentionPattern(), DecodeAttentionPattern(), AttentionPattern(), RopePattern(), HeadRopePattern(),
+            SwigluPattern(), GemmPattern(), SoftmaxPattern(), RmsNormPattern(), QkvRopeFusion()]
 

@@ -35,7 +35,7 @@ from nkipy_amd.core import dtypes as dt
 from nkipy_amd.core.backend.ir import Node, Value
 from nkipy_amd.dispatch import launchers as LA
 from nkipy_amd.dispatch.patterns import (
-    LaunchStep, Match, SoftmaxPattern, _users_of, op_of, scalar_value,
+    LaunchStep, Match, RmsNormPattern, SoftmaxPattern, _users_of, op_of, scalar_value,
 )
 from nkipy_amd.dispatch.plan import Slot
 from nkipy_amd.dispatch.views import View, _is_view_node, resolve
@@ -192,6 +192,291 @@ class RopePattern:
             if vw.base is not c0.base and vw.base is not s0.base:
                 nodes += _owned(L, vw, inside)
         return RopeMatch(nodes, x0, x_half, c0, s0, roles, out)
+
+
+# ---------------------------------------------------------------------------
+# Per-head RMSNorm + RoPE in bf16 steps
+# ---------------------------------------------------------------------------
+class HeadRopeMatch(Match):
+    """One or two tensors of heads (q, k) rotated with shared tables, each
+    optionally normalised first: one ``nk_head_rope_bf16`` launch."""
+
+    name = "head_rope"
+
+    def __init__(self, nodes, inputs, outputs, members, table, bsd):
+        super().__init__(nodes, inputs, outputs)
+        self.members, self.table, self.bsd = members, table, bsd
+
+    def steps(self, plan):
+        members, tb = self.members, self.table
+        B, S, D = self.bsd
+
+        def make(addr):
+            specs = []
+            for m in members:
+                xv, nm = m["x"], m["norm"]
+                specs.append(LA.HeadRopeSpec(
+                    addr(xv.base) + 2 * xv.offset, addr(m["out"]), m["H"], m["x_str"], m["o_str"], m["x_half"],
+                    norm=nm is not None, eps=nm.eps if nm is not None else 0.0,
+                    w_ptr=addr(nm.w) if nm is not None and nm.w is not None else 0,
+                    mul_recip=bool(nm.mul_recip) if nm is not None else False))
+            te = 4 if tb["f32"] else 2
+            return LA.head_rope(specs, addr(tb["cos"]) + te * tb["cos_off"], addr(tb["sin"]) + te * tb["sin_off"],
+                                B, S, D, table_f32=tb["f32"],
+                                pos_ptr=addr(tb["pos"]) if tb["pos"] is not None else 0,
+                                table_row=tb["row"], table_stride=tb["ss"], table_rows=tb["rows"])
+
+        parts = [f"{'rmsnorm + ' if m['norm'] is not None else ''}rope {m['H']} heads" for m in members]
+        desc = f"head rope B={B} S={S} D={D} bf16 steps: " + ", ".join(parts) + \
+            (" (runtime position)" if tb["pos"] is not None else "")
+        return [LaunchStep("head_rope", desc, self.inputs, self.outputs, make)]
+
+
+class HeadRopePattern:
+    """Split-half RoPE whose products, sum and difference are bf16 arrays
+    (examples/models/qwen3/kernels/rope.py:23-48 applied to bf16 q / k with
+    the tables cast to bf16, attention.py:84-97)::
+
+        out = concatenate([x0 * c - x1 * s, x0 * s + x1 * c], -1)     all bf16
+
+    with c / s views of one position axis of a table that is an fp32
+    constant cast to bf16, a bf16 array, or either taken at a runtime
+    position (``cos[start_pos]``).  The tensors of heads rotated with the
+    same tables (q and k) form one match, which also claims the table chain
+    (cast, take, layout) and, for a tensor that is a per-head RMSNorm output
+    read only by the rotation (attention.py:79-80), that norm and the views
+    that feed it (the split of the fused QKV projection): the kernel reads
+    the projection in place."""
+
+    def find(self, L):
+        members = []
+        for n in L.live:
+            if n.op == "concatenate" and id(n) not in L.covered:
+                m = self._member(L, n)
+                if m is not None:
+                    members.append(m)
+        groups = {}
+        for m in members:
+            groups.setdefault(m["tkey"], []).append(m)
+        for ms in groups.values():
+            i = 0
+            while i < len(ms):
+                match = self._build(L, ms[i:i + 2]) if i + 1 < len(ms) else None
+                if match is not None:
+                    i += 2
+                    yield match
+                    continue
+                match = self._build(L, ms[i:i + 1])
+                i += 1
+                if match is not None:
+                    yield match
+
+    # -- one rotated tensor ----------------------------------------------
+    @staticmethod
+    def _key(vw: View):
+        return vw.base.id, vw.offset, [tuple(d) for d in vw.dims]
+
+    def _member(self, L, n: Node):
+        if len(n.inputs) != 2 or n.out.dtype != dt.bfloat16 or n.out.ndim != 4 or n.attrs["dimension"] != 3:
+            return None
+        A, Bv = n.inputs
+        D = n.out.shape[-1]
+        half = D // 2
+        if op_of(A) != "subtract" or op_of(Bv) != "add" or A.shape != Bv.shape or A.shape[-1] * 2 != D:
+            return None
+        if D % 16 or D > 128 or any(v.dtype != dt.bfloat16 for v in (A, Bv)):
+            return None
+        muls = list(A.node.inputs) + list(Bv.node.inputs)
+        if any(op_of(v) != "multiply" or v.dtype != dt.bfloat16 for v in muls):
+            return None
+        ops = [[resolve(u, widen_ok=False) for u in v.node.inputs] for v in muls]
+        if any(o.base.dtype != dt.bfloat16 for pair in ops for o in pair):
+            return None
+        # the activation: the base that is one operand of every product
+        for xb in dict.fromkeys(o.base.id for o in ops[0]):
+            sides = []
+            for pair in ops:
+                hit = [k for k in (0, 1) if pair[k].base.id == xb]
+                if len(hit) != 1:
+                    break
+                sides.append((pair[hit[0]], pair[1 - hit[0]]))
+            else:
+                m = self._roles(L, n, sides, muls, half)
+                if m is not None:
+                    return m
+        return None
+
+    def _roles(self, L, n, sides, muls, half):
+        (x0, c0), (x1, s0) = sides[0], sides[1]
+        key = self._key
+        # second half: x0 * s + x1 * c, either order
+        if key(sides[2][0]) == key(x0) and key(sides[3][0]) == key(x1):
+            s1, c1 = sides[2][1], sides[3][1]
+        elif key(sides[3][0]) == key(x0) and key(sides[2][0]) == key(x1):
+            s1, c1 = sides[3][1], sides[2][1]
+        else:
+            return None
+        if key(c1) != key(c0) or key(s1) != key(s0) or key(c0) == key(s0):
+            return None
+        if [tuple(d) for d in x0.dims] != [tuple(d) for d in x1.dims]:
+            return None
+        B, S, H, D = n.out.shape
+        xs = [x0.simple(d) for d in range(4)]
+        if any(v is None for v in xs) or xs[3] != 1:
+            return None
+        x_half = x1.offset - x0.offset
+        # tables: frequency contiguous, broadcast over batch and heads
+        geo = []
+        for tv in (c0, s0):
+            st = [tv.simple(d) for d in range(4)]
+            if any(v is None for v in st) or st[3] != 1 or st[0] != 0 or st[2] != 0:
+                return None
+            geo.append(st[1])
+        if geo[0] != geo[1]:
+            return None
+        tc, ts = self._table(L, c0), self._table(L, s0)
+        if tc is None or ts is None or tc["kind"] != ts["kind"] or tc["f32"] != ts["f32"] or \
+                tc["pos_id"] != ts["pos_id"] or tc["row"] != ts["row"] or tc["rows"] != ts["rows"]:
+            return None
+        nodes = [n, n.inputs[0].node, n.inputs[1].node] + [v.node for v in muls]
+        chain = []  # layout / table nodes, claimed when nothing else reads them
+        for vw in (x0, x1, c0, s0, c1, s1):
+            chain += vw.nodes
+        chain += tc["nodes"] + ts["nodes"]
+        table = {"f32": tc["f32"], "cos": tc["value"], "sin": ts["value"], "cos_off": tc["off"],
+                 "sin_off": ts["off"], "pos": tc["pos"], "row": tc["row"], "rows": tc["rows"], "ss": geo[0]}
+        tkey = (tc["value"].id, ts["value"].id, tc["off"], ts["off"], tc["pos_id"], geo[0], tc["f32"], B, S, D)
+        return {"n": n, "nodes": nodes, "chain": chain, "x": x0, "x_str": tuple(xs[:3]), "x_half": x_half,
+                "H": H, "out": n.out, "o_str": tuple(_contiguous(n.out.shape)[:3]), "norm": None,
+                "bsd": (B, S, D), "table": table, "tkey": tkey}
+
+    @staticmethod
+    def _table(L, tv: View):
+        """A bf16 table view: (value read by the kernel, element offset,
+        fp32?, runtime row, nodes between)."""
+        T = tv.base
+
+        def cast_const(v):
+            if op_of(v) == "convert" and v.dtype == dt.bfloat16 and v.node.inputs[0].dtype == dt.float32 \
+                    and op_of(v.node.inputs[0]) == "constant":
+                return v.node.inputs[0]
+            return None
+
+        if op_of(T) == "take" and T.node.attrs.get("axis") == 0 and T.ndim == 2:
+            src, idx = T.node.inputs
+            if idx.size != 1 or idx.dtype not in (dt.int32,) or src.ndim != 2 or tv.offset >= src.shape[1]:
+                return None
+            c = cast_const(src)
+            val, f32, nodes = (c, True, [T.node, src.node]) if c is not None else (src, False, [T.node])
+            if not f32 and src.dtype != dt.bfloat16:
+                return None
+            return {"kind": "take", "value": val, "off": tv.offset, "f32": f32, "pos": idx, "pos_id": idx.id,
+                    "row": src.shape[1], "rows": src.shape[0], "nodes": nodes}
+        c = cast_const(T)
+        if c is not None:
+            return {"kind": "table", "value": c, "off": tv.offset, "f32": True, "pos": None, "pos_id": None,
+                    "row": 0, "rows": 1, "nodes": [T.node]}
+        if T.dtype == dt.bfloat16:
+            return {"kind": "table", "value": T, "off": tv.offset, "f32": False, "pos": None, "pos_id": None,
+                    "row": 0, "rows": 1, "nodes": []}
+        return None
+
+    # -- the RMSNorm that produced a rotated tensor ------------------------
+    @staticmethod
+    def _norm(L, m):
+        """(norm match, view of its input rows) when the rotated tensor is
+        exactly the output of a per-head RMSNorm over D (no residual)."""
+        X = m["x"].base
+        B, S, D = m["bsd"]
+        dense = tuple(_contiguous(X.shape)[:3])
+        if X.shape != (B, S, m["H"], D) or m["x"].offset != 0 or m["x_half"] != D // 2 or \
+                any(n > 1 and a != b for n, a, b in zip(X.shape, m["x_str"], dense)) or X.id in L.result_ids:
+            return None
+        cands, cur = [], X.node
+        if cur is not None and cur.op == "convert":
+            cur = cur.inputs[0].node
+        if cur is not None and cur.op == "multiply":
+            cands.append(cur)
+            cands += [v.node for v in cur.inputs if v.node is not None and v.node.op in ("divide", "multiply")]
+        elif cur is not None and cur.op == "divide":
+            cands.append(cur)
+        pat = RmsNormPattern()
+        for q in cands:
+            nm = pat._match(L, q)
+            if nm is None or nm.y is not X or nm.r is not None or nm.x.dtype != dt.bfloat16:
+                continue
+            if nm.w is not None and (nm.w.dtype != dt.bfloat16 or nm.w.shape != (D,)):
+                continue
+            xv = resolve(nm.x, widen_ok=False)
+            if xv.base.dtype != dt.bfloat16 or xv.shape != (B, S, m["H"], D):
+                continue
+            st = [xv.simple(d) for d in range(4)]
+            if any(v is None for v in st) or st[3] != 1:
+                continue
+            return nm, xv, tuple(st[:3])
+        return None
+
+    # -- the match ----------------------------------------------------------
+    def _build(self, L, ms):
+        t0 = ms[0]["table"]
+        use = []
+        for m in ms:
+            m = dict(m)
+            nr = self._norm(L, m)
+            if nr is not None:
+                nm, xv, st = nr
+                m.update(norm=nm, x=xv, x_str=st, x_half=m["bsd"][2] // 2)
+                m["nodes"] = m["nodes"] + nm.node_list
+                m["chain"] = m["chain"] + xv.nodes
+            use.append(m)
+        for attempt in (use, [dict(m, norm=None, x=o["x"], x_str=o["x_str"], x_half=o["x_half"],
+                                   nodes=o["nodes"], chain=o["chain"]) for m, o in zip(use, ms)]):
+            match = self._claim(L, attempt, t0)
+            if match is not None:
+                return match
+        return None
+
+    @staticmethod
+    def _claim(L, ms, tb):
+        core = []
+        for m in ms:
+            core += m["nodes"]
+        core_ids = {id(q) for q in core}
+        # layout and table nodes that nothing outside the match reads
+        chain = [q for q in dict.fromkeys(q for m in ms for q in m["chain"]) if id(q) not in core_ids]
+        owned = {id(q) for q in chain}
+        changed = True
+        while changed:
+            changed = False
+            for q in chain:
+                if id(q) not in owned:
+                    continue
+                if q.out.id in L.result_ids or any(id(u) not in core_ids and id(u) not in owned
+                                                   for u in L.users.get(q.out.id, [])):
+                    owned.discard(id(q))
+                    changed = True
+        nodes = core + [q for q in chain if id(q) in owned]
+        node_ids = {id(q) for q in nodes}
+        inputs = []
+        for m in ms:
+            inputs.append(m["x"].base)
+            if m["norm"] is not None and m["norm"].w is not None:
+                inputs.append(m["norm"].w)
+        inputs += [tb["cos"], tb["sin"]] + ([tb["pos"]] if tb["pos"] is not None else [])
+        if any(v.node is not None and id(v.node) in node_ids for v in inputs):
+            return None
+        match = HeadRopeMatch(nodes, list(dict.fromkeys(inputs)), [m["out"] for m in ms], ms, tb, ms[0]["bsd"])
+        if not match.validate(L):
+            return None
+        # the outputs are written at the last claimed node: nothing may read
+        # them earlier
+        order = {id(q): i for i, q in enumerate(L.live)}
+        last = order[id(match.last)]
+        for m in ms:
+            if any(order.get(id(u), last + 1) <= last and id(u) not in node_ids
+                   for u in L.users.get(m["out"].id, [])):
+                return None
+        return match
 
 
 # ---------------------------------------------------------------------------

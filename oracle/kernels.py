@@ -262,6 +262,41 @@ def rope_complex_f64(x, theta):
     return np.concatenate([z.real, z.imag], axis=-1)
 
 
+def rope_split_half_bf16_steps(x, cos, sin):
+    """The rotation as examples/models/qwen3/kernels/rope.py:23-48 computes
+    it on bf16 arrays (attention.py:84-97 casts the tables to the activation
+    dtype): x (B, S, H, D) and the tables (S or 1, D/2) hold bf16 values, and
+    every product, the difference and the sum are rounded to bf16 (each
+    product of two bf16 values is exact in fp32)."""
+    x = np.asarray(x, np.float32)
+    h = x.shape[-1] // 2
+    c = bf16_round(np.asarray(cos, np.float32))[None, :, None, :]
+    s = bf16_round(np.asarray(sin, np.float32))[None, :, None, :]
+    x0, x1 = x[..., :h], x[..., h:]
+    return np.concatenate([bf16_round(bf16_round(x0 * c) - bf16_round(x1 * s)),
+                           bf16_round(bf16_round(x0 * s) + bf16_round(x1 * c))], axis=-1)
+
+
+def qwen3_head_prologue(qkv, q_norm_weight, k_norm_weight, eps, n_heads, n_kv_heads, head_dim, positions,
+                        theta):
+    """q and k of examples/models/qwen3/kernels/attention.py:72-97 from the
+    bf16 QKV projection (B, S, (Hq + 2 Hkv) D): split into heads, per-head
+    RMSNorm (fp32 arithmetic, bf16 result), the bf16-step rotation with the
+    fp32 tables cast to bf16 and taken at ``positions`` (one per token of
+    the sequence axis).  Returns (q, k) as bf16 values."""
+    qkv = np.asarray(qkv, np.float32)
+    B, S, _ = qkv.shape
+    D = head_dim
+    q = qkv[..., :n_heads * D].reshape(B, S, n_heads, D)
+    k = qkv[..., n_heads * D:(n_heads + n_kv_heads) * D].reshape(B, S, n_kv_heads, D)
+    q = rmsnorm_kernel(q, q_norm_weight, eps, round_out=bf16_round)
+    k = rmsnorm_kernel(k, k_norm_weight, eps, round_out=bf16_round)
+    cos, sin = rope_tables(D, int(np.max(positions)) + 1, theta)
+    pos = np.asarray(positions)
+    return (rope_split_half_bf16_steps(q, cos[pos], sin[pos]),
+            rope_split_half_bf16_steps(k, cos[pos], sin[pos]))
+
+
 # ---------------------------------------------------------------------------
 # fp8 decoder layer -- tests/kernels/llama_decoder_dynamo.py:95-337 with the
 # weights of a torch Linear (out, in) stored as e4m3fn codes and a per-output

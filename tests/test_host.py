@@ -423,6 +423,69 @@ def test_divide_rounds_as_multiply_is_checked_per_divisor():
         assert bool(l.args.flags & LA.ATT_DIVIDE) is not same
 
 
+def test_lowering_qwen3_head_prologue_is_one_launch():
+    """The Qwen3 attention prologue (split of the QKV projection, per-head
+    q / k RMSNorm, tables cast to bf16 and taken at the runtime position,
+    bf16-step RoPE) lowers to one head_rope launch that reads the projection
+    in place and the fp32 tables directly; the decode layer keeps only the v
+    split, the two cache writes and the attention between the projections."""
+    from nkipy_amd.kernels.qwen3 import qwen3_attention_kernel
+
+    B, MAXS, HID, H, D, HKV = 2, 512, 512, 8, 128, 2
+    N = (H + 2 * HKV) * D
+
+    def decode(x, qkv_weight, q_norm_weight, k_norm_weight, cache_k, cache_v, start_pos, o_weight):
+        return qwen3_attention_kernel(x, qkv_weight, q_norm_weight, k_norm_weight, 1e-6, H, D, HKV,
+                                      cache_k, cache_v, start_pos, o_weight)
+
+    args = [_bf16((B, 1, HID)), _bf16((HID, N)), _bf16((D,)), _bf16((D,)), _bf16((B, MAXS, HKV, D)),
+            _bf16((B, MAXS, HKV, D)), np.array([7], np.int32), _bf16((H * D, HID))]
+    g = NKIPyKernel.trace(decode).specialize(*args)
+    plan = lower(g)
+    _assert_temps_written_before_read(plan)
+    assert plan.kernel_kinds == ["gemm", "elementwise", "head_rope", "gather", "gather", "decode_attention", "gemm"]
+    (step,) = [st for st in plan.steps if st.kind == "head_rope"]
+    (launch,) = step.launches(lambda v: 1 << 40)
+    a = launch.args
+    assert launch.symbol == "nk_head_rope_bf16"
+    assert a.tflags == LA.HR_TABLE_F32 and a.pos == 1 << 40
+    assert (a.t_row, a.t_rows, a.t_ss, a.S, a.D) == (D // 2, MAXS, 0, 1, D)
+    q, k = a.t[0], a.t[1]
+    for t, heads, col0 in ((q, H, 0), (k, HKV, H * D)):
+        assert t.flags == LA.HR_NORM | LA.HR_W and t.H == heads and t.rows == B * heads
+        assert (t.x_sb, t.x_sh, t.x_half) == (N, D, D // 2)  # the projection read in place
+        assert t.x == (1 << 40) + 2 * col0
+        assert (t.o_sb, t.o_sh) == (heads * D, D)
+        assert np.float32(t.eps) == np.float32(1e-6)
+    assert launch.grid[0] == -(-B * H // 16) + -(-B * HKV // 16)
+    # prefill: the tables sliced by position instead of taken
+    S = 256
+
+    def prefill(x, qkv_weight, q_norm_weight, k_norm_weight, cache_k, cache_v, o_weight):
+        return qwen3_attention_kernel(x, qkv_weight, q_norm_weight, k_norm_weight, 1e-6, H, D, HKV,
+                                      cache_k, cache_v, None, o_weight)
+
+    g = NKIPyKernel.trace(prefill).specialize(_bf16((B, S, HID)), _bf16((HID, N)), _bf16((D,)), _bf16((D,)),
+                                              _bf16((B, MAXS, HKV, D)), _bf16((B, MAXS, HKV, D)),
+                                              _bf16((H * D, HID)))
+    plan = lower(g)
+    _assert_temps_written_before_read(plan)
+    kinds = plan.kernel_kinds
+    assert kinds.count("head_rope") == 1 and "rmsnorm" not in kinds, kinds
+    (step,) = [st for st in plan.steps if st.kind == "head_rope"]
+    (launch,) = step.launches(lambda v: 1 << 40)
+    a = launch.args
+    assert a.pos is None and (a.t_ss, a.S) == (D // 2, S)
+    assert (a.t[0].x_ss, a.t[0].x_sb) == (N, S * N)
+    # without the pattern the same graph takes the generic steps
+    from nkipy_amd.dispatch.patterns import default_patterns
+    from nkipy_amd.dispatch.patterns_attention import HeadRopePattern
+
+    pats = [p for p in default_patterns() if not isinstance(p, HeadRopePattern)]
+    kinds = lower(g, pats).kernel_kinds
+    assert "head_rope" not in kinds and kinds.count("rmsnorm") == 2
+
+
 def test_lowering_qwen3_prefill_attention_is_one_step():
     """The Qwen3 prefill form (bf16 scores over the whole cache, mask rows
     [:S, :MAXS], bf16 softmax) lowers to one attention step with the score

@@ -144,6 +144,57 @@ def test_causal_gqa_attention_vs_f64_loop():
                                rtol=1e-5, atol=1e-6)
 
 
+def test_rope_bf16_steps_matches_torch_bf16_ops():
+    """The bf16-step rotation equals torch's evaluation of the same NumPy
+    expression on bfloat16 tensors (each op rounded to bf16) bit for bit;
+    dropping the rounding of the products changes a visible share of the
+    outputs, so the check pins the cast points."""
+    rng = np.random.default_rng(23)
+    x = N.bf16_round(rng.standard_normal((2, 7, 3, 64)) * 2.0)
+    cos, sin = K.rope_tables(64, 7, 1.0e6)
+    got = K.rope_split_half_bf16_steps(x, cos, sin)
+    bt = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16)
+    xt, ct, st = bt(x), bt(cos)[None, :, None, :], bt(sin)[None, :, None, :]
+    x0, x1 = xt[..., :32], xt[..., 32:]
+    ref = torch.cat([x0 * ct - x1 * st, x0 * st + x1 * ct], dim=-1).to(torch.float32).numpy()
+    np.testing.assert_array_equal(got, ref)
+    c, s = N.bf16_round(cos)[None, :, None, :], N.bf16_round(sin)[None, :, None, :]
+    fused = N.bf16_round(np.concatenate([x[..., :32] * c - x[..., 32:] * s, x[..., :32] * s + x[..., 32:] * c], -1))
+    assert np.mean(fused != ref) > 0.01
+    # position 0 (cos 1, sin 0) is the identity
+    np.testing.assert_array_equal(got[:, 0], x[:, 0])
+
+
+def test_qwen3_head_prologue_matches_torch_bf16_ops():
+    """Split, per-head RMSNorm and bf16-step rotation of the Qwen3 prologue
+    against torch on bfloat16 tensors (norm in fp32, cast to bf16, then each
+    rotation op in bf16) at positions 5 and 9 of a sequence of two tokens."""
+    rng = np.random.default_rng(29)
+    B, S, H, Hkv, D = 2, 2, 4, 2, 64
+    qkv = N.bf16_round(rng.standard_normal((B, S, (H + 2 * Hkv) * D)))
+    wq, wk = N.bf16_round(rng.uniform(0.5, 1.5, D)), N.bf16_round(rng.uniform(0.5, 1.5, D))
+    pos = np.array([5, 9])
+    q, k = K.qwen3_head_prologue(qkv, wq, wk, 1e-6, H, Hkv, D, pos, 1.0e6)
+    bt = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16)
+    cos, sin = K.rope_tables(D, 10, 1.0e6)
+    ct, st = bt(cos[pos])[None, :, None, :], bt(sin[pos])[None, :, None, :]
+
+    def head(x, w):
+        xf = bt(x).to(torch.float32)
+        ms = (xf * xf).mean(-1, keepdim=True) + 1e-6
+        y = (xf / torch.sqrt(ms) * bt(w).to(torch.float32)).to(torch.bfloat16)
+        y0, y1 = y[..., :D // 2], y[..., D // 2:]
+        return torch.cat([y0 * ct - y1 * st, y0 * st + y1 * ct], dim=-1).to(torch.float32).numpy()
+
+    rq = head(qkv[..., :H * D].reshape(B, S, H, D), wq)
+    rk = head(qkv[..., H * D:(H + Hkv) * D].reshape(B, S, Hkv, D), wk)
+    # the norm's fp32 mean may round differently between the two summation
+    # orders; everything after it is identical
+    for a, b in ((q, rq), (k, rk)):
+        assert np.mean(a == b) >= 0.995
+        np.testing.assert_allclose(a, b, rtol=2 ** -7, atol=1e-6)
+
+
 def test_rope_split_half_is_the_complex_rotation():
     rng = np.random.default_rng(11)
     x = N.bf16_round(rng.standard_normal((2, 9, 3, 16)))
