@@ -81,6 +81,9 @@ struct GemmArgs {
   int64_t rope_ts;
   int32_t rope_seq;       // row m sits at position m % rope_seq
   int32_t rope_nq, rope_nk, rope_pad;
+  // split-K entries (*_splitk): K ranges of kc (a multiple of 64), range
+  // blockIdx.y; fp32 partial sums of range s at C + s * M * ldc
+  int32_t ksplit, kc;
 };
 
 // ---------------------------------------------------------------------------
@@ -1901,6 +1904,36 @@ NK_GEMM_NN64(false, float, false, nk_gemm8k_nn_bf16_f32)
 NK_GEMM_NN64(true, bf16, false, nk_gemm8k_swiglu_nn_bf16_bf16)
 NK_GEMM_NN64(false, bf16, true, nk_gemm8k_nn_bf16_bf16_r16)
 NK_GEMM_NN64(true, bf16, true, nk_gemm8k_swiglu_nn_bf16_bf16_r16)
+
+// Split-K entries for short M (a decode batch, a short prefill), where the
+// 256 x 256 tiles leave most CUs idle: workgroup (tile, s) computes the
+// tile's fp32 partial sum over K range s with the unchanged body, handed the
+// range as its operands: A and B advanced to the range's first k, K = the
+// range's length, C = the range's partial plane (flags: at most GEMM_VEC,
+// so the epilogue stores the plain sums).  The bodies' buffer ranges
+// then end where the range ends (rows of NN B, columns of A and NT B past
+// it read zeros, as at a real K end), and the ranges' planes are added in
+// order by the reduction kernel of gemv.hip, which applies the epilogue.
+template <bool NT, int BSZ>
+__device__ __forceinline__ GemmArgs splitk_args(const GemmArgs &a) {
+  GemmArgs s = a;
+  const int64_t k0 = (int64_t)blockIdx.y * a.kc;
+  s.K = min((int64_t)a.kc, a.K - k0);
+  s.A = reinterpret_cast<const uint16_t *>(a.A) + k0;
+  s.B0 = reinterpret_cast<const uint8_t *>(a.B0) + (NT ? k0 * BSZ : k0 * a.ldb * BSZ);
+  s.C = reinterpret_cast<float *>(a.C) + (int64_t)blockIdx.y * a.M * a.ldc;
+  return s;
+}
+
+extern "C" __global__ __launch_bounds__(512, 1) void nk_gemm8k_nn_bf16_f32_splitk(GemmArgs a) {
+  gemm_nn64_body<false, float, false>(splitk_args<false, 2>(a));
+}
+extern "C" __global__ __launch_bounds__(512, 1) void nk_gemm8_nt_bf16_f32_splitk(GemmArgs a) {
+  gemm_pp_body<true, false, false, float>(splitk_args<true, 2>(a));
+}
+extern "C" __global__ __launch_bounds__(512, 1) void nk_gemm8k_nt_e4m3_f32_splitk(GemmArgs a) {
+  gemm_pp64_body<false, float, false, false>(splitk_args<true, 1>(a));
+}
 
 NK_GEMM_ROPE(false, false, nk_gemm8_nn_bf16_bf16_rope)
 NK_GEMM_ROPE(true, false, nk_gemm8_nt_bf16_bf16_rope)

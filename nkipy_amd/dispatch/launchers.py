@@ -236,6 +236,7 @@ class GemmArgs(ctypes.Structure):
         ("rope_q", ctypes.c_void_p), ("rope_k", ctypes.c_void_p),
         ("rope_ts", ctypes.c_int64), ("rope_seq", ctypes.c_int32),
         ("rope_nq", ctypes.c_int32), ("rope_nk", ctypes.c_int32), ("rope_pad", ctypes.c_int32),
+        ("ksplit", ctypes.c_int32), ("kc", ctypes.c_int32),
     ]
 
 
@@ -399,6 +400,87 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
     nbytes = M * K * 2 + n_mm * N * K * b_dtype.itemsize + M * N * c_dtype.itemsize
     return Launch("gemm", symbol, (tiles_m * tiles_n, 1, 1), (512 if pingpong else 256, 1, 1), args,
                   bytes=nbytes, flops=2 * M * N * K * n_mm)
+
+
+SPLITK_TARGET_WGS = 256  # one 8-wave GEMM workgroup per CU
+
+
+def gemm_splitk_split(M: int, N: int, K: int, swiglu: bool = False):
+    """(ksplit, kc) for :func:`gemm_splitk`: K ranges of kc (a multiple of
+    64) so that tiles x ranges is about one workgroup per CU; ksplit 1 when
+    the tiles alone fill the part."""
+    tiles = -(-M // GEMM_BM) * -(-N // GEMM_BN)
+    ks = max(1, min(SPLITK_TARGET_WGS // tiles, -(-K // 64)))
+    kc = -(-(-(-K // ks)) // 64) * 64
+    return -(-K // kc), kc
+
+
+def gemm_splitk_workspace_bytes(M: int, N: int, K: int, swiglu: bool = False) -> int:
+    ks, _ = gemm_splitk_split(M, N, K, swiglu)
+    return 4 * ks * M * N * (2 if swiglu else 1)
+
+
+def gemm_splitk(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: str, b_dtype, c_dtype,
+                ws_ptr: int, lda: int = None, ldb: int = None, ldc: int = None, bias_ptr: int = 0,
+                scale_ptr: int = 0, resid_ptr: int = 0, up_ptr: int = 0, up_scale_ptr: int = 0,
+                round_before_bias: bool = False, round_before_resid: bool = False) -> List[Launch]:
+    """The operation of :func:`gemm` (no rotary form) for few rows: the MFMA
+    kernels over K ranges (grid y) into fp32 partial planes in the workspace
+    at ``ws_ptr`` (``gemm_splitk_workspace_bytes``; the SwiGLU form runs the
+    gate and the up weights into two sets of planes), then the reduction of
+    :func:`gemv` adds the ranges in order and applies the epilogue.  bf16 NN,
+    bf16 NT and fp8 NT weights."""
+    if layout not in ("nn", "nt"):
+        raise LaunchError(f"unknown GEMM layout {layout}")
+    b_dtype, c_dtype = dt.canonical(b_dtype), dt.canonical(c_dtype)
+    fp8 = b_dtype == dt.float8_e4m3fn
+    if fp8 and layout == "nn":
+        raise LaunchError("the split-K GEMM has no fp8 NN variant")
+    if not fp8 and b_dtype != dt.bfloat16:
+        raise LaunchError(f"GEMM weights must be bf16 or float8_e4m3fn, got {dt.name(b_dtype)}")
+    if c_dtype not in (dt.bfloat16, dt.float32):
+        raise LaunchError(f"GEMM output must be bf16 or float32, got {dt.name(c_dtype)}")
+    if M <= 0 or N <= 0 or K <= 0:
+        raise LaunchError(f"GEMM needs positive sizes, got M={M} N={N} K={K}")
+    if not ws_ptr or ws_ptr % 16:
+        raise LaunchError("the split-K GEMM needs a 16-byte aligned workspace")
+    swiglu = bool(up_ptr)
+    lda = K if lda is None else lda
+    ldb = (N if layout == "nn" else K) if ldb is None else ldb
+    ldc = N if ldc is None else ldc
+    if swiglu and (fp8 != bool(up_scale_ptr)):
+        raise LaunchError("SwiGLU with fp8 weights needs scales for both weights")
+    if swiglu and (bias_ptr or resid_ptr or c_dtype != dt.bfloat16):
+        raise LaunchError("the SwiGLU epilogue writes bf16 without bias / residual")
+    if fp8 and not scale_ptr:
+        raise LaunchError("fp8 weights need per-column scales")
+    ks, kc = gemm_splitk_split(M, N, K, swiglu)
+    plane = M * N
+    launches = []
+    for i, bp in enumerate([b_ptr] + ([up_ptr] if swiglu else [])):
+        # the operand checks of gemm(); fp32 partial sums, no epilogue
+        part = gemm(a_ptr, bp, ws_ptr + 4 * i * ks * plane, M, N, K, layout=layout, b_dtype=b_dtype,
+                    c_dtype=dt.float32, lda=lda, ldb=ldb, ldc=N, pingpong=True,
+                    scale_ptr=1 if fp8 else 0)
+        args = part.args
+        args.scale0 = None
+        args.flags &= GEMM_VEC
+        args.ksplit, args.kc = ks, kc
+        launches.append(Launch("gemm", part.symbol + "_splitk", (part.grid[0], ks, 1), part.block, args,
+                               bytes=M * K * 2 + N * K * b_dtype.itemsize + 4 * ks * plane,
+                               flops=2 * M * N * K))
+    flags = (GEMM_BIAS if bias_ptr else 0) | (GEMM_SCALE if scale_ptr else 0) | (GEMM_RESID if resid_ptr else 0)
+    if round_before_bias and bias_ptr:
+        flags |= GEMM_RND_BIAS
+    if round_before_resid and resid_ptr:
+        flags |= GEMM_RND_RESID
+    out = GemvArgs(a_ptr, b_ptr, up_ptr or None, c_ptr, bias_ptr or None, scale_ptr or None,
+                   up_scale_ptr or None, resid_ptr or None, ws_ptr, M, N, K, lda, ldb, ldc, ks, kc, flags, 0)
+    ctag = "bf16" if c_dtype == dt.bfloat16 else "f32"
+    sw = "_swiglu" if swiglu else ""
+    launches.append(Launch("gemv", f"nk_gemv_out_{ctag}{sw}", (-(-plane // 256), 1, 1), (256, 1, 1), out,
+                           bytes=4 * ks * plane * len(launches) + plane * c_dtype.itemsize))
+    return launches
 
 
 # ---------------------------------------------------------------------------

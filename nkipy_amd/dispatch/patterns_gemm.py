@@ -155,6 +155,7 @@ class GemmMatch(Match):
         self.up, self.up_offset = up, up_offset
         self.n_out = n_out
         self.rnd = rnd
+        self.split_k = True  # few rows: partial sums over K ranges
 
     def steps(self, plan):
         x, w, out = self.x, self.w, self.out
@@ -167,13 +168,20 @@ class GemmMatch(Match):
         rnd_bias, rnd_resid = self.rnd
 
         # a few rows (a decode token per sequence): the split-K projection,
-        # which streams the weights over the whole part
+        # which streams the weights over the whole part; up to a tile of rows
+        # (a decode batch): the MFMA kernels over K ranges, so that the
+        # grid fills the part
+        fp8 = w.value.dtype == dt.float8_e4m3fn
         small = M <= LA.GEMV_MAX_M
+        splitk = (self.split_k and not small and M <= LA.GEMM_BM and not (fp8 and w.layout == "nn")
+                  and LA.gemm_splitk_split(M, N, K, up is not None)[0] > 1)
         ws = None
         if small:
-            fp8 = w.value.dtype == dt.float8_e4m3fn
             ws = Slot(plan.add_buffer(LA.gemv_workspace_bytes(M, N, K, w.layout, fp8, up is not None), "temp",
                                       "gemv.partials"))
+        elif splitk:
+            ws = Slot(plan.add_buffer(LA.gemm_splitk_workspace_bytes(M, N, K, up is not None), "temp",
+                                      "gemm.partials"))
 
         def make(addr):
             up_ptr = 0
@@ -189,6 +197,14 @@ class GemmMatch(Match):
                                resid_ptr=addr(resid) if resid is not None else 0,
                                up_ptr=up_ptr, up_scale_ptr=up_scale,
                                round_before_bias=rnd_bias, round_before_resid=rnd_resid)
+            if splitk:
+                return LA.gemm_splitk(addr(x), addr(w.value), addr(out), M, N, K, layout=w.layout,
+                                      b_dtype=w.value.dtype, c_dtype=out.dtype, ldb=ldb, ws_ptr=addr(ws),
+                                      bias_ptr=addr(bias) if bias is not None else 0,
+                                      scale_ptr=addr(w.scale) if w.scale is not None else 0,
+                                      resid_ptr=addr(resid) if resid is not None else 0,
+                                      up_ptr=up_ptr, up_scale_ptr=up_scale,
+                                      round_before_bias=rnd_bias, round_before_resid=rnd_resid)
             return LA.gemm(addr(x), addr(w.value), addr(out), M, N, K, layout=w.layout,
                            b_dtype=w.value.dtype, c_dtype=out.dtype, ldb=ldb,
                            bias_ptr=addr(bias) if bias is not None else 0,
@@ -252,12 +268,19 @@ def _fold_epilogue(L, v: Value, nodes: List[Node]):
 
 
 class GemmPattern:
+    """``split_k=False`` keeps every projection of more than a few rows on
+    one K loop per tile (the summation order of the fused rotary GEMM)."""
+
+    def __init__(self, split_k: bool = True):
+        self.split_k = split_k
+
     def find(self, L):
         for n in L.live:
             if id(n) in L.covered or not _plain_dot(n):
                 continue
             m = self._match(L, n)
             if m is not None and m.validate(L):
+                m.split_k = self.split_k
                 yield m
 
     def _match(self, L, n: Node):

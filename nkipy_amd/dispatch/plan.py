@@ -255,15 +255,15 @@ class PlanExecutor:
         from nkipy_amd.runtime.hip import check_current
 
         check_current(self.rt, "plan")
-        plan = self.plan
-        bases: Dict[int, int] = {i: b.ptr for i, b in self._owned.items()}
-        for name, idx in plan.input_buffers.items():
-            bases[idx] = io_ptrs[name]
-        for name, idx in plan.output_buffers.items():
-            bases[idx] = io_ptrs[name]
-        key = tuple(sorted((k, v) for k, v in io_ptrs.items()))
+        key = tuple(sorted(io_ptrs.items()))
         bp = self._bound.get(key)
         if bp is None:
+            plan = self.plan
+            bases: Dict[int, int] = {i: b.ptr for i, b in self._owned.items()}
+            for name, idx in plan.input_buffers.items():
+                bases[idx] = io_ptrs[name]
+            for name, idx in plan.output_buffers.items():
+                bases[idx] = io_ptrs[name]
             if len(self._bound) > 64:
                 self._bound.clear()
             bp = self._bind(bases)

@@ -149,6 +149,8 @@ class DeviceKernel:
         self._in_specs = {n: (sh, dt.canonical(d)) for n, sh, d in ins}
         self._out_specs = {n: (sh, dt.canonical(d)) for n, sh, d in outs}
         self._staging: Dict[str, DeviceTensor] = {}
+        # I/O sets already validated -> outputs that need staging
+        self._io_checked: Dict[tuple, tuple] = {}
 
     # ------------------------------------------------------------------
     @classmethod
@@ -290,8 +292,17 @@ class DeviceKernel:
             for out_name, in_name in self.plan.alias_outputs.items():
                 if in_name in inputs:
                     outputs[out_name] = inputs[in_name]
-        self._validate_io(inputs, outputs)
-        staged = self._overlapping_outputs(inputs, outputs)
+        # a serving loop calls with the same tensors every step: the checks
+        # of names, shapes, dtypes, aliasing and overlap run once per set
+        key = (tuple((k, t.ptr, t.shape, t.dtype) for k, t in inputs.items()),
+               tuple((k, t.ptr, t.shape, t.dtype) for k, t in outputs.items()))
+        staged = self._io_checked.get(key)
+        if staged is None:
+            self._validate_io(inputs, outputs)
+            staged = tuple(self._overlapping_outputs(inputs, outputs))
+            if len(self._io_checked) > 64:
+                self._io_checked.clear()
+            self._io_checked[key] = staged
         if staged:
             run_outputs = dict(outputs)
             for on in staged:

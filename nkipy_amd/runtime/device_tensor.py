@@ -15,6 +15,7 @@ NumPy side uses the stand-in dtypes of :mod:`nkipy_amd.core.dtypes`.
 from __future__ import annotations
 
 import ctypes
+import math
 from typing import Tuple
 
 import numpy as np
@@ -96,6 +97,7 @@ class DeviceTensor:
         self.shape = shape
         self.dtype = dt.canonical(dtype)
         self.name = name
+        self._size = math.prod(shape) if shape else 1
 
     # -- properties ------------------------------------------------------
     @property
@@ -105,7 +107,7 @@ class DeviceTensor:
 
     @property
     def size(self) -> int:
-        return int(np.prod(self.shape)) if self.shape else 1
+        return self._size
 
     @property
     def nbytes(self) -> int:

@@ -153,3 +153,118 @@ def test_decode_projection_lowers_to_gemv(gpu):
     assert [l.symbol for l in step.launches(lambda v: 1 << 40)] == ["nk_gemv_nn_bf16_m1", "nk_gemv_out_bf16"]
     got = dt.to_float32(baremetal_jit(proj)(*args))
     _close(got, x.astype(np.float64) @ w.astype(np.float64), axis=-1)
+
+
+# ---------------------------------------------------------------------------
+# The MFMA GEMM over K ranges (8 < M <= 256: a decode batch)
+# ---------------------------------------------------------------------------
+SPLITK = [  # (layout, fp8, M, N, K): K ranges of 64-multiples, the last with a tail
+    ("nn", False, 32, 6144, 4096), ("nn", False, 200, 264, 520), ("nn", False, 9, 1024, 1000),
+    ("nt", False, 16, 1000, 1000), ("nt", False, 64, 4096, 4096), ("nt", True, 64, 4104, 1008),
+    ("nt", True, 33, 512, 14336), ("nt", True, 256, 4096, 4096),
+]
+
+
+@pytest.mark.parametrize("layout,fp8,M,Nn,Kk", SPLITK)
+@pytest.mark.parametrize("epi", ["plain", "f32", "bias_resid", "rounded"])
+def test_gemm_splitk_matches_float64(gpu, layout, fp8, M, Nn, Kk, epi):
+    print(f"gemm splitk {layout} fp8={fp8} M={M} N={Nn} K={Kk} {epi} split={LA.gemm_splitk_split(M, Nn, Kk)}",
+          flush=True)
+    rng = np.random.default_rng(M * 3 + Nn + Kk)
+    x = N.bf16_round(rng.standard_normal((M, Kk)))
+    wdev, scale, wmat = _weights(rng, layout, Nn, Kk, fp8)
+    prod = x.astype(np.float64) @ wmat
+    bias = N.bf16_round(rng.standard_normal(Nn) * 0.1)
+    res = N.bf16_round(rng.standard_normal((M, Nn)))
+    out = dt.float32 if epi == "f32" else dt.bfloat16
+    kw, ref = {}, prod
+    t = {"x": DeviceTensor.from_numpy(dt.to_bf16(x)), "w": DeviceTensor.from_numpy(wdev)}
+    if scale is not None:
+        t["s"] = DeviceTensor.from_numpy(scale)
+        kw["scale_ptr"] = t["s"].ptr
+    if epi in ("bias_resid", "rounded"):
+        t["b"] = DeviceTensor.from_numpy(dt.to_bf16(bias))
+        t["r"] = DeviceTensor.from_numpy(dt.to_bf16(res))
+        kw.update(bias_ptr=t["b"].ptr, resid_ptr=t["r"].ptr)
+        if epi == "rounded":
+            kw.update(round_before_bias=True, round_before_resid=True)
+            ref = N.bf16_round(N.bf16_round(prod) + bias) + res
+        else:
+            ref = prod + bias + res
+    c = DeviceTensor.empty((M, Nn), out)
+    ws = DeviceTensor.empty((LA.gemm_splitk_workspace_bytes(M, Nn, Kk),), dt.uint8)
+    _run(gpu, LA.gemm_splitk(t["x"].ptr, t["w"].ptr, c.ptr, M, Nn, Kk, layout=layout,
+                             b_dtype=dt.float8_e4m3fn if fp8 else dt.bfloat16, c_dtype=out, ws_ptr=ws.ptr, **kw))
+    got = c.numpy() if out == dt.float32 else dt.to_float32(c.numpy())
+    if out == dt.float32:
+        np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
+    else:
+        _close(got, ref, axis=-1, rounded=N.bf16_round(prod) if epi == "rounded" else None)
+
+
+@pytest.mark.parametrize("layout,fp8,M,Nn,Kk", [("nn", False, 48, 2048, 4096), ("nt", True, 24, 1024, 2048),
+                                                ("nt", False, 130, 300, 712)])
+def test_gemm_splitk_swiglu(gpu, layout, fp8, M, Nn, Kk):
+    rng = np.random.default_rng(Nn + Kk + M)
+    x = N.bf16_round(rng.standard_normal((M, Kk)))
+    wg, sg, mg = _weights(rng, layout, Nn, Kk, fp8)
+    wu, su, mu = _weights(rng, layout, Nn, Kk, fp8)
+    ref = K.silu(x.astype(np.float64) @ mg) * (x.astype(np.float64) @ mu)
+    t = [DeviceTensor.from_numpy(v) for v in (dt.to_bf16(x), wg, wu)]
+    kw = {}
+    if fp8:
+        s = [DeviceTensor.from_numpy(v) for v in (sg, su)]
+        kw = {"scale_ptr": s[0].ptr, "up_scale_ptr": s[1].ptr}
+    h = DeviceTensor.empty((M, Nn), dt.bfloat16)
+    ws = DeviceTensor.empty((LA.gemm_splitk_workspace_bytes(M, Nn, Kk, swiglu=True),), dt.uint8)
+    launches = LA.gemm_splitk(t[0].ptr, t[1].ptr, h.ptr, M, Nn, Kk, layout=layout,
+                              b_dtype=dt.float8_e4m3fn if fp8 else dt.bfloat16, c_dtype=dt.bfloat16,
+                              ws_ptr=ws.ptr, up_ptr=t[2].ptr, **kw)
+    assert len(launches) == 3
+    _run(gpu, launches)
+    _close(dt.to_float32(h.numpy()), ref, axis=-1)
+
+
+@pytest.mark.parametrize("layout,fp8", [("nn", False), ("nt", False), ("nt", True)])
+def test_gemm_splitk_against_unsplit(gpu, layout, fp8):
+    """Same operands through the K ranges and through one K loop: fp32
+    results within the difference of the two summation orders."""
+    M, Nn, Kk = 40, 3072, 4096
+    rng = np.random.default_rng(9)
+    x = N.bf16_round(rng.standard_normal((M, Kk)))
+    wdev, scale, _ = _weights(rng, layout, Nn, Kk, fp8)
+    t = [DeviceTensor.from_numpy(v) for v in (dt.to_bf16(x), wdev)]
+    kw = {}
+    if fp8:
+        sd = DeviceTensor.from_numpy(scale)
+        kw["scale_ptr"] = sd.ptr
+    bt = dt.float8_e4m3fn if fp8 else dt.bfloat16
+    c1, c2 = DeviceTensor.empty((M, Nn), dt.float32), DeviceTensor.empty((M, Nn), dt.float32)
+    ws = DeviceTensor.empty((LA.gemm_splitk_workspace_bytes(M, Nn, Kk),), dt.uint8)
+    assert LA.gemm_splitk_split(M, Nn, Kk)[0] > 1
+    _run(gpu, LA.gemm_splitk(t[0].ptr, t[1].ptr, c1.ptr, M, Nn, Kk, layout=layout, b_dtype=bt,
+                             c_dtype=dt.float32, ws_ptr=ws.ptr, **kw))
+    _run(gpu, [LA.gemm(t[0].ptr, t[1].ptr, c2.ptr, M, Nn, Kk, layout=layout, b_dtype=bt, c_dtype=dt.float32,
+                       **kw)])
+    a, b = c1.numpy(), c2.numpy()
+    np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-5 * np.abs(b).max())
+
+
+def test_decode_batch_projection_lowers_to_splitk(gpu):
+    """A traced 32-token projection (x (32, 1, 4096) @ W (4096, 6144), bf16)
+    lowers to the MFMA kernel over K ranges and matches float64."""
+    from nkipy_amd.runtime import DeviceKernel, baremetal_jit
+
+    def proj(x, w):
+        return np.matmul(x, w)
+
+    rng = np.random.default_rng(4)
+    x = N.bf16_round(rng.standard_normal((32, 1, 4096)))
+    w = N.bf16_round(rng.standard_normal((4096, 6144)) * 0.02)
+    args = [dt.to_bf16(a) for a in (x, w)]
+    dk = DeviceKernel.compile_and_load(proj, *args)
+    (step,) = dk.plan.steps
+    assert [l.symbol for l in step.launches(lambda v: 1 << 40)] == ["nk_gemm8k_nn_bf16_f32_splitk",
+                                                                    "nk_gemv_out_bf16"]
+    got = dt.to_float32(baremetal_jit(proj)(*args))
+    _close(got, x.astype(np.float64) @ w.astype(np.float64), axis=-1)

@@ -17,6 +17,7 @@ from nkipy_amd.core.trace import NKIPyKernel
 from nkipy_amd.dispatch.lower import lower
 from nkipy_amd.dispatch.patterns import default_patterns
 from nkipy_amd.dispatch.patterns_attention import QkvRopeFusion
+from nkipy_amd.dispatch.patterns_gemm import GemmPattern
 from nkipy_amd.kernels.decoder import qkv_rope_fp8, rope_kernel, rope_tables
 from nkipy_amd.runtime import DeviceKernel, DeviceTensor
 from oracle import kernels as K
@@ -46,7 +47,9 @@ def _run(graph, plan, inputs, name):
 def _both(fn, inputs):
     graph = NKIPyKernel.trace(fn).specialize(*inputs.values())
     fused = lower(graph)
-    plain = lower(graph, [p for p in default_patterns() if not isinstance(p, QkvRopeFusion)])
+    # the plain projection on one K loop per tile, as the fused kernel sums
+    plain = lower(graph, [GemmPattern(split_k=False) if isinstance(p, GemmPattern) else p
+                          for p in default_patterns() if not isinstance(p, QkvRopeFusion)])
     assert "gemm_rope" in fused.kernel_kinds and "rope" not in fused.kernel_kinds
     assert plain.kernel_kinds.count("rope") == 2
     return _run(graph, fused, inputs, "fused"), _run(graph, plain, inputs, "plain")
