@@ -8,7 +8,7 @@
 //   nk_gemv_{nn,nt}_{bf16,e4m3}[_swiglu]   partial sums over one K range
 //       into an fp32 workspace P[split][m][n] (a second array for the up
 //       weights of the SwiGLU form);
-//   nk_gemv_out_{bf16,f32}[_swiglu]        the splits added in split order,
+//   nk_gemv_out_{bf16,f32}[_swiglu]        the splits added in a fixed order,
 //       then the epilogue (per-column scale, bias, bf16 roundings, residual;
 //       or silu(g) u) as the GEMM's, and the store.
 // fp32 accumulation throughout; fp8 codes are decoded exactly (e4m3 fits in
@@ -281,30 +281,43 @@ NK_GEMV(nn, e4m3, true)
 NK_GEMV(nt, bf16, false)
 NK_GEMV(nt, e4m3, true)
 
-// The splits added in split order, then the GEMM's epilogue: thread -> one
-// output (m, n)
+// The splits added, then the GEMM's epilogue.  A workgroup serves 64
+// consecutive outputs (flattened m * N + n); wave j adds splits j, j + 4,
+// j + 8, ... in order, each of its loads covering the 64 outputs (256
+// contiguous bytes) and all of them issued before the first add (16 at a
+// time); wave 0 then combines the four wave sums as (s0 + s1) + (s2 + s3).
+// A fixed order, one or two memory round trips for up to 64 splits.
 template <typename TC, bool SWIGLU>
 __device__ __forceinline__ void gemv_out_body(const GemvArgs &a) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= a.M * a.N) return;
-  const int64_t m = i / a.N, n = i % a.N;
+  __shared__ float red[2][4][64];
+  const int lane = threadIdx.x & 63, j = threadIdx.x >> 6;
   const int64_t plane = a.M * a.N;
+  const int64_t o = (int64_t)blockIdx.x * 64 + lane;
+  const bool live = o < plane;
+  const int64_t i = live ? o : 0;  // dead lanes read output 0, store nothing
   float g = 0.f, u = 0.f;
-  for (int s0 = 0; s0 < a.ksplit; s0 += 8) {  // loads of a batch first
-    float x[8], y[8];
+  for (int s0 = j; s0 < a.ksplit; s0 += 64) {
+    float x[16], y[16];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int s = min(s0 + j, a.ksplit - 1);
-      x[j] = a.ws[s * plane + i];
-      y[j] = SWIGLU ? a.ws[(a.ksplit + s) * plane + i] : 0.f;
+    for (int q = 0; q < 16; ++q) {
+      const int s = min(s0 + 4 * q, a.ksplit - 1);
+      x[q] = a.ws[s * plane + i];
+      y[q] = SWIGLU ? a.ws[(a.ksplit + s) * plane + i] : 0.f;
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (s0 + j < a.ksplit) {
-        g += x[j];
-        if constexpr (SWIGLU) u += y[j];
+    for (int q = 0; q < 16; ++q)
+      if (s0 + 4 * q < a.ksplit) {
+        g += x[q];
+        if constexpr (SWIGLU) u += y[q];
       }
   }
+  red[0][j][lane] = g;
+  if constexpr (SWIGLU) red[1][j][lane] = u;
+  __syncthreads();
+  if (j != 0 || !live) return;
+  g = (red[0][0][lane] + red[0][1][lane]) + (red[0][2][lane] + red[0][3][lane]);
+  if constexpr (SWIGLU) u = (red[1][0][lane] + red[1][1][lane]) + (red[1][2][lane] + red[1][3][lane]);
+  const int64_t m = i / a.N, n = i % a.N;
   float v;
   if constexpr (SWIGLU) {
     if (a.flags & GEMM_SCALE) {

@@ -405,18 +405,34 @@ def gemm(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
 SPLITK_TARGET_WGS = 256  # one 8-wave GEMM workgroup per CU
 
 
-def gemm_splitk_split(M: int, N: int, K: int, swiglu: bool = False):
+def gemm_splitk_split(M: int, N: int, K: int, swiglu: bool = False, fp8: bool = False):
     """(ksplit, kc) for :func:`gemm_splitk`: K ranges of kc (a multiple of
-    64) so that tiles x ranges is about one workgroup per CU; ksplit 1 when
-    the tiles alone fill the part."""
+    64) so that tiles x ranges is about one workgroup per CU.  Past 64 rows
+    each range's fp32 partial plane (4 M N bytes, written once and read once)
+    costs as much as its share of the K loop saves, so the planes are held
+    to half the weight bytes (measured at 4096 x 4096: 256 rows in 16 ranges
+    66 us against 80 us in one loop, 128 rows in 8 ranges 42 us); ksplit 1
+    when the tiles alone fill the part."""
     tiles = -(-M // GEMM_BM) * -(-N // GEMM_BN)
     ks = max(1, min(SPLITK_TARGET_WGS // tiles, -(-K // 64)))
+    if M > 64:
+        ks = max(1, min(ks, (N * K * (1 if fp8 else 2)) // (2 * 4 * M * N)))
     kc = -(-(-(-K // ks)) // 64) * 64
     return -(-K // kc), kc
 
 
-def gemm_splitk_workspace_bytes(M: int, N: int, K: int, swiglu: bool = False) -> int:
-    ks, _ = gemm_splitk_split(M, N, K, swiglu)
+def gemm_splitk_useful(M: int, N: int, K: int, swiglu: bool = False, fp8: bool = False) -> bool:
+    """Whether the K-range form beats one K loop per tile: up to 64 rows
+    whenever it splits; up to 256 rows only when the tiles leave most CUs
+    idle (at most 32 tiles) -- 512 or more rows, or 256 rows of a 14336-wide
+    projection, measured slower split."""
+    if M > GEMM_BM or (M > 64 and -(-N // GEMM_BN) > 32):
+        return False
+    return gemm_splitk_split(M, N, K, swiglu, fp8)[0] > 1
+
+
+def gemm_splitk_workspace_bytes(M: int, N: int, K: int, swiglu: bool = False, fp8: bool = False) -> int:
+    ks, _ = gemm_splitk_split(M, N, K, swiglu, fp8)
     return 4 * ks * M * N * (2 if swiglu else 1)
 
 
@@ -454,7 +470,7 @@ def gemm_splitk(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, l
         raise LaunchError("the SwiGLU epilogue writes bf16 without bias / residual")
     if fp8 and not scale_ptr:
         raise LaunchError("fp8 weights need per-column scales")
-    ks, kc = gemm_splitk_split(M, N, K, swiglu)
+    ks, kc = gemm_splitk_split(M, N, K, swiglu, fp8)
     plane = M * N
     launches = []
     for i, bp in enumerate([b_ptr] + ([up_ptr] if swiglu else [])):
@@ -478,7 +494,7 @@ def gemm_splitk(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, l
                    up_scale_ptr or None, resid_ptr or None, ws_ptr, M, N, K, lda, ldb, ldc, ks, kc, flags, 0)
     ctag = "bf16" if c_dtype == dt.bfloat16 else "f32"
     sw = "_swiglu" if swiglu else ""
-    launches.append(Launch("gemv", f"nk_gemv_out_{ctag}{sw}", (-(-plane // 256), 1, 1), (256, 1, 1), out,
+    launches.append(Launch("gemv", f"nk_gemv_out_{ctag}{sw}", (-(-plane // 64), 1, 1), (256, 1, 1), out,
                            bytes=4 * ks * plane * len(launches) + plane * c_dtype.itemsize))
     return launches
 
@@ -498,6 +514,15 @@ class GemvArgs(ctypes.Structure):
 
 
 GEMV_MAX_M = 8  # rows the split-K projection kernels take
+
+
+def gemv_preferred(M: int, layout: str, fp8: bool) -> bool:
+    """Whether :func:`gemv` beats the MFMA GEMM over K ranges for M rows
+    (measured on 4096 x 4096 / 6144 projections: one row for bf16 weights,
+    up to four for fp8 NT, any row count the split-K GEMM lacks)."""
+    if M == 1 or (fp8 and layout == "nn"):
+        return M <= GEMV_MAX_M
+    return fp8 and M <= 4
 GEMV_MAX_KC = 1024
 GEMV_NT_ROWS = 16  # weight rows (output columns) per NT workgroup
 _GEMV_TARGET_WGS = 1024
@@ -583,7 +608,7 @@ def gemv(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
     return [Launch("gemv", f"nk_gemv_{layout}_{btag}{sw}_m{mt}", (blocks * ks, 1, 1), (256, 1, 1), args,
                    bytes=M * K * 2 + n_mm * N * K * b_dtype.itemsize + 4 * ks * M * N * n_mm,
                    flops=2 * M * N * K * n_mm),
-            Launch("gemv", f"nk_gemv_out_{ctag}{sw}", (-(-M * N // 256), 1, 1), (256, 1, 1), args,
+            Launch("gemv", f"nk_gemv_out_{ctag}{sw}", (-(-M * N // 64), 1, 1), (256, 1, 1), args,
                    bytes=4 * ks * M * N * n_mm + M * N * c_dtype.itemsize)]
 
 

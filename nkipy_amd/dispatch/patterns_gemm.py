@@ -172,15 +172,16 @@ class GemmMatch(Match):
         # (a decode batch): the MFMA kernels over K ranges, so that the
         # grid fills the part
         fp8 = w.value.dtype == dt.float8_e4m3fn
-        small = M <= LA.GEMV_MAX_M
-        splitk = (self.split_k and not small and M <= LA.GEMM_BM and not (fp8 and w.layout == "nn")
-                  and LA.gemm_splitk_split(M, N, K, up is not None)[0] > 1)
+        small = LA.gemv_preferred(M, w.layout, fp8)
+        splitk = (self.split_k and not small and not (fp8 and w.layout == "nn")
+                  and LA.gemm_splitk_useful(M, N, K, up is not None, fp8))
+        small = small or (M <= LA.GEMV_MAX_M and not splitk)
         ws = None
         if small:
             ws = Slot(plan.add_buffer(LA.gemv_workspace_bytes(M, N, K, w.layout, fp8, up is not None), "temp",
                                       "gemv.partials"))
         elif splitk:
-            ws = Slot(plan.add_buffer(LA.gemm_splitk_workspace_bytes(M, N, K, up is not None), "temp",
+            ws = Slot(plan.add_buffer(LA.gemm_splitk_workspace_bytes(M, N, K, up is not None, fp8), "temp",
                                       "gemm.partials"))
 
         def make(addr):

@@ -168,8 +168,8 @@ SPLITK = [  # (layout, fp8, M, N, K): K ranges of 64-multiples, the last with a 
 @pytest.mark.parametrize("layout,fp8,M,Nn,Kk", SPLITK)
 @pytest.mark.parametrize("epi", ["plain", "f32", "bias_resid", "rounded"])
 def test_gemm_splitk_matches_float64(gpu, layout, fp8, M, Nn, Kk, epi):
-    print(f"gemm splitk {layout} fp8={fp8} M={M} N={Nn} K={Kk} {epi} split={LA.gemm_splitk_split(M, Nn, Kk)}",
-          flush=True)
+    split = LA.gemm_splitk_split(M, Nn, Kk, fp8=fp8)
+    print(f"gemm splitk {layout} fp8={fp8} M={M} N={Nn} K={Kk} {epi} split={split}", flush=True)
     rng = np.random.default_rng(M * 3 + Nn + Kk)
     x = N.bf16_round(rng.standard_normal((M, Kk)))
     wdev, scale, wmat = _weights(rng, layout, Nn, Kk, fp8)
@@ -192,7 +192,7 @@ def test_gemm_splitk_matches_float64(gpu, layout, fp8, M, Nn, Kk, epi):
         else:
             ref = prod + bias + res
     c = DeviceTensor.empty((M, Nn), out)
-    ws = DeviceTensor.empty((LA.gemm_splitk_workspace_bytes(M, Nn, Kk),), dt.uint8)
+    ws = DeviceTensor.empty((LA.gemm_splitk_workspace_bytes(M, Nn, Kk, fp8=fp8),), dt.uint8)
     _run(gpu, LA.gemm_splitk(t["x"].ptr, t["w"].ptr, c.ptr, M, Nn, Kk, layout=layout,
                              b_dtype=dt.float8_e4m3fn if fp8 else dt.bfloat16, c_dtype=out, ws_ptr=ws.ptr, **kw))
     got = c.numpy() if out == dt.float32 else dt.to_float32(c.numpy())
@@ -216,7 +216,7 @@ def test_gemm_splitk_swiglu(gpu, layout, fp8, M, Nn, Kk):
         s = [DeviceTensor.from_numpy(v) for v in (sg, su)]
         kw = {"scale_ptr": s[0].ptr, "up_scale_ptr": s[1].ptr}
     h = DeviceTensor.empty((M, Nn), dt.bfloat16)
-    ws = DeviceTensor.empty((LA.gemm_splitk_workspace_bytes(M, Nn, Kk, swiglu=True),), dt.uint8)
+    ws = DeviceTensor.empty((LA.gemm_splitk_workspace_bytes(M, Nn, Kk, swiglu=True, fp8=fp8),), dt.uint8)
     launches = LA.gemm_splitk(t[0].ptr, t[1].ptr, h.ptr, M, Nn, Kk, layout=layout,
                               b_dtype=dt.float8_e4m3fn if fp8 else dt.bfloat16, c_dtype=dt.bfloat16,
                               ws_ptr=ws.ptr, up_ptr=t[2].ptr, **kw)
@@ -240,8 +240,8 @@ def test_gemm_splitk_against_unsplit(gpu, layout, fp8):
         kw["scale_ptr"] = sd.ptr
     bt = dt.float8_e4m3fn if fp8 else dt.bfloat16
     c1, c2 = DeviceTensor.empty((M, Nn), dt.float32), DeviceTensor.empty((M, Nn), dt.float32)
-    ws = DeviceTensor.empty((LA.gemm_splitk_workspace_bytes(M, Nn, Kk),), dt.uint8)
-    assert LA.gemm_splitk_split(M, Nn, Kk)[0] > 1
+    ws = DeviceTensor.empty((LA.gemm_splitk_workspace_bytes(M, Nn, Kk, fp8=fp8),), dt.uint8)
+    assert LA.gemm_splitk_split(M, Nn, Kk, fp8=fp8)[0] > 1
     _run(gpu, LA.gemm_splitk(t[0].ptr, t[1].ptr, c1.ptr, M, Nn, Kk, layout=layout, b_dtype=bt,
                              c_dtype=dt.float32, ws_ptr=ws.ptr, **kw))
     _run(gpu, [LA.gemm(t[0].ptr, t[1].ptr, c2.ptr, M, Nn, Kk, layout=layout, b_dtype=bt, c_dtype=dt.float32,
