@@ -1,6 +1,6 @@
 """Benchmark of the hot path on one MI355X.
 
-One JSON line on stdout.  Five workloads run through the product path
+One JSON line on stdout.  Seven workloads run through the product path
 (traced NumPy kernel -> plan -> gfx950 kernels through the C-ABI runtime),
 each with its own roofline, CPU baseline and parity record:
 
@@ -16,6 +16,10 @@ each with its own roofline, CPU baseline and parity record:
      cache of 4096 rows (8 KV heads), scores rounded to bf16, mask rows
      [:2048, :4096], bf16 softmax (an extra line beside the five
      configurations)
+  7  Qwen3 attention layer decode step: one token for each of 8 sequences
+     (hidden 4096, 32 / 8 heads) against 4096-row bf16 caches at position
+     4000 -- projections, q / k norm and RoPE, cache writes, attention,
+     output projection (an extra line: the serving path)
 
 Timing: inputs are resident in HBM; bandwidth-bound steps rotate over
 buffer sets whose total exceeds the 256 MB Infinity Cache; every timed
@@ -36,7 +40,7 @@ run of this script can be split per workload and per launch position;
 ``python bench.py --summarize DIR`` prints those summaries (no GPU needed).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--configs 1,2,3,4,5,6] [--mark-sections] [--calibrate-copy]
+                       [--configs 1,2,3,4,5,6,7] [--mark-sections] [--calibrate-copy]
        python bench.py --summarize DIR [--traffic-json PATH]
 """
 
@@ -72,6 +76,8 @@ DEC_B, DEC_S, DEC_HQ, DEC_HKV, DEC_D, DEC_F = 8, 2048, 32, 8, 128, 14336
 DEC_HID = DEC_HQ * DEC_D
 DEC_M = DEC_B * DEC_S
 QP_B, QP_S, QP_MAXS, QP_HQ, QP_HKV = 1, 2048, 4096, 32, 8
+# Qwen3 attention layer, one decode token per sequence
+QD_B, QD_MAXS, QD_POS, QD_HID, QD_HQ, QD_HKV = 8, 4096, 4000, 4096, 32, 8
 
 
 def _linattn_prefix_bytes():
@@ -106,8 +112,44 @@ def sections():
         6: ("qwen3_prefill_attention", [("rowmax", "mfma", 2 * QP_B * QP_HQ * QP_S * QP_S * DEC_D // 2),
                                         ("rowsum", "mfma", 2 * QP_B * QP_HQ * QP_S * QP_S * DEC_D // 2),
                                         ("attention", "mfma", 4 * QP_B * QP_HQ * QP_S * QP_S * DEC_D // 2)]),
+        7: ("qwen3_decode_step", _decode_launches()),
         9: ("copy_calibration", [("copy16", "hbm", 2 * 2**30)]),
     }
+
+
+def _decode_launches():
+    """Bytes each launch of the Qwen3 decode step moves (its inputs and
+    outputs as this decomposition has them: partial sums of the K-range
+    projections, the fp32 scores and split outputs of the attention)."""
+    from nkipy_amd.dispatch.launchers import gemm_splitk_split
+
+    B, H, Hkv, D, hid = QD_B, QD_HQ, QD_HKV, DEC_D, QD_HID
+    L, nqkv = QD_POS + 1, (QD_HQ + 2 * QD_HKV) * DEC_D
+    nsp = -(-L // 128)
+    ks1, _ = gemm_splitk_split(B, nqkv, hid)
+    ks2, _ = gemm_splitk_split(B, hid, H * D)
+    kv = 2 * B * L * Hkv * D
+    return [("qkv_partials", "hbm", 2 * hid * nqkv + 2 * B * hid + 4 * ks1 * B * nqkv),
+            ("qkv_reduce", "hbm", 4 * ks1 * B * nqkv + 2 * B * nqkv),
+            ("v_split", "hbm", 2 * 2 * B * Hkv * D),
+            ("head_rope", "hbm", 2 * 2 * B * (H + Hkv) * D),
+            ("cache_k_write", "hbm", 2 * 2 * B * Hkv * D),
+            ("cache_v_write", "hbm", 2 * 2 * B * Hkv * D),
+            ("scores", "hbm", kv + 4 * B * H * L),
+            ("rowstat", "hbm", 4 * B * H * L),
+            ("values", "hbm", kv + 4 * B * H * L + 4 * B * H * nsp * D),
+            ("combine", "hbm", 4 * B * H * nsp * D + 2 * B * H * D),
+            ("o_partials", "hbm", 2 * H * D * hid + 2 * B * H * D + 4 * ks2 * B * hid),
+            ("o_reduce", "hbm", 4 * ks2 * B * hid + 2 * B * hid)]
+
+
+def _decode_step_bytes():
+    """Algorithmic HBM bytes of one decode step: both weights, the K / V
+    rows attended, the token's activations and its cache rows."""
+    B, H, Hkv, D, hid = QD_B, QD_HQ, QD_HKV, DEC_D, QD_HID
+    nqkv = (H + 2 * Hkv) * D
+    return (2 * hid * nqkv + 2 * H * D * hid + 2 * 2 * B * (QD_POS + 1) * Hkv * D
+            + 2 * 2 * B * hid + 2 * 2 * B * Hkv * D)
 
 
 MARK_BASE = 1000  # marker grid = MARK_BASE + workload id
@@ -617,6 +659,89 @@ def bench_qwen3_prefill(a, rt, mk):
     return entry, cpu
 
 
+def bench_qwen3_decode(a, rt, mk):
+    from nkipy_amd.core import dtypes as dt
+    from nkipy_amd.kernels.qwen3 import qwen3_attention_kernel
+    from nkipy_amd.runtime import DeviceKernel, DeviceTensor
+
+    B, MAXS, pos, hid, H, Hkv, D = QD_B, QD_MAXS, QD_POS, QD_HID, QD_HQ, QD_HKV, DEC_D
+    eps = 1e-6
+
+    def decode(x, qkv_weight, q_norm_weight, k_norm_weight, cache_k, cache_v, start_pos, o_weight):
+        return qwen3_attention_kernel(x, qkv_weight, q_norm_weight, k_norm_weight, eps, H, D, Hkv,
+                                      cache_k, cache_v, start_pos, o_weight)
+
+    rng = np.random.default_rng(42)
+    host = {"x": dt.round_to_bf16(rng.standard_normal((B, 1, hid), dtype=np.float32)),
+            "qkv_weight": dt.round_to_bf16(rng.standard_normal((hid, (H + 2 * Hkv) * D), dtype=np.float32)
+                                           * hid ** -0.5),
+            "q_norm_weight": dt.round_to_bf16(rng.uniform(0.5, 1.5, D).astype(np.float32)),
+            "k_norm_weight": dt.round_to_bf16(rng.uniform(0.5, 1.5, D).astype(np.float32)),
+            "cache_k": dt.round_to_bf16(rng.standard_normal((B, MAXS, Hkv, D), dtype=np.float32)),
+            "cache_v": dt.round_to_bf16(rng.standard_normal((B, MAXS, Hkv, D), dtype=np.float32)),
+            "o_weight": dt.round_to_bf16(rng.standard_normal((H * D, hid), dtype=np.float32) * (H * D) ** -0.5)}
+    order = ["x", "qkv_weight", "q_norm_weight", "k_norm_weight", "cache_k", "cache_v"]
+    args = [dt.to_bf16(host[n]) for n in order] + [np.array([pos], np.int32), dt.to_bf16(host["o_weight"])]
+    dk = DeviceKernel.compile_and_load(decode, *args, name="qwen3_decode_step")
+    names = [p.name for p in dk.graph.parameters]
+    # every set holds its own weights and caches (218 MB): a layer's weights
+    # are not cache-resident between its steps in a model of many layers
+    per_set = sum(v.nbytes for v in args)
+    sets = []
+    for _ in range(_sets_for(per_set)):
+        ins = {n: DeviceTensor.from_numpy(v, name=n) for n, v in zip(names, args)}
+        outs = {"output0": DeviceTensor.empty((B, 1, hid), dt.bfloat16, name="output0"),
+                "cache_k": ins["cache_k.must_alias_input"], "cache_v": ins["cache_v.must_alias_input"]}
+        sets.append((ins, outs))
+    bounds = [dk.executor.bind(dk._io_ptrs(i, o)) for i, o in sets]
+    if len(bounds[0].launches) != len(sections()[7][1]):
+        raise RuntimeError(f"Qwen3 decode step has an unexpected launch list: "
+                           f"{[l.symbol for l in bounds[0].launches]}")
+    steps, warm = max(20, a.steps // 2), max(5, a.warmup)
+    mk.mark(7)
+    ms = _time_steps(bounds, steps, warm, rt)
+    recs = _kernel_records(7, bounds[0].launches, _time_in_step(bounds, max(20, steps // 2), rt, mk))
+    # one synchronous call at a time (host dispatch, launches, wait): the
+    # latency a serving loop that waits for each token sees
+    ins0, outs0 = sets[0]
+    for _ in range(10):
+        dk(ins0, outs0)
+    t0 = time.perf_counter()
+    n_sync = 50
+    for _ in range(n_sync):
+        dk(ins0, outs0)
+    sync_us = (time.perf_counter() - t0) / n_sync * 1e6
+    work = _decode_step_bytes()
+    step_rec = {"label": "step", "kernel": " + ".join(l.symbol for l in bounds[0].launches), "bound": "hbm"}
+    roof = _roofline(7, step_rec, us=ms * 1e3, work=work)
+    roof["traffic"] = None
+    entry = {"config": 7, "workload": "qwen3_decode_step",
+             "shape": {"batch": B, "cache_rows": MAXS, "position": pos, "hidden": hid, "heads": H,
+                       "kv_heads": Hkv, "head_dim": D},
+             "dtype": "bf16 (the traced cast points of the Qwen3 attention layer)",
+             "us_per_step": round(ms * 1e3, 2), "synchronous_call_us": round(sync_us, 1),
+             "roofline": roof, "kernels": recs,
+             "note": "one token per sequence through the whole attention layer (QKV projection, q / k norm and "
+                     "RoPE, cache writes, attention over pos + 1 cached rows, output projection); steps queued "
+                     "back to back over rotating weight / cache sets; synchronous_call_us waits for each step"}
+
+    def cpu():
+        from oracle import kernels as K
+
+        f32 = {k: dt.to_float32(dt.to_bf16(v)) for k, v in host.items()}
+        run = lambda: K.qwen3_decode_layer(f32["x"], f32["qkv_weight"], f32["q_norm_weight"], f32["k_norm_weight"],
+                                           eps, H, Hkv, D, f32["cache_k"], f32["cache_v"], pos, f32["o_weight"])
+        t, ts, ref = _timed(run, 3)
+        got = dt.to_float32(outs0["output0"].numpy())
+        return ({"value": round(t * 1e6, 0), "unit": "us per decode step", "cores": _blas_threads(),
+                 "kind": "port",
+                 "sample": f"the whole step, all {B} sequences (NumPy float64 products, op-by-op bf16 cast "
+                           f"points), median of {len(ts)} runs; host has {_host_cores()} cores"},
+                _parity(got, ref[0]))
+
+    return entry, cpu
+
+
 def calibrate_copy(rt, mk, nbytes=1 << 30, reps=3):
     """Plain streaming copy of a known size: rocprof's FETCH_SIZE / WRITE_SIZE
     for nk_copy16 read against 1 GiB give the counter scale factors."""
@@ -774,7 +899,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--configs", default="1,2,3,4,5,6")
+    ap.add_argument("--configs", default="1,2,3,4,5,6,7")
     ap.add_argument("--mark-sections", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 1 GiB streaming copy (calibrates HBM traffic counters)")
@@ -802,7 +927,7 @@ def main():
         calibrate_copy(rt, mk)
 
     benches = {1: bench_softmax, 2: bench_rmsnorm, 3: bench_swiglu, 4: bench_linattn, 5: bench_decoder,
-               6: bench_qwen3_prefill}
+               6: bench_qwen3_prefill, 7: bench_qwen3_decode}
     entries, legs = {}, {}
     for cid in sorted(want):
         e, leg = benches[cid](a, rt, mk)
@@ -847,6 +972,7 @@ def main():
         "parity_ok": head["parity"]["ok"] if head["parity"] else None,
         "decoder_layer_fp8_us": entries[5]["value"] if 5 in entries else None,
         "qwen3_prefill_attention_us": entries[6]["us_per_step"] if 6 in entries else None,
+        "qwen3_decode_step_us": entries[7]["us_per_step"] if 7 in entries else None,
         "configs": [entries[c] for c in sorted(entries)],
     }
     print(json.dumps(line), flush=True)

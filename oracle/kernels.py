@@ -460,6 +460,31 @@ def decode_attention(q, cache_k, cache_v, pos, round_prod=False, round_score=Fal
     return out
 
 
+def qwen3_decode_layer(x, qkv_weight, q_norm_weight, k_norm_weight, eps, n_heads, n_kv_heads, head_dim,
+                       cache_k, cache_v, pos, o_weight, theta=1.0e6):
+    """One decode token per sequence through examples/models/qwen3/kernels/
+    attention.py:25-156 (tensor-parallel degree 1, start_pos = pos): the bf16
+    QKV projection, the head prologue (:func:`qwen3_head_prologue`), the
+    cache rows at pos overwritten with k and v, attention over the cache
+    with the traced cast points (:func:`decode_attention`; the mask row adds
+    -1e5 past pos, whose weights are exactly 0), the bf16 weighted values and
+    the bf16 output projection.  Returns (out (B, 1, hidden), cache_k,
+    cache_v) as bf16 values (the caches are copies)."""
+    x = np.asarray(x, np.float32)
+    B = x.shape[0]
+    H, Hkv, D = n_heads, n_kv_heads, head_dim
+    qkv = bf16_round((x.astype(np.float64) @ np.asarray(qkv_weight, np.float64)).astype(np.float32))
+    q, k = qwen3_head_prologue(qkv, q_norm_weight, k_norm_weight, eps, H, Hkv, D, np.array([pos]), theta)
+    v = qkv[..., (H + Hkv) * D:].reshape(B, 1, Hkv, D)
+    ck = np.array(cache_k, np.float32, copy=True)
+    cv = np.array(cache_v, np.float32, copy=True)
+    ck[:, pos] = k[:, 0]
+    cv[:, pos] = v[:, 0]
+    att = bf16_round(decode_attention(q[:, 0], ck, cv, pos, True, True, True))
+    out = att.reshape(B, 1, H * D).astype(np.float64) @ np.asarray(o_weight, np.float64)
+    return bf16_round(out.astype(np.float32)), ck, cv
+
+
 # ---------------------------------------------------------------------------
 # Qwen3 prefill attention over a KV cache -- examples/models/qwen3/kernels/
 # attention.py:107-140 with bf16 activations (start_pos None): keys / values

@@ -96,3 +96,47 @@ def test_qwen3_decode_fused_equals_generic(gpu):
     # the token's keys went to position 300
     assert np.abs(outs[0]["cache_k"][:, 300] - host["cache_k"][:, 300]).max() > 0
     np.testing.assert_array_equal(outs[0]["cache_k"][:, 301:], host["cache_k"][:, 301:])
+
+
+@pytest.mark.parametrize("B,MAXS,HID,H,HKV,pos", [(2, 512, 512, 8, 2, 300), (8, 4096, 4096, 32, 8, 4000),
+                                                  (32, 512, 1024, 8, 2, 77)])
+def test_qwen3_decode_layer_matches_oracle(gpu, B, MAXS, HID, H, HKV, pos):
+    """The traced bf16 Qwen3 attention layer for one decode token per
+    sequence (projections on the split-K kernels, the fused head prologue,
+    the cache writes, the split decode attention) against the oracle's
+    composition of the same steps: the output at the bf16 bar, the new
+    cache rows within a rounding step of the norm's sum order, every other
+    cache row untouched."""
+    from nkipy_amd.kernels.qwen3 import qwen3_attention_kernel
+
+    D = 128
+    print(f"qwen3 decode layer B={B} MAXS={MAXS} HID={HID} H={H}/{HKV} pos={pos}", flush=True)
+
+    def decode(x, qkv_weight, q_norm_weight, k_norm_weight, cache_k, cache_v, start_pos, o_weight):
+        return qwen3_attention_kernel(x, qkv_weight, q_norm_weight, k_norm_weight, 1e-6, H, D, HKV,
+                                      cache_k, cache_v, start_pos, o_weight)
+
+    rng = np.random.default_rng(B + pos)
+    host = {"x": N.bf16_round(rng.standard_normal((B, 1, HID))),
+            "qkv_weight": N.bf16_round(rng.standard_normal((HID, (H + 2 * HKV) * D)) * HID ** -0.5),
+            "q_norm_weight": N.bf16_round(rng.uniform(0.5, 1.5, D)),
+            "k_norm_weight": N.bf16_round(rng.uniform(0.5, 1.5, D)),
+            "cache_k": N.bf16_round(rng.standard_normal((B, MAXS, HKV, D))),
+            "cache_v": N.bf16_round(rng.standard_normal((B, MAXS, HKV, D))),
+            "o_weight": N.bf16_round(rng.standard_normal((H * D, HID)) * (H * D) ** -0.5)}
+    args = [dt.to_bf16(host[n]) for n in ("x", "qkv_weight", "q_norm_weight", "k_norm_weight", "cache_k",
+                                          "cache_v")] + [np.array([pos], np.int32), dt.to_bf16(host["o_weight"])]
+    dk = DeviceKernel.compile_and_load(decode, *args, name=f"qwen3_decode_b{B}")
+    assert "decode_attention" in dk.plan.kernel_kinds and "head_rope" in dk.plan.kernel_kinds
+    names = list(dk.input_tensors_info)
+    ins = {n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(names, args)}
+    res = {k: dt.to_float32(v.numpy()) for k, v in dk(ins).items()}
+    out, ck, cv = K.qwen3_decode_layer(host["x"], host["qkv_weight"], host["q_norm_weight"], host["k_norm_weight"],
+                                       1e-6, H, HKV, D, host["cache_k"], host["cache_v"], pos, host["o_weight"])
+    _close(res["output0"], out)
+    for name, ref in (("cache_k", ck), ("cache_v", cv)):
+        got = res[name]
+        rest = np.ones(MAXS, bool)
+        rest[pos] = False
+        np.testing.assert_array_equal(got[:, rest], ref[:, rest])
+        _close(got[:, pos], ref[:, pos])
