@@ -131,10 +131,8 @@ def _decode_launches():
     kv = 2 * B * L * Hkv * D
     return [("qkv_partials", "hbm", 2 * hid * nqkv + 2 * B * hid + 4 * ks1 * B * nqkv),
             ("qkv_reduce", "hbm", 4 * ks1 * B * nqkv + 2 * B * nqkv),
-            ("v_split", "hbm", 2 * 2 * B * Hkv * D),
-            ("head_rope", "hbm", 2 * 2 * B * (H + Hkv) * D),
-            ("cache_k_write", "hbm", 2 * 2 * B * Hkv * D),
-            ("cache_v_write", "hbm", 2 * 2 * B * Hkv * D),
+            # q, k, v heads in; q out, k / v into the caches' rows at pos
+            ("head_rope_cache_rows", "hbm", 2 * B * (H + 2 * Hkv) * D + 2 * B * (H + 2 * Hkv) * D),
             ("scores", "hbm", kv + 4 * B * H * L),
             ("rowstat", "hbm", 4 * B * H * L),
             ("values", "hbm", kv + 4 * B * H * L + 4 * B * H * nsp * D),

@@ -109,6 +109,11 @@ extern "C" __global__ __launch_bounds__(256) void nk_rope_bf16(RopeArgs a) {
 // bf16, indexed [row * t_row + s * t_ss + f]; row is the runtime position
 // pos[0] (negative counts from the end, then clamped into the table, as the
 // gather kernel treats an index) or 0.
+// A third target copies its rows unchanged (HR_COPY: the v heads).  A target
+// with o_sp != 0 writes its rows at the runtime position of the output's
+// position axis (the cache write cache[:, pos] = k of one decode token): the
+// scatter kernel's rule, negative counts from the end and a position outside
+// the o_rows positions drops the store.
 // ---------------------------------------------------------------------------
 struct HeadRopeTarget {
   const uint16_t *x;         // bf16 input rows, d contiguous
@@ -119,12 +124,13 @@ struct HeadRopeTarget {
   int64_t x_half;            // element offset of the second half in an input row
   int64_t rows;              // B * S * H
   int64_t blocks;            // workgroups serving this target
+  int64_t o_sp, o_rows;      // runtime output position: element stride, positions
   float eps;
   int32_t H, flags, pad;
 };
 
 struct HeadRopeArgs {
-  HeadRopeTarget t[2];
+  HeadRopeTarget t[3];
   const void *cos_t;
   const void *sin_t;
   const int32_t *pos;  // runtime table row, or null
@@ -134,7 +140,7 @@ struct HeadRopeArgs {
   int32_t S, D, tflags, pad;
 };
 
-enum { HR_NORM = 1, HR_MUL_RECIP = 2, HR_W = 4 };  // per target
+enum { HR_NORM = 1, HR_MUL_RECIP = 2, HR_W = 4, HR_COPY = 8 };  // per target
 enum { HR_TABLE_F32 = 1 };
 
 __device__ __forceinline__ float rbf(float v) { return bf16_to_f32(f32_to_bf16(v)); }
@@ -142,18 +148,20 @@ __device__ __forceinline__ float rbf(float v) { return bf16_to_f32(f32_to_bf16(v
 extern "C" __global__ __launch_bounds__(256) void nk_head_rope_bf16(HeadRopeArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 15;
-  const bool t1 = (int64_t)blockIdx.x >= a.t[0].blocks;
+  const int64_t bid = blockIdx.x, b0 = a.t[0].blocks, b01 = b0 + a.t[1].blocks;
+  const int tg = bid >= b01 ? 2 : (bid >= b0 ? 1 : 0);
   // uniform per workgroup: scalar selects, no indexing of the argument array
-  const uint16_t *x = t1 ? a.t[1].x : a.t[0].x;
-  uint16_t *out = t1 ? a.t[1].out : a.t[0].out;
-  const uint16_t *w = t1 ? a.t[1].w : a.t[0].w;
-  const int64_t x_sb = t1 ? a.t[1].x_sb : a.t[0].x_sb, x_ss = t1 ? a.t[1].x_ss : a.t[0].x_ss;
-  const int64_t x_sh = t1 ? a.t[1].x_sh : a.t[0].x_sh, x_half = t1 ? a.t[1].x_half : a.t[0].x_half;
-  const int64_t o_sb = t1 ? a.t[1].o_sb : a.t[0].o_sb, o_ss = t1 ? a.t[1].o_ss : a.t[0].o_ss;
-  const int64_t o_sh = t1 ? a.t[1].o_sh : a.t[0].o_sh, nrows = t1 ? a.t[1].rows : a.t[0].rows;
-  const float eps = t1 ? a.t[1].eps : a.t[0].eps;
-  const int H = t1 ? a.t[1].H : a.t[0].H, flags = t1 ? a.t[1].flags : a.t[0].flags;
-  const int64_t row = ((int64_t)blockIdx.x - (t1 ? a.t[0].blocks : 0)) * 16 + (tid >> 4);
+#define HR_SEL(f) (tg == 2 ? a.t[2].f : (tg == 1 ? a.t[1].f : a.t[0].f))
+  const uint16_t *x = HR_SEL(x);
+  uint16_t *out = HR_SEL(out);
+  const uint16_t *w = HR_SEL(w);
+  const int64_t x_sb = HR_SEL(x_sb), x_ss = HR_SEL(x_ss), x_sh = HR_SEL(x_sh), x_half = HR_SEL(x_half);
+  const int64_t o_sb = HR_SEL(o_sb), o_ss = HR_SEL(o_ss), o_sh = HR_SEL(o_sh), nrows = HR_SEL(rows);
+  const int64_t o_sp = HR_SEL(o_sp), o_rows = HR_SEL(o_rows);
+  const float eps = HR_SEL(eps);
+  const int H = HR_SEL(H), flags = HR_SEL(flags);
+#undef HR_SEL
+  const int64_t row = (bid - (tg == 2 ? b01 : (tg == 1 ? b0 : 0))) * 16 + (tid >> 4);
 
   const int D = a.D, half = D >> 1, hl = D >> 4;  // hl: lanes per half row
   const bool second = lane >= hl;
@@ -224,7 +232,10 @@ extern "C" __global__ __launch_bounds__(256) void nk_head_rope_bf16(HeadRopeArgs
   // partner lane: the other half of the same frequencies
   const int src = ((tid & 63) & ~15) + (second ? lane - hl : lane + hl);
   float y[8];
-  {
+  if (flags & HR_COPY) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) y[j] = v[j];
+  } else {
 #pragma clang fp contract(off)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -235,8 +246,13 @@ extern "C" __global__ __launch_bounds__(256) void nk_head_rope_bf16(HeadRopeArgs
       y[j] = rbf(second ? oth + own : own - oth);
     }
   }
-  if (live) {
-    const int64_t oo = b * o_sb + s * o_ss + h * o_sh + col;
-    *reinterpret_cast<uint4 *>(out + oo) = pack8(y);
+  int64_t oo = b * o_sb + s * o_ss + h * o_sh + col;
+  bool store = live;
+  if (o_sp != 0) {
+    int64_t j = a.pos[0];
+    if (j < 0) j += o_rows;
+    store = store && j >= 0 && j < o_rows;
+    oo += (store ? j : 0) * o_sp;
   }
+  if (store) *reinterpret_cast<uint4 *>(out + oo) = pack8(y);
 }

@@ -616,17 +616,18 @@ class HeadRopeTarget(ctypes.Structure):
     _fields_ = [("x", ctypes.c_void_p), ("out", ctypes.c_void_p), ("w", ctypes.c_void_p)] + \
         [(f"{t}_{s}", ctypes.c_int64) for t in "xo" for s in ("sb", "ss", "sh")] + \
         [("x_half", ctypes.c_int64), ("rows", ctypes.c_int64), ("blocks", ctypes.c_int64),
+         ("o_sp", ctypes.c_int64), ("o_rows", ctypes.c_int64),
          ("eps", ctypes.c_float), ("H", ctypes.c_int32), ("flags", ctypes.c_int32), ("pad", ctypes.c_int32)]
 
 
 class HeadRopeArgs(ctypes.Structure):
-    _fields_ = [("t", HeadRopeTarget * 2), ("cos_t", ctypes.c_void_p), ("sin_t", ctypes.c_void_p),
+    _fields_ = [("t", HeadRopeTarget * 3), ("cos_t", ctypes.c_void_p), ("sin_t", ctypes.c_void_p),
                 ("pos", ctypes.c_void_p), ("t_row", ctypes.c_int64), ("t_ss", ctypes.c_int64),
                 ("t_rows", ctypes.c_int64), ("S", ctypes.c_int32), ("D", ctypes.c_int32),
                 ("tflags", ctypes.c_int32), ("pad", ctypes.c_int32)]
 
 
-HR_NORM, HR_MUL_RECIP, HR_W = 1, 2, 4
+HR_NORM, HR_MUL_RECIP, HR_W, HR_COPY = 1, 2, 4, 8
 HR_TABLE_F32 = 1
 
 
@@ -636,7 +637,11 @@ class HeadRopeSpec:
     ``x_ptr`` through element strides (b, s, h), the second half of a row
     ``x_half`` elements after the first; rotated rows to ``out_ptr`` through
     ``out_strides``.  ``norm``: RMSNorm each row first (``eps``, optional
-    bf16 weight at ``w_ptr``, ``mul_recip`` for the 1/sqrt form)."""
+    bf16 weight at ``w_ptr``, ``mul_recip`` for the 1/sqrt form).  ``copy``:
+    the rows unchanged instead (no norm, no rotation).  ``out_pos_stride``:
+    the rows go to position pos (the runtime position, negative from the
+    end, dropped outside ``out_positions``) of the output's position axis of
+    that element stride (a cache write)."""
     x_ptr: int
     out_ptr: int
     H: int
@@ -647,6 +652,9 @@ class HeadRopeSpec:
     eps: float = 0.0
     w_ptr: int = 0
     mul_recip: bool = False
+    copy: bool = False
+    out_pos_stride: int = 0
+    out_positions: int = 0
 
 
 def head_rope(targets, cos_ptr: int, sin_ptr: int, B: int, S: int, D: int, *, table_f32: bool,
@@ -659,8 +667,8 @@ def head_rope(targets, cos_ptr: int, sin_ptr: int, B: int, S: int, D: int, *, ta
     with row the int32 at ``pos_ptr`` (negative from the end, clamped into
     ``table_rows``) or 0."""
     targets = list(targets)
-    if not 1 <= len(targets) <= 2:
-        raise LaunchError("head_rope takes one or two tensors of heads")
+    if not 1 <= len(targets) <= 3:
+        raise LaunchError("head_rope takes one to three tensors of heads")
     if D % 16 or not 16 <= D <= 128:
         raise LaunchError(f"head_rope needs a head dim that is a multiple of 16 up to 128, got {D}")
     half = D // 2
@@ -680,11 +688,16 @@ def head_rope(targets, cos_ptr: int, sin_ptr: int, B: int, S: int, D: int, *, ta
         rows_all += rows
         if rows <= 0:
             raise LaunchError("head_rope needs at least one row")
+        if t.copy and t.norm:
+            raise LaunchError("head_rope: a copied tensor is not normalised")
+        if t.out_pos_stride and (not pos_ptr or t.out_positions < 1 or int(t.out_pos_stride) % 8):
+            raise LaunchError("head_rope: a write at the runtime position needs the position, the output's "
+                              "positions and an aligned stride")
         flags = (HR_NORM if t.norm else 0) | (HR_MUL_RECIP if t.norm and t.mul_recip else 0) | \
-            (HR_W if t.norm and t.w_ptr else 0)
+            (HR_W if t.norm and t.w_ptr else 0) | (HR_COPY if t.copy else 0)
         args.t[i] = HeadRopeTarget(t.x_ptr, t.out_ptr, t.w_ptr or None, *[int(v) for v in t.x_strides],
                                    *[int(v) for v in t.out_strides], int(t.x_half), rows, -(-rows // 16),
-                                   float(t.eps), int(t.H), flags, 0)
+                                   int(t.out_pos_stride), int(t.out_positions), float(t.eps), int(t.H), flags, 0)
     if rows_all >= 2**31:
         raise LaunchError("head_rope: too many rows for one launch")
     args.cos_t, args.sin_t, args.pos = cos_ptr, sin_ptr, pos_ptr or None

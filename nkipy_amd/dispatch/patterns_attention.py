@@ -215,18 +215,22 @@ class HeadRopeMatch(Match):
             specs = []
             for m in members:
                 xv, nm = m["x"], m["norm"]
+                o_sp, o_rows = m.get("o_pos", (0, 0))
                 specs.append(LA.HeadRopeSpec(
                     addr(xv.base) + 2 * xv.offset, addr(m["out"]), m["H"], m["x_str"], m["o_str"], m["x_half"],
                     norm=nm is not None, eps=nm.eps if nm is not None else 0.0,
                     w_ptr=addr(nm.w) if nm is not None and nm.w is not None else 0,
-                    mul_recip=bool(nm.mul_recip) if nm is not None else False))
+                    mul_recip=bool(nm.mul_recip) if nm is not None else False,
+                    copy=m.get("copy", False), out_pos_stride=o_sp, out_positions=o_rows))
             te = 4 if tb["f32"] else 2
             return LA.head_rope(specs, addr(tb["cos"]) + te * tb["cos_off"], addr(tb["sin"]) + te * tb["sin_off"],
                                 B, S, D, table_f32=tb["f32"],
                                 pos_ptr=addr(tb["pos"]) if tb["pos"] is not None else 0,
                                 table_row=tb["row"], table_stride=tb["ss"], table_rows=tb["rows"])
 
-        parts = [f"{'rmsnorm + ' if m['norm'] is not None else ''}rope {m['H']} heads" for m in members]
+        parts = [(f"copy {m['H']} heads" if m.get("copy") else
+                  f"{'rmsnorm + ' if m['norm'] is not None else ''}rope {m['H']} heads")
+                 + (" -> cache row" if m.get("o_pos") else "") for m in members]
         desc = f"head rope B={B} S={S} D={D} bf16 steps: " + ", ".join(parts) + \
             (" (runtime position)" if tb["pos"] is not None else "")
         return [LaunchStep("head_rope", desc, self.inputs, self.outputs, make)]
@@ -429,11 +433,77 @@ class HeadRopePattern:
                 m["nodes"] = m["nodes"] + nm.node_list
                 m["chain"] = m["chain"] + xv.nodes
             use.append(m)
-        for attempt in (use, [dict(m, norm=None, x=o["x"], x_str=o["x_str"], x_half=o["x_half"],
-                                   nodes=o["nodes"], chain=o["chain"]) for m, o in zip(use, ms)]):
+        attempts = [use, [dict(m, norm=None, x=o["x"], x_str=o["x_str"], x_half=o["x_half"],
+                               nodes=o["nodes"], chain=o["chain"]) for m, o in zip(use, ms)]]
+        written = self._cache_writes(L, use, t0)
+        if written is not None:
+            attempts.insert(0, written)
+        for attempt in attempts:
             match = self._claim(L, attempt, t0)
             if match is not None:
                 return match
+        return None
+
+    # -- the cache writes of one decode token --------------------------------
+    @staticmethod
+    def _scatter(L, node, pos, B, H, D):
+        """``cache[:, pos] = src`` (attention.py:101-105 with start_pos) as
+        an in-place update of a cache argument the kernel's output aliases
+        (the caller's buffer is written, as the scatter kernel writes it):
+        (node, cache rows, output strides, runtime position stride)."""
+        if node.op != "scatter_along_axis" or id(node) in L.covered or node.attrs.get("axis") != 1 or \
+                node.inputs[1] is not pos:
+            return None
+        P, _, src = node.inputs
+        if not P.is_parameter or P.dtype != dt.bfloat16 or P.ndim != 4 or P.shape[0] != B or \
+                tuple(P.shape[2:]) != (H, D) or tuple(src.shape) != (B, 1, H, D):
+            return None
+        if len(L.users.get(P.id, [])) != 1:  # nothing else reads the cache before its update
+            return None
+        if not any(L.g.results[a.output_index] is node.out and f"{a.param_name}.must_alias_input" == P.name
+                   for a in L.g.aliases):
+            return None
+        A = P.shape[1]
+        return {"node": node, "src": src, "out": node.out, "o_str": (A * H * D, 0, D), "o_pos": (H * D, A)}
+
+    def _cache_writes(self, L, ms, tb):
+        """The decode form (one token, tables taken at the runtime position,
+        q and a normalised k of one projection): k written into its cache
+        row by the launch instead of by a scatter step, and the v heads of
+        the same projection copied into theirs (a third target).  Returns
+        the members with those writes, or None."""
+        if len(ms) != 2 or tb["pos"] is None or ms[0]["bsd"][1] != 1:
+            return None
+        B, _, D = ms[0]["bsd"]
+        pos = tb["pos"]
+        kk = [i for i, m in enumerate(ms) if m["norm"] is not None and m["out"].id not in L.result_ids
+              and len(L.users.get(m["out"].id, [])) == 1]
+        for i in kk:
+            km = ms[i]
+            kw = self._scatter(L, L.users[km["out"].id][0], pos, B, km["H"], D)
+            if kw is None or kw["src"] is not km["out"]:
+                continue
+            base = km["x"].base
+            for n in L.live:
+                if n is kw["node"] or n.op != "scatter_along_axis":
+                    continue
+                src = n.inputs[2]
+                vv = resolve(src, widen_ok=False)
+                if vv.base is not base or src.ndim != 4:
+                    continue
+                vw = self._scatter(L, n, pos, B, src.shape[2], D)
+                if vw is None:
+                    continue
+                st = [vv.simple(d) for d in range(4)]
+                if any(v is None for v in st) or st[3] != 1:
+                    continue
+                out = [dict(m) for m in ms]
+                out[i].update(out=kw["out"], o_str=kw["o_str"], o_pos=kw["o_pos"],
+                              nodes=km["nodes"] + [kw["node"]])
+                out.append({"n": n, "nodes": [n], "chain": list(vv.nodes), "x": vv, "x_str": tuple(st[:3]),
+                            "x_half": D // 2, "H": src.shape[2], "out": vw["out"], "o_str": vw["o_str"],
+                            "o_pos": vw["o_pos"], "norm": None, "copy": True, "bsd": km["bsd"]})
+                return out
         return None
 
     @staticmethod

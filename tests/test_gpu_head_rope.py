@@ -150,3 +150,63 @@ def test_rope_only_bf16_tables(gpu):
     fused, generic = _run_both(rot, args)
     np.testing.assert_array_equal(fused[0], generic[0])
     np.testing.assert_array_equal(fused[0], K.rope_split_half_bf16_steps(x, cb, sb))
+
+
+def _decode_prologue_with_cache(H, Hkv, D):
+    def prologue(qkv, q_norm_weight, k_norm_weight, cache_k, cache_v, start_pos):
+        B, S, _ = qkv.shape
+        xq, xk, xv = np.split(qkv, [H * D, (H + Hkv) * D], axis=2)
+        xq = rmsnorm_kernel(xq.reshape(B, S, H, D), q_norm_weight, EPS)
+        xk = rmsnorm_kernel(xk.reshape(B, S, Hkv, D), k_norm_weight, EPS)
+        cos, sin = compute_cos_sin_cache(D, cache_k.shape[1], base=THETA)
+        cos = tensor_apis.constant(cos).astype(qkv.dtype)
+        sin = tensor_apis.constant(sin).astype(qkv.dtype)
+        xq, xk = apply_rotary_emb_kernel(xq, xk, cos[start_pos], sin[start_pos])
+        cache_k[:, start_pos] = xk
+        cache_v[:, start_pos] = xv.reshape(B, S, Hkv, D)
+        return xq
+    return prologue
+
+
+@pytest.mark.parametrize("B,H,Hkv,D,MAXS,pos", [(2, 8, 2, 128, 512, 300), (8, 32, 8, 128, 4096, 4000),
+                                                 (3, 4, 4, 64, 256, -2), (1, 8, 2, 128, 256, 259)])
+def test_head_rope_writes_cache_rows(gpu, B, H, Hkv, D, MAXS, pos):
+    """The decode prologue with its cache writes (cache[:, pos] = k, v) in
+    the same launch: q and both caches bit-identical to the generic
+    lowering (norm kernel, programs, gathers and scatters), a negative
+    position counting from the end, a position past the cache dropping the
+    writes as the scatter does (and reading the clamped table row)."""
+    print(f"head rope cache writes B={B} H={H}/{Hkv} D={D} MAXS={MAXS} pos={pos}", flush=True)
+    rng = np.random.default_rng(B * 7 + MAXS)
+    qkv = N.bf16_round(rng.standard_normal((B, 1, (H + 2 * Hkv) * D)))
+    wq, wk = N.bf16_round(rng.uniform(0.5, 1.5, D)), N.bf16_round(rng.uniform(0.5, 1.5, D))
+    ck = N.bf16_round(rng.standard_normal((B, MAXS, Hkv, D)))
+    cv = N.bf16_round(rng.standard_normal((B, MAXS, Hkv, D)))
+    args = [dt.to_bf16(qkv), dt.to_bf16(wq), dt.to_bf16(wk), dt.to_bf16(ck), dt.to_bf16(cv),
+            np.array([pos], np.int32)]
+    fn = _decode_prologue_with_cache(H, Hkv, D)
+    g = NKIPyKernel.trace(fn).specialize(*args)
+    fused_plan = lower(g)
+    generic_plan = lower(g, [p for p in default_patterns() if not isinstance(p, HeadRopePattern)])
+    assert fused_plan.kernel_kinds == ["head_rope"], fused_plan.kernel_kinds
+    assert "gather" in generic_plan.kernel_kinds
+    names = [p.name for p in g.parameters]
+    outs = []
+    for i, plan in enumerate((fused_plan, generic_plan)):
+        dk = DeviceKernel(g, plan, f"cache_prologue_{i}")
+        res = dk({n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(names, args)})
+        outs.append({k: dt.to_float32(v.numpy()) for k, v in res.items()})
+    for k in outs[0]:
+        np.testing.assert_array_equal(outs[0][k], outs[1][k], err_msg=k)
+    row = pos + MAXS if pos < 0 else pos
+    if row < MAXS:
+        q, k = K.qwen3_head_prologue(qkv, wq, wk, EPS, H, Hkv, D, np.array([row]), THETA)
+        _check_oracle(outs[0]["output0"], q, "head rope cache q")
+        _check_oracle(outs[0]["cache_k"][:, row], k[:, 0], "head rope cache k")
+        np.testing.assert_array_equal(outs[0]["cache_v"][:, row],
+                                      qkv[:, 0, (H + Hkv) * D:].reshape(B, Hkv, D))
+        keep = np.arange(MAXS) != row
+    else:
+        keep = np.ones(MAXS, bool)  # the scatter drops a position past the cache
+    np.testing.assert_array_equal(outs[0]["cache_k"][:, keep], ck[:, keep])
+    np.testing.assert_array_equal(outs[0]["cache_v"][:, keep], cv[:, keep])

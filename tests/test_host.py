@@ -426,9 +426,10 @@ def test_divide_rounds_as_multiply_is_checked_per_divisor():
 def test_lowering_qwen3_head_prologue_is_one_launch():
     """The Qwen3 attention prologue (split of the QKV projection, per-head
     q / k RMSNorm, tables cast to bf16 and taken at the runtime position,
-    bf16-step RoPE) lowers to one head_rope launch that reads the projection
-    in place and the fp32 tables directly; the decode layer keeps only the v
-    split, the two cache writes and the attention between the projections."""
+    bf16-step RoPE, the k / v cache writes at that position) lowers to one
+    head_rope launch that reads the projection in place and the fp32 tables
+    directly and writes k and v into the caches' rows: the decode layer is
+    the two projections around it and the attention."""
     from nkipy_amd.kernels.qwen3 import qwen3_attention_kernel
 
     B, MAXS, HID, H, D, HKV = 2, 512, 512, 8, 128, 2
@@ -443,21 +444,26 @@ def test_lowering_qwen3_head_prologue_is_one_launch():
     g = NKIPyKernel.trace(decode).specialize(*args)
     plan = lower(g)
     _assert_temps_written_before_read(plan)
-    assert plan.kernel_kinds == ["gemm", "elementwise", "head_rope", "gather", "gather", "decode_attention", "gemm"]
+    assert plan.kernel_kinds == ["gemm", "head_rope", "decode_attention", "gemm"]
     (step,) = [st for st in plan.steps if st.kind == "head_rope"]
     (launch,) = step.launches(lambda v: 1 << 40)
     a = launch.args
     assert launch.symbol == "nk_head_rope_bf16"
     assert a.tflags == LA.HR_TABLE_F32 and a.pos == 1 << 40
     assert (a.t_row, a.t_rows, a.t_ss, a.S, a.D) == (D // 2, MAXS, 0, 1, D)
-    q, k = a.t[0], a.t[1]
-    for t, heads, col0 in ((q, H, 0), (k, HKV, H * D)):
-        assert t.flags == LA.HR_NORM | LA.HR_W and t.H == heads and t.rows == B * heads
+    q, k, v = a.t[0], a.t[1], a.t[2]
+    for t, heads, col0 in ((q, H, 0), (k, HKV, H * D), (v, HKV, (H + HKV) * D)):
+        assert t.H == heads and t.rows == B * heads
         assert (t.x_sb, t.x_sh, t.x_half) == (N, D, D // 2)  # the projection read in place
         assert t.x == (1 << 40) + 2 * col0
-        assert (t.o_sb, t.o_sh) == (heads * D, D)
-        assert np.float32(t.eps) == np.float32(1e-6)
-    assert launch.grid[0] == -(-B * H // 16) + -(-B * HKV // 16)
+    for t in (q, k):
+        assert t.flags == LA.HR_NORM | LA.HR_W and np.float32(t.eps) == np.float32(1e-6)
+    assert v.flags == LA.HR_COPY
+    assert (q.o_sb, q.o_sh, q.o_sp) == (H * D, D, 0)
+    # k and v go to row pos of their caches (B, MAXS, HKV, D)
+    for t in (k, v):
+        assert (t.o_sb, t.o_sh, t.o_sp, t.o_rows) == (MAXS * HKV * D, D, HKV * D, MAXS)
+    assert launch.grid[0] == -(-B * H // 16) + 2 * -(-B * HKV // 16)
     # prefill: the tables sliced by position instead of taken
     S = 256
 
