@@ -77,7 +77,8 @@ DEC_HID = DEC_HQ * DEC_D
 DEC_M = DEC_B * DEC_S
 QP_B, QP_S, QP_MAXS, QP_HQ, QP_HKV = 1, 2048, 4096, 32, 8
 # Qwen3 attention layer, one decode token per sequence
-QD_B, QD_MAXS, QD_POS, QD_HID, QD_HQ, QD_HKV = 8, 4096, 4000, 4096, 32, 8
+QD_B, QD_MAXS, QD_POS, QD_HID, QD_HQ, QD_HKV, QD_EPS = 8, 4096, 4000, 4096, 32, 8, 1e-6
+QD_OTHER_BATCHES = (1, 32)
 
 
 def _linattn_prefix_bytes():
@@ -141,10 +142,10 @@ def _decode_launches():
             ("o_reduce", "hbm", 4 * ks2 * B * hid + 2 * B * hid)]
 
 
-def _decode_step_bytes():
+def _decode_step_bytes(B=QD_B):
     """Algorithmic HBM bytes of one decode step: both weights, the K / V
     rows attended, the token's activations and its cache rows."""
-    B, H, Hkv, D, hid = QD_B, QD_HQ, QD_HKV, DEC_D, QD_HID
+    H, Hkv, D, hid = QD_HQ, QD_HKV, DEC_D, QD_HID
     nqkv = (H + 2 * Hkv) * D
     return (2 * hid * nqkv + 2 * H * D * hid + 2 * 2 * B * (QD_POS + 1) * Hkv * D
             + 2 * 2 * B * hid + 2 * 2 * B * Hkv * D)
@@ -657,19 +658,20 @@ def bench_qwen3_prefill(a, rt, mk):
     return entry, cpu
 
 
-def bench_qwen3_decode(a, rt, mk):
+def _decode_case(B, rt):
+    """The traced Qwen3 decode layer at batch B with its rotating buffer
+    sets: (kernel, sets of (inputs, outputs), bound plans, host arrays)."""
     from nkipy_amd.core import dtypes as dt
     from nkipy_amd.kernels.qwen3 import qwen3_attention_kernel
     from nkipy_amd.runtime import DeviceKernel, DeviceTensor
 
-    B, MAXS, pos, hid, H, Hkv, D = QD_B, QD_MAXS, QD_POS, QD_HID, QD_HQ, QD_HKV, DEC_D
-    eps = 1e-6
+    MAXS, pos, hid, H, Hkv, D = QD_MAXS, QD_POS, QD_HID, QD_HQ, QD_HKV, DEC_D
 
     def decode(x, qkv_weight, q_norm_weight, k_norm_weight, cache_k, cache_v, start_pos, o_weight):
-        return qwen3_attention_kernel(x, qkv_weight, q_norm_weight, k_norm_weight, eps, H, D, Hkv,
+        return qwen3_attention_kernel(x, qkv_weight, q_norm_weight, k_norm_weight, QD_EPS, H, D, Hkv,
                                       cache_k, cache_v, start_pos, o_weight)
 
-    rng = np.random.default_rng(42)
+    rng = np.random.default_rng(42 + B)
     host = {"x": dt.round_to_bf16(rng.standard_normal((B, 1, hid), dtype=np.float32)),
             "qkv_weight": dt.round_to_bf16(rng.standard_normal((hid, (H + 2 * Hkv) * D), dtype=np.float32)
                                            * hid ** -0.5),
@@ -680,45 +682,66 @@ def bench_qwen3_decode(a, rt, mk):
             "o_weight": dt.round_to_bf16(rng.standard_normal((H * D, hid), dtype=np.float32) * (H * D) ** -0.5)}
     order = ["x", "qkv_weight", "q_norm_weight", "k_norm_weight", "cache_k", "cache_v"]
     args = [dt.to_bf16(host[n]) for n in order] + [np.array([pos], np.int32), dt.to_bf16(host["o_weight"])]
-    dk = DeviceKernel.compile_and_load(decode, *args, name="qwen3_decode_step")
+    dk = DeviceKernel.compile_and_load(decode, *args, name=f"qwen3_decode_step_b{B}")
     names = [p.name for p in dk.graph.parameters]
-    # every set holds its own weights and caches (218 MB): a layer's weights
-    # are not cache-resident between its steps in a model of many layers
-    per_set = sum(v.nbytes for v in args)
+    # every set holds its own weights and caches: a layer's weights are not
+    # cache-resident between its steps in a model of many layers
     sets = []
-    for _ in range(_sets_for(per_set)):
+    for _ in range(_sets_for(sum(v.nbytes for v in args))):
         ins = {n: DeviceTensor.from_numpy(v, name=n) for n, v in zip(names, args)}
         outs = {"output0": DeviceTensor.empty((B, 1, hid), dt.bfloat16, name="output0"),
                 "cache_k": ins["cache_k.must_alias_input"], "cache_v": ins["cache_v.must_alias_input"]}
         sets.append((ins, outs))
     bounds = [dk.executor.bind(dk._io_ptrs(i, o)) for i, o in sets]
+    return dk, sets, bounds, host
+
+
+def _sync_call_us(dk, ins, outs, n=50):
+    """One synchronous call at a time (host dispatch, launches, wait): the
+    latency a serving loop that waits for each token sees."""
+    for _ in range(10):
+        dk(ins, outs)
+    t0 = time.perf_counter()
+    for _ in range(n):
+        dk(ins, outs)
+    return (time.perf_counter() - t0) / n * 1e6
+
+
+def bench_qwen3_decode(a, rt, mk):
+    from nkipy_amd.core import dtypes as dt
+
+    B, MAXS, pos, hid, H, Hkv, D = QD_B, QD_MAXS, QD_POS, QD_HID, QD_HQ, QD_HKV, DEC_D
+    steps, warm = max(20, a.steps // 2), max(5, a.warmup)
+    dk, sets, bounds, host = _decode_case(B, rt)
     if len(bounds[0].launches) != len(sections()[7][1]):
         raise RuntimeError(f"Qwen3 decode step has an unexpected launch list: "
                            f"{[l.symbol for l in bounds[0].launches]}")
-    steps, warm = max(20, a.steps // 2), max(5, a.warmup)
     mk.mark(7)
     ms = _time_steps(bounds, steps, warm, rt)
     recs = _kernel_records(7, bounds[0].launches, _time_in_step(bounds, max(20, steps // 2), rt, mk))
-    # one synchronous call at a time (host dispatch, launches, wait): the
-    # latency a serving loop that waits for each token sees
     ins0, outs0 = sets[0]
-    for _ in range(10):
-        dk(ins0, outs0)
-    t0 = time.perf_counter()
-    n_sync = 50
-    for _ in range(n_sync):
-        dk(ins0, outs0)
-    sync_us = (time.perf_counter() - t0) / n_sync * 1e6
-    work = _decode_step_bytes()
+    sync_us = _sync_call_us(dk, ins0, outs0)
     step_rec = {"label": "step", "kernel": " + ".join(l.symbol for l in bounds[0].launches), "bound": "hbm"}
-    roof = _roofline(7, step_rec, us=ms * 1e3, work=work)
+    roof = _roofline(7, step_rec, us=ms * 1e3, work=_decode_step_bytes(B))
     roof["traffic"] = None
+    # the same step at one token and at a larger batch (no per-launch split)
+    batches = []
+    for b in QD_OTHER_BATCHES:
+        dkb, setsb, boundsb, _ = _decode_case(b, rt)
+        msb = _time_steps(boundsb, steps, warm, rt)
+        wb = _decode_step_bytes(b)
+        batches.append({"batch": b, "us_per_step": round(msb * 1e3, 2),
+                        "synchronous_call_us": round(_sync_call_us(dkb, *setsb[0]), 1),
+                        "launches": len(boundsb[0].launches), "bytes": wb,
+                        "achieved_GBs": round(wb / (msb * 1e-3) / 1e9, 1),
+                        "frac": round(wb / (msb * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+        del dkb, setsb, boundsb
     entry = {"config": 7, "workload": "qwen3_decode_step",
              "shape": {"batch": B, "cache_rows": MAXS, "position": pos, "hidden": hid, "heads": H,
                        "kv_heads": Hkv, "head_dim": D},
              "dtype": "bf16 (the traced cast points of the Qwen3 attention layer)",
              "us_per_step": round(ms * 1e3, 2), "synchronous_call_us": round(sync_us, 1),
-             "roofline": roof, "kernels": recs,
+             "roofline": roof, "kernels": recs, "other_batches": batches,
              "note": "one token per sequence through the whole attention layer (QKV projection, q / k norm and "
                      "RoPE, cache writes, attention over pos + 1 cached rows, output projection); steps queued "
                      "back to back over rotating weight / cache sets; synchronous_call_us waits for each step"}
@@ -728,7 +751,8 @@ def bench_qwen3_decode(a, rt, mk):
 
         f32 = {k: dt.to_float32(dt.to_bf16(v)) for k, v in host.items()}
         run = lambda: K.qwen3_decode_layer(f32["x"], f32["qkv_weight"], f32["q_norm_weight"], f32["k_norm_weight"],
-                                           eps, H, Hkv, D, f32["cache_k"], f32["cache_v"], pos, f32["o_weight"])
+                                           QD_EPS, H, Hkv, D, f32["cache_k"], f32["cache_v"], pos,
+                                           f32["o_weight"])
         t, ts, ref = _timed(run, 3)
         got = dt.to_float32(outs0["output0"].numpy())
         return ({"value": round(t * 1e6, 0), "unit": "us per decode step", "cores": _blas_threads(),
