@@ -1031,19 +1031,18 @@ extern "C" __global__ __launch_bounds__(256, 3) void nk_attention_causal_d128_k3
 // splits past pos exit at once) and the step runs as four launches over a
 // workspace (DecodeAttnArgs::ws):
 //   scores   one workgroup per (batch, KV head, split): the split's K rows
-//            into LDS with 16-byte loads (rows padded to 272 bytes, so the
-//            row reads below are conflict free), thread = (key, half of the
-//            rep queries), fp32 dot products with q from LDS (broadcast
-//            reads), the cast points; the scores and each query's max over
-//            the split go to the workspace;
+//            read into registers (16 bytes per lane), fp32 dot products
+//            with q from LDS, reduced over the 16 lanes of a row, the cast
+//            points; the scores and each query's max over the split go to
+//            the workspace;
 //   rowstat  one workgroup per (batch, query head): the row's max m over
 //            the split maxima and the sum l of e = exp(s - m) (block
 //            reduction), each step rounded to bf16 with DEC_SOFTMAX_BF16;
 //   values   one workgroup per (batch, KV head, split): the split's V rows
-//            into LDS and its weights p = e / l (again each step rounded
-//            with DEC_SOFTMAX_BF16) from the scores, m and l; thread =
-//            (column, half of the queries), fp32 sum of p v over the
-//            split's keys, written per split;
+//            read into registers and its weights p = e / l (again each step
+//            rounded with DEC_SOFTMAX_BF16) from the scores, m and l into
+//            LDS; fp32 sums of p v over key groups added in a fixed order,
+//            written per split;
 //   combine  one workgroup per (batch, query head): the splits' partial
 //            outputs added in split order, rounded to bf16.
 // Workspace (fp32), with nsplit = ceil(Smax / DKS) and rows r = b * Hq + h:
@@ -1051,9 +1050,8 @@ extern "C" __global__ __launch_bounds__(256, 3) void nk_attention_causal_d128_k3
 //   split maxima      [r][nsplit] after B * Hq * Smax
 //   partial outputs   [r][nsplit][128] after that
 //   row statistics    [r][2] (m, l) after that
-#define DQ_MAX 16       // query heads per KV head
+#define DQ_MAX 16       // query heads per KV head (kernels for 1, 2, 4, 8, 16)
 #define DKS 128         // keys per split
-#define DK_ROW 272      // padded K row (bytes)
 
 enum { DEC_RND_PROD = 1, DEC_RND_SCORE = 2, DEC_SOFTMAX_BF16 = 4, DEC_DIVIDE = 8 };
 
@@ -1080,13 +1078,19 @@ __device__ __forceinline__ int decode_keys(const DecodeAttnArgs &a) {
   return pos + 1;
 }
 
-extern "C" __global__ __launch_bounds__(256) void nk_decode_scores_d128(DecodeAttnArgs a) {
-  __shared__ __attribute__((aligned(16))) float qs[DQ_MAX][AD];
-  __shared__ __attribute__((aligned(16))) uint8_t kt[DKS * DK_ROW];
-  __shared__ float smax[DQ_MAX][4];
+// Scores: lane (c, r) of wave w, c = lane % 16, r = lane / 16, holds
+// dims 8c .. 8c+7 of the split's keys w * 32 + r + 4 i (i < 8), read
+// straight from the cache (each load instruction covers four whole 256-byte
+// rows); q of the REPT queries comes from LDS.  A key's dot product is the
+// 16 lanes' partial sums added by the row kernels' four DPP steps, taken
+// from lane c = 0.  No K tile in LDS: 2 KiB of LDS per workgroup.
+template <int REPT>
+__device__ __forceinline__ void decode_scores_body(const DecodeAttnArgs &a) {
+  __shared__ __attribute__((aligned(16))) float qs[REPT][AD];
+  __shared__ float smax[4][REPT];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int rep = a.Hq / a.Hkv;
+  const int rep = a.Hq / a.Hkv;  // <= REPT
   const int sp = blockIdx.x % a.nsplit;
   const int bg = blockIdx.x / a.nsplit;
   const int b = bg / a.Hkv, g = bg % a.Hkv;
@@ -1095,29 +1099,24 @@ extern "C" __global__ __launch_bounds__(256) void nk_decode_scores_d128(DecodeAt
   if (k0 >= L) return;  // uniform: the whole workgroup
   const int nk = min(DKS, L - k0);
   const uint16_t *kb = a.k + (int64_t)b * a.k_sb + (int64_t)g * a.k_sh + (int64_t)k0 * a.k_ss;
+  const int c = lane & 15, r = lane >> 4;
 
-  // K rows of the split: 16-byte chunk c of row r by thread (r % 16) * 16 +
-  // c, rows r = that + 16 i; then q of the rep heads (thread -> 8 values
-  // of one head).  Every load is issued before the first store (one memory
-  // latency, not nine) and none sits behind a branch: rows past pos load
-  // the last attended row again and store zeros
+  // every load before the first use: K (rows past pos load the last
+  // attended row, their scores are dropped), then q (thread -> 8 values of
+  // one query)
+  uint4 kr[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = min(wave * 32 + r + 4 * i, nk - 1);
+    kr[i] = *reinterpret_cast<const uint4 *>(kb + (int64_t)row * a.k_ss + c * 8);
+  }
   {
-    const int c = tid & 15, r0 = tid >> 4;
-    uint4 w[DKS / 16];
-#pragma unroll
-    for (int i = 0; i < DKS / 16; ++i) {
-      const int row = min(r0 + 16 * i, nk - 1);
-      w[i] = *reinterpret_cast<const uint4 *>(kb + (int64_t)row * a.k_ss + c * 8);
-    }
-    const int qi = tid >> 4;  // 16 threads x 8 values per head, rep <= 16
-    const uint4 qw = *reinterpret_cast<const uint4 *>(a.q + (int64_t)b * a.q_sb +
-                                                      (int64_t)(g * rep + min(qi, rep - 1)) * a.q_sh + c * 8);
-#pragma unroll
-    for (int i = 0; i < DKS / 16; ++i)
-      *reinterpret_cast<uint4 *>(kt + (r0 + 16 * i) * DK_ROW + c * 16) =
-          r0 + 16 * i < nk ? w[i] : make_uint4(0, 0, 0, 0);
-    if (qi < rep) {
-      float *qd = &qs[qi][c * 8];
+    const int qi = tid >> 4, qc = tid & 15;
+    if (qi < REPT) {
+      const int qq = min(qi, rep - 1);
+      const uint4 qw = *reinterpret_cast<const uint4 *>(a.q + (int64_t)b * a.q_sb +
+                                                        (int64_t)(g * rep + qq) * a.q_sh + qc * 8);
+      float *qd = &qs[qi][qc * 8];
       qd[0] = __uint_as_float(qw.x << 16); qd[1] = __uint_as_float(qw.x & 0xffff0000u);
       qd[2] = __uint_as_float(qw.y << 16); qd[3] = __uint_as_float(qw.y & 0xffff0000u);
       qd[4] = __uint_as_float(qw.z << 16); qd[5] = __uint_as_float(qw.z & 0xffff0000u);
@@ -1126,50 +1125,57 @@ extern "C" __global__ __launch_bounds__(256) void nk_decode_scores_d128(DecodeAt
   }
   __syncthreads();
 
-  // thread -> key r of the split, queries qi = half, half + 2, ...
-  const int r = tid & (DKS - 1), half = tid >> 7;
-  float acc[DQ_MAX / 2];
+  float qv[REPT][8];
 #pragma unroll
-  for (int j = 0; j < DQ_MAX / 2; ++j) acc[j] = 0.f;
-  for (int c = 0; c < 16; ++c) {
-    const uint4 w = *reinterpret_cast<const uint4 *>(kt + r * DK_ROW + c * 16);
-    float kf[8];
-    kf[0] = __uint_as_float(w.x << 16); kf[1] = __uint_as_float(w.x & 0xffff0000u);
-    kf[2] = __uint_as_float(w.y << 16); kf[3] = __uint_as_float(w.y & 0xffff0000u);
-    kf[4] = __uint_as_float(w.z << 16); kf[5] = __uint_as_float(w.z & 0xffff0000u);
-    kf[6] = __uint_as_float(w.w << 16); kf[7] = __uint_as_float(w.w & 0xffff0000u);
-#pragma unroll
-    for (int j = 0; j < DQ_MAX / 2; ++j) {
-      const int qi = half + 2 * j;
-      if (qi < rep) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[j] = fmaf(qs[qi][c * 8 + e], kf[e], acc[j]);
-      }
-    }
+  for (int q = 0; q < REPT; ++q) {
+    const float4 lo = *reinterpret_cast<const float4 *>(&qs[q][c * 8]);
+    const float4 hi = *reinterpret_cast<const float4 *>(&qs[q][c * 8 + 4]);
+    qv[q][0] = lo.x; qv[q][1] = lo.y; qv[q][2] = lo.z; qv[q][3] = lo.w;
+    qv[q][4] = hi.x; qv[q][5] = hi.y; qv[q][6] = hi.z; qv[q][7] = hi.w;
   }
   const int64_t row0 = (int64_t)b * a.Hq + g * rep;  // score row of query 0
-  float *sc = a.ws + row0 * a.Smax;
-  float *mx = a.ws + (int64_t)a.B * a.Hq * a.Smax + row0 * a.nsplit + sp;
+  float *sc = a.ws + row0 * a.Smax + k0;
+  float mloc[REPT];
 #pragma unroll
-  for (int j = 0; j < DQ_MAX / 2; ++j) {
-    const int qi = half + 2 * j;
-    if (qi < rep) {  // uniform over the workgroup
-      float s = acc[j];
+  for (int q = 0; q < REPT; ++q) mloc[q] = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int key = wave * 32 + r + 4 * i;
+    float kf[8];
+    kf[0] = __uint_as_float(kr[i].x << 16); kf[1] = __uint_as_float(kr[i].x & 0xffff0000u);
+    kf[2] = __uint_as_float(kr[i].y << 16); kf[3] = __uint_as_float(kr[i].y & 0xffff0000u);
+    kf[4] = __uint_as_float(kr[i].z << 16); kf[5] = __uint_as_float(kr[i].z & 0xffff0000u);
+    kf[6] = __uint_as_float(kr[i].w << 16); kf[7] = __uint_as_float(kr[i].w & 0xffff0000u);
+#pragma unroll
+    for (int q = 0; q < REPT; ++q) {
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d = fmaf(qv[q][e], kf[e], d);
+      d = d + dpp<0xB1>(d);
+      d = d + dpp<0x4E>(d);
+      d = d + dpp<0x124>(d);
+      d = d + dpp<0x128>(d);
+      float s = __shfl(d, lane & ~15);  // lane c = 0's sum
       if (a.flags & DEC_RND_PROD) s = bf16r(s);
       s = (a.flags & DEC_DIVIDE) ? s / a.scale : s * a.scale;
       if (a.flags & DEC_RND_SCORE) s = bf16r(s);
-      if (r < nk) sc[(int64_t)qi * a.Smax + k0 + r] = s;
-      float m = r < nk ? s : -INFINITY;
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-      if (lane == 0) smax[qi][wave] = m;
+      if (c == 0 && q < rep && key < nk) sc[(int64_t)q * a.Smax + key] = s;
+      if (key < nk) mloc[q] = fmaxf(mloc[q], s);
     }
   }
+  // the split's max per query: over the four key groups of the wave, then
+  // over the waves
+#pragma unroll
+  for (int q = 0; q < REPT; ++q) {
+    float m = mloc[q];
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    if (lane == 0) smax[wave][q] = m;
+  }
   __syncthreads();
-  // waves 0, 1 hold the even queries, waves 2, 3 the odd ones
   if (tid < rep) {
-    const int w0 = (tid & 1) * 2;
-    mx[(int64_t)tid * a.nsplit] = fmaxf(smax[tid][w0], smax[tid][w0 + 1]);
+    float *mx = a.ws + (int64_t)a.B * a.Hq * a.Smax + row0 * a.nsplit + sp;
+    mx[(int64_t)tid * a.nsplit] = fmaxf(fmaxf(smax[0][tid], smax[1][tid]), fmaxf(smax[2][tid], smax[3][tid]));
   }
 }
 
@@ -1223,12 +1229,20 @@ extern "C" __global__ __launch_bounds__(256) void nk_decode_rowstat_d128(DecodeA
   }
 }
 
-extern "C" __global__ __launch_bounds__(256) void nk_decode_values_d128(DecodeAttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t vt[DKS * AD];
-  __shared__ float ps[DQ_MAX][DKS];
+// Weighted values: the split's weights p (REPT per key, 0 past pos or rep)
+// into LDS first; lane (c, r) of wave w holds columns 8c .. 8c+7 of keys
+// w * 32 + r + 4 i (i < 8), read straight from the cache with the scores
+// and statistics (every load issued before the first use), and sums p v
+// over its keys in order; the four key groups of a wave are added by xor
+// shuffles (16, then 32), the four waves through LDS as (w0 + w1) +
+// (w2 + w3).  10 KiB of LDS per workgroup at REPT = 4.
+template <int REPT>
+__device__ __forceinline__ void decode_values_body(const DecodeAttnArgs &a) {
+  __shared__ __attribute__((aligned(16))) float ps[DKS][REPT];
+  __shared__ float red[4][REPT][AD];
 
-  const int tid = threadIdx.x;
-  const int rep = a.Hq / a.Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rep = a.Hq / a.Hkv;  // <= REPT
   const int sp = blockIdx.x % a.nsplit;
   const int bg = blockIdx.x / a.nsplit;
   const int b = bg / a.Hkv, g = bg % a.Hkv;
@@ -1239,39 +1253,34 @@ extern "C" __global__ __launch_bounds__(256) void nk_decode_values_d128(DecodeAt
   const uint16_t *vb = a.v + (int64_t)b * a.v_sb + (int64_t)g * a.v_sh + (int64_t)k0 * a.v_ss;
   const int64_t row0 = (int64_t)b * a.Hq + g * rep;
   const float *pw = a.ws + row0 * a.Smax + k0;
+  const int c = lane & 15, r = lane >> 4;
 
-  // V rows as the K rows of the scores kernel, then this thread's scores
-  // (key kk, queries q0, q0 + 2, ...) and their rows' statistics: all loads
-  // first and none behind a branch (indexes clamped into range, results
-  // past pos or rep dropped)
-  {
-    const int c = tid & 15, r0 = tid >> 4;
-    uint4 w[DKS / 16];
+  uint4 vr[8];
 #pragma unroll
-    for (int i = 0; i < DKS / 16; ++i) {
-      const int row = min(r0 + 16 * i, nk - 1);
-      w[i] = *reinterpret_cast<const uint4 *>(vb + (int64_t)row * a.v_ss + c * 8);
-    }
+  for (int i = 0; i < 8; ++i) {
+    const int row = min(wave * 32 + r + 4 * i, nk - 1);
+    vr[i] = *reinterpret_cast<const uint4 *>(vb + (int64_t)row * a.v_ss + c * 8);
+  }
+  {
+    // this thread's (key kk, queries q0, q0 + 2, ...) weights
+    constexpr int NJ = (REPT + 1) / 2;
     const int kk = tid & (DKS - 1), q0 = tid >> 7;
     const float *rs = a.ws + (int64_t)a.B * a.Hq * (a.Smax + a.nsplit + (int64_t)a.nsplit * AD) + row0 * 2;
-    float pv[DQ_MAX / 2], st[DQ_MAX / 2][2];
+    float pv[NJ], st[NJ][2];
 #pragma unroll
-    for (int j = 0; j < DQ_MAX / 2; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int qc = min(q0 + 2 * j, rep - 1);
       pv[j] = pw[(int64_t)qc * a.Smax + min(kk, nk - 1)];
       st[j][0] = rs[qc * 2];
       st[j][1] = rs[qc * 2 + 1];
     }
-#pragma unroll
-    for (int i = 0; i < DKS / 16; ++i)
-      *reinterpret_cast<uint4 *>(vt + (r0 + 16 * i) * AD + c * 8) = r0 + 16 * i < nk ? w[i] : make_uint4(0, 0, 0, 0);
     const bool rnd = (a.flags & DEC_SOFTMAX_BF16) != 0;
 #pragma unroll
-    for (int j = 0; j < DQ_MAX / 2; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int qi = q0 + 2 * j;
-      if (qi < rep) {
-        float p = 0.f;  // (keys past pos: weight 0, never added)
-        if (kk < nk) {
+      if (qi < REPT) {
+        float p = 0.f;  // (keys past pos, queries past rep: weight 0)
+        if (kk < nk && qi < rep) {
           float d = pv[j] - st[j][0];
           if (rnd) d = bf16r(d);
           float e = expf(d);
@@ -1279,40 +1288,70 @@ extern "C" __global__ __launch_bounds__(256) void nk_decode_values_d128(DecodeAt
           p = e / st[j][1];
           if (rnd) p = bf16r(p);
         }
-        ps[qi][kk] = p;
+        ps[kk][qi] = p;
       }
     }
   }
   __syncthreads();
 
-  // thread -> column d, queries qi = half, half + 2, ...
-  const int d = tid & (AD - 1), half = tid >> 7;
-  float acc[DQ_MAX / 2];
+  float acc[REPT][8];
 #pragma unroll
-  for (int j = 0; j < DQ_MAX / 2; ++j) acc[j] = 0.f;
-  // keys in order; past nk (a partial last split) the weights are 0 and
-  // not added, so the sum is that of the split's own keys
-  for (int k8 = 0; k8 < nk; k8 += 8) {
+  for (int q = 0; q < REPT; ++q)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[q][e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int key = wave * 32 + r + 4 * i;
+    const bool in = key < nk;  // rows past pos: weight 0 and values 0
     float vv[8];
+    vv[0] = __uint_as_float(vr[i].x << 16); vv[1] = __uint_as_float(vr[i].x & 0xffff0000u);
+    vv[2] = __uint_as_float(vr[i].y << 16); vv[3] = __uint_as_float(vr[i].y & 0xffff0000u);
+    vv[4] = __uint_as_float(vr[i].z << 16); vv[5] = __uint_as_float(vr[i].z & 0xffff0000u);
+    vv[6] = __uint_as_float(vr[i].w << 16); vv[7] = __uint_as_float(vr[i].w & 0xffff0000u);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) vv[u] = bf16_to_f32(vt[(k8 + u) * AD + d]);
+    for (int e = 0; e < 8; ++e) vv[e] = in ? vv[e] : 0.f;
 #pragma unroll
-    for (int j = 0; j < DQ_MAX / 2; ++j) {
-      const int qi = half + 2 * j;
-      if (qi < rep) {
+    for (int q = 0; q < REPT; ++q) {
+      const float p = ps[key][q];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (k8 + u < nk) acc[j] = fmaf(ps[qi][k8 + u], vv[u], acc[j]);
-      }
+      for (int e = 0; e < 8; ++e) acc[q][e] = fmaf(p, vv[e], acc[q][e]);
     }
   }
-  float *op = a.ws + (int64_t)a.B * a.Hq * (a.Smax + a.nsplit) + (row0 * a.nsplit + sp) * AD;
 #pragma unroll
-  for (int j = 0; j < DQ_MAX / 2; ++j) {
-    const int qi = half + 2 * j;
-    if (qi < rep) op[(int64_t)qi * a.nsplit * AD + d] = acc[j];
+  for (int q = 0; q < REPT; ++q)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = acc[q][e];
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      acc[q][e] = v;
+    }
+  if (r == 0) {
+#pragma unroll
+    for (int q = 0; q < REPT; ++q)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red[wave][q][c * 8 + e] = acc[q][e];
   }
+  __syncthreads();
+  const int d = tid & (AD - 1), qh = tid >> 7;
+  float *op = a.ws + (int64_t)a.B * a.Hq * (a.Smax + a.nsplit) + (row0 * a.nsplit + sp) * AD;
+  for (int q = qh; q < rep; q += 2)
+    op[(int64_t)q * a.nsplit * AD + d] = (red[0][q][d] + red[1][q][d]) + (red[2][q][d] + red[3][q][d]);
 }
+
+// kernels for up to REPT query heads per KV head
+#define NK_DECODE_REP(R)                                                                           \
+  extern "C" __global__ __launch_bounds__(256) void nk_decode_scores_d128_r##R(DecodeAttnArgs a) { \
+    decode_scores_body<R>(a);                                                                      \
+  }                                                                                                \
+  extern "C" __global__ __launch_bounds__(256) void nk_decode_values_d128_r##R(DecodeAttnArgs a) { \
+    decode_values_body<R>(a);                                                                      \
+  }
+NK_DECODE_REP(1)
+NK_DECODE_REP(2)
+NK_DECODE_REP(4)
+NK_DECODE_REP(8)
+NK_DECODE_REP(16)
 
 extern "C" __global__ __launch_bounds__(128) void nk_decode_combine_d128(DecodeAttnArgs a) {
   const int d = threadIdx.x;

@@ -1067,10 +1067,11 @@ def decode_attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, pos_ptr: in
                           *strides["o"], B, Smax, Hq, Hkv, float(scale), int(flags), int(ws_ptr), nsplit)
     kv = B * Smax * Hkv * D * 2  # one cache's bytes (an upper bound: keys past pos are not read)
     sc = 4 * B * Hq * Smax
-    return [Launch("attention", "nk_decode_scores_d128", (B * Hkv * nsplit, 1, 1), (256, 1, 1), args,
+    rt = next(r for r in (1, 2, 4, 8, 16) if r >= rep)  # kernels for up to rt queries per KV head
+    return [Launch("attention", f"nk_decode_scores_d128_r{rt}", (B * Hkv * nsplit, 1, 1), (256, 1, 1), args,
                    bytes=kv + B * Hq * D * 2 + sc, flops=2 * B * Hq * Smax * D),
             Launch("attention", "nk_decode_rowstat_d128", (B * Hq, 1, 1), (256, 1, 1), args, bytes=sc),
-            Launch("attention", "nk_decode_values_d128", (B * Hkv * nsplit, 1, 1), (256, 1, 1), args,
+            Launch("attention", f"nk_decode_values_d128_r{rt}", (B * Hkv * nsplit, 1, 1), (256, 1, 1), args,
                    bytes=kv + sc + 4 * B * Hq * nsplit * D, flops=2 * B * Hq * Smax * D),
             Launch("attention", "nk_decode_combine_d128", (B * Hq, 1, 1), (128, 1, 1), args,
                    bytes=4 * B * Hq * nsplit * D + B * Hq * D * 2)]

@@ -28,7 +28,7 @@ def _close(got, ref):
 @pytest.mark.parametrize("B,Smax,Hq,Hkv,pos", [(1, 128, 4, 1, 0), (2, 256, 8, 2, 100), (2, 300, 4, 2, 299),
                                                 (3, 1024, 16, 4, 1023), (1, 1024, 16, 1, 600),
                                                 (1, 4096, 32, 8, 4095), (2, 5000, 8, 2, 4321),
-                                                (1, 8192, 4, 4, 129)])
+                                                (1, 8192, 4, 4, 129), (2, 700, 16, 2, 650), (3, 384, 12, 4, 200)])
 @pytest.mark.parametrize("casts", [True, False])
 def test_decode_attention_kernel(gpu, B, Smax, Hq, Hkv, pos, casts):
     """Splits of 128 cache positions: one (pos 0), a partial last split
