@@ -1063,6 +1063,12 @@ def decode_attention(q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, pos_ptr: in
     nsplit = -(-Smax // DEC_SPLIT)
     if B * Hkv * nsplit >= 2**31 or B * Hq >= 2**31:
         raise LaunchError("decode attention grid too large")
+    rounded = DEC_RND_PROD | DEC_RND_SCORE
+    if flags & DEC_DIVIDE and flags & rounded == rounded and divide_rounds_as_multiply(scale):
+        # a bf16 product divided and rounded to bf16 equals its product by
+        # RN(1 / scale) rounded to bf16, for every bf16 product (checked)
+        scale = float(np.float32(1) / np.float32(scale))
+        flags &= ~DEC_DIVIDE
     args = DecodeAttnArgs(q_ptr, k_ptr, v_ptr, o_ptr, pos_ptr, *strides["q"], *strides["k"], *strides["v"],
                           *strides["o"], B, Smax, Hq, Hkv, float(scale), int(flags), int(ws_ptr), nsplit)
     kv = B * Smax * Hkv * D * 2  # one cache's bytes (an upper bound: keys past pos are not read)

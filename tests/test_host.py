@@ -416,11 +416,22 @@ def test_divide_rounds_as_multiply_is_checked_per_divisor():
         if same:  # spot check of the claim on random scores
             np.testing.assert_array_equal(dt.round_to_bf16(s / np.float32(c)),
                                           dt.round_to_bf16(s * (np.float32(1) / np.float32(c))))
-        st = {"q": (8 * 128, 128, 8 * 128), "k": (8 * 128, 128, 0), "v": (8 * 128, 128, 0), "o": (8 * 128, 128, 8 * 128)}
+        st = {"q": (8 * 128, 128, 8 * 128), "k": (8 * 128, 128, 0), "v": (8 * 128, 128, 0),
+              "o": (8 * 128, 128, 8 * 128)}
         (_, _, l) = LA.attention(1 << 20, 1 << 20, 1 << 20, 1 << 20, 1, 256, 1, 1, 128, 1 / c, st,
                                  score_flags=LA.ATT_RND_PROD | LA.ATT_RND_SCORE | LA.ATT_DIVIDE | LA.ATT_SOFTMAX_BF16,
                                  divisor=c, rowstat_ptr=1 << 20)
         assert bool(l.args.flags & LA.ATT_DIVIDE) is not same
+        # the decode step: the same rewrite when the product and the score
+        # are rounded; an fp32 product keeps the divide
+        dst = {"q": (128, 128), "k": (128, 128, 128), "v": (128, 128, 128), "o": (128, 128)}
+        for flags, rewrite in ((LA.DEC_RND_PROD | LA.DEC_RND_SCORE | LA.DEC_SOFTMAX_BF16, same),
+                               (LA.DEC_RND_SCORE, False)):
+            ls = LA.decode_attention(1 << 20, 1 << 20, 1 << 20, 1 << 20, 1 << 20, 1, 256, 1, 1, 128, c, dst,
+                                     flags=flags | LA.DEC_DIVIDE, ws_ptr=1 << 20)
+            a = ls[0].args
+            assert bool(a.flags & LA.DEC_DIVIDE) is not rewrite
+            assert np.float32(a.scale) == (np.float32(1) / np.float32(c) if rewrite else np.float32(c))
 
 
 def test_lowering_qwen3_head_prologue_is_one_launch():
