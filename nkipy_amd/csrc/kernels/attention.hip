@@ -1078,12 +1078,13 @@ __device__ __forceinline__ int decode_keys(const DecodeAttnArgs &a) {
   return pos + 1;
 }
 
-// Scores: lane (c, r) of wave w, c = lane % 16, r = lane / 16, holds
-// dims 8c .. 8c+7 of the split's keys w * 32 + r + 4 i (i < 8), read
-// straight from the cache (each load instruction covers four whole 256-byte
-// rows); q of the REPT queries comes from LDS.  A key's dot product is the
-// 16 lanes' partial sums added by the row kernels' four DPP steps, taken
-// from lane c = 0.  No K tile in LDS: 2 KiB of LDS per workgroup.
+// Scores: lane (r, c) of wave w, r = lane / 4, c = lane % 4, holds dims
+// 8 (c + 4 j) .. +7 (j < 4) of keys w * 32 + r + 16 i (i < 2), read
+// straight from the cache (each load instruction covers 64 contiguous
+// bytes of 16 rows); q of the REPT queries comes from LDS.  A key's dot
+// product is the quad's four partial sums added by two DPP steps (the four
+// lanes then hold the same sum), whose cast points each lane applies; lane
+// c = 0 stores.  2 KiB of LDS per workgroup at REPT = 4.
 template <int REPT>
 __device__ __forceinline__ void decode_scores_body(const DecodeAttnArgs &a) {
   __shared__ __attribute__((aligned(16))) float qs[REPT][AD];
@@ -1099,16 +1100,18 @@ __device__ __forceinline__ void decode_scores_body(const DecodeAttnArgs &a) {
   if (k0 >= L) return;  // uniform: the whole workgroup
   const int nk = min(DKS, L - k0);
   const uint16_t *kb = a.k + (int64_t)b * a.k_sb + (int64_t)g * a.k_sh + (int64_t)k0 * a.k_ss;
-  const int c = lane & 15, r = lane >> 4;
+  const int r = lane >> 2, c = lane & 3;
 
   // every load before the first use: K (rows past pos load the last
   // attended row, their scores are dropped), then q (thread -> 8 values of
   // one query)
-  uint4 kr[8];
+  uint4 kr[2][4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = min(wave * 32 + r + 4 * i, nk - 1);
-    kr[i] = *reinterpret_cast<const uint4 *>(kb + (int64_t)row * a.k_ss + c * 8);
+  for (int i = 0; i < 2; ++i) {
+    const int row = min(wave * 32 + r + 16 * i, nk - 1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      kr[i][j] = *reinterpret_cast<const uint4 *>(kb + (int64_t)row * a.k_ss + (c + 4 * j) * 8);
   }
   {
     const int qi = tid >> 4, qc = tid & 15;
@@ -1125,37 +1128,42 @@ __device__ __forceinline__ void decode_scores_body(const DecodeAttnArgs &a) {
   }
   __syncthreads();
 
-  float qv[REPT][8];
+  float kf[2][4][8];
 #pragma unroll
-  for (int q = 0; q < REPT; ++q) {
-    const float4 lo = *reinterpret_cast<const float4 *>(&qs[q][c * 8]);
-    const float4 hi = *reinterpret_cast<const float4 *>(&qs[q][c * 8 + 4]);
-    qv[q][0] = lo.x; qv[q][1] = lo.y; qv[q][2] = lo.z; qv[q][3] = lo.w;
-    qv[q][4] = hi.x; qv[q][5] = hi.y; qv[q][6] = hi.z; qv[q][7] = hi.w;
-  }
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint4 w = kr[i][j];
+      kf[i][j][0] = __uint_as_float(w.x << 16); kf[i][j][1] = __uint_as_float(w.x & 0xffff0000u);
+      kf[i][j][2] = __uint_as_float(w.y << 16); kf[i][j][3] = __uint_as_float(w.y & 0xffff0000u);
+      kf[i][j][4] = __uint_as_float(w.z << 16); kf[i][j][5] = __uint_as_float(w.z & 0xffff0000u);
+      kf[i][j][6] = __uint_as_float(w.w << 16); kf[i][j][7] = __uint_as_float(w.w & 0xffff0000u);
+    }
   const int64_t row0 = (int64_t)b * a.Hq + g * rep;  // score row of query 0
   float *sc = a.ws + row0 * a.Smax + k0;
   float mloc[REPT];
 #pragma unroll
-  for (int q = 0; q < REPT; ++q) mloc[q] = -INFINITY;
+  for (int q = 0; q < REPT; ++q) {
+    float qv[4][8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int key = wave * 32 + r + 4 * i;
-    float kf[8];
-    kf[0] = __uint_as_float(kr[i].x << 16); kf[1] = __uint_as_float(kr[i].x & 0xffff0000u);
-    kf[2] = __uint_as_float(kr[i].y << 16); kf[3] = __uint_as_float(kr[i].y & 0xffff0000u);
-    kf[4] = __uint_as_float(kr[i].z << 16); kf[5] = __uint_as_float(kr[i].z & 0xffff0000u);
-    kf[6] = __uint_as_float(kr[i].w << 16); kf[7] = __uint_as_float(kr[i].w & 0xffff0000u);
+    for (int j = 0; j < 4; ++j) {
+      const float4 lo = *reinterpret_cast<const float4 *>(&qs[q][(c + 4 * j) * 8]);
+      const float4 hi = *reinterpret_cast<const float4 *>(&qs[q][(c + 4 * j) * 8 + 4]);
+      qv[j][0] = lo.x; qv[j][1] = lo.y; qv[j][2] = lo.z; qv[j][3] = lo.w;
+      qv[j][4] = hi.x; qv[j][5] = hi.y; qv[j][6] = hi.z; qv[j][7] = hi.w;
+    }
+    mloc[q] = -INFINITY;
 #pragma unroll
-    for (int q = 0; q < REPT; ++q) {
+    for (int i = 0; i < 2; ++i) {
+      const int key = wave * 32 + r + 16 * i;
       float d = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) d = fmaf(qv[q][e], kf[e], d);
-      d = d + dpp<0xB1>(d);
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = fmaf(qv[j][e], kf[i][j][e], d);
+      d = d + dpp<0xB1>(d);  // the quad's sum: the same value in its four lanes
       d = d + dpp<0x4E>(d);
-      d = d + dpp<0x124>(d);
-      d = d + dpp<0x128>(d);
-      float s = __shfl(d, lane & ~15);  // lane c = 0's sum
+      float s = d;
       if (a.flags & DEC_RND_PROD) s = bf16r(s);
       s = (a.flags & DEC_DIVIDE) ? s / a.scale : s * a.scale;
       if (a.flags & DEC_RND_SCORE) s = bf16r(s);
@@ -1163,13 +1171,13 @@ __device__ __forceinline__ void decode_scores_body(const DecodeAttnArgs &a) {
       if (key < nk) mloc[q] = fmaxf(mloc[q], s);
     }
   }
-  // the split's max per query: over the four key groups of the wave, then
-  // over the waves
+  // the split's max per query: over the 16 key rows of the wave, then over
+  // the waves
 #pragma unroll
   for (int q = 0; q < REPT; ++q) {
     float m = mloc[q];
-    m = fmaxf(m, __shfl_xor(m, 16, 64));
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
+#pragma unroll
+    for (int off = 4; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
     if (lane == 0) smax[wave][q] = m;
   }
   __syncthreads();
