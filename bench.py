@@ -153,6 +153,7 @@ def _decode_step_bytes(B=QD_B):
 
 MARK_BASE = 1000  # marker grid = MARK_BASE + workload id
 LAUNCH_MARK = 100  # marker grid = MARK_BASE + LAUNCH_MARK + launch index (back-to-back runs)
+END_MARK = 99  # marker grid = MARK_BASE + END_MARK: the workload's labelled dispatches end
 CUS, XCDS = 256, 8  # MI355X
 
 
@@ -195,6 +196,12 @@ class Marker:
         itself: every dispatch up to the next marker is that launch."""
         if self.enabled:
             self.mark(LAUNCH_MARK + i)
+
+    def end(self):
+        """Closes the current workload: dispatches up to the next workload
+        marker are not labelled."""
+        if self.enabled:
+            self.mark(END_MARK)
 
 
 def _time_steps(bounds, steps, warmup, rt):
@@ -719,6 +726,7 @@ def bench_qwen3_decode(a, rt, mk):
     mk.mark(7)
     ms = _time_steps(bounds, steps, warm, rt)
     recs = _kernel_records(7, bounds[0].launches, _time_in_step(bounds, max(20, steps // 2), rt, mk))
+    mk.end()  # the synchronous calls and the other batch sizes below are not labelled
     ins0, outs0 = sets[0]
     sync_us = _sync_call_us(dk, ins0, outs0)
     step_rec = {"label": "step", "kernel": " + ".join(l.symbol for l in bounds[0].launches), "bound": "hbm"}
@@ -798,6 +806,9 @@ def _label_dispatches(rows):
             continue  # runtime copies and fills
         if r["name"] == "nk_copy16" and (r["wgs"] - MARK_BASE) in secs:
             cur, pos, fixed = r["wgs"] - MARK_BASE, 0, None
+            continue
+        if r["name"] == "nk_copy16" and r["wgs"] - MARK_BASE == END_MARK:
+            cur, pos, fixed = None, 0, None
             continue
         if r["name"] == "nk_copy16" and cur is not None and 0 <= r["wgs"] - MARK_BASE - LAUNCH_MARK < 64:
             fixed = r["wgs"] - MARK_BASE - LAUNCH_MARK
