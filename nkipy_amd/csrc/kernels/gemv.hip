@@ -14,15 +14,21 @@
 // fp32 accumulation throughout; fp8 codes are decoded exactly (e4m3 fits in
 // fp32) and scaled in the epilogue, as in the GEMM.
 //
+// Products are v_dot2_f32_bf16 (two bf16 products of a packed pair added
+// to an fp32 accumulator: two multiply-adds per lane-instruction, operands
+// used as stored).
 // NN (B is K x N, row-major, ldb): a workgroup owns 256 columns and one K
 // range.  Thread t: column chunk t / 8 (8 columns), k lane t % 8 (rows
-// k0 + t % 8, + 8, ...); a wave's load of one row step covers 8 rows x 128
-// bytes (bf16) or 64 bytes (fp8).  The 8 k lanes of a chunk are added by a
-// fixed shuffle tree.
+// k0 + t % 8 + 16 j and the row 8 below it, a pair for the dot products);
+// a wave's load of one row step covers 8 rows x 128 bytes (bf16) or 64
+// bytes (fp8).  A's rows of the range sit in LDS already paired the same
+// way (x[k], x[k + 8]).  The 8 k lanes of a chunk are added by a fixed
+// shuffle tree.
 // NT (B is N x K, row-major, ldb): a workgroup owns 4 waves x NT_ROWS rows
 // and one K range; the 64 lanes of a wave take 16-byte chunks of each row
-// in turn (1 KiB contiguous per load), the lanes are added by a fixed
-// shuffle tree.
+// in turn (1 KiB contiguous per load; consecutive k pair up in each 32-bit
+// word, as in A's rows in LDS), the lanes are added by a fixed shuffle
+// tree.
 // A's rows of the K range sit in LDS as bf16 (M x KC <= 8 x 1024).
 // Kernels come for row counts up to MT = 1, 4 and 8 (accumulators sized to
 // MT; _m<MT> in the symbol).
@@ -79,6 +85,49 @@ template <> struct W8<true> {
   }
 };
 
+typedef __bf16 gv_bf16x2 __attribute__((ext_vector_type(2)));
+// acc + lo(x) lo(w) + hi(x) hi(w) on packed bf16 pairs
+__device__ __forceinline__ float dot2(uint32_t x, uint32_t w, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(gv_bf16x2, x), __builtin_bit_cast(gv_bf16x2, w), acc,
+                                         false);
+}
+// 8 bf16 columns of two k rows -> 8 (row lo, row hi) pairs, column order
+__device__ __forceinline__ void pair8(const uint4 &lo, const uint4 &hi, uint32_t (&p)[8]) {
+  const uint32_t l[4] = {lo.x, lo.y, lo.z, lo.w}, h[4] = {hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    p[2 * i] = __builtin_amdgcn_perm(h[i], l[i], 0x05040100u);
+    p[2 * i + 1] = __builtin_amdgcn_perm(h[i], l[i], 0x07060302u);
+  }
+}
+// raw 8 weights -> 8 bf16 (fp8 decoded exactly)
+template <bool FP8>
+__device__ __forceinline__ uint4 w8_bf16(const typename W8<FP8>::raw &w) {
+  if constexpr (FP8) {
+    return e4m3x8_to_bf16x8(w);
+  } else {
+    return w;
+  }
+}
+
+// A's rows m < MT of the K range as the NN kernel's pairs: word q of row m
+// holds (x[k], x[k + 8]), k = k0 + 16 (q / 8) + q % 8; zero past the range
+// (the next range's rows), past K and for rows past M
+template <int MT>
+__device__ __forceinline__ void stage_a_pairs(const GemvArgs &a, uint32_t *xp, int64_t k0, int np) {
+  const int kend = (int)min((int64_t)a.kc, a.K - k0);
+  for (int i = threadIdx.x; i < MT * np; i += 256) {
+    const int m = i / np, q = i % np;
+    const int kl = 16 * (q >> 3) + (q & 7), kh = kl + 8;
+    uint32_t lo = 0, hi = 0;
+    if (m < a.M) {
+      if (kl < kend) lo = a.A[m * a.lda + k0 + kl];
+      if (kh < kend) hi = a.A[m * a.lda + k0 + kh];
+    }
+    xp[m * np + q] = lo | (hi << 16);
+  }
+}
+
 // A's rows m < MT, columns [k0, k0 + kc) into LDS as bf16: zeros past K and
 // for the rows past M, which the kernels then compute with (every
 // accumulator loop has a fixed trip count, so the accumulators stay in
@@ -97,12 +146,13 @@ __device__ __forceinline__ void stage_a(const GemvArgs &a, uint16_t *xs, int64_t
 
 template <bool FP8, bool SWIGLU, int MT>
 __device__ __forceinline__ void gemv_nn_body(const GemvArgs &a) {
-  __shared__ __attribute__((aligned(16))) uint16_t xs[GV_MAX_M * GV_MAX_KC];
+  __shared__ __attribute__((aligned(16))) uint32_t xp[GV_MAX_M * (GV_MAX_KC / 2)];
   const int tid = threadIdx.x;
   const int ks = blockIdx.x % a.ksplit;
   const int64_t n0 = (int64_t)(blockIdx.x / a.ksplit) * 256;
   const int64_t k0 = (int64_t)ks * a.kc;
-  stage_a<MT>(a, xs, k0);
+  const int np = ((a.kc + 15) >> 4) * 8;  // pairs per row of the range
+  stage_a_pairs<MT>(a, xp, k0, np);
   __syncthreads();
 
   const int cc = tid >> 3, kl = tid & 7;
@@ -118,7 +168,8 @@ __device__ __forceinline__ void gemv_nn_body(const GemvArgs &a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[w][m][e] = 0.f;
   const int kend = (int)min((int64_t)a.kc, a.K - k0);
-  // rows kl, kl + 8, ... of the range, two in flight
+  // pair j of this lane: rows kl + 16 j and kl + 16 j + 8 of the range (the
+  // second zero past the range end)
   for (int kk = kl; kk < kend; kk += 16) {
     const bool two = kk + 8 < kend;
     const int64_t r0 = k0 + kk, r1 = two ? r0 + 8 : r0;
@@ -129,21 +180,24 @@ __device__ __forceinline__ void gemv_nn_body(const GemvArgs &a) {
       b1[0] = W8<FP8>::load(a.B1, r0 * a.ldb + colc);
       b1[1] = W8<FP8>::load(a.B1, r1 * a.ldb + colc);
     }
+    const int q = (kk >> 4) * 8 + kl;
+    uint32_t wp[8], up[8];
+    {
+      const uint4 z = make_uint4(0, 0, 0, 0);
+      const uint4 hi = w8_bf16<FP8>(b0[1]);
+      pair8(w8_bf16<FP8>(b0[0]), two ? hi : z, wp);
+      if constexpr (SWIGLU) {
+        const uint4 hu = w8_bf16<FP8>(b1[1]);
+        pair8(w8_bf16<FP8>(b1[0]), two ? hu : z, up);
+      }
+    }
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      if (h == 1 && !two) break;
-      const int kr = kk + 8 * h;
-      float f[8], fu[8];
-      W8<FP8>::decode(b0[h], f);
-      if constexpr (SWIGLU) W8<FP8>::decode(b1[h], fu);
+    for (int m = 0; m < MT; ++m) {
+      const uint32_t x2 = xp[m * np + q];
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        const float xv = bf16_to_f32(xs[m * a.kc + kr]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          acc[0][m][e] = fmaf(xv, f[e], acc[0][m][e]);
-          if constexpr (SWIGLU) acc[1][m][e] = fmaf(xv, fu[e], acc[1][m][e]);
-        }
+      for (int e = 0; e < 8; ++e) {
+        acc[0][m][e] = dot2(x2, wp[e], acc[0][m][e]);
+        if constexpr (SWIGLU) acc[1][m][e] = dot2(x2, up[e], acc[1][m][e]);
       }
     }
   }
@@ -210,32 +264,32 @@ __device__ __forceinline__ void gemv_nt_body(const GemvArgs &a) {
     }
 #pragma unroll
     for (int h = 0; h < CK / 8; ++h) {
-      float xv[MT][8];
+      uint4 xw[MT];
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        const uint4 xw = *reinterpret_cast<const uint4 *>(xs + m * a.kc + kk + 8 * h);
-        W8<false>::decode(xw, xv[m]);
-      }
+      for (int m = 0; m < MT; ++m) xw[m] = *reinterpret_cast<const uint4 *>(xs + m * a.kc + kk + 8 * h);
 #pragma unroll
       for (int r = 0; r < NT_ROWS; ++r) {
-        float f[8], fu[8];
+        uint4 f, fu;
         if constexpr (FP8) {
-          const uint2 half = h ? make_uint2(raw0[r].z, raw0[r].w) : make_uint2(raw0[r].x, raw0[r].y);
-          W8<true>::decode(half, f);
-          if constexpr (SWIGLU) {
-            const uint2 hu = h ? make_uint2(raw1[r].z, raw1[r].w) : make_uint2(raw1[r].x, raw1[r].y);
-            W8<true>::decode(hu, fu);
-          }
+          f = e4m3x8_to_bf16x8(h ? make_uint2(raw0[r].z, raw0[r].w) : make_uint2(raw0[r].x, raw0[r].y));
+          if constexpr (SWIGLU)
+            fu = e4m3x8_to_bf16x8(h ? make_uint2(raw1[r].z, raw1[r].w) : make_uint2(raw1[r].x, raw1[r].y));
         } else {
-          W8<false>::decode(raw0[r], f);
-          if constexpr (SWIGLU) W8<false>::decode(raw1[r], fu);
+          f = raw0[r];
+          if constexpr (SWIGLU) fu = raw1[r];
         }
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            acc[0][m][r] = fmaf(xv[m][e], f[e], acc[0][m][r]);
-            if constexpr (SWIGLU) acc[1][m][r] = fmaf(xv[m][e], fu[e], acc[1][m][r]);
+          // consecutive k pair up in each word of both operands
+          acc[0][m][r] = dot2(xw[m].x, f.x, acc[0][m][r]);
+          acc[0][m][r] = dot2(xw[m].y, f.y, acc[0][m][r]);
+          acc[0][m][r] = dot2(xw[m].z, f.z, acc[0][m][r]);
+          acc[0][m][r] = dot2(xw[m].w, f.w, acc[0][m][r]);
+          if constexpr (SWIGLU) {
+            acc[1][m][r] = dot2(xw[m].x, fu.x, acc[1][m][r]);
+            acc[1][m][r] = dot2(xw[m].y, fu.y, acc[1][m][r]);
+            acc[1][m][r] = dot2(xw[m].z, fu.z, acc[1][m][r]);
+            acc[1][m][r] = dot2(xw[m].w, fu.w, acc[1][m][r]);
           }
         }
       }
