@@ -1196,23 +1196,27 @@ extern "C" __global__ __launch_bounds__(256) void nk_decode_rowstat_d128(DecodeA
   const bool rnd = (a.flags & DEC_SOFTMAX_BF16) != 0;
   const float *sc = a.ws + row * a.Smax;
   const float *mx = a.ws + (int64_t)a.B * a.Hq * a.Smax + row * a.nsplit;
-  constexpr int U = 8;  // loads of a batch first (one latency a batch)
+  constexpr int U = 16;  // loads of a batch first: one latency for 4096 keys
+  // the first batch of scores is loaded with the split maxima (it does not
+  // depend on the max); the maxima are shared out over the threads, then
+  // the workgroup's max
+  float x[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) x[u] = sc[min(u * 256 + tid, L - 1)];
+  __shared__ float mred[4];
   float m = -INFINITY;
-  for (int i0 = 0; i0 < nsp; i0 += U) {
-    float x[U];
+  for (int i = tid; i < nsp; i += 256) m = fmaxf(m, mx[i]);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const float y = mx[min(i0 + u, nsp - 1)];  // (in range: the max is unchanged)
-      x[u] = y;
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) m = fmaxf(m, x[u]);
-  }
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if (lane == 0) mred[wave] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(mred[0], mred[1]), fmaxf(mred[2], mred[3]));
   float sum = 0.f;
   for (int j0 = 0; j0 < L; j0 += 256 * U) {
-    float x[U];
+    if (j0 > 0) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) x[u] = sc[min(j0 + u * 256 + tid, L - 1)];
+      for (int u = 0; u < U; ++u) x[u] = sc[min(j0 + u * 256 + tid, L - 1)];
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (j0 + u * 256 + tid < L) {
@@ -1368,12 +1372,12 @@ extern "C" __global__ __launch_bounds__(128) void nk_decode_combine_d128(DecodeA
   const int nsp = (decode_keys(a) + DKS - 1) / DKS;
   const float *op = a.ws + (int64_t)a.B * a.Hq * (a.Smax + a.nsplit) + row * a.nsplit * AD + d;
   float o = 0.f;
-  for (int i0 = 0; i0 < nsp; i0 += 8) {  // loads of a batch first, added in split order
-    float x[8];
+  for (int i0 = 0; i0 < nsp; i0 += 32) {  // loads of a batch first (32 splits: 4096 keys), added in split order
+    float x[32];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) x[u] = op[(int64_t)min(i0 + u, nsp - 1) * AD];
+    for (int u = 0; u < 32; ++u) x[u] = op[(int64_t)min(i0 + u, nsp - 1) * AD];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < 32; ++u)
       if (i0 + u < nsp) o += x[u];
   }
   a.o[(int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d] = f32_to_bf16(o);
