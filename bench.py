@@ -122,13 +122,14 @@ def _decode_launches():
     """Bytes each launch of the Qwen3 decode step moves (its inputs and
     outputs as this decomposition has them: partial sums of the K-range
     projections, the fp32 scores and split outputs of the attention)."""
-    from nkipy_amd.dispatch.launchers import gemm_splitk_split
+    from nkipy_amd.dispatch.launchers import gemv_mfma_preferred, gemv_mfma_split
 
     B, H, Hkv, D, hid = QD_B, QD_HQ, QD_HKV, DEC_D, QD_HID
     L, nqkv = QD_POS + 1, (QD_HQ + 2 * QD_HKV) * DEC_D
     nsp = -(-L // 128)
-    ks1, _ = gemm_splitk_split(B, nqkv, hid)
-    ks2, _ = gemm_splitk_split(B, hid, H * D)
+    assert gemv_mfma_preferred(B, nqkv, hid) and gemv_mfma_preferred(B, hid, H * D)
+    ks1, _ = gemv_mfma_split(B, nqkv, hid)
+    ks2, _ = gemv_mfma_split(B, hid, H * D)
     kv = 2 * B * L * Hkv * D
     return [("qkv_partials", "hbm", 2 * hid * nqkv + 2 * B * hid + 4 * ks1 * B * nqkv),
             ("qkv_reduce", "hbm", 4 * ks1 * B * nqkv + 2 * B * nqkv),

@@ -42,7 +42,6 @@ typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-typedef __attribute__((address_space(3))) void lds_void;
 
 #define AD 128  // head dim
 
@@ -408,28 +407,6 @@ template <int N> struct SlotTag {
   static constexpr int value = N;
 };
 
-// LDS DMA issued from inline asm: the compiler does not model it, so it adds
-// no waits of its own before the reads of other ring slots (its alias
-// analysis cannot separate slots of one array); every wait is explicit.
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ i32x4_t rsrc_words(const void *p, int64_t bytes) {
-  const uint64_t ad = (uint64_t)p;
-  i32x4_t r;
-  r[0] = (int)(uint32_t)ad;
-  r[1] = (int)(uint32_t)(ad >> 32) & 0xffff;
-  r[2] = (int)bytes;
-  r[3] = 0x00020000;  // raw, untyped
-  return r;
-}
-// LDS byte address of a shared-memory array
-__device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) { return (uint32_t)(uintptr_t)(lds_void *)p; }
-// lane l of the wave fills LDS byte address lds + 16 l from byte offset off
-// of the resource
-__device__ __forceinline__ void dma16_asm(i32x4_t r, uint32_t lds, uint32_t off) {
-  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :: "v"(off), "s"(r), "s"(m) : "memory", "m0");
-}
 
 // the score cast points of the flags (uniform branches: every lane takes the
 // same ones; the quotient of a finite score needs no infinity fallback in

@@ -255,6 +255,35 @@ NK_DEVICE void buf_st16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(q, r, off, 0, NT ? 2 : 0);
 }
 
+// ---------------------------------------------------------------------------
+// LDS DMA (buffer_load_dwordx4 ... lds) issued as inline asm.  The compiler's
+// wait insertion does not model it, so it adds no waits of its own for it
+// (its alias analysis cannot separate the slots of one LDS array): every
+// wait on a move is explicit in the kernel that issues it.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void;
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+// buffer resource words over `bytes` bytes at p (raw, untyped): a move past
+// the end fills its 16 bytes with zeros and reads no memory
+NK_DEVICE i32x4_t rsrc_words(const void *p, int64_t bytes) {
+  const uint64_t ad = (uint64_t)p;
+  i32x4_t r;
+  r[0] = (int)(uint32_t)ad;
+  r[1] = (int)(uint32_t)(ad >> 32) & 0xffff;
+  r[2] = (int)bytes;
+  r[3] = 0x00020000;
+  return r;
+}
+// LDS byte address of a shared-memory array
+NK_DEVICE uint32_t lds_addr(const uint8_t *p) { return (uint32_t)(uintptr_t)(lds_void *)p; }
+// lane l of the wave fills LDS byte address lds + 16 l (lds wave-uniform)
+// from byte offset off of the resource
+NK_DEVICE void dma16_asm(i32x4_t r, uint32_t lds, uint32_t off) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :: "v"(off), "s"(r), "s"(m) : "memory", "m0");
+}
+
 // Raw form of an 8-element chunk: U 16-byte words (1 for 2-byte types, 2 for
 // fp32).  Kernels issue every raw load of a row first, then decode, so all
 // of a thread's HBM requests are in flight together.

@@ -155,7 +155,6 @@ __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >>
 #define OOB 0x80000000u
 #define BUF_WORD3 0x00020000  // gfx9 buffer resource word 3 (raw, untyped)
 
-typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, BUF_WORD3);
@@ -1153,29 +1152,7 @@ __device__ __forceinline__ void gemm_epilogue_rope_lds(const GemmArgs &a, const 
   }
 }
 
-// LDS DMA issued as inline asm: the compiler's wait insertion does not model
-// it, so it adds no waits of its own for it; every ordering is explicit
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ i32x4_t rsrc_words(const void *p, int64_t bytes) {
-  const uint64_t a = (uint64_t)p;
-  i32x4_t r;
-  r[0] = (int)(uint32_t)a;
-  r[1] = (int)(uint32_t)(a >> 32) & 0xffff;
-  r[2] = (int)bytes;
-  r[3] = BUF_WORD3;
-  return r;
-}
-// LDS byte address of a shared-memory pointer
-__device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) { return (uint32_t)(uintptr_t)(lds_void *)p; }
-// lds: wave-uniform LDS byte address of the 1 KiB block (lane l fills
-// lds + 16 l)
-__device__ __forceinline__ void dma16_asm(i32x4_t r, uint32_t lds, uint32_t off) {
-  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :: "v"(off), "s"(r), "s"(m) : "memory", "m0");
-}
-
-// the same move with a uniform (SGPR) part of the offset: voff + soff
+// LDS DMA as in dma16_asm, with a uniform (SGPR) part of the offset: voff + soff
 __device__ __forceinline__ void dma16_asm_so(i32x4_t r, uint32_t lds, uint32_t voff, uint32_t soff) {
   const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
   const uint32_t so = __builtin_amdgcn_readfirstlane(soff);

@@ -398,3 +398,154 @@ extern "C" __global__ __launch_bounds__(256) void nk_gemv_out_f32(GemvArgs a) { 
 extern "C" __global__ __launch_bounds__(256) void nk_gemv_out_bf16_swiglu(GemvArgs a) {
   gemv_out_body<bf16, true>(a);
 }
+
+// ---------------------------------------------------------------------------
+// MFMA form of the NN partial sums (bf16 K x N weights) for up to 16 MT rows.
+// The VALU kernel above spends a multiply-add per row on every weight; here
+// the rows ride on 16x16x32 MFMAs (A: 16 rows x 32 k, zero rows past M) and
+// the weights are streamed once:
+//  * a workgroup (4 waves) owns 256 columns and one K range of kc (a
+//    multiple of 32, at most GK_MAX_KC / MT); wave w owns columns 64 w..64 w + 63
+//    (four 16-column tiles);
+//  * the weights of the range move global -> LDS by DMA in stages of 32 k
+//    rows x 256 columns (16 KiB: two column halves [32 k][128 n] of 256-byte
+//    rows, 16-byte chunk c of row k at slot c ^ ((k & 3) << 2)) through a
+//    ring of three slots, two stages ahead of the one read (two workgroups
+//    fit a CU);
+//    B fragments come out transposed (ds_read_b64_tr_b16: lane (g, i) reads
+//    k rows 8 g + 4 s + i / 4 at columns c + 4 (i % 4), and receives k
+//    8 g + 4 s .. + 3 of column c + i);
+//  * A's rows of the range move into LDS by DMA once, rows of kc + 8
+//    elements (an odd number of 16-byte chunks, so the 16 rows of a fragment
+//    read fall on 16 distinct bank groups), zeros past M and past the range.
+// Rows past the range end, and columns past N, are moves out of the
+// resource's range: zeros, no memory read.  The partial sums go to the
+// workspace as in nk_gemv_nn_*: P[split][m][n], rows m < M.
+// ---------------------------------------------------------------------------
+#define GK_MAX_KC 512
+
+typedef short gk_s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) gk_s16x4 gk_lds_s16x4;
+typedef __bf16 gk_bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 gk_bf16x4 __attribute__((ext_vector_type(4)));
+typedef float gk_f32x4 __attribute__((ext_vector_type(4)));
+
+template <int MT>
+__device__ __forceinline__ void gemv_mfma_nn_body(const GemvArgs &a) {
+  constexpr int GK_STAGES = 3;
+  constexpr int SB = 32 * 256 * 2;                                       // one stage
+  constexpr int AB = ((16 * MT * (GK_MAX_KC / MT + 8) * 2 + 1023) / 1024) * 1024;  // A rows, whole 1 KiB moves
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[GK_STAGES * SB];
+  __shared__ __attribute__((aligned(1024))) uint8_t as[AB];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int ks = blockIdx.x % a.ksplit;
+  const int64_t n0 = (int64_t)(blockIdx.x / a.ksplit) * 256;
+  const int64_t k0 = (int64_t)ks * a.kc;
+  const int kend = (int)min((int64_t)a.kc, a.K - k0);  // a multiple of 8
+  const int nst = (kend + 31) >> 5;                    // stages of this range
+  const int cpr = a.kc >> 3;                           // 16-byte chunks per A row
+
+  // A: slot s of the row-padded layout holds row s / (cpr + 1), chunk
+  // s % (cpr + 1) (the last chunk of a row is padding)
+  {
+    const i32x4_t ra = rsrc_words(a.A, a.M * a.lda * 2);
+    const int nslot = 16 * MT * (cpr + 1);
+    for (int j = wave; j * 64 < nslot; j += 4) {
+      const int s = j * 64 + lane;
+      const int r = s / (cpr + 1), c = s % (cpr + 1);
+      const bool in = s < nslot && c < cpr && 8 * c < kend && r < a.M;
+      dma16_asm(ra, lds_addr(as) + j * 1024, in ? (uint32_t)((r * a.lda + k0 + 8 * c) * 2) : 0x80000000u);
+    }
+  }
+  // B stage t into ring slot t % GK_STAGES: block b = wave + 4 j (j < 4)
+  // covers k rows 4 (b % 8) + lane / 16 of column half b / 8
+  const i32x4_t rb = rsrc_words(reinterpret_cast<const uint16_t *>(a.B0) + k0 * a.ldb, (int64_t)kend * a.ldb * 2);
+  uint32_t boff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int b = wave + 4 * j;
+    const int kr = 4 * (b & 7) + g4;
+    const int lc = l16 ^ ((kr & 3) << 2);
+    const int64_t col = n0 + 128 * (b >> 3) + 8 * lc;
+    boff[j] = col < a.N ? (uint32_t)((kr * a.ldb + col) * 2) : 0x80000000u;
+  }
+  const uint32_t tstep = (uint32_t)(32 * a.ldb * 2);
+  auto stage = [&](int t) __attribute__((always_inline)) {
+    const uint32_t base = lds_addr(ring) + (t % GK_STAGES) * SB;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int b = wave + 4 * j;
+      // stages past the range read nothing (every offset out of range)
+      dma16_asm(rb, base + b * 1024, t < nst && boff[j] != 0x80000000u ? boff[j] + t * tstep : 0x80000000u);
+    }
+  };
+#pragma unroll
+  for (int t = 0; t < GK_STAGES - 1; ++t) stage(t);
+
+  // fragment offsets: B tile jt of this wave (columns 64 wave + 16 jt), A
+  // tile mt (rows 16 mt + l16, chunk g4 of the stage's four)
+  uint32_t bfo[4];
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt) {
+    const int br = 64 * wave + 16 * jt;
+    const int nl = (br & 127) + 4 * (l16 & 3);
+    const int k = 8 * g4 + (l16 >> 2);
+    bfo[jt] = (br >> 7) * 8192 + k * 256 + (((nl >> 3) ^ ((k & 3) << 2)) << 4) + (nl & 7) * 2;
+  }
+  const uint32_t afo = (uint32_t)((l16 * (cpr + 1) + g4) * 16);
+
+  gk_f32x4 acc[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[mt][jt][r] = 0.f;
+  for (int t = 0; t < nst; ++t) {
+    // stage t (and A) landed for this wave: only the GK_STAGES - 2 later
+    // stages' moves may be outstanding; the barrier then covers every
+    // wave's moves and every wave's reads of the slot refilled next
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (4 * (GK_STAGES - 2)));
+    lds_barrier();
+    stage(t + GK_STAGES - 1);
+    const uint8_t *S = ring + (t % GK_STAGES) * SB;
+    gk_bf16x8 bf[4], af[MT];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      const gk_s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((gk_lds_s16x4 *)(S + bfo[jt]));
+      const gk_s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((gk_lds_s16x4 *)(S + bfo[jt] + 4 * 256));
+      bf[jt] = __builtin_shufflevector(__builtin_bit_cast(gk_bf16x4, v0), __builtin_bit_cast(gk_bf16x4, v1), 0, 1,
+                                       2, 3, 4, 5, 6, 7);
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      af[mt] = *reinterpret_cast<const gk_bf16x8 *>(as + afo + (16 * mt * (cpr + 1) + 4 * t) * 16);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+        acc[mt][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bf[jt], acc[mt][jt], 0, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no move outlives the workgroup
+
+  // D rows 16 mt + 4 g4 + r, column 64 wave + 16 jt + l16
+  float *P = a.ws + (int64_t)ks * a.M * a.N;
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt) {
+    const int64_t n = n0 + 64 * wave + 16 * jt + l16;
+    if (n < a.N) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = 16 * mt + 4 * g4 + r;
+          if (m < a.M) P[m * a.N + n] = acc[mt][jt][r];
+        }
+    }
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void nk_gemv_mfma_nn_bf16_t1(GemvArgs a) { gemv_mfma_nn_body<1>(a); }
+extern "C" __global__ __launch_bounds__(256) void nk_gemv_mfma_nn_bf16_t2(GemvArgs a) { gemv_mfma_nn_body<2>(a); }

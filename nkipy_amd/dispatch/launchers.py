@@ -612,6 +612,87 @@ def gemv(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, layout: 
                    bytes=4 * ks * M * N * n_mm + M * N * c_dtype.itemsize)]
 
 
+GEMV_MFMA_MAX_M = 32
+GEMV_MFMA_MAX_KC = 512  # A's rows of the range in LDS: 16 x 512 or 32 x 256
+_GEMV_MFMA_TARGET_WGS = 512
+
+
+def gemv_mfma_split(M: int, N: int, K: int):
+    """(ksplit, kc) of :func:`gemv_mfma`: K ranges of 256 while the grid of
+    N / 256 x ksplit workgroups stays within one round of 512 (two per CU),
+    else the shortest range (a multiple of 32, at most 512 for 16 rows, 256
+    for 32) that keeps it there.  Measured with cold weights: a second
+    round of workgroups costs more than longer ranges do."""
+    tiles = -(-N // 256)
+    kmax = GEMV_MFMA_MAX_KC if M <= 16 else GEMV_MFMA_MAX_KC // 2
+    kc = 256
+    ks = -(-K // kc)
+    if tiles * ks > _GEMV_MFMA_TARGET_WGS:
+        ks = max(1, _GEMV_MFMA_TARGET_WGS // tiles)
+        kc = min(kmax, -(-(-(-K // ks)) // 32) * 32)
+        ks = -(-K // kc)
+    return ks, kc
+
+
+def gemv_mfma_preferred(M: int, N: int, K: int) -> bool:
+    """Whether :func:`gemv_mfma` is the form for M rows of bf16 NN weights
+    (measured with cold weights at 4096 / 6144 / 24576 x 4096 and 4096 x
+    14336 against the VALU form and the MFMA GEMM over K ranges): up to 16
+    rows always (at one row it ties the VALU form), 32 rows while ranges of
+    256 keep the grid within one round of workgroups."""
+    if M <= 16:
+        return M > 0
+    return M <= GEMV_MFMA_MAX_M and -(-N // 256) * -(-K // 256) <= _GEMV_MFMA_TARGET_WGS
+
+
+def gemv_mfma_workspace_bytes(M: int, N: int, K: int) -> int:
+    ks, _ = gemv_mfma_split(M, N, K)
+    return 4 * ks * M * N
+
+
+def gemv_mfma(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, c_dtype, ws_ptr: int,
+              lda: int = None, ldb: int = None, ldc: int = None, bias_ptr: int = 0, resid_ptr: int = 0,
+              round_before_bias: bool = False, round_before_resid: bool = False) -> List[Launch]:
+    """The operation of :func:`gemv` for bf16 NN weights (K x N) and up to 32
+    rows, with the products on MFMA (16-row tiles): partial sums over K
+    ranges into the workspace at ``ws_ptr`` (``gemv_mfma_workspace_bytes``),
+    then the reduction of :func:`gemv` (ranges added in order, then the
+    epilogue).  Two launches."""
+    c_dtype = dt.canonical(c_dtype)
+    if c_dtype not in (dt.bfloat16, dt.float32):
+        raise LaunchError(f"GEMM output must be bf16 or float32, got {dt.name(c_dtype)}")
+    if not (0 < M <= GEMV_MFMA_MAX_M) or N <= 0 or K <= 0:
+        raise LaunchError(f"the MFMA projection takes 1..{GEMV_MFMA_MAX_M} rows, got M={M} N={N} K={K}")
+    lda = K if lda is None else lda
+    ldb = N if ldb is None else ldb
+    ldc = N if ldc is None else ldc
+    if K % 8 or lda % 8 or ldb % 8 or N % 8:
+        raise LaunchError("the MFMA projection needs K, N, lda and ldb to be multiples of 8 (16-byte rows)")
+    if lda < K or ldb < N or ldc < N:
+        raise LaunchError("GEMM leading dimension smaller than the matrix")
+    for p, al in ((a_ptr, 16), (b_ptr, 16), (ws_ptr, 16)):
+        if not p or p % al:
+            raise LaunchError("GEMM operand, weight and workspace pointers must be 16-byte aligned")
+    ks, kc = gemv_mfma_split(M, N, K)
+    if kc % 32 or kc > GEMV_MFMA_MAX_KC // (1 if M <= 16 else 2):
+        raise LaunchError(f"K range of {kc} does not fit the MFMA projection")
+    if kc * ldb * 2 >= 2**31 or M * lda * 2 >= 2**31 or M * N >= 2**31:
+        raise LaunchError("the MFMA projection addresses a K range's weights with 32-bit offsets")
+    flags = (GEMM_BIAS if bias_ptr else 0) | (GEMM_RESID if resid_ptr else 0)
+    if round_before_bias and bias_ptr:
+        flags |= GEMM_RND_BIAS
+    if round_before_resid and resid_ptr:
+        flags |= GEMM_RND_RESID
+    args = GemvArgs(a_ptr, b_ptr, None, c_ptr, bias_ptr or None, None, None, resid_ptr or None, ws_ptr,
+                    M, N, K, lda, ldb, ldc, ks, kc, flags, 0)
+    tiles = 1 if M <= 16 else 2
+    ctag = "bf16" if c_dtype == dt.bfloat16 else "f32"
+    return [Launch("gemv", f"nk_gemv_mfma_nn_bf16_t{tiles}", (-(-N // 256) * ks, 1, 1), (256, 1, 1), args,
+                   bytes=M * K * 2 + N * K * 2 + 4 * ks * M * N, flops=2 * M * N * K),
+            Launch("gemv", f"nk_gemv_out_{ctag}", (-(-M * N // 64), 1, 1), (256, 1, 1), args,
+                   bytes=4 * ks * M * N + M * N * c_dtype.itemsize)]
+
+
 class HeadRopeTarget(ctypes.Structure):
     _fields_ = [("x", ctypes.c_void_p), ("out", ctypes.c_void_p), ("w", ctypes.c_void_p)] + \
         [(f"{t}_{s}", ctypes.c_int64) for t in "xo" for s in ("sb", "ss", "sh")] + \

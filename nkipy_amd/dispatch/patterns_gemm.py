@@ -172,12 +172,18 @@ class GemmMatch(Match):
         # (a decode batch): the MFMA kernels over K ranges, so that the
         # grid fills the part
         fp8 = w.value.dtype == dt.float8_e4m3fn
-        small = LA.gemv_preferred(M, w.layout, fp8)
-        splitk = (self.split_k and not small and not (fp8 and w.layout == "nn")
+        # bf16 NN weights of a projection up to 16-32 rows: the MFMA form of
+        # the few-row kernels (16-row tiles, weights streamed once)
+        mfma = (self.split_k and w.layout == "nn" and not fp8 and up is None
+                and LA.gemv_mfma_preferred(M, N, K))
+        small = not mfma and LA.gemv_preferred(M, w.layout, fp8)
+        splitk = (self.split_k and not mfma and not small and not (fp8 and w.layout == "nn")
                   and LA.gemm_splitk_useful(M, N, K, up is not None, fp8))
-        small = small or (M <= LA.GEMV_MAX_M and not splitk)
+        small = small or (not mfma and M <= LA.GEMV_MAX_M and not splitk)
         ws = None
-        if small:
+        if mfma:
+            ws = Slot(plan.add_buffer(LA.gemv_mfma_workspace_bytes(M, N, K), "temp", "gemv.partials"))
+        elif small:
             ws = Slot(plan.add_buffer(LA.gemv_workspace_bytes(M, N, K, w.layout, fp8, up is not None), "temp",
                                       "gemv.partials"))
         elif splitk:
@@ -190,6 +196,11 @@ class GemmMatch(Match):
             if up is not None:
                 up_ptr = addr(up.value) + off * up.value.dtype.itemsize
                 up_scale = addr(up.scale) if up.scale is not None else 0
+            if mfma:
+                return LA.gemv_mfma(addr(x), addr(w.value), addr(out), M, N, K, c_dtype=out.dtype, ldb=ldb,
+                                    ws_ptr=addr(ws), bias_ptr=addr(bias) if bias is not None else 0,
+                                    resid_ptr=addr(resid) if resid is not None else 0,
+                                    round_before_bias=rnd_bias, round_before_resid=rnd_resid)
             if small:
                 return LA.gemv(addr(x), addr(w.value), addr(out), M, N, K, layout=w.layout,
                                b_dtype=w.value.dtype, c_dtype=out.dtype, ldb=ldb, ws_ptr=addr(ws),

@@ -1,8 +1,9 @@
-"""GPU parity of the split-K projection kernels (M <= 8 rows, the decode
-case) against NumPy float64 matmul on the same bf16 / fp8 values, across
-layouts, row counts, N and K tails and the GEMM's epilogues; and against the
-MFMA GEMM on the same operands; and the lowering of a decode-shaped
-projection onto them."""
+"""GPU parity of the few-row projection kernels (the decode case: the VALU
+form up to 8 rows, the MFMA form up to 32 rows of bf16 K x N weights, the
+MFMA GEMM over K ranges) against NumPy float64 matmul on the same bf16 /
+fp8 values, across layouts, row counts, N and K tails and the GEMM's
+epilogues; against each other on the same operands; and the lowering of
+decode-shaped projections onto them."""
 
 import os
 
@@ -135,24 +136,94 @@ def test_gemv_against_mfma_gemm(gpu, layout, fp8):
     np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-5 * np.abs(b).max())
 
 
-def test_decode_projection_lowers_to_gemv(gpu):
-    """A traced decode-shaped projection (x (1, 1, 4096) @ W (4096, 6144),
-    bf16) lowers to the split-K kernels and matches float64."""
+@pytest.mark.parametrize("layout,symbol", [("nn", "nk_gemv_mfma_nn_bf16_t1"), ("nt", "nk_gemv_nt_bf16_m1")])
+def test_decode_projection_lowers_to_gemv(gpu, layout, symbol):
+    """A traced decode-shaped projection (x (1, 1, 4096) @ W, W (4096, 6144)
+    or W^T with W (6144, 4096), bf16) lowers to the few-row kernels (bf16
+    K x N weights: the MFMA form) and matches float64."""
     from nkipy_amd.runtime import DeviceKernel, baremetal_jit
 
-    def proj(x, w):
+    def proj_nn(x, w):
         return np.matmul(x, w)
 
+    def proj_nt(x, w):
+        return np.matmul(x, w.T)
+
+    proj = proj_nn if layout == "nn" else proj_nt
     rng = np.random.default_rng(3)
     x = N.bf16_round(rng.standard_normal((1, 1, 4096)))
-    w = N.bf16_round(rng.standard_normal((4096, 6144)) * 0.02)
+    w = N.bf16_round(rng.standard_normal((4096, 6144) if layout == "nn" else (6144, 4096)) * 0.02)
     args = [dt.to_bf16(a) for a in (x, w)]
     dk = DeviceKernel.compile_and_load(proj, *args)
     assert dk.plan.kernel_kinds == ["gemm"]
     (step,) = dk.plan.steps
-    assert [l.symbol for l in step.launches(lambda v: 1 << 40)] == ["nk_gemv_nn_bf16_m1", "nk_gemv_out_bf16"]
+    assert [l.symbol for l in step.launches(lambda v: 1 << 40)] == [symbol, "nk_gemv_out_bf16"]
     got = dt.to_float32(baremetal_jit(proj)(*args))
-    _close(got, x.astype(np.float64) @ w.astype(np.float64), axis=-1)
+    wm = w.astype(np.float64) if layout == "nn" else w.astype(np.float64).T
+    _close(got, x.astype(np.float64) @ wm, axis=-1)
+
+
+# ---------------------------------------------------------------------------
+# The MFMA form of the few-row projection (bf16 K x N weights, M <= 32)
+# ---------------------------------------------------------------------------
+MFMA_CASES = [  # (M, N, K, ldb): 16-row tiles full / partial / two, N and K tails, strided weights
+    (1, 6144, 4096, None), (5, 264, 1000, None), (8, 4096, 14336, None), (13, 1000, 328, 1008),
+    (16, 2048, 4104, None), (17, 520, 2056, None), (32, 4096, 4096, 4104), (2, 24576, 520, None),
+]
+
+
+@pytest.mark.parametrize("M,Nn,Kk,ldb", MFMA_CASES)
+@pytest.mark.parametrize("epi", ["plain", "f32", "bias_resid", "rounded"])
+def test_gemv_mfma_matches_float64(gpu, M, Nn, Kk, ldb, epi):
+    rng = np.random.default_rng(M * 11 + Nn + Kk)
+    ks, kc = LA.gemv_mfma_split(M, Nn, Kk)
+    print(f"gemv_mfma M={M} N={Nn} K={Kk} ldb={ldb} {epi} split={ks}x{kc}", flush=True)
+    x = N.bf16_round(rng.standard_normal((M, Kk)))
+    ld = Nn if ldb is None else ldb
+    wfull = N.bf16_round(rng.standard_normal((Kk, ld)) * 0.05)
+    wmat = wfull[:, :Nn].astype(np.float64)
+    prod = x.astype(np.float64) @ wmat
+    bias = N.bf16_round(rng.standard_normal(Nn) * 0.1)
+    res = N.bf16_round(rng.standard_normal((M, Nn)))
+    out = dt.float32 if epi == "f32" else dt.bfloat16
+    kw = {}
+    ref = prod
+    t = {"x": DeviceTensor.from_numpy(dt.to_bf16(x)), "w": DeviceTensor.from_numpy(dt.to_bf16(wfull))}
+    if epi in ("bias_resid", "rounded"):
+        t["b"] = DeviceTensor.from_numpy(dt.to_bf16(bias))
+        t["r"] = DeviceTensor.from_numpy(dt.to_bf16(res))
+        kw.update(bias_ptr=t["b"].ptr, resid_ptr=t["r"].ptr)
+        if epi == "rounded":
+            kw.update(round_before_bias=True, round_before_resid=True)
+            ref = N.bf16_round(N.bf16_round(prod) + bias) + res
+        else:
+            ref = prod + bias + res
+    c = DeviceTensor.empty((M, Nn), out)
+    ws = DeviceTensor.empty((LA.gemv_mfma_workspace_bytes(M, Nn, Kk),), dt.uint8)
+    _run(gpu, LA.gemv_mfma(t["x"].ptr, t["w"].ptr, c.ptr, M, Nn, Kk, c_dtype=out, ws_ptr=ws.ptr, ldb=ld, **kw))
+    got = c.numpy() if out == dt.float32 else dt.to_float32(c.numpy())
+    if out == dt.float32:
+        np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
+    else:
+        _close(got, ref, axis=-1, rounded=N.bf16_round(prod) if epi == "rounded" else None)
+
+
+def test_gemv_mfma_against_valu_form(gpu):
+    """The same operands through the MFMA and the VALU few-row kernels: fp32
+    results within the difference of two summation orders."""
+    M, Nn, Kk = 8, 4096, 4096
+    rng = np.random.default_rng(6)
+    x = N.bf16_round(rng.standard_normal((M, Kk)))
+    w = N.bf16_round(rng.standard_normal((Kk, Nn)) * 0.05)
+    t = [DeviceTensor.from_numpy(dt.to_bf16(v)) for v in (x, w)]
+    c1, c2 = DeviceTensor.empty((M, Nn), dt.float32), DeviceTensor.empty((M, Nn), dt.float32)
+    w1 = DeviceTensor.empty((LA.gemv_mfma_workspace_bytes(M, Nn, Kk),), dt.uint8)
+    w2 = DeviceTensor.empty((LA.gemv_workspace_bytes(M, Nn, Kk, "nn", False),), dt.uint8)
+    _run(gpu, LA.gemv_mfma(t[0].ptr, t[1].ptr, c1.ptr, M, Nn, Kk, c_dtype=dt.float32, ws_ptr=w1.ptr))
+    _run(gpu, LA.gemv(t[0].ptr, t[1].ptr, c2.ptr, M, Nn, Kk, layout="nn", b_dtype=dt.bfloat16,
+                      c_dtype=dt.float32, ws_ptr=w2.ptr))
+    a, b = c1.numpy(), c2.numpy()
+    np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-5 * np.abs(b).max())
 
 
 # ---------------------------------------------------------------------------
@@ -250,21 +321,22 @@ def test_gemm_splitk_against_unsplit(gpu, layout, fp8):
     np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-5 * np.abs(b).max())
 
 
-def test_decode_batch_projection_lowers_to_splitk(gpu):
-    """A traced 32-token projection (x (32, 1, 4096) @ W (4096, 6144), bf16)
-    lowers to the MFMA kernel over K ranges and matches float64."""
+@pytest.mark.parametrize("M,symbol", [(32, "nk_gemv_mfma_nn_bf16_t2"), (64, "nk_gemm8k_nn_bf16_f32_splitk")])
+def test_decode_batch_projection_lowers_to_splitk(gpu, M, symbol):
+    """A traced decode-batch projection (x (M, 1, 4096) @ W (4096, 6144),
+    bf16): 32 tokens take the MFMA few-row form, 64 the MFMA GEMM over K
+    ranges; both match float64."""
     from nkipy_amd.runtime import DeviceKernel, baremetal_jit
 
     def proj(x, w):
         return np.matmul(x, w)
 
     rng = np.random.default_rng(4)
-    x = N.bf16_round(rng.standard_normal((32, 1, 4096)))
+    x = N.bf16_round(rng.standard_normal((M, 1, 4096)))
     w = N.bf16_round(rng.standard_normal((4096, 6144)) * 0.02)
     args = [dt.to_bf16(a) for a in (x, w)]
     dk = DeviceKernel.compile_and_load(proj, *args)
     (step,) = dk.plan.steps
-    assert [l.symbol for l in step.launches(lambda v: 1 << 40)] == ["nk_gemm8k_nn_bf16_f32_splitk",
-                                                                    "nk_gemv_out_bf16"]
+    assert [l.symbol for l in step.launches(lambda v: 1 << 40)] == [symbol, "nk_gemv_out_bf16"]
     got = dt.to_float32(baremetal_jit(proj)(*args))
     _close(got, x.astype(np.float64) @ w.astype(np.float64), axis=-1)
