@@ -329,6 +329,40 @@ def test_launchers_reject_operands_the_kernels_cannot_take():
     assert ok.grid[0] == 2 * 3 and ok.flops == 2 * 300 * 520 * 136
 
 
+def test_few_row_projection_forms_split_and_route():
+    """The MFMA few-row projection: K ranges of 256 while the grid fits one
+    round of 512 workgroups, else the shortest multiple of 32 that fits (at
+    most 512 for 16 rows, 256 for 32); ranges cover K; routing up to 16
+    rows, and 32 while ranges of 256 fit one round; operand checks."""
+    A = 1 << 20
+    assert LA.gemv_mfma_split(8, 6144, 4096) == (16, 256)
+    assert LA.gemv_mfma_split(8, 4096, 14336) == (32, 448)
+    assert LA.gemv_mfma_split(8, 24576, 4096) == (8, 512)
+    assert LA.gemv_mfma_split(32, 4096, 14336) == (56, 256)
+    for M, N, K in ((1, 6144, 4096), (13, 1000, 328), (8, 151936, 4096), (17, 520, 2056), (5, 264, 8)):
+        ks, kc = LA.gemv_mfma_split(M, N, K)
+        assert kc % 32 == 0 and kc <= (512 if M <= 16 else 256)
+        assert (ks - 1) * kc < K <= ks * kc
+        launches = LA.gemv_mfma(A, A, A, M, N, K, c_dtype=dt.bfloat16, ws_ptr=A)
+        assert [l.symbol for l in launches] == [f"nk_gemv_mfma_nn_bf16_t{1 if M <= 16 else 2}",
+                                                "nk_gemv_out_bf16"]
+        assert launches[0].grid[0] == -(-N // 256) * ks
+        assert LA.gemv_mfma_workspace_bytes(M, N, K) == 4 * ks * M * N
+    assert LA.gemv_mfma_preferred(1, 4096, 4096) and LA.gemv_mfma_preferred(16, 24576, 14336)
+    assert LA.gemv_mfma_preferred(32, 6144, 4096) and not LA.gemv_mfma_preferred(32, 4096, 14336)
+    assert not LA.gemv_mfma_preferred(33, 64, 64) and not LA.gemv_mfma_preferred(0, 64, 64)
+    with pytest.raises(LA.LaunchError):
+        LA.gemv_mfma(A, A, A, 33, 64, 64, c_dtype=dt.bfloat16, ws_ptr=A)  # rows
+    with pytest.raises(LA.LaunchError):
+        LA.gemv_mfma(A, A, A, 8, 60, 64, c_dtype=dt.bfloat16, ws_ptr=A)  # N % 8
+    with pytest.raises(LA.LaunchError):
+        LA.gemv_mfma(A, A + 8, A, 8, 64, 64, c_dtype=dt.bfloat16, ws_ptr=A)  # weight alignment
+    with pytest.raises(LA.LaunchError):
+        LA.gemv_mfma(A, A, A, 8, 64, 64, c_dtype=dt.bfloat16, ws_ptr=0)  # workspace
+    with pytest.raises(LA.LaunchError):
+        LA.gemv_mfma(A, A, A, 8, 64, 64, c_dtype=dt.float16, ws_ptr=A)  # output dtype
+
+
 # ---------------------------------------------------------------------------
 # in-place aliasing: a deferred read of a mutated parameter must not see the update
 # ---------------------------------------------------------------------------
