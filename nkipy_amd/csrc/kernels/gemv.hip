@@ -1,5 +1,6 @@
-// Projections of a few rows (M <= 8, one decode token per sequence) on
-// gfx950: C[M, N] = A[M, K] @ B with the epilogues of the MFMA GEMM (gemm.hip).
+// Projections of a few rows (M <= 8 on the VALU, M <= 32 on MFMA; a decode
+// token per sequence) on gfx950: C[M, N] = A[M, K] @ B with the epilogues of
+// the MFMA GEMM (gemm.hip).
 //
 // At such M the GEMM's 256-row tiles compute mostly padding and its grid
 // has N / 256 workgroups: a token's projection is weight streaming, bound by
@@ -8,6 +9,8 @@
 //   nk_gemv_{nn,nt}_{bf16,e4m3}[_swiglu]   partial sums over one K range
 //       into an fp32 workspace P[split][m][n] (a second array for the up
 //       weights of the SwiGLU form);
+//   nk_gemv_mfma_nn_bf16_t{1,2}           the same for bf16 K x N weights on
+//       16-row MFMA tiles (below);
 //   nk_gemv_out_{bf16,f32}[_swiglu]        the splits added in a fixed order,
 //       then the epilogue (per-column scale, bias, bf16 roundings, residual;
 //       or silu(g) u) as the GEMM's, and the store.
