@@ -423,7 +423,11 @@ extern "C" __global__ __launch_bounds__(256) void nk_gemv_out_bf16_swiglu(GemvAr
 //    read fall on 16 distinct bank groups), zeros past M and past the range.
 // Rows past the range end, and columns past N, are moves out of the
 // resource's range: zeros, no memory read.  The partial sums go to the
-// workspace as in nk_gemv_nn_*: P[split][m][n], rows m < M.
+// workspace as in nk_gemv_nn_*: P[split][m][n], rows m < M.  SwiGLU form
+// (_swiglu): a workgroup owns 128 output columns; a stage holds those
+// columns of the gate weights in its first half and of the up weights in
+// its second, so waves 0-1 sum gate columns and waves 2-3 up columns, into
+// the two sets of planes the SwiGLU reduction reads.
 // ---------------------------------------------------------------------------
 #define GK_MAX_KC 512
 
@@ -433,7 +437,7 @@ typedef __bf16 gk_bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 gk_bf16x4 __attribute__((ext_vector_type(4)));
 typedef float gk_f32x4 __attribute__((ext_vector_type(4)));
 
-template <int MT>
+template <int MT, bool SWIGLU>
 __device__ __forceinline__ void gemv_mfma_nn_body(const GemvArgs &a) {
   constexpr int GK_STAGES = 3;
   constexpr int SB = 32 * 256 * 2;                                       // one stage
@@ -444,7 +448,7 @@ __device__ __forceinline__ void gemv_mfma_nn_body(const GemvArgs &a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, g4 = lane >> 4;
   const int ks = blockIdx.x % a.ksplit;
-  const int64_t n0 = (int64_t)(blockIdx.x / a.ksplit) * 256;
+  const int64_t n0 = (int64_t)(blockIdx.x / a.ksplit) * (SWIGLU ? 128 : 256);
   const int64_t k0 = (int64_t)ks * a.kc;
   const int kend = (int)min((int64_t)a.kc, a.K - k0);  // a multiple of 8
   const int nst = (kend + 31) >> 5;                    // stages of this range
@@ -465,13 +469,15 @@ __device__ __forceinline__ void gemv_mfma_nn_body(const GemvArgs &a) {
   // B stage t into ring slot t % GK_STAGES: block b = wave + 4 j (j < 4)
   // covers k rows 4 (b % 8) + lane / 16 of column half b / 8
   const i32x4_t rb = rsrc_words(reinterpret_cast<const uint16_t *>(a.B0) + k0 * a.ldb, (int64_t)kend * a.ldb * 2);
+  const i32x4_t ru = rsrc_words(SWIGLU ? reinterpret_cast<const uint16_t *>(a.B1) + k0 * a.ldb : nullptr,
+                                SWIGLU ? (int64_t)kend * a.ldb * 2 : 0);
   uint32_t boff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int b = wave + 4 * j;
     const int kr = 4 * (b & 7) + g4;
     const int lc = l16 ^ ((kr & 3) << 2);
-    const int64_t col = n0 + 128 * (b >> 3) + 8 * lc;
+    const int64_t col = n0 + (SWIGLU ? 0 : 128 * (b >> 3)) + 8 * lc;
     boff[j] = col < a.N ? (uint32_t)((kr * a.ldb + col) * 2) : 0x80000000u;
   }
   const uint32_t tstep = (uint32_t)(32 * a.ldb * 2);
@@ -481,7 +487,8 @@ __device__ __forceinline__ void gemv_mfma_nn_body(const GemvArgs &a) {
     for (int j = 0; j < 4; ++j) {
       const int b = wave + 4 * j;
       // stages past the range read nothing (every offset out of range)
-      dma16_asm(rb, base + b * 1024, t < nst && boff[j] != 0x80000000u ? boff[j] + t * tstep : 0x80000000u);
+      dma16_asm((SWIGLU && (b >> 3)) ? ru : rb, base + b * 1024,
+                t < nst && boff[j] != 0x80000000u ? boff[j] + t * tstep : 0x80000000u);
     }
   };
 #pragma unroll
@@ -533,11 +540,12 @@ __device__ __forceinline__ void gemv_mfma_nn_body(const GemvArgs &a) {
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no move outlives the workgroup
 
-  // D rows 16 mt + 4 g4 + r, column 64 wave + 16 jt + l16
-  float *P = a.ws + (int64_t)ks * a.M * a.N;
+  // D rows 16 mt + 4 g4 + r, column 64 wave + 16 jt + l16 (SwiGLU: column
+  // 64 (wave % 2) + 16 jt + l16 of the gate or the up planes)
+  float *P = a.ws + ((SWIGLU ? (int64_t)(wave >> 1) * a.ksplit : 0) + ks) * a.M * a.N;
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt) {
-    const int64_t n = n0 + 64 * wave + 16 * jt + l16;
+    const int64_t n = n0 + 64 * (SWIGLU ? (wave & 1) : wave) + 16 * jt + l16;
     if (n < a.N) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
@@ -550,5 +558,15 @@ __device__ __forceinline__ void gemv_mfma_nn_body(const GemvArgs &a) {
   }
 }
 
-extern "C" __global__ __launch_bounds__(256) void nk_gemv_mfma_nn_bf16_t1(GemvArgs a) { gemv_mfma_nn_body<1>(a); }
-extern "C" __global__ __launch_bounds__(256) void nk_gemv_mfma_nn_bf16_t2(GemvArgs a) { gemv_mfma_nn_body<2>(a); }
+extern "C" __global__ __launch_bounds__(256) void nk_gemv_mfma_nn_bf16_t1(GemvArgs a) {
+  gemv_mfma_nn_body<1, false>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void nk_gemv_mfma_nn_bf16_t2(GemvArgs a) {
+  gemv_mfma_nn_body<2, false>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void nk_gemv_mfma_nn_bf16_swiglu_t1(GemvArgs a) {
+  gemv_mfma_nn_body<1, true>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void nk_gemv_mfma_nn_bf16_swiglu_t2(GemvArgs a) {
+  gemv_mfma_nn_body<2, true>(a);
+}

@@ -617,13 +617,14 @@ GEMV_MFMA_MAX_KC = 512  # A's rows of the range in LDS: 16 x 512 or 32 x 256
 _GEMV_MFMA_TARGET_WGS = 512
 
 
-def gemv_mfma_split(M: int, N: int, K: int):
+def gemv_mfma_split(M: int, N: int, K: int, swiglu: bool = False):
     """(ksplit, kc) of :func:`gemv_mfma`: K ranges of 256 while the grid of
-    N / 256 x ksplit workgroups stays within one round of 512 (two per CU),
-    else the shortest range (a multiple of 32, at most 512 for 16 rows, 256
-    for 32) that keeps it there.  Measured with cold weights: a second
-    round of workgroups costs more than longer ranges do."""
-    tiles = -(-N // 256)
+    column blocks (256 columns, 128 for the SwiGLU pair) x ksplit
+    workgroups stays within one round of 512 (two per CU), else the
+    shortest range (a multiple of 32, at most 512 for 16 rows, 256 for 32)
+    that keeps it there.  Measured with cold weights: a second round of
+    workgroups costs more than longer ranges do."""
+    tiles = -(-N // (128 if swiglu else 256))
     kmax = GEMV_MFMA_MAX_KC if M <= 16 else GEMV_MFMA_MAX_KC // 2
     kc = 256
     ks = -(-K // kc)
@@ -634,7 +635,7 @@ def gemv_mfma_split(M: int, N: int, K: int):
     return ks, kc
 
 
-def gemv_mfma_preferred(M: int, N: int, K: int) -> bool:
+def gemv_mfma_preferred(M: int, N: int, K: int, swiglu: bool = False) -> bool:
     """Whether :func:`gemv_mfma` is the form for M rows of bf16 NN weights
     (measured with cold weights at 4096 / 6144 / 24576 x 4096 and 4096 x
     14336 against the VALU form and the MFMA GEMM over K ranges): up to 16
@@ -642,22 +643,24 @@ def gemv_mfma_preferred(M: int, N: int, K: int) -> bool:
     256 keep the grid within one round of workgroups."""
     if M <= 16:
         return M > 0
-    return M <= GEMV_MFMA_MAX_M and -(-N // 256) * -(-K // 256) <= _GEMV_MFMA_TARGET_WGS
+    tiles = -(-N // (128 if swiglu else 256))
+    return M <= GEMV_MFMA_MAX_M and tiles * -(-K // 256) <= _GEMV_MFMA_TARGET_WGS
 
 
-def gemv_mfma_workspace_bytes(M: int, N: int, K: int) -> int:
-    ks, _ = gemv_mfma_split(M, N, K)
-    return 4 * ks * M * N
+def gemv_mfma_workspace_bytes(M: int, N: int, K: int, swiglu: bool = False) -> int:
+    ks, _ = gemv_mfma_split(M, N, K, swiglu)
+    return 4 * ks * M * N * (2 if swiglu else 1)
 
 
 def gemv_mfma(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, c_dtype, ws_ptr: int,
               lda: int = None, ldb: int = None, ldc: int = None, bias_ptr: int = 0, resid_ptr: int = 0,
-              round_before_bias: bool = False, round_before_resid: bool = False) -> List[Launch]:
+              up_ptr: int = 0, round_before_bias: bool = False, round_before_resid: bool = False) -> List[Launch]:
     """The operation of :func:`gemv` for bf16 NN weights (K x N) and up to 32
     rows, with the products on MFMA (16-row tiles): partial sums over K
     ranges into the workspace at ``ws_ptr`` (``gemv_mfma_workspace_bytes``),
     then the reduction of :func:`gemv` (ranges added in order, then the
-    epilogue).  Two launches."""
+    epilogue; silu(x @ W) * (x @ U) with the up weights at ``up_ptr``, same
+    layout and ``ldb``).  Two launches."""
     c_dtype = dt.canonical(c_dtype)
     if c_dtype not in (dt.bfloat16, dt.float32):
         raise LaunchError(f"GEMM output must be bf16 or float32, got {dt.name(c_dtype)}")
@@ -666,14 +669,17 @@ def gemv_mfma(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, c_d
     lda = K if lda is None else lda
     ldb = N if ldb is None else ldb
     ldc = N if ldc is None else ldc
+    swiglu = bool(up_ptr)
     if K % 8 or lda % 8 or ldb % 8 or N % 8:
         raise LaunchError("the MFMA projection needs K, N, lda and ldb to be multiples of 8 (16-byte rows)")
     if lda < K or ldb < N or ldc < N:
         raise LaunchError("GEMM leading dimension smaller than the matrix")
-    for p, al in ((a_ptr, 16), (b_ptr, 16), (ws_ptr, 16)):
-        if not p or p % al:
+    for p in (a_ptr, b_ptr, ws_ptr) + ((up_ptr,) if swiglu else ()):
+        if not p or p % 16:
             raise LaunchError("GEMM operand, weight and workspace pointers must be 16-byte aligned")
-    ks, kc = gemv_mfma_split(M, N, K)
+    if swiglu and (bias_ptr or resid_ptr or c_dtype != dt.bfloat16):
+        raise LaunchError("the SwiGLU epilogue writes bf16 without bias / residual")
+    ks, kc = gemv_mfma_split(M, N, K, swiglu)
     if kc % 32 or kc > GEMV_MFMA_MAX_KC // (1 if M <= 16 else 2):
         raise LaunchError(f"K range of {kc} does not fit the MFMA projection")
     if kc * ldb * 2 >= 2**31 or M * lda * 2 >= 2**31 or M * N >= 2**31:
@@ -683,14 +689,17 @@ def gemv_mfma(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, c_d
         flags |= GEMM_RND_BIAS
     if round_before_resid and resid_ptr:
         flags |= GEMM_RND_RESID
-    args = GemvArgs(a_ptr, b_ptr, None, c_ptr, bias_ptr or None, None, None, resid_ptr or None, ws_ptr,
+    args = GemvArgs(a_ptr, b_ptr, up_ptr or None, c_ptr, bias_ptr or None, None, None, resid_ptr or None, ws_ptr,
                     M, N, K, lda, ldb, ldc, ks, kc, flags, 0)
     tiles = 1 if M <= 16 else 2
+    n_mm = 2 if swiglu else 1
+    sw = "_swiglu" if swiglu else ""
     ctag = "bf16" if c_dtype == dt.bfloat16 else "f32"
-    return [Launch("gemv", f"nk_gemv_mfma_nn_bf16_t{tiles}", (-(-N // 256) * ks, 1, 1), (256, 1, 1), args,
-                   bytes=M * K * 2 + N * K * 2 + 4 * ks * M * N, flops=2 * M * N * K),
-            Launch("gemv", f"nk_gemv_out_{ctag}", (-(-M * N // 64), 1, 1), (256, 1, 1), args,
-                   bytes=4 * ks * M * N + M * N * c_dtype.itemsize)]
+    blocks = -(-N // (128 if swiglu else 256))
+    return [Launch("gemv", f"nk_gemv_mfma_nn_bf16{sw}_t{tiles}", (blocks * ks, 1, 1), (256, 1, 1), args,
+                   bytes=M * K * 2 + n_mm * N * K * 2 + 4 * ks * M * N * n_mm, flops=2 * M * N * K * n_mm),
+            Launch("gemv", f"nk_gemv_out_{ctag}{sw}", (-(-M * N // 64), 1, 1), (256, 1, 1), args,
+                   bytes=4 * ks * M * N * n_mm + M * N * c_dtype.itemsize)]
 
 
 class HeadRopeTarget(ctypes.Structure):

@@ -174,15 +174,17 @@ class GemmMatch(Match):
         fp8 = w.value.dtype == dt.float8_e4m3fn
         # bf16 NN weights of a projection up to 16-32 rows: the MFMA form of
         # the few-row kernels (16-row tiles, weights streamed once)
-        mfma = (self.split_k and w.layout == "nn" and not fp8 and up is None
-                and LA.gemv_mfma_preferred(M, N, K))
+        mfma = (self.split_k and w.layout == "nn" and not fp8
+                and (up is None or (up.layout == "nn" and up.value.dtype == dt.bfloat16))
+                and LA.gemv_mfma_preferred(M, N, K, up is not None))
         small = not mfma and LA.gemv_preferred(M, w.layout, fp8)
         splitk = (self.split_k and not mfma and not small and not (fp8 and w.layout == "nn")
                   and LA.gemm_splitk_useful(M, N, K, up is not None, fp8))
         small = small or (not mfma and M <= LA.GEMV_MAX_M and not splitk)
         ws = None
         if mfma:
-            ws = Slot(plan.add_buffer(LA.gemv_mfma_workspace_bytes(M, N, K), "temp", "gemv.partials"))
+            ws = Slot(plan.add_buffer(LA.gemv_mfma_workspace_bytes(M, N, K, up is not None), "temp",
+                                      "gemv.partials"))
         elif small:
             ws = Slot(plan.add_buffer(LA.gemv_workspace_bytes(M, N, K, w.layout, fp8, up is not None), "temp",
                                       "gemv.partials"))
@@ -199,7 +201,7 @@ class GemmMatch(Match):
             if mfma:
                 return LA.gemv_mfma(addr(x), addr(w.value), addr(out), M, N, K, c_dtype=out.dtype, ldb=ldb,
                                     ws_ptr=addr(ws), bias_ptr=addr(bias) if bias is not None else 0,
-                                    resid_ptr=addr(resid) if resid is not None else 0,
+                                    resid_ptr=addr(resid) if resid is not None else 0, up_ptr=up_ptr,
                                     round_before_bias=rnd_bias, round_before_resid=rnd_resid)
             if small:
                 return LA.gemv(addr(x), addr(w.value), addr(out), M, N, K, layout=w.layout,

@@ -208,6 +208,36 @@ def test_gemv_mfma_matches_float64(gpu, M, Nn, Kk, ldb, epi):
         _close(got, ref, axis=-1, rounded=N.bf16_round(prod) if epi == "rounded" else None)
 
 
+@pytest.mark.parametrize("M,Nn,Kk,fused", [(1, 14336, 4096, False), (8, 1536, 2048, True), (17, 520, 1000, False),
+                                            (32, 768, 4096, True)])
+def test_gemv_mfma_swiglu(gpu, M, Nn, Kk, fused):
+    """silu(x @ G) * (x @ U) on the MFMA few-row form: separate gate / up
+    weights, or one (K, 2N) weight with the up half N columns in (ldb 2N)."""
+    rng = np.random.default_rng(M + Nn + Kk)
+    print(f"gemv_mfma swiglu M={M} N={Nn} K={Kk} fused={fused} split={LA.gemv_mfma_split(M, Nn, Kk, True)}",
+          flush=True)
+    x = N.bf16_round(rng.standard_normal((M, Kk)))
+    g = N.bf16_round(rng.standard_normal((Kk, Nn)) * 0.05)
+    u = N.bf16_round(rng.standard_normal((Kk, Nn)) * 0.05)
+    ref = K.silu(x.astype(np.float64) @ g.astype(np.float64)) * (x.astype(np.float64) @ u.astype(np.float64))
+    xd = DeviceTensor.from_numpy(dt.to_bf16(x))
+    if fused:
+        wd = DeviceTensor.from_numpy(dt.to_bf16(np.concatenate([g, u], axis=1)))
+        gp, up, ldb = wd.ptr, wd.ptr + Nn * 2, 2 * Nn
+        keep = [wd]
+    else:
+        gd, ud = DeviceTensor.from_numpy(dt.to_bf16(g)), DeviceTensor.from_numpy(dt.to_bf16(u))
+        gp, up, ldb = gd.ptr, ud.ptr, Nn
+        keep = [gd, ud]
+    h = DeviceTensor.empty((M, Nn), dt.bfloat16)
+    ws = DeviceTensor.empty((LA.gemv_mfma_workspace_bytes(M, Nn, Kk, swiglu=True),), dt.uint8)
+    launches = LA.gemv_mfma(xd.ptr, gp, h.ptr, M, Nn, Kk, c_dtype=dt.bfloat16, ws_ptr=ws.ptr, ldb=ldb, up_ptr=up)
+    assert launches[0].symbol.startswith("nk_gemv_mfma_nn_bf16_swiglu_")
+    _run(gpu, launches)
+    del keep
+    _close(dt.to_float32(h.numpy()), ref, axis=-1)
+
+
 def test_gemv_mfma_against_valu_form(gpu):
     """The same operands through the MFMA and the VALU few-row kernels: fp32
     results within the difference of two summation orders."""

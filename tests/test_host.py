@@ -348,6 +348,13 @@ def test_few_row_projection_forms_split_and_route():
                                                 "nk_gemv_out_bf16"]
         assert launches[0].grid[0] == -(-N // 256) * ks
         assert LA.gemv_mfma_workspace_bytes(M, N, K) == 4 * ks * M * N
+    assert LA.gemv_mfma_split(8, 14336, 4096, swiglu=True) == (8, 512)  # 112 blocks of 128 columns
+    assert LA.gemv_mfma_workspace_bytes(8, 1536, 2048, swiglu=True) == 2 * 4 * 8 * 8 * 1536
+    sw = LA.gemv_mfma(A, A, A, 8, 1536, 2048, c_dtype=dt.bfloat16, ws_ptr=A, up_ptr=A + 3072, ldb=3072)
+    assert [l.symbol for l in sw] == ["nk_gemv_mfma_nn_bf16_swiglu_t1", "nk_gemv_out_bf16_swiglu"]
+    assert sw[0].grid[0] == 12 * 8
+    with pytest.raises(LA.LaunchError):
+        LA.gemv_mfma(A, A, A, 8, 64, 64, c_dtype=dt.bfloat16, ws_ptr=A, up_ptr=A, bias_ptr=A)  # SwiGLU + bias
     assert LA.gemv_mfma_preferred(1, 4096, 4096) and LA.gemv_mfma_preferred(16, 24576, 14336)
     assert LA.gemv_mfma_preferred(32, 6144, 4096) and not LA.gemv_mfma_preferred(32, 4096, 14336)
     assert not LA.gemv_mfma_preferred(33, 64, 64) and not LA.gemv_mfma_preferred(0, 64, 64)
