@@ -54,6 +54,29 @@ def test_feedforward_fused_gate_up(gpu):
     _close(y, K.feedforward_fused(x3, gu, wd, round_h=N.bf16_round))
 
 
+@pytest.mark.parametrize("fused", [False, True])
+def test_decode_batch_mlp_on_few_row_kernels(gpu, fused):
+    """A decode batch (8 tokens) through the traced SwiGLU MLP, separate or
+    fused gate / up weights: both GEMMs take the MFMA few-row kernels (the
+    gate / up pair in its SwiGLU form) and match the oracle."""
+    x, wg, wu, wd = _inputs(8, 2048, 1536, seed=9)
+    if fused:
+        x3 = x.reshape(8, 1, 2048)
+        args = [dt.to_bf16(a) for a in (x3, np.concatenate([wg, wu], axis=1), wd)]
+        fn, ref = feedforward_kernel, K.feedforward_fused(x3, np.concatenate([wg, wu], axis=1), wd,
+                                                          round_h=N.bf16_round)
+    else:
+        args = [dt.to_bf16(a) for a in (x, wg, wu, wd)]
+        fn, ref = swiglu_mlp_kernel, K.swiglu_mlp(x, wg, wu, wd, round_h=N.bf16_round)
+    dk = DeviceKernel.compile_and_load(fn, *args)
+    assert dk.plan.kernel_kinds == ["gemm_swiglu", "gemm"]
+    syms = [[l.symbol for l in st.launches(lambda v: 1 << 40)] for st in dk.plan.steps]
+    assert syms == [["nk_gemv_mfma_nn_bf16_swiglu_t1", "nk_gemv_out_bf16_swiglu"],
+                    ["nk_gemv_mfma_nn_bf16_t1", "nk_gemv_out_bf16"]]
+    y = dt.to_float32(baremetal_jit(fn)(*args))
+    _close(y, ref, axis=-1)
+
+
 def test_linear_nt(gpu):
     rng = np.random.default_rng(5)
     x = N.bf16_round(rng.standard_normal((7, 1, 2048)))
