@@ -9,7 +9,7 @@
 //   nk_gemv_{nn,nt}_{bf16,e4m3}[_swiglu]   partial sums over one K range
 //       into an fp32 workspace P[split][m][n] (a second array for the up
 //       weights of the SwiGLU form);
-//   nk_gemv_mfma_nn_bf16_t{1,2}           the same for bf16 K x N weights on
+//   nk_gemv_mfma_{nn_bf16,nt_bf16,nt_e4m3}[_swiglu]_t{1,2}   the same on
 //       16-row MFMA tiles (below);
 //   nk_gemv_out_{bf16,f32}[_swiglu]        the splits added in a fixed order,
 //       then the epilogue (per-column scale, bias, bf16 roundings, residual;
@@ -570,3 +570,144 @@ extern "C" __global__ __launch_bounds__(256) void nk_gemv_mfma_nn_bf16_swiglu_t1
 extern "C" __global__ __launch_bounds__(256) void nk_gemv_mfma_nn_bf16_swiglu_t2(GemvArgs a) {
   gemv_mfma_nn_body<2, true>(a);
 }
+
+// ---------------------------------------------------------------------------
+// MFMA form of the NT partial sums (weights N x K, each row contiguous in k:
+// bf16, or fp8 e4m3 decoded exactly to bf16) for up to 16 MT rows.  Every
+// wave loads its B fragments straight from global memory into registers,
+// and A's (16 rows x 32 k, L2-resident) the same way: no LDS and no
+// barrier.  The K range goes in super-steps of 64 k in which lane (g, i)
+// owns k 16g..16g+15 of column i's row (32 contiguous bytes of bf16, 16 of
+// fp8, so the four lanes of a row read 128 / 64 contiguous bytes); the
+// super-step's two 16x16x32 MFMAs take k 16g + 8s .. + 7 (s = 0, 1) in
+// the fragment slots 8g..8g+7 of both operands, a permutation of the 64 k
+// that A and B share.  PF super-steps are in flight.  A workgroup (4
+// waves) owns 256 columns and one K range of kc (a multiple of 32); wave w
+// owns columns 64w.. (four 16-column tiles).  The SwiGLU form owns 128
+// columns: waves 0-1 read the gate rows, waves 2-3 the up rows, into the
+// two sets of planes of the SwiGLU reduction.  Columns past N and k past the
+// range are loads out of the resource's range (zeros, no memory read; fp8
+// ranges end on a multiple of 16).  Partial sums as in nk_gemv_nt_*:
+// P[split][m][n].
+// ---------------------------------------------------------------------------
+template <int MT, bool FP8, bool SWIGLU>
+__device__ __forceinline__ void gemv_mfma_nt_body(const GemvArgs &a) {
+  constexpr int ES = FP8 ? 1 : 2;       // weight element bytes
+  constexpr int NB = FP8 ? 1 : 2;       // 16-byte weight loads per tile and super-step
+  constexpr int PF = FP8 ? 4 : 2;       // super-steps in flight
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int ks = blockIdx.x % a.ksplit;
+  const int64_t n0 = (int64_t)(blockIdx.x / a.ksplit) * (SWIGLU ? 128 : 256);
+  const int64_t k0 = (int64_t)ks * a.kc;
+  const int kend = (int)min((int64_t)a.kc, a.K - k0);  // a multiple of 8 (16 with fp8)
+  const int nss = (kend + 63) >> 6;                    // super-steps
+  const bool up = SWIGLU && wave >= 2;
+  const int64_t nw = n0 + 64 * (SWIGLU ? (wave & 1) : wave);  // this wave's first column
+
+  // byte offsets at super-step 0 (+ 64 elements per super-step); out of
+  // range: 2^31
+  const auto rb = buf_rsrc(up ? a.B1 : a.B0, (uint32_t)(a.N * a.ldb * ES));
+  const auto ra = buf_rsrc(a.A, (uint32_t)(a.M * a.lda * 2));
+  uint32_t boff[4], aoff[MT];
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt) {
+    const int64_t n = nw + 16 * jt + l16;
+    boff[jt] = n < a.N ? (uint32_t)((n * a.ldb + k0 + 16 * g4) * ES) : 0x80000000u;
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * mt + l16;
+    aoff[mt] = m < a.M ? (uint32_t)((m * a.lda + k0 + 16 * g4) * 2) : 0x80000000u;
+  }
+  uint4 bq[PF][4][NB], aq[PF][MT][2];
+  auto issue = [&](int u, int t) __attribute__((always_inline)) {
+    // this lane's 8-k chunks of super-step t: 64 t + 16 g4 + 8 s < kend
+    const int kb = 64 * t + 16 * g4;
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int q = 0; q < NB; ++q) {
+        const bool in = kb + 8 * q < kend && boff[jt] != 0x80000000u;
+        bq[u][jt][q] = buf_ld16<false>(rb, in ? boff[jt] + 64 * t * ES + 16 * q : 0x80000000u);
+      }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const bool in = kb + 8 * q < kend && aoff[mt] != 0x80000000u;
+        aq[u][mt][q] = buf_ld16<false>(ra, in ? aoff[mt] + 128 * t + 16 * q : 0x80000000u);
+      }
+  };
+#pragma unroll
+  for (int u = 0; u < PF; ++u) issue(u, u);
+
+  gk_f32x4 acc[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[mt][jt][r] = 0.f;
+  for (int t0 = 0; t0 < nss; t0 += PF) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      if (t0 + u < nss) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          gk_bf16x8 bf[4];
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt) {
+            if constexpr (FP8) {
+              const uint4 w = bq[u][jt][0];
+              bf[jt] = __builtin_bit_cast(gk_bf16x8, e4m3x8_to_bf16x8(s ? make_uint2(w.z, w.w) : make_uint2(w.x, w.y)));
+            } else {
+              bf[jt] = __builtin_bit_cast(gk_bf16x8, bq[u][jt][s]);
+            }
+          }
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const gk_bf16x8 af = __builtin_bit_cast(gk_bf16x8, aq[u][mt][s]);
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt)
+              acc[mt][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf[jt], acc[mt][jt], 0, 0, 0);
+          }
+        }
+      }
+      issue(u, t0 + u + PF);  // past the range: loads of zeros, no memory read
+    }
+  }
+
+  // D rows 16 mt + 4 g4 + r, column nw + 16 jt + l16
+  float *P = a.ws + ((SWIGLU ? (int64_t)(wave >> 1) * a.ksplit : 0) + ks) * a.M * a.N;
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt) {
+    const int64_t n = nw + 16 * jt + l16;
+    if (n < a.N) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = 16 * mt + 4 * g4 + r;
+          if (m < a.M) P[m * a.N + n] = acc[mt][jt][r];
+        }
+    }
+  }
+}
+
+#define NK_GEMV_MFMA_NT(wt, FP8)                                                                            \
+  extern "C" __global__ __launch_bounds__(256) void nk_gemv_mfma_nt_##wt##_t1(GemvArgs a) {                 \
+    gemv_mfma_nt_body<1, FP8, false>(a);                                                                    \
+  }                                                                                                         \
+  extern "C" __global__ __launch_bounds__(256) void nk_gemv_mfma_nt_##wt##_t2(GemvArgs a) {                 \
+    gemv_mfma_nt_body<2, FP8, false>(a);                                                                    \
+  }                                                                                                         \
+  extern "C" __global__ __launch_bounds__(256) void nk_gemv_mfma_nt_##wt##_swiglu_t1(GemvArgs a) {          \
+    gemv_mfma_nt_body<1, FP8, true>(a);                                                                     \
+  }                                                                                                         \
+  extern "C" __global__ __launch_bounds__(256) void nk_gemv_mfma_nt_##wt##_swiglu_t2(GemvArgs a) {          \
+    gemv_mfma_nt_body<2, FP8, true>(a);                                                                     \
+  }
+NK_GEMV_MFMA_NT(bf16, false)
+NK_GEMV_MFMA_NT(e4m3, true)

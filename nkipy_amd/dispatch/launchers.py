@@ -635,14 +635,19 @@ def gemv_mfma_split(M: int, N: int, K: int, swiglu: bool = False):
     return ks, kc
 
 
-def gemv_mfma_preferred(M: int, N: int, K: int, swiglu: bool = False) -> bool:
-    """Whether :func:`gemv_mfma` is the form for M rows of bf16 NN weights
-    (measured with cold weights at 4096 / 6144 / 24576 x 4096 and 4096 x
-    14336 against the VALU form and the MFMA GEMM over K ranges): up to 16
-    rows always (at one row it ties the VALU form), 32 rows while ranges of
-    256 keep the grid within one round of workgroups."""
+def gemv_mfma_preferred(M: int, N: int, K: int, swiglu: bool = False, layout: str = "nn",
+                        fp8: bool = False) -> bool:
+    """Whether :func:`gemv_mfma` is the form for M rows (measured with cold
+    weights at 4096 / 6144 / 24576 x 4096 and 4096 x 14336 against the VALU
+    form and the MFMA GEMM over K ranges): bf16 NN weights up to 16 rows (at
+    one row it ties the VALU form), NT weights (bf16 or fp8) from 2 to 16
+    rows (one NT row streams faster on the VALU form), and 32 rows while
+    ranges of 256 keep the grid within one round of workgroups.  No fp8 NN
+    form."""
+    if M <= 0 or (fp8 and layout == "nn") or (layout == "nt" and M == 1):
+        return False
     if M <= 16:
-        return M > 0
+        return True
     tiles = -(-N // (128 if swiglu else 256))
     return M <= GEMV_MFMA_MAX_M and tiles * -(-K // 256) <= _GEMV_MFMA_TARGET_WGS
 
@@ -653,51 +658,69 @@ def gemv_mfma_workspace_bytes(M: int, N: int, K: int, swiglu: bool = False) -> i
 
 
 def gemv_mfma(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int, *, c_dtype, ws_ptr: int,
-              lda: int = None, ldb: int = None, ldc: int = None, bias_ptr: int = 0, resid_ptr: int = 0,
-              up_ptr: int = 0, round_before_bias: bool = False, round_before_resid: bool = False) -> List[Launch]:
-    """The operation of :func:`gemv` for bf16 NN weights (K x N) and up to 32
-    rows, with the products on MFMA (16-row tiles): partial sums over K
-    ranges into the workspace at ``ws_ptr`` (``gemv_mfma_workspace_bytes``),
-    then the reduction of :func:`gemv` (ranges added in order, then the
-    epilogue; silu(x @ W) * (x @ U) with the up weights at ``up_ptr``, same
-    layout and ``ldb``).  Two launches."""
-    c_dtype = dt.canonical(c_dtype)
+              layout: str = "nn", b_dtype=dt.bfloat16, lda: int = None, ldb: int = None, ldc: int = None,
+              bias_ptr: int = 0, scale_ptr: int = 0, resid_ptr: int = 0, up_ptr: int = 0, up_scale_ptr: int = 0,
+              round_before_bias: bool = False, round_before_resid: bool = False) -> List[Launch]:
+    """The operation of :func:`gemv` with the products on MFMA (16-row
+    tiles, up to 32 rows): bf16 NN weights (K x N) through an LDS ring, or
+    NT weights (N x K, bf16 or fp8 e4m3 with per-column scales) loaded
+    straight into registers.  Partial sums over K ranges into the workspace
+    at ``ws_ptr`` (``gemv_mfma_workspace_bytes``), then the reduction of
+    :func:`gemv` (ranges added in order, then the epilogue; silu(x @ W) *
+    (x @ U) with the up weights at ``up_ptr``, same layout and ``ldb``).
+    Two launches."""
+    if layout not in ("nn", "nt"):
+        raise LaunchError(f"unknown GEMM layout {layout}")
+    b_dtype, c_dtype = dt.canonical(b_dtype), dt.canonical(c_dtype)
+    fp8 = b_dtype == dt.float8_e4m3fn
+    if b_dtype != dt.bfloat16 and not (fp8 and layout == "nt"):
+        raise LaunchError(f"the MFMA projection takes bf16 weights, or fp8 NT weights; got {dt.name(b_dtype)} "
+                          f"{layout.upper()}")
     if c_dtype not in (dt.bfloat16, dt.float32):
         raise LaunchError(f"GEMM output must be bf16 or float32, got {dt.name(c_dtype)}")
     if not (0 < M <= GEMV_MFMA_MAX_M) or N <= 0 or K <= 0:
         raise LaunchError(f"the MFMA projection takes 1..{GEMV_MFMA_MAX_M} rows, got M={M} N={N} K={K}")
     lda = K if lda is None else lda
-    ldb = N if ldb is None else ldb
+    ldb = (N if layout == "nn" else K) if ldb is None else ldb
     ldc = N if ldc is None else ldc
     swiglu = bool(up_ptr)
-    if K % 8 or lda % 8 or ldb % 8 or N % 8:
-        raise LaunchError("the MFMA projection needs K, N, lda and ldb to be multiples of 8 (16-byte rows)")
-    if lda < K or ldb < N or ldc < N:
+    if K % 8 or lda % 8 or ldb % 8 or (layout == "nn" and N % 8):
+        raise LaunchError("the MFMA projection needs K, lda, ldb (and N for NN weights) to be multiples of 8")
+    if fp8 and (K % 16 or ldb % 16):
+        raise LaunchError("fp8 NT weights need K and ldb to be multiples of 16 (16-byte rows)")
+    if lda < K or ldc < N or ldb < (N if layout == "nn" else K):
         raise LaunchError("GEMM leading dimension smaller than the matrix")
-    for p in (a_ptr, b_ptr, ws_ptr) + ((up_ptr,) if swiglu else ()):
-        if not p or p % 16:
-            raise LaunchError("GEMM operand, weight and workspace pointers must be 16-byte aligned")
+    for p, al in ((a_ptr, 16), (b_ptr, 16), (ws_ptr, 16)) + (((up_ptr, 16),) if swiglu else ()):
+        if not p or p % al:
+            raise LaunchError("GEMM operand, weight and workspace pointers must be aligned for 128-bit access")
+    if fp8 and not scale_ptr:
+        raise LaunchError("fp8 weights need per-column scales")
+    if swiglu and (fp8 != bool(up_scale_ptr)):
+        raise LaunchError("SwiGLU with fp8 weights needs scales for both weights")
     if swiglu and (bias_ptr or resid_ptr or c_dtype != dt.bfloat16):
         raise LaunchError("the SwiGLU epilogue writes bf16 without bias / residual")
     ks, kc = gemv_mfma_split(M, N, K, swiglu)
     if kc % 32 or kc > GEMV_MFMA_MAX_KC // (1 if M <= 16 else 2):
         raise LaunchError(f"K range of {kc} does not fit the MFMA projection")
-    if kc * ldb * 2 >= 2**31 or M * lda * 2 >= 2**31 or M * N >= 2**31:
-        raise LaunchError("the MFMA projection addresses a K range's weights with 32-bit offsets")
-    flags = (GEMM_BIAS if bias_ptr else 0) | (GEMM_RESID if resid_ptr else 0)
+    wbytes = kc * ldb * 2 if layout == "nn" else N * ldb * b_dtype.itemsize
+    if wbytes >= 2**31 or M * lda * 2 >= 2**31 or M * N >= 2**31:
+        raise LaunchError("the MFMA projection addresses its weights with 32-bit offsets")
+    flags = (GEMM_BIAS if bias_ptr else 0) | (GEMM_SCALE if scale_ptr else 0) | (GEMM_RESID if resid_ptr else 0)
     if round_before_bias and bias_ptr:
         flags |= GEMM_RND_BIAS
     if round_before_resid and resid_ptr:
         flags |= GEMM_RND_RESID
-    args = GemvArgs(a_ptr, b_ptr, up_ptr or None, c_ptr, bias_ptr or None, None, None, resid_ptr or None, ws_ptr,
-                    M, N, K, lda, ldb, ldc, ks, kc, flags, 0)
+    args = GemvArgs(a_ptr, b_ptr, up_ptr or None, c_ptr, bias_ptr or None, scale_ptr or None,
+                    up_scale_ptr or None, resid_ptr or None, ws_ptr, M, N, K, lda, ldb, ldc, ks, kc, flags, 0)
     tiles = 1 if M <= 16 else 2
     n_mm = 2 if swiglu else 1
     sw = "_swiglu" if swiglu else ""
+    btag = "e4m3" if fp8 else "bf16"
     ctag = "bf16" if c_dtype == dt.bfloat16 else "f32"
     blocks = -(-N // (128 if swiglu else 256))
-    return [Launch("gemv", f"nk_gemv_mfma_nn_bf16{sw}_t{tiles}", (blocks * ks, 1, 1), (256, 1, 1), args,
-                   bytes=M * K * 2 + n_mm * N * K * 2 + 4 * ks * M * N * n_mm, flops=2 * M * N * K * n_mm),
+    return [Launch("gemv", f"nk_gemv_mfma_{layout}_{btag}{sw}_t{tiles}", (blocks * ks, 1, 1), (256, 1, 1), args,
+                   bytes=M * K * 2 + n_mm * N * K * b_dtype.itemsize + 4 * ks * M * N * n_mm,
+                   flops=2 * M * N * K * n_mm),
             Launch("gemv", f"nk_gemv_out_{ctag}{sw}", (-(-M * N // 64), 1, 1), (256, 1, 1), args,
                    bytes=4 * ks * M * N * n_mm + M * N * c_dtype.itemsize)]
 

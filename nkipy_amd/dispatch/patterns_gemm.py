@@ -172,11 +172,11 @@ class GemmMatch(Match):
         # (a decode batch): the MFMA kernels over K ranges, so that the
         # grid fills the part
         fp8 = w.value.dtype == dt.float8_e4m3fn
-        # bf16 NN weights of a projection up to 16-32 rows: the MFMA form of
-        # the few-row kernels (16-row tiles, weights streamed once)
-        mfma = (self.split_k and w.layout == "nn" and not fp8
-                and (up is None or (up.layout == "nn" and up.value.dtype == dt.bfloat16))
-                and LA.gemv_mfma_preferred(M, N, K, up is not None))
+        # a projection of up to 16-32 rows: the MFMA form of the few-row
+        # kernels (16-row tiles, weights streamed once)
+        mfma = (self.split_k
+                and (up is None or (up.layout == w.layout and up.value.dtype == w.value.dtype))
+                and LA.gemv_mfma_preferred(M, N, K, up is not None, w.layout, fp8))
         small = not mfma and LA.gemv_preferred(M, w.layout, fp8)
         splitk = (self.split_k and not mfma and not small and not (fp8 and w.layout == "nn")
                   and LA.gemm_splitk_useful(M, N, K, up is not None, fp8))
@@ -200,8 +200,11 @@ class GemmMatch(Match):
                 up_scale = addr(up.scale) if up.scale is not None else 0
             if mfma:
                 return LA.gemv_mfma(addr(x), addr(w.value), addr(out), M, N, K, c_dtype=out.dtype, ldb=ldb,
-                                    ws_ptr=addr(ws), bias_ptr=addr(bias) if bias is not None else 0,
+                                    layout=w.layout, b_dtype=w.value.dtype, ws_ptr=addr(ws),
+                                    bias_ptr=addr(bias) if bias is not None else 0,
+                                    scale_ptr=addr(w.scale) if w.scale is not None else 0,
                                     resid_ptr=addr(resid) if resid is not None else 0, up_ptr=up_ptr,
+                                    up_scale_ptr=up_scale,
                                     round_before_bias=rnd_bias, round_before_resid=rnd_resid)
             if small:
                 return LA.gemv(addr(x), addr(w.value), addr(out), M, N, K, layout=w.layout,

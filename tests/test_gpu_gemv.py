@@ -238,6 +238,88 @@ def test_gemv_mfma_swiglu(gpu, M, Nn, Kk, fused):
     _close(dt.to_float32(h.numpy()), ref, axis=-1)
 
 
+NT_MFMA_CASES = [  # (fp8, M, N, K): NT weights (bf16 / fp8), row tiles full / partial / two, N and K tails
+    (False, 2, 6144, 4096), (False, 13, 1000, 328), (False, 32, 520, 2056), (False, 8, 4096, 14336),
+    (True, 4, 6144, 4096), (True, 16, 1000, 336), (True, 17, 264, 4096), (True, 8, 4096, 14336),
+]
+
+
+@pytest.mark.parametrize("fp8,M,Nn,Kk", NT_MFMA_CASES)
+@pytest.mark.parametrize("epi", ["plain", "f32", "bias_resid"])
+def test_gemv_mfma_nt_matches_float64(gpu, fp8, M, Nn, Kk, epi):
+    rng = np.random.default_rng(M * 13 + Nn + Kk)
+    print(f"gemv_mfma nt fp8={fp8} M={M} N={Nn} K={Kk} {epi} split={LA.gemv_mfma_split(M, Nn, Kk)}", flush=True)
+    x = N.bf16_round(rng.standard_normal((M, Kk)))
+    wdev, scale, wmat = _weights(rng, "nt", Nn, Kk, fp8)
+    prod = x.astype(np.float64) @ wmat
+    out = dt.float32 if epi == "f32" else dt.bfloat16
+    t = {"x": DeviceTensor.from_numpy(dt.to_bf16(x)), "w": DeviceTensor.from_numpy(wdev)}
+    kw, ref = {}, prod
+    if scale is not None:
+        t["s"] = DeviceTensor.from_numpy(scale)
+        kw["scale_ptr"] = t["s"].ptr
+    if epi == "bias_resid":
+        bias = N.bf16_round(rng.standard_normal(Nn) * 0.1)
+        res = N.bf16_round(rng.standard_normal((M, Nn)))
+        t["b"] = DeviceTensor.from_numpy(dt.to_bf16(bias))
+        t["r"] = DeviceTensor.from_numpy(dt.to_bf16(res))
+        kw.update(bias_ptr=t["b"].ptr, resid_ptr=t["r"].ptr)
+        ref = prod + bias + res
+    c = DeviceTensor.empty((M, Nn), out)
+    ws = DeviceTensor.empty((LA.gemv_mfma_workspace_bytes(M, Nn, Kk),), dt.uint8)
+    launches = LA.gemv_mfma(t["x"].ptr, t["w"].ptr, c.ptr, M, Nn, Kk, c_dtype=out, ws_ptr=ws.ptr, layout="nt",
+                            b_dtype=dt.float8_e4m3fn if fp8 else dt.bfloat16, **kw)
+    assert launches[0].symbol.startswith(f"nk_gemv_mfma_nt_{'e4m3' if fp8 else 'bf16'}_t")
+    _run(gpu, launches)
+    got = c.numpy() if out == dt.float32 else dt.to_float32(c.numpy())
+    if out == dt.float32:
+        np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
+    else:
+        _close(got, ref, axis=-1)
+
+
+@pytest.mark.parametrize("fp8,M,Nn,Kk", [(False, 8, 1536, 2048), (True, 8, 1024, 4096), (True, 32, 520, 1024)])
+def test_gemv_mfma_nt_swiglu(gpu, fp8, M, Nn, Kk):
+    rng = np.random.default_rng(Nn + Kk + M)
+    x = N.bf16_round(rng.standard_normal((M, Kk)))
+    wg, sg, mg = _weights(rng, "nt", Nn, Kk, fp8)
+    wu, su, mu = _weights(rng, "nt", Nn, Kk, fp8)
+    ref = K.silu(x.astype(np.float64) @ mg) * (x.astype(np.float64) @ mu)
+    t = [DeviceTensor.from_numpy(v) for v in (dt.to_bf16(x), wg, wu)]
+    kw = {}
+    if fp8:
+        s = [DeviceTensor.from_numpy(v) for v in (sg, su)]
+        kw = {"scale_ptr": s[0].ptr, "up_scale_ptr": s[1].ptr}
+    h = DeviceTensor.empty((M, Nn), dt.bfloat16)
+    ws = DeviceTensor.empty((LA.gemv_mfma_workspace_bytes(M, Nn, Kk, swiglu=True),), dt.uint8)
+    launches = LA.gemv_mfma(t[0].ptr, t[1].ptr, h.ptr, M, Nn, Kk, c_dtype=dt.bfloat16, ws_ptr=ws.ptr, layout="nt",
+                            b_dtype=dt.float8_e4m3fn if fp8 else dt.bfloat16, up_ptr=t[2].ptr, **kw)
+    assert "_swiglu_t" in launches[0].symbol
+    _run(gpu, launches)
+    _close(dt.to_float32(h.numpy()), ref, axis=-1)
+
+
+def test_fp8_decode_batch_projection_lowers_to_mfma_nt(gpu):
+    """A traced 8-token fp8 projection (x @ dequant(W)^T with per-output
+    scales, as the fp8 decoder layer's) takes the MFMA few-row NT form."""
+    from nkipy_amd.kernels.decoder import linear_fp8
+    from nkipy_amd.runtime import DeviceKernel, baremetal_jit
+
+    def proj(x, w, s):
+        return linear_fp8(x, w, s).astype(x.dtype)
+
+    rng = np.random.default_rng(8)
+    x = N.bf16_round(rng.standard_normal((8, 1, 4096)))
+    wdev, scale, wmat = _weights(rng, "nt", 6144, 4096, True)
+    args = [dt.to_bf16(x), wdev, scale]
+    dk = DeviceKernel.compile_and_load(proj, *args)
+    assert dk.plan.kernel_kinds == ["gemm"]
+    (step,) = dk.plan.steps
+    assert [l.symbol for l in step.launches(lambda v: 1 << 40)] == ["nk_gemv_mfma_nt_e4m3_t1", "nk_gemv_out_bf16"]
+    got = dt.to_float32(baremetal_jit(proj)(*args))
+    _close(got, x.astype(np.float64) @ wmat, axis=-1)
+
+
 def test_gemv_mfma_against_valu_form(gpu):
     """The same operands through the MFMA and the VALU few-row kernels: fp32
     results within the difference of two summation orders."""

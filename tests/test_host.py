@@ -358,6 +358,22 @@ def test_few_row_projection_forms_split_and_route():
     assert LA.gemv_mfma_preferred(1, 4096, 4096) and LA.gemv_mfma_preferred(16, 24576, 14336)
     assert LA.gemv_mfma_preferred(32, 6144, 4096) and not LA.gemv_mfma_preferred(32, 4096, 14336)
     assert not LA.gemv_mfma_preferred(33, 64, 64) and not LA.gemv_mfma_preferred(0, 64, 64)
+    # NT weights: one row stays on the VALU form; no fp8 NN form
+    assert not LA.gemv_mfma_preferred(1, 4096, 4096, layout="nt")
+    assert LA.gemv_mfma_preferred(2, 4096, 4096, layout="nt", fp8=True)
+    assert not LA.gemv_mfma_preferred(8, 4096, 4096, layout="nn", fp8=True)
+    nt = LA.gemv_mfma(A, A, A, 8, 1000, 336, c_dtype=dt.bfloat16, ws_ptr=A, layout="nt",
+                      b_dtype=dt.float8_e4m3fn, scale_ptr=A)
+    assert [l.symbol for l in nt] == ["nk_gemv_mfma_nt_e4m3_t1", "nk_gemv_out_bf16"] and nt[0].args.flags & LA.GEMM_SCALE
+    with pytest.raises(LA.LaunchError):
+        LA.gemv_mfma(A, A, A, 8, 1000, 328, c_dtype=dt.bfloat16, ws_ptr=A, layout="nt",
+                     b_dtype=dt.float8_e4m3fn, scale_ptr=A)  # fp8 K % 16
+    with pytest.raises(LA.LaunchError):
+        LA.gemv_mfma(A, A, A, 8, 1000, 336, c_dtype=dt.bfloat16, ws_ptr=A, layout="nt",
+                     b_dtype=dt.float8_e4m3fn)  # fp8 without scales
+    with pytest.raises(LA.LaunchError):
+        LA.gemv_mfma(A, A, A, 8, 1024, 1024, c_dtype=dt.bfloat16, ws_ptr=A, b_dtype=dt.float8_e4m3fn,
+                     scale_ptr=A)  # fp8 NN
     with pytest.raises(LA.LaunchError):
         LA.gemv_mfma(A, A, A, 33, 64, 64, c_dtype=dt.bfloat16, ws_ptr=A)  # rows
     with pytest.raises(LA.LaunchError):
