@@ -110,3 +110,12 @@ def assert_matches_numpy(got, ref, what: str):
     bound = tol * np.abs(r) + tol * scale
     bad = err > bound
     assert not bad.any(), f"{what}: {int(bad.sum())} of {r.size} out of tolerance, max abs {err.max():.3e}"
+
+
+def launch_symbols(plan):
+    """Kernel symbols of a plan's launches in order, for a freshly lowered
+    plan or for one loaded from the artefact cache (a kernel compiled
+    earlier in the same process with the same graph)."""
+    if hasattr(plan, "records"):
+        return [r.symbol for r in plan.records]
+    return [l.symbol for st in plan.steps for l in st.launches(lambda v: 1 << 40)]

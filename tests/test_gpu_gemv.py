@@ -9,7 +9,7 @@ import os
 
 import numpy as np
 import pytest
-from parity import assert_close
+from parity import assert_close, launch_symbols
 
 from nkipy_amd.core import dtypes as dt
 from nkipy_amd.dispatch import launchers as LA
@@ -156,8 +156,7 @@ def test_decode_projection_lowers_to_gemv(gpu, layout, symbol):
     args = [dt.to_bf16(a) for a in (x, w)]
     dk = DeviceKernel.compile_and_load(proj, *args)
     assert dk.plan.kernel_kinds == ["gemm"]
-    (step,) = dk.plan.steps
-    assert [l.symbol for l in step.launches(lambda v: 1 << 40)] == [symbol, "nk_gemv_out_bf16"]
+    assert launch_symbols(dk.plan) == [symbol, "nk_gemv_out_bf16"]
     got = dt.to_float32(baremetal_jit(proj)(*args))
     wm = w.astype(np.float64) if layout == "nn" else w.astype(np.float64).T
     _close(got, x.astype(np.float64) @ wm, axis=-1)
@@ -314,8 +313,7 @@ def test_fp8_decode_batch_projection_lowers_to_mfma_nt(gpu):
     args = [dt.to_bf16(x), wdev, scale]
     dk = DeviceKernel.compile_and_load(proj, *args)
     assert dk.plan.kernel_kinds == ["gemm"]
-    (step,) = dk.plan.steps
-    assert [l.symbol for l in step.launches(lambda v: 1 << 40)] == ["nk_gemv_mfma_nt_e4m3_t1", "nk_gemv_out_bf16"]
+    assert launch_symbols(dk.plan) == ["nk_gemv_mfma_nt_e4m3_t1", "nk_gemv_out_bf16"]
     got = dt.to_float32(baremetal_jit(proj)(*args))
     _close(got, x.astype(np.float64) @ wmat, axis=-1)
 
@@ -448,7 +446,6 @@ def test_decode_batch_projection_lowers_to_splitk(gpu, M, symbol):
     w = N.bf16_round(rng.standard_normal((4096, 6144)) * 0.02)
     args = [dt.to_bf16(a) for a in (x, w)]
     dk = DeviceKernel.compile_and_load(proj, *args)
-    (step,) = dk.plan.steps
-    assert [l.symbol for l in step.launches(lambda v: 1 << 40)] == [symbol, "nk_gemv_out_bf16"]
+    assert launch_symbols(dk.plan) == [symbol, "nk_gemv_out_bf16"]
     got = dt.to_float32(baremetal_jit(proj)(*args))
     _close(got, x.astype(np.float64) @ w.astype(np.float64), axis=-1)
