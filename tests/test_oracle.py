@@ -195,6 +195,41 @@ def test_qwen3_head_prologue_matches_torch_bf16_ops():
         np.testing.assert_allclose(a, b, rtol=2 ** -7, atol=1e-6)
 
 
+def test_greedy_sampling_matches_torch_bf16_ops():
+    """The composed greedy sampling against an independent evaluation on
+    torch bfloat16 tensors: RMSNorm in fp32 with the weight, cast to bf16,
+    the last position's logits as an fp32 product rounded to bf16, argmax.
+    Every row's index attains the torch maximum, and equals torch's argmax
+    where that maximum is unique; the first position or a norm without its
+    weight picks other tokens."""
+    rng = np.random.default_rng(31)
+    B, S, H, V = 6, 5, 64, 1000
+    h = N.bf16_round(rng.standard_normal((B, S, H)))
+    w = N.bf16_round(rng.uniform(0.2, 3.0, H))
+    lm = N.bf16_round(rng.standard_normal((H, V)))
+    idx = K.greedy_sampling_bf16(h, w, lm, 1e-6).reshape(-1)
+    bt = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16)
+
+    def torch_logits(last, weight):
+        hf = bt(h).to(torch.float32)
+        ms = (hf * hf).mean(-1, keepdim=True) + 1e-6
+        hn = hf / torch.sqrt(ms)
+        if weight:
+            hn = hn * bt(w).to(torch.float32)
+        hn = hn.to(torch.bfloat16).to(torch.float32)
+        row = hn[:, -1 if last else 0, :]
+        return (row @ bt(lm).to(torch.float32)).to(torch.bfloat16).to(torch.float32).numpy()
+
+    lg = torch_logits(True, True)
+    mx = lg.max(-1)
+    np.testing.assert_array_equal(lg[np.arange(B), idx], mx)
+    unique = (lg == mx[:, None]).sum(-1) == 1
+    assert unique.sum() >= B - 1
+    np.testing.assert_array_equal(idx[unique], lg.argmax(-1)[unique])
+    assert (torch_logits(False, True).argmax(-1) != idx).any()
+    assert (torch_logits(True, False).argmax(-1) != idx).any()
+
+
 def test_rope_split_half_is_the_complex_rotation():
     rng = np.random.default_rng(11)
     x = N.bf16_round(rng.standard_normal((2, 9, 3, 16)))
