@@ -26,4 +26,18 @@ Pins (tests/test_oracle.py):
   * decoder layer    -- composed of the pinned parts above plus RoPE (pinned by
                         rotation-norm invariance and position 0 = identity) and
                         causal attention (pinned by a float64 per-query loop).
+  * Qwen3 forms      -- the bf16 softmax steps, the bf16-step RoPE, the head
+                        prologue, decode and prefill attention with their cast
+                        points, and greedy sampling: each against torch's
+                        op-by-op evaluation on bfloat16 tensors (bit for bit
+                        where no fp32 sum is involved); decode attention
+                        without casts equals the last row of causal attention.
+                        The decode layer is composed of these parts.
+
+Parity unpinned: the accumulation of bf16 reductions.  The oracle (like this
+backend and torch) sums a bf16 row in fp32 and rounds once; the reference's
+reduce keeps its accumulator in the input dtype
+(nkipy/src/nkipy/core/ops/reduce.py:66-79), and no fixture says what its CPU
+path returns for a bf16 np.sum (ml_dtypes is absent).  This reaches the row
+sums of the Qwen3 softmax (decode and prefill).
 """
