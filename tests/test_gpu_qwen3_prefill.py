@@ -99,7 +99,9 @@ def test_bf16_attention_unmasked_statistics_chunks(gpu):
     rng = np.random.default_rng(29)
     q, k, v = (N.bf16_round(rng.standard_normal((B, S, h, D))) for h in (Hq, Hkv, Hkv))
     args = [dt.to_bf16(a) for a in (q, k, v)]
-    dk = DeviceKernel.compile_and_load(bf16_attention, *args, name="bf16_attention_unmasked")
+    # (a fresh lowering: the test reads the plan's launch arguments)
+    dk = DeviceKernel.compile_and_load(bf16_attention, *args, name="bf16_attention_unmasked",
+                                       use_cached_if_exists=False)
     assert dk.plan.kernel_kinds == ["attention"], dk.plan.kernel_kinds
     (launches,) = [st.launches(lambda v: 1 << 40) for st in dk.plan.steps]
     assert [l.args.causal for l in launches] == [0, 0, 0] and launches[0].args.nch == 5
@@ -118,7 +120,8 @@ def test_prefill_attention_long_rows_many_chunks(gpu):
     q = N.bf16_round(rng.standard_normal((B, S, Hq, D)))
     ck, cv = (N.bf16_round(rng.standard_normal((B, MAXS, Hkv, D))) for _ in range(2))
     args = [dt.to_bf16(a) for a in (q, ck, cv)]
-    dk = DeviceKernel.compile_and_load(prefill_attention_kernel, *args, name="prefill_long")
+    dk = DeviceKernel.compile_and_load(prefill_attention_kernel, *args, name="prefill_long",
+                                       use_cached_if_exists=False)
     (launches,) = [st.launches(lambda v: 1 << 40) for st in dk.plan.steps]
     assert (launches[0].args.ckb, launches[0].args.nch) == (20, 8)
     ins = {n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(dk.input_tensors_info, args)}
