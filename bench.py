@@ -205,13 +205,14 @@ class Marker:
             self.mark(END_MARK)
 
 
-def _time_steps(bounds, steps, warmup, rt):
+def _time_steps(bounds, steps, warmup, rt, graph=False):
     """Mean milliseconds per step over ``steps`` steps run round robin over
     the bound plans, back to back on the runtime stream, bracketed by HIP
     events (event pairs around every launch would insert markers between
-    kernels)."""
+    kernels); ``graph`` replays each plan as its captured HIP graph."""
+    run = (lambda b: b.run_graph()) if graph else (lambda b: b.run())
     for i in range(warmup):
-        bounds[i % len(bounds)].run()
+        run(bounds[i % len(bounds)])
     rt.sync()
     # The part ramps its clocks over the first ~20 ms of sustained load, so
     # the timed region starts after DEVICE_WARM_S of the same work.
@@ -219,13 +220,13 @@ def _time_steps(bounds, steps, warmup, rt):
     i = 0
     while time.perf_counter() < t_end:
         for _ in range(16):
-            bounds[i % len(bounds)].run()
+            run(bounds[i % len(bounds)])
             i += 1
         rt.sync()
     e0, e1 = rt.event(), rt.event()
     e0.record()
     for k in range(steps):
-        bounds[k % len(bounds)].run()
+        run(bounds[k % len(bounds)])
     e1.record()
     rt.sync()
     total = e0.elapsed_ms(e1)
@@ -710,14 +711,15 @@ def _decode_case(B, rt):
     return dk, sets, bounds, host
 
 
-def _sync_call_us(dk, ins, outs, n=50):
+def _sync_call_us(dk, ins, outs, n=50, graph=False):
     """One synchronous call at a time (host dispatch, launches, wait): the
-    latency a serving loop that waits for each token sees."""
+    latency a serving loop that waits for each token sees; ``graph`` replays
+    the step as one captured HIP graph."""
     for _ in range(10):
-        dk(ins, outs)
+        dk(ins, outs, graph=graph)
     t0 = time.perf_counter()
     for _ in range(n):
-        dk(ins, outs)
+        dk(ins, outs, graph=graph)
     return (time.perf_counter() - t0) / n * 1e6
 
 
@@ -736,6 +738,8 @@ def bench_qwen3_decode(a, rt, mk):
     mk.end()  # the synchronous calls and the other batch sizes below are not labelled
     ins0, outs0 = sets[0]
     sync_us = _sync_call_us(dk, ins0, outs0)
+    sync_graph_us = _sync_call_us(dk, ins0, outs0, graph=True)
+    graph_ms = _time_steps(bounds, steps, warm, rt, graph=True)
     step_rec = {"label": "step", "kernel": " + ".join(l.symbol for l in bounds[0].launches), "bound": "hbm"}
     roof = _roofline(7, step_rec, us=ms * 1e3, work=_decode_step_bytes(B))
     roof["traffic"] = None
@@ -747,6 +751,7 @@ def bench_qwen3_decode(a, rt, mk):
         wb = _decode_step_bytes(b)
         batches.append({"batch": b, "us_per_step": round(msb * 1e3, 2),
                         "synchronous_call_us": round(_sync_call_us(dkb, *setsb[0]), 1),
+                        "synchronous_graph_call_us": round(_sync_call_us(dkb, *setsb[0], graph=True), 1),
                         "launches": len(boundsb[0].launches), "bytes": wb,
                         "achieved_GBs": round(wb / (msb * 1e-3) / 1e9, 1),
                         "frac": round(wb / (msb * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
@@ -756,10 +761,12 @@ def bench_qwen3_decode(a, rt, mk):
                        "kv_heads": Hkv, "head_dim": D},
              "dtype": "bf16 (the traced cast points of the Qwen3 attention layer)",
              "us_per_step": round(ms * 1e3, 2), "synchronous_call_us": round(sync_us, 1),
+             "us_per_step_graph": round(graph_ms * 1e3, 2), "synchronous_graph_call_us": round(sync_graph_us, 1),
              "roofline": roof, "kernels": recs, "other_batches": batches,
              "note": "one token per sequence through the whole attention layer (QKV projection, q / k norm and "
                      "RoPE, cache writes, attention over pos + 1 cached rows, output projection); steps queued "
-                     "back to back over rotating weight / cache sets; synchronous_call_us waits for each step"}
+                     "back to back over rotating weight / cache sets; synchronous_call_us waits for each step; the "
+                     "_graph figures replay each step as one captured HIP graph"}
 
     def cpu():
         from oracle import kernels as K

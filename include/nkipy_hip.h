@@ -135,6 +135,25 @@ int nkh_launch_batch(int count, void *const *functions,
                      const size_t *kernarg_offsets,
                      const size_t *kernarg_sizes);
 
+/* Graph replay of a batch: the launches of nkh_launch_batch (same arrays,
+ * count >= 1) are captured once from the runtime stream into a HIP graph,
+ * which nkh_graph_launch replays on that stream with one host call and no
+ * per-launch argument handling: the argument blocks are copied at capture,
+ * so the device addresses in them are fixed for the graph's lifetime.  The
+ * reference replays a loaded model through nrt_execute per call
+ * (spike/src/model.cpp:90-110); this is that replay for serving loops whose
+ * host dispatch of many small launches would otherwise show.  Graphs are
+ * released by nkh_graph_destroy (which drains the stream first) or at
+ * nkh_shutdown; a handle not created by this runtime, or already destroyed,
+ * is NKH_ERR_INVALID. */
+int nkh_graph_create(int count, void *const *functions,
+                     const unsigned *grids, const unsigned *blocks,
+                     const unsigned *shared, const uint8_t *kernargs,
+                     const size_t *kernarg_offsets,
+                     const size_t *kernarg_sizes, void **graph);
+int nkh_graph_launch(void *graph);
+int nkh_graph_destroy(void *graph);
+
 /* Chunked causal linear attention, phi = elu + 1, chunk 64, d = d_v = 128:
  * o[s, t, :] = sum_{u<=t} (phi(q_t).phi(k_u)) v_u / sum_{u<=t} phi(q_t).phi(k_u)
  * over `bh` sequences of `t` tokens; q, k, v, o are (bh, t, 128) bf16,

@@ -37,6 +37,7 @@ struct Runtime {
   std::map<uintptr_t, size_t> allocations;  // base -> bytes
   std::set<hipModule_t> modules;
   std::set<hipEvent_t> events;
+  std::set<hipGraphExec_t> graphs;
 };
 
 Runtime g_rt;
@@ -183,6 +184,8 @@ int nkh_shutdown(void) {
   g_rt.modules.clear();
   for (auto ev : g_rt.events) hipEventDestroy(ev);
   g_rt.events.clear();
+  for (auto g : g_rt.graphs) hipGraphExecDestroy(g);
+  g_rt.graphs.clear();
   hipStreamDestroy(g_rt.stream);
   g_rt.stream = nullptr;
   g_rt.device = -1;
@@ -443,6 +446,73 @@ int nkh_launch_batch(int count, void *const *functions, const unsigned *grids,
       return rc;
     }
   }
+  return NKH_OK;
+}
+
+int nkh_graph_create(int count, void *const *functions, const unsigned *grids,
+                     const unsigned *blocks, const unsigned *shared,
+                     const uint8_t *kernargs, const size_t *kernarg_offsets,
+                     const size_t *kernarg_sizes, void **graph) {
+  if (!graph) return set_error(NKH_ERR_INVALID, "graph output pointer is null");
+  *graph = nullptr;
+  if (count <= 0) return set_error(NKH_ERR_INVALID, "a graph needs at least one launch");
+  if (!functions || !grids || !blocks || !shared || !kernargs ||
+      !kernarg_offsets || !kernarg_sizes)
+    return set_error(NKH_ERR_INVALID, "null array in nkh_graph_create");
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc = require_init();
+  if (rc) return rc;
+  // Capture records the launches (kernel nodes with their argument blocks
+  // copied) on the runtime stream; nothing runs until nkh_graph_launch.
+  NKH_HIP(hipStreamBeginCapture(g_rt.stream, hipStreamCaptureModeThreadLocal),
+          "hipStreamBeginCapture");
+  for (int i = 0; i < count && !rc; ++i) {
+    rc = launch_locked(functions[i], grids[3 * i], grids[3 * i + 1],
+                       grids[3 * i + 2], blocks[3 * i], blocks[3 * i + 1],
+                       blocks[3 * i + 2], shared[i],
+                       kernargs + kernarg_offsets[i], kernarg_sizes[i]);
+    if (rc) g_last_error = "launch " + std::to_string(i) + " of graph: " + g_last_error;
+  }
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(g_rt.stream, &g);
+  if (rc) {
+    if (g) hipGraphDestroy(g);
+    return rc;
+  }
+  if (e != hipSuccess) return hip_error(e, "hipStreamEndCapture");
+  hipGraphExec_t exec = nullptr;
+  e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  if (e != hipSuccess) return hip_error(e, "hipGraphInstantiate");
+  g_rt.graphs.insert(exec);
+  *graph = exec;
+  return NKH_OK;
+}
+
+int nkh_graph_launch(void *graph) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc = require_init();
+  if (rc) return rc;
+  auto it = g_rt.graphs.find(reinterpret_cast<hipGraphExec_t>(graph));
+  if (it == g_rt.graphs.end())
+    return set_error(NKH_ERR_INVALID, "not a live graph of this runtime");
+  NKH_HIP(hipGraphLaunch(*it, g_rt.stream), "hipGraphLaunch");
+  return NKH_OK;
+}
+
+int nkh_graph_destroy(void *graph) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  int rc = require_init();
+  if (rc) return rc;
+  auto it = g_rt.graphs.find(reinterpret_cast<hipGraphExec_t>(graph));
+  if (it == g_rt.graphs.end())
+    return set_error(NKH_ERR_INVALID, "not a live graph of this runtime");
+  // a replay still queued keeps its own reference: the stream is drained
+  // first so that the executable is not released under it
+  NKH_HIP(hipStreamSynchronize(g_rt.stream), "hipStreamSynchronize");
+  hipGraphExec_t g = *it;
+  g_rt.graphs.erase(it);
+  NKH_HIP(hipGraphExecDestroy(g), "hipGraphExecDestroy");
   return NKH_OK;
 }
 

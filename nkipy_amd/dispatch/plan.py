@@ -143,6 +143,7 @@ class BoundPlan:
         self._kernargs = bytes(buf)
         self._offsets = (sz * n)(*offsets)
         self._sizes = (sz * n)(*[len(b) for b in blobs])
+        self._graph = None
 
     def run(self):
         from nkipy_amd.runtime.hip import _check, check_current
@@ -157,6 +158,37 @@ class BoundPlan:
             ),
             "plan launch",
         )
+
+    def run_graph(self):
+        """The launches replayed as one HIP graph, captured on the first call
+        (``nkh_graph_create``): one host call per execution, whatever the
+        launch count.  The graph holds copies of the packed argument blocks,
+        so it stays valid as long as the addresses bound here do."""
+        from nkipy_amd.runtime.hip import _check, check_current
+
+        check_current(self.rt, "plan")
+        if self._n == 0:
+            return
+        if self._graph is None:
+            h = ctypes.c_void_p()
+            _check(
+                self.rt.lib.nkh_graph_create(
+                    self._n, self._fns, self._grids, self._blocks, self._shared,
+                    self._kernargs, self._offsets, self._sizes, ctypes.byref(h),
+                ),
+                "plan graph capture",
+            )
+            self._graph = h.value
+        _check(self.rt.lib.nkh_graph_launch(ctypes.c_void_p(self._graph)), "plan graph launch")
+
+    def release_graph(self):
+        """Destroys the captured graph, if any (the runtime drains its stream
+        first); a runtime already shut down released it itself."""
+        from nkipy_amd.runtime.hip import _check
+
+        g, self._graph = self._graph, None
+        if g is not None and not self.rt.is_closed:
+            _check(self.rt.lib.nkh_graph_destroy(ctypes.c_void_p(g)), "plan graph release")
 
     def run_range(self, start: int, stop: int):
         """Launches ``start .. stop-1`` of the plan (all of them: ``run``)."""
@@ -265,13 +297,18 @@ class PlanExecutor:
             for name, idx in plan.output_buffers.items():
                 bases[idx] = io_ptrs[name]
             if len(self._bound) > 64:
+                self._release_graphs()
                 self._bound.clear()
             bp = self._bind(bases)
             self._bound[key] = bp
         return bp
 
-    def run(self, io_ptrs: Dict[str, int]):
-        self.bind(io_ptrs).run()
+    def run(self, io_ptrs: Dict[str, int], graph: bool = False):
+        bp = self.bind(io_ptrs)
+        if graph:
+            bp.run_graph()
+        else:
+            bp.run()
 
     def run_checks(self):
         """The plan's host-side checks (:data:`CHECKS`) over what the last
@@ -284,6 +321,10 @@ class PlanExecutor:
             self.rt.d2h(words.ctypes.data, buf.ptr + int(c["offset"]), 4 * count)
             CHECKS[c["kind"]](words, c.get("desc", ""))
 
+    def _release_graphs(self):
+        for bp in self._bound.values():
+            bp.release_graph()
+
     def forget(self):
         """Drop every bound launch list and owned buffer without touching the
         device (the runtime they belong to is gone)."""
@@ -291,6 +332,7 @@ class PlanExecutor:
         self._bound.clear()
 
     def close(self):
+        self._release_graphs()
         for b in self._owned.values():
             b.free()
         self._owned.clear()

@@ -285,7 +285,14 @@ class DeviceKernel:
         return hits
 
     def __call__(self, inputs: Dict[str, DeviceTensor], outputs: Dict[str, DeviceTensor] = None,
-                 save_trace: bool = False, ntff_name: Optional[str] = None, sync: bool = True):
+                 save_trace: bool = False, ntff_name: Optional[str] = None, sync: bool = True,
+                 graph: bool = False):
+        """Runs the kernel on ``inputs`` into ``outputs`` (allocated when
+        None and returned).  ``sync`` waits for the launches and runs the
+        plan's host checks; ``graph`` replays the launches as one HIP graph
+        captured on the first call with these tensors (a serving loop that
+        calls with the same tensors every step pays one host call per step);
+        ``save_trace`` writes a per-launch profile instead."""
         auto = outputs is None
         if auto:
             outputs = {t.name: t for t in self.allocate_output_tensors()}
@@ -311,12 +318,12 @@ class DeviceKernel:
                     shape, dtype = self._out_specs[on]
                     st = self._staging[on] = DeviceTensor.empty(shape, dtype, name=on)
                 run_outputs[on] = st
-            self._execute(self._io_ptrs(inputs, run_outputs), save_trace, ntff_name)
+            self._execute(self._io_ptrs(inputs, run_outputs), save_trace, ntff_name, graph)
             rt = get_runtime()
             for on in staged:
                 rt.d2d(outputs[on].ptr, run_outputs[on].ptr, outputs[on].nbytes)
         else:
-            self._execute(self._io_ptrs(inputs, outputs), save_trace, ntff_name)
+            self._execute(self._io_ptrs(inputs, outputs), save_trace, ntff_name, graph)
         if sync:
             get_runtime().sync()
             # words the kernels left for the host (e.g. the linear-attention
@@ -335,9 +342,10 @@ class DeviceKernel:
             return os.path.splitext(str(self.neff_path))[0] + ".ntff"
         return f"{self.name}.ntff"
 
-    def _execute(self, io_ptrs: Dict[str, int], save_trace: bool, ntff_name: Optional[str]):
+    def _execute(self, io_ptrs: Dict[str, int], save_trace: bool, ntff_name: Optional[str],
+                 graph: bool = False):
         if not save_trace:
-            self.executor.run(io_ptrs)
+            self.executor.run(io_ptrs, graph=graph)
             return
         self._run_profiled(io_ptrs, self.trace_path(ntff_name))
 

@@ -97,6 +97,9 @@ def _bind(lib):
             ctypes.c_int,
         ),
     }
+    sigs["nkh_graph_create"] = (sigs["nkh_launch_batch"][0] + [ctypes.POINTER(vp)], ctypes.c_int)
+    sigs["nkh_graph_launch"] = ([vp], ctypes.c_int)
+    sigs["nkh_graph_destroy"] = ([vp], ctypes.c_int)
     sigs["nkh_profile_range_push"] = ([ctypes.c_char_p, c_int_p], ctypes.c_int)
     sigs["nkh_profile_range_pop"] = ([], ctypes.c_int)
     i64 = ctypes.c_int64
@@ -120,6 +123,7 @@ EXPORTED_SYMBOLS = (
     "nkh_event_destroy", "nkh_event_record", "nkh_event_elapsed_ms",
     "nkh_launch_batch", "nkh_linear_attention_workspace_size", "nkh_linear_attention",
     "nkh_linear_attention_noalloc", "nkh_profile_range_push", "nkh_profile_range_pop",
+    "nkh_graph_create", "nkh_graph_launch", "nkh_graph_destroy",
 )
 
 _lib = None

@@ -249,3 +249,75 @@ def test_bf16_decode_loop_fused_generic_and_reloaded(gpu, tmp_path):
     np.testing.assert_array_equal(dt.numpy_storage(out2["output0"].numpy()), dt.numpy_storage(f_outs[-1]))
     np.testing.assert_array_equal(dt.numpy_storage(out2["cache_k"].numpy()), dt.numpy_storage(f_ck))
     np.testing.assert_array_equal(dt.numpy_storage(out2["cache_v"].numpy()), dt.numpy_storage(f_cv))
+
+
+def test_bf16_decode_loop_graph_replay_equals_launches(gpu, tmp_path):
+    """The fused bf16 decode step replayed as one HIP graph (captured on the
+    first call with the loop's tensors, reused on every later step, the
+    token and position rewritten in place between steps) equals the same
+    step launched one kernel at a time on a second copy of the caches, bit
+    for bit at every step, with the eager step and a synchronisation between
+    consecutive replays."""
+    import ctypes
+
+    from nkipy_amd.core import dtypes as dt
+    from nkipy_amd.kernels.qwen3 import qwen3_attention_kernel
+    from nkipy_amd.runtime.hip import SpikeError, _check, get_runtime
+    from oracle import numerics as N
+
+    Bb, Sb, MAXSb, Hb, Db, HKVb = 2, 64, 256, 4, 128, 2
+    HIDb = Hb * Db
+
+    def pre(x, qkv_weight, q_norm_weight, k_norm_weight, cache_k, cache_v, o_weight):
+        return qwen3_attention_kernel(x, qkv_weight, q_norm_weight, k_norm_weight, EPS, Hb, Db, HKVb,
+                                      cache_k, cache_v, None, o_weight)
+
+    def dec(x, qkv_weight, q_norm_weight, k_norm_weight, cache_k, cache_v, start_pos, o_weight):
+        return qwen3_attention_kernel(x, qkv_weight, q_norm_weight, k_norm_weight, EPS, Hb, Db, HKVb,
+                                      cache_k, cache_v, start_pos, o_weight)
+
+    rng = np.random.default_rng(29)
+    bf = lambda a: dt.to_bf16(N.bf16_round(a))
+    w = {"qkv_weight": bf(rng.standard_normal((HIDb, (Hb + 2 * HKVb) * Db)) * 0.05),
+         "q_norm_weight": bf(rng.uniform(0.5, 1.5, Db)), "k_norm_weight": bf(rng.uniform(0.5, 1.5, Db)),
+         "o_weight": bf(rng.standard_normal((Hb * Db, HIDb)) * 0.05)}
+    x0 = bf(rng.standard_normal((Bb, Sb, HIDb)))
+    toks = [bf(rng.standard_normal((Bb, 1, HIDb))) for _ in range(5)]
+    zeros = bf(np.zeros((Bb, MAXSb, HKVb, Db)))
+    pos0 = np.array([Sb], np.int32)
+    build = str(tmp_path / "build")
+    kp = DeviceKernel.compile_and_load(pre, x0, w["qkv_weight"], w["q_norm_weight"], w["k_norm_weight"],
+                                       zeros, zeros, w["o_weight"], build_dir=build)
+    kd = DeviceKernel.compile_and_load(dec, toks[0], w["qkv_weight"], w["q_norm_weight"], w["k_norm_weight"],
+                                       zeros, zeros, pos0, w["o_weight"], build_dir=build)
+    assert "decode_attention" in kd.plan.kernel_kinds, kd.plan.kernel_kinds
+    dw = {k: DeviceTensor.from_numpy(v, name=k) for k, v in w.items()}
+    sets = []
+    for _ in range(2):
+        ck = DeviceTensor.from_numpy(zeros, name="cache_k")
+        cv = DeviceTensor.from_numpy(zeros, name="cache_v")
+        hs = DeviceTensor.from_numpy(x0, name="hidden_states")
+        kp(inputs=_layer_inputs(dw, hs, ck, cv), outputs={"output0": hs, "cache_k": ck, "cache_v": cv})
+        sets.append((ck, cv, DeviceTensor.from_numpy(toks[0], name="x"),
+                     DeviceTensor.from_numpy(pos0, name="start_pos")))
+    graphs = set()
+    for i, t in enumerate(toks):
+        outs = []
+        for (ck, cv, tok, pos), graph in zip(sets, (False, True)):
+            tok.write_from_numpy(t)
+            pos.write_from_numpy(np.array([Sb + i], np.int32))
+            kd(inputs=_layer_inputs(dw, tok, ck, cv, pos), outputs={"output0": tok, "cache_k": ck, "cache_v": cv},
+               graph=graph)
+            outs.append((tok.numpy(), ck.numpy(), cv.numpy()))
+        graphs |= {bp._graph for bp in kd.executor._bound.values() if bp._graph is not None}
+        for what, a, b in zip(("output", "cache_k", "cache_v"), *outs):
+            np.testing.assert_array_equal(dt.numpy_storage(b), dt.numpy_storage(a), err_msg=f"step {i} {what}")
+    assert len(graphs) == 1, graphs  # captured once, replayed on every later step
+    rt = get_runtime()
+    with pytest.raises(SpikeError, match="not a live graph"):
+        _check(rt.lib.nkh_graph_launch(ctypes.c_void_p(16)), "graph launch")
+    bound = list(kd.executor._bound.values())
+    kd.executor.close()  # releases the captured graph
+    assert bound and all(bp._graph is None for bp in bound)
+    with pytest.raises(SpikeError, match="not a live graph"):
+        _check(rt.lib.nkh_graph_destroy(ctypes.c_void_p(graphs.pop())), "graph release")
