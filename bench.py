@@ -132,9 +132,9 @@ def _decode_launches():
     ks2, _ = gemv_mfma_split(B, hid, H * D)
     kv = 2 * B * L * Hkv * D
     return [("qkv_partials", "hbm", 2 * hid * nqkv + 2 * B * hid + 4 * ks1 * B * nqkv),
-            ("qkv_reduce", "hbm", 4 * ks1 * B * nqkv + 2 * B * nqkv),
-            # q, k, v heads in; q out, k / v into the caches' rows at pos
-            ("head_rope_cache_rows", "hbm", 2 * B * (H + 2 * Hkv) * D + 2 * B * (H + 2 * Hkv) * D),
+            # the q, k, v heads' partial sums in (added here); q out, k / v
+            # into the caches' rows at pos
+            ("head_rope_cache_rows", "hbm", 4 * ks1 * B * nqkv + 2 * B * (H + 2 * Hkv) * D),
             ("scores", "hbm", kv + 4 * B * H * L),
             ("rowstat", "hbm", 4 * B * H * L),
             ("values", "hbm", kv + 4 * B * H * L + 4 * B * H * nsp * D),

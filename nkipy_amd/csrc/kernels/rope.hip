@@ -114,6 +114,13 @@ extern "C" __global__ __launch_bounds__(256) void nk_rope_bf16(RopeArgs a) {
 // position axis (the cache write cache[:, pos] = k of one decode token): the
 // scatter kernel's rule, negative counts from the end and a position outside
 // the o_rows positions drops the store.
+// HR_PLANES: x addresses the fp32 partial sums of the projection that
+// produced the rows (nplanes planes of `plane` elements, the layout of the
+// few-row projections' workspace) instead of its bf16 output; the planes
+// are added as nk_gemv_out_bf16 adds them (plane p into sum p mod 4 in
+// order from 0, then (s0 + s1) + (s2 + s3), then + 0 and the bf16 rounding),
+// so the rows equal that kernel's output bit for bit and its launch is
+// saved.
 // ---------------------------------------------------------------------------
 struct HeadRopeTarget {
   const uint16_t *x;         // bf16 input rows, d contiguous
@@ -138,9 +145,13 @@ struct HeadRopeArgs {
   int64_t t_ss;        // table element stride over s
   int64_t t_rows;      // table rows (runtime row clamp)
   int32_t S, D, tflags, pad;
+  int64_t plane;       // HR_PLANES: elements per partial-sum plane
+  int32_t nplanes;     // HR_PLANES: planes (1 .. HR_MAX_PLANES)
+  int32_t pad2;
 };
 
-enum { HR_NORM = 1, HR_MUL_RECIP = 2, HR_W = 4, HR_COPY = 8 };  // per target
+enum { HR_NORM = 1, HR_MUL_RECIP = 2, HR_W = 4, HR_COPY = 8, HR_PLANES = 16 };  // per target
+constexpr int HR_MAX_PLANES = 32;
 enum { HR_TABLE_F32 = 1 };
 
 __device__ __forceinline__ float rbf(float v) { return bf16_to_f32(f32_to_bf16(v)); }
@@ -175,9 +186,41 @@ extern "C" __global__ __launch_bounds__(256) void nk_head_rope_bf16(HeadRopeArgs
   const int f0 = live ? 8 * (second ? lane - hl : lane) : 0;  // first frequency of the lane
   const int64_t col = (second ? half : 0) + f0;                // element of the row
 
-  // every load first: x chunk, weight chunk, table chunks
-  const uint4 xr = *reinterpret_cast<const uint4 *>(x + (live ? b * x_sb + s * x_ss + h * x_sh
-                                                                     + (second ? x_half : 0) + f0 : 0));
+  // every load first: x chunk (or its partial sums), weight chunk, table chunks
+  const int64_t xo = live ? b * x_sb + s * x_ss + h * x_sh + (second ? x_half : 0) + f0 : 0;
+  float v[8];
+  if (flags & HR_PLANES) {
+    const float *xp = reinterpret_cast<const float *>(x) + xo;
+    const int np = a.nplanes;
+    float g[4][8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) g[j][e] = 0.f;
+#pragma unroll
+    for (int s0 = 0; s0 < HR_MAX_PLANES; s0 += 4) {
+      if (s0 >= np) break;  // uniform
+      float4 q[4][2];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 *pp = reinterpret_cast<const float4 *>(xp + (int64_t)min(s0 + j, np - 1) * a.plane);
+        q[j][0] = pp[0];
+        q[j][1] = pp[1];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (s0 + j < np) {
+          const float qv[8] = {q[j][0].x, q[j][0].y, q[j][0].z, q[j][0].w,
+                               q[j][1].x, q[j][1].y, q[j][1].z, q[j][1].w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) g[j][e] += qv[e];
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = rbf(((g[0][e] + g[1][e]) + (g[2][e] + g[3][e])) + 0.f);
+  } else {
+    unpack8(*reinterpret_cast<const uint4 *>(x + xo), v);
+  }
   uint4 wr = make_uint4(0, 0, 0, 0);
   if (flags & HR_W) wr = *reinterpret_cast<const uint4 *>(w + (live ? col : 0));
   int64_t trow = 0;
@@ -204,8 +247,6 @@ extern "C" __global__ __launch_bounds__(256) void nk_head_rope_bf16(HeadRopeArgs
     unpack8(*reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.sin_t) + to), sn);
   }
 
-  float v[8];
-  unpack8(xr, v);
 #pragma unroll
   for (int j = 0; j < 8; ++j) v[j] = live ? v[j] : 0.f;
   if (flags & HR_NORM) {

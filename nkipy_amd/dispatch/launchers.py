@@ -737,10 +737,12 @@ class HeadRopeArgs(ctypes.Structure):
     _fields_ = [("t", HeadRopeTarget * 3), ("cos_t", ctypes.c_void_p), ("sin_t", ctypes.c_void_p),
                 ("pos", ctypes.c_void_p), ("t_row", ctypes.c_int64), ("t_ss", ctypes.c_int64),
                 ("t_rows", ctypes.c_int64), ("S", ctypes.c_int32), ("D", ctypes.c_int32),
-                ("tflags", ctypes.c_int32), ("pad", ctypes.c_int32)]
+                ("tflags", ctypes.c_int32), ("pad", ctypes.c_int32),
+                ("plane", ctypes.c_int64), ("nplanes", ctypes.c_int32), ("pad2", ctypes.c_int32)]
 
 
-HR_NORM, HR_MUL_RECIP, HR_W, HR_COPY = 1, 2, 4, 8
+HR_NORM, HR_MUL_RECIP, HR_W, HR_COPY, HR_PLANES = 1, 2, 4, 8, 16
+HR_MAX_PLANES = 32  # partial-sum planes the head prologue adds itself
 HR_TABLE_F32 = 1
 
 
@@ -771,15 +773,24 @@ class HeadRopeSpec:
 
 
 def head_rope(targets, cos_ptr: int, sin_ptr: int, B: int, S: int, D: int, *, table_f32: bool,
-              pos_ptr: int = 0, table_row: int = 0, table_stride: int = 0, table_rows: int = 1) -> Launch:
+              pos_ptr: int = 0, table_row: int = 0, table_stride: int = 0, table_rows: int = 1,
+              planes: Tuple[int, int] = None) -> Launch:
     """Per-head RMSNorm (optional) and split-half rotary embedding in bf16
     steps of one or two tensors of heads (q and k) sharing cos / sin tables:
     y = bf16(norm(x)); out = [bf16(bf16(y0 c) - bf16(y1 s)), bf16(bf16(y0 s)
     + bf16(y1 c))].  Tables are read at element ``row * table_row + s *
     table_stride + f`` (fp32 rounded to bf16 when ``table_f32``, else bf16),
     with row the int32 at ``pos_ptr`` (negative from the end, clamped into
-    ``table_rows``) or 0."""
+    ``table_rows``) or 0.  ``planes = (plane, count)``: every target's x
+    addresses fp32 partial sums of a few-row projection (``count`` planes of
+    ``plane`` elements, the workspace of :func:`gemv_mfma` with ldc = N and
+    no epilogue terms), which the kernel adds as ``nk_gemv_out_bf16`` does,
+    so the projection's reduction launch is not needed."""
     targets = list(targets)
+    if planes is not None and not (0 < int(planes[1]) <= HR_MAX_PLANES and int(planes[0]) > 0
+                                   and int(planes[0]) % 8 == 0):
+        raise LaunchError(f"head_rope adds 1..{HR_MAX_PLANES} partial-sum planes of a multiple of 8 elements, "
+                          f"got {planes}")
     if not 1 <= len(targets) <= 3:
         raise LaunchError("head_rope takes one to three tensors of heads")
     if D % 16 or not 16 <= D <= 128:
@@ -807,7 +818,7 @@ def head_rope(targets, cos_ptr: int, sin_ptr: int, B: int, S: int, D: int, *, ta
             raise LaunchError("head_rope: a write at the runtime position needs the position, the output's "
                               "positions and an aligned stride")
         flags = (HR_NORM if t.norm else 0) | (HR_MUL_RECIP if t.norm and t.mul_recip else 0) | \
-            (HR_W if t.norm and t.w_ptr else 0) | (HR_COPY if t.copy else 0)
+            (HR_W if t.norm and t.w_ptr else 0) | (HR_COPY if t.copy else 0) | (HR_PLANES if planes else 0)
         args.t[i] = HeadRopeTarget(t.x_ptr, t.out_ptr, t.w_ptr or None, *[int(v) for v in t.x_strides],
                                    *[int(v) for v in t.out_strides], int(t.x_half), rows, -(-rows // 16),
                                    int(t.out_pos_stride), int(t.out_positions), float(t.eps), int(t.H), flags, 0)
@@ -816,10 +827,13 @@ def head_rope(targets, cos_ptr: int, sin_ptr: int, B: int, S: int, D: int, *, ta
     args.cos_t, args.sin_t, args.pos = cos_ptr, sin_ptr, pos_ptr or None
     args.t_row, args.t_ss, args.t_rows = int(table_row), int(table_stride), int(table_rows)
     args.S, args.D, args.tflags = S, D, HR_TABLE_F32 if table_f32 else 0
+    if planes is not None:
+        args.plane, args.nplanes = int(planes[0]), int(planes[1])
     blocks = sum(int(args.t[i].blocks) for i in range(len(targets)))
     tb = 4 if table_f32 else 2
+    xb = 4 * int(planes[1]) if planes is not None else 2
     return Launch("rope", "nk_head_rope_bf16", (blocks, 1, 1), (256, 1, 1), args,
-                  bytes=2 * rows_all * D * 2 + 2 * S * half * tb,
+                  bytes=rows_all * D * (xb + 2) + 2 * S * half * tb,
                   flops=rows_all * D * (6 + (4 if any(t.norm for t in targets) else 0)))
 
 

@@ -491,7 +491,8 @@ def default_patterns():
 
 def _build_default_patterns():
     from nkipy_amd.dispatch.patterns_attention import (
-        AttentionPattern, DecodeAttentionPattern, HeadRopePattern, QkvRopeFusion, RopePattern,
+        AttentionPattern, DecodeAttentionPattern, HeadRopePattern, ProjectionPlanesFusion, QkvRopeFusion,
+        RopePattern,
     )
     from nkipy_amd.dispatch.patterns_gemm import GemmPattern, SwigluPattern
     from nkipy_amd.dispatch.patterns_linattn import LinearAttentionPattern
@@ -501,5 +502,6 @@ def _build_default_patterns():
     # after a projection goes into the GEMM epilogue; the RoPE of q / k then
     # folds into its QKV projection
     return [LinearAttentionPattern(), DecodeAttentionPattern(), AttentionPattern(), RopePattern(), HeadRopePattern(),
-            SwigluPattern(), GemmPattern(), SoftmaxPattern(), RmsNormPattern(), QkvRopeFusion()]
+            SwigluPattern(), GemmPattern(), SoftmaxPattern(), RmsNormPattern(), QkvRopeFusion(),
+            ProjectionPlanesFusion()]
 

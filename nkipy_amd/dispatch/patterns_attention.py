@@ -206,18 +206,23 @@ class HeadRopeMatch(Match):
     def __init__(self, nodes, inputs, outputs, members, table, bsd):
         super().__init__(nodes, inputs, outputs)
         self.members, self.table, self.bsd = members, table, bsd
+        self.planes_src = None  # a GemmMatch whose partial sums this step adds (ProjectionPlanesFusion)
 
     def steps(self, plan):
         members, tb = self.members, self.table
         B, S, D = self.bsd
+
+        planes = self.planes_src.planes if self.planes_src is not None else None
 
         def make(addr):
             specs = []
             for m in members:
                 xv, nm = m["x"], m["norm"]
                 o_sp, o_rows = m.get("o_pos", (0, 0))
+                # the rows, or their fp32 partial sums at the same element offset
+                x_ptr = addr(planes[0]) + 4 * xv.offset if planes else addr(xv.base) + 2 * xv.offset
                 specs.append(LA.HeadRopeSpec(
-                    addr(xv.base) + 2 * xv.offset, addr(m["out"]), m["H"], m["x_str"], m["o_str"], m["x_half"],
+                    x_ptr, addr(m["out"]), m["H"], m["x_str"], m["o_str"], m["x_half"],
                     norm=nm is not None, eps=nm.eps if nm is not None else 0.0,
                     w_ptr=addr(nm.w) if nm is not None and nm.w is not None else 0,
                     mul_recip=bool(nm.mul_recip) if nm is not None else False,
@@ -226,13 +231,15 @@ class HeadRopeMatch(Match):
             return LA.head_rope(specs, addr(tb["cos"]) + te * tb["cos_off"], addr(tb["sin"]) + te * tb["sin_off"],
                                 B, S, D, table_f32=tb["f32"],
                                 pos_ptr=addr(tb["pos"]) if tb["pos"] is not None else 0,
-                                table_row=tb["row"], table_stride=tb["ss"], table_rows=tb["rows"])
+                                table_row=tb["row"], table_stride=tb["ss"], table_rows=tb["rows"],
+                                planes=(planes[2], planes[1]) if planes else None)
 
         parts = [(f"copy {m['H']} heads" if m.get("copy") else
                   f"{'rmsnorm + ' if m['norm'] is not None else ''}rope {m['H']} heads")
                  + (" -> cache row" if m.get("o_pos") else "") for m in members]
         desc = f"head rope B={B} S={S} D={D} bf16 steps: " + ", ".join(parts) + \
-            (" (runtime position)" if tb["pos"] is not None else "")
+            (" (runtime position)" if tb["pos"] is not None else "") + \
+            (f" from {planes[1]} partial-sum planes" if planes else "")
         return [LaunchStep("head_rope", desc, self.inputs, self.outputs, make)]
 
 
@@ -597,6 +604,59 @@ def _first_column(vw: View, n_cols: int) -> int:
     span = sum((n - 1) * s for d in vw.dims for n, s in d if n > 1 and s % n_cols)
     c = vw.offset % n_cols
     return c if c + span < n_cols else 0
+
+
+class ProjectionPlanesFusion:
+    """Hands the fp32 partial sums of a few-row projection straight to the
+    head prologue that is its only reader (the Qwen3 decode step: the QKV
+    projection of one token per sequence, then q / k norm, RoPE and the
+    cache writes, examples/models/qwen3/kernels/attention.py:44-97).  The
+    prologue adds the planes in the projection's reduction order
+    (``LA.head_rope(planes=...)``), so the bf16 projection output is never
+    written and its reduction launch is saved.  Taken only when the
+    projection has no epilogue terms (no scale, bias, residual or SwiGLU)
+    and writes bf16; the projection decides at step time whether its form
+    has planes (``GemmMatch.planes``).  Finds nothing on its own."""
+
+    def find(self, L):
+        return iter(())
+
+    def refine(self, L):
+        from nkipy_amd.dispatch.patterns_gemm import GemmMatch
+
+        gemms = {m.out.id: m for m in L.matches if isinstance(m, GemmMatch)}
+        for hm in [m for m in L.matches if isinstance(m, HeadRopeMatch)]:
+            bases = {L.match_alias.get(mb["x"].base.id, mb["x"].base).id for mb in hm.members}
+            if len(bases) != 1:
+                continue
+            gm = gemms.get(bases.pop())
+            if gm is None or not self._eligible(L, gm, hm):
+                continue
+            gm.planes_consumer = hm
+            hm.planes_src = gm
+
+    @staticmethod
+    def _eligible(L, gm, hm) -> bool:
+        out = gm.out
+        if (gm.up is not None or gm.bias is not None or gm.resid is not None or gm.w.scale is not None
+                or out.dtype != dt.bfloat16 or not gm.split_k or out.id in L.result_ids
+                or (gm.n_out is not None and gm.n_out != out.shape[-1])):
+            return False
+        # every reader of the projection (through views) is the prologue
+        work, seen = [out], {out.id}
+        while work:
+            v = work.pop()
+            for u in L.users.get(v.id, ()):
+                m = L.covered.get(id(u))
+                if m is hm:
+                    continue
+                if m is None and _is_view_node(u, True) and u.out.id not in L.result_ids:
+                    if u.out.id not in seen:
+                        seen.add(u.out.id)
+                        work.append(u.out)
+                    continue
+                return False
+        return True
 
 
 class QkvRopeFusion:

@@ -156,6 +156,11 @@ class GemmMatch(Match):
         self.n_out = n_out
         self.rnd = rnd
         self.split_k = True  # few rows: partial sums over K ranges
+        # a head prologue that adds this projection's partial sums itself
+        # (ProjectionPlanesFusion), and what it reads: (workspace slot,
+        # planes, elements per plane), set at step time
+        self.planes_consumer = None
+        self.planes = None
 
     def steps(self, plan):
         x, w, out = self.x, self.w, self.out
@@ -182,9 +187,13 @@ class GemmMatch(Match):
                   and LA.gemm_splitk_useful(M, N, K, up is not None, fp8))
         small = small or (not mfma and M <= LA.GEMV_MAX_M and not splitk)
         ws = None
+        fold = False
         if mfma:
             ws = Slot(plan.add_buffer(LA.gemv_mfma_workspace_bytes(M, N, K, up is not None), "temp",
                                       "gemv.partials"))
+            ks = LA.gemv_mfma_split(M, N, K, up is not None)[0]
+            fold = self.planes_consumer is not None and ks <= LA.HR_MAX_PLANES and N % 8 == 0
+            self.planes = (ws, ks, M * N) if fold else None
         elif small:
             ws = Slot(plan.add_buffer(LA.gemv_workspace_bytes(M, N, K, w.layout, fp8, up is not None), "temp",
                                       "gemv.partials"))
@@ -199,13 +208,15 @@ class GemmMatch(Match):
                 up_ptr = addr(up.value) + off * up.value.dtype.itemsize
                 up_scale = addr(up.scale) if up.scale is not None else 0
             if mfma:
-                return LA.gemv_mfma(addr(x), addr(w.value), addr(out), M, N, K, c_dtype=out.dtype, ldb=ldb,
-                                    layout=w.layout, b_dtype=w.value.dtype, ws_ptr=addr(ws),
-                                    bias_ptr=addr(bias) if bias is not None else 0,
-                                    scale_ptr=addr(w.scale) if w.scale is not None else 0,
-                                    resid_ptr=addr(resid) if resid is not None else 0, up_ptr=up_ptr,
-                                    up_scale_ptr=up_scale,
-                                    round_before_bias=rnd_bias, round_before_resid=rnd_resid)
+                ls = LA.gemv_mfma(addr(x), addr(w.value), addr(out), M, N, K, c_dtype=out.dtype, ldb=ldb,
+                                  layout=w.layout, b_dtype=w.value.dtype, ws_ptr=addr(ws),
+                                  bias_ptr=addr(bias) if bias is not None else 0,
+                                  scale_ptr=addr(w.scale) if w.scale is not None else 0,
+                                  resid_ptr=addr(resid) if resid is not None else 0, up_ptr=up_ptr,
+                                  up_scale_ptr=up_scale,
+                                  round_before_bias=rnd_bias, round_before_resid=rnd_resid)
+                # with a planes consumer the reduction is the head prologue's
+                return ls[:1] if fold else ls
             if small:
                 return LA.gemv(addr(x), addr(w.value), addr(out), M, N, K, layout=w.layout,
                                b_dtype=w.value.dtype, c_dtype=out.dtype, ldb=ldb, ws_ptr=addr(ws),
@@ -233,7 +244,8 @@ class GemmMatch(Match):
         kind = "gemm_swiglu" if up is not None else "gemm"
         desc = (f"{'swiglu ' if up is not None else ''}gemm {w.layout} M={M} N={N} K={K} "
                 f"{dt.name(w.value.dtype)} -> {dt.name(out.dtype)}"
-                + (" +bias" if bias is not None else "") + (" +residual" if resid is not None else ""))
+                + (" +bias" if bias is not None else "") + (" +residual" if resid is not None else "")
+                + (" (partial sums to the head prologue)" if fold else ""))
         return [LaunchStep(kind, desc, self.inputs, self.outputs, make)]
 
 

@@ -210,3 +210,57 @@ def test_head_rope_writes_cache_rows(gpu, B, H, Hkv, D, MAXS, pos):
         keep = np.ones(MAXS, bool)  # the scatter drops a position past the cache
     np.testing.assert_array_equal(outs[0]["cache_k"][:, keep], ck[:, keep])
     np.testing.assert_array_equal(outs[0]["cache_v"][:, keep], cv[:, keep])
+
+
+def _projected_prologue(H, Hkv, D):
+    prologue = _decode_prologue_with_cache(H, Hkv, D)
+
+    def fn(x, qkv_weight, q_norm_weight, k_norm_weight, cache_k, cache_v, start_pos):
+        return prologue(np.matmul(x, qkv_weight), q_norm_weight, k_norm_weight, cache_k, cache_v, start_pos)
+    return fn
+
+
+@pytest.mark.parametrize("B,H,Hkv,D,hid,planes", [(8, 32, 8, 128, 4096, 16), (1, 8, 2, 128, 512, 2),
+                                                   (16, 16, 4, 64, 2048, 8), (3, 32, 8, 128, 8192, 20),
+                                                   (1, 4, 2, 64, 16384, None)])
+def test_head_rope_adds_projection_planes(gpu, B, H, Hkv, D, hid, planes):
+    """The decode projection of one token per sequence feeding the head
+    prologue: the prologue adds the projection's fp32 partial-sum planes
+    itself (two launches) and its q and cache rows equal those of the
+    lowering that reduces the planes in their own launch first (three
+    launches), bit for bit; a sequence whose token is all -0.0 checks the
+    signed zero the reduction's + 0 turns into +0.  Past 32 planes the
+    reduction keeps its launch."""
+    from nkipy_amd.dispatch.patterns_attention import ProjectionPlanesFusion
+
+    print(f"projection planes B={B} H={H}/{Hkv} D={D} hid={hid} planes={planes}", flush=True)
+    MAXS, pos = 256, 100
+    rng = np.random.default_rng(B * 13 + hid)
+    x = N.bf16_round(rng.standard_normal((B, 1, hid)))
+    x[0] = -0.0
+    w = N.bf16_round(rng.standard_normal((hid, (H + 2 * Hkv) * D)) * hid ** -0.5)
+    wq, wk = N.bf16_round(rng.uniform(0.5, 1.5, D)), N.bf16_round(rng.uniform(0.5, 1.5, D))
+    ck = N.bf16_round(rng.standard_normal((B, MAXS, Hkv, D)))
+    cv = N.bf16_round(rng.standard_normal((B, MAXS, Hkv, D)))
+    args = [dt.to_bf16(a) for a in (x, w, wq, wk, ck, cv)] + [np.array([pos], np.int32)]
+    g = NKIPyKernel.trace(_projected_prologue(H, Hkv, D)).specialize(*args)
+    fused = lower(g)
+    split = lower(g, [p for p in default_patterns() if not isinstance(p, ProjectionPlanesFusion)])
+    syms = lambda p: [l.symbol for s in p.steps for l in s.launches(lambda v: 1 << 20)]
+    assert fused.kernel_kinds == split.kernel_kinds == ["gemm", "head_rope"], fused.kernel_kinds
+    sf, ss = syms(fused), syms(split)
+    assert ss[1:] == ["nk_gemv_out_bf16", "nk_head_rope_bf16"], ss
+    if planes is None:
+        assert sf == ss, sf
+    else:
+        assert sf == [ss[0], "nk_head_rope_bf16"], sf
+        assert fused.steps[1].launches(lambda v: 1 << 20)[0].args.nplanes == planes
+    names = [p.name for p in g.parameters]
+    outs = []
+    for i, plan in enumerate((fused, split)):
+        dk = DeviceKernel(g, plan, f"projected_prologue_{i}")
+        res = dk({n: DeviceTensor.from_numpy(a, name=n) for n, a in zip(names, args)})
+        outs.append({k: dt.numpy_storage(v.numpy()) for k, v in res.items()})
+    for k in outs[0]:
+        np.testing.assert_array_equal(outs[0][k], outs[1][k], err_msg=k)
+    assert not np.signbit(dt.to_float32(outs[0]["cache_v"])[0, pos]).any()

@@ -495,9 +495,9 @@ def test_lowering_qwen3_head_prologue_is_one_launch():
     """The Qwen3 attention prologue (split of the QKV projection, per-head
     q / k RMSNorm, tables cast to bf16 and taken at the runtime position,
     bf16-step RoPE, the k / v cache writes at that position) lowers to one
-    head_rope launch that reads the projection in place and the fp32 tables
-    directly and writes k and v into the caches' rows: the decode layer is
-    the two projections around it and the attention."""
+    head_rope launch that reads the projection's partial sums in place and
+    the fp32 tables directly and writes k and v into the caches' rows: the
+    decode layer is the two projections around it and the attention."""
     from nkipy_amd.kernels.qwen3 import qwen3_attention_kernel
 
     B, MAXS, HID, H, D, HKV = 2, 512, 512, 8, 128, 2
@@ -520,13 +520,15 @@ def test_lowering_qwen3_head_prologue_is_one_launch():
     assert a.tflags == LA.HR_TABLE_F32 and a.pos == 1 << 40
     assert (a.t_row, a.t_rows, a.t_ss, a.S, a.D) == (D // 2, MAXS, 0, 1, D)
     q, k, v = a.t[0], a.t[1], a.t[2]
+    # the projection's fp32 partial sums read in place (K ranges of 256: two planes)
+    assert (a.plane, a.nplanes) == (B * N, LA.gemv_mfma_split(B, N, HID)[0]) == (B * N, 2)
     for t, heads, col0 in ((q, H, 0), (k, HKV, H * D), (v, HKV, (H + HKV) * D)):
         assert t.H == heads and t.rows == B * heads
-        assert (t.x_sb, t.x_sh, t.x_half) == (N, D, D // 2)  # the projection read in place
-        assert t.x == (1 << 40) + 2 * col0
+        assert (t.x_sb, t.x_sh, t.x_half) == (N, D, D // 2)
+        assert t.x == (1 << 40) + 4 * col0
     for t in (q, k):
-        assert t.flags == LA.HR_NORM | LA.HR_W and np.float32(t.eps) == np.float32(1e-6)
-    assert v.flags == LA.HR_COPY
+        assert t.flags == LA.HR_NORM | LA.HR_W | LA.HR_PLANES and np.float32(t.eps) == np.float32(1e-6)
+    assert v.flags == LA.HR_COPY | LA.HR_PLANES
     assert (q.o_sb, q.o_sh, q.o_sp) == (H * D, D, 0)
     # k and v go to row pos of their caches (B, MAXS, HKV, D)
     for t in (k, v):
@@ -601,3 +603,47 @@ def test_lowering_qwen3_prefill_attention_is_one_step():
     g = NKIPyKernel.trace(causal_gqa_attention_kernel).specialize(q, q, q)
     ((launch,),) = [st.launches(lambda v: 1 << 40) for st in lower(g).steps]
     assert launch.symbol == "nk_attention_causal_d128_sp" and launch.args.flags == 0
+
+
+def test_projection_planes_fold_into_head_prologue():
+    """The Qwen3 decode step lowers its QKV projection to the partial-sum
+    launch alone, the head prologue adding the planes; a projection whose
+    output is also a kernel result keeps its reduction launch."""
+    from nkipy_amd.core.trace import NKIPyKernel
+    from nkipy_amd.dispatch.lower import lower
+    from nkipy_amd.kernels.qwen3 import qwen3_attention_kernel
+    from nkipy_amd.kernels.rmsnorm import rmsnorm_kernel
+
+    B, MAXS, H, Hkv, D = 2, 256, 4, 2, 128
+    hid = H * D
+
+    def decode(x, qkv_weight, q_norm_weight, k_norm_weight, cache_k, cache_v, start_pos, o_weight):
+        return qwen3_attention_kernel(x, qkv_weight, q_norm_weight, k_norm_weight, 1e-6, H, D, Hkv,
+                                      cache_k, cache_v, start_pos, o_weight)
+
+    def both(x, qkv_weight, q_norm_weight, k_norm_weight, start_pos):
+        from nkipy_amd.core import tensor_apis
+        from nkipy_amd.kernels.qwen3 import apply_rotary_emb_kernel, compute_cos_sin_cache
+
+        qkv = np.matmul(x, qkv_weight)
+        xq = rmsnorm_kernel(qkv[:, :, :H * D].reshape(B, 1, H, D), q_norm_weight, 1e-6)
+        xk = rmsnorm_kernel(qkv[:, :, H * D:(H + Hkv) * D].reshape(B, 1, Hkv, D), k_norm_weight, 1e-6)
+        cos, sin = compute_cos_sin_cache(D, MAXS, base=1e6)
+        cos = tensor_apis.constant(cos).astype(qkv.dtype)
+        sin = tensor_apis.constant(sin).astype(qkv.dtype)
+        xq, xk = apply_rotary_emb_kernel(xq, xk, cos[start_pos], sin[start_pos])
+        return xq, xk, qkv
+
+    bf = lambda s: dt.to_bf16(np.zeros(s, np.float32))
+    g = NKIPyKernel.trace(decode).specialize(bf((B, 1, hid)), bf((hid, (H + 2 * Hkv) * D)), bf(D), bf(D),
+                                             bf((B, MAXS, Hkv, D)), bf((B, MAXS, Hkv, D)),
+                                             np.array([7], np.int32), bf((H * D, hid)))
+    p = lower(g)
+    assert p.kernel_kinds[:2] == ["gemm", "head_rope"], p.kernel_kinds
+    assert "partial sums to the head prologue" in p.steps[0].desc and "partial-sum planes" in p.steps[1].desc
+    assert [l.symbol for l in p.steps[0].launches(lambda v: 1 << 20)] == ["nk_gemv_mfma_nn_bf16_t1"]
+    g2 = NKIPyKernel.trace(both).specialize(bf((B, 1, hid)), bf((hid, (H + 2 * Hkv) * D)), bf(D), bf(D),
+                                            np.array([7], np.int32))
+    p2 = lower(g2)
+    assert "head_rope" in p2.kernel_kinds, p2.kernel_kinds
+    assert all("partial" not in s.desc for s in p2.steps), [s.desc for s in p2.steps]
