@@ -738,6 +738,15 @@ def bench_qwen3_decode(a, rt, mk):
     mk.end()  # the synchronous calls and the other batch sizes below are not labelled
     ins0, outs0 = sets[0]
     sync_us = _sync_call_us(dk, ins0, outs0)
+    # the same wait around the bound launch list alone (no argument handling)
+    for _ in range(10):
+        bounds[0].run()
+        rt.sync()
+    t0 = time.perf_counter()
+    for _ in range(50):
+        bounds[0].run()
+        rt.sync()
+    sync_bound_us = (time.perf_counter() - t0) / 50 * 1e6
     sync_graph_us = _sync_call_us(dk, ins0, outs0, graph=True)
     graph_ms = _time_steps(bounds, steps, warm, rt, graph=True)
     step_rec = {"label": "step", "kernel": " + ".join(l.symbol for l in bounds[0].launches), "bound": "hbm"}
@@ -761,6 +770,7 @@ def bench_qwen3_decode(a, rt, mk):
                        "kv_heads": Hkv, "head_dim": D},
              "dtype": "bf16 (the traced cast points of the Qwen3 attention layer)",
              "us_per_step": round(ms * 1e3, 2), "synchronous_call_us": round(sync_us, 1),
+             "synchronous_bound_launch_us": round(sync_bound_us, 1),
              "us_per_step_graph": round(graph_ms * 1e3, 2), "synchronous_graph_call_us": round(sync_graph_us, 1),
              "roofline": roof, "kernels": recs, "other_batches": batches,
              "note": "one token per sequence through the whole attention layer (QKV projection, q / k norm and "
